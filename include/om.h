@@ -1,0 +1,208 @@
+/*
+ * om.h — C ABI of libom_hip.so, the MI355X (gfx950) kernels of the OneModel training path.
+ *
+ * This is the boundary a host tape binds (the reference's C# tape through [LibraryImport], or this repository's C++
+ * tape in onemodel-csharp_amd/train). Every entry point:
+ *   - takes plain device pointers (float*, int32_t*) and sizes; no C++ or framework types cross the ABI;
+ *   - is asynchronous on the context's HIP stream; only om_download and om_ctx_sync block;
+ *   - returns om_status (OM_OK = 0) and leaves a message in om_last_error(ctx) on failure;
+ *   - validates shapes and pointers on the host before launching, so a kernel never sees a shape it does not handle;
+ *   - is deterministic: tiling, split-K and reduction orders depend only on the shape.
+ * Arithmetic follows the reference's CPU training path (fp32 tensors, fp64 where the reference sums in double) within
+ * 1e-5 scaled error; integer work (labels, pool indices, CTC alignment) is bit-exact, and so is the optimizer step
+ * given the same gradient.
+ *
+ * Citations name the reference function (recursive-ai-oss/onemodel-csharp, file:line) each entry point replaces.
+ */
+#ifndef OM_H
+#define OM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t om_status;
+enum {
+    OM_OK = 0,
+    OM_E_ARG = 1,    /* bad shape, size or pointer: the reference's TensorShapeException / ArgumentException */
+    OM_E_OOM = 2,    /* the arena or the device is out of memory */
+    OM_E_DEVICE = 3, /* a HIP runtime error */
+    OM_E_STATE = 4   /* the call is not valid in the context's current state (InvalidOperationException) */
+};
+
+typedef struct om_ctx om_ctx;
+
+/* ---------------------------------------------------------------------------------------------- context */
+/* One context per host thread and device; it owns one HIP stream and the arena. */
+om_status om_ctx_create(int device, om_ctx **out);
+om_status om_ctx_destroy(om_ctx *ctx);
+om_status om_ctx_sync(om_ctx *ctx);
+const char *om_last_error(om_ctx *ctx);
+/* The context's hipStream_t, for callers that time or order work around the library's launches. */
+void *om_ctx_stream(om_ctx *ctx);
+/* Version of this ABI (major * 100 + minor). */
+int om_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------- arena */
+/* Device memory in two regions, in the spirit of the reference's buffer lifetimes (ActivationScope.cs:18-106,
+ * BufferPool.cs:26-161): PERSISTENT holds parameters, gradients and optimizer moments for the life of the context;
+ * STEP holds a step's activations and temporary gradients and is rewound by om_step_reset at the step edge
+ * (the ActivationScope.Dispose equivalent). Allocations are 256-byte aligned bump allocations; a step that outgrows
+ * its slab chains another slab, so addresses handed out stay valid until the reset. */
+enum { OM_REGION_PERSISTENT = 0, OM_REGION_STEP = 1 };
+om_status om_arena_reserve(om_ctx *ctx, uint64_t persistent_bytes, uint64_t step_bytes);
+om_status om_alloc(om_ctx *ctx, int region, uint64_t bytes, void **out);
+om_status om_step_reset(om_ctx *ctx);
+/* Bytes in use and reserved, per region. */
+om_status om_arena_stats(om_ctx *ctx, int region, uint64_t *used, uint64_t *reserved);
+/* Host<->device copies at step edges (a region is the unit of transfer, ExecutionBackend.cs:8-13). */
+om_status om_upload(om_ctx *ctx, void *dst_device, const void *src_host, uint64_t bytes);
+om_status om_download(om_ctx *ctx, void *dst_host, const void *src_device, uint64_t bytes);
+om_status om_copy(om_ctx *ctx, void *dst_device, const void *src_device, uint64_t bytes);
+/* dst = 0 (Backprop.ZeroGrad, Engine.cs:77-91); a fill kernel, so it is safe inside a captured graph. */
+om_status om_zero(om_ctx *ctx, void *dst_device, uint64_t bytes);
+om_status om_fill(om_ctx *ctx, float *dst, float value, int64_t n);
+
+/* ---------------------------------------------------------------------------------------------- GEMM */
+/* C[m,n] = op(A)[m,k] * op(B)[k,n] (+ bias[n]) on fp32 MFMA, for `batch` independent products. Row-major operands
+ * with leading dimensions lda/ldb/ldc; trans_a means A is stored [k,m], trans_b means B is stored [n,k].
+ * accumulate != 0 adds the product into C (C = C + AB, one rounding of the finished dot product), the leaf
+ * accumulation of Engine.AccumulateLeaf (Engine.cs:292-328). Replaces Dense.Gemm / Kernels.Gemm.Run
+ * (Dense.cs:12-49, Gemm.cs:48). Batch item z reads A at a + (z / batch_div) * sa_outer + (z % batch_div) * sa_inner
+ * (likewise B, C), which addresses heads inside [batch, seq, heads, dim] activations without a permute copy. */
+typedef struct {
+    int32_t batch, batch_div;
+    int64_t sa_outer, sa_inner, sb_outer, sb_inner, sc_outer, sc_inner;
+} om_batch;
+om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, const float *a, int lda,
+                  const float *b, int ldb, float *c, int ldc, const float *bias, int accumulate,
+                  const om_batch *batch);
+
+/* ---------------------------------------------------------------------------------------------- dense layers */
+/* Ops.Linear forward (Ops.Layers.cs:715-733): y[rows,out] = x[rows,in] * w[out,in]^T + b[out] (b may be NULL). */
+om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
+                        int out);
+/* Linear backward = MatMul backward + Permute backward + bias SumTo (BackwardOps.cs:69-82, 107-118, 201-269):
+ * dx = g w, dw = g^T x written directly as [out,in], db = fp64 column sums of g. Each output pointer may be NULL;
+ * the acc_* flags add into the destination instead of overwriting it (leaf accumulation). */
+om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
+                        int rows, int in, int out, int acc_dx, int acc_dw, int acc_db);
+/* Bias gradient alone: db[n] (+)= (float) sum over rows of g[row, n] in double (BackwardOps.SumTo). */
+om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- elementwise */
+/* ReluUn / ReluGradBin (TrainElementwise.cs:41-45, 93-98; Ops.cs:94-107; BackwardOps.cs:66-68). */
+om_status om_relu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n);
+om_status om_relu_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int64_t n, int accumulate);
+/* Ops.Gelu erf form and GeluGradBin (Ops.Nn.cs:86-112; TrainElementwise.cs:59-85; Transcendental.cs:167-263). */
+om_status om_gelu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n);
+om_status om_gelu_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int64_t n, int accumulate);
+/* y = a + b, y = a - b, y = a * b (same shapes; Ops.cs:15-56). */
+om_status om_add(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
+om_status om_sub(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
+om_status om_mul(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
+/* dst += src, or dst = src * alpha + dst (Engine.AddInto, Engine.cs:331-344; Neg backward is alpha = -1). */
+om_status om_axpy(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n);
+/* dst = src * alpha (a copy when alpha is 1). */
+om_status om_scale(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n);
+
+/* ---------------------------------------------------------------------------------------------- reductions */
+/* Ops.Sum / Ops.Mean over all elements in double (Ops.Nn.cs:162-231); *out is a device float. */
+om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mean);
+/* Mean over the middle axis of [outer, n, inner] (Ops.Nn.cs:186-231) and its backward: dx = g / n broadcast
+ * (BackwardNn.cs:145-168). The backward reads g from device memory; g_scalar_index < 0 means g has [outer, inner]
+ * values, otherwise it is one scalar at g[0] broadcast to everything (Mean over all elements). */
+om_status om_mean_axis(om_ctx *ctx, const float *x, float *y, int outer, int n, int inner);
+om_status om_mean_axis_bwd(om_ctx *ctx, const float *g, float *dx, int outer, int n, int inner, int accumulate);
+om_status om_mean_all_bwd(om_ctx *ctx, const float *g_scalar, float *dx, int64_t n, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- normalisation */
+/* Ops.LayerNorm (Ops.Layers.cs:109-141; NormKernels.cs:79-127): saves mean and 1/sigma per row. */
+om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, const float *beta, float *y, float *mean,
+                           float *rstd, int rows, int cols, float eps);
+/* LayerNormBackward (BackwardNn.cs:170-223): dx, and dgamma/dbeta as fp64 column sums (any may be NULL). */
+om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                           const float *rstd, float *dx, float *dgamma, float *dbeta, int rows, int cols, int acc_dx,
+                           int acc_params);
+
+/* ---------------------------------------------------------------------------------------------- softmax family */
+/* Softmax.Rows (Softmax.cs:27-133) and its backward (BackwardNn.cs:26-52). */
+om_status om_softmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols);
+om_status om_softmax_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int rows, int cols, int accumulate);
+/* Ops.LogSoftmax (Ops.Layers.cs:47-96) and backward (BackwardNn.cs:54-80). */
+om_status om_logsoftmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols);
+om_status om_logsoftmax_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int rows, int cols,
+                            int accumulate);
+/* Ops.NllLoss (Ops.Layers.cs:644-699) -> *loss (device float); a target outside [0,cols) that is not ignore_index
+ * is reported through *bad_row (device int32, -1 when none), the reference's ArgumentOutOfRangeException. */
+om_status om_nll_fwd(om_ctx *ctx, const float *logp, const int32_t *target, float *loss, int32_t *bad_row, int rows,
+                     int cols, int mean, int ignore_index);
+/* Fused softmax cross-entropy gradient = LogSoftmax backward of NllBackward (BackwardNn.cs:54-80, 602-632), in the
+ * reference's rounding order: dlogits = d - exp(logp) * (float)sum(d), d = -g/count at the target. */
+om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,
+                      int rows, int cols, int mean, int ignore_index, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- attention */
+/* Ops.Attention (Ops.Layers.cs:746-807) and AttentionBackward (BackwardNn.cs:636-701). q,o are [B,Lq,H,D] and
+ * k,v [B,Lk,H,D] (the Linear outputs, heads interleaved; the reference's split/merge permutes become addressing),
+ * mask is NULL, [Lq,Lk] (mask_batched 0) or [B,Lq,Lk] additive. The forward saves the weights P [B,H,Lq,Lk]
+ * (HBM is plentiful; the reference recomputes them). The backward writes dq, dk, dv in the q/k/v layouts and uses
+ * `ds` [B,H,Lq,Lk] as scratch. */
+om_status om_attention_fwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *mask,
+                           int mask_batched, float *o, float *p, int B, int H, int lq, int lk, int d, float scale);
+om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *p,
+                           const float *g, float *dq, float *dk, float *dv, float *ds, int B, int H, int lq, int lk,
+                           int d, float scale, int acc);
+
+/* ---------------------------------------------------------------------------------------------- convolution, pooling */
+/* Ops.Conv2d, groups 1, square stride/padding (Ops.Layers.cs:279-336; Conv.cs:54) as implicit GEMM on MFMA, and
+ * ConvBackward (BackwardNn.cs:317-402): dx = col2im(W^T g) as an implicit GEMM over g, dw = g im2col(x) with a
+ * deterministic split over images and pixels, db = fp64 sums. Output pointers may be NULL. */
+om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
+                        int H, int W, int Cout, int KH, int KW, int stride, int pad);
+om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
+                        int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad, int acc_dx,
+                        int acc_params);
+/* Ops.MaxPool2d (Ops.cs:151-178; TensorKernels.cs:242-296): Int32 flat argmax, first wins, NaN wins; and
+ * MaxPoolBackward (BackwardOps.cs:285-298): dx = 0, dx[idx] += g. */
+om_status om_maxpool_fwd(om_ctx *ctx, const float *x, float *y, int32_t *idx, int N, int C, int H, int W, int KH,
+                         int KW, int SH, int SW, int PH, int PW);
+om_status om_maxpool_bwd(om_ctx *ctx, const float *g, const int32_t *idx, float *dx, int N, int C, int H, int W,
+                         int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- CTC */
+/* Ops.CtcLoss (CtcLoss.cs:40-153) in double with the reference's exp/ln/logadd (Ctc.cs:515-616); reduction
+ * 0 = None ([B] losses), 1 = Mean, 2 = Sum (a scalar). Inputs are validated on the host from the host copies of the
+ * lengths and targets. `lp` is [T,B,C] on the device; targets/in_len/tgt_len are device copies of the host arrays.
+ * om_ctc_bwd = CtcBackward (BackwardRecurrent.cs:253-296): dlp[t,b,c] (+)= -scale * exp(...), g on the device. */
+om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                     const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                     const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
+                     int zero_infinity, float *loss);
+om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                     const int32_t *tgt_len, const float *g, float *dlp, int max_tgt_len, int T, int B, int C,
+                     int blank, int reduction, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- optimizer */
+/* Adam.UpdateRange (Optimizers.cs:554-589) over n contiguous elements: the tape keeps parameters, gradients and
+ * both moments each contiguous in the persistent region in Parameters() order, so one launch updates every
+ * parameter (a run per contiguous group of parameters that have gradients). vmax is NULL unless AMSGrad.
+ * step_size and sqrt_bc2 come from om_adam_scalars (Adam.BeginStep, Optimizers.cs:501-508). IEEE float, no fused
+ * multiply-add: bit-identical to the reference's CPU update given the same gradient. */
+om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v, float *vmax, int64_t n, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, int decoupled, float step_size,
+                       float sqrt_bc2);
+/* Host helper: Adam.IntPow + BeginStep in double for step t (1-based). */
+void om_adam_scalars(float lr, float beta1, float beta2, int64_t t, float *step_size, float *sqrt_bc2);
+/* Sgd.Update (Optimizers.cs, class Sgd) over n contiguous elements; buf may be NULL (no momentum); first != 0 on
+ * the parameter's first step (the momentum buffer starts from the gradient). */
+om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t n, float lr, float momentum,
+                      float dampening, float weight_decay, int nesterov, int first);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OM_H */

@@ -1,0 +1,258 @@
+// CTC loss forward and gradient in double (Ops.CtcLoss, CtcLoss.cs:40-153; CtcLossMath, CtcLoss.cs:155-281;
+// CtcBackward, BackwardRecurrent.cs:253-296), with the reference's own fixed exp/ln/logadd (Ctc.cs:515-616).
+//
+// One workgroup per sequence. The recursions are sequential in t; within a step every extended-label position s is
+// independent, so threads own positions and meet at a barrier per step. Each value is computed by exactly the
+// operations of the reference in the same order (no contraction: -ffp-contract=off), so the loss, the alignment
+// sums and the gradient are bit-identical to the CPU recursions.
+#include "om_internal.hpp"
+
+#include <cmath>
+
+namespace {
+
+constexpr int kBlock = 64;
+
+__device__ double ctc_exp(double x) {
+    if (!(x > -700.0)) return 0.0;
+    if (x > 700.0) x = 700.0;
+    double k = floor((x * 1.4426950408889634) + 0.5);
+    double r = (x - (k * 6.93147180369123816490e-01)) - (k * 1.90821492927058770002e-10);
+    double p = 1.0 / 6227020800.0;
+    p = (p * r) + (1.0 / 479001600.0);
+    p = (p * r) + (1.0 / 39916800.0);
+    p = (p * r) + (1.0 / 3628800.0);
+    p = (p * r) + (1.0 / 362880.0);
+    p = (p * r) + (1.0 / 40320.0);
+    p = (p * r) + (1.0 / 5040.0);
+    p = (p * r) + (1.0 / 720.0);
+    p = (p * r) + (1.0 / 120.0);
+    p = (p * r) + (1.0 / 24.0);
+    p = (p * r) + (1.0 / 6.0);
+    p = (p * r) + 0.5;
+    p = (p * r) + 1.0;
+    p = (p * r) + 1.0;
+    return p * __longlong_as_double((long long)((int)k + 1023) << 52);
+}
+__device__ double ctc_log(double x) {
+    if (x == 0.0) return -__longlong_as_double(0x7FF0000000000000LL);
+    if (!(x > 0.0) || isinf(x)) return x;
+    long long bits = __double_as_longlong(x);
+    int e = (int)((bits >> 52) & 0x7FF);
+    if (e == 0) {
+        bits = __double_as_longlong(x * 18014398509481984.0);
+        e = (int)((bits >> 52) & 0x7FF) - 54;
+    }
+    e -= 1023;
+    double m = __longlong_as_double((bits & 0x000FFFFFFFFFFFFFLL) | 0x3FF0000000000000LL);
+    if (m > 1.4142135623730951) {
+        m *= 0.5;
+        e++;
+    }
+    double s = (m - 1.0) / (m + 1.0);
+    double z = s * s;
+    double q = 1.0 / 19.0;
+    q = (q * z) + (1.0 / 17.0);
+    q = (q * z) + (1.0 / 15.0);
+    q = (q * z) + (1.0 / 13.0);
+    q = (q * z) + (1.0 / 11.0);
+    q = (q * z) + (1.0 / 9.0);
+    q = (q * z) + (1.0 / 7.0);
+    q = (q * z) + (1.0 / 5.0);
+    q = (q * z) + (1.0 / 3.0);
+    q = (q * z) + 1.0;
+    return (e * 0.6931471805599453) + (2.0 * s * q);
+}
+__device__ __forceinline__ bool is_neg_inf(double v) { return isinf(v) && v < 0.0; }
+__device__ double ctc_logadd(double a, double b) {
+    if (a < b) {
+        double t = a;
+        a = b;
+        b = t;
+    }
+    if (is_neg_inf(b)) return a;
+    double d = b - a;
+    return d < -40.0 ? a : a + ctc_log(1.0 + ctc_exp(d));
+}
+
+__device__ __forceinline__ int label_at(const int32_t *tgt, int blank, int s) { return (s & 1) == 0 ? blank : tgt[s >> 1]; }
+__device__ __forceinline__ bool can_skip(const int32_t *tgt, int s) {
+    return s >= 2 && (s & 1) == 1 && tgt[s >> 1] != tgt[(s >> 1) - 1];
+}
+
+// alpha[t*ext + s] for t < len (CtcLossMath.Alpha); returns nll via *nll_out from thread 0.
+__device__ void alpha_pass(const float *lp, int B, int C, int b, int len, const int32_t *tgt, int L, int blank,
+                           double *alpha, double *nll_out) {
+    const int ext = 2 * L + 1;
+    const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
+    for (int t = 0; t < len; t++) {
+        for (int s = threadIdx.x; s < ext; s += blockDim.x) {
+            double a;
+            if (t == 0) {
+                a = s <= 1 ? 0.0 : NEG;
+            } else {
+                a = alpha[(t - 1) * ext + s];
+                if (s >= 1) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 1]);
+                if (can_skip(tgt, s)) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 2]);
+            }
+            alpha[t * ext + s] = is_neg_inf(a) ? NEG : a + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        double nll;
+        if (len == 0) {
+            nll = L == 0 ? 0.0 : __longlong_as_double(0x7FF0000000000000LL);
+        } else {
+            double p = alpha[(len - 1) * ext + ext - 1];
+            if (ext >= 2) p = ctc_logadd(p, alpha[(len - 1) * ext + ext - 2]);
+            nll = is_neg_inf(p) ? __longlong_as_double(0x7FF0000000000000LL) : -p;
+        }
+        *nll_out = nll;
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(kBlock) k_ctc_fwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
+                                                    const int32_t *__restrict__ in_len,
+                                                    const int32_t *__restrict__ tgt_len, int T, int B, int C, int blank,
+                                                    int max_ext, double *__restrict__ alpha_ws,
+                                                    double *__restrict__ per) {
+    __shared__ double nll;
+    int b = blockIdx.x;
+    int off = 0;
+    for (int i = 0; i < b; i++) off += tgt_len[i];
+    double *alpha = alpha_ws + (int64_t)b * (T > 0 ? T : 1) * max_ext;
+    alpha_pass(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
+    if (threadIdx.x == 0) per[b] = nll;
+}
+// Reduction in sequence order (CtcLoss.cs:98-125).
+__global__ void k_ctc_reduce(const double *__restrict__ per, const int32_t *__restrict__ tgt_len, int B, int reduction,
+                             int zero_inf, float *__restrict__ loss) {
+    if (threadIdx.x != 0) return;
+    double sum = 0.0;
+    for (int b = 0; b < B; b++) {
+        double v = per[b];
+        if (isinf(v) && v > 0 && zero_inf) v = 0.0;
+        if (reduction == 0) loss[b] = (float)v;
+        else sum += reduction == 1 ? v / (double)(tgt_len[b] > 1 ? tgt_len[b] : 1) : v;
+    }
+    if (reduction != 0) loss[0] = (float)(reduction == 1 ? sum / B : sum);
+}
+
+// CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence: recompute alpha, run beta backwards in t, and for every
+// class accumulate logadd(alpha + beta) over its positions in increasing s.
+__global__ void __launch_bounds__(kBlock) k_ctc_bwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
+                                                    const int32_t *__restrict__ in_len,
+                                                    const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
+                                                    float *__restrict__ dlp, int T, int B,
+                                                    int C, int blank, int reduction, int max_ext, int acc,
+                                                    double *__restrict__ ws) {
+    __shared__ double nll;
+    const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
+    int b = blockIdx.x;
+    int len = in_len[b], L = tgt_len[b];
+    int off = 0;
+    for (int i = 0; i < b; i++) off += tgt_len[i];
+    const int32_t *tgt = targets + off;
+    int tt = T > 0 ? T : 1;
+    double *alpha = ws + (int64_t)b * 2 * tt * max_ext;
+    double *beta = alpha + (int64_t)tt * max_ext;
+    // dlp for this sequence starts from zero (or the existing gradient when accumulating).
+    if (!acc)
+        for (int i = threadIdx.x; i < T * C; i += blockDim.x) dlp[((int64_t)(i / C) * B + b) * C + i % C] = 0.0f;
+    alpha_pass(lp, B, C, b, len, tgt, L, blank, alpha, &nll);
+    if (len == 0 || (isinf(nll) && nll > 0)) return;
+    double scale = reduction == 0 ? (double)g[b] : (double)g[0];
+    if (reduction == 1) scale = scale / (double)(L > 1 ? L : 1) / (double)B;
+    const int ext = 2 * L + 1;
+    for (int t = len - 1; t >= 0; t--) {
+        for (int s = threadIdx.x; s < ext; s += blockDim.x) {
+            double v;
+            if (t == len - 1) {
+                v = s >= ext - 2 ? 0.0 : NEG;
+            } else {
+                v = beta[(t + 1) * ext + s];
+                if (s + 1 < ext) v = ctc_logadd(v, beta[(t + 1) * ext + s + 1]);
+                if (s + 2 < ext && can_skip(tgt, s + 2)) v = ctc_logadd(v, beta[(t + 1) * ext + s + 2]);
+            }
+            beta[t * ext + s] = is_neg_inf(v) ? NEG : v + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < C; c += blockDim.x) {
+            double a = NEG;
+            for (int s = 0; s < ext; s++) {
+                if (label_at(tgt, blank, s) != c) continue;
+                double ab = alpha[t * ext + s] + beta[t * ext + s];
+                if (!is_neg_inf(ab) && ab == ab) a = ctc_logadd(a, ab);
+            }
+            if (is_neg_inf(a)) continue;
+            double l = (double)lp[((int64_t)t * B + b) * C + c];
+            float *d = dlp + ((int64_t)t * B + b) * C + c;
+            *d = *d + (float)(-scale * ctc_exp(a - l + nll));
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                     const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                     const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
+                     int zero_infinity, float *loss) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && loss && h_in_len && h_tgt_len && (h_targets || n_targets == 0),
+               "om_ctc_fwd: NULL pointer");
+    OM_REQUIRE(ctx, T >= 0 && B > 0 && C > 0, "om_ctc_fwd: CtcLoss needs log-probabilities [T,B,C]");
+    OM_REQUIRE(ctx, (unsigned)blank < (unsigned)C, "om_ctc_fwd: The blank index %d is outside [0, %d).", blank, C);
+    OM_REQUIRE(ctx, reduction >= 0 && reduction <= 2, "om_ctc_fwd: bad reduction %d", reduction);
+    int64_t total = 0;
+    for (int b = 0; b < B; b++) {
+        OM_REQUIRE(ctx, (unsigned)h_in_len[b] <= (unsigned)T,
+                   "om_ctc_fwd: Input length %d of sequence %d is outside [0, %d].", h_in_len[b], b, T);
+        OM_REQUIRE(ctx, h_tgt_len[b] >= 0, "om_ctc_fwd: Target length %d of sequence %d is negative.", h_tgt_len[b], b);
+        total += h_tgt_len[b];
+    }
+    OM_REQUIRE(ctx, total == n_targets, "om_ctc_fwd: The target lengths sum to %lld but %d labels were given.",
+               (long long)total, n_targets);
+    for (int i = 0; i < n_targets; i++)
+        OM_REQUIRE(ctx, (unsigned)h_targets[i] < (unsigned)C && h_targets[i] != blank,
+                   "om_ctc_fwd: Target label %d must be in [0, %d) and differ from the blank %d.", h_targets[i], C,
+                   blank);
+    int max_ext = 1;
+    for (int b = 0; b < B; b++) max_ext = 2 * h_tgt_len[b] + 1 > max_ext ? 2 * h_tgt_len[b] + 1 : max_ext;
+    om_status s;
+    float *scr;
+    uint64_t need = sizeof(double) * ((uint64_t)B * (T > 0 ? T : 1) * max_ext + B);
+    s = om::scratch(ctx, need, &scr);
+    if (s) return s;
+    double *alpha = reinterpret_cast<double *>(scr);
+    double *per = alpha + (uint64_t)B * (T > 0 ? T : 1) * max_ext;
+    hipLaunchKernelGGL(k_ctc_fwd, dim3(B), dim3(kBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, T, B, C, blank,
+                       max_ext, alpha, per);
+    hipLaunchKernelGGL(k_ctc_reduce, dim3(1), dim3(64), 0, ctx->stream, per, tgt_len, B, reduction, zero_infinity,
+                       loss);
+    return OM_LAUNCH_CHECK(ctx, "om_ctc_fwd");
+}
+
+om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                     const int32_t *tgt_len, const float *g, float *dlp, int max_tgt_len, int T, int B, int C,
+                     int blank, int reduction, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && g && dlp && T >= 0 && B > 0 && C > 0 && max_tgt_len >= 0,
+               "om_ctc_bwd: bad arguments");
+    const int max_ext = 2 * max_tgt_len + 1;
+    om_status s;
+    float *scr;
+    uint64_t tt = T > 0 ? T : 1;
+    s = om::scratch(ctx, sizeof(double) * 2ull * B * tt * max_ext, &scr);
+    if (s) return s;
+    hipLaunchKernelGGL(k_ctc_bwd, dim3(B), dim3(kBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, g, dlp, T, B, C,
+                       blank, reduction, max_ext, accumulate, reinterpret_cast<double *>(scr));
+    return OM_LAUNCH_CHECK(ctx, "om_ctc_bwd");
+}
+
+}  // extern "C"

@@ -1,0 +1,293 @@
+// Bandwidth-bound element-wise maps and reductions of the training path. Grid-stride loops over float4 where the
+// pointers and length allow it; every element sees the same IEEE operations in the same order as the reference's
+// lane loops (TrainElementwise.cs), so position and vector width never change a result.
+#include "om_internal.hpp"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+inline unsigned ew_grid(int64_t n4) { return om::grid1d(n4, kBlock, 4096); }
+
+inline bool aligned4(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// One functor per map; `apply(a, b)` gets the two inputs of an element.
+struct ReluF {
+    __device__ float operator()(float x, float) const { return x > 0.0f ? x : (x == x ? 0.0f : x); }
+};
+struct ReluGradF {
+    __device__ float operator()(float g, float y) const { return y > 0.0f ? g : 0.0f; }
+};
+struct GeluF {
+    __device__ float operator()(float x, float) const {
+        float e, ope;
+        omd::erf_parts(x * 0.70710677f, e, ope);
+        float res = (0.5f * x) * ope;
+        if (x == -__int_as_float(0x7F800000)) res = -0.0f;
+        return omd::canon(x == x ? res : x);
+    }
+};
+struct GeluGradF {
+    __device__ float operator()(float g, float v) const {
+        float e, ope;
+        omd::erf_parts(v * 0.70710677f, e, ope);
+        float cdf = 0.5f * (1.0f + e);
+        float pdf = omd::exp_poly((-0.5f * v) * v) * 0.3989423f;
+        return omd::canon(g * (cdf + v * pdf));
+    }
+};
+struct AddF {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct SubF {
+    __device__ float operator()(float a, float b) const { return a - b; }
+};
+struct MulF {
+    __device__ float operator()(float a, float b) const { return a * b; }
+};
+
+template <class F, bool ACC>
+__global__ void __launch_bounds__(kBlock) k_map2(const float *__restrict__ a, const float *__restrict__ b,
+                                                 float *__restrict__ y, int64_t n, F f) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    int64_t n4 = n >> 2;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a);
+    const float4 *b4 = reinterpret_cast<const float4 *>(b);
+    float4 *y4 = reinterpret_cast<float4 *>(y);
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        float4 va = a4[i], vb = b ? b4[i] : va, r;
+        r.x = f(va.x, vb.x);
+        r.y = f(va.y, vb.y);
+        r.z = f(va.z, vb.z);
+        r.w = f(va.w, vb.w);
+        if (ACC) {
+            float4 o = y4[i];
+            r.x = o.x + r.x; r.y = o.y + r.y; r.z = o.z + r.z; r.w = o.w + r.w;
+        }
+        y4[i] = r;
+    }
+    for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float r = f(a[i], b ? b[i] : a[i]);
+        y[i] = ACC ? y[i] + r : r;
+    }
+}
+template <class F, bool ACC>
+__global__ void __launch_bounds__(kBlock) k_map2_scalar(const float *__restrict__ a, const float *__restrict__ b,
+                                                        float *__restrict__ y, int64_t n, F f) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float r = f(a[i], b ? b[i] : a[i]);
+        y[i] = ACC ? y[i] + r : r;
+    }
+}
+
+template <class F>
+om_status map2(om_ctx *ctx, const char *name, const float *a, const float *b, float *y, int64_t n, int acc, F f) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, n >= 0, "%s: negative length", name);
+    if (n == 0) return OM_OK;
+    OM_REQUIRE(ctx, a && y, "%s: NULL pointer", name);
+    bool vec = aligned4(a) && aligned4(y) && (!b || aligned4(b));
+    dim3 grid(ew_grid(vec ? (n + 3) / 4 : n)), block(kBlock);
+    if (vec) {
+        if (acc) hipLaunchKernelGGL((k_map2<F, true>), grid, block, 0, ctx->stream, a, b, y, n, f);
+        else hipLaunchKernelGGL((k_map2<F, false>), grid, block, 0, ctx->stream, a, b, y, n, f);
+    } else {
+        if (acc) hipLaunchKernelGGL((k_map2_scalar<F, true>), grid, block, 0, ctx->stream, a, b, y, n, f);
+        else hipLaunchKernelGGL((k_map2_scalar<F, false>), grid, block, 0, ctx->stream, a, b, y, n, f);
+    }
+    return OM_LAUNCH_CHECK(ctx, name);
+}
+
+__global__ void __launch_bounds__(kBlock) k_axpy(float alpha, const float *__restrict__ s, float *__restrict__ d,
+                                                 int64_t n, int overwrite) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float v = alpha == 1.0f ? s[i] : s[i] * alpha;
+        d[i] = overwrite ? v : d[i] + v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- reductions
+// Sum of all elements in double: stage 1 gives one partial per block (fixed element->block assignment from n),
+// stage 2 adds the partials in block order.
+constexpr int kSumBlocks = 1024;
+__global__ void __launch_bounds__(kBlock) k_sum_partial(const float *__restrict__ x, int64_t n,
+                                                        double *__restrict__ part) {
+    __shared__ double sh[kBlock / 64];
+    double acc = 0.0;
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) acc += (double)x[i];
+    double t = omd::block_sum<kBlock / 64>(acc, sh);
+    if (threadIdx.x == 0) part[blockIdx.x] = t;
+}
+__global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ part, int np, float *__restrict__ out,
+                                                  double divisor) {
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < np; i += 64) acc += part[i];
+    acc = omd::wave_sum(acc);
+    if (threadIdx.x == 0) out[0] = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;
+}
+
+// Column sums of a [rows, cols] matrix in double: block (x = column tile of 256, y = row chunk) -> partial[chunk][col];
+// then each column adds its chunk partials in chunk order.
+__global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restrict__ g, int rows, int cols,
+                                                           int rows_per_chunk, double *__restrict__ part) {
+    int col = blockIdx.x * kBlock + threadIdx.x;
+    int r0 = blockIdx.y * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
+    if (col >= cols) return;
+    double acc = 0.0;
+    for (int r = r0; r < r1; r++) acc += (double)g[(int64_t)r * cols + col];
+    part[(int64_t)blockIdx.y * cols + col] = acc;
+}
+__global__ void __launch_bounds__(kBlock) k_colsum_final(const double *__restrict__ part, int chunks, int cols,
+                                                         float *__restrict__ out, int acc) {
+    int col = blockIdx.x * kBlock + threadIdx.x;
+    if (col >= cols) return;
+    double s = 0.0;
+    for (int c = 0; c < chunks; c++) s += part[(int64_t)c * cols + col];
+    float v = (float)s;
+    out[col] = acc ? out[col] + v : v;
+}
+
+// Mean over the middle axis of [outer, n, inner]. inner == 1: one wavefront per output (contiguous row);
+// otherwise one thread per output (threads along inner read contiguous memory).
+__global__ void __launch_bounds__(kBlock) k_mean_rows(const float *__restrict__ x, float *__restrict__ y, int outer,
+                                                      int n) {
+    int wave = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (wave >= outer) return;
+    const float *xr = x + (int64_t)wave * n;
+    double acc = 0.0;
+    for (int k = lane; k < n; k += 64) acc += (double)xr[k];
+    acc = omd::wave_sum(acc);
+    if (lane == 0) y[wave] = (float)(acc / n);
+}
+__global__ void __launch_bounds__(kBlock) k_mean_inner(const float *__restrict__ x, float *__restrict__ y, int outer,
+                                                       int n, int inner) {
+    int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= (int64_t)outer * inner) return;
+    int o = (int)(t / inner), i = (int)(t % inner);
+    double acc = 0.0;
+    for (int k = 0; k < n; k++) acc += (double)x[((int64_t)o * n + k) * inner + i];
+    y[t] = (float)(acc / n);
+}
+__global__ void __launch_bounds__(kBlock) k_mean_axis_bwd(const float *__restrict__ g, float *__restrict__ dx,
+                                                          int outer, int n, int inner, int acc) {
+    int64_t total = (int64_t)outer * n * inner, stride = (int64_t)gridDim.x * kBlock;
+    float fn = (float)n;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
+        int64_t o = t / ((int64_t)n * inner), i = t % inner;
+        float v = g[o * inner + i] / fn;
+        dx[t] = acc ? dx[t] + v : v;
+    }
+}
+__global__ void __launch_bounds__(kBlock) k_mean_all_bwd(const float *__restrict__ g, float *__restrict__ dx,
+                                                         int64_t n, int acc) {
+    float v = g[0] / (float)n;
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) dx[t] = acc ? dx[t] + v : v;
+}
+
+}  // namespace
+
+extern "C" {
+
+om_status om_relu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n) {
+    return map2(ctx, "om_relu_fwd", x, nullptr, y, n, 0, ReluF{});
+}
+om_status om_relu_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int64_t n, int accumulate) {
+    OM_REQUIRE(ctx, y || n == 0, "om_relu_bwd: NULL saved output");
+    return map2(ctx, "om_relu_bwd", g, y, dx, n, accumulate, ReluGradF{});
+}
+om_status om_gelu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n) {
+    return map2(ctx, "om_gelu_fwd", x, nullptr, y, n, 0, GeluF{});
+}
+om_status om_gelu_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int64_t n, int accumulate) {
+    OM_REQUIRE(ctx, x || n == 0, "om_gelu_bwd: NULL saved input");
+    return map2(ctx, "om_gelu_bwd", g, x, dx, n, accumulate, GeluGradF{});
+}
+om_status om_add(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n) {
+    OM_REQUIRE(ctx, b || n == 0, "om_add: NULL operand");
+    return map2(ctx, "om_add", a, b, y, n, 0, AddF{});
+}
+om_status om_sub(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n) {
+    OM_REQUIRE(ctx, b || n == 0, "om_sub: NULL operand");
+    return map2(ctx, "om_sub", a, b, y, n, 0, SubF{});
+}
+om_status om_mul(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n) {
+    OM_REQUIRE(ctx, b || n == 0, "om_mul: NULL operand");
+    return map2(ctx, "om_mul", a, b, y, n, 0, MulF{});
+}
+om_status om_axpy(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n) {
+    OM_CHECK_CTX(ctx);
+    if (n <= 0) return OM_OK;
+    OM_REQUIRE(ctx, src && dst, "om_axpy: NULL pointer");
+    hipLaunchKernelGGL(k_axpy, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, alpha, src, dst, n, 0);
+    return OM_LAUNCH_CHECK(ctx, "om_axpy");
+}
+om_status om_scale(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n) {
+    OM_CHECK_CTX(ctx);
+    if (n <= 0) return OM_OK;
+    OM_REQUIRE(ctx, src && dst, "om_scale: NULL pointer");
+    hipLaunchKernelGGL(k_axpy, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, alpha, src, dst, n, 1);
+    return OM_LAUNCH_CHECK(ctx, "om_scale");
+}
+
+om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mean) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && out && n >= 0, "om_sum_all: bad arguments");
+    float *scr;
+    om_status s = om::scratch(ctx, sizeof(double) * kSumBlocks, &scr);
+    if (s) return s;
+    double *part = reinterpret_cast<double *>(scr);
+    int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
+    hipLaunchKernelGGL(k_sum_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, x, n, part);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, out, mean ? (double)n : 0.0);
+    return OM_LAUNCH_CHECK(ctx, "om_sum_all");
+}
+
+om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && db && rows >= 0 && cols > 0, "om_colsum: bad arguments");
+    int rpc = rows <= 32 ? (rows > 0 ? rows : 1) : 32;
+    int chunks = rows > 0 ? (rows + rpc - 1) / rpc : 1;
+    float *scr;
+    om_status s = om::scratch(ctx, sizeof(double) * (uint64_t)chunks * cols, &scr);
+    if (s) return s;
+    double *part = reinterpret_cast<double *>(scr);
+    if (rows == 0) return om_fill(ctx, db, 0.0f, accumulate ? 0 : cols);
+    dim3 g1((cols + kBlock - 1) / kBlock, chunks);
+    hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, ctx->stream, g, rows, cols, rpc, part);
+    hipLaunchKernelGGL(k_colsum_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, part, chunks,
+                       cols, db, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_colsum");
+}
+
+om_status om_mean_axis(om_ctx *ctx, const float *x, float *y, int outer, int n, int inner) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && outer > 0 && n > 0 && inner > 0, "om_mean_axis: bad arguments");
+    if (inner == 1)
+        hipLaunchKernelGGL(k_mean_rows, dim3(om::grid1d((int64_t)outer * 64, kBlock, 1 << 30)), dim3(kBlock), 0,
+                           ctx->stream, x, y, outer, n);
+    else
+        hipLaunchKernelGGL(k_mean_inner, dim3(om::grid1d((int64_t)outer * inner, kBlock, 1 << 30)), dim3(kBlock), 0,
+                           ctx->stream, x, y, outer, n, inner);
+    return OM_LAUNCH_CHECK(ctx, "om_mean_axis");
+}
+
+om_status om_mean_axis_bwd(om_ctx *ctx, const float *g, float *dx, int outer, int n, int inner, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && dx && outer > 0 && n > 0 && inner > 0, "om_mean_axis_bwd: bad arguments");
+    hipLaunchKernelGGL(k_mean_axis_bwd, dim3(ew_grid((int64_t)outer * n * inner)), dim3(kBlock), 0, ctx->stream, g,
+                       dx, outer, n, inner, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_mean_axis_bwd");
+}
+
+om_status om_mean_all_bwd(om_ctx *ctx, const float *g, float *dx, int64_t n, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && dx && n > 0, "om_mean_all_bwd: bad arguments");
+    hipLaunchKernelGGL(k_mean_all_bwd, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, g, dx, n, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_mean_all_bwd");
+}
+
+}  // extern "C"

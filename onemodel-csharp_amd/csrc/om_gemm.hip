@@ -1,0 +1,218 @@
+// Dense fp32 MFMA GEMM (om_gemm), the Linear layer forward/backward built on it, and the split-K reduction.
+#include "om_gemm.hpp"
+
+namespace omg {
+
+template <int BM, int BN, bool TA, bool TB, bool VEC>
+__global__ void __launch_bounds__(NT) k_gemm(Params p) {
+    __shared__ __attribute__((aligned(16))) float As[2 * BK * (BM + PAD)];
+    __shared__ __attribute__((aligned(16))) float Bs[2 * BK * (BN + PAD)];
+    const int tiles_n = (p.n + BN - 1) / BN, tiles_m = (p.m + BM - 1) / BM;
+    int tm, tn, zz;
+    tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
+    if (zz >= p.batch * p.splits) return;
+    const int z = zz / p.splits, split = zz % p.splits;
+    const int outer = z / p.batch_div, inner = z % p.batch_div;
+    const float *A = p.a + outer * p.sa_outer + inner * p.sa_inner;
+    const float *B = p.b + outer * p.sb_outer + inner * p.sb_inner;
+    float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
+    const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = split * p.k_split, kend = min(p.k, kbeg + p.k_split);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
+
+    using LA = typename std::conditional<TA, LoadRContig<BM, VEC>, LoadKContig<BM, VEC>>::type;
+    using LB = typename std::conditional<TB, LoadKContig<BN, VEC>, LoadRContig<BN, VEC>>::type;
+    LA la;
+    LB lb;
+    Tile<BM, BN> t;
+    const int M = p.m, N = p.n;
+    const int64_t lda = p.lda, ldb = p.ldb;
+    run_k<BM, BN>(
+        t, la, lb, [&](LA &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
+        [&](LB &l, int k0) { l.fetch(B, ldb, N, kend, n0, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
+    store_tile<BM, BN>(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
+}
+
+__global__ void k_splitk_reduce(Params p) {
+    int64_t total = (int64_t)p.m * p.n;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
+        int row = (int)(e / p.n), col = (int)(e % p.n);
+        float v = 0.0f;
+        for (int s = 0; s < p.splits; s++) v += p.ws[(int64_t)s * total + e];
+        if (p.alpha != 1.0f) v = v * p.alpha;
+        if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
+        float *dst = p.c + (int64_t)row * p.ldc + col;
+        *dst = p.accumulate ? *dst + v : v;
+    }
+}
+
+template <int BM, int BN, bool TA, bool TB, bool VEC>
+static void launch_t(const Params &p, int batch, hipStream_t st) {
+    int64_t tiles = (int64_t)((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
+    // One linear grid over (z, m-tile, n-tile), n fastest.
+    int64_t total = tiles * batch * p.splits;
+    hipLaunchKernelGGL((k_gemm<BM, BN, TA, TB, VEC>), dim3((unsigned)total), dim3(NT), 0, st, p);
+}
+
+template <int BM, int BN>
+static void launch_bmbn(const Params &p, int batch, bool ta, bool tb, bool vec, hipStream_t st) {
+#define OMG_CASE(TA, TB, V) \
+    if (ta == TA && tb == TB && vec == V) return launch_t<BM, BN, TA, TB, V>(p, batch, st);
+    OMG_CASE(false, false, false)
+    OMG_CASE(false, false, true)
+    OMG_CASE(false, true, false)
+    OMG_CASE(false, true, true)
+    OMG_CASE(true, false, false)
+    OMG_CASE(true, false, true)
+    OMG_CASE(true, true, false)
+    OMG_CASE(true, true, true)
+#undef OMG_CASE
+}
+
+Choice choose(int m, int n, int k, int batch, int cus) {
+    static const int cand[][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
+    Choice c{64, 64, 1, k};
+    if (n <= 32) c = Choice{128, 32, 1, k};
+    else if (m <= 32) c = Choice{32, 128, 1, k};
+    else {
+        for (auto &cd : cand) {
+            int64_t tiles = (int64_t)((m + cd[0] - 1) / cd[0]) * ((n + cd[1] - 1) / cd[1]) * batch;
+            if (tiles >= cus) {
+                c = Choice{cd[0], cd[1], 1, k};
+                return c;
+            }
+        }
+    }
+    // Too few tiles to fill the chip: split K (single product only), deterministic fixed-order reduce afterwards.
+    int64_t tiles = (int64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * batch;
+    if (batch == 1 && k >= 512) {
+        int want = (int)((2 * cus + tiles - 1) / tiles);
+        int maxs = k / 256;
+        int s = want < maxs ? want : maxs;
+        if (s > 1) {
+            int ks = ((k + s - 1) / s + BK - 1) / BK * BK;
+            c.splits = (k + ks - 1) / ks;
+            c.k_split = ks;
+        }
+    }
+    return c;
+}
+
+om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what) {
+    if (p.m <= 0 || p.n <= 0 || batch <= 0) return OM_OK;
+    p.batch = batch;
+    bool vec = ((uintptr_t)p.a % 16 == 0) && ((uintptr_t)p.b % 16 == 0) && p.lda % 4 == 0 && p.ldb % 4 == 0 &&
+               p.sa_outer % 4 == 0 && p.sa_inner % 4 == 0 && p.sb_outer % 4 == 0 && p.sb_inner % 4 == 0;
+    Choice c = p.k > 0 ? choose(p.m, p.n, p.k, batch, ctx->num_cus) : Choice{64, 64, 1, 1};
+    if (p.k <= 0) {  // empty product: C = epilogue(0)
+        c.k_split = 1;
+    }
+    p.splits = c.splits;
+    p.k_split = c.splits > 1 ? c.k_split : (p.k > 0 ? p.k : 1);
+    p.ws = nullptr;
+    p.xcd_remap = 1;
+    if (p.splits > 1) {
+        float *ws;
+        om_status s = om::scratch(ctx, sizeof(float) * (uint64_t)p.splits * p.m * p.n, &ws);
+        if (s) return s;
+        p.ws = ws;
+    }
+    if (c.bm == 128 && c.bn == 128) launch_bmbn<128, 128>(p, batch, ta, tb, vec, ctx->stream);
+    else if (c.bm == 128 && c.bn == 64) launch_bmbn<128, 64>(p, batch, ta, tb, vec, ctx->stream);
+    else if (c.bm == 64 && c.bn == 128) launch_bmbn<64, 128>(p, batch, ta, tb, vec, ctx->stream);
+    else if (c.bm == 128 && c.bn == 32) launch_bmbn<128, 32>(p, batch, ta, tb, vec, ctx->stream);
+    else if (c.bm == 32 && c.bn == 128) launch_bmbn<32, 128>(p, batch, ta, tb, vec, ctx->stream);
+    else launch_bmbn<64, 64>(p, batch, ta, tb, vec, ctx->stream);
+    om_status s = OM_LAUNCH_CHECK(ctx, what);
+    if (s || p.splits <= 1) return s;
+    hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, ctx->stream,
+                       p);
+    return OM_LAUNCH_CHECK(ctx, what);
+}
+
+Params dense_params(int m, int n, int k, const float *a, int64_t lda, const float *b, int64_t ldb, float *c,
+                    int64_t ldc) {
+    Params p{};
+    p.m = m;
+    p.n = n;
+    p.k = k;
+    p.batch_div = 1;
+    p.a = a;
+    p.lda = lda;
+    p.b = b;
+    p.ldb = ldb;
+    p.c = c;
+    p.ldc = ldc;
+    p.alpha = 1.0f;
+    p.splits = 1;
+    return p;
+}
+
+}  // namespace omg
+
+extern "C" {
+
+om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, const float *a, int lda,
+                  const float *b, int ldb, float *c, int ldc, const float *bias, int accumulate,
+                  const om_batch *batch) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, m >= 0 && n >= 0 && k >= 0, "om_gemm: negative size %d x %d x %d", m, n, k);
+    if (m == 0 || n == 0) return OM_OK;
+    OM_REQUIRE(ctx, c && (k == 0 || (a && b)), "om_gemm: NULL operand");
+    OM_REQUIRE(ctx, lda >= (trans_a ? m : k) && ldb >= (trans_b ? k : n) && ldc >= n,
+               "om_gemm: leading dimensions %d/%d/%d too small for %s%s %dx%dx%d", lda, ldb, ldc, trans_a ? "T" : "N",
+               trans_b ? "T" : "N", m, n, k);
+    omg::Params p = omg::dense_params(m, n, k, a, lda, b, ldb, c, ldc);
+    p.bias = bias;
+    p.accumulate = accumulate;
+    int nb = 1;
+    if (batch) {
+        OM_REQUIRE(ctx, batch->batch >= 1 && batch->batch_div >= 1, "om_gemm: bad batch %d / %d", batch->batch,
+                   batch->batch_div);
+        nb = batch->batch;
+        p.batch_div = batch->batch_div;
+        p.sa_outer = batch->sa_outer;
+        p.sa_inner = batch->sa_inner;
+        p.sb_outer = batch->sb_outer;
+        p.sb_inner = batch->sb_inner;
+        p.sc_outer = batch->sc_outer;
+        p.sc_inner = batch->sc_inner;
+    }
+    return omg::launch_dense(ctx, p, trans_a != 0, trans_b != 0, nb, "om_gemm");
+}
+
+om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
+                        int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && y && rows >= 0 && in > 0 && out > 0, "om_linear_fwd: bad arguments");
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
+    p.bias = b;
+    return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd");
+}
+
+om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
+                        int rows, int in, int out, int acc_dx, int acc_dw, int acc_db) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && rows >= 0 && in > 0 && out > 0, "om_linear_bwd: bad arguments");
+    OM_REQUIRE(ctx, (!dx || w) && (!dw || x), "om_linear_bwd: a needed saved tensor is NULL");
+    om_status s = OM_OK;
+    if (dx) {
+        omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dx, in);
+        p.accumulate = acc_dx;
+        s = omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd dx");
+        if (s) return s;
+    }
+    if (dw) {
+        omg::Params p = omg::dense_params(out, in, rows, g, out, x, in, dw, in);
+        p.accumulate = acc_dw;
+        s = omg::launch_dense(ctx, p, true, false, 1, "om_linear_bwd dw");
+        if (s) return s;
+    }
+    if (db) s = om_colsum(ctx, g, db, rows, out, acc_db);
+    return s;
+}
+
+}  // extern "C"

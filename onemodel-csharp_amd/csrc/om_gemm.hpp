@@ -1,0 +1,19 @@
+// Host-side entry points of the MFMA GEMM engine, shared by the dense, attention and convolution translation units.
+#pragma once
+
+#include "om_gemm_core.hpp"
+
+namespace omg {
+
+// Tile shape and K split chosen from the shape and the CU count only (so results never depend on anything else).
+struct Choice {
+    int bm, bn, splits, k_split;
+};
+Choice choose(int m, int n, int k, int batch, int cus);
+// A zeroed Params for a single dense product C[m,n] = A[m,k] B[k,n] with the given leading dimensions.
+Params dense_params(int m, int n, int k, const float *a, int64_t lda, const float *b, int64_t ldb, float *c,
+                    int64_t ldc);
+// Launches a dense (optionally batched) product; adds the split-K reduce when the chooser splits K.
+om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what);
+
+}  // namespace omg

@@ -1,0 +1,247 @@
+// fp32 MFMA GEMM engine for gfx950, shared by the dense products (om_gemm.hip), attention (om_attention.hip) and
+// the implicit-GEMM convolutions (om_conv.hip).
+//
+// Structure: a workgroup of 256 threads (4 wavefronts, 2 x 2) computes a BM x BN tile of C; each wavefront owns a
+// (BM/2) x (BN/2) sub-tile made of 16 x 16 blocks accumulated by v_mfma_f32_16x16x4_f32 (A fragment: lane l holds
+// A[l%16][l/16]; B fragment: lane l holds B[l/16][l%16]; result: lane l holds C[4*(l/16)+r][l%16], r = 0..3).
+// K advances in chunks of BK = 16 staged through LDS, double-buffered: while the MFMAs consume chunk t from one LDS
+// buffer, the global loads of chunk t+1 are in flight in registers and land in the other buffer. LDS holds both
+// operands k-major ([BK][BM+16] and [BK][BN+16]); the +16 pad puts the two k-rows read by one half-wavefront on
+// disjoint banks. Operands are read through "loader" policies, so the same engine runs plain row-major matrices and
+// gathered (im2col) convolution operands without materialising them.
+#pragma once
+
+#include "om_internal.hpp"
+
+namespace omg {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int BK = 16;
+constexpr int NT = 256;
+constexpr int PAD = 16;
+
+// Everything a kernel instance needs; plain data so it can be passed by value.
+struct Params {
+    int m, n, k;
+    int batch;  // independent products (grid covers batch * splits * tiles)
+    // batch item z: outer = z / batch_div, inner = z % batch_div
+    int batch_div;
+    // dense operands
+    const float *a;
+    int64_t lda, sa_outer, sa_inner;
+    const float *b;
+    int64_t ldb, sb_outer, sb_inner;
+    float *c;
+    int64_t ldc, sc_outer, sc_inner;
+    // epilogue: v = acc * alpha (+ mask) (+ bias) ; C = accumulate ? C + v : v
+    float alpha;
+    const float *bias;
+    int bias_per_row;
+    const float *mask;  // additive [Lq, Lk] per batch outer index (attention scores)
+    int64_t mask_outer_stride;
+    int accumulate;
+    // split-K: grid.z = batch * splits; split s covers k in [s*k_split, (s+1)*k_split) and writes its partial sum to
+    // ws + s*m*n (row-major m x n) instead of C; a reduce pass then applies the epilogue.
+    int splits;
+    int k_split;
+    float *ws;
+    // convolution geometry (gather loaders)
+    int cin, h, w, cout, kh, kw, stride, pad, oh, ow;
+    int xcd_remap;
+};
+
+// ------------------------------------------------------------------------------------------------ loaders
+// A loader fills the LDS tile T[BK][ROWS + PAD] (k-major) for k in [k0, k0 + BK) and rows in [r0, r0 + ROWS) of its
+// logical operand (A: rows are m; B: rows are n). `fetch` issues the global loads into registers, `put` writes them
+// to LDS. Out-of-range elements are zero.
+
+// Dense operand whose rows are contiguous along k ("A not transposed" [m][k], or "B transposed" [n][k]).
+template <int ROWS, bool VEC>
+struct LoadKContig {
+    static constexpr int TOT = ROWS * BK / 4;          // float4 per chunk
+    static constexpr int NV = (TOT + NT - 1) / NT;     // float4 per thread
+    float4 v[NV];
+    __device__ __forceinline__ void fetch(const float *base, int64_t ld, int rows, int kend, int r0, int k0) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            int f = threadIdx.x + i * NT;
+            if (TOT % NT != 0 && f >= TOT) break;
+            int r = f / (BK / 4), kq = (f % (BK / 4)) * 4;
+            int gr = r0 + r, gk = k0 + kq;
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (gr < rows) {
+                const float *p = base + (int64_t)gr * ld + gk;
+                if (VEC && gk + 3 < kend) {
+                    t = *reinterpret_cast<const float4 *>(p);
+                } else {
+                    if (gk + 0 < kend) t.x = p[0];
+                    if (gk + 1 < kend) t.y = p[1];
+                    if (gk + 2 < kend) t.z = p[2];
+                    if (gk + 3 < kend) t.w = p[3];
+                }
+            }
+            v[i] = t;
+        }
+    }
+    __device__ __forceinline__ void put(float *T) const {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            int f = threadIdx.x + i * NT;
+            if (TOT % NT != 0 && f >= TOT) break;
+            int r = f / (BK / 4), kq = (f % (BK / 4)) * 4;
+            T[(kq + 0) * (ROWS + PAD) + r] = v[i].x;
+            T[(kq + 1) * (ROWS + PAD) + r] = v[i].y;
+            T[(kq + 2) * (ROWS + PAD) + r] = v[i].z;
+            T[(kq + 3) * (ROWS + PAD) + r] = v[i].w;
+        }
+    }
+};
+
+// Dense operand contiguous along its rows ("A transposed" stored [k][m], or "B not transposed" stored [k][n]).
+template <int ROWS, bool VEC>
+struct LoadRContig {
+    static constexpr int TOT = ROWS * BK / 4;
+    static constexpr int NV = (TOT + NT - 1) / NT;
+    float4 v[NV];
+    __device__ __forceinline__ void fetch(const float *base, int64_t ld, int rows, int kend, int r0, int k0) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            int f = threadIdx.x + i * NT;
+            if (TOT % NT != 0 && f >= TOT) break;
+            int kk = f / (ROWS / 4), rq = (f % (ROWS / 4)) * 4;
+            int gk = k0 + kk, gr = r0 + rq;
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (gk < kend) {
+                const float *p = base + (int64_t)gk * ld + gr;
+                if (VEC && gr + 3 < rows) {
+                    t = *reinterpret_cast<const float4 *>(p);
+                } else {
+                    if (gr + 0 < rows) t.x = p[0];
+                    if (gr + 1 < rows) t.y = p[1];
+                    if (gr + 2 < rows) t.z = p[2];
+                    if (gr + 3 < rows) t.w = p[3];
+                }
+            }
+            v[i] = t;
+        }
+    }
+    __device__ __forceinline__ void put(float *T) const {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            int f = threadIdx.x + i * NT;
+            if (TOT % NT != 0 && f >= TOT) break;
+            int kk = f / (ROWS / 4), rq = (f % (ROWS / 4)) * 4;
+            *reinterpret_cast<float4 *>(&T[kk * (ROWS + PAD) + rq]) = v[i];
+        }
+    }
+};
+
+// ------------------------------------------------------------------------------------------------ engine
+template <int BM, int BN>
+struct Tile {
+    static constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
+    floatx4 acc[TM][TN];
+
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    // One BK chunk from LDS: 4 MFMA k-steps of 4.
+    __device__ __forceinline__ void mma(const float *As, const float *Bs, int wm0, int wn0, int lane) {
+        const int ml = lane & 15, kl = lane >> 4;
+#pragma unroll
+        for (int ks = 0; ks < BK / 4; ks++) {
+            float a[TM], b[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) a[i] = As[(ks * 4 + kl) * (BM + PAD) + wm0 + i * 16 + ml];
+#pragma unroll
+            for (int j = 0; j < TN; j++) b[j] = Bs[(ks * 4 + kl) * (BN + PAD) + wn0 + j * 16 + ml];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+};
+
+// Maps the linear workgroup id so that consecutive tiles of the (z, m, n) walk land on one XCD: the hardware deals
+// workgroups round-robin over the 8 XCDs, each with its own L2, and neighbouring tiles share operand panels.
+__device__ __forceinline__ void tile_coords(const Params &p, int tiles_n, int tiles_m, int &tm, int &tn, int &z) {
+    int total = gridDim.x;
+    int lin = blockIdx.x;
+    if (p.xcd_remap && (total & 7) == 0) {
+        int per = total >> 3;
+        lin = (lin & 7) * per + (lin >> 3);
+    }
+    tn = lin % tiles_n;
+    int rest = lin / tiles_n;
+    tm = rest % tiles_m;
+    z = rest / tiles_m;
+}
+
+// Epilogue for one accumulator tile: writes C (or the split-K partial).
+template <int BM, int BN>
+__device__ __forceinline__ void store_tile(const Params &p, Tile<BM, BN> &t, int m0, int n0, int wm0, int wn0,
+                                           int lane, float *cbase, int64_t ldc, const float *mask, int split) {
+    const int col_l = lane & 15, row_l = (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < Tile<BM, BN>::TM; i++)
+#pragma unroll
+        for (int j = 0; j < Tile<BM, BN>::TN; j++) {
+            int col = n0 + wn0 + j * 16 + col_l;
+            if (col >= p.n) continue;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int row = m0 + wm0 + i * 16 + row_l + r;
+                if (row >= p.m) continue;
+                float v = t.acc[i][j][r];
+                if (p.splits > 1) {
+                    p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
+                    continue;
+                }
+                if (p.alpha != 1.0f) v = v * p.alpha;
+                if (mask) v = v + mask[(int64_t)row * p.n + col];
+                if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
+                float *dst = cbase + (int64_t)row * ldc + col;
+                *dst = p.accumulate ? *dst + v : v;
+            }
+        }
+}
+
+// The main loop, generic over the two loaders. `fa(la, k0)` / `fb(lb, k0)` issue the global loads of a chunk.
+template <int BM, int BN, class LA, class LB, class FA, class FB>
+__device__ __forceinline__ void run_k(Tile<BM, BN> &t, LA &la, LB &lb, FA fa, FB fb, int kbeg, int kend, float *As0,
+                                      float *Bs0, int wm0, int wn0, int lane) {
+    constexpr int ASZ = BK * (BM + PAD), BSZ = BK * (BN + PAD);
+    t.zero();
+    if (kbeg >= kend) return;
+    int nk = (kend - kbeg + BK - 1) / BK;
+    fa(la, kbeg);
+    fb(lb, kbeg);
+    la.put(As0);
+    lb.put(Bs0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        int cur = kt & 1;
+        bool more = kt + 1 < nk;
+        if (more) {
+            fa(la, kbeg + (kt + 1) * BK);
+            fb(lb, kbeg + (kt + 1) * BK);
+        }
+        t.mma(As0 + cur * ASZ, Bs0 + cur * BSZ, wm0, wn0, lane);
+        if (more) {
+            la.put(As0 + (cur ^ 1) * ASZ);
+            lb.put(Bs0 + (cur ^ 1) * BSZ);
+        }
+        __syncthreads();
+    }
+}
+
+// Fixed-order reduction of split-K partials with the full epilogue. One thread per output element.
+__global__ void k_splitk_reduce(Params p);
+
+}  // namespace omg

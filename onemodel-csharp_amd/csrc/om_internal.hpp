@@ -1,0 +1,184 @@
+// Internal definitions shared by the libom_hip.so translation units: the context, the arena, error handling and
+// small device helpers. Everything here is gfx950 (CDNA4): 64-wide wavefronts, fp32 MFMA, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <vector>
+
+#include "../../include/om.h"
+
+struct om_slab {
+    char *base = nullptr;
+    uint64_t size = 0;
+};
+
+struct om_region {
+    std::vector<om_slab> slabs;
+    size_t cur = 0;       // slab being filled
+    uint64_t off = 0;     // bytes used in slabs[cur]
+    uint64_t used = 0;    // bytes handed out in this region since the last reset
+    uint64_t default_slab = 0;
+};
+
+struct om_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    om_region region[2];
+    // Device scratch owned by the context (split-K partials, per-row statistics); grown on demand between steps.
+    float *scratch = nullptr;
+    uint64_t scratch_bytes = 0;
+    int num_cus = 256;
+};
+
+namespace om {
+
+om_status fail(om_ctx *ctx, om_status code, const char *fmt, ...);
+om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
+// Returns device scratch of at least `bytes` (kept by the context; valid until the next call that grows it, which
+// first synchronises the stream so no in-flight kernel still reads the old buffer).
+om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
+
+inline unsigned grid1d(int64_t n, int block, int64_t max_blocks = 1 << 20) {
+    int64_t g = (n + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > max_blocks) g = max_blocks;
+    return (unsigned)g;
+}
+
+}  // namespace om
+
+#define OM_CHECK_CTX(ctx)                     \
+    do {                                      \
+        if (!(ctx)) return OM_E_ARG;          \
+    } while (0)
+#define OM_REQUIRE(ctx, cond, ...)                                   \
+    do {                                                             \
+        if (!(cond)) return om::fail((ctx), OM_E_ARG, __VA_ARGS__);  \
+    } while (0)
+#define OM_LAUNCH_CHECK(ctx, what) om::check_hip((ctx), hipGetLastError(), (what))
+
+// ------------------------------------------------------------------------------------------------ device helpers
+namespace omd {
+
+__device__ __forceinline__ float canon(float x) { return x == x ? x : __int_as_float(0x7FC00000); }
+
+// Wavefront (64 lanes) sum of a double by butterfly shuffles; every lane gets the total. The combine order is fixed
+// (xor 32, 16, ..., 1), so the result depends only on the lane values.
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Block sum of a double over `nw` wavefronts through LDS; all threads get the total (fixed order: wave 0..nw-1).
+template <int NW>
+__device__ __forceinline__ double block_sum(double v, double *sh) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[w] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) t += sh[i];
+    return t;
+}
+
+// The reference's fp32 polynomials (Transcendental.cs:39-263), restated with one IEEE rounding per operation; the
+// library is built with -ffp-contract=off so no multiply-add is fused behind our back.
+__device__ __forceinline__ float exp_poly(float x) {
+    const float magic = 12582912.0f;
+    float t = x * 1.44269502f + magic;
+    float nf = t - magic;
+    float r = (x - nf * 0.693145751953125f) - nf * 1.4286068e-6f;
+    float q = 0.0013814613f;
+    q = 0.00836871f + q * r;
+    q = 0.04166839f + q * r;
+    q = 0.16666521f + q * r;
+    q = 0.49999994f + q * r;
+    float p = 1.0f + (r + (r * r) * q);
+    int n = __float_as_int(t) - __float_as_int(magic);
+    int a = n >> 1, b = n - a;
+    float res = (p * __int_as_float((a + 127) << 23)) * __int_as_float((b + 127) << 23);
+    if (x > 88.72283172607422f) res = __int_as_float(0x7F800000);
+    if (x < -103.97207641601562f) res = 0.0f;
+    return canon(x == x ? res : x);
+}
+__device__ __forceinline__ float exp_nonpos(float x) {
+    const float magic = 12582912.0f;
+    float t = x * 1.44269502f + magic;
+    float nf = t - magic;
+    float r = (x - nf * 0.693145751953125f) - nf * 1.4286068e-6f;
+    float q = 0.0013814613f;
+    q = 0.00836871f + q * r;
+    q = 0.04166839f + q * r;
+    q = 0.16666521f + q * r;
+    q = 0.49999994f + q * r;
+    float p = 1.0f + (r + (r * r) * q);
+    int n = __float_as_int(t) - __float_as_int(magic);
+    float res = p * __int_as_float((n + 127) << 23);
+    if (x < -87.33654f) res = 0.0f;
+    return x == x ? res : __int_as_float(0x7FC00000);
+}
+__device__ __forceinline__ void erf_parts(float x, float &erf, float &ope) {
+    unsigned sign = __float_as_uint(x) & 0x80000000u;
+    float ax = __uint_as_float(__float_as_uint(x) & 0x7FFFFFFFu);
+    float z = ax * ax;
+    float p = -0.0007692853f;
+    p = 0.0052003083f + p * z;
+    p = -0.02686312f + p * z;
+    p = 0.11283774f + p * z;
+    p = -0.37612638f + p * z;
+    p = 1.1283792f + p * z;
+    float small = ax * p;
+    float t = 1.0f / ax;
+    float s = t - 1.0f;
+    float g = -0.00057763467f;
+    g = 0.0017893383f + g * s;
+    g = -0.00010074016f + g * s;
+    g = -0.004373198f + g * s;
+    g = 0.0034639547f + g * s;
+    g = 0.0015023724f + g * s;
+    g = -0.0009413088f + g * s;
+    g = -0.0018891813f + g * s;
+    g = -0.0002586738f + g * s;
+    g = 0.0052144383f + g * s;
+    g = -0.0103428485f + g * s;
+    g = 0.015788378f + g * s;
+    g = -0.018338649f + g * s;
+    g = 0.008167262f + g * s;
+    g = 0.035529688f + g * s;
+    g = -0.1543716f + g * s;
+    g = 0.42758358f + g * s;
+    float split = ax * 4097.0f;
+    float axHi = split - (split - ax);
+    float axLo = ax - axHi;
+    float zLo = ((axHi * axHi - z) + 2.0f * (axHi * axLo)) + axLo * axLo;
+    if (!(ax < 64.0f)) zLo = 0.0f;
+    float expNegZ = exp_poly(0.0f - z) * (1.0f - zLo);
+    float erfc = expNegZ * (t * g);
+    bool isSmall = ax < 0.5f;
+    float erfAbs = isSmall ? small : 1.0f - erfc;
+    float erfSigned = __uint_as_float(__float_as_uint(erfAbs) | sign);
+    float opeLarge = x < 0.0f ? erfc : 2.0f - erfc;
+    float opeSmall = 1.0f + __uint_as_float(__float_as_uint(small) | sign);
+    bool ok = x == x;
+    erf = canon(ok ? erfSigned : x);
+    ope = canon(ok ? (isSmall ? opeSmall : opeLarge) : x);
+}
+
+}  // namespace omd

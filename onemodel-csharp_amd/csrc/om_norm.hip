@@ -1,0 +1,453 @@
+// Row kernels: LayerNorm forward/backward, softmax and log-softmax forward/backward, NLL and the fused softmax
+// cross-entropy gradient, and the attention score-gradient row pass. All HBM-bound: rows are read with coalesced
+// loads, reductions stay in registers and wavefront shuffles, column sums go through LDS and a fixed-order second
+// pass.
+#include "om_internal.hpp"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// The reference's canonical 16-partial sum (RowReduce.Sum16, Softmax.cs:139-179) over one row held by 16 lanes:
+// lane t accumulates elements j = t, t+16, ... in increasing j; the halving combine p[t]+p[t+8], +4, +2, +1 is done
+// with shuffles inside the 16-lane group, so the bits equal the reference's at every lane width.
+__device__ __forceinline__ float sum16_combine(float p) {
+    p = p + __shfl_down(p, 8, 16);
+    p = p + __shfl_down(p, 4, 16);
+    p = p + __shfl_down(p, 2, 16);
+    p = p + __shfl_down(p, 1, 16);
+    return __shfl(p, 0, 16);
+}
+// Row maximum ignoring NaN (RowReduce.Max, Softmax.cs:181-212); max is exact, so the order does not matter.
+__device__ __forceinline__ float max16(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+        float w = __shfl_xor(v, o, 16);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// LayerNorm forward: one row per 16-lane group (4 rows per wavefront). NormKernels.Rows (NormKernels.cs:79-127):
+// mean = Sum16(x)/n, ssq = Sum16((x-mean)^2), inv = 1/sqrt(ssq/n + eps), y = (((x-mean)*inv)*gamma)+beta.
+__global__ void __launch_bounds__(kBlock) k_ln_fwd(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                   const float *__restrict__ beta, float *__restrict__ y,
+                                                   float *__restrict__ mean_out, float *__restrict__ rstd_out,
+                                                   int rows, int cols, float eps) {
+    int row = (blockIdx.x * kBlock + threadIdx.x) >> 4;
+    int t = threadIdx.x & 15;
+    if (row >= rows) return;  // whole 16-lane groups leave together
+    const float *xr = x + (int64_t)row * cols;
+    float *yr = y + (int64_t)row * cols;
+    float n = (float)cols;
+    float p = 0.0f;
+    for (int j = t; j < cols; j += 16) p += xr[j];
+    float mean = sum16_combine(p) / n;
+    p = 0.0f;
+    for (int j = t; j < cols; j += 16) {
+        float d = xr[j] - mean;
+        p += d * d;
+    }
+    float ssq = sum16_combine(p);
+    float inv = 1.0f / sqrtf(ssq / n + eps);
+    if (t == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = inv;
+    }
+    for (int j = t; j < cols; j += 16) yr[j] = omd::canon(((xr[j] - mean) * inv) * gamma[j] + beta[j]);
+}
+
+// LayerNorm backward (BackwardNn.cs:170-223), cols <= 64*kMaxPer: a wavefront per row, a block per chunk of rows.
+// dx is written per row; the dgamma/dbeta column contributions are kept per lane in double and summed over the
+// block's waves in LDS (fixed order), giving partial[chunk][col] for the second pass.
+constexpr int kMaxPer = 16;
+__global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, const float *__restrict__ x,
+                                                   const float *__restrict__ gamma, const float *__restrict__ mean,
+                                                   const float *__restrict__ rstd, float *__restrict__ dx,
+                                                   double *__restrict__ part_g, double *__restrict__ part_b, int rows,
+                                                   int cols, int rows_per_chunk, int acc_dx) {
+    __shared__ double lds[kBlock / 64][64 * kMaxPer];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
+    const int per = (cols + 63) >> 6;
+    double pg[kMaxPer], pb[kMaxPer];
+#pragma unroll
+    for (int i = 0; i < kMaxPer; i++) pg[i] = pb[i] = 0.0;
+    for (int r = r0 + w; r < r1; r += kBlock / 64) {
+        const float *xr = x + (int64_t)r * cols;
+        const float *gr = g + (int64_t)r * cols;
+        float m = mean[r], s = rstd[r];
+        double sum1 = 0.0, sum2 = 0.0;
+        float xh[kMaxPer], gv[kMaxPer];
+#pragma unroll
+        for (int i = 0; i < kMaxPer; i++) {
+            int j = lane + 64 * i;
+            xh[i] = 0.0f;
+            gv[i] = 0.0f;
+            if (i < per && j < cols) {
+                float xhat = (xr[j] - m) * s;
+                float gg = gr[j];
+                float dxhat = gg * gamma[j];
+                sum1 += (double)dxhat;
+                sum2 += (double)(dxhat * xhat);
+                pg[i] += (double)(gg * xhat);
+                pb[i] += (double)gg;
+                xh[i] = xhat;
+                gv[i] = gg;
+            }
+        }
+        sum1 = omd::wave_sum(sum1);
+        sum2 = omd::wave_sum(sum2);
+        if (dx) {
+            float m1 = (float)(sum1 / cols), m2 = (float)(sum2 / cols);
+            float *dr = dx + (int64_t)r * cols;
+#pragma unroll
+            for (int i = 0; i < kMaxPer; i++) {
+                int j = lane + 64 * i;
+                if (i < per && j < cols) {
+                    float v = s * (((gv[i] * gamma[j]) - m1) - (xh[i] * m2));
+                    dr[j] = acc_dx ? dr[j] + v : v;
+                }
+            }
+        }
+    }
+    if (!part_g && !part_b) return;
+    for (int pass = 0; pass < 2; pass++) {
+        double *part = pass == 0 ? part_g : part_b;
+        if (!part) continue;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kMaxPer; i++)
+            if (i < per) lds[w][lane + 64 * i] = pass == 0 ? pg[i] : pb[i];
+        __syncthreads();
+        for (int j = threadIdx.x; j < cols; j += kBlock) {
+            double t = 0.0;
+#pragma unroll
+            for (int q = 0; q < kBlock / 64; q++) t += lds[q][j];
+            part[(int64_t)blockIdx.x * cols + j] = t;
+        }
+    }
+}
+// Generic (any width) LayerNorm backward for dx only: a wavefront per row, columns strided.
+__global__ void __launch_bounds__(kBlock) k_ln_bwd_dx_wide(const float *__restrict__ g, const float *__restrict__ x,
+                                                           const float *__restrict__ gamma,
+                                                           const float *__restrict__ mean,
+                                                           const float *__restrict__ rstd, float *__restrict__ dx,
+                                                           int rows, int cols, int acc_dx) {
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *xr = x + (int64_t)r * cols, *gr = g + (int64_t)r * cols;
+    float m = mean[r], s = rstd[r];
+    double sum1 = 0.0, sum2 = 0.0;
+    for (int j = lane; j < cols; j += 64) {
+        float xhat = (xr[j] - m) * s, dxhat = gr[j] * gamma[j];
+        sum1 += (double)dxhat;
+        sum2 += (double)(dxhat * xhat);
+    }
+    sum1 = omd::wave_sum(sum1);
+    sum2 = omd::wave_sum(sum2);
+    float m1 = (float)(sum1 / cols), m2 = (float)(sum2 / cols);
+    float *dr = dx + (int64_t)r * cols;
+    for (int j = lane; j < cols; j += 64) {
+        float xhat = (xr[j] - m) * s;
+        float v = s * (((gr[j] * gamma[j]) - m1) - (xhat * m2));
+        dr[j] = acc_dx ? dr[j] + v : v;
+    }
+}
+// Generic column partials of g*xhat and g for wide rows: one thread per column per chunk of rows.
+__global__ void __launch_bounds__(kBlock) k_ln_param_partial_wide(const float *__restrict__ g,
+                                                                  const float *__restrict__ x,
+                                                                  const float *__restrict__ mean,
+                                                                  const float *__restrict__ rstd,
+                                                                  double *__restrict__ part_g,
+                                                                  double *__restrict__ part_b, int rows, int cols,
+                                                                  int rows_per_chunk) {
+    int col = blockIdx.x * kBlock + threadIdx.x;
+    if (col >= cols) return;
+    int r0 = blockIdx.y * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
+    double a = 0.0, b = 0.0;
+    for (int r = r0; r < r1; r++) {
+        float gg = g[(int64_t)r * cols + col];
+        float xhat = (x[(int64_t)r * cols + col] - mean[r]) * rstd[r];
+        a += (double)(gg * xhat);
+        b += (double)gg;
+    }
+    if (part_g) part_g[(int64_t)blockIdx.y * cols + col] = a;
+    if (part_b) part_b[(int64_t)blockIdx.y * cols + col] = b;
+}
+__global__ void __launch_bounds__(kBlock) k_chunk_final(const double *__restrict__ part, int chunks, int cols,
+                                                        float *__restrict__ out, int acc) {
+    int col = blockIdx.x * kBlock + threadIdx.x;
+    if (col >= cols) return;
+    double s = 0.0;
+    for (int c = 0; c < chunks; c++) s += part[(int64_t)c * cols + col];
+    float v = (float)s;
+    out[col] = acc ? out[col] + v : v;
+}
+
+// Softmax rows, exact flavour (Softmax.cs:70-133): max, e = expNonPositive(x - max), l = Sum16(e), y = e / l.
+__global__ void __launch_bounds__(kBlock) k_softmax_rows(const float *x, float *y, int rows, int cols) {
+    int row = (blockIdx.x * kBlock + threadIdx.x) >> 4;
+    int t = threadIdx.x & 15;
+    if (row >= rows) return;
+    const float *xr = x + (int64_t)row * cols;
+    float *yr = y + (int64_t)row * cols;
+    float mx = -__int_as_float(0x7F800000);
+    for (int j = t; j < cols; j += 16) {
+        float v = xr[j];
+        mx = v > mx ? v : mx;
+    }
+    mx = max16(mx);
+    float p = 0.0f;
+    for (int j = t; j < cols; j += 16) {
+        float e = omd::exp_nonpos(xr[j] - mx);
+        yr[j] = e;
+        p += e;
+    }
+    float l = sum16_combine(p);
+    for (int j = t; j < cols; j += 16) yr[j] = omd::canon(yr[j] / l);
+}
+
+// y * (g - (float)sum(double)(g*y)) per row (BackwardNn.cs:26-52); with `scale` (attention, BackwardNn.cs:674-688)
+// the result is multiplied by scale. Wavefront per row; in place on g allowed.
+__global__ void __launch_bounds__(kBlock) k_softmax_bwd_rows(const float *g, const float *__restrict__ y, float *dx,
+                                                             int rows, int cols, float scale, int use_scale,
+                                                             int acc) {
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *gr = g + (int64_t)r * cols, *yr = y + (int64_t)r * cols;
+    float *dr = dx + (int64_t)r * cols;
+    double dot = 0.0;
+    for (int j = lane; j < cols; j += 64) dot += (double)(gr[j] * yr[j]);
+    dot = omd::wave_sum(dot);
+    float df = (float)dot;
+    for (int j = lane; j < cols; j += 64) {
+        float v = yr[j] * (gr[j] - df);
+        if (use_scale) v = v * scale;
+        dr[j] = acc ? dr[j] + v : v;
+    }
+}
+
+// LogSoftmax rows (Ops.Layers.cs:47-96): max, double sum of exp(x - max), lse = max + log((float)sum).
+__global__ void __launch_bounds__(kBlock) k_logsoftmax_rows(const float *__restrict__ x, float *__restrict__ y,
+                                                            int rows, int cols) {
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *xr = x + (int64_t)r * cols;
+    float mx = -__int_as_float(0x7F800000);
+    for (int j = lane; j < cols; j += 64) mx = xr[j] > mx ? xr[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float w = __shfl_xor(mx, o, 64);
+        mx = w > mx ? w : mx;
+    }
+    double sum = 0.0;
+    for (int j = lane; j < cols; j += 64) sum += (double)expf(xr[j] - mx);
+    sum = omd::wave_sum(sum);
+    float lse = mx + logf((float)sum);
+    for (int j = lane; j < cols; j += 64) y[(int64_t)r * cols + j] = xr[j] - lse;
+}
+// LogSoftmax backward (BackwardNn.cs:54-80): dx = g - exp(y) * (float)sum(double) g.
+__global__ void __launch_bounds__(kBlock) k_logsoftmax_bwd_rows(const float *__restrict__ g,
+                                                                const float *__restrict__ y, float *__restrict__ dx,
+                                                                int rows, int cols, int acc) {
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *gr = g + (int64_t)r * cols, *yr = y + (int64_t)r * cols;
+    double sum = 0.0;
+    for (int j = lane; j < cols; j += 64) sum += (double)gr[j];
+    float s = (float)omd::wave_sum(sum);
+    for (int j = lane; j < cols; j += 64) {
+        float v = gr[j] - expf(yr[j]) * s;
+        float *d = dx + (int64_t)r * cols + j;
+        *d = acc ? *d + v : v;
+    }
+}
+
+// NllLoss forward (Ops.Layers.cs:644-699): one block; double sum of -logp[i, t_i] over counted rows; the first
+// out-of-range row (smallest index) is reported.
+__global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ logp, const int32_t *__restrict__ tg,
+                                                    float *__restrict__ loss, int32_t *__restrict__ bad, int rows,
+                                                    int cols, int mean, int ignore) {
+    __shared__ double sh[kBlock / 64];
+    __shared__ int shbad;
+    if (threadIdx.x == 0) shbad = 0x7FFFFFFF;
+    __syncthreads();
+    double acc = 0.0;
+    double cnt = 0.0;
+    for (int i = threadIdx.x; i < rows; i += kBlock) {
+        int t = tg[i];
+        if (t == ignore) continue;
+        if ((unsigned)t >= (unsigned)cols) {
+            atomicMin(&shbad, i);
+            continue;
+        }
+        acc -= (double)logp[(int64_t)i * cols + t];
+        cnt += 1.0;
+    }
+    double total = omd::block_sum<kBlock / 64>(acc, sh);
+    double count = omd::block_sum<kBlock / 64>(cnt, sh);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int b = shbad == 0x7FFFFFFF ? -1 : shbad;
+        if (bad) bad[0] = b;
+        loss[0] = b >= 0 ? __int_as_float(0x7FC00000)
+                         : (float)(mean ? total / (count > 1.0 ? count : 1.0) : total);
+    }
+}
+
+// Fused NllBackward + LogSoftmax backward (BackwardNn.cs:54-80, 602-632). scale = g/max(1,count) (or g); the NLL
+// gradient d has -scale at the target; its double row sum is s = -scale (0 for an ignored row); dx = d - exp(y)*s.
+__global__ void __launch_bounds__(kBlock) k_xent_count(const int32_t *__restrict__ tg, int rows, int ignore,
+                                                       int *__restrict__ count) {
+    __shared__ double sh[kBlock / 64];
+    double c = 0.0;
+    for (int i = threadIdx.x; i < rows; i += kBlock) c += tg[i] != ignore ? 1.0 : 0.0;
+    double t = omd::block_sum<kBlock / 64>(c, sh);
+    if (threadIdx.x == 0) count[0] = (int)t;
+}
+__global__ void __launch_bounds__(kBlock) k_xent_bwd(const float *__restrict__ gs, const int *__restrict__ count,
+                                                     const float *__restrict__ y, const int32_t *__restrict__ tg,
+                                                     float *__restrict__ dx, int rows, int cols, int mean, int ignore,
+                                                     int acc) {
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float g = gs[0];
+    int c = count[0];
+    float scale = mean ? g / (float)(c > 1 ? c : 1) : g;
+    int t = tg[r];
+    bool counted = t != ignore;
+    float s = counted ? -scale : 0.0f;
+    for (int j = lane; j < cols; j += 64) {
+        float d = (counted && j == t) ? -scale : 0.0f;
+        float v = d - expf(y[(int64_t)r * cols + j]) * s;
+        float *o = dx + (int64_t)r * cols + j;
+        *o = acc ? *o + v : v;
+    }
+}
+
+inline unsigned rows_grid(int rows, int lanes_per_row) {
+    return om::grid1d((int64_t)rows * lanes_per_row, kBlock, 1 << 30);
+}
+
+}  // namespace
+
+extern "C" {
+
+om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, const float *beta, float *y, float *mean,
+                           float *rstd, int rows, int cols, float eps) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && gamma && beta && y && rows >= 0 && cols > 0, "om_layernorm_fwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    hipLaunchKernelGGL(k_ln_fwd, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma, beta, y, mean,
+                       rstd, rows, cols, eps);
+    return OM_LAUNCH_CHECK(ctx, "om_layernorm_fwd");
+}
+
+om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                           const float *rstd, float *dx, float *dgamma, float *dbeta, int rows, int cols, int acc_dx,
+                           int acc_params) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
+    const int rpc = 32;
+    int chunks = (rows + rpc - 1) / rpc;
+    bool params = dgamma || dbeta;
+    double *pg = nullptr, *pb = nullptr;
+    if (params) {
+        float *scr;
+        om_status s = om::scratch(ctx, sizeof(double) * 2ull * chunks * cols, &scr);
+        if (s) return s;
+        pg = dgamma ? reinterpret_cast<double *>(scr) : nullptr;
+        pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
+    }
+    if (cols <= 64 * kMaxPer) {
+        hipLaunchKernelGGL(k_ln_bwd, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, pg, pb,
+                           rows, cols, rpc, acc_dx);
+    } else {
+        if (dx)
+            hipLaunchKernelGGL(k_ln_bwd_dx_wide, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g, x, gamma,
+                               mean, rstd, dx, rows, cols, acc_dx);
+        if (params)
+            hipLaunchKernelGGL(k_ln_param_partial_wide, dim3((cols + kBlock - 1) / kBlock, chunks), dim3(kBlock), 0,
+                               ctx->stream, g, x, mean, rstd, pg, pb, rows, cols, rpc);
+    }
+    if (dgamma)
+        hipLaunchKernelGGL(k_chunk_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, pg, chunks,
+                           cols, dgamma, acc_params);
+    if (dbeta)
+        hipLaunchKernelGGL(k_chunk_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, pb, chunks,
+                           cols, dbeta, acc_params);
+    return OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
+}
+
+om_status om_softmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && rows >= 0 && cols > 0, "om_softmax_fwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    hipLaunchKernelGGL(k_softmax_rows, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, y, rows, cols);
+    return OM_LAUNCH_CHECK(ctx, "om_softmax_fwd");
+}
+
+om_status om_softmax_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int rows, int cols, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && y && dx && rows >= 0 && cols > 0, "om_softmax_bwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    hipLaunchKernelGGL(k_softmax_bwd_rows, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g, y, dx, rows,
+                       cols, 1.0f, 0, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_softmax_bwd");
+}
+
+om_status om_logsoftmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && rows >= 0 && cols > 0, "om_logsoftmax_fwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    hipLaunchKernelGGL(k_logsoftmax_rows, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, x, y, rows, cols);
+    return OM_LAUNCH_CHECK(ctx, "om_logsoftmax_fwd");
+}
+
+om_status om_logsoftmax_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int rows, int cols,
+                            int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && y && dx && rows >= 0 && cols > 0, "om_logsoftmax_bwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    hipLaunchKernelGGL(k_logsoftmax_bwd_rows, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g, y, dx, rows,
+                       cols, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_logsoftmax_bwd");
+}
+
+om_status om_nll_fwd(om_ctx *ctx, const float *logp, const int32_t *target, float *loss, int32_t *bad_row, int rows,
+                     int cols, int mean, int ignore_index) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, logp && target && loss && rows >= 0 && cols > 0, "om_nll_fwd: bad arguments");
+    hipLaunchKernelGGL(k_nll_fwd, dim3(1), dim3(kBlock), 0, ctx->stream, logp, target, loss, bad_row, rows, cols, mean,
+                       ignore_index);
+    return OM_LAUNCH_CHECK(ctx, "om_nll_fwd");
+}
+
+om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,
+                      int rows, int cols, int mean, int ignore_index, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g_scalar && logp && target && dlogits && rows >= 0 && cols > 0, "om_xent_bwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    float *scr;
+    om_status s = om::scratch(ctx, 256, &scr);
+    if (s) return s;
+    int *count = reinterpret_cast<int *>(scr);
+    hipLaunchKernelGGL(k_xent_count, dim3(1), dim3(kBlock), 0, ctx->stream, target, rows, ignore_index, count);
+    hipLaunchKernelGGL(k_xent_bwd, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g_scalar, count, logp,
+                       target, dlogits, rows, cols, mean, ignore_index, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_xent_bwd");
+}
+
+}  // extern "C"
+
+// Used by the attention backward (om_attention.hip): ds = (p * (dp - rowsum(dp*p))) * scale, in place on dp.
+om_status om_internal_attn_ds(om_ctx *ctx, float *dp, const float *p, int rows, int cols, float scale) {
+    hipLaunchKernelGGL(k_softmax_bwd_rows, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, dp, p, dp, rows,
+                       cols, scale, 1, 0);
+    return OM_LAUNCH_CHECK(ctx, "attention ds");
+}
+om_status om_internal_softmax_rows(om_ctx *ctx, float *x, int rows, int cols) {
+    hipLaunchKernelGGL(k_softmax_rows, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, x, rows, cols);
+    return OM_LAUNCH_CHECK(ctx, "attention softmax");
+}

@@ -1,0 +1,413 @@
+"""Kernel-level parity of lib/libom_hip.so against the CPU oracle (oracle/om_oracle.c), on the GPU.
+
+Bars: floating-point results within 1e-5 scaled error (max|a-b|/max|ref|, the
+reference's metric, AutogradModelTests.cs:20-30); integer work (pool indices) and the optimizer update bit-exact;
+kernels that restate the reference's fixed-order arithmetic (LayerNorm forward, softmax rows, GELU, CTC) are checked
+bit-for-bit as well.
+"""
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+from conftest import scaled
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from gpu_util import Dev
+    d = Dev()
+    yield d
+    d.ctx.close()
+
+
+@pytest.fixture(scope="module")
+def T():
+    from oracle import tape
+    return tape
+
+
+def rnd(rng, *shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+
+# ------------------------------------------------------------------------------------------------ GEMM
+def oracle_gemm(T, ta, tb, A, B, m, n, k):
+    Cm = np.empty((m, n), np.float32)
+    T.lib().or_gemm(ta, tb, m, n, k, T.fp(A), A.shape[1], T.fp(B), B.shape[1], T.fp(Cm), n, 0)
+    return Cm
+
+
+def test_mfma_fragment_layout(dev):
+    """One 16x16x4 product with distinct small integers: exact in fp32, so any lane-layout mistake shows."""
+    A = np.arange(64, dtype=np.float32).reshape(16, 4) - 20
+    B = (np.arange(64, dtype=np.float32).reshape(4, 16) % 7) - 3
+    a, b, c = dev.put(A), dev.put(B), dev.empty((16, 16))
+    dev.call("om_gemm", 0, 0, 16, 16, 4, a, 4, b, 16, c, 16, None, 0, None)
+    assert np.array_equal(dev.get(c), A @ B)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,n,k", [(64, 64, 64), (37, 53, 29), (256, 384, 384), (5, 300, 1000), (384, 384, 4096),
+                                   (130, 10, 257)])
+def test_gemm_parity(dev, T, ta, tb, m, n, k):
+    rng = np.random.default_rng(m * 1000 + n + k)
+    A = rnd(rng, *((k, m) if ta else (m, k)))
+    B = rnd(rng, *((n, k) if tb else (k, n)))
+    ref = oracle_gemm(T, ta, tb, A, B, m, n, k)
+    a, b, c = dev.put(A), dev.put(B), dev.empty((m, n))
+    dev.call("om_gemm", ta, tb, m, n, k, a, A.shape[1], b, B.shape[1], c, n, None, 0, None)
+    got = dev.get(c)
+    assert scaled(got, ref) <= TOL
+    # and the GPU product obeys the same sequential-accumulation bound as the CPU one
+    A64 = (A.T if ta else A).astype(np.float64)
+    B64 = (B.T if tb else B).astype(np.float64)
+    bound = k * 2.0 ** -24 * (np.abs(A64) @ np.abs(B64)) + 1e-30
+    assert np.all(np.abs(got - A64 @ B64) <= bound)
+
+
+def test_gemm_accumulate_bias_and_batch(dev, T):
+    rng = np.random.default_rng(7)
+    m, n, k, H, L = 24, 16, 32, 3, 24
+    # A in [B, L, H, D] head-interleaved layout, batch item z = b*H + h
+    Bsz = 2
+    Q = rnd(rng, Bsz, L, H, k)
+    Kt = rnd(rng, Bsz, L, H, n * 0 + k)
+    base = rnd(rng, Bsz * H, L, L)
+    q, kk, c = dev.put(Q), dev.put(Kt), dev.put(base)
+    pkg = dev.pkg
+    bt = pkg.om_batch(Bsz * H, H, L * H * k, k, L * H * k, k, H * L * L, L * L)
+    dev.call("om_gemm", 0, 1, L, L, k, q, H * k, kk, H * k, c, L, None, 1, C.byref(bt))
+    got = dev.get(c)
+    for b in range(Bsz):
+        for h in range(H):
+            ref = oracle_gemm(T, 0, 1, np.ascontiguousarray(Q[b, :, h]), np.ascontiguousarray(Kt[b, :, h]), L, L, k)
+            assert scaled(got[b * H + h], base[b * H + h] + ref) <= TOL
+    bias = rnd(rng, n)
+    A, Bm = rnd(rng, m, k), rnd(rng, k, n)
+    a, b2, c2, bb = dev.put(A), dev.put(Bm), dev.empty((m, n)), dev.put(bias)
+    dev.call("om_gemm", 0, 0, m, n, k, a, k, b2, n, c2, n, bb, 0, None)
+    assert scaled(dev.get(c2), oracle_gemm(T, 0, 0, A, Bm, m, n, k) + bias) <= TOL
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    a = dev.empty((4, 4))
+    assert dev.status("om_gemm", 0, 0, 4, 4, 4, a, 2, a, 4, a, 4, None, 0, None) == 1
+    assert b"leading dimensions" in dev.ctx.L.om_last_error(dev.ctx.h)
+
+
+# ------------------------------------------------------------------------------------------------ Linear
+@pytest.mark.parametrize("rows,inf,outf", [(64, 784, 256), (64, 256, 10), (4096, 384, 1536), (300, 37, 9)])
+def test_linear_fwd_bwd(dev, T, rows, inf, outf):
+    rng = np.random.default_rng(rows + inf + outf)
+    x, w, b, g = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf), rnd(rng, rows, outf)
+    y_ref = np.empty((rows, outf), np.float32)
+    T.lib().or_linear_fwd(T.fp(x), T.fp(w), T.fp(b), T.fp(y_ref), rows, inf, outf)
+    dx_r, dw_r, db_r = np.empty_like(x), np.empty_like(w), np.empty_like(b)
+    T.lib().or_linear_bwd(T.fp(g), T.fp(x), T.fp(w), T.fp(dx_r), T.fp(dw_r), T.fp(db_r), rows, inf, outf)
+    X, W, Bb, G = dev.put(x), dev.put(w), dev.put(b), dev.put(g)
+    Y, DX, DW, DB = dev.empty((rows, outf)), dev.empty(x.shape), dev.empty(w.shape), dev.empty(b.shape)
+    dev.call("om_linear_fwd", X, W, Bb, Y, rows, inf, outf)
+    dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 0, 0, 0)
+    assert scaled(dev.get(Y), y_ref) <= TOL
+    assert scaled(dev.get(DX), dx_r) <= TOL
+    assert scaled(dev.get(DW), dw_r) <= TOL
+    assert scaled(dev.get(DB), db_r) <= 1e-7  # fp64 column sums: equal after rounding
+    # accumulate into existing leaves
+    dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 1, 1, 1)
+    assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
+    assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
+
+
+# ------------------------------------------------------------------------------------------------ element-wise
+def test_relu_gelu_bit_exact(dev, T):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([rnd(rng, 100003, scale=3.0), np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -7.0, 6.0],
+                                                               np.float32)])
+    g = rnd(rng, x.size)
+    n = x.size
+    X, G, Y, D = dev.put(x), dev.put(g), dev.empty(x.shape), dev.empty(x.shape)
+    ry, rd = np.empty_like(x), np.empty_like(x)
+    T.lib().or_relu_fwd(T.fp(x), T.fp(ry), C.c_int64(n))
+    dev.call("om_relu_fwd", X, Y, n)
+    assert np.array_equal(dev.get(Y).view(np.uint32), ry.view(np.uint32))
+    T.lib().or_relu_bwd(T.fp(g), T.fp(ry), T.fp(rd), C.c_int64(n))
+    dev.call("om_relu_bwd", G, Y, D, n, 0)
+    assert np.array_equal(dev.get(D).view(np.uint32), rd.view(np.uint32))
+    T.lib().or_gelu_fwd(T.fp(x), T.fp(ry), C.c_int64(n))
+    dev.call("om_gelu_fwd", X, Y, n)
+    assert np.array_equal(dev.get(Y).view(np.uint32), ry.view(np.uint32))
+    T.lib().or_gelu_bwd(T.fp(g), T.fp(x), T.fp(rd), C.c_int64(n))
+    dev.call("om_gelu_bwd", G, X, D, n, 0)
+    assert np.array_equal(dev.get(D).view(np.uint32), rd.view(np.uint32))
+
+
+def test_add_sub_mul_axpy_mean(dev, T):
+    rng = np.random.default_rng(4)
+    a, b = rnd(rng, 1001), rnd(rng, 1001)
+    A, B, Y = dev.put(a), dev.put(b), dev.empty((1001,))
+    for name, f in (("om_add", np.add), ("om_sub", np.subtract), ("om_mul", np.multiply)):
+        dev.call(name, A, B, Y, 1001)
+        assert np.array_equal(dev.get(Y), f(a, b))
+    dev.call("om_axpy", C.c_float(-1.0), A, Y, 1001)
+    assert np.array_equal(dev.get(Y), a * b - a)
+    x = rnd(rng, 3, 7, 5)
+    X, M = dev.put(x), dev.empty((3, 5))
+    dev.call("om_mean_axis", X, M, 3, 7, 5)
+    ref = np.empty((3, 5), np.float32)
+    T.lib().or_mean_axis(T.fp(x), T.fp(ref), 3, 7, 5)
+    assert np.array_equal(dev.get(M), ref)
+    x2 = rnd(rng, 40, 3136)
+    X2, M2 = dev.put(x2), dev.empty((40,))
+    dev.call("om_mean_axis", X2, M2, 40, 3136, 1)
+    ref2 = np.empty(40, np.float32)
+    T.lib().or_mean_axis(T.fp(x2), T.fp(ref2), 40, 3136, 1)
+    assert scaled(dev.get(M2), ref2) <= 1e-7
+    S = dev.empty((1,))
+    dev.call("om_sum_all", X2, S, x2.size, 1)
+    assert abs(dev.get(S)[0] - T.lib().or_sum_all(T.fp(x2), C.c_int64(x2.size), 1)) <= 1e-7 * max(1, abs(x2.mean()))
+    g = dev.put(np.array([0.75], np.float32))
+    D = dev.empty(x2.shape)
+    dev.call("om_mean_all_bwd", g, D, x2.size, 0)
+    assert np.all(dev.get(D) == np.float32(0.75) / np.float32(x2.size))
+
+
+# ------------------------------------------------------------------------------------------------ norms and softmax
+@pytest.mark.parametrize("rows,cols", [(4096, 384), (512, 768), (7, 1536), (33, 2000)])
+def test_layernorm(dev, T, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x, g = rnd(rng, rows, cols, scale=2.0) + 0.5, rnd(rng, rows, cols)
+    gam, bet = (1 + 0.1 * rnd(rng, cols)), 0.1 * rnd(rng, cols)
+    y, mu, iv = np.empty_like(x), np.empty(rows, np.float32), np.empty(rows, np.float32)
+    T.lib().or_layernorm_fwd(T.fp(x), T.fp(gam), T.fp(bet), T.fp(y), T.fp(mu), T.fp(iv), rows, cols, C.c_float(1e-5))
+    X, G, GA, BE = dev.put(x), dev.put(g), dev.put(gam), dev.put(bet)
+    Y, MU, IV = dev.empty(x.shape), dev.empty((rows,)), dev.empty((rows,))
+    dev.call("om_layernorm_fwd", X, GA, BE, Y, MU, IV, rows, cols, C.c_float(1e-5))
+    assert np.array_equal(dev.get(Y), y)  # the reference's Sum16 order, bit for bit
+    assert np.array_equal(dev.get(MU), mu) and np.array_equal(dev.get(IV), iv)
+    dx, dg, db = np.empty_like(x), np.empty(cols, np.float32), np.empty(cols, np.float32)
+    T.lib().or_layernorm_bwd(T.fp(g), T.fp(x), T.fp(gam), T.fp(mu), T.fp(iv), T.fp(dx), T.fp(dg), T.fp(db), rows, cols)
+    DX, DG, DB = dev.empty(x.shape), dev.empty((cols,)), dev.empty((cols,))
+    dev.call("om_layernorm_bwd", G, X, GA, MU, IV, DX, DG, DB, rows, cols, 0, 0)
+    assert scaled(dev.get(DX), dx) <= 1e-6
+    assert scaled(dev.get(DG), dg) <= 1e-7 and scaled(dev.get(DB), db) <= 1e-7
+
+
+@pytest.mark.parametrize("rows,cols", [(1000, 128), (300, 512), (17, 37)])
+def test_softmax_rows(dev, T, rows, cols):
+    rng = np.random.default_rng(rows)
+    x = rnd(rng, rows, cols, scale=3.0)
+    x[0, 5:] = -np.inf
+    x[1, :] = -np.inf  # all masked: NaN row, as the reference
+    ref = np.empty_like(x)
+    T.lib().or_softmax_rows(T.fp(x), T.fp(ref), rows, cols)
+    X, Y = dev.put(x), dev.empty(x.shape)
+    dev.call("om_softmax_fwd", X, Y, rows, cols)
+    got = dev.get(Y)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    g = rnd(rng, rows, cols)
+    g[1] = 0
+    dref = np.empty_like(x)
+    T.lib().or_softmax_bwd(T.fp(g), T.fp(ref), T.fp(dref), rows, cols)
+    G, D = dev.put(g), dev.empty(x.shape)
+    dev.call("om_softmax_bwd", G, Y, D, rows, cols, 0)
+    dgot = dev.get(D)
+    ok = np.isfinite(dref)
+    assert np.array_equal(np.isfinite(dgot), ok) and scaled(dgot[ok], dref[ok]) <= 1e-6
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 10), (4096, 9), (1024, 37)])
+def test_cross_entropy(dev, T, rows, cols):
+    rng = np.random.default_rng(cols)
+    z = rnd(rng, rows, cols, scale=2.0)
+    tg = rng.integers(0, cols, rows).astype(np.int32)
+    tg[3] = -100  # ignored row
+    lp = np.empty_like(z)
+    T.lib().or_logsoftmax_fwd(T.fp(z), T.fp(lp), rows, cols)
+    bad = C.c_int(0)
+    loss = T.lib().or_nll_fwd(T.fp(lp), T.ip(tg), rows, cols, 1, -100, C.byref(bad))
+    dn, dz = np.empty_like(z), np.empty_like(z)
+    T.lib().or_nll_bwd(C.c_float(1.0), T.ip(tg), T.fp(dn), rows, cols, 1, -100)
+    T.lib().or_logsoftmax_bwd(T.fp(dn), T.fp(lp), T.fp(dz), rows, cols)
+    Z, TG, LP, L, BAD, DZ = dev.put(z), dev.put(tg), dev.empty(z.shape), dev.empty((1,)), dev.empty((1,), np.int32), \
+        dev.empty(z.shape)
+    one = dev.put(np.ones(1, np.float32))
+    dev.call("om_logsoftmax_fwd", Z, LP, rows, cols)
+    dev.call("om_nll_fwd", LP, TG, L, BAD, rows, cols, 1, -100)
+    dev.call("om_xent_bwd", one, LP, TG, DZ, rows, cols, 1, -100, 0)
+    assert scaled(dev.get(LP), lp) <= 1e-6
+    assert abs(dev.get(L)[0] - loss) <= 1e-6 * abs(loss) and dev.get(BAD)[0] == -1
+    assert scaled(dev.get(DZ), dz) <= 1e-6
+    tg[5] = cols  # out of range: reported, as the reference's ArgumentOutOfRangeException
+    dev.call("om_nll_fwd", LP, dev.put(tg), L, BAD, rows, cols, 1, -100)
+    assert dev.get(BAD)[0] == 5
+
+
+# ------------------------------------------------------------------------------------------------ attention
+@pytest.mark.parametrize("B,H,L,D,masked", [(2, 3, 40, 32, True), (2, 12, 128, 32, True), (1, 4, 512, 64, False)])
+def test_attention(dev, T, B, H, L, D, masked):
+    rng = np.random.default_rng(L + D)
+    q, k, v, g = (rnd(rng, B, L, H, D) for _ in range(4))  # [B, L, H, D] interleaved, as the Linear outputs
+    mask = None
+    if masked:
+        lens = rng.integers(L // 2, L + 1, B)
+        mask = np.zeros((B, L, L), np.float32)
+        for b in range(B):
+            mask[b, :, lens[b]:] = -np.inf
+    tq, tk, tv, tg = (np.ascontiguousarray(a.transpose(0, 2, 1, 3)) for a in (q, k, v, g))
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref = np.empty_like(tq)
+    T.lib().or_attention_fwd(T.fp(tq), T.fp(tk), T.fp(tv), T.fp(mask) if masked else None, 1, T.fp(o_ref), B, H, L, L,
+                             D, C.c_float(scale))
+    dq, dk, dv = np.empty_like(tq), np.empty_like(tk), np.empty_like(tv)
+    T.lib().or_attention_bwd(T.fp(tq), T.fp(tk), T.fp(tv), T.fp(mask) if masked else None, 1, T.fp(tg), T.fp(dq),
+                             T.fp(dk), T.fp(dv), B, H, L, L, D, C.c_float(scale))
+    Q, K, V, G = dev.put(q), dev.put(k), dev.put(v), dev.put(g)
+    M = dev.put(mask) if masked else None
+    O, P, DS = dev.empty(q.shape), dev.empty((B, H, L, L)), dev.empty((B, H, L, L))
+    DQ, DK, DV = dev.empty(q.shape), dev.empty(q.shape), dev.empty(q.shape)
+    dev.call("om_attention_fwd", Q, K, V, M, 1, O, P, B, H, L, L, D, C.c_float(scale))
+    dev.call("om_attention_bwd", Q, K, V, P, G, DQ, DK, DV, DS, B, H, L, L, D, C.c_float(scale), 0)
+    back = lambda t: dev.get(t).transpose(0, 2, 1, 3)
+    assert scaled(back(O), o_ref) <= TOL
+    for got, ref in ((DQ, dq), (DK, dk), (DV, dv)):
+        assert scaled(back(got), ref) <= TOL
+
+
+# ------------------------------------------------------------------------------------------------ conv and pool
+@pytest.mark.parametrize("N,Cin,H,W,Cout,K,S,P", [(2, 64, 14, 14, 64, 3, 1, 1), (2, 1, 32, 128, 32, 3, 1, 1),
+                                                  (3, 32, 16, 64, 64, 3, 1, 1), (2, 5, 9, 11, 7, 3, 2, 1),
+                                                  (1, 128, 4, 32, 256, 3, 1, 1)])
+def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
+    rng = np.random.default_rng(N * Cin + Cout)
+    x, w, b = rnd(rng, N, Cin, H, W), rnd(rng, Cout, Cin, K, K, scale=0.2), rnd(rng, Cout)
+    OH, OW = (H + 2 * P - K) // S + 1, (W + 2 * P - K) // S + 1
+    g = rnd(rng, N, Cout, OH, OW)
+    y = np.empty((N, Cout, OH, OW), np.float32)
+    T.lib().or_conv2d_fwd(T.fp(x), T.fp(w), T.fp(b), T.fp(y), N, Cin, H, W, Cout, K, K, S, P)
+    dx, dw, db = np.empty_like(x), np.empty_like(w), np.empty_like(b)
+    T.lib().or_conv2d_bwd(T.fp(g), T.fp(x), T.fp(w), T.fp(dx), T.fp(dw), T.fp(db), N, Cin, H, W, Cout, K, K, S, P)
+    X, Wd, Bd, G = dev.put(x), dev.put(w), dev.put(b), dev.put(g)
+    Y, DX, DW, DB = dev.empty(y.shape), dev.empty(x.shape), dev.empty(w.shape), dev.empty(b.shape)
+    dev.call("om_conv2d_fwd", X, Wd, Bd, Y, N, Cin, H, W, Cout, K, K, S, P)
+    dev.call("om_conv2d_bwd", G, X, Wd, DX, DW, DB, N, Cin, H, W, Cout, K, K, S, P, 0, 0)
+    assert scaled(dev.get(Y), y) <= TOL
+    assert scaled(dev.get(DX), dx) <= TOL
+    assert scaled(dev.get(DW), dw) <= TOL
+    assert scaled(dev.get(DB), db) <= 1e-7
+
+
+@pytest.mark.parametrize("shape,k,s", [((2, 3, 8, 12), (2, 2), (2, 2)), ((2, 4, 8, 6), (2, 1), (2, 1)),
+                                       ((1, 2, 9, 9), (3, 3), (2, 2))])
+def test_maxpool_bit_exact(dev, T, shape, k, s):
+    rng = np.random.default_rng(sum(shape))
+    x = rng.integers(-2, 3, shape).astype(np.float32)  # many ties
+    x.reshape(-1)[7] = np.nan
+    N, Cc, H, W = shape
+    OH, OW = (H - k[0]) // s[0] + 1, (W - k[1]) // s[1] + 1
+    y, idx = np.empty((N, Cc, OH, OW), np.float32), np.empty((N, Cc, OH, OW), np.int32)
+    T.lib().or_maxpool_fwd(T.fp(x), T.fp(y), T.ip(idx), N, Cc, H, W, k[0], k[1], s[0], s[1], 0, 0)
+    g = rnd(rng, *y.shape)
+    dx = np.empty_like(x)
+    T.lib().or_maxpool_bwd(T.fp(g), T.ip(idx), T.fp(dx), C.c_int64(idx.size), C.c_int64(x.size))
+    X, Y, I, G, DX = dev.put(x), dev.empty(y.shape), dev.empty(y.shape, np.int32), dev.put(g), dev.empty(x.shape)
+    dev.call("om_maxpool_fwd", X, Y, I, N, Cc, H, W, k[0], k[1], s[0], s[1], 0, 0)
+    dev.call("om_maxpool_bwd", G, I, DX, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], 0, 0, 0)
+    assert np.array_equal(dev.get(I), idx)
+    assert np.array_equal(dev.get(Y).view(np.uint32), y.view(np.uint32))
+    assert np.array_equal(dev.get(DX), dx)
+
+
+# ------------------------------------------------------------------------------------------------ CTC
+def ctc_cases():
+    from conftest import load_golden
+    o = load_golden("autograd_crnn")
+    yield "fixture", o["out.lp"], o["in.targets"].astype(np.int32), o["in.input_lengths"].astype(np.int32), \
+        o["in.target_lengths"].astype(np.int32)
+    rng = np.random.default_rng(11)
+    Tn, B, Cc = 32, 32, 37
+    z = rng.standard_normal((Tn, B, Cc)).astype(np.float32)
+    lp = (z - np.log(np.exp(z.astype(np.float64)).sum(-1, keepdims=True))).astype(np.float32)
+    tl = rng.integers(1, 11, B).astype(np.int32)
+    tl[0] = 0
+    il = np.full(B, Tn, np.int32)
+    il[1] = 3  # too short for its target: +inf / zero gradient
+    tl[1] = 5
+    labels = rng.integers(1, Cc, int(tl.sum())).astype(np.int32)
+    yield "c4", lp, labels, il, tl
+
+
+@pytest.mark.parametrize("red", [0, 1, 2])
+def test_ctc_bit_exact(dev, T, red):
+    for name, lp, tg, il, tl in ctc_cases():
+        Tn, B, Cc = lp.shape
+        n_out = B if red == 0 else 1
+        ref = np.empty(n_out, np.float32)
+        T.lib().or_ctc_loss(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), Tn, B, Cc, 0, red, 0, T.fp(ref))
+        gin = np.linspace(0.5, 1.5, n_out).astype(np.float32)
+        dref = np.empty_like(lp)
+        T.lib().or_ctc_grad(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), T.fp(gin), Tn, B, Cc, 0, red, T.fp(dref))
+        LP, TG, IL, TL, L, GIN, D = dev.put(lp), dev.put(tg), dev.put(il), dev.put(tl), dev.empty((n_out,)), \
+            dev.put(gin), dev.empty(lp.shape, fill=123.0)
+        hil, htl, htg = (a.ctypes.data_as(C.c_void_p) for a in (il, tl, tg))
+        dev.call("om_ctc_fwd", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L)
+        dev.call("om_ctc_bwd", LP, TG, IL, TL, GIN, D, int(tl.max()), Tn, B, Cc, 0, red, 0)
+        got = dev.get(L)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
+        assert np.array_equal(dev.get(D).view(np.uint32), dref.view(np.uint32)), name
+
+
+def test_ctc_rejects_bad_targets(dev):
+    lp = dev.empty((3, 1, 4), fill=0.0)
+    tg = np.array([0], np.int32)  # the blank as a label
+    il, tl = np.array([3], np.int32), np.array([1], np.int32)
+    st = dev.status("om_ctc_fwd", lp, dev.put(tg), dev.put(il), dev.put(tl), il.ctypes.data_as(C.c_void_p),
+                    tl.ctypes.data_as(C.c_void_p), tg.ctypes.data_as(C.c_void_p), 1, 3, 1, 4, 0, 1, 0, lp)
+    assert st == 1 and b"differ from the blank" in dev.ctx.L.om_last_error(dev.ctx.h)
+
+
+# ------------------------------------------------------------------------------------------------ optimizers
+@pytest.mark.parametrize("cfg", [dict(wd=0.01, dec=1, ams=0), dict(wd=0.1, dec=0, ams=0), dict(wd=0.05, dec=1, ams=1),
+                                 dict(wd=0.0, dec=0, ams=0)])
+def test_adam_bit_exact(dev, T, cfg):
+    rng = np.random.default_rng(5)
+    n = 1_000_003
+    p0, m0, v0 = rnd(rng, n), rnd(rng, n, scale=0.01), np.abs(rnd(rng, n, scale=1e-4))
+    vm0 = v0 * 1.5
+    P, M, V, VM = dev.put(p0), dev.put(m0), dev.put(v0), dev.put(vm0)
+    p, m, v, vm = p0.copy(), m0.copy(), v0.copy(), vm0.copy()
+    for t in range(1, 4):
+        g = rnd(rng, n, scale=0.1)
+        ss, sq = C.c_float(), C.c_float()
+        T.lib().or_adam_scalars(C.c_float(1e-3), C.c_float(0.9), C.c_float(0.999), C.c_int64(t), C.byref(ss),
+                                C.byref(sq))
+        T.lib().or_adam_update(T.fp(p), T.fp(g), T.fp(m), T.fp(v), T.fp(vm) if cfg["ams"] else None, C.c_int64(n),
+                               C.c_float(1e-3), C.c_float(0.9), C.c_float(0.999), C.c_float(1e-8),
+                               C.c_float(cfg["wd"]), cfg["dec"], ss, sq)
+        ss2, sq2 = C.c_float(), C.c_float()
+        dev.ctx.L.om_adam_scalars(1e-3, 0.9, 0.999, t, C.byref(ss2), C.byref(sq2))
+        assert ss2.value == ss.value and sq2.value == sq.value
+        dev.call("om_adam_step", P, dev.put(g), M, V, VM if cfg["ams"] else None, n, C.c_float(1e-3), C.c_float(0.9),
+                 C.c_float(0.999), C.c_float(1e-8), C.c_float(cfg["wd"]), cfg["dec"], ss2, sq2)
+    for got, ref in ((P, p), (M, m), (V, v)):
+        assert np.array_equal(dev.get(got).view(np.uint32), ref.view(np.uint32))
+
+
+def test_sgd_bit_exact(dev, T):
+    rng = np.random.default_rng(6)
+    n = 10007
+    p0 = rnd(rng, n)
+    P, BUF = dev.put(p0), dev.empty((n,), fill=0.0)
+    p, buf = p0.copy(), np.zeros(n, np.float32)
+    for t in range(3):
+        g = rnd(rng, n)
+        T.lib().or_sgd_update(T.fp(p), T.fp(g), T.fp(buf), C.c_int64(n), C.c_float(0.1), C.c_float(0.9),
+                              C.c_float(0.0), C.c_float(1e-2), 1, int(t == 0))
+        dev.call("om_sgd_step", P, dev.put(g), BUF, n, C.c_float(0.1), C.c_float(0.9), C.c_float(0.0),
+                 C.c_float(1e-2), 1, int(t == 0))
+    assert np.array_equal(dev.get(P), p) and np.array_equal(dev.get(BUF), buf)
