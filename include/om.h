@@ -108,6 +108,15 @@ om_status om_mul(om_ctx *ctx, const float *a, const float *b, float *y, int64_t 
 om_status om_axpy(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n);
 /* dst = src * alpha (a copy when alpha is 1). */
 om_status om_scale(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n);
+/* y = x.Permute(perm) made contiguous (rank <= 6): the Clone() of a permuted view, and with the inverse permutation
+ * the Permute backward (BackwardOps.cs:107-118). accumulate adds into y. */
+om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int32_t *shape, const int32_t *perm,
+                     int accumulate);
+/* Losses.Mse = Mean(Mul(Sub(pred, target), same)) (Losses.cs:86-91; Ops.cs:23-56; Ops.Nn.cs:162-231): diff = pred -
+ * target is saved, *loss (device) = (float)(sum in double of fl(diff*diff) / n). The backward is the chain's rounding
+ * order: t = (g / (float)n) * diff, dpred = t + t (the two Mul emissions added, Engine.AddInto). */
+om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n);
+om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- reductions */
 /* Ops.Sum / Ops.Mean over all elements in double (Ops.Nn.cs:162-231); *out is a device float. */

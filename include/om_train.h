@@ -1,0 +1,70 @@
+/*
+ * om_train.h — C ABI of libom_train.so, the C++ training tape that sits above libom_hip.so (include/om.h).
+ *
+ * The reference keeps its tape in C# (RecursiveAI.OneModel.Training over the tensor layer's autograd); this image has
+ * no .NET toolchain, so the tape is restated in C++ with the reference's surface: modules that register parameters in
+ * order (NnModule.cs:54-165), ops that record backward records, Tensor.Backward() (Engine.cs:21-207), losses
+ * (Losses.cs), ZeroGrad and SGD/Adam/AdamW Step() (Optimizers.cs:184-608). A model here is one of the benchmark's
+ * training configurations, built on the device with its synthetic inputs; this ABI is what tests and bench.py drive.
+ *
+ * Conventions as in om.h: status codes (0 = OK), messages from omt_last_error, no C++ types across the boundary.
+ */
+#ifndef OM_TRAIN_H
+#define OM_TRAIN_H
+
+#include <stdint.h>
+
+#include "om.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct omt_model omt_model;
+
+/* Configuration sizes; 0 keeps the configuration's default (batch, sequence length / image side, layer count). */
+typedef struct {
+    int32_t batch, seq, layers, hw;
+} omt_scale;
+
+/* Builds configuration `cfg` (1 = MLP 784-256-10, 2 = conv block, 3 = MiniLM-shaped pre-LN block, 4 = CRNN + CTC,
+ * 5 = BERT-base-shaped 4-layer stack) on `device`: parameters from the SplitMix64 generator in registration order
+ * (Kaiming-uniform +-1/sqrt(fan_in), LayerNorm 1/0), synthetic inputs from seed 20261201 + 100*cfg + index, and an
+ * AdamW(lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0.01) over the parameter arena. */
+om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out);
+void omt_destroy(omt_model *m);
+const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */
+
+/* One training step: ZeroGrad, forward, loss.Backward(), optimizer.Step(); *loss is read back at the end. */
+om_status omt_step(omt_model *m, float *loss);
+/* ZeroGrad, forward and backward only (gradients are left in the arena). */
+om_status omt_forward_backward(omt_model *m, float *loss);
+/* optimizer.Step() alone, on the gradients currently in the arena. */
+om_status omt_optimizer_step(omt_model *m);
+/* The model's om_ctx (its stream orders every launch of the step). */
+om_ctx *omt_ctx(omt_model *m);
+
+/* Parameters in Parameters() order. which: 0 value, 1 gradient, 2 first moment, 3 second moment. */
+int omt_param_count(omt_model *m);
+om_status omt_param_info(omt_model *m, int i, char *name, int name_cap, int *ndim, int32_t *dims);
+om_status omt_param_read(omt_model *m, int i, int which, float *host, int64_t numel);
+om_status omt_param_write(omt_model *m, int i, int which, const float *host, int64_t numel);
+/* Optimizer step count (Optimizer.StepCount). */
+int64_t omt_step_count(omt_model *m);
+
+/* Named inputs ("x", "target", "labels", "lengths", "mask", "in_len", "tgt_len"): float or int32 host copies.
+ * is_int reports the element type; omt_input_read copies numel elements. */
+int omt_input_count(omt_model *m);
+om_status omt_input_info(omt_model *m, int i, char *name, int name_cap, int *is_int, int *ndim, int32_t *dims);
+om_status omt_input_read(omt_model *m, int i, void *host, int64_t numel);
+/* Gradient of an input that requires one (C2's image), after a backward. */
+om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel);
+
+/* Host helper with no device: the SplitMix64 generator of the tape (for cross-checks against the reference's
+ * Generator): kind 0 = uniform [lo, hi), 1 = benchmark normal, 2 = ints in [lo, hi). */
+void omt_generate(uint64_t seed, int kind, float lo, float hi, void *out, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OM_TRAIN_H */

@@ -53,6 +53,9 @@ _OM_SIGS = {
     "om_mul": [vp, vp, vp, vp, i64],
     "om_axpy": [vp, f32, vp, vp, i64],
     "om_scale": [vp, f32, vp, vp, i64],
+    "om_permute": [vp, vp, vp, ci, vp, vp, ci],
+    "om_mse_fwd": [vp, vp, vp, vp, vp, i64],
+    "om_mse_bwd": [vp, vp, vp, vp, i64, ci],
     "om_sum_all": [vp, vp, vp, i64, ci],
     "om_mean_axis": [vp, vp, vp, ci, ci, ci],
     "om_mean_axis_bwd": [vp, vp, vp, ci, ci, ci, ci],
@@ -109,6 +112,152 @@ def load_hip():
 
 def om_symbols():
     return list(_OM_SIGS)
+
+
+class omt_scale(C.Structure):
+    _fields_ = [("batch", i32), ("seq", i32), ("layers", i32), ("hw", i32)]
+
+
+_OMT_SIGS = {
+    "omt_config_create": ([ci, ci, C.POINTER(omt_scale), C.POINTER(vp)], i32),
+    "omt_destroy": ([vp], None),
+    "omt_last_error": ([vp], C.c_char_p),
+    "omt_step": ([vp, C.POINTER(f32)], i32),
+    "omt_forward_backward": ([vp, C.POINTER(f32)], i32),
+    "omt_optimizer_step": ([vp], i32),
+    "omt_ctx": ([vp], vp),
+    "omt_param_count": ([vp], ci),
+    "omt_param_info": ([vp, ci, C.c_char_p, ci, C.POINTER(ci), C.POINTER(i32)], i32),
+    "omt_param_read": ([vp, ci, ci, vp, i64], i32),
+    "omt_param_write": ([vp, ci, ci, vp, i64], i32),
+    "omt_step_count": ([vp], i64),
+    "omt_input_count": ([vp], ci),
+    "omt_input_info": ([vp, ci, C.c_char_p, ci, C.POINTER(ci), C.POINTER(ci), C.POINTER(i32)], i32),
+    "omt_input_read": ([vp, ci, vp, i64], i32),
+    "omt_input_grad": ([vp, ci, vp, i64], i32),
+    "omt_generate": ([u64, ci, f32, f32, vp, i64], None),
+}
+_TRAIN = None
+
+
+def load_train():
+    """Loads lib/libom_train.so (the C++ tape, linked against libom_hip.so). Raises if it is missing."""
+    global _TRAIN
+    if _TRAIN is not None:
+        return _TRAIN
+    load_hip()
+    path = lib_path("libom_train.so")
+    if not os.path.exists(path):
+        raise OmError(f"{path} is missing: build it with `python onemodel-csharp_amd/build.py`")
+    L = C.CDLL(path)
+    for name, (args, res) in _OMT_SIGS.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _TRAIN = L
+    return L
+
+
+def omt_symbols():
+    return list(_OMT_SIGS)
+
+
+class Model:
+    """One benchmark configuration on the device (include/om_train.h): `step()` is ZeroGrad + forward +
+    loss.Backward() + AdamW.Step() and returns the loss."""
+
+    def __init__(self, cfg: int, device: int = 0, batch=0, seq=0, layers=0, hw=0):
+        import numpy as np
+        self.np = np
+        self.L = load_train()
+        h = vp()
+        sc = omt_scale(batch, seq, layers, hw)
+        st = self.L.omt_config_create(device, cfg, C.byref(sc), C.byref(h))
+        if st != 0:
+            raise OmError(f"omt_config_create({cfg}) failed ({st}): {self.L.omt_last_error(None).decode()}")
+        self.h = h
+        self.cfg = cfg
+
+    def _check(self, st, what):
+        if st != 0:
+            raise OmError(f"{what} failed ({st}): {self.L.omt_last_error(self.h).decode()}")
+
+    def step(self) -> float:
+        v = f32()
+        self._check(self.L.omt_step(self.h, C.byref(v)), "omt_step")
+        return v.value
+
+    def forward_backward(self) -> float:
+        v = f32()
+        self._check(self.L.omt_forward_backward(self.h, C.byref(v)), "omt_forward_backward")
+        return v.value
+
+    def optimizer_step(self):
+        self._check(self.L.omt_optimizer_step(self.h), "omt_optimizer_step")
+
+    @property
+    def ctx(self):
+        return self.L.omt_ctx(self.h)
+
+    def params(self):
+        """[(name, shape)] in Parameters() order."""
+        out = []
+        for i in range(self.L.omt_param_count(self.h)):
+            name = C.create_string_buffer(256)
+            nd = ci()
+            dims = (i32 * 8)()
+            self._check(self.L.omt_param_info(self.h, i, name, 256, C.byref(nd), dims), "omt_param_info")
+            out.append((name.value.decode(), tuple(dims[:nd.value])))
+        return out
+
+    def read_param(self, i, which=0):
+        np = self.np
+        shape = self.params()[i][1]
+        a = np.empty(shape, np.float32)
+        self._check(self.L.omt_param_read(self.h, i, which, a.ctypes.data, a.size), "omt_param_read")
+        return a
+
+    def write_param(self, i, values, which=0):
+        np = self.np
+        a = np.ascontiguousarray(values, np.float32)
+        self._check(self.L.omt_param_write(self.h, i, which, a.ctypes.data, a.size), "omt_param_write")
+
+    def inputs(self):
+        """{name: numpy array} host copies of the synthetic inputs."""
+        np = self.np
+        out = {}
+        for i in range(self.L.omt_input_count(self.h)):
+            name = C.create_string_buffer(64)
+            is_int, nd = ci(), ci()
+            dims = (i32 * 8)()
+            self._check(self.L.omt_input_info(self.h, i, name, 64, C.byref(is_int), C.byref(nd), dims), "input_info")
+            a = np.empty(tuple(dims[:nd.value]), np.int32 if is_int.value else np.float32)
+            self._check(self.L.omt_input_read(self.h, i, a.ctypes.data, a.size), "omt_input_read")
+            out[name.value.decode()] = a
+        return out
+
+    def input_grad(self, name):
+        np = self.np
+        ins = self.inputs()
+        i = list(ins).index(name)
+        a = np.empty(ins[name].shape, np.float32)
+        self._check(self.L.omt_input_grad(self.h, i, a.ctypes.data, a.size), "omt_input_grad")
+        return a
+
+    @property
+    def step_count(self):
+        return self.L.omt_step_count(self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.L.omt_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Context:

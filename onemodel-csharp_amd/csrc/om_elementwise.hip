@@ -188,9 +188,101 @@ __global__ void __launch_bounds__(kBlock) k_mean_all_bwd(const float *__restrict
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) dx[t] = acc ? dx[t] + v : v;
 }
 
+// y[j] = x[perm-order]: y index -> its coordinates -> x offset through the permuted strides.
+struct PermDesc {
+    int ndim;
+    int64_t ydim[6];
+    int64_t xstride_for_y[6];
+};
+__global__ void __launch_bounds__(kBlock) k_permute(const float *__restrict__ x, float *__restrict__ y, int64_t n,
+                                                    PermDesc d, int acc) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        int64_t r = i, off = 0;
+        for (int a = d.ndim - 1; a >= 0; a--) {
+            int64_t c = r % d.ydim[a];
+            r /= d.ydim[a];
+            off += c * d.xstride_for_y[a];
+        }
+        float v = x[off];
+        y[i] = acc ? y[i] + v : v;
+    }
+}
+
+// MSE: diff and per-block double partial sums of fl(diff*diff); a final pass adds the partials in block order.
+__global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict__ p, const float *__restrict__ t,
+                                                        float *__restrict__ diff, int64_t n,
+                                                        double *__restrict__ part) {
+    __shared__ double sh[kBlock / 64];
+    double acc = 0.0;
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float d = p[i] - t[i];
+        diff[i] = d;
+        acc += (double)(d * d);
+    }
+    double s = omd::block_sum<kBlock / 64>(acc, sh);
+    if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+__global__ void __launch_bounds__(kBlock) k_mse_bwd(const float *__restrict__ gs, const float *__restrict__ diff,
+                                                    float *__restrict__ dp, int64_t n, int acc) {
+    float dsq = gs[0] / (float)n;
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        float t = dsq * diff[i];
+        float v = t + t;
+        dp[i] = acc ? dp[i] + v : v;
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int32_t *shape, const int32_t *perm,
+                     int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && shape && perm && ndim >= 1 && ndim <= 6, "om_permute: bad arguments (rank %d)", ndim);
+    int64_t xs[6], n = 1;
+    bool seen[6] = {false, false, false, false, false, false};
+    for (int a = ndim - 1; a >= 0; a--) {
+        OM_REQUIRE(ctx, shape[a] >= 0, "om_permute: negative extent");
+        xs[a] = n;
+        n *= shape[a];
+    }
+    PermDesc d;
+    d.ndim = ndim;
+    for (int a = 0; a < ndim; a++) {
+        OM_REQUIRE(ctx, perm[a] >= 0 && perm[a] < ndim && !seen[perm[a]], "om_permute: perm is not a permutation");
+        seen[perm[a]] = true;
+        d.ydim[a] = shape[perm[a]];
+        d.xstride_for_y[a] = xs[perm[a]];
+    }
+    if (n == 0) return OM_OK;
+    hipLaunchKernelGGL(k_permute, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, x, y, n, d, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_permute");
+}
+
+om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, pred && target && diff && loss && n > 0, "om_mse_fwd: bad arguments");
+    float *scr;
+    om_status s = om::scratch(ctx, sizeof(double) * kSumBlocks, &scr);
+    if (s) return s;
+    double *part = reinterpret_cast<double *>(scr);
+    int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
+    hipLaunchKernelGGL(k_mse_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, pred, target, diff, n, part);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, loss, (double)n);
+    return OM_LAUNCH_CHECK(ctx, "om_mse_fwd");
+}
+
+om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g_scalar && diff && dpred && n > 0, "om_mse_bwd: bad arguments");
+    hipLaunchKernelGGL(k_mse_bwd, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, g_scalar, diff, dpred, n,
+                       accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_mse_bwd");
+}
 
 om_status om_relu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n) {
     return map2(ctx, "om_relu_fwd", x, nullptr, y, n, 0, ReluF{});

@@ -1,0 +1,561 @@
+// Modules, the parameter arena, optimizers, the benchmark configurations and the C ABI of include/om_train.h.
+#include <cmath>
+#include <cstring>
+#include <map>
+
+#include "om_train.h"
+#include "tape.hpp"
+
+namespace omt {
+
+// ------------------------------------------------------------------------------------------------ generator
+uint64_t Generator::next_u64() {
+    // SplitMix64 (Steele, Lea and Flood 2014), as Generator.NextUInt64 (Generator.cs:27-31)
+    uint64_t z = (s_ += 0x9E3779B97F4A7C15ULL);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+    return z ^ (z >> 31);
+}
+float Generator::next_single() { return (float)(next_u64() >> 40) * (1.0f / 16777216.0f); }
+void Generator::fill_uniform(float lo, float hi, std::vector<float> &v) {
+    for (float &x : v) x = uniform(lo, hi);
+}
+void Generator::fill_normal(std::vector<float> &v) {
+    for (float &x : v) {
+        double u1 = ((double)(next_u64() >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(next_u64() >> 11) * (1.0 / 9007199254740992.0);
+        x = (float)(std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2));
+    }
+}
+void Generator::fill_ints(int32_t lo, int32_t hi, std::vector<int32_t> &v) {
+    uint64_t span = (uint64_t)(hi - lo);
+    for (int32_t &x : v) x = lo + (int32_t)(next_u64() % span);
+}
+
+static float fan_in_bound(int fan_in) { return 1.0f / std::sqrt((float)fan_in); }  // Layers.cs:59
+
+// ------------------------------------------------------------------------------------------------ modules
+Tensor Module::param(const std::string &name, std::vector<int> shape, std::vector<float> init) {
+    auto t = std::make_shared<TensorImpl>();
+    t->shape = std::move(shape);
+    t->numel = numel_of(t->shape);
+    t->requires_grad = true;
+    t->name = name;
+    params_.emplace_back(name, t);
+    init_.push_back(std::move(init));
+    return t;
+}
+void Module::named_parameters(std::vector<std::pair<std::string, Tensor>> &out, const std::string &prefix) const {
+    for (auto &p : params_) out.emplace_back(prefix + p.first, p.second);
+    for (auto &c : children_) c.second->named_parameters(out, prefix + c.first + ".");
+}
+void Module::take_init(std::vector<std::vector<float>> &out) {
+    for (auto &v : init_) out.push_back(std::move(v));
+    init_.clear();
+    for (auto &c : children_) c.second->take_init(out);
+}
+
+Linear::Linear(int in, int out, Generator &g, bool bias) {
+    float bd = fan_in_bound(in);
+    std::vector<float> wv((size_t)in * out), bv(bias ? out : 0);
+    g.fill_uniform(-bd, bd, wv);  // weight first, then bias (Layers.cs:59-64)
+    if (bias) g.fill_uniform(-bd, bd, bv);
+    w = param("weight", {out, in}, std::move(wv));
+    if (bias) b = param("bias", {out}, std::move(bv));
+}
+Conv2d::Conv2d(int cin, int cout, int k, Generator &g, int padding, int stride_) : stride(stride_), pad(padding) {
+    float bd = fan_in_bound(cin * k * k);
+    std::vector<float> wv((size_t)cout * cin * k * k), bv(cout);
+    g.fill_uniform(-bd, bd, wv);  // Layers.cs:105-110
+    g.fill_uniform(-bd, bd, bv);
+    w = param("weight", {cout, cin, k, k}, std::move(wv));
+    b = param("bias", {cout}, std::move(bv));
+}
+LayerNorm::LayerNorm(int n, float eps_) : eps(eps_) {
+    w = param("weight", {n}, std::vector<float>(n, 1.0f));  // Layers.cs:255-262
+    b = param("bias", {n}, std::vector<float>(n, 0.0f));
+}
+MultiHeadAttention::MultiHeadAttention(int width, int heads_, Generator &g) : heads(heads_) {
+    if (heads < 1 || width % heads) throw Error(OM_E_ARG, "Width must be divisible by the head count.");
+    q = child("q", std::make_unique<Linear>(width, width, g));  // drawn q, k, v, o (Layers.cs:486-494)
+    k = child("k", std::make_unique<Linear>(width, width, g));
+    v = child("v", std::make_unique<Linear>(width, width, g));
+    o = child("o", std::make_unique<Linear>(width, width, g));
+}
+Tensor MultiHeadAttention::operator()(const Tensor &x, const Tensor &mask) const {
+    // Layers.cs:497-516: q/k/v projections, split heads, attention, merge heads, output projection.
+    return (*o)(attention_heads((*q)(x), (*k)(x), (*v)(x), mask, heads));
+}
+
+// Post-norm TransformerEncoderLayer (Layers.cs:523-578).
+struct EncoderLayer : Module {
+    MultiHeadAttention *attn;
+    LayerNorm *norm1, *norm2;
+    Linear *ff1, *ff2;
+    EncoderLayer(int width, int heads, int ff, Generator &g) {
+        attn = child("attn", std::make_unique<MultiHeadAttention>(width, heads, g));
+        norm1 = child("norm1", std::make_unique<LayerNorm>(width));
+        ff1 = child("ff1", std::make_unique<Linear>(width, ff, g));
+        ff2 = child("ff2", std::make_unique<Linear>(ff, width, g));
+        norm2 = child("norm2", std::make_unique<LayerNorm>(width));
+    }
+    Tensor operator()(const Tensor &x, const Tensor &mask) const {
+        Tensor x1 = (*norm1)(add(x, (*attn)(x, mask)));
+        return (*norm2)(add(x1, (*ff2)(gelu((*ff1)(x1)))));
+    }
+};
+// The C3 block: pre-norm, composed from the reference's pieces (children ln1, attn, ln2, ff1, ff2).
+struct PreNormBlock : Module {
+    LayerNorm *ln1, *ln2;
+    MultiHeadAttention *attn;
+    Linear *ff1, *ff2;
+    PreNormBlock(int width, int heads, int ff, Generator &g) {
+        ln1 = child("ln1", std::make_unique<LayerNorm>(width));
+        attn = child("attn", std::make_unique<MultiHeadAttention>(width, heads, g));
+        ln2 = child("ln2", std::make_unique<LayerNorm>(width));
+        ff1 = child("ff1", std::make_unique<Linear>(width, ff, g));
+        ff2 = child("ff2", std::make_unique<Linear>(ff, width, g));
+    }
+    Tensor operator()(const Tensor &x, const Tensor &mask) const {
+        Tensor h = add(x, (*attn)((*ln1)(x), mask));
+        return add(h, (*ff2)(gelu((*ff1)((*ln2)(h)))));
+    }
+};
+
+}  // namespace omt
+
+// ------------------------------------------------------------------------------------------------ model
+using namespace omt;
+
+struct Input {
+    std::string name;
+    Tensor t;                    // device copy (persistent region)
+    std::vector<float> hf;       // host copy (float inputs)
+    std::vector<int32_t> hi;     // host copy (int inputs)
+    bool is_int = false;
+};
+
+struct omt_model {
+    std::unique_ptr<Device> device;
+    std::unique_ptr<Module> root;
+    std::vector<std::pair<std::string, Tensor>> params;
+    std::vector<Tensor> leaves;  // params + inputs that require gradients
+    std::vector<int64_t> offset;
+    int64_t total = 0;
+    float *pb = nullptr, *gb = nullptr, *mb = nullptr, *vb = nullptr;
+    std::vector<Input> inputs;
+    std::function<Tensor(omt_model &)> loss_fn;
+    // AdamW hyper-parameters
+    float lr = 1e-3f, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, wd = 0.01f;
+    int64_t step_count = 0;
+    std::string err;
+
+    Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
+        Input in;
+        in.name = name;
+        in.t = std::make_shared<TensorImpl>();
+        in.t->shape = std::move(shape);
+        in.t->numel = numel_of(in.t->shape);
+        in.t->data = (float *)device->persistent(sizeof(float) * (uint64_t)in.t->numel);
+        in.t->name = name;
+        check(device->ctx(), om_upload(device->ctx(), in.t->data, host.data(), sizeof(float) * host.size()), "upload");
+        if (requires_grad) {
+            in.t->requires_grad = true;
+            in.t->grad = (float *)device->persistent(sizeof(float) * (uint64_t)in.t->numel);
+            leaves.push_back(in.t);
+        }
+        in.hf = std::move(host);
+        inputs.push_back(std::move(in));
+        return inputs.back();
+    }
+    Input &add_int_input(const std::string &name, std::vector<int> shape, std::vector<int32_t> host) {
+        Input in;
+        in.name = name;
+        in.is_int = true;
+        in.t = std::make_shared<TensorImpl>();
+        in.t->shape = std::move(shape);
+        in.t->numel = numel_of(in.t->shape);
+        in.t->idata = (int32_t *)device->persistent(sizeof(int32_t) * (uint64_t)(in.t->numel > 0 ? in.t->numel : 1));
+        in.t->name = name;
+        check(device->ctx(), om_upload(device->ctx(), in.t->idata, host.data(), sizeof(int32_t) * host.size()),
+              "upload");
+        in.hi = std::move(host);
+        inputs.push_back(std::move(in));
+        return inputs.back();
+    }
+    const Input &input(const std::string &name) const {
+        for (auto &i : inputs)
+            if (i.name == name) return i;
+        throw Error(OM_E_ARG, "no input " + name);
+    }
+
+    // Lays the parameters out contiguously (Parameters() order, 16-byte aligned) in four persistent blocks: values,
+    // gradients, first and second moments; uploads the initial values once.
+    void finalize(std::vector<std::vector<float>> &&init) {
+        root->named_parameters(params);
+        offset.resize(params.size());
+        int64_t off = 0;
+        for (size_t i = 0; i < params.size(); i++) {
+            offset[i] = off;
+            off += (params[i].second->numel + 3) & ~int64_t(3);
+        }
+        total = off;
+        uint64_t bytes = sizeof(float) * (uint64_t)(total > 0 ? total : 4);
+        om_ctx *c = device->ctx();
+        pb = (float *)device->persistent(bytes);
+        gb = (float *)device->persistent(bytes);
+        mb = (float *)device->persistent(bytes);
+        vb = (float *)device->persistent(bytes);
+        std::vector<float> host((size_t)total, 0.0f);
+        for (size_t i = 0; i < params.size(); i++) {
+            if (init[i].size() != (size_t)params[i].second->numel) throw Error(OM_E_STATE, "init size mismatch");
+            std::memcpy(host.data() + offset[i], init[i].data(), sizeof(float) * init[i].size());
+            Tensor &t = params[i].second;
+            t->name = params[i].first;
+            t->data = pb + offset[i];
+            t->grad = gb + offset[i];
+            leaves.insert(leaves.begin() + (long)i, t);
+        }
+        check(c, om_upload(c, pb, host.data(), bytes), "upload params");
+        check(c, om_zero(c, gb, bytes), "zero grads");
+        check(c, om_zero(c, mb, bytes), "zero m");
+        check(c, om_zero(c, vb, bytes), "zero v");
+        device->sync();
+    }
+
+    // AdamW.Step (Optimizers.cs:184-219, 501-589): BeginStep scalars on the host, then one fused update per run of
+    // consecutive parameters that have gradients (a parameter without one is skipped, as in the reference).
+    void optimizer_step() {
+        settle_grads(leaves);
+        float ss, sq;
+        om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
+        om_ctx *c = device->ctx();
+        size_t i = 0;
+        while (i < params.size()) {
+            if (!params[i].second->grad_exists || !params[i].second->requires_grad) {
+                i++;
+                continue;
+            }
+            size_t j = i;
+            while (j + 1 < params.size() && params[j + 1].second->grad_exists && params[j + 1].second->requires_grad) j++;
+            int64_t beg = offset[i], end = offset[j] + params[j].second->numel;
+            check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, end - beg, lr, beta1, beta2, eps,
+                                  wd, 1, ss, sq),
+                  "om_adam_step");
+            i = j + 1;
+        }
+        step_count++;
+    }
+
+    float forward_backward() {
+        device->step_reset();
+        zero_grad(leaves);
+        Tensor loss = loss_fn(*this);
+        backward(loss);
+        float v = 0.0f;
+        check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
+        return v;
+    }
+    float step() {
+        device->step_reset();
+        zero_grad(leaves);
+        Tensor loss = loss_fn(*this);
+        backward(loss);
+        optimizer_step();
+        float v = 0.0f;
+        check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
+        return v;
+    }
+};
+
+// ------------------------------------------------------------------------------------------------ configurations
+static uint64_t cfg_seed(int cfg, int index) { return 20261201ull + 100ull * (uint64_t)cfg + (uint64_t)index; }
+static std::vector<float> normal(int cfg, int index, int64_t n) {
+    Generator g(cfg_seed(cfg, index));
+    std::vector<float> v((size_t)n);
+    g.fill_normal(v);
+    return v;
+}
+static std::vector<int32_t> ints(int cfg, int index, int64_t n, int lo, int hi) {
+    Generator g(cfg_seed(cfg, index));
+    std::vector<int32_t> v((size_t)n);
+    g.fill_ints(lo, hi, v);
+    return v;
+}
+static int pick(int v, int d) { return v > 0 ? v : d; }
+
+static void build(omt_model &M, int cfg, const omt_scale &sc) {
+    Generator g(cfg_seed(cfg, 0));
+    if (cfg == 1) {
+        const int B = pick(sc.batch, 64);
+        struct Mlp : Module {
+            Linear *l1, *l2;
+        };
+        auto m = std::make_unique<Mlp>();
+        m->l1 = m->child("0", std::make_unique<Linear>(784, 256, g));
+        m->l2 = m->child("2", std::make_unique<Linear>(256, 10, g));
+        Mlp *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, 784}, normal(1, 1, (int64_t)B * 784), false);
+        M.add_int_input("labels", {B}, ints(1, 2, B, 0, 10));
+        M.loss_fn = [mp](omt_model &s) {
+            return cross_entropy((*mp->l2)(relu((*mp->l1)(s.input("x").t))), s.input("labels").t);
+        };
+    } else if (cfg == 2) {
+        const int B = pick(sc.batch, 32), HW = pick(sc.hw, 56);
+        struct ConvNet : Module {
+            Conv2d *conv;
+            Linear *fc;
+        };
+        auto m = std::make_unique<ConvNet>();
+        m->conv = m->child("0", std::make_unique<Conv2d>(64, 64, 3, g, 1));
+        m->fc = m->child("4", std::make_unique<Linear>(64, 10, g));
+        ConvNet *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, 64, HW, HW}, normal(2, 1, (int64_t)B * 64 * HW * HW), true);
+        M.add_int_input("labels", {B}, ints(2, 2, B, 0, 10));
+        M.loss_fn = [mp, B](omt_model &s) {
+            Tensor h = relu((*mp->conv)(s.input("x").t));
+            // GlobalAvgPool2d (Ops.Layers.cs:463-472) = Reshape + Mean(axis 2) + Reshape, then Flatten
+            Tensor gap = reshape(mean_axis(reshape(h, {B, 64, -1}), 2), {B, 64, 1, 1});
+            return cross_entropy((*mp->fc)(reshape(gap, {B, 64})), s.input("labels").t);
+        };
+    } else if (cfg == 3) {
+        const int B = pick(sc.batch, 32), L = pick(sc.seq, 128), D = 384, H = 12, F = 1536;
+        auto m = std::make_unique<PreNormBlock>(D, H, F, g);
+        PreNormBlock *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, L, D}, normal(3, 1, (int64_t)B * L * D), false);
+        M.add_input("target", {B, L, D}, normal(3, 2, (int64_t)B * L * D), false);
+        std::vector<int32_t> len = ints(3, 3, B, L < 64 ? L : 64, L + 1);
+        std::vector<float> mask((size_t)B * L * L, 0.0f);
+        for (int b = 0; b < B; b++)
+            for (int i = 0; i < L; i++)
+                for (int j = len[b]; j < L; j++) mask[((size_t)b * L + i) * L + j] = -INFINITY;
+        M.add_int_input("lengths", {B}, len);
+        M.add_input("mask", {B, L, L}, std::move(mask), false);
+        M.loss_fn = [mp](omt_model &s) {
+            return mse((*mp)(s.input("x").t, s.input("mask").t), s.input("target").t);
+        };
+    } else if (cfg == 4) {
+        const int B = pick(sc.batch, 32);
+        struct Crnn : Module {
+            Conv2d *conv[4];
+            Linear *head;
+        };
+        auto m = std::make_unique<Crnn>();
+        const int ch[5] = {1, 32, 64, 128, 256};
+        for (int i = 0; i < 4; i++)
+            m->conv[i] = m->child(std::to_string(3 * i), std::make_unique<Conv2d>(ch[i], ch[i + 1], 3, g, 1));
+        m->head = m->child("out", std::make_unique<Linear>(256, 37, g));
+        Crnn *mp = m.get();
+        M.root = std::move(m);
+        Generator gx(cfg_seed(4, 1));
+        std::vector<float> x((size_t)B * 32 * 128);
+        gx.fill_uniform(0.0f, 1.0f, x);
+        M.add_input("x", {B, 1, 32, 128}, std::move(x), false);
+        std::vector<int32_t> tl = ints(4, 2, B, 1, 11);
+        int64_t tot = 0;
+        for (int32_t l : tl) tot += l;
+        M.add_int_input("labels", {(int)tot}, ints(4, 3, tot, 1, 37));
+        M.add_int_input("in_len", {B}, std::vector<int32_t>(B, 32));
+        M.add_int_input("tgt_len", {B}, tl);
+        M.loss_fn = [mp](omt_model &s) {
+            static const int pools[4][2] = {{2, 2}, {2, 2}, {2, 1}, {2, 1}};
+            Tensor h = s.input("x").t;
+            for (int i = 0; i < 4; i++) h = max_pool2d(relu((*mp->conv[i])(h)), pools[i][0], pools[i][1], pools[i][0], pools[i][1]);
+            Tensor f = mean_axis(h, 2);        // [B, 256, T]
+            Tensor seq = permute(f, {2, 0, 1});  // [T, B, 256]
+            Tensor lp = log_softmax((*mp->head)(seq));
+            return ctc_loss(lp, s.input("labels").hi, s.input("in_len").hi, s.input("tgt_len").hi, 0, 1);
+        };
+    } else if (cfg == 5) {
+        const int B = pick(sc.batch, 8), L = pick(sc.seq, 512), NL = pick(sc.layers, 4), D = 768, H = 12, F = 3072;
+        struct Bert : Module {
+            std::vector<EncoderLayer *> layers;
+            Linear *head;
+        };
+        auto m = std::make_unique<Bert>();
+        for (int i = 0; i < NL; i++)
+            m->layers.push_back(m->child("layer" + std::to_string(i), std::make_unique<EncoderLayer>(D, H, F, g)));
+        m->head = m->child("head", std::make_unique<Linear>(D, 9, g));
+        Bert *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, L, D}, normal(5, 1, (int64_t)B * L * D), false);
+        M.add_int_input("labels", {B * L}, ints(5, 2, (int64_t)B * L, 0, 9));
+        M.loss_fn = [mp, B, L](omt_model &s) {
+            Tensor h = s.input("x").t;
+            for (EncoderLayer *l : mp->layers) h = (*l)(h, nullptr);
+            return cross_entropy(reshape((*mp->head)(h), {B * L, 9}), s.input("labels").t);
+        };
+    } else {
+        throw Error(OM_E_ARG, "unknown configuration " + std::to_string(cfg));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ C ABI
+static std::string g_create_err;
+
+template <class F>
+static om_status guard(omt_model *m, F f) {
+    try {
+        if (m) set_dev(m->device.get());
+        f();
+        return OM_OK;
+    } catch (const Error &e) {
+        if (m) m->err = e.what();
+        else g_create_err = e.what();
+        return e.code;
+    } catch (const std::exception &e) {
+        if (m) m->err = e.what();
+        else g_create_err = e.what();
+        return OM_E_STATE;
+    }
+}
+
+extern "C" {
+
+om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out) {
+    if (!out) return OM_E_ARG;
+    *out = nullptr;
+    auto *m = new omt_model();
+    om_status s = guard(nullptr, [&] {
+        m->device = std::make_unique<Device>(device);
+        set_dev(m->device.get());
+        omt_scale sc{0, 0, 0, 0};
+        if (scale) sc = *scale;
+        build(*m, cfg, sc);
+        std::vector<std::vector<float>> init;
+        m->root->take_init(init);
+        m->finalize(std::move(init));
+    });
+    if (s != OM_OK) {
+        delete m;
+        return s;
+    }
+    *out = m;
+    return OM_OK;
+}
+
+void omt_destroy(omt_model *m) {
+    if (!m) return;
+    set_dev(m->device.get());
+    m->root.reset();
+    m->params.clear();
+    m->leaves.clear();
+    m->inputs.clear();
+    m->device.reset();
+    set_dev(nullptr);
+    delete m;
+}
+
+const char *omt_last_error(omt_model *m) { return m ? m->err.c_str() : g_create_err.c_str(); }
+
+om_status omt_step(omt_model *m, float *loss) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        float v = m->step();
+        if (loss) *loss = v;
+    });
+}
+om_status omt_forward_backward(omt_model *m, float *loss) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        float v = m->forward_backward();
+        settle_grads(m->leaves);
+        if (loss) *loss = v;
+    });
+}
+om_status omt_optimizer_step(omt_model *m) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        m->optimizer_step();
+        m->device->sync();
+    });
+}
+om_ctx *omt_ctx(omt_model *m) { return m ? m->device->ctx() : nullptr; }
+
+int omt_param_count(omt_model *m) { return m ? (int)m->params.size() : 0; }
+om_status omt_param_info(omt_model *m, int i, char *name, int cap, int *ndim, int32_t *dims) {
+    if (!m || i < 0 || i >= (int)m->params.size()) return OM_E_ARG;
+    const auto &p = m->params[i];
+    if (name && cap > 0) {
+        std::strncpy(name, p.first.c_str(), (size_t)cap - 1);
+        name[cap - 1] = 0;
+    }
+    if (ndim) *ndim = (int)p.second->shape.size();
+    if (dims)
+        for (size_t d = 0; d < p.second->shape.size(); d++) dims[d] = p.second->shape[d];
+    return OM_OK;
+}
+static float *param_block(omt_model *m, int which) {
+    return which == 0 ? m->pb : which == 1 ? m->gb : which == 2 ? m->mb : which == 3 ? m->vb : nullptr;
+}
+om_status omt_param_read(omt_model *m, int i, int which, float *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->params.size() || !param_block(m, which) || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        if (numel != m->params[i].second->numel) throw Error(OM_E_ARG, "omt_param_read: wrong element count");
+        if (which == 1) settle_grads(m->leaves);
+        check(m->device->ctx(), om_download(m->device->ctx(), host, param_block(m, which) + m->offset[i],
+                                            sizeof(float) * (uint64_t)numel), "download");
+    });
+}
+om_status omt_param_write(omt_model *m, int i, int which, const float *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->params.size() || !param_block(m, which) || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        if (numel != m->params[i].second->numel) throw Error(OM_E_ARG, "omt_param_write: wrong element count");
+        check(m->device->ctx(), om_upload(m->device->ctx(), param_block(m, which) + m->offset[i], host,
+                                          sizeof(float) * (uint64_t)numel), "upload");
+        m->device->sync();
+    });
+}
+int64_t omt_step_count(omt_model *m) { return m ? m->step_count : -1; }
+
+int omt_input_count(omt_model *m) { return m ? (int)m->inputs.size() : 0; }
+om_status omt_input_info(omt_model *m, int i, char *name, int cap, int *is_int, int *ndim, int32_t *dims) {
+    if (!m || i < 0 || i >= (int)m->inputs.size()) return OM_E_ARG;
+    const Input &in = m->inputs[i];
+    if (name && cap > 0) {
+        std::strncpy(name, in.name.c_str(), (size_t)cap - 1);
+        name[cap - 1] = 0;
+    }
+    if (is_int) *is_int = in.is_int ? 1 : 0;
+    if (ndim) *ndim = (int)in.t->shape.size();
+    if (dims)
+        for (size_t d = 0; d < in.t->shape.size(); d++) dims[d] = in.t->shape[d];
+    return OM_OK;
+}
+om_status omt_input_read(omt_model *m, int i, void *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->inputs.size() || !host) return OM_E_ARG;
+    const Input &in = m->inputs[i];
+    if (numel != in.t->numel) return OM_E_ARG;
+    if (in.is_int) std::memcpy(host, in.hi.data(), sizeof(int32_t) * (size_t)numel);
+    else std::memcpy(host, in.hf.data(), sizeof(float) * (size_t)numel);
+    return OM_OK;
+}
+om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->inputs.size() || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        const Input &in = m->inputs[i];
+        if (!in.t->grad || numel != in.t->numel) throw Error(OM_E_ARG, "input has no gradient of that size");
+        settle_grads(m->leaves);
+        check(m->device->ctx(), om_download(m->device->ctx(), host, in.t->grad, sizeof(float) * (uint64_t)numel),
+              "download");
+    });
+}
+
+void omt_generate(uint64_t seed, int kind, float lo, float hi, void *out, int64_t n) {
+    Generator g(seed);
+    if (kind == 2) {
+        std::vector<int32_t> v((size_t)n);
+        g.fill_ints((int32_t)lo, (int32_t)hi, v);
+        std::memcpy(out, v.data(), sizeof(int32_t) * (size_t)n);
+    } else {
+        std::vector<float> v((size_t)n);
+        if (kind == 0) g.fill_uniform(lo, hi, v);
+        else g.fill_normal(v);
+        std::memcpy(out, v.data(), sizeof(float) * (size_t)n);
+    }
+}
+
+}  // extern "C"

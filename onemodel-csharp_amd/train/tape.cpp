@@ -1,0 +1,544 @@
+// The tape: device and step allocator, the reverse-mode engine, and the recording ops.
+#include "tape.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace omt {
+
+void check(om_ctx *ctx, om_status s, const char *what) {
+    if (s != OM_OK) throw Error(s, std::string(what) + ": " + om_last_error(ctx));
+}
+
+namespace {
+thread_local Device *g_dev = nullptr;
+uint64_t g_pass = 0;
+}  // namespace
+
+Device &dev() {
+    if (!g_dev) throw Error(OM_E_STATE, "no device context is installed on this thread");
+    return *g_dev;
+}
+void set_dev(Device *d) { g_dev = d; }
+
+Device::Device(int device) {
+    om_status s = om_ctx_create(device, &ctx_);
+    if (s != OM_OK) throw Error(s, std::string("om_ctx_create: ") + om_last_error(nullptr));
+    check(ctx_, om_arena_reserve(ctx_, 0, 1ull << 30), "om_arena_reserve");
+}
+Device::~Device() {
+    if (ctx_) om_ctx_destroy(ctx_);
+}
+float *Device::step_floats(int64_t n) {
+    void *p = nullptr;
+    check(ctx_, om_alloc(ctx_, OM_REGION_STEP, (uint64_t)(n > 0 ? n : 1) * sizeof(float), &p), "om_alloc");
+    return static_cast<float *>(p);
+}
+int32_t *Device::step_ints(int64_t n) {
+    void *p = nullptr;
+    check(ctx_, om_alloc(ctx_, OM_REGION_STEP, (uint64_t)(n > 0 ? n : 1) * sizeof(int32_t), &p), "om_alloc");
+    return static_cast<int32_t *>(p);
+}
+void *Device::persistent(uint64_t bytes) {
+    void *p = nullptr;
+    check(ctx_, om_alloc(ctx_, OM_REGION_PERSISTENT, bytes, &p), "om_alloc");
+    return p;
+}
+void Device::step_reset() { check(ctx_, om_step_reset(ctx_), "om_step_reset"); }
+void Device::sync() { check(ctx_, om_ctx_sync(ctx_), "om_ctx_sync"); }
+
+int64_t numel_of(const std::vector<int> &shape) {
+    int64_t n = 1;
+    for (int d : shape) n *= d;
+    return n;
+}
+Tensor make(const std::vector<int> &shape) {
+    auto t = std::make_shared<TensorImpl>();
+    t->shape = shape;
+    t->numel = numel_of(shape);
+    t->data = dev().step_floats(t->numel);
+    return t;
+}
+Tensor make_ints(const std::vector<int> &shape) {
+    auto t = std::make_shared<TensorImpl>();
+    t->shape = shape;
+    t->numel = numel_of(shape);
+    t->idata = dev().step_ints(t->numel);
+    return t;
+}
+
+static om_ctx *C() { return dev().ctx(); }
+#define OMT(call) check(C(), (call), #call)
+
+static std::string shape_str(const std::vector<int> &s) {
+    std::string r = "[";
+    for (size_t i = 0; i < s.size(); i++) r += (i ? "," : "") + std::to_string(s[i]);
+    return r + "]";
+}
+[[noreturn]] static void shape_error(const std::string &m) { throw Error(OM_E_ARG, m); }
+
+// ------------------------------------------------------------------------------------------------ engine
+float *Engine::dest(Record &r, int i, int *acc) {
+    *acc = 0;
+    if (i >= (int)r.inputs.size() || !r.needs(i)) return nullptr;
+    TensorImpl &x = *r.inputs[i];
+    if (x.is_leaf()) {
+        // AccumulateLeaf (Engine.cs:292-328): the first gradient creates Grad, later ones add into it.
+        if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
+        *acc = x.grad_live ? 1 : 0;
+        x.grad_live = x.grad_exists = true;
+        return x.grad;
+    }
+    Record &p = *x.grad_fn;
+    if (!p.pending) {
+        p.pending = dev().step_floats(x.numel);
+        p.pending_borrowed = false;
+        return p.pending;
+    }
+    if (p.pending_borrowed) {  // copy-on-write: the buffer belongs to another record's gradient
+        float *nb = dev().step_floats(x.numel);
+        OMT(om_copy(C(), nb, p.pending, sizeof(float) * (uint64_t)x.numel));
+        p.pending = nb;
+        p.pending_borrowed = false;
+    }
+    *acc = 1;  // Engine.AddInto (Engine.cs:331-344)
+    return p.pending;
+}
+
+void Engine::emit_alias(Record &r, int i, const float *g) {
+    if (i >= (int)r.inputs.size() || !r.needs(i)) return;
+    TensorImpl &x = *r.inputs[i];
+    uint64_t bytes = sizeof(float) * (uint64_t)x.numel;
+    if (x.is_leaf()) {
+        if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
+        if (x.grad_live) OMT(om_axpy(C(), 1.0f, g, x.grad, x.numel));
+        else OMT(om_copy(C(), x.grad, g, bytes));
+        x.grad_live = x.grad_exists = true;
+        return;
+    }
+    Record &p = *x.grad_fn;
+    if (!p.pending) {
+        p.pending = const_cast<float *>(g);
+        p.pending_borrowed = true;
+        return;
+    }
+    if (p.pending_borrowed) {
+        float *nb = dev().step_floats(x.numel);
+        OMT(om_add(C(), p.pending, g, nb, x.numel));
+        p.pending = nb;
+        p.pending_borrowed = false;
+        return;
+    }
+    OMT(om_axpy(C(), 1.0f, g, p.pending, x.numel));
+}
+
+void Engine::run(const Tensor &root) {
+    float *g = dev().step_floats(1);
+    OMT(om_fill(C(), g, 1.0f, 1));
+    if (root->is_leaf()) {
+        Record tmp;
+        tmp.inputs = {root};
+        emit_alias(tmp, 0, g);
+        return;
+    }
+    // Reverse topological order: iterative DFS post-order over input edges in input order (Engine.cs:130-158).
+    uint64_t mark = ++g_pass;
+    std::vector<Record *> order;
+    std::vector<std::pair<Record *, size_t>> stack;
+    root->grad_fn->mark = mark;
+    stack.emplace_back(root->grad_fn.get(), 0);
+    while (!stack.empty()) {
+        Record *rec = stack.back().first;
+        size_t next = stack.back().second;
+        if (next < rec->inputs.size()) {
+            stack.back().second = next + 1;
+            const Tensor &x = rec->inputs[next];
+            if (x && x->grad_fn && x->grad_fn->mark != mark) {
+                x->grad_fn->mark = mark;
+                stack.emplace_back(x->grad_fn.get(), 0);
+            }
+        } else {
+            order.push_back(rec);
+            stack.pop_back();
+        }
+    }
+    root->grad_fn->pending = g;
+    root->grad_fn->pending_borrowed = false;
+    for (size_t i = order.size(); i-- > 0;) {
+        Record *r = order[i];
+        float *gi = r->pending;
+        r->pending = nullptr;
+        if (!gi) continue;
+        if (!r->rule) throw Error(OM_E_STATE, std::string("backward ran through a released ") + r->op + " record");
+        r->rule(*this, *r, gi);
+    }
+    // Release the records (BackwardRecord.Release): a second backward through this graph is an error.
+    for (Record *r : order) {
+        r->rule = nullptr;
+        r->inputs.clear();
+    }
+}
+
+void backward(const Tensor &root) {
+    if (!root || !root->requires_grad) throw Error(OM_E_STATE, "Backward needs a tensor that requires gradients.");
+    if (root->numel != 1) throw Error(OM_E_ARG, "Backward without a gradient needs a one-element tensor.");
+    Engine e;
+    e.run(root);
+}
+
+void zero_grad(const std::vector<Tensor> &leaves) {
+    for (const Tensor &t : leaves)
+        if (t->grad_exists) t->grad_live = false;  // the zero fill is deferred (settle_grads)
+}
+void settle_grads(const std::vector<Tensor> &leaves) {
+    for (const Tensor &t : leaves)
+        if (t->grad_exists && !t->grad_live) {
+            OMT(om_zero(C(), t->grad, sizeof(float) * (uint64_t)t->numel));
+            t->grad_live = true;
+        }
+}
+
+// ------------------------------------------------------------------------------------------------ ops
+static bool tracked(std::initializer_list<const Tensor *> xs) {
+    for (const Tensor *x : xs)
+        if (*x && (*x)->requires_grad) return true;
+    return false;
+}
+static void attach(const Tensor &out, const char *op, std::vector<Tensor> inputs,
+                   std::function<void(Engine &, Record &, const float *)> rule) {
+    auto r = std::make_shared<Record>();
+    r->op = op;
+    r->inputs = std::move(inputs);
+    r->rule = std::move(rule);
+    r->out_numel = out->numel;
+    out->requires_grad = true;
+    out->grad_fn = r;
+}
+
+Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
+    if (w->shape.size() != 2 || x->shape.empty() || x->shape.back() != w->shape[1])
+        shape_error("Linear: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w->shape) + " ([out, in]).");
+    const int in = w->shape[1], out = w->shape[0];
+    const int rows = (int)(x->numel / in);
+    std::vector<int> ys = x->shape;
+    ys.back() = out;
+    Tensor y = make(ys);
+    OMT(om_linear_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, rows, in, out));
+    if (tracked({&x, &w, &b})) {
+        std::vector<Tensor> ins{x, w};
+        if (b) ins.push_back(b);
+        attach(y, "Linear", ins, [rows, in, out](Engine &e, Record &r, const float *g) {
+            int ax, aw, ab = 0;
+            float *dx = e.dest(r, 0, &ax);
+            float *dw = e.dest(r, 1, &aw);
+            float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+            OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw, ab));
+        });
+    }
+    return y;
+}
+
+Tensor relu(const Tensor &x) {
+    Tensor y = make(x->shape);
+    OMT(om_relu_fwd(C(), x->data, y->data, x->numel));
+    if (tracked({&x})) {
+        float *yd = y->data;
+        int64_t n = x->numel;
+        attach(y, "Relu", {x}, [yd, n](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_relu_bwd(C(), g, yd, dx, n, a));
+        });
+    }
+    return y;
+}
+
+Tensor gelu(const Tensor &x) {
+    Tensor y = make(x->shape);
+    OMT(om_gelu_fwd(C(), x->data, y->data, x->numel));
+    if (tracked({&x})) {
+        int64_t n = x->numel;
+        attach(y, "Gelu", {x}, [n](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_gelu_bwd(C(), g, r.inputs[0]->data, dx, n, a));
+        });
+    }
+    return y;
+}
+
+Tensor add(const Tensor &a, const Tensor &b) {
+    if (a->shape != b->shape) shape_error("Add: shapes " + shape_str(a->shape) + " and " + shape_str(b->shape) + " differ.");
+    Tensor y = make(a->shape);
+    OMT(om_add(C(), a->data, b->data, y->data, a->numel));
+    if (tracked({&a, &b}))
+        attach(y, "Add", {a, b}, [](Engine &e, Record &r, const float *g) {
+            e.emit_alias(r, 0, g);
+            e.emit_alias(r, 1, g);
+        });
+    return y;
+}
+
+Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, float eps) {
+    const int cols = x->shape.back();
+    if (gamma->shape != std::vector<int>{cols} || beta->shape != std::vector<int>{cols})
+        shape_error("LayerNorm over " + std::to_string(cols) + " features needs gamma and beta of shape [" +
+                    std::to_string(cols) + "].");
+    const int rows = (int)(x->numel / cols);
+    Tensor y = make(x->shape);
+    bool rec = tracked({&x, &gamma, &beta});
+    float *mean = rec ? dev().step_floats(rows) : nullptr;
+    float *rstd = rec ? dev().step_floats(rows) : nullptr;
+    OMT(om_layernorm_fwd(C(), x->data, gamma->data, beta->data, y->data, mean, rstd, rows, cols, eps));
+    if (rec)
+        attach(y, "LayerNorm", {x, gamma, beta}, [rows, cols, mean, rstd](Engine &e, Record &r, const float *g) {
+            int ax, ag, ab;
+            float *dx = e.dest(r, 0, &ax);
+            float *dg = e.dest(r, 1, &ag);
+            float *db = e.dest(r, 2, &ab);
+            if (dg && db && ag != ab) {  // keep one accumulate flag for the pair: materialise the other's zeros
+                if (!ag) OMT(om_zero(C(), dg, sizeof(float) * cols));
+                if (!ab) OMT(om_zero(C(), db, sizeof(float) * cols));
+                ag = ab = 1;
+            }
+            OMT(om_layernorm_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx, dg, db, rows, cols, ax,
+                                 dg ? ag : ab));
+        });
+    return y;
+}
+
+Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &mask, int heads) {
+    if (q->shape.size() != 3 || k->shape != q->shape || v->shape != q->shape || heads < 1 || q->shape[2] % heads)
+        shape_error("Attention needs [B, L, H*D] q/k/v of equal shape, got " + shape_str(q->shape));
+    const int B = q->shape[0], L = q->shape[1], D = q->shape[2] / heads;
+    if (D % 2) shape_error("Attention needs an even head dimension, got " + std::to_string(D));
+    if (mask && mask->shape != std::vector<int>{B, L, L})
+        shape_error("The mask must be [" + std::to_string(B) + "," + std::to_string(L) + "," + std::to_string(L) +
+                    "], not " + shape_str(mask->shape));
+    Tensor o = make(q->shape);
+    float *p = dev().step_floats((int64_t)B * heads * L * L);
+    const float *md = mask ? mask->data : nullptr;
+    OMT(om_attention_fwd(C(), q->data, k->data, v->data, md, 1, o->data, p, B, heads, L, L, D, 0.0f));
+    if (tracked({&q, &k, &v}))
+        attach(o, "Attention", {q, k, v}, [p, B, heads, L, D](Engine &e, Record &r, const float *g) {
+            int a[3];
+            float *d[3];
+            for (int i = 0; i < 3; i++) d[i] = e.dest(r, i, &a[i]);
+            // one accumulate flag per call: outputs whose flag differs go through a temporary
+            int common = a[0];
+            float *tmp[3] = {nullptr, nullptr, nullptr};
+            for (int i = 0; i < 3; i++)
+                if (d[i] && a[i] != common) {
+                    tmp[i] = dev().step_floats(r.inputs[i]->numel);
+                }
+            float *ds = dev().step_floats((int64_t)B * heads * L * L);
+            OMT(om_attention_bwd(C(), r.inputs[0]->data, r.inputs[1]->data, r.inputs[2]->data, p, g,
+                                 tmp[0] ? tmp[0] : d[0], tmp[1] ? tmp[1] : d[1], tmp[2] ? tmp[2] : d[2], ds, B, heads,
+                                 L, L, D, 0.0f, common));
+            for (int i = 0; i < 3; i++)
+                if (tmp[i]) {
+                    if (a[i]) OMT(om_axpy(C(), 1.0f, tmp[i], d[i], r.inputs[i]->numel));
+                    else OMT(om_copy(C(), d[i], tmp[i], sizeof(float) * (uint64_t)r.inputs[i]->numel));
+                }
+        });
+    return o;
+}
+
+Tensor reshape(const Tensor &x, const std::vector<int> &shape) {
+    std::vector<int> s = shape;
+    int64_t known = 1;
+    int infer = -1;
+    for (size_t i = 0; i < s.size(); i++) {
+        if (s[i] == -1) infer = (int)i;
+        else known *= s[i];
+    }
+    if (infer >= 0) s[infer] = (int)(x->numel / (known ? known : 1));
+    if (numel_of(s) != x->numel) shape_error("Cannot reshape " + shape_str(x->shape) + " to " + shape_str(shape));
+    auto y = std::make_shared<TensorImpl>();
+    y->shape = s;
+    y->numel = x->numel;
+    y->data = x->data;  // a view: same memory
+    y->idata = x->idata;
+    if (tracked({&x})) attach(y, "Reshape", {x}, [](Engine &e, Record &r, const float *g) { e.emit_alias(r, 0, g); });
+    return y;
+}
+
+Tensor permute(const Tensor &x, const std::vector<int> &perm) {
+    const int nd = (int)x->shape.size();
+    if ((int)perm.size() != nd) shape_error("Permute: rank mismatch");
+    std::vector<int> ys(nd), inv(nd);
+    for (int i = 0; i < nd; i++) {
+        ys[i] = x->shape[perm[i]];
+        inv[perm[i]] = i;
+    }
+    Tensor y = make(ys);
+    std::vector<int32_t> s32(x->shape.begin(), x->shape.end()), p32(perm.begin(), perm.end());
+    OMT(om_permute(C(), x->data, y->data, nd, s32.data(), p32.data(), 0));
+    if (tracked({&x})) {
+        std::vector<int32_t> yshape(ys.begin(), ys.end()), inv32(inv.begin(), inv.end());
+        attach(y, "Permute", {x}, [yshape, inv32, nd](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_permute(C(), g, dx, nd, yshape.data(), inv32.data(), a));
+        });
+    }
+    return y;
+}
+
+Tensor mean_axis(const Tensor &x, int axis) {
+    const int nd = (int)x->shape.size();
+    int ax = axis < 0 ? axis + nd : axis;
+    if (ax < 0 || ax >= nd) shape_error("Mean: axis out of range");
+    int outer = 1, inner = 1, n = x->shape[ax];
+    std::vector<int> ys;
+    for (int i = 0; i < nd; i++) {
+        if (i < ax) outer *= x->shape[i];
+        if (i > ax) inner *= x->shape[i];
+        if (i != ax) ys.push_back(x->shape[i]);
+    }
+    Tensor y = make(ys);
+    OMT(om_mean_axis(C(), x->data, y->data, outer, n, inner));
+    if (tracked({&x}))
+        attach(y, "Mean", {x}, [outer, n, inner](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_mean_axis_bwd(C(), g, dx, outer, n, inner, a));
+        });
+    return y;
+}
+
+Tensor log_softmax(const Tensor &x) {
+    const int cols = x->shape.back();
+    const int rows = (int)(x->numel / cols);
+    Tensor y = make(x->shape);
+    OMT(om_logsoftmax_fwd(C(), x->data, y->data, rows, cols));
+    if (tracked({&x})) {
+        float *yd = y->data;
+        attach(y, "LogSoftmax", {x}, [yd, rows, cols](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_logsoftmax_bwd(C(), g, yd, dx, rows, cols, a));
+        });
+    }
+    return y;
+}
+
+Tensor cross_entropy(const Tensor &logits, const Tensor &labels) {
+    if (logits->shape.size() != 2 || !labels->idata || labels->shape != std::vector<int>{logits->shape[0]})
+        shape_error("NllLoss needs [N, C] log-probabilities and [N] Int32 targets, not " + shape_str(logits->shape) +
+                    " and " + shape_str(labels->shape));
+    const int rows = logits->shape[0], cols = logits->shape[1];
+    Tensor logp = make(logits->shape);
+    OMT(om_logsoftmax_fwd(C(), logits->data, logp->data, rows, cols));
+    Tensor loss = make({});
+    OMT(om_nll_fwd(C(), logp->data, labels->idata, loss->data, nullptr, rows, cols, 1, -100));
+    if (tracked({&logits})) {
+        float *lp = logp->data;
+        const int32_t *tg = labels->idata;
+        attach(loss, "CrossEntropy", {logits}, [lp, tg, rows, cols](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dz = e.dest(r, 0, &a);
+            OMT(om_xent_bwd(C(), g, lp, tg, dz, rows, cols, 1, -100, a));
+        });
+    }
+    return loss;
+}
+
+Tensor mse(const Tensor &pred, const Tensor &target) {
+    if (pred->shape != target->shape)
+        shape_error("Mse: shapes " + shape_str(pred->shape) + " and " + shape_str(target->shape) + " differ.");
+    const int64_t n = pred->numel;
+    float *diff = dev().step_floats(n);
+    Tensor loss = make({});
+    OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
+    if (tracked({&pred, &target}))
+        attach(loss, "Mse", {pred, target}, [diff, n](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dp = e.dest(r, 0, &a);
+            if (dp) OMT(om_mse_bwd(C(), g, diff, dp, n, a));
+            if (r.needs(1)) {  // Sub backward negates the second input's gradient
+                float *t = dev().step_floats(n);
+                OMT(om_mse_bwd(C(), g, diff, t, n, 0));
+                int b;
+                float *dt = e.dest(r, 1, &b);
+                if (b) OMT(om_axpy(C(), -1.0f, t, dt, n));
+                else OMT(om_scale(C(), -1.0f, t, dt, n));
+            }
+        });
+    return loss;
+}
+
+Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad) {
+    if (x->shape.size() != 4 || w->shape.size() != 4 || w->shape[1] != x->shape[1])
+        shape_error("Conv2d: weights " + shape_str(w->shape) + " do not fit input " + shape_str(x->shape));
+    const int N = x->shape[0], Cin = x->shape[1], H = x->shape[2], W = x->shape[3];
+    const int Cout = w->shape[0], KH = w->shape[2], KW = w->shape[3];
+    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
+    if (OH < 1 || OW < 1) shape_error("Invalid convolution geometry for input " + shape_str(x->shape));
+    Tensor y = make({N, Cout, OH, OW});
+    OMT(om_conv2d_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, N, Cin, H, W, Cout, KH, KW, stride, pad));
+    if (tracked({&x, &w, &b})) {
+        std::vector<Tensor> ins{x, w};
+        if (b) ins.push_back(b);
+        attach(y, "Conv2d", ins, [=](Engine &e, Record &r, const float *g) {
+            int ax, aw, ab = 0;
+            float *dx = e.dest(r, 0, &ax);
+            float *dw = e.dest(r, 1, &aw);
+            float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+            if (dw && db && aw != ab) {
+                if (!aw) OMT(om_zero(C(), dw, sizeof(float) * (uint64_t)r.inputs[1]->numel));
+                if (!ab) OMT(om_zero(C(), db, sizeof(float) * (uint64_t)Cout));
+                aw = ab = 1;
+            }
+            OMT(om_conv2d_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, N, Cin, H, W, Cout, KH, KW,
+                              stride, pad, ax, dw ? aw : ab));
+        });
+    }
+    return y;
+}
+
+Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw) {
+    if (x->shape.size() != 4) shape_error("MaxPool2d needs an (N,C,H,W) input, not " + shape_str(x->shape));
+    const int N = x->shape[0], Cc = x->shape[1], H = x->shape[2], W = x->shape[3];
+    const int OH = (H - kh) / sh + 1, OW = (W - kw) / sw + 1;
+    Tensor y = make({N, Cc, OH, OW});
+    bool rec = tracked({&x});
+    int32_t *idx = rec ? dev().step_ints((int64_t)N * Cc * OH * OW) : nullptr;
+    OMT(om_maxpool_fwd(C(), x->data, y->data, idx, N, Cc, H, W, kh, kw, sh, sw, 0, 0));
+    if (rec)
+        attach(y, "MaxPool2d", {x}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_maxpool_bwd(C(), g, idx, dx, N, Cc, H, W, OH, OW, kh, kw, sh, sw, 0, 0, a));
+        });
+    return y;
+}
+
+Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std::vector<int32_t> &in_len,
+                const std::vector<int32_t> &tgt_len, int blank, int reduction) {
+    if (lp->shape.size() != 3) shape_error("CtcLoss needs log-probabilities [T,B,C], not " + shape_str(lp->shape));
+    const int T = lp->shape[0], B = lp->shape[1], Cc = lp->shape[2];
+    if ((int)in_len.size() != B || (int)tgt_len.size() != B)
+        shape_error("Expected " + std::to_string(B) + " input and target lengths");
+    int32_t *dt = dev().step_ints((int64_t)targets.size());
+    int32_t *dil = dev().step_ints(B);
+    int32_t *dtl = dev().step_ints(B);
+    OMT(om_upload(C(), dt, targets.data(), sizeof(int32_t) * targets.size()));
+    OMT(om_upload(C(), dil, in_len.data(), sizeof(int32_t) * (uint64_t)B));
+    OMT(om_upload(C(), dtl, tgt_len.data(), sizeof(int32_t) * (uint64_t)B));
+    Tensor loss = reduction == 0 ? make({B}) : make({});
+    OMT(om_ctc_fwd(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(), (int)targets.size(), T,
+                   B, Cc, blank, reduction, 0, loss->data));
+    if (tracked({&lp})) {
+        int maxl = 0;
+        for (int32_t l : tgt_len) maxl = l > maxl ? l : maxl;
+        attach(loss, "CtcLoss", {lp}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *d = e.dest(r, 0, &a);
+            OMT(om_ctc_bwd(C(), r.inputs[0]->data, dt, dil, dtl, g, d, maxl, T, B, Cc, blank, reduction, a));
+        });
+    }
+    return loss;
+}
+
+}  // namespace omt

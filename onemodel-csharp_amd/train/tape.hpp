@@ -1,0 +1,201 @@
+// The host-side training tape: the MI355X build's stand-in for the reference's C# autograd layer
+// (src/OneModel/Tensors/Autograd, src/OneModel.Training). It keeps the reference's surface and semantics —
+// tensors that record a backward record per op, Tensor.Backward() over the records in reverse topological order with
+// one pending gradient per record, leaf gradients that accumulate, ZeroGrad, modules registering parameters in order,
+// losses, SGD/Adam/AdamW — and does every piece of arithmetic through the C ABI of libom_hip.so (include/om.h).
+// No tensor data ever lives on the host: inputs cross at step edges, the loss crosses back at the end of a step.
+#pragma once
+
+#include <cstdint>
+#include <functional>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "om.h"
+
+namespace omt {
+
+// Errors raised inside the tape; the C ABI turns them into status codes and messages.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+void check(om_ctx *ctx, om_status s, const char *what);
+
+struct Record;
+struct TensorImpl;
+using Tensor = std::shared_ptr<TensorImpl>;
+using RecordP = std::shared_ptr<Record>;
+
+// A float32 tensor in device memory (row-major, contiguous), or an int32 one (labels, pool indices).
+struct TensorImpl {
+    std::vector<int> shape;
+    int64_t numel = 0;
+    float *data = nullptr;
+    int32_t *idata = nullptr;
+    bool requires_grad = false;
+    RecordP grad_fn;  // null for leaves
+    // Leaf gradient (persistent region, allocated with the parameter arena). `grad_exists` mirrors the reference's
+    // non-empty Tensor.Grad; `grad_live` says the buffer holds this step's values (false right after ZeroGrad, whose
+    // zero fill is deferred until something reads the gradient, so the first emission can overwrite).
+    float *grad = nullptr;
+    bool grad_exists = false;
+    bool grad_live = false;
+    std::string name;
+    bool is_leaf() const { return !grad_fn; }
+};
+
+class Engine;
+// A backward record (BackwardRecord.cs:17-150): inputs in order and the rule that turns the output gradient into
+// gradients for them.
+struct Record {
+    const char *op = "";
+    std::vector<Tensor> inputs;
+    std::function<void(Engine &, Record &, const float *g)> rule;
+    // pending gradient of the output (Engine.cs:129-191)
+    float *pending = nullptr;
+    bool pending_borrowed = false;  // aliases another gradient; copy before writing into it
+    int64_t out_numel = 0;
+    uint64_t mark = 0;
+    bool needs(int i) const { return inputs[i] && inputs[i]->requires_grad; }
+};
+
+// The device context and the step-scoped allocator.
+class Device {
+   public:
+    explicit Device(int device);
+    ~Device();
+    om_ctx *ctx() const { return ctx_; }
+    float *step_floats(int64_t n);
+    int32_t *step_ints(int64_t n);
+    void *persistent(uint64_t bytes);
+    void step_reset();
+    void sync();
+
+   private:
+    om_ctx *ctx_ = nullptr;
+};
+
+Device &dev();            // the device of the current thread's model (set by Model)
+void set_dev(Device *d);  // installs it
+
+Tensor make(const std::vector<int> &shape);                    // step-region float tensor
+Tensor make_ints(const std::vector<int> &shape);               // step-region int32 tensor
+int64_t numel_of(const std::vector<int> &shape);
+
+// The reverse-mode engine (Engine.Execute, Engine.cs:124-207 and Emit/AccumulateLeaf/AddInto, Engine.cs:210-344).
+class Engine {
+   public:
+    // Destination for a freshly computed gradient of input i: the producer's pending buffer or the leaf's gradient,
+    // with *acc telling the kernel to add (C = C + v) instead of overwrite. nullptr when the input needs no gradient.
+    float *dest(Record &r, int i, int *acc);
+    // Hands the incoming gradient itself on to input i (EmitAliased, Engine.cs:245-249): no copy unless it has to
+    // be added to an existing gradient.
+    void emit_alias(Record &r, int i, const float *g);
+    void run(const Tensor &root);
+};
+
+void backward(const Tensor &root);  // Tensor.Backward() of a one-element tensor
+void zero_grad(const std::vector<Tensor> &leaves);
+// Materialises deferred zero fills (before the optimizer reads gradients).
+void settle_grads(const std::vector<Tensor> &leaves);
+
+// ------------------------------------------------------------------------------------------------ ops
+// Each records a backward record when an input requires a gradient (the reference's Ops.*).
+Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b);
+Tensor relu(const Tensor &x);
+Tensor gelu(const Tensor &x);
+Tensor add(const Tensor &a, const Tensor &b);
+Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, float eps);
+// Multi-head attention core over Linear outputs q/k/v [B, L, H*D] (heads interleaved), additive mask [B, L, L] or
+// empty; returns [B, L, H*D]. The reference's Reshape/Permute/Attention/Permute/Reshape with the permutes folded into
+// the kernels' addressing.
+Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &mask, int heads);
+Tensor reshape(const Tensor &x, const std::vector<int> &shape);
+Tensor permute(const Tensor &x, const std::vector<int> &perm);
+Tensor mean_axis(const Tensor &x, int axis);
+Tensor log_softmax(const Tensor &x);
+Tensor cross_entropy(const Tensor &logits, const Tensor &labels);  // Losses.CrossEntropy: NllLoss(LogSoftmax)
+Tensor mse(const Tensor &pred, const Tensor &target);              // Losses.Mse: Mean((pred-target)^2)
+Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad);
+Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw);
+Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std::vector<int32_t> &in_len,
+                const std::vector<int32_t> &tgt_len, int blank, int reduction);
+
+// ------------------------------------------------------------------------------------------------ modules
+// SplitMix64 (Generator.cs:10-48).
+class Generator {
+   public:
+    explicit Generator(uint64_t seed) : s_(seed) {}
+    uint64_t next_u64();
+    float next_single();
+    float uniform(float lo, float hi) { return lo + (hi - lo) * next_single(); }
+    void fill_uniform(float lo, float hi, std::vector<float> &v);
+    void fill_normal(std::vector<float> &v);  // benchmark inputs: Box-Muller in double
+    void fill_ints(int32_t lo, int32_t hi, std::vector<int32_t> &v);
+
+   private:
+    uint64_t s_;
+};
+
+// NnModule (NnModule.cs): parameters in registration order, then children in registration order.
+class Module {
+   public:
+    virtual ~Module() = default;
+    Tensor param(const std::string &name, std::vector<int> shape, std::vector<float> init);
+    template <class M>
+    M *child(const std::string &name, std::unique_ptr<M> m) {
+        M *p = m.get();
+        children_.emplace_back(name, std::move(m));
+        return p;
+    }
+    void named_parameters(std::vector<std::pair<std::string, Tensor>> &out, const std::string &prefix = "") const;
+    // Moves the host initial values out, in named_parameters() order, for the model to upload into its arena.
+    void take_init(std::vector<std::vector<float>> &out);
+
+   private:
+    std::vector<std::pair<std::string, Tensor>> params_;
+    std::vector<std::pair<std::string, std::unique_ptr<Module>>> children_;
+    std::vector<std::vector<float>> init_;  // host values until the parameters are laid out in device memory
+};
+
+class Linear : public Module {
+   public:
+    Linear(int in, int out, Generator &g, bool bias = true);
+    Tensor operator()(const Tensor &x) const { return linear(x, w, b); }
+    Tensor w, b;
+};
+class Conv2d : public Module {
+   public:
+    Conv2d(int cin, int cout, int k, Generator &g, int padding = 0, int stride = 1);
+    Tensor operator()(const Tensor &x) const { return conv2d(x, w, b, stride, pad); }
+    Tensor w, b;
+    int stride, pad;
+};
+class LayerNorm : public Module {
+   public:
+    explicit LayerNorm(int n, float eps = 1e-5f);
+    Tensor operator()(const Tensor &x) const { return layer_norm(x, w, b, eps); }
+    Tensor w, b;
+    float eps;
+};
+class MultiHeadAttention : public Module {
+   public:
+    MultiHeadAttention(int width, int heads, Generator &g);
+    Tensor operator()(const Tensor &x, const Tensor &mask) const;
+    Linear *q, *k, *v, *o;
+    int heads;
+};
+
+// ------------------------------------------------------------------------------------------------ optimizers
+// Optimizer.Step (Optimizers.cs:184-219) over a model's parameter arena.
+class Optimizer {
+   public:
+    virtual ~Optimizer() = default;
+    virtual void step() = 0;
+    int64_t step_count = 0;
+};
+
+}  // namespace omt
