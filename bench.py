@@ -1,0 +1,193 @@
+"""Benchmark: training steps per second of one fwd+bwd+AdamW step of the MiniLM-shaped pre-LN encoder block (C3:
+hidden 384, 12 heads of 32, FFN 1536 GELU, seq 128, batch 32, padding mask, MSE, AdamW) on one MI355X, through the
+C++ tape (lib/libom_train.so) and the gfx950 kernels (lib/libom_hip.so).
+
+A step is ZeroGrad + forward + loss.Backward() + optimizer.Step() + loss readback, on inputs already resident in HBM.
+Prints one JSON line with the throughput, the roofline of the dominant kernel (timed live here with HIP events on the
+library's stream) and the CPU baseline (the oracle's C restatement of the reference CPU path, timed on this host's
+cores on a bounded sample of the same workload).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config 3] [--cpu-seconds S] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "train steps/sec (fwd+bwd+AdamW) at 1 GPU; bwd MFMA util % and HBM GB/s"
+FP32_MFMA_PEAK = 157.3  # TFLOP/s, MI355X dense fp32 matrix
+HBM_PEAK = 8000.0       # GB/s
+
+WORKLOADS = {
+    1: ("C1: MLP 784-256-10, batch 64, CE, AdamW", 64, 0),
+    2: ("C2: Conv2d 3x3 64->64 on 32x64x56x56, ReLU, GAP, Linear 64->10, CE, AdamW", 32, 0),
+    3: ("C3: MiniLM-shaped pre-LN encoder block, hidden 384, 12 heads (d=32), FFN 1536 GELU, seq 128, batch 32, "
+        "padding mask, MSE, AdamW", 32, 128),
+    4: ("C4: CRNN 4 conv3x3+ReLU+maxpool stages (32/64/128/256) on 32x1x32x128, Linear 256->37, CTC, AdamW", 32, 32),
+    5: ("C5: BERT-base-shaped 4 post-LN encoder layers, hidden 768, 12 heads, FFN 3072, seq 512, batch 8, "
+        "token head 768->9, CE, AdamW", 8, 512),
+}
+
+
+def load_pkg():
+    import importlib.util
+    pkg_dir = os.path.join(ROOT, "onemodel-csharp_amd")
+    spec = importlib.util.spec_from_file_location("onemodel_csharp_amd", os.path.join(pkg_dir, "__init__.py"),
+                                                  submodule_search_locations=[pkg_dir])
+    m = importlib.util.module_from_spec(spec)
+    sys.modules["onemodel_csharp_amd"] = m
+    spec.loader.exec_module(m)
+    return m
+
+
+class HipEvents:
+    """hipEvent timing on a given stream through the HIP runtime the library already loaded."""
+
+    def __init__(self):
+        self.hip = C.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def time(self, stream, fn, reps: int) -> float:
+        """Average milliseconds of fn() over reps launches, measured between two events on `stream`."""
+        e0, e1 = C.c_void_p(), C.c_void_p()
+        assert self.hip.hipEventCreate(C.byref(e0)) == 0 and self.hip.hipEventCreate(C.byref(e1)) == 0
+        self.hip.hipEventRecord(e0, stream)
+        for _ in range(reps):
+            fn()
+        self.hip.hipEventRecord(e1, stream)
+        self.hip.hipEventSynchronize(e1)
+        ms = C.c_float()
+        self.hip.hipEventElapsedTime(C.byref(ms), e0, e1)
+        self.hip.hipEventDestroy(e0)
+        self.hip.hipEventDestroy(e1)
+        return ms.value / reps
+
+
+def _dev_buf(L, ctx, n, value):
+    p = C.c_void_p()
+    assert L.om_alloc(ctx, 0, 4 * n, C.byref(p)) == 0, L.om_last_error(ctx)
+    assert L.om_fill(ctx, p, value, n) == 0
+    return p
+
+
+def time_dominant_kernel(pkg, model, ev, reps: int = 50):
+    """The largest GEMM of the C3 step (the FFN weight gradient dW = g^T x, [1536, 384] over K = 4096 tokens: one
+    om_gemm call = the MFMA kernel plus its split-K reduce) timed with HIP events on the model's stream."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    M, N, K = 1536, 384, 4096
+    g, x, dw = _dev_buf(L, ctx, K * M, 0.01), _dev_buf(L, ctx, K * N, 0.02), _dev_buf(L, ctx, M * N, 0.0)
+
+    def launch():
+        st = L.om_gemm(ctx, 1, 0, M, N, K, g, M, x, N, dw, N, None, 0, None)
+        if st != 0:
+            raise RuntimeError(L.om_last_error(ctx).decode())
+
+    for _ in range(5):
+        launch()
+    ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
+    flops = 2.0 * M * N * K
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": "om_gemm TN (FFN dW = g^T x, 1536x384, K=4096) incl. split-K reduce",
+            "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": None, "ms_per_launch": round(ms, 5),
+            "flops_per_launch": flops}
+
+
+def time_adamw(pkg, model, ev, reps: int = 50):
+    """The fused AdamW over C5's parameter count (28.36M) — 28 algorithmic bytes per parameter — on the same stream."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    n = 28_358_409
+    p, g, m, v = (_dev_buf(L, ctx, n + 3, val) for val in (0.5, 1e-3, 0.0, 0.0))
+    ss, sq = C.c_float(), C.c_float()
+    L.om_adam_scalars(1e-3, 0.9, 0.999, 1, C.byref(ss), C.byref(sq))
+
+    def launch():
+        L.om_adam_step(ctx, p, g, m, v, None, n, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, ss, sq)
+
+    for _ in range(3):
+        launch()
+    ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
+    gbs = 28.0 * n / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": "om_adam_step (C5 arena, 28.36M params)", "achieved": round(gbs, 1),
+            "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
+
+
+def cpu_baseline(cfg: int, seconds: float):
+    """The oracle's step (C restatement of the reference CPU path) on this host's cores: as many steps as fit in
+    about `seconds` (at least one), at the benchmark's full size."""
+    from oracle import models
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    oc = models.make_config(cfg)
+    oc.step()  # warm-up (page-in, thread pool)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oc.step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(n / el, 4), "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full-size C{cfg} steps (ZeroGrad+fwd+bwd+AdamW) of oracle/om_oracle.c via oracle/tape.py, "
+                      f"{el:.1f} s, OpenMP {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    pkg = load_pkg()
+    model = pkg.Model(a.config)
+    for _ in range(a.warmup):
+        model.step()
+    pkg.load_hip().om_ctx_sync(model.ctx)
+    t0 = time.perf_counter()
+    loss = None
+    for _ in range(a.steps):
+        loss = model.step()  # each step ends with the loss readback (a stream synchronisation)
+    pkg.load_hip().om_ctx_sync(model.ctx)
+    el = time.perf_counter() - t0
+    sps = a.steps / el
+    desc, batch, seq = WORKLOADS[a.config]
+    out = {
+        "metric": METRIC, "value": round(sps, 3), "unit": "steps/s", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(1000.0 * el / a.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": desc, "global_batch": batch, "seq_len": seq, "parallelism": "none (1 GPU)"},
+        "final_loss": loss,
+    }
+    if not a.no_kernels:
+        ev = HipEvents()
+        out["roofline"] = time_dominant_kernel(pkg, model, ev)
+        out["kernels"] = {"adamw": time_adamw(pkg, model, ev)}
+    if not a.no_cpu:
+        cb = cpu_baseline(a.config, a.cpu_seconds)
+        cb["gpu_over_cpu"] = round(sps / cb["value"], 1)
+        out["cpu_baseline"] = cb
+    model.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -17,6 +17,7 @@ using namespace omg;
 // pixels). Thread t always covers tile row t % ROWS, so its pixel decomposition is computed once per tile.
 template <int ROWS>
 struct LoadIm2colKP {
+    static constexpr bool KLAYOUT = false;
     static constexpr int TOT = ROWS * BK, NE = (TOT + NT - 1) / NT;
     float v[NE];
     int oy, ox;
@@ -58,6 +59,7 @@ struct LoadIm2colKP {
 // B operand of dW: B[k = p][n' = kk] = x[ci][oy*s - pad + ky][ox*s - pad + kx]; rows are kk = (ci, ky, kx).
 template <int ROWS>
 struct LoadIm2colPK {
+    static constexpr bool KLAYOUT = false;
     static constexpr int TOT = ROWS * BK, NE = (TOT + NT - 1) / NT;
     float v[NE];
     int ci, ky, kx;
@@ -102,6 +104,7 @@ struct LoadIm2colPK {
 // zero where no output pixel maps there; rows are input pixels q.
 template <int ROWS>
 struct LoadConvDx {
+    static constexpr bool KLAYOUT = false;
     static constexpr int TOT = ROWS * BK, NE = (TOT + NT - 1) / NT;
     float v[NE];
     int iy, ix;
@@ -147,8 +150,8 @@ struct LoadConvDx {
 // mode 2: dW partial (A = g_n [Cout][P], B = im2col(x_n)^T, C = ws[n*splits + s] [Cout][Cin*KK], K range split s)
 template <int BM, int BN, int MODE, bool VEC>
 __global__ void __launch_bounds__(NT) k_conv(Params p) {
-    __shared__ __attribute__((aligned(16))) float As[2 * BK * (BM + PAD)];
-    __shared__ __attribute__((aligned(16))) float Bs[2 * BK * (BN + PAD)];
+    __shared__ __attribute__((aligned(16))) float As[2 * lds_size<BM, BK, true>()];
+    __shared__ __attribute__((aligned(16))) float Bs[2 * lds_size<BN, BK, false>()];
     const int tiles_n = (p.n + BN - 1) / BN, tiles_m = (p.m + BM - 1) / BM;
     int tm, tn, zz;
     tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
@@ -160,29 +163,29 @@ __global__ void __launch_bounds__(NT) k_conv(Params p) {
     const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
     const float *A = p.a + img * p.sa_outer;  // W (mode 0/1: sa_outer = 0) or g_n (mode 2)
     const float *Bsrc = p.b + img * p.sb_outer;
-    LoadKContig<BM, VEC> la;
-    Tile<BM, BN> t;
+    LoadKContig<BM, BK, VEC> la;
+    Tile<BM, BN, BK, true, false> t;
     const int M = p.m;
     const int64_t lda = p.lda;
     if constexpr (MODE == 0) {
         LoadIm2colKP<BN> lb;
         lb.init(p, n0);
-        run_k<BM, BN>(
-            t, la, lb, [&](LoadKContig<BM, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
+        run_k<BM, BN, BK>(
+            t, la, lb, [&](LoadKContig<BM, BK, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
             [&](LoadIm2colKP<BN> &l, int k0) { l.fetch(p, Bsrc, kend, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
-        store_tile<BM, BN>(p, t, m0, n0, wm0, wn0, lane, p.c + img * p.sc_outer, p.ldc, nullptr, 0);
+        store_tile(p, t, m0, n0, wm0, wn0, lane, p.c + img * p.sc_outer, p.ldc, nullptr, 0);
     } else if constexpr (MODE == 1) {
         LoadConvDx<BN> lb;
         lb.init(p, n0);
-        run_k<BM, BN>(
-            t, la, lb, [&](LoadKContig<BM, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
+        run_k<BM, BN, BK>(
+            t, la, lb, [&](LoadKContig<BM, BK, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
             [&](LoadConvDx<BN> &l, int k0) { l.fetch(p, Bsrc, kend, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
-        store_tile<BM, BN>(p, t, m0, n0, wm0, wn0, lane, p.c + img * p.sc_outer, p.ldc, nullptr, 0);
+        store_tile(p, t, m0, n0, wm0, wn0, lane, p.c + img * p.sc_outer, p.ldc, nullptr, 0);
     } else {
         LoadIm2colPK<BN> lb;
         lb.init(p, n0);
-        run_k<BM, BN>(
-            t, la, lb, [&](LoadKContig<BM, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
+        run_k<BM, BN, BK>(
+            t, la, lb, [&](LoadKContig<BM, BK, VEC> &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
             [&](LoadIm2colPK<BN> &l, int k0) { l.fetch(p, Bsrc, kend, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
         // partial of (image, split) -> ws slot img * splits + split (plain store, reduced in order afterwards)
         Params q = p;
@@ -190,7 +193,7 @@ __global__ void __launch_bounds__(NT) k_conv(Params p) {
         q.alpha = 1.0f;
         q.bias = nullptr;
         q.accumulate = 0;
-        store_tile<BM, BN>(q, t, m0, n0, wm0, wn0, lane, p.ws + (int64_t)zz * p.m * p.n, p.n, nullptr, 0);
+        store_tile(q, t, m0, n0, wm0, wn0, lane, p.ws + (int64_t)zz * p.m * p.n, p.n, nullptr, 0);
     }
 }
 

@@ -129,26 +129,53 @@ __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ par
     if (threadIdx.x == 0) out[0] = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;
 }
 
-// Column sums of a [rows, cols] matrix in double: block (x = column tile of 256, y = row chunk) -> partial[chunk][col];
-// then each column adds its chunk partials in chunk order.
+// Column sums of a [rows, cols] matrix in double. Stage 1: a block covers 64 columns (one per lane, coalesced
+// rows) of a chunk of kColChunk rows; its 4 wavefronts take every 4th row and are combined in LDS in wave order,
+// giving partial[chunk][col]. Stage 2: a wavefront per column adds its chunk partials (lanes, then a fixed butterfly).
+constexpr int kColChunk = 256;
 __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restrict__ g, int rows, int cols,
-                                                           int rows_per_chunk, double *__restrict__ part) {
-    int col = blockIdx.x * kBlock + threadIdx.x;
-    int r0 = blockIdx.y * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
-    if (col >= cols) return;
+                                                           double *__restrict__ part) {
+    __shared__ double sh[kBlock / 64][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int col = blockIdx.x * 64 + lane;
+    const int r0 = blockIdx.y * kColChunk, r1 = min(rows, r0 + kColChunk);
     double acc = 0.0;
-    for (int r = r0; r < r1; r++) acc += (double)g[(int64_t)r * cols + col];
-    part[(int64_t)blockIdx.y * cols + col] = acc;
+    if (col < cols)
+        for (int r = r0 + w; r < r1; r += kBlock / 64) acc += (double)g[(int64_t)r * cols + col];
+    sh[w][lane] = acc;
+    __syncthreads();
+    if (w == 0 && col < cols) {
+        double t = 0.0;
+#pragma unroll
+        for (int q = 0; q < kBlock / 64; q++) t += sh[q][lane];
+        part[(int64_t)blockIdx.y * cols + col] = t;
+    }
 }
-__global__ void __launch_bounds__(kBlock) k_colsum_final(const double *__restrict__ part, int chunks, int cols,
-                                                         float *__restrict__ out, int acc) {
-    int col = blockIdx.x * kBlock + threadIdx.x;
+
+}  // namespace
+
+// A wavefront per column: lanes add chunk partials c = lane, lane+64, ... then a butterfly; used by every two-stage
+// column reduction of the library (bias, LayerNorm and convolution-bias gradients).
+__global__ void __launch_bounds__(256) om_k_chunk_final(const double *__restrict__ part, int chunks, int cols,
+                                                        float *__restrict__ out, int acc) {
+    int col = (blockIdx.x * 256 + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (col >= cols) return;
     double s = 0.0;
-    for (int c = 0; c < chunks; c++) s += part[(int64_t)c * cols + col];
-    float v = (float)s;
-    out[col] = acc ? out[col] + v : v;
+    for (int c = lane; c < chunks; c += 64) s += part[(int64_t)c * cols + col];
+    s = omd::wave_sum(s);
+    if (lane == 0) {
+        float v = (float)s;
+        out[col] = acc ? out[col] + v : v;
+    }
 }
+
+om_status om::chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc) {
+    hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)cols * 64, 256, 1 << 30)), dim3(256), 0,
+                       ctx->stream, part, chunks, cols, out, acc);
+    return OM_LAUNCH_CHECK(ctx, "column reduction");
+}
+
+namespace {
 
 // Mean over the middle axis of [outer, n, inner]. inner == 1: one wavefront per output (contiguous row);
 // otherwise one thread per output (threads along inner read contiguous memory).
@@ -341,17 +368,16 @@ om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mea
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && db && rows >= 0 && cols > 0, "om_colsum: bad arguments");
-    int rpc = rows <= 32 ? (rows > 0 ? rows : 1) : 32;
-    int chunks = rows > 0 ? (rows + rpc - 1) / rpc : 1;
+    if (rows == 0) return om_fill(ctx, db, 0.0f, accumulate ? 0 : cols);
+    int chunks = (rows + kColChunk - 1) / kColChunk;
     float *scr;
     om_status s = om::scratch(ctx, sizeof(double) * (uint64_t)chunks * cols, &scr);
     if (s) return s;
     double *part = reinterpret_cast<double *>(scr);
-    if (rows == 0) return om_fill(ctx, db, 0.0f, accumulate ? 0 : cols);
-    dim3 g1((cols + kBlock - 1) / kBlock, chunks);
-    hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, ctx->stream, g, rows, cols, rpc, part);
-    hipLaunchKernelGGL(k_colsum_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, part, chunks,
-                       cols, db, accumulate);
+    dim3 g1((cols + 63) / 64, chunks);
+    hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, ctx->stream, g, rows, cols, part);
+    hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)cols * 64, kBlock, 1 << 30)), dim3(kBlock), 0,
+                       ctx->stream, part, chunks, cols, db, accumulate);
     return OM_LAUNCH_CHECK(ctx, "om_colsum");
 }
 

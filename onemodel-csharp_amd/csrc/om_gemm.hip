@@ -1,12 +1,23 @@
 // Dense fp32 MFMA GEMM (om_gemm), the Linear layer forward/backward built on it, and the split-K reduction.
+//
+// Tile selection is a function of the shape and the CU count only. Well-aligned operands (every pointer 16-byte
+// aligned, leading dimensions multiples of 4) run the BK = 32 "fast set" of tiles; anything else runs 64 x 64 tiles
+// with element-guarded loads. The chooser prefers tilings whose workgroup count fills whole rounds of the 256 CUs
+// (128 x 192 for 4096 x 1536 gives exactly 256 tiles, 64 x 96 for 4096 x 384 likewise), because a last round that
+// is half empty costs as much as a full one.
+#include <cstdlib>
+#include <cstring>
+
 #include "om_gemm.hpp"
 
 namespace omg {
 
-template <int BM, int BN, bool TA, bool TB, bool VEC>
+template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
 __global__ void __launch_bounds__(NT) k_gemm(Params p) {
-    __shared__ __attribute__((aligned(16))) float As[2 * BK * (BM + PAD)];
-    __shared__ __attribute__((aligned(16))) float Bs[2 * BK * (BN + PAD)];
+    using LA = typename std::conditional<TA, LoadRContig<BM, BKT, VEC>, LoadKContig<BM, BKT, VEC>>::type;
+    using LB = typename std::conditional<TB, LoadKContig<BN, BKT, VEC>, LoadRContig<BN, BKT, VEC>>::type;
+    __shared__ __attribute__((aligned(16))) float As[2 * lds_size<BM, BKT, LA::KLAYOUT>()];
+    __shared__ __attribute__((aligned(16))) float Bs[2 * lds_size<BN, BKT, LB::KLAYOUT>()];
     const int tiles_n = (p.n + BN - 1) / BN, tiles_m = (p.m + BM - 1) / BM;
     int tm, tn, zz;
     tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
@@ -22,17 +33,15 @@ __global__ void __launch_bounds__(NT) k_gemm(Params p) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
 
-    using LA = typename std::conditional<TA, LoadRContig<BM, VEC>, LoadKContig<BM, VEC>>::type;
-    using LB = typename std::conditional<TB, LoadKContig<BN, VEC>, LoadRContig<BN, VEC>>::type;
     LA la;
     LB lb;
-    Tile<BM, BN> t;
+    Tile<BM, BN, BKT, LA::KLAYOUT, LB::KLAYOUT> t;
     const int M = p.m, N = p.n;
     const int64_t lda = p.lda, ldb = p.ldb;
-    run_k<BM, BN>(
+    run_k<BM, BN, BKT>(
         t, la, lb, [&](LA &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
         [&](LB &l, int k0) { l.fetch(B, ldb, N, kend, n0, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
-    store_tile<BM, BN>(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
+    store_tile(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
 }
 
 __global__ void k_splitk_reduce(Params p) {
@@ -49,18 +58,28 @@ __global__ void k_splitk_reduce(Params p) {
     }
 }
 
-template <int BM, int BN, bool TA, bool TB, bool VEC>
+template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
 static void launch_t(const Params &p, int batch, hipStream_t st) {
     int64_t tiles = (int64_t)((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
     // One linear grid over (z, m-tile, n-tile), n fastest.
     int64_t total = tiles * batch * p.splits;
-    hipLaunchKernelGGL((k_gemm<BM, BN, TA, TB, VEC>), dim3((unsigned)total), dim3(NT), 0, st, p);
+    hipLaunchKernelGGL((k_gemm<BM, BN, BKT, TA, TB, VEC>), dim3((unsigned)total), dim3(NT), 0, st, p);
 }
 
+// Fast set: aligned operands, BK = 32, the three layouts the training path uses (NN, NT, TN).
 template <int BM, int BN>
-static void launch_bmbn(const Params &p, int batch, bool ta, bool tb, bool vec, hipStream_t st) {
+static bool launch_fast(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+    if (!ta && !tb) launch_t<BM, BN, 32, false, false, true>(p, batch, st);
+    else if (!ta && tb) launch_t<BM, BN, 32, false, true, true>(p, batch, st);
+    else if (ta && !tb) launch_t<BM, BN, 32, true, false, true>(p, batch, st);
+    else return false;
+    return true;
+}
+// General set: any layout and alignment, BK = 16.
+template <int BM, int BN>
+static void launch_general(const Params &p, int batch, bool ta, bool tb, bool vec, hipStream_t st) {
 #define OMG_CASE(TA, TB, V) \
-    if (ta == TA && tb == TB && vec == V) return launch_t<BM, BN, TA, TB, V>(p, batch, st);
+    if (ta == TA && tb == TB && vec == V) return launch_t<BM, BN, 16, TA, TB, V>(p, batch, st);
     OMG_CASE(false, false, false)
     OMG_CASE(false, false, true)
     OMG_CASE(false, true, false)
@@ -72,28 +91,69 @@ static void launch_bmbn(const Params &p, int batch, bool ta, bool tb, bool vec, 
 #undef OMG_CASE
 }
 
-Choice choose(int m, int n, int k, int batch, int cus) {
-    static const int cand[][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-    Choice c{64, 64, 1, k};
-    if (n <= 32) c = Choice{128, 32, 1, k};
-    else if (m <= 32) c = Choice{32, 128, 1, k};
-    else {
-        for (auto &cd : cand) {
-            int64_t tiles = (int64_t)((m + cd[0] - 1) / cd[0]) * ((n + cd[1] - 1) / cd[1]) * batch;
-            if (tiles >= cus) {
-                c = Choice{cd[0], cd[1], 1, k};
-                return c;
+namespace {
+struct Cand {
+    int bm, bn;
+    float eff;  // relative per-tile efficiency (bigger tiles reuse more per LDS byte and per barrier)
+};
+const Cand kFast[] = {{128, 192, 1.00f}, {192, 128, 1.00f}, {128, 128, 0.97f}, {128, 64, 0.85f},
+                      {64, 128, 0.85f},  {64, 96, 0.78f},   {96, 64, 0.78f},   {64, 64, 0.70f}};
+
+// Optional override for tuning runs: OM_GEMM_TILE="bm,bn[,splits]".
+bool env_override(Choice &c, int k) {
+    static const char *s = std::getenv("OM_GEMM_TILE");
+    if (!s || !*s) return false;
+    int bm = 0, bn = 0, sp = 1;
+    if (sscanf(s, "%d,%d,%d", &bm, &bn, &sp) < 2) return false;
+    for (const Cand &cd : kFast)
+        if (cd.bm == bm && cd.bn == bn) {
+            c = Choice{bm, bn, 1, k};
+            if (sp > 1) {
+                int ks = ((k + sp - 1) / sp + 31) / 32 * 32;
+                c.splits = (k + ks - 1) / ks;
+                c.k_split = ks;
             }
+            return true;
+        }
+    return false;
+}
+}  // namespace
+
+// Measured on MI355X over the training path's shapes (64 x 64 and 64 x 96 tiles run the most workgroups per CU at
+// once, which hides the global-load latency best): a single product whose 64 x 64 tiling leaves fewer than two
+// workgroups per CU and whose K is long splits K so that about six workgroups per CU are in flight (split count a
+// power of two, at least 256 k per split, partial products reduced in a fixed order); otherwise 64 x 96 when N is a
+// multiple of 96 (4096 x 384 becomes exactly 256 tiles), else 64 x 64.
+Choice choose_fast(int m, int n, int k, int batch, int cus) {
+    Choice best{64, 64, 1, k};
+    if (env_override(best, k)) return best;
+    int64_t tiles64 = (int64_t)((m + 63) / 64) * ((n + 63) / 64) * batch;
+    if (batch == 1 && tiles64 < 2 * cus && k >= 1024) {
+        int64_t want = (6 * (int64_t)cus + tiles64 - 1) / tiles64;
+        int s = 1;
+        while (s < want && s < 16 && k / (2 * s) >= 256) s *= 2;
+        if (s > 1) {
+            int ks = ((k + s - 1) / s + 31) / 32 * 32;
+            best.splits = (k + ks - 1) / ks;
+            best.k_split = ks;
+            return best;
         }
     }
-    // Too few tiles to fill the chip: split K (single product only), deterministic fixed-order reduce afterwards.
-    int64_t tiles = (int64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * batch;
-    if (batch == 1 && k >= 512) {
-        int want = (int)((2 * cus + tiles - 1) / tiles);
+    if (n % 96 == 0 && m >= 64) best.bn = 96;
+    return best;
+}
+
+Choice choose(int m, int n, int k, int batch, int cus) {
+    if (n <= 32) return Choice{128, 32, 1, k};
+    if (m <= 32) return Choice{32, 128, 1, k};
+    Choice c{64, 64, 1, k};
+    int64_t tiles = (int64_t)((m + 63) / 64) * ((n + 63) / 64) * batch;
+    if (batch == 1 && tiles < cus && k >= 1024) {
+        int want = (int)((cus + tiles - 1) / tiles);
         int maxs = k / 256;
         int s = want < maxs ? want : maxs;
         if (s > 1) {
-            int ks = ((k + s - 1) / s + BK - 1) / BK * BK;
+            int ks = ((k + s - 1) / s + 15) / 16 * 16;
             c.splits = (k + ks - 1) / ks;
             c.k_split = ks;
         }
@@ -106,10 +166,11 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     p.batch = batch;
     bool vec = ((uintptr_t)p.a % 16 == 0) && ((uintptr_t)p.b % 16 == 0) && p.lda % 4 == 0 && p.ldb % 4 == 0 &&
                p.sa_outer % 4 == 0 && p.sa_inner % 4 == 0 && p.sb_outer % 4 == 0 && p.sb_inner % 4 == 0;
-    Choice c = p.k > 0 ? choose(p.m, p.n, p.k, batch, ctx->num_cus) : Choice{64, 64, 1, 1};
-    if (p.k <= 0) {  // empty product: C = epilogue(0)
-        c.k_split = 1;
-    }
+    bool fast = vec && !(ta && tb) && p.k > 0 && p.m > 32 && p.n > 32 && p.m % 4 == 0 && p.n % 4 == 0 &&
+                p.k % 4 == 0;
+    Choice c = p.k <= 0 ? Choice{64, 64, 1, 1}
+                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ctx->num_cus)
+                                : choose(p.m, p.n, p.k, batch, ctx->num_cus));
     p.splits = c.splits;
     p.k_split = c.splits > 1 ? c.k_split : (p.k > 0 ? p.k : 1);
     p.ws = nullptr;
@@ -120,12 +181,21 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
         if (s) return s;
         p.ws = ws;
     }
-    if (c.bm == 128 && c.bn == 128) launch_bmbn<128, 128>(p, batch, ta, tb, vec, ctx->stream);
-    else if (c.bm == 128 && c.bn == 64) launch_bmbn<128, 64>(p, batch, ta, tb, vec, ctx->stream);
-    else if (c.bm == 64 && c.bn == 128) launch_bmbn<64, 128>(p, batch, ta, tb, vec, ctx->stream);
-    else if (c.bm == 128 && c.bn == 32) launch_bmbn<128, 32>(p, batch, ta, tb, vec, ctx->stream);
-    else if (c.bm == 32 && c.bn == 128) launch_bmbn<32, 128>(p, batch, ta, tb, vec, ctx->stream);
-    else launch_bmbn<64, 64>(p, batch, ta, tb, vec, ctx->stream);
+    hipStream_t st = ctx->stream;
+    if (fast) {
+        if (c.bm == 128 && c.bn == 192) launch_fast<128, 192>(p, batch, ta, tb, st);
+        else if (c.bm == 192 && c.bn == 128) launch_fast<192, 128>(p, batch, ta, tb, st);
+        else if (c.bm == 128 && c.bn == 128) launch_fast<128, 128>(p, batch, ta, tb, st);
+        else if (c.bm == 128 && c.bn == 64) launch_fast<128, 64>(p, batch, ta, tb, st);
+        else if (c.bm == 64 && c.bn == 128) launch_fast<64, 128>(p, batch, ta, tb, st);
+        else if (c.bm == 64 && c.bn == 96) launch_fast<64, 96>(p, batch, ta, tb, st);
+        else if (c.bm == 96 && c.bn == 64) launch_fast<96, 64>(p, batch, ta, tb, st);
+        else launch_fast<64, 64>(p, batch, ta, tb, st);
+    } else {
+        if (c.bm == 128 && c.bn == 32) launch_general<128, 32>(p, batch, ta, tb, vec, st);
+        else if (c.bm == 32 && c.bn == 128) launch_general<32, 128>(p, batch, ta, tb, vec, st);
+        else launch_general<64, 64>(p, batch, ta, tb, vec, st);
+    }
     om_status s = OM_LAUNCH_CHECK(ctx, what);
     if (s || p.splits <= 1) return s;
     hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, ctx->stream,

@@ -3,12 +3,19 @@
 //
 // Structure: a workgroup of 256 threads (4 wavefronts, 2 x 2) computes a BM x BN tile of C; each wavefront owns a
 // (BM/2) x (BN/2) sub-tile made of 16 x 16 blocks accumulated by v_mfma_f32_16x16x4_f32 (A fragment: lane l holds
-// A[l%16][l/16]; B fragment: lane l holds B[l/16][l%16]; result: lane l holds C[4*(l/16)+r][l%16], r = 0..3).
-// K advances in chunks of BK = 16 staged through LDS, double-buffered: while the MFMAs consume chunk t from one LDS
-// buffer, the global loads of chunk t+1 are in flight in registers and land in the other buffer. LDS holds both
-// operands k-major ([BK][BM+16] and [BK][BN+16]); the +16 pad puts the two k-rows read by one half-wavefront on
-// disjoint banks. Operands are read through "loader" policies, so the same engine runs plain row-major matrices and
-// gathered (im2col) convolution operands without materialising them.
+// A[l%16][k(l/16)]; B fragment: lane l holds B[k(l/16)][l%16]; result: lane l holds C[4*(l/16)+r][l%16]).
+//
+// K advances in chunks of BKT staged through LDS, double-buffered: while the MFMAs consume chunk t from one LDS
+// buffer, the global loads of chunk t+1 are in flight in registers and land in the other buffer.
+//
+// Each operand keeps the LDS layout its global layout gives for free:
+//   - "K layout" [ROWS][BKT+4] for operands whose rows are contiguous along k (A not transposed, B transposed): the
+//     global float4 along k is stored as it is, and a lane reads the four k of its fragment for four MFMA steps with
+//     one ds_read_b128. The +4 pad spreads the 8 lanes of a b128 phase over all 32 banks.
+//   - "R layout" [BKT][ROWS+4] for operands contiguous along their rows (A transposed, B not transposed, and the
+//     gathered convolution operands): float4 stores along the row, one ds_read_b32 per fragment and step.
+// The MFMA k order inside each block of 16 is permuted so that both layouts agree: lane group kl (= l/16) at step s
+// (0..3) holds k = 16*blk + 4*kl + s. The product sums the same terms; only the order of the fp32 additions differs.
 #pragma once
 
 #include "om_internal.hpp"
@@ -17,9 +24,9 @@ namespace omg {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 16;
+constexpr int BK = 16;  // chunk depth of the convolution kernels
 constexpr int NT = 256;
-constexpr int PAD = 16;
+constexpr int PAD = 4;  // row pad (floats) of both LDS layouts
 
 // Everything a kernel instance needs; plain data so it can be passed by value.
 struct Params {
@@ -41,8 +48,8 @@ struct Params {
     const float *mask;  // additive [Lq, Lk] per batch outer index (attention scores)
     int64_t mask_outer_stride;
     int accumulate;
-    // split-K: grid.z = batch * splits; split s covers k in [s*k_split, (s+1)*k_split) and writes its partial sum to
-    // ws + s*m*n (row-major m x n) instead of C; a reduce pass then applies the epilogue.
+    // split-K: grid covers batch * splits; split s covers k in [s*k_split, (s+1)*k_split) and writes its partial
+    // sum to ws + s*m*n (row-major m x n) instead of C; a reduce pass then applies the epilogue.
     int splits;
     int k_split;
     float *ws;
@@ -52,22 +59,23 @@ struct Params {
 };
 
 // ------------------------------------------------------------------------------------------------ loaders
-// A loader fills the LDS tile T[BK][ROWS + PAD] (k-major) for k in [k0, k0 + BK) and rows in [r0, r0 + ROWS) of its
-// logical operand (A: rows are m; B: rows are n). `fetch` issues the global loads into registers, `put` writes them
-// to LDS. Out-of-range elements are zero.
+// A loader fills one LDS buffer for k in [k0, k0 + BKT) and rows in [r0, r0 + ROWS) of its logical operand (A: rows
+// are m; B: rows are n). `fetch` issues the global loads into registers, `put` writes them to LDS. Out-of-range
+// elements are zero. KLAYOUT says which of the two LDS layouts `put` writes.
 
 // Dense operand whose rows are contiguous along k ("A not transposed" [m][k], or "B transposed" [n][k]).
-template <int ROWS, bool VEC>
+template <int ROWS, int BKT, bool VEC>
 struct LoadKContig {
-    static constexpr int TOT = ROWS * BK / 4;          // float4 per chunk
-    static constexpr int NV = (TOT + NT - 1) / NT;     // float4 per thread
+    static constexpr bool KLAYOUT = true;
+    static constexpr int TOT = ROWS * BKT / 4;       // float4 per chunk
+    static constexpr int NV = (TOT + NT - 1) / NT;   // float4 per thread
     float4 v[NV];
     __device__ __forceinline__ void fetch(const float *base, int64_t ld, int rows, int kend, int r0, int k0) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             int f = threadIdx.x + i * NT;
             if (TOT % NT != 0 && f >= TOT) break;
-            int r = f / (BK / 4), kq = (f % (BK / 4)) * 4;
+            int r = f / (BKT / 4), kq = (f % (BKT / 4)) * 4;
             int gr = r0 + r, gk = k0 + kq;
             float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
             if (gr < rows) {
@@ -89,19 +97,17 @@ struct LoadKContig {
         for (int i = 0; i < NV; i++) {
             int f = threadIdx.x + i * NT;
             if (TOT % NT != 0 && f >= TOT) break;
-            int r = f / (BK / 4), kq = (f % (BK / 4)) * 4;
-            T[(kq + 0) * (ROWS + PAD) + r] = v[i].x;
-            T[(kq + 1) * (ROWS + PAD) + r] = v[i].y;
-            T[(kq + 2) * (ROWS + PAD) + r] = v[i].z;
-            T[(kq + 3) * (ROWS + PAD) + r] = v[i].w;
+            int r = f / (BKT / 4), kq = (f % (BKT / 4)) * 4;
+            *reinterpret_cast<float4 *>(&T[r * (BKT + PAD) + kq]) = v[i];
         }
     }
 };
 
 // Dense operand contiguous along its rows ("A transposed" stored [k][m], or "B not transposed" stored [k][n]).
-template <int ROWS, bool VEC>
+template <int ROWS, int BKT, bool VEC>
 struct LoadRContig {
-    static constexpr int TOT = ROWS * BK / 4;
+    static constexpr bool KLAYOUT = false;
+    static constexpr int TOT = ROWS * BKT / 4;
     static constexpr int NV = (TOT + NT - 1) / NT;
     float4 v[NV];
     __device__ __forceinline__ void fetch(const float *base, int64_t ld, int rows, int kend, int r0, int k0) {
@@ -137,9 +143,16 @@ struct LoadRContig {
     }
 };
 
+// LDS floats of one buffer of an operand tile.
+template <int ROWS, int BKT, bool KLAYOUT>
+constexpr int lds_size() {
+    return KLAYOUT ? ROWS * (BKT + PAD) : BKT * (ROWS + PAD);
+}
+
 // ------------------------------------------------------------------------------------------------ engine
-template <int BM, int BN>
+template <int BM, int BN, int BKT, bool AK, bool BKL>
 struct Tile {
+    static_assert(BKT % 16 == 0, "chunk depth must be a multiple of 16");
     static constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 16, TN = WN / 16;
     floatx4 acc[TM][TN];
 
@@ -149,21 +162,33 @@ struct Tile {
 #pragma unroll
             for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    // One BK chunk from LDS: 4 MFMA k-steps of 4.
+    // Four MFMA k-values of one operand fragment for the 16-k block `blk`: k = 16*blk + 4*kl + s, s = 0..3.
+    template <int ROWS, bool KL>
+    __device__ __forceinline__ static floatx4 frag(const float *T, int blk, int row, int kl) {
+        if constexpr (KL) {
+            return *reinterpret_cast<const floatx4 *>(&T[row * (BKT + PAD) + blk * 16 + kl * 4]);
+        } else {
+            const float *p = &T[(blk * 16 + kl * 4) * (ROWS + PAD) + row];
+            return floatx4{p[0], p[ROWS + PAD], p[2 * (ROWS + PAD)], p[3 * (ROWS + PAD)]};
+        }
+    }
+    // One chunk from LDS.
     __device__ __forceinline__ void mma(const float *As, const float *Bs, int wm0, int wn0, int lane) {
         const int ml = lane & 15, kl = lane >> 4;
 #pragma unroll
-        for (int ks = 0; ks < BK / 4; ks++) {
-            float a[TM], b[TN];
+        for (int blk = 0; blk < BKT / 16; blk++) {
+            floatx4 a[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; i++) a[i] = As[(ks * 4 + kl) * (BM + PAD) + wm0 + i * 16 + ml];
+            for (int i = 0; i < TM; i++) a[i] = frag<BM, AK>(As, blk, wm0 + i * 16 + ml, kl);
 #pragma unroll
-            for (int j = 0; j < TN; j++) b[j] = Bs[(ks * 4 + kl) * (BN + PAD) + wn0 + j * 16 + ml];
+            for (int j = 0; j < TN; j++) b[j] = frag<BN, BKL>(Bs, blk, wn0 + j * 16 + ml, kl);
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int s = 0; s < 4; s++)
 #pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
         }
     }
 };
@@ -184,14 +209,14 @@ __device__ __forceinline__ void tile_coords(const Params &p, int tiles_n, int ti
 }
 
 // Epilogue for one accumulator tile: writes C (or the split-K partial).
-template <int BM, int BN>
-__device__ __forceinline__ void store_tile(const Params &p, Tile<BM, BN> &t, int m0, int n0, int wm0, int wn0,
-                                           int lane, float *cbase, int64_t ldc, const float *mask, int split) {
+template <class TL>
+__device__ __forceinline__ void store_tile(const Params &p, TL &t, int m0, int n0, int wm0, int wn0, int lane,
+                                           float *cbase, int64_t ldc, const float *mask, int split) {
     const int col_l = lane & 15, row_l = (lane >> 4) * 4;
 #pragma unroll
-    for (int i = 0; i < Tile<BM, BN>::TM; i++)
+    for (int i = 0; i < TL::TM; i++)
 #pragma unroll
-        for (int j = 0; j < Tile<BM, BN>::TN; j++) {
+        for (int j = 0; j < TL::TN; j++) {
             int col = n0 + wn0 + j * 16 + col_l;
             if (col >= p.n) continue;
 #pragma unroll
@@ -213,13 +238,13 @@ __device__ __forceinline__ void store_tile(const Params &p, Tile<BM, BN> &t, int
 }
 
 // The main loop, generic over the two loaders. `fa(la, k0)` / `fb(lb, k0)` issue the global loads of a chunk.
-template <int BM, int BN, class LA, class LB, class FA, class FB>
-__device__ __forceinline__ void run_k(Tile<BM, BN> &t, LA &la, LB &lb, FA fa, FB fb, int kbeg, int kend, float *As0,
-                                      float *Bs0, int wm0, int wn0, int lane) {
-    constexpr int ASZ = BK * (BM + PAD), BSZ = BK * (BN + PAD);
+template <int BM, int BN, int BKT, class LA, class LB, class FA, class FB>
+__device__ __forceinline__ void run_k(Tile<BM, BN, BKT, LA::KLAYOUT, LB::KLAYOUT> &t, LA &la, LB &lb, FA fa, FB fb,
+                                      int kbeg, int kend, float *As0, float *Bs0, int wm0, int wn0, int lane) {
+    constexpr int ASZ = lds_size<BM, BKT, LA::KLAYOUT>(), BSZ = lds_size<BN, BKT, LB::KLAYOUT>();
     t.zero();
     if (kbeg >= kend) return;
-    int nk = (kend - kbeg + BK - 1) / BK;
+    int nk = (kend - kbeg + BKT - 1) / BKT;
     fa(la, kbeg);
     fb(lb, kbeg);
     la.put(As0);
@@ -229,8 +254,8 @@ __device__ __forceinline__ void run_k(Tile<BM, BN> &t, LA &la, LB &lb, FA fa, FB
         int cur = kt & 1;
         bool more = kt + 1 < nk;
         if (more) {
-            fa(la, kbeg + (kt + 1) * BK);
-            fb(lb, kbeg + (kt + 1) * BK);
+            fa(la, kbeg + (kt + 1) * BKT);
+            fb(lb, kbeg + (kt + 1) * BKT);
         }
         t.mma(As0 + cur * ASZ, Bs0 + cur * BSZ, wm0, wn0, lane);
         if (more) {
@@ -240,8 +265,5 @@ __device__ __forceinline__ void run_k(Tile<BM, BN> &t, LA &la, LB &lb, FA fa, FB
         __syncthreads();
     }
 }
-
-// Fixed-order reduction of split-K partials with the full epilogue. One thread per output element.
-__global__ void k_splitk_reduce(Params p);
 
 }  // namespace omg

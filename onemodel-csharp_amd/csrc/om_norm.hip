@@ -175,15 +175,6 @@ __global__ void __launch_bounds__(kBlock) k_ln_param_partial_wide(const float *_
     if (part_g) part_g[(int64_t)blockIdx.y * cols + col] = a;
     if (part_b) part_b[(int64_t)blockIdx.y * cols + col] = b;
 }
-__global__ void __launch_bounds__(kBlock) k_chunk_final(const double *__restrict__ part, int chunks, int cols,
-                                                        float *__restrict__ out, int acc) {
-    int col = blockIdx.x * kBlock + threadIdx.x;
-    if (col >= cols) return;
-    double s = 0.0;
-    for (int c = 0; c < chunks; c++) s += part[(int64_t)c * cols + col];
-    float v = (float)s;
-    out[col] = acc ? out[col] + v : v;
-}
 
 // Softmax rows, exact flavour (Softmax.cs:70-133): max, e = expNonPositive(x - max), l = Sum16(e), y = e / l.
 __global__ void __launch_bounds__(kBlock) k_softmax_rows(const float *x, float *y, int rows, int cols) {
@@ -371,13 +362,11 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
             hipLaunchKernelGGL(k_ln_param_partial_wide, dim3((cols + kBlock - 1) / kBlock, chunks), dim3(kBlock), 0,
                                ctx->stream, g, x, mean, rstd, pg, pb, rows, cols, rpc);
     }
-    if (dgamma)
-        hipLaunchKernelGGL(k_chunk_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, pg, chunks,
-                           cols, dgamma, acc_params);
-    if (dbeta)
-        hipLaunchKernelGGL(k_chunk_final, dim3((cols + kBlock - 1) / kBlock), dim3(kBlock), 0, ctx->stream, pb, chunks,
-                           cols, dbeta, acc_params);
-    return OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
+    om_status s = OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
+    if (s) return s;
+    if (dgamma && (s = om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params))) return s;
+    if (dbeta && (s = om::chunk_final(ctx, pb, chunks, cols, dbeta, acc_params))) return s;
+    return OM_OK;
 }
 
 om_status om_softmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols) {
