@@ -132,7 +132,7 @@ __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ par
 // Column sums of a [rows, cols] matrix in double. Stage 1: a block covers 64 columns (one per lane, coalesced
 // rows) of a chunk of kColChunk rows; its 4 wavefronts take every 4th row and are combined in LDS in wave order,
 // giving partial[chunk][col]. Stage 2: a wavefront per column adds its chunk partials (lanes, then a fixed butterfly).
-constexpr int kColChunk = 256;
+constexpr int kColChunk = 64;
 __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restrict__ g, int rows, int cols,
                                                            double *__restrict__ part) {
     __shared__ double sh[kBlock / 64][64];
@@ -156,22 +156,32 @@ __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restri
 
 // A wavefront per column: lanes add chunk partials c = lane, lane+64, ... then a butterfly; used by every two-stage
 // column reduction of the library (bias, LayerNorm and convolution-bias gradients).
-__global__ void __launch_bounds__(256) om_k_chunk_final(const double *__restrict__ part, int chunks, int cols,
-                                                        float *__restrict__ out, int acc) {
+__global__ void __launch_bounds__(256) om_k_chunk_final(const double *__restrict__ part, float *__restrict__ out,
+                                                        const double *__restrict__ part2, float *__restrict__ out2,
+                                                        int chunks, int cols, int acc) {
     int col = (blockIdx.x * 256 + threadIdx.x) >> 6, lane = threadIdx.x & 63;
-    if (col >= cols) return;
+    if (col >= 2 * cols || (col >= cols && !part2)) return;
+    const double *src = part;
+    float *dst = out;
+    if (col >= cols) {
+        col -= cols;
+        src = part2;
+        dst = out2;
+    }
     double s = 0.0;
-    for (int c = lane; c < chunks; c += 64) s += part[(int64_t)c * cols + col];
+    for (int c = lane; c < chunks; c += 64) s += src[(int64_t)c * cols + col];
     s = omd::wave_sum(s);
     if (lane == 0) {
         float v = (float)s;
-        out[col] = acc ? out[col] + v : v;
+        dst[col] = acc ? dst[col] + v : v;
     }
 }
 
-om_status om::chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc) {
-    hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)cols * 64, 256, 1 << 30)), dim3(256), 0,
-                       ctx->stream, part, chunks, cols, out, acc);
+om_status om::chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,
+                          const double *part2, float *out2) {
+    int waves = part2 ? 2 * cols : cols;
+    hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)waves * 64, 256, 1 << 30)), dim3(256), 0,
+                       ctx->stream, part, out, part2, out2, chunks, cols, acc);
     return OM_LAUNCH_CHECK(ctx, "column reduction");
 }
 
@@ -376,9 +386,9 @@ om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, 
     double *part = reinterpret_cast<double *>(scr);
     dim3 g1((cols + 63) / 64, chunks);
     hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, ctx->stream, g, rows, cols, part);
-    hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)cols * 64, kBlock, 1 << 30)), dim3(kBlock), 0,
-                       ctx->stream, part, chunks, cols, db, accumulate);
-    return OM_LAUNCH_CHECK(ctx, "om_colsum");
+    s = OM_LAUNCH_CHECK(ctx, "om_colsum");
+    if (s) return s;
+    return om::chunk_final(ctx, part, chunks, cols, db, accumulate);
 }
 
 om_status om_mean_axis(om_ctx *ctx, const float *x, float *y, int outer, int n, int inner) {

@@ -44,17 +44,35 @@ __global__ void __launch_bounds__(NT) k_gemm(Params p) {
     store_tile(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
 }
 
+// Adds the split-K partials in split order and applies the epilogue; four consecutive columns per thread.
 __global__ void k_splitk_reduce(Params p) {
-    int64_t total = (int64_t)p.m * p.n;
+    const int64_t total = (int64_t)p.m * p.n;
+    const int nq = (p.n + 3) / 4;
+    const int64_t quads = (int64_t)p.m * nq;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        int row = (int)(e / p.n), col = (int)(e % p.n);
-        float v = 0.0f;
-        for (int s = 0; s < p.splits; s++) v += p.ws[(int64_t)s * total + e];
-        if (p.alpha != 1.0f) v = v * p.alpha;
-        if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
-        float *dst = p.c + (int64_t)row * p.ldc + col;
-        *dst = p.accumulate ? *dst + v : v;
+    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += stride) {
+        int row = (int)(q / nq), col0 = (int)(q % nq) * 4;
+        int64_t e = (int64_t)row * p.n + col0;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (col0 + 3 < p.n && (p.n & 3) == 0) {
+            for (int s = 0; s < p.splits; s++) {
+                float4 t = *reinterpret_cast<const float4 *>(p.ws + (int64_t)s * total + e);
+                v[0] += t.x;
+                v[1] += t.y;
+                v[2] += t.z;
+                v[3] += t.w;
+            }
+        } else {
+            for (int s = 0; s < p.splits; s++)
+                for (int u = 0; u < 4 && col0 + u < p.n; u++) v[u] += p.ws[(int64_t)s * total + e + u];
+        }
+        for (int u = 0; u < 4 && col0 + u < p.n; u++) {
+            float x = v[u];
+            if (p.alpha != 1.0f) x = x * p.alpha;
+            if (p.bias) x = x + p.bias[p.bias_per_row ? row : col0 + u];
+            float *dst = p.c + (int64_t)row * p.ldc + col0 + u;
+            *dst = p.accumulate ? *dst + x : x;
+        }
     }
 }
 

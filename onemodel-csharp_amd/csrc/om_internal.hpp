@@ -43,8 +43,10 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 // Returns device scratch of at least `bytes` (kept by the context; valid until the next call that grows it, which
 // first synchronises the stream so no in-flight kernel still reads the old buffer).
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
-// out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column.
-om_status chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc);
+// out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column; a second
+// (part2, out2) pair of the same shape is reduced in the same launch when given.
+om_status chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,
+                      const double *part2 = nullptr, float *out2 = nullptr);
 
 inline unsigned grid1d(int64_t n, int block, int64_t max_blocks = 1 << 20) {
     int64_t g = (n + block - 1) / block;

@@ -57,6 +57,54 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd(const float *__restrict__ x, 
     for (int j = t; j < cols; j += 16) yr[j] = omd::canon(((xr[j] - mean) * inv) * gamma[j] + beta[j]);
 }
 
+// The same computation with the block's 16 rows staged through LDS: global traffic is float4-coalesced and the
+// 16-lane strided Sum16 walks run on LDS (row stride cols+16 keeps the four rows of a wavefront on distinct banks);
+// y goes back out through LDS as well. Requires cols % 4 == 0 and cols <= kLnLdsMaxCols.
+constexpr int kLnRows = kBlock / 16;
+constexpr int kLnLdsMaxCols = 960;  // keeps dynamic LDS under 64 KB
+__global__ void __launch_bounds__(kBlock) k_ln_fwd_lds(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta, float *__restrict__ y,
+                                                       float *__restrict__ mean_out, float *__restrict__ rstd_out,
+                                                       int rows, int cols, float eps) {
+    extern __shared__ float sh[];  // [kLnRows][cols + 16]
+    const int ld = cols + 16, c4 = cols >> 2;
+    const int r0 = blockIdx.x * kLnRows;
+    const int nr = min(kLnRows, rows - r0);
+    const int n4 = nr * c4;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (int64_t)r0 * cols);
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+        int r = i / c4, q = i - r * c4;
+        *reinterpret_cast<float4 *>(sh + r * ld + 4 * q) = x4[i];
+    }
+    __syncthreads();
+    const int lr = threadIdx.x >> 4, t = threadIdx.x & 15;
+    if (lr < nr) {
+        float *xr = sh + lr * ld;
+        const float n = (float)cols;
+        float p = 0.0f;
+        for (int j = t; j < cols; j += 16) p += xr[j];
+        float mean = sum16_combine(p) / n;
+        p = 0.0f;
+        for (int j = t; j < cols; j += 16) {
+            float d = xr[j] - mean;
+            p += d * d;
+        }
+        float ssq = sum16_combine(p);
+        float inv = 1.0f / sqrtf(ssq / n + eps);
+        if (t == 0) {
+            if (mean_out) mean_out[r0 + lr] = mean;
+            if (rstd_out) rstd_out[r0 + lr] = inv;
+        }
+        for (int j = t; j < cols; j += 16) xr[j] = omd::canon(((xr[j] - mean) * inv) * gamma[j] + beta[j]);
+    }
+    __syncthreads();
+    float4 *y4 = reinterpret_cast<float4 *>(y + (int64_t)r0 * cols);
+    for (int i = threadIdx.x; i < n4; i += kBlock) {
+        int r = i / c4, q = i - r * c4;
+        y4[i] = *reinterpret_cast<const float4 *>(sh + r * ld + 4 * q);
+    }
+}
+
 // LayerNorm backward (BackwardNn.cs:170-223), cols <= 64*kMaxPer: a wavefront per row, a block per chunk of rows.
 // dx is written per row; the dgamma/dbeta column contributions are kept per lane in double and summed over the
 // block's waves in LDS (fixed order), giving partial[chunk][col] for the second pass.
@@ -330,8 +378,15 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && gamma && beta && y && rows >= 0 && cols > 0, "om_layernorm_fwd: bad arguments");
     if (rows == 0) return OM_OK;
-    hipLaunchKernelGGL(k_ln_fwd, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma, beta, y, mean,
-                       rstd, rows, cols, eps);
+    const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    if (cols % 4 == 0 && cols <= kLnLdsMaxCols && aligned) {
+        const size_t lds = (size_t)kLnRows * (cols + 16) * sizeof(float);
+        hipLaunchKernelGGL(k_ln_fwd_lds, dim3((rows + kLnRows - 1) / kLnRows), dim3(kBlock), lds, ctx->stream, x,
+                           gamma, beta, y, mean, rstd, rows, cols, eps);
+    } else {
+        hipLaunchKernelGGL(k_ln_fwd, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma, beta, y,
+                           mean, rstd, rows, cols, eps);
+    }
     return OM_LAUNCH_CHECK(ctx, "om_layernorm_fwd");
 }
 
@@ -340,7 +395,7 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
                            int acc_params) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
-    const int rpc = 32;
+    const int rpc = 8;  // rows per block: 512 blocks for 4096 rows
     int chunks = (rows + rpc - 1) / rpc;
     bool params = dgamma || dbeta;
     double *pg = nullptr, *pb = nullptr;
@@ -364,8 +419,9 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
     }
     om_status s = OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
     if (s) return s;
-    if (dgamma && (s = om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params))) return s;
-    if (dbeta && (s = om::chunk_final(ctx, pb, chunks, cols, dbeta, acc_params))) return s;
+    if (dgamma && dbeta) return om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params, pb, dbeta);
+    if (dgamma) return om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params);
+    if (dbeta) return om::chunk_final(ctx, pb, chunks, cols, dbeta, acc_params);
     return OM_OK;
 }
 

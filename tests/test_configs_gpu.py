@@ -84,11 +84,14 @@ def test_config_step_parity(pkg, case):
         opt.step()
         for i, t in enumerate(opt.params):
             assert np.array_equal(m.read_param(i).view(np.uint32), t.data.view(np.uint32)), names[i]
-        # independent post-step parameters: device step vs oracle step. Adam divides each gradient by its own
-        # magnitude, so an element whose gradient is within a few rounding errors of zero turns a 1e-7 difference of
-        # the gradient into a visible difference of its step. Elements with |g| >= 1e-4 max|g| (relative gradient error
-        # below 1e-2 at the 1e-5 bar) and elements whose gradient is exactly zero on both sides must agree to 1e-5
-        # scaled; the rest are counted and only bounded by Adam's largest step (2 lr).
+        # independent post-step parameters: device step vs oracle step. Adam's first step moves an element by
+        # lr * g / (|g| + eps), whose derivative in g is lr * eps / (|g| + eps)^2, so a gradient difference within the
+        # 1e-5 gradient bar (|dg| <= 1e-5 max|g|) moves the parameter by at most lr * eps * 1e-5 max|g| / (|g| + eps)^2.
+        # That stays within the 1e-5 post-step bar (1e-5 max|p|) exactly when (|g| + eps)^2 >= lr * eps * max|g| /
+        # max|p|: on those elements, and on elements whose gradient is exactly zero on both sides, the gradient bar
+        # implies the post-step bar and the test asserts it. On the rest (gradients a few eps in size, e.g. bias
+        # elements of a mean loss over 1.5M outputs) no 1e-5 gradient contract can fix the step, so they are counted
+        # and only bounded by Adam's largest step (2 lr).
         oc.opt.step()
         ill_total, n_total, worst_post = 0, 0, 0.0
         for i, p in enumerate(oc.params):
@@ -96,10 +99,12 @@ def test_config_step_parity(pkg, case):
                 continue
             after = m.read_param(i)
             g = p.grad
-            well = (np.abs(g) >= 1e-4 * float(np.max(np.abs(g)))) | ((g == 0) & (grads_dev[i] == 0))
+            pmax = max(float(np.max(np.abs(p.data))), 1e-30)
+            gabs = np.abs(g).astype(np.float64)
+            well = ((gabs + 1e-8) ** 2 >= 1e-3 * 1e-8 * float(np.max(gabs)) / pmax) | ((g == 0) & (grads_dev[i] == 0))
             ill_total += int((~well).sum())
             n_total += well.size
-            e = scaled(after[well], p.data[well])
+            e = float(np.max(np.abs(after[well] - p.data[well]), initial=0.0)) / pmax
             worst_post = max(worst_post, e)
             assert e <= 1e-5, (names[i], e)
             assert np.all(np.abs(after - p.data) <= 2.0 * 1e-3 + 1e-6), names[i]
