@@ -7,7 +7,8 @@ Prints one JSON line with the throughput, the roofline of the dominant kernel (t
 library's stream) and the CPU baseline (the oracle's C restatement of the reference CPU path, timed on this host's
 cores on a bounded sample of the same workload).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config 3] [--cpu-seconds S] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config 3] [--cpu-seconds S] [--no-cpu] [--no-kernels]
+    python bench.py --pmc-probe     # the launches the FETCH_SIZE / WRITE_SIZE counter runs read
 """
 from __future__ import annotations
 
@@ -101,7 +102,7 @@ def time_dominant_kernel(pkg, model, ev, reps: int = 50):
     achieved = flops / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "kernel": "om_gemm TN (FFN dW = g^T x, 1536x384, K=4096) incl. split-K reduce",
             "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": None, "ms_per_launch": round(ms, 5),
+            "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": measured_traffic(), "ms_per_launch": round(ms, 5),
             "flops_per_launch": flops}
 
 
@@ -123,6 +124,38 @@ def time_adamw(pkg, model, ev, reps: int = 50):
     gbs = 28.0 * n / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "kernel": "om_adam_step (C5 arena, 28.36M params)", "achieved": round(gbs, 1),
             "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
+
+
+COPY_PROBE_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dominant_kernel_traffic.json")
+
+
+def pmc_probe(pkg, model):
+    """Launches, in order, three plain device copies of COPY_PROBE_BYTES, three dominant-kernel GEMMs and three AdamW
+    steps, and nothing else, so that a `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE) run over this mode reads the
+    counters of a copy of known size beside those of the kernels it scales."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    n = COPY_PROBE_BYTES // 4
+    src, dst = _dev_buf(L, ctx, n, 1.0), _dev_buf(L, ctx, n, 0.0)
+    L.om_ctx_sync(ctx)
+    for _ in range(3):
+        assert L.om_copy(ctx, dst, src, COPY_PROBE_BYTES) == 0
+    L.om_ctx_sync(ctx)
+    time_dominant_kernel(pkg, model, HipEvents(), reps=3)
+    time_adamw(pkg, model, HipEvents(), reps=3)
+    L.om_ctx_sync(ctx)
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed counter summary (two rocprofv3 --pmc runs of
+    `bench.py --pmc-probe`, each counter scaled by its reading for the known-size copy), or None without one."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return int(t["fetch_bytes"] + t["write_bytes"])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def cpu_baseline(cfg: int, seconds: float):
@@ -153,12 +186,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the launches a counter run needs (no timing line)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
     pkg = load_pkg()
     model = pkg.Model(a.config)
+    if a.pmc_probe:
+        pmc_probe(pkg, model)
+        model.close()
+        return
     for _ in range(a.warmup):
         model.step()
     pkg.load_hip().om_ctx_sync(model.ctx)

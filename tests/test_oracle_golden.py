@@ -119,6 +119,33 @@ def test_cnn_fixture(oracle):
     assert scaled(stats["rv2"], o["out.rv2"]) < 1e-5
 
 
+def test_mse_mean_sub_permute_closed_forms(oracle):
+    """The C3 loss path and the view backward, pinned by closed forms: Mse = Mean((p - t)^2) with the double sum of
+    the squares, dL/dp = 2 (p - t) / n and dL/dt = -dL/dp (one float rounding of each factor apart); Permute backward
+    applies the inverse permutation exactly."""
+    T = oracle
+    rng = np.random.default_rng(11)
+    p = rng.standard_normal((3, 5, 4)).astype(np.float32)
+    t = rng.standard_normal((3, 5, 4)).astype(np.float32)
+    P, Tt = T.Tensor(p.copy(), True), T.Tensor(t.copy(), True)
+    loss = T.mse(P, Tt)
+    d = (p - t).astype(np.float32)
+    assert float(loss.data) == np.float32(np.sum((d * d).astype(np.float64)) / d.size)
+    T.backward(loss)
+    exact = 2.0 * d.astype(np.float64) / d.size
+    assert np.all(np.abs(P.grad - exact) <= 2.0 ** -22 * np.abs(exact))
+    assert np.array_equal(Tt.grad, -P.grad)
+    # a mean over all elements spreads g / n
+    X = T.Tensor(p.copy(), True)
+    T.backward(T.mean_all(X))
+    assert np.all(X.grad == np.float32(1.0) / np.float32(p.size))
+    # permute backward is the inverse permutation, bit for bit
+    X = T.Tensor(p.copy(), True)
+    W = rng.standard_normal((4, 3, 5)).astype(np.float32)
+    T.backward(T.sum_all(T.mul(T.permute(X, (2, 0, 1)), T.Tensor(W))))
+    assert np.array_equal(X.grad, W.transpose(1, 2, 0))
+
+
 def test_mlp_training_curve(oracle):
     from oracle import models
     o = load_golden("training_mlp")
