@@ -82,13 +82,25 @@ def _dev_buf(L, ctx, n, value):
     return p
 
 
+def _dev_rand(L, ctx, n, scale, seed):
+    """A device buffer of n floats drawn from N(0, scale^2): MFMA power, and so the clock the GPU holds, depends on
+    the operand bits, so timing on constant data would flatter the kernel."""
+    import numpy as np
+    h = (np.random.default_rng(seed).standard_normal(n) * scale).astype(np.float32)
+    p = C.c_void_p()
+    assert L.om_alloc(ctx, 0, 4 * n, C.byref(p)) == 0, L.om_last_error(ctx)
+    assert L.om_upload(ctx, p, h.ctypes.data_as(C.c_void_p), 4 * n) == 0, L.om_last_error(ctx)
+    return p
+
+
 def time_dominant_kernel(pkg, model, ev, reps: int = 50):
     """The largest GEMM of the C3 step (the FFN weight gradient dW = g^T x, [1536, 384] over K = 4096 tokens: one
-    om_gemm call = the MFMA kernel plus its split-K reduce) timed with HIP events on the model's stream."""
+    om_gemm call = the MFMA kernel plus its split-K reduce) on random operands, timed with HIP events on the model's
+    stream."""
     L = pkg.load_hip()
     ctx = model.ctx
     M, N, K = 1536, 384, 4096
-    g, x, dw = _dev_buf(L, ctx, K * M, 0.01), _dev_buf(L, ctx, K * N, 0.02), _dev_buf(L, ctx, M * N, 0.0)
+    g, x, dw = _dev_rand(L, ctx, K * M, 1e-3, 1), _dev_rand(L, ctx, K * N, 1.0, 2), _dev_buf(L, ctx, M * N, 0.0)
 
     def launch():
         st = L.om_gemm(ctx, 1, 0, M, N, K, g, M, x, N, dw, N, None, 0, None)
@@ -111,7 +123,8 @@ def time_adamw(pkg, model, ev, reps: int = 50):
     L = pkg.load_hip()
     ctx = model.ctx
     n = 28_358_409
-    p, g, m, v = (_dev_buf(L, ctx, n + 3, val) for val in (0.5, 1e-3, 0.0, 0.0))
+    p, g = _dev_rand(L, ctx, n + 3, 0.05, 3), _dev_rand(L, ctx, n + 3, 1e-3, 4)
+    m, v = _dev_buf(L, ctx, n + 3, 0.0), _dev_buf(L, ctx, n + 3, 0.0)
     ss, sq = C.c_float(), C.c_float()
     L.om_adam_scalars(1e-3, 0.9, 0.999, 1, C.byref(ss), C.byref(sq))
 

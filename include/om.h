@@ -166,6 +166,17 @@ om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const fl
                            const float *g, float *dq, float *dk, float *dv, float *ds, int B, int H, int lq, int lk,
                            int d, float scale, int acc);
 
+/* The same with explicit row strides (in floats): q/k/v rows ld_qkv apart (3*H*D when the three projections are one
+ * packed [rows, 3*H*D] Linear output, so q, k, v are column offsets 0, H*D, 2*H*D into it), o rows ld_o apart, and in
+ * the backward g rows ld_g and dq/dk/dv rows ld_d apart. The two entry points above are these with every stride H*D.
+ * Same reference functions (Ops.Layers.cs:746-807, BackwardNn.cs:636-701; the packing replaces the q/k/v Linear
+ * calls of MultiHeadAttention.Forward, Layers.cs:497-516). */
+om_status om_attention_fwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                              const float *mask, int mask_batched, float *o, int ld_o, float *p, int B, int H, int lq,
+                              int lk, int d, float scale);
+om_status om_attention_bwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                              const float *p, const float *g, int ld_g, float *dq, float *dk, float *dv, int ld_d,
+                              float *ds, int B, int H, int lq, int lk, int d, float scale, int acc);
 /* ---------------------------------------------------------------------------------------------- convolution, pooling */
 /* Ops.Conv2d, groups 1, square stride/padding (Ops.Layers.cs:279-336; Conv.cs:54) as implicit GEMM on MFMA, and
  * ConvBackward (BackwardNn.cs:317-402): dx = col2im(W^T g) as an implicit GEMM over g, dw = g im2col(x) with a

@@ -70,6 +70,8 @@ _OM_SIGS = {
     "om_xent_bwd": [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci],
     "om_attention_fwd": [vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, f32],
     "om_attention_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
+    "om_attention_fwd_ld": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, ci, ci, ci, ci, ci, f32],
+    "om_attention_bwd_ld": [vp, vp, vp, vp, ci, vp, vp, ci, vp, vp, vp, ci, vp, ci, ci, ci, ci, ci, f32, ci],
     "om_conv2d_fwd": [vp, vp, vp, vp, vp] + [ci] * 9,
     "om_conv2d_bwd": [vp, vp, vp, vp, vp, vp, vp] + [ci] * 9 + [ci, ci],
     "om_maxpool_fwd": [vp, vp, vp, vp] + [ci] * 10,

@@ -15,17 +15,18 @@ om_status om_internal_softmax_rows(om_ctx *ctx, float *x, int rows, int cols);
 
 namespace {
 
-// Per-head view of an interleaved [B, L, H, D] tensor as batch item z = b*H + h: rows of stride H*D.
-void head_view(omg::Params &p, int which, const float *base, int L, int H, int D) {
-    int64_t outer = (int64_t)L * H * D, inner = D;
+// Per-head view of a [B, L, (H, D)] tensor whose rows are `ld` floats apart (ld = H*D for a plain Linear output,
+// 3*H*D for a packed q|k|v projection) as batch item z = b*H + h.
+void head_view(omg::Params &p, int which, const float *base, int L, int D, int64_t ld) {
+    int64_t outer = (int64_t)L * ld, inner = D;
     if (which == 0) {
         p.a = base;
-        p.lda = (int64_t)H * D;
+        p.lda = ld;
         p.sa_outer = outer;
         p.sa_inner = inner;
     } else {
         p.b = base;
-        p.ldb = (int64_t)H * D;
+        p.ldb = ld;
         p.sb_outer = outer;
         p.sb_inner = inner;
     }
@@ -60,18 +61,21 @@ om_status check(om_ctx *ctx, const char *what, const void *q, const void *k, con
 
 extern "C" {
 
-om_status om_attention_fwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *mask,
-                           int mask_batched, float *o, float *p, int B, int H, int lq, int lk, int d, float scale) {
+om_status om_attention_fwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                              const float *mask, int mask_batched, float *o, int ld_o, float *p, int B, int H, int lq,
+                              int lk, int d, float scale) {
     OM_CHECK_CTX(ctx);
     om_status s = check(ctx, "om_attention_fwd", q, k, v, B, H, lq, lk, d);
     if (s) return s;
     OM_REQUIRE(ctx, o && p, "om_attention_fwd: NULL output or weights buffer");
+    OM_REQUIRE(ctx, ld_qkv >= H * d && ld_o >= H * d, "om_attention_fwd: row strides %d / %d below H*D = %d", ld_qkv,
+               ld_o, H * d);
     if (scale == 0.0f || scale != scale) scale = 1.0f / sqrtf((float)d);
     // S = scale * Q K^T + mask  -> p
     omg::Params ps = omg::dense_params(lq, lk, d, nullptr, 0, nullptr, 0, p, lk);
     ps.batch_div = H;
-    head_view(ps, 0, q, lq, H, d);
-    head_view(ps, 1, k, lk, H, d);
+    head_view(ps, 0, q, lq, d, ld_qkv);
+    head_view(ps, 1, k, lk, d, ld_qkv);
     ps.sc_outer = (int64_t)H * lq * lk;
     ps.sc_inner = (int64_t)lq * lk;
     ps.alpha = scale;
@@ -81,31 +85,38 @@ om_status om_attention_fwd(om_ctx *ctx, const float *q, const float *k, const fl
     if (s) return s;
     s = om_internal_softmax_rows(ctx, p, B * H * lq, lk);
     if (s) return s;
-    // O = P V -> o in [B, Lq, H, D]
-    omg::Params po = omg::dense_params(lq, d, lk, nullptr, 0, nullptr, 0, o, (int64_t)H * d);
+    // O = P V -> o in [B, Lq, H, D] rows of stride ld_o
+    omg::Params po = omg::dense_params(lq, d, lk, nullptr, 0, nullptr, 0, o, ld_o);
     po.batch_div = H;
     score_view(po, 0, p, H, lq, lk);
-    head_view(po, 1, v, lk, H, d);
-    po.sc_outer = (int64_t)lq * H * d;
+    head_view(po, 1, v, lk, d, ld_qkv);
+    po.sc_outer = (int64_t)lq * ld_o;
     po.sc_inner = d;
     return omg::launch_dense(ctx, po, false, false, B * H, "attention output");
 }
 
-om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *p,
-                           const float *g, float *dq, float *dk, float *dv, float *ds, int B, int H, int lq, int lk,
-                           int d, float scale, int acc) {
+om_status om_attention_fwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *mask,
+                           int mask_batched, float *o, float *p, int B, int H, int lq, int lk, int d, float scale) {
+    return om_attention_fwd_ld(ctx, q, k, v, H * d, mask, mask_batched, o, H * d, p, B, H, lq, lk, d, scale);
+}
+
+om_status om_attention_bwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                              const float *p, const float *g, int ld_g, float *dq, float *dk, float *dv, int ld_d,
+                              float *ds, int B, int H, int lq, int lk, int d, float scale, int acc) {
     OM_CHECK_CTX(ctx);
     om_status s = check(ctx, "om_attention_bwd", q, k, v, B, H, lq, lk, d);
     if (s) return s;
     OM_REQUIRE(ctx, p && g && ds, "om_attention_bwd: NULL weights, gradient or scratch");
+    OM_REQUIRE(ctx, ld_qkv >= H * d && ld_g >= H * d && ld_d >= H * d,
+               "om_attention_bwd: row strides %d / %d / %d below H*D = %d", ld_qkv, ld_g, ld_d, H * d);
     if (scale == 0.0f || scale != scale) scale = 1.0f / sqrtf((float)d);
     const int Z = B * H;
     if (dv) {  // dV = P^T dO : [Lk, D] = [Lq, Lk]^T [Lq, D]
-        omg::Params pv = omg::dense_params(lk, d, lq, nullptr, 0, nullptr, 0, dv, (int64_t)H * d);
+        omg::Params pv = omg::dense_params(lk, d, lq, nullptr, 0, nullptr, 0, dv, ld_d);
         pv.batch_div = H;
         score_view(pv, 0, p, H, lq, lk);
-        head_view(pv, 1, g, lq, H, d);
-        pv.sc_outer = (int64_t)lk * H * d;
+        head_view(pv, 1, g, lq, d, ld_g);
+        pv.sc_outer = (int64_t)lk * ld_d;
         pv.sc_inner = d;
         pv.accumulate = acc;
         s = omg::launch_dense(ctx, pv, true, false, Z, "attention dV");
@@ -115,8 +126,8 @@ om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const fl
     {  // dP = dO V^T : [Lq, Lk] -> ds
         omg::Params pp = omg::dense_params(lq, lk, d, nullptr, 0, nullptr, 0, ds, lk);
         pp.batch_div = H;
-        head_view(pp, 0, g, lq, H, d);
-        head_view(pp, 1, v, lk, H, d);
+        head_view(pp, 0, g, lq, d, ld_g);
+        head_view(pp, 1, v, lk, d, ld_qkv);
         pp.sc_outer = (int64_t)H * lq * lk;
         pp.sc_inner = (int64_t)lq * lk;
         s = omg::launch_dense(ctx, pp, false, true, Z, "attention dP");
@@ -125,28 +136,34 @@ om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const fl
     s = om_internal_attn_ds(ctx, ds, p, Z * lq, lk, scale);
     if (s) return s;
     if (dq) {  // dQ = dS K : [Lq, D] = [Lq, Lk] [Lk, D]
-        omg::Params pq = omg::dense_params(lq, d, lk, nullptr, 0, nullptr, 0, dq, (int64_t)H * d);
+        omg::Params pq = omg::dense_params(lq, d, lk, nullptr, 0, nullptr, 0, dq, ld_d);
         pq.batch_div = H;
         score_view(pq, 0, ds, H, lq, lk);
-        head_view(pq, 1, k, lk, H, d);
-        pq.sc_outer = (int64_t)lq * H * d;
+        head_view(pq, 1, k, lk, d, ld_qkv);
+        pq.sc_outer = (int64_t)lq * ld_d;
         pq.sc_inner = d;
         pq.accumulate = acc;
         s = omg::launch_dense(ctx, pq, false, false, Z, "attention dQ");
         if (s) return s;
     }
     if (dk) {  // dK = dS^T Q : [Lk, D] = [Lq, Lk]^T [Lq, D]
-        omg::Params pk = omg::dense_params(lk, d, lq, nullptr, 0, nullptr, 0, dk, (int64_t)H * d);
+        omg::Params pk = omg::dense_params(lk, d, lq, nullptr, 0, nullptr, 0, dk, ld_d);
         pk.batch_div = H;
         score_view(pk, 0, ds, H, lq, lk);
-        head_view(pk, 1, q, lq, H, d);
-        pk.sc_outer = (int64_t)lk * H * d;
+        head_view(pk, 1, q, lq, d, ld_qkv);
+        pk.sc_outer = (int64_t)lk * ld_d;
         pk.sc_inner = d;
         pk.accumulate = acc;
         s = omg::launch_dense(ctx, pk, true, false, Z, "attention dK");
         if (s) return s;
     }
     return OM_OK;
+}
+
+om_status om_attention_bwd(om_ctx *ctx, const float *q, const float *k, const float *v, const float *p,
+                           const float *g, float *dq, float *dk, float *dv, float *ds, int B, int H, int lq, int lk,
+                           int d, float scale, int acc) {
+    return om_attention_bwd_ld(ctx, q, k, v, H * d, p, g, H * d, dq, dk, dv, H * d, ds, B, H, lq, lk, d, scale, acc);
 }
 
 }  // extern "C"

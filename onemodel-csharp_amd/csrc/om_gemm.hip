@@ -9,6 +9,7 @@
 #include <cstring>
 
 #include "om_gemm.hpp"
+#include "om_gemm_x.hpp"
 
 namespace omg {
 
@@ -109,62 +110,132 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 #undef OMG_CASE
 }
 
-namespace {
-struct Cand {
-    int bm, bn;
-    float eff;  // relative per-tile efficiency (bigger tiles reuse more per LDS byte and per barrier)
-};
-const Cand kFast[] = {{128, 192, 1.00f}, {192, 128, 1.00f}, {128, 128, 0.97f}, {128, 64, 0.85f},
-                      {64, 128, 0.85f},  {64, 96, 0.78f},   {96, 64, 0.78f},   {64, 64, 0.70f}};
+// Tile-exact set (om_gemm_x.hpp): NN, NT, TN.
+template <int BM, int BN, int BKT>
+static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+    const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
+    if (!ta && !tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, false, false>), dim3(total), dim3(NT), 0, st, p);
+    else if (!ta && tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, false, true>), dim3(total), dim3(NT), 0, st, p);
+    else if (ta && !tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false>), dim3(total), dim3(NT), 0, st, p);
+    else return false;
+    return true;
+}
 
-// Optional override for tuning runs: OM_GEMM_TILE="bm,bn[,splits]".
-bool env_override(Choice &c, int k) {
-    static const char *s = std::getenv("OM_GEMM_TILE");
-    if (!s || !*s) return false;
-    int bm = 0, bn = 0, sp = 1;
-    if (sscanf(s, "%d,%d,%d", &bm, &bn, &sp) < 2) return false;
-    for (const Cand &cd : kFast)
-        if (cd.bm == bm && cd.bn == bn) {
-            c = Choice{bm, bn, 1, k};
-            if (sp > 1) {
-                int ks = ((k + sp - 1) / sp + 31) / 32 * 32;
-                c.splits = (k + ks - 1) / ks;
-                c.k_split = ks;
-            }
-            return true;
-        }
+struct XTile {
+    int bm, bn, bkt;
+};
+const XTile kXTiles[] = {{64, 64, 32},  {64, 96, 32},   {96, 64, 32},  {64, 128, 32}, {128, 64, 32},
+                         {128, 128, 32}, {64, 64, 64},  {64, 96, 64},  {128, 128, 64}};
+
+static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+#define OMG_X(BM, BN, BKT) \
+    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT>(p, batch, ta, tb, st);
+    OMG_X(64, 64, 32)
+    OMG_X(64, 96, 32)
+    OMG_X(96, 64, 32)
+    OMG_X(64, 128, 32)
+    OMG_X(128, 64, 32)
+    OMG_X(128, 128, 32)
+    OMG_X(64, 64, 64)
+    OMG_X(64, 96, 64)
+    OMG_X(128, 128, 64)
+#undef OMG_X
     return false;
+}
+
+// Whether tile t covers the product exactly (full tiles, whole chunks per split, 32-bit in-tile offsets).
+static bool x_fits(const XTile &t, const Params &p, int splits, int k_split) {
+    if (p.m % t.bm || p.n % t.bn || p.k % t.bkt || k_split % t.bkt) return false;
+    if (splits > 1 && (int64_t)(splits - 1) * k_split >= p.k) return false;
+    const int64_t ld = p.lda > p.ldb ? p.lda : p.ldb;
+    const int rows = t.bm > t.bn ? t.bm : t.bn;
+    return ld * (rows > t.bkt ? rows : t.bkt) < (int64_t)1 << 31;
+}
+
+namespace {
+// Tuned choices for the products of the training path's configurations (MI355X, random operands, one sweep of
+// the tile-exact kernels over tiles x chunk depths x split counts): exact shape -> tile and split count.
+struct Tuned {
+    int m, n, k;
+    bool ta, tb;
+    int bm, bn, bkt, splits;
+};
+const Tuned kTuned[] = {
+    // Linear forward y = x W^T (NT)
+    {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 64, 64, 1},
+    {4096, 384, 1536, false, true, 64, 96, 32, 1},    {4096, 1152, 384, false, true, 64, 96, 32, 1},
+    {4096, 768, 768, false, true, 64, 64, 32, 1},     {4096, 3072, 768, false, true, 128, 128, 32, 1},
+    {4096, 768, 3072, false, true, 64, 64, 32, 1},    {4096, 2304, 768, false, true, 64, 64, 32, 1},
+    // input gradient dx = g W (NN)
+    {4096, 384, 384, false, false, 64, 96, 32, 1},    {4096, 384, 1536, false, false, 64, 96, 32, 1},
+    {4096, 1536, 384, false, false, 64, 64, 64, 1},   {4096, 384, 1152, false, false, 64, 96, 32, 1},
+    {4096, 768, 768, false, false, 64, 64, 32, 1},    {4096, 768, 3072, false, false, 64, 64, 32, 1},
+    {4096, 3072, 768, false, false, 128, 128, 32, 1}, {4096, 768, 2304, false, false, 64, 64, 32, 1},
+    // weight gradient dW = g^T x (TN), K = tokens
+    {384, 384, 4096, true, false, 64, 96, 32, 8},     {1536, 384, 4096, true, false, 64, 96, 32, 8},
+    {384, 1536, 4096, true, false, 64, 96, 32, 8},    {1152, 384, 4096, true, false, 64, 64, 32, 4},
+    {768, 768, 4096, true, false, 64, 96, 32, 8},     {3072, 768, 4096, true, false, 64, 96, 32, 2},
+    {768, 3072, 4096, true, false, 64, 96, 32, 2},    {2304, 768, 4096, true, false, 64, 96, 32, 2},
+};
+
+// K length of one split: k / splits rounded up to whole chunks.
+int split_len(int k, int splits, int bkt) { return ((k + splits - 1) / splits + bkt - 1) / bkt * bkt; }
+
+Choice with_splits(int bm, int bn, int bkt, int k, int splits) {
+    Choice c{bm, bn, 1, k, bkt};
+    if (splits > 1) {
+        c.k_split = split_len(k, splits, bkt);
+        c.splits = (k + c.k_split - 1) / c.k_split;
+        if (c.splits <= 1) c.k_split = k;
+    }
+    return c;
+}
+
+// Tuning runs: OM_GEMM_X="bm,bn,bkt[,splits]" forces a tile-exact configuration where it fits.
+bool env_override(Choice &c, int k) {
+    static const char *s = std::getenv("OM_GEMM_X");
+    if (!s || !*s || !strcmp(s, "off")) return false;
+    int bm = 0, bn = 0, bk = 32, sp = 1;
+    if (sscanf(s, "%d,%d,%d,%d", &bm, &bn, &bk, &sp) < 3) return false;
+    c = with_splits(bm, bn, bk, k, sp);
+    return true;
+}
+bool x_disabled() {
+    static const char *s = std::getenv("OM_GEMM_X");
+    return s && !strcmp(s, "off");
 }
 }  // namespace
 
-// Measured on MI355X over the training path's shapes (64 x 64 and 64 x 96 tiles run the most workgroups per CU at
-// once, which hides the global-load latency best): a single product whose 64 x 64 tiling leaves fewer than two
-// workgroups per CU and whose K is long splits K so that about six workgroups per CU are in flight (split count a
-// power of two, at least 256 k per split, partial products reduced in a fixed order); otherwise 64 x 96 when N is a
-// multiple of 96 (4096 x 384 becomes exactly 256 tiles), else 64 x 64.
-Choice choose_fast(int m, int n, int k, int batch, int cus) {
-    Choice best{64, 64, 1, k};
+// Aligned operands: the tuned table for the training path's products, else the rule it was distilled into
+// (MI355X measurements, random operands):
+//   - long-K products with few 64 x 64 tiles (weight gradients, K = tokens) split K into a power-of-two number of
+//     slices of at least 256 k, with tiles x splits near three workgroups per CU (64 x 96 tiles when N allows);
+//   - otherwise 64 x 96 when N is a multiple of 96 and its tiles fit in one round of the CUs (4096 x 384 becomes
+//     exactly 256 tiles: one per CU), else 64 x 64 (occupancy 4, best once there are several tiles per CU).
+Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus) {
+    Choice best{64, 64, 1, k, 32};
     if (env_override(best, k)) return best;
-    int64_t tiles64 = (int64_t)((m + 63) / 64) * ((n + 63) / 64) * batch;
-    if (batch == 1 && tiles64 < 2 * cus && k >= 1024) {
-        int64_t want = (6 * (int64_t)cus + tiles64 - 1) / tiles64;
+    if (batch == 1)
+        for (const Tuned &t : kTuned)
+            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
+                return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+    const bool n96 = n % 96 == 0 && m >= 64;
+    int64_t tiles = (int64_t)((m + 63) / 64) * (n96 ? n / 96 : (n + 63) / 64) * batch;
+    if (batch == 1 && tiles < 2 * cus && k >= 1024) {
+        double want = 3.0 * cus / (double)tiles;
         int s = 1;
-        while (s < want && s < 16 && k / (2 * s) >= 256) s *= 2;
-        if (s > 1) {
-            int ks = ((k + s - 1) / s + 31) / 32 * 32;
-            best.splits = (k + ks - 1) / ks;
-            best.k_split = ks;
-            return best;
-        }
+        while (s < 16 && k / (2 * s) >= 256 && 2.0 * s <= want * 1.41421356) s *= 2;
+        if (s > 1) return with_splits(64, n96 ? 96 : 64, 32, k, s);
     }
-    if (n % 96 == 0 && m >= 64) best.bn = 96;
+    int64_t tiles96 = (int64_t)((m + 63) / 64) * ((n + 95) / 96) * batch;
+    if (n96 && tiles96 <= cus) best.bn = 96;
     return best;
 }
 
 Choice choose(int m, int n, int k, int batch, int cus) {
-    if (n <= 32) return Choice{128, 32, 1, k};
-    if (m <= 32) return Choice{32, 128, 1, k};
-    Choice c{64, 64, 1, k};
+    if (n <= 32) return Choice{128, 32, 1, k, 16};
+    if (m <= 32) return Choice{32, 128, 1, k, 16};
+    Choice c{64, 64, 1, k, 16};
     int64_t tiles = (int64_t)((m + 63) / 64) * ((n + 63) / 64) * batch;
     if (batch == 1 && tiles < cus && k >= 1024) {
         int want = (int)((cus + tiles - 1) / tiles);
@@ -186,9 +257,11 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
                p.sa_outer % 4 == 0 && p.sa_inner % 4 == 0 && p.sb_outer % 4 == 0 && p.sb_inner % 4 == 0;
     bool fast = vec && !(ta && tb) && p.k > 0 && p.m > 32 && p.n > 32 && p.m % 4 == 0 && p.n % 4 == 0 &&
                 p.k % 4 == 0;
-    Choice c = p.k <= 0 ? Choice{64, 64, 1, 1}
-                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ctx->num_cus)
+    Choice c = p.k <= 0 ? Choice{64, 64, 1, 1, 16}
+                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus)
                                 : choose(p.m, p.n, p.k, batch, ctx->num_cus));
+    bool use_x = fast && !x_disabled() && x_fits(XTile{c.bm, c.bn, c.bkt}, p, c.splits, c.k_split);
+    if (fast && !use_x && c.bkt != 32) c = with_splits(c.bm, c.bn, 32, p.k, c.splits);  // guarded set: BK = 32
     p.splits = c.splits;
     p.k_split = c.splits > 1 ? c.k_split : (p.k > 0 ? p.k : 1);
     p.ws = nullptr;
@@ -200,7 +273,9 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
         p.ws = ws;
     }
     hipStream_t st = ctx->stream;
-    if (fast) {
+    bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st);
+    if (launched) {
+    } else if (fast) {
         if (c.bm == 128 && c.bn == 192) launch_fast<128, 192>(p, batch, ta, tb, st);
         else if (c.bm == 192 && c.bn == 128) launch_fast<192, 128>(p, batch, ta, tb, st);
         else if (c.bm == 128 && c.bn == 128) launch_fast<128, 128>(p, batch, ta, tb, st);

@@ -1,0 +1,237 @@
+// Tile-exact fp32 MFMA GEMM for gfx950: the kernel the training path's dense products run on.
+//
+// Preconditions, checked on the host: every tile is full (m % BM == 0, n % BN == 0), every split's K range is a
+// multiple of BKT, operands are 16-byte aligned with leading dimensions (and batch strides) multiples of 4. With
+// those, the main loop carries no bounds logic at all: each thread issues a fixed list of float4 global loads and
+// LDS stores per chunk.
+//
+// Pipeline (one workgroup of 4 wavefronts, 2 x 2, each a (BM/2) x (BN/2) sub-tile):
+//   - global loads run two chunks ahead, into two register sets used alternately (the loop is unrolled by two so
+//     the sets are static); the loads of chunk t+2 are in flight while chunk t is multiplied and chunk t+1 is being
+//     written to LDS, which gives each load about two chunks of MFMA time to land;
+//   - LDS is double-buffered, one barrier per chunk;
+//   - inside a chunk, the fragments of 16-k block b+1 are read from LDS while the MFMAs of block b issue.
+// Operand layouts in LDS are those of om_gemm_core.hpp (K layout [rows][BKT+4], R layout [BKT][rows+4]). For an
+// R-layout operand the wavefront's 16-row (or 16-column) MFMA blocks are interleaved: block i of a wavefront's TX
+// blocks covers rows {TX*c + i}, so the TX fragments a lane needs for one k sit side by side and arrive in one wide
+// LDS read (b64 / b96 / b128) instead of TX separate ones; the epilogue maps rows and columns back accordingly, and
+// for an interleaved B a lane's TX output columns are adjacent, so C is written with wide stores.
+#pragma once
+
+#include "om_gemm_core.hpp"
+
+namespace omg {
+namespace gx {
+
+// Exact loader of one operand chunk: ROWS x BKT values (KCONTIG: rows contiguous along k; else along the rows).
+template <int ROWS, int BKT, bool KCONTIG>
+struct Ld {
+    static constexpr int TOT = ROWS * BKT / 4;
+    static_assert(TOT % NT == 0, "a chunk must split evenly over the workgroup");
+    static constexpr int NV = TOT / NT;
+    static constexpr int LDSZ = KCONTIG ? ROWS * (BKT + PAD) : BKT * (ROWS + PAD);
+    const float *base;  // operand origin of this tile (row r0, k 0)
+    int64_t ld;
+    int goff[NV];  // per-load element offset from (r0, k0)
+    int soff[NV];  // per-load LDS offset
+
+    __device__ __forceinline__ Ld(const float *b, int64_t ld_, int r0) : ld(ld_) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            int f = threadIdx.x + i * NT;
+            if constexpr (KCONTIG) {
+                int r = f / (BKT / 4), kq = (f % (BKT / 4)) * 4;
+                goff[i] = (int)(r * ld) + kq;
+                soff[i] = r * (BKT + PAD) + kq;
+            } else {
+                int kk = f / (ROWS / 4), rq = (f % (ROWS / 4)) * 4;
+                goff[i] = (int)(kk * ld) + rq;
+                soff[i] = kk * (ROWS + PAD) + rq;
+            }
+        }
+        base = b + (KCONTIG ? (int64_t)r0 * ld : (int64_t)r0);
+    }
+    __device__ __forceinline__ void fetch(floatx4 (&v)[NV], int k0) const {
+        const float *p = base + (KCONTIG ? (int64_t)k0 : (int64_t)k0 * ld);
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = *reinterpret_cast<const floatx4 *>(p + goff[i]);
+    }
+    __device__ __forceinline__ void put(const floatx4 (&v)[NV], float *T) const {
+#pragma unroll
+        for (int i = 0; i < NV; i++) *reinterpret_cast<floatx4 *>(T + soff[i]) = v[i];
+    }
+};
+
+// Fragments of one 16-k block for TX MFMA blocks of one operand: f[s][x] is the value lane (l%16, kl = l/16) feeds
+// to the MFMA of block x at step s (k = 16*blk + 4*kl + s).
+template <int ROWS, int BKT, int TX, bool KL>
+__device__ __forceinline__ void read_frag(float (&f)[4][TX], const float *T, int blk, int w0, int l16, int kl) {
+    if constexpr (KL) {
+#pragma unroll
+        for (int x = 0; x < TX; x++) {
+            floatx4 v = *reinterpret_cast<const floatx4 *>(&T[(w0 + x * 16 + l16) * (BKT + PAD) + blk * 16 + kl * 4]);
+#pragma unroll
+            for (int s = 0; s < 4; s++) f[s][x] = v[s];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const float *p = &T[(blk * 16 + kl * 4 + s) * (ROWS + PAD) + w0 + TX * l16];
+            if constexpr (TX % 4 == 0) {
+#pragma unroll
+                for (int x = 0; x < TX; x += 4) {
+                    floatx4 v = *reinterpret_cast<const floatx4 *>(p + x);
+                    f[s][x] = v[0];
+                    f[s][x + 1] = v[1];
+                    f[s][x + 2] = v[2];
+                    f[s][x + 3] = v[3];
+                }
+            } else if constexpr (TX % 2 == 0) {
+#pragma unroll
+                for (int x = 0; x < TX; x += 2) {
+                    float2 v = *reinterpret_cast<const float2 *>(p + x);
+                    f[s][x] = v.x;
+                    f[s][x + 1] = v.y;
+                }
+            } else {
+#pragma unroll
+                for (int x = 0; x < TX; x++) f[s][x] = p[x];
+            }
+        }
+    }
+}
+
+template <int BM, int BN, int BKT, bool TA, bool TB>
+__global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
+    constexpr bool AK = !TA, BKL = TB;  // operands in K layout
+    constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
+    using LA = Ld<BM, BKT, AK>;
+    using LB = Ld<BN, BKT, BKL>;
+    __shared__ __attribute__((aligned(16))) float As[2 * LA::LDSZ];
+    __shared__ __attribute__((aligned(16))) float Bs[2 * LB::LDSZ];
+
+    const int tiles_n = p.n / BN, tiles_m = p.m / BM;
+    int tm, tn, zz;
+    tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
+    if (zz >= p.batch * p.splits) return;
+    const int z = zz / p.splits, split = zz % p.splits;
+    const int outer = z / p.batch_div, inner = z % p.batch_div;
+    const float *A = p.a + outer * p.sa_outer + inner * p.sa_inner;
+    const float *B = p.b + outer * p.sb_outer + inner * p.sb_inner;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = split * p.k_split;
+    const int nk = (min(p.k, kbeg + p.k_split) - kbeg) / BKT;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
+    const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const LA la(A, p.lda, m0);
+    const LB lb(B, p.ldb, n0);
+    // Fragment sets for even and odd 16-k blocks.
+    float fa0[4][TM], fb0[4][TN], fa1[4][TM], fb1[4][TN];
+    auto rd = [&](float(&fa)[4][TM], float(&fb)[4][TN], const float *Ab, const float *Bb, int blk) {
+        read_frag<BM, BKT, TM, AK>(fa, Ab, blk, wm0, l16, kl);
+        read_frag<BN, BKT, TN, BKL>(fb, Bb, blk, wn0, l16, kl);
+    };
+    auto mm = [&](const float(&fa)[4][TM], const float(&fb)[4][TN]) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+    };
+    // Blocks 0 .. NB-2 of the chunk in (Ab, Bb): the fragments of block b+1 are read while block b multiplies.
+    auto body = [&](const float *Ab, const float *Bb) {
+#pragma unroll
+        for (int blk = 0; blk + 1 < NB; blk++) {
+            if (blk & 1) rd(fa0, fb0, Ab, Bb, blk + 1);
+            else rd(fa1, fb1, Ab, Bb, blk + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (blk & 1) mm(fa1, fb1);
+            else mm(fa0, fb0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    static_assert(NB % 2 == 0, "chunks hold an even number of 16-k blocks");
+
+    if (nk > 0) {
+        floatx4 ra0[LA::NV], rb0[LB::NV], ra1[LA::NV], rb1[LB::NV];
+        const int klast = kbeg + (nk - 1) * BKT;
+        float *A0 = As, *A1 = As + LA::LDSZ, *B0 = Bs, *B1 = Bs + LB::LDSZ;
+        la.fetch(ra0, kbeg);
+        lb.fetch(rb0, kbeg);
+        la.fetch(ra1, min(kbeg + BKT, klast));
+        lb.fetch(rb1, min(kbeg + BKT, klast));
+        la.put(ra0, A0);
+        lb.put(rb0, B0);
+        __syncthreads();
+        rd(fa0, fb0, A0, B0, 0);
+        // One chunk that has a successor: issue the loads of chunk t+2 into the free register set, multiply blocks
+        // 0 .. NB-2, write chunk t+1 (landed meanwhile) into the other LDS buffer, barrier, read block 0 of chunk
+        // t+1 while the last block of chunk t multiplies. Chunk t sits in buffer t & 1, register set t & 1 is free.
+#define OMG_X_HALF(RA, RB, RAN, RBN, AC, BC, AN, BN_, KF)   \
+    la.fetch(RA, min(KF, klast));                          \
+    lb.fetch(RB, min(KF, klast));                          \
+    __builtin_amdgcn_sched_barrier(0);                     \
+    body(AC, BC);                                          \
+    la.put(RAN, AN);                                       \
+    lb.put(RBN, BN_);                                      \
+    __syncthreads();                                       \
+    rd(fa0, fb0, AN, BN_, 0);                              \
+    __builtin_amdgcn_sched_barrier(0);                     \
+    mm(fa1, fb1);                                          \
+    __builtin_amdgcn_sched_barrier(0);
+        int t = 0;
+        // Both halves of the loop body always run (loads past the last chunk are clamped to it), so the body has
+        // no branch: a branchy body lets the compiler merge the halves and index the register sets dynamically.
+        for (; t + 2 < nk; t += 2) {
+            OMG_X_HALF(ra0, rb0, ra1, rb1, A0, B0, A1, B1, kbeg + (t + 2) * BKT)
+            OMG_X_HALF(ra1, rb1, ra0, rb0, A1, B1, A0, B0, kbeg + (t + 3) * BKT)
+        }
+        const float *Al = A0, *Bl = B0;
+        if (nk - t == 2) {
+            OMG_X_HALF(ra0, rb0, ra1, rb1, A0, B0, A1, B1, klast)
+            Al = A1;
+            Bl = B1;
+        }
+#undef OMG_X_HALF
+        // The last chunk (block 0's fragments are in set 0).
+        body(Al, Bl);
+        mm(fa1, fb1);
+    }
+
+    // Epilogue: output register r of MFMA block (i, j) on this lane is row rho = 4*kl + r, column l16 of the block.
+    float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
+    const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rho = 4 * kl + r;
+            const int row = m0 + wm0 + (AK ? i * 16 + rho : TM * rho + i);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int col = n0 + wn0 + (BKL ? j * 16 + l16 : TN * l16 + j);
+                float v = acc[i][j][r];
+                if (p.splits > 1) {
+                    p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
+                    continue;
+                }
+                if (p.alpha != 1.0f) v = v * p.alpha;
+                if (mask) v = v + mask[(int64_t)row * p.n + col];
+                if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
+                float *dst = C + (int64_t)row * p.ldc + col;
+                *dst = p.accumulate ? *dst + v : v;
+            }
+        }
+}
+
+}  // namespace gx
+}  // namespace omg

@@ -49,6 +49,10 @@ void Module::named_parameters(std::vector<std::pair<std::string, Tensor>> &out, 
     for (auto &p : params_) out.emplace_back(prefix + p.first, p.second);
     for (auto &c : children_) c.second->named_parameters(out, prefix + c.first + ".");
 }
+void Module::colocation_groups(std::vector<std::vector<Tensor>> &out) const {
+    for (auto &g : colocate_) out.push_back(g);
+    for (auto &c : children_) c.second->colocation_groups(out);
+}
 void Module::take_init(std::vector<std::vector<float>> &out) {
     for (auto &v : init_) out.push_back(std::move(v));
     init_.clear();
@@ -81,10 +85,12 @@ MultiHeadAttention::MultiHeadAttention(int width, int heads_, Generator &g) : he
     k = child("k", std::make_unique<Linear>(width, width, g));
     v = child("v", std::make_unique<Linear>(width, width, g));
     o = child("o", std::make_unique<Linear>(width, width, g));
+    colocate({q->w, k->w, v->w});  // one [3W, W] weight and one [3W] bias for the packed projection
+    colocate({q->b, k->b, v->b});
 }
 Tensor MultiHeadAttention::operator()(const Tensor &x, const Tensor &mask) const {
     // Layers.cs:497-516: q/k/v projections, split heads, attention, merge heads, output projection.
-    return (*o)(attention_heads((*q)(x), (*k)(x), (*v)(x), mask, heads));
+    return (*o)(attention_qkv(x, q->w, q->b, k->w, k->b, v->w, v->b, mask, heads));
 }
 
 // Post-norm TransformerEncoderLayer (Layers.cs:523-578).
@@ -141,6 +147,7 @@ struct omt_model {
     std::vector<std::pair<std::string, Tensor>> params;
     std::vector<Tensor> leaves;  // params + inputs that require gradients
     std::vector<int64_t> offset;
+    std::vector<int> phys;  // parameter indices in arena order
     int64_t total = 0;
     float *pb = nullptr, *gb = nullptr, *mb = nullptr, *vb = nullptr;
     std::vector<Input> inputs;
@@ -193,11 +200,38 @@ struct omt_model {
     // gradients, first and second moments; uploads the initial values once.
     void finalize(std::vector<std::vector<float>> &&init) {
         root->named_parameters(params);
-        offset.resize(params.size());
+        std::vector<std::vector<Tensor>> groups;
+        root->colocation_groups(groups);
+        // Physical order: Parameters() order, except that a colocation group is placed whole where its first member
+        // would go. Every tensor starts 16-byte aligned; a group's members are only packed without gaps when their
+        // sizes are multiples of four floats (the packed kernels check contiguity before relying on it).
+        offset.assign(params.size(), -1);
+        phys.clear();
+        auto index_of = [&](const Tensor &t) {
+            for (size_t i = 0; i < params.size(); i++)
+                if (params[i].second == t) return (int)i;
+            return -1;
+        };
         int64_t off = 0;
-        for (size_t i = 0; i < params.size(); i++) {
+        auto place = [&](int i) {
             offset[i] = off;
             off += (params[i].second->numel + 3) & ~int64_t(3);
+            phys.push_back(i);
+        };
+        for (size_t i = 0; i < params.size(); i++) {
+            if (offset[i] >= 0) continue;
+            const std::vector<Tensor> *grp = nullptr;
+            for (auto &g : groups)
+                for (auto &t : g)
+                    if (t == params[i].second) grp = &g;
+            if (!grp) {
+                place((int)i);
+                continue;
+            }
+            for (auto &t : *grp) {
+                int j = index_of(t);
+                if (j >= 0 && offset[j] < 0) place(j);
+            }
         }
         total = off;
         uint64_t bytes = sizeof(float) * (uint64_t)(total > 0 ? total : 4);
@@ -230,15 +264,18 @@ struct omt_model {
         float ss, sq;
         om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
         om_ctx *c = device->ctx();
+        // Runs of physically consecutive parameters with gradients (the alignment gaps between them are zero in
+        // every block, and Adam keeps a zero parameter with a zero gradient and zero moments at zero).
+        auto live = [&](size_t q) { return params[phys[q]].second->grad_exists && params[phys[q]].second->requires_grad; };
         size_t i = 0;
-        while (i < params.size()) {
-            if (!params[i].second->grad_exists || !params[i].second->requires_grad) {
+        while (i < phys.size()) {
+            if (!live(i)) {
                 i++;
                 continue;
             }
             size_t j = i;
-            while (j + 1 < params.size() && params[j + 1].second->grad_exists && params[j + 1].second->requires_grad) j++;
-            int64_t beg = offset[i], end = offset[j] + params[j].second->numel;
+            while (j + 1 < phys.size() && live(j + 1)) j++;
+            int64_t beg = offset[phys[i]], end = offset[phys[j]] + params[phys[j]].second->numel;
             check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, end - beg, lr, beta1, beta2, eps,
                                   wd, 1, ss, sq),
                   "om_adam_step");

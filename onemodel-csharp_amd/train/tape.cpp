@@ -344,6 +344,68 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
     return o;
 }
 
+Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const Tensor &wk, const Tensor &bk,
+                     const Tensor &wv, const Tensor &bv, const Tensor &mask, int heads) {
+    const int64_t W = wq->shape.size() == 2 ? wq->shape[0] : 0;
+    const int64_t WW = W * W;
+    auto packed = [&](const float *a, const float *b, const float *c, int64_t n) {
+        return a && b && c && b == a + n && c == b + n;
+    };
+    const bool square = W > 0 && wq->shape == std::vector<int>{(int)W, (int)W} && wk->shape == wq->shape &&
+                        wv->shape == wq->shape && bq && bk && bv && bq->numel == W && bk->numel == W &&
+                        bv->numel == W && x->shape.size() == 3 && x->shape[2] == W;
+    if (!square || !packed(wq->data, wk->data, wv->data, WW) || !packed(bq->data, bk->data, bv->data, W))
+        return attention_heads(linear(x, wq, bq), linear(x, wk, bk), linear(x, wv, bv), mask, heads);
+    if (heads < 1 || W % heads) shape_error("Attention: width " + std::to_string(W) + " is not a multiple of the head count");
+    const int B = x->shape[0], L = x->shape[1], D = (int)(W / heads), w = (int)W;
+    if (D % 2) shape_error("Attention needs an even head dimension, got " + std::to_string(D));
+    if (mask && mask->shape != std::vector<int>{B, L, L})
+        shape_error("The mask must be [" + std::to_string(B) + "," + std::to_string(L) + "," + std::to_string(L) +
+                    "], not " + shape_str(mask->shape));
+    const int rows = B * L;
+    // q | k | v as one Linear(W -> 3W): the weights [3W, W] and biases [3W] are the packed arena blocks.
+    float *qkv = dev().step_floats((int64_t)rows * 3 * W);
+    OMT(om_linear_fwd(C(), x->data, wq->data, bq->data, qkv, rows, w, 3 * w));
+    Tensor o = make(x->shape);
+    float *p = dev().step_floats((int64_t)B * heads * L * L);
+    const float *md = mask ? mask->data : nullptr;
+    OMT(om_attention_fwd_ld(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, o->data, w, p, B, heads, L, L, D, 0.0f));
+    if (tracked({&x, &wq, &bq, &wk, &bk, &wv, &bv}))
+        attach(o, "AttentionQKV", {x, wq, bq, wk, bk, wv, bv},
+               [qkv, p, B, L, heads, D, w, rows, WW](Engine &e, Record &r, const float *g) {
+                   const int64_t W = w;
+                   float *dqkv = dev().step_floats((int64_t)rows * 3 * W);
+                   float *ds = dev().step_floats((int64_t)B * heads * L * L);
+                   OMT(om_attention_bwd_ld(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, p, g, w, dqkv, dqkv + W,
+                                           dqkv + 2 * W, 3 * w, ds, B, heads, L, L, D, 0.0f, 0));
+                   int ax, a[6];
+                   float *dx = e.dest(r, 0, &ax);
+                   float *d[6];
+                   for (int i = 0; i < 6; i++) d[i] = e.dest(r, 1 + i, &a[i]);
+                   // d = {dwq, dbq, dwk, dbk, dwv, dbv}: one dW / db launch when the three leaves' gradients are the
+                   // packed blocks with one accumulate flag, else through a temporary added or copied into each.
+                   auto direct = [&](int first, int64_t n) {
+                       return d[first] && d[first + 2] && d[first + 4] && d[first + 2] == d[first] + n &&
+                              d[first + 4] == d[first + 2] + n && a[first] == a[first + 2] && a[first] == a[first + 4];
+                   };
+                   const bool dw_direct = direct(0, WW), db_direct = direct(1, W);
+                   const bool any_w = d[0] || d[2] || d[4], any_b = d[1] || d[3] || d[5];
+                   float *dw = !any_w ? nullptr : dw_direct ? d[0] : dev().step_floats(3 * WW);
+                   float *db = !any_b ? nullptr : db_direct ? d[1] : dev().step_floats(3 * W);
+                   OMT(om_linear_bwd(C(), dqkv, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, w, 3 * w, ax,
+                                     dw_direct ? a[0] : 0, db_direct ? a[1] : 0));
+                   for (int i = 0; i < 6; i++) {
+                       const bool isw = (i % 2) == 0;
+                       if (!d[i] || (isw ? dw_direct : db_direct)) continue;
+                       const int64_t n = isw ? WW : W;
+                       const float *src = (isw ? dw : db) + (i / 2) * n;
+                       if (a[i]) OMT(om_axpy(C(), 1.0f, src, d[i], n));
+                       else OMT(om_copy(C(), d[i], src, sizeof(float) * (uint64_t)n));
+                   }
+               });
+    return o;
+}
+
 Tensor reshape(const Tensor &x, const std::vector<int> &shape) {
     std::vector<int> s = shape;
     int64_t known = 1;

@@ -113,6 +113,12 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
 // empty; returns [B, L, H*D]. The reference's Reshape/Permute/Attention/Permute/Reshape with the permutes folded into
 // the kernels' addressing.
 Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const Tensor &mask, int heads);
+// The q/k/v projections and the attention core of MultiHeadAttention (Layers.cs:497-516) in one record: when the
+// three weights (and the three biases) sit back to back in the arena, the projections are one [rows, 3W] Linear
+// (one GEMM forward, one dX GEMM over K = 3W, one dW GEMM over M = 3W, one bias sum in the backward) and attention
+// reads q, k, v as column blocks of it; otherwise it is the three Linear calls and attention_heads.
+Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const Tensor &wk, const Tensor &bk,
+                     const Tensor &wv, const Tensor &bv, const Tensor &mask, int heads);
 Tensor reshape(const Tensor &x, const std::vector<int> &shape);
 Tensor permute(const Tensor &x, const std::vector<int> &perm);
 Tensor mean_axis(const Tensor &x, int axis);
@@ -152,6 +158,10 @@ class Module {
         return p;
     }
     void named_parameters(std::vector<std::pair<std::string, Tensor>> &out, const std::string &prefix = "") const;
+    // Asks the arena to place these parameters back to back, in this order (values, gradients and moments alike),
+    // so one kernel can treat them as one tensor. Parameters() order is unchanged.
+    void colocate(std::vector<Tensor> group) { colocate_.push_back(std::move(group)); }
+    void colocation_groups(std::vector<std::vector<Tensor>> &out) const;
     // Moves the host initial values out, in named_parameters() order, for the model to upload into its arena.
     void take_init(std::vector<std::vector<float>> &out);
 
@@ -159,6 +169,7 @@ class Module {
     std::vector<std::pair<std::string, Tensor>> params_;
     std::vector<std::pair<std::string, std::unique_ptr<Module>>> children_;
     std::vector<std::vector<float>> init_;  // host values until the parameters are laid out in device memory
+    std::vector<std::vector<Tensor>> colocate_;
 };
 
 class Linear : public Module {

@@ -279,6 +279,40 @@ def test_attention(dev, T, B, H, L, D, masked):
         assert scaled(back(got), ref) <= TOL
 
 
+@pytest.mark.parametrize("B,H,L,D", [(2, 3, 40, 32), (4, 12, 128, 32)])
+def test_attention_packed_qkv_strides(dev, T, B, H, L, D):
+    """om_attention_*_ld on q|k|v packed as one [B, L, 3*H*D] projection output, with o and dq|dk|dv in the same
+    packed layouts: the same results as the oracle on the unpacked tensors."""
+    rng = np.random.default_rng(B * L + D)
+    W = H * D
+    qkv = rnd(rng, B, L, 3 * W)
+    g = rnd(rng, B, L, W)
+    lens = rng.integers(L // 2, L + 1, B)
+    mask = np.zeros((B, L, L), np.float32)
+    for b in range(B):
+        mask[b, :, lens[b]:] = -np.inf
+    heads = lambda a: np.ascontiguousarray(a.reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    tq, tk, tv = (heads(qkv[:, :, i * W:(i + 1) * W]) for i in range(3))
+    tg = heads(g)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref = np.empty_like(tq)
+    T.lib().or_attention_fwd(T.fp(tq), T.fp(tk), T.fp(tv), T.fp(mask), 1, T.fp(o_ref), B, H, L, L, D, C.c_float(scale))
+    dq, dk, dv = np.empty_like(tq), np.empty_like(tk), np.empty_like(tv)
+    T.lib().or_attention_bwd(T.fp(tq), T.fp(tk), T.fp(tv), T.fp(mask), 1, T.fp(tg), T.fp(dq), T.fp(dk), T.fp(dv), B, H,
+                             L, L, D, C.c_float(scale))
+    QKV, G, M = dev.put(qkv), dev.put(g), dev.put(mask)
+    O, P, DS, DQKV = dev.empty((B, L, W)), dev.empty((B, H, L, L)), dev.empty((B, H, L, L)), dev.empty((B, L, 3 * W))
+    off = lambda buf, i: buf.data_ptr() + 4 * i * W
+    dev.call("om_attention_fwd_ld", QKV, off(QKV, 1), off(QKV, 2), 3 * W, M, 1, O, W, P, B, H, L, L, D,
+             C.c_float(scale))
+    dev.call("om_attention_bwd_ld", QKV, off(QKV, 1), off(QKV, 2), 3 * W, P, G, W, DQKV, off(DQKV, 1), off(DQKV, 2),
+             3 * W, DS, B, H, L, L, D, C.c_float(scale), 0)
+    assert scaled(heads(dev.get(O)), o_ref) <= TOL
+    d = dev.get(DQKV)
+    for i, ref in enumerate((dq, dk, dv)):
+        assert scaled(heads(d[:, :, i * W:(i + 1) * W]), ref) <= TOL
+
+
 # ------------------------------------------------------------------------------------------------ conv and pool
 @pytest.mark.parametrize("N,Cin,H,W,Cout,K,S,P", [(2, 64, 14, 14, 64, 3, 1, 1), (2, 1, 32, 128, 32, 3, 1, 1),
                                                   (3, 32, 16, 64, 64, 3, 1, 1), (2, 5, 9, 11, 7, 3, 2, 1),
