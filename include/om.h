@@ -86,10 +86,24 @@ om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, co
 om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
                         int out);
 /* Linear backward = MatMul backward + Permute backward + bias SumTo (BackwardOps.cs:69-82, 107-118, 201-269):
- * dx = g w, dw = g^T x written directly as [out,in], db = fp64 column sums of g. Each output pointer may be NULL;
- * the acc_* flags add into the destination instead of overwriting it (leaf accumulation). */
+ * dx = g w, dw = g^T x written directly as [out,in], db = fp64 column sums of g (computed inside the dW launch when
+ * both are requested and the tile allows it). Each output pointer may be NULL; the acc_* flags add into the
+ * destination instead of overwriting it (leaf accumulation). */
 om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
                         int rows, int in, int out, int acc_dx, int acc_dw, int acc_db);
+/* Linear followed by the residual Add of an encoder block (Ops.Layers.cs:715-733, then Ops.Add, Ops.cs:15-56):
+ * y = resid + (x w^T + b), in that rounding order, in one launch. */
+om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,
+                              float *y, int rows, int in, int out);
+/* Linear followed by GELU (erf form, Ops.Nn.cs:86-112) in one launch: h = x w^T + b (the pre-activation GELU's
+ * backward reads) and a = gelu(h), both [rows, out]. */
+om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *h, float *a, int rows,
+                             int in, int out);
+/* The input gradient of Linear(GELU(h)) with respect to h in one launch: dh = GeluGradBin(g w, h)
+ * (MatMul backward BackwardOps.cs:69-82, then GELU backward BackwardNn.cs:12-14); g is [rows, out], w [out, in],
+ * h and dh [rows, in]. */
+om_status om_linear_bwd_dx_gelu(om_ctx *ctx, const float *g, const float *w, const float *h, float *dh, int rows,
+                                int in, int out);
 /* Bias gradient alone: db[n] (+)= (float) sum over rows of g[row, n] in double (BackwardOps.SumTo). */
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate);
 
@@ -177,6 +191,16 @@ om_status om_attention_fwd_ld(om_ctx *ctx, const float *q, const float *k, const
 om_status om_attention_bwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
                               const float *p, const float *g, int ld_g, float *dq, float *dk, float *dv, int ld_d,
                               float *ds, int B, int H, int lq, int lk, int d, float scale, int acc);
+/* Self-attention (Lq = Lk = L) as the reference computes it, with no saved weights: the forward returns O only, and
+ * the backward recomputes S and P from q, k and the mask (AttentionBackward, BackwardNn.cs:636-701, recomputes them
+ * the same way). For D = 32 and L in {64, 128} each is one fused kernel (scores, exact row softmax and the products
+ * on chip); other shapes run the GEMM path with the scores in context scratch. Strides as in the _ld entry points. */
+om_status om_attention_fwd_fused(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                 const float *mask, int mask_batched, float *o, int ld_o, int B, int H, int L, int d,
+                                 float scale);
+om_status om_attention_bwd_fused(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                 const float *mask, int mask_batched, const float *g, int ld_g, float *dq, float *dk,
+                                 float *dv, int ld_d, int B, int H, int L, int d, float scale, int acc);
 /* ---------------------------------------------------------------------------------------------- convolution, pooling */
 /* Ops.Conv2d, groups 1, square stride/padding (Ops.Layers.cs:279-336; Conv.cs:54) as implicit GEMM on MFMA, and
  * ConvBackward (BackwardNn.cs:317-402): dx = col2im(W^T g) as an implicit GEMM over g, dw = g im2col(x) with a

@@ -43,6 +43,9 @@ _OM_SIGS = {
     "om_gemm": [vp, ci, ci, ci, ci, ci, vp, ci, vp, ci, vp, ci, vp, ci, C.POINTER(om_batch)],
     "om_linear_fwd": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci],
+    "om_linear_fwd_resid": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_linear_gelu_fwd": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_linear_bwd_dx_gelu": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_colsum": [vp, vp, vp, ci, ci, ci],
     "om_relu_fwd": [vp, vp, vp, i64],
     "om_relu_bwd": [vp, vp, vp, vp, i64, ci],
@@ -72,6 +75,8 @@ _OM_SIGS = {
     "om_attention_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
     "om_attention_fwd_ld": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, ci, ci, ci, ci, ci, f32],
     "om_attention_bwd_ld": [vp, vp, vp, vp, ci, vp, vp, ci, vp, vp, vp, ci, vp, ci, ci, ci, ci, ci, f32, ci],
+    "om_attention_fwd_fused": [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, ci, ci, ci, f32],
+    "om_attention_bwd_fused": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
     "om_conv2d_fwd": [vp, vp, vp, vp, vp] + [ci] * 9,
     "om_conv2d_bwd": [vp, vp, vp, vp, vp, vp, vp] + [ci] * 9 + [ci, ci],
     "om_maxpool_fwd": [vp, vp, vp, vp] + [ci] * 10,

@@ -1,0 +1,360 @@
+// Fused scaled dot-product attention for short sequences (Ops.Attention, Ops.Layers.cs:746-807; AttentionBackward,
+// BackwardNn.cs:636-701; definition docs/kernels-attention.md:10-33).
+//
+// The unfused path (om_attention.hip) runs five GEMM launches and two row passes over a [B, H, L, L] score tensor
+// in HBM. For L <= 128 a workgroup holds whole score rows on chip, so forward and backward are one kernel each and
+// the scores never reach HBM:
+//   forward  (one workgroup per batch item, head and 64 queries; a wavefront per 16 queries):
+//            S = scale * Q K^T + mask on MFMA, P = Softmax.Rows(S) in registers, O = P V on MFMA;
+//   backward (one workgroup per batch item and head; a wavefront per 16 queries), recomputing P as the reference
+//            does: S, P, dP = dO V^T, dS = P (dP - rowsum(dP P)) scale with the row sum in double, then
+//            dV = P^T dO, dK = dS^T Q, dQ = dS K, with P^T and dS^T staged through LDS.
+// The softmax is the reference's exact row kernel: in the 16x16 MFMA result layout, lane t of a 16-lane group holds
+// the row's columns t, t+16, ..., which are exactly the elements of Sum16's partial t, so the partials are summed in
+// increasing column order per lane and combined with the halving shuffles, as in Softmax.Rows (Softmax.cs:27-133).
+// Q, K, V (and O, dO, dQ, dK, dV) are [B, L, H*D] row blocks of stride ld (packed q|k|v projections welcome).
+#include "om_gemm.hpp"
+
+om_status om_internal_softmax_rows(om_ctx *ctx, float *x, int rows, int cols);
+extern "C" om_status om_attention_bwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                         const float *p, const float *g, int ld_g, float *dq, float *dk, float *dv,
+                                         int ld_d, float *ds, int B, int H, int lq, int lk, int d, float scale,
+                                         int acc);
+extern "C" om_status om_attention_fwd_ld(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                         const float *mask, int mask_batched, float *o, int ld_o, float *p, int B,
+                                         int H, int lq, int lk, int d, float scale);
+
+namespace {
+
+using omg::floatx4;
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Copies `rows` rows of D floats (global stride ld) into LDS rows of stride D + 4.
+template <int D, int NTH>
+__device__ __forceinline__ void stage(float *dst, const float *src, int64_t ld, int rows) {
+    constexpr int Q4 = D / 4;
+    for (int f = threadIdx.x; f < rows * Q4; f += NTH) {
+        int r = f / Q4, c = (f % Q4) * 4;
+        *reinterpret_cast<floatx4 *>(&dst[r * (D + 4) + c]) = *reinterpret_cast<const floatx4 *>(src + r * ld + c);
+    }
+}
+
+// S = scale * X Y^T (+ mask) for the 16 rows x0.. of X against all L rows of Y (both staged [rows][D+4]):
+// s[j] holds columns 16j.. in the MFMA result layout (lane t, group kl, register r = row 4kl+r, column 16j+t).
+template <int D, int L>
+__device__ __forceinline__ void scores(floatx4 (&s)[L / 16], const float *Xs, const float *Ys, int x0, int t, int kl) {
+    constexpr int LDX = D + 4;
+#pragma unroll
+    for (int j = 0; j < L / 16; j++) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int blk = 0; blk < D / 16; blk++) {
+        floatx4 a = *reinterpret_cast<const floatx4 *>(&Xs[(x0 + t) * LDX + 16 * blk + 4 * kl]);
+#pragma unroll
+        for (int j = 0; j < L / 16; j++) {
+            floatx4 b = *reinterpret_cast<const floatx4 *>(&Ys[(16 * j + t) * LDX + 16 * blk + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[j] = mfma4(a[u], b[u], s[j]);
+        }
+    }
+}
+
+// This lane's mask values for its four rows (row stride L), loaded early so their latency hides behind the staging.
+template <int L>
+__device__ __forceinline__ void load_mask(float (&mv)[4][L / 16], const float *mrow, int t) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int j = 0; j < L / 16; j++) mv[r][j] = mrow ? mrow[r * L + 16 * j + t] : 0.0f;
+}
+
+// Scale, additive mask and the exact row softmax, in place: s becomes P.
+template <int L>
+__device__ __forceinline__ void softmax_rows(floatx4 (&s)[L / 16], const float (&mv)[4][L / 16], bool masked,
+                                             float scale) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float mx = -__int_as_float(0x7F800000);
+#pragma unroll
+        for (int j = 0; j < L / 16; j++) {
+            float x = s[j][r] * scale;
+            if (masked) x = x + mv[r][j];
+            s[j][r] = x;
+            mx = x > mx ? x : mx;
+        }
+        mx = omd::max16(mx);
+        float p = 0.0f;
+#pragma unroll
+        for (int j = 0; j < L / 16; j++) {
+            float e = omd::exp_nonpos(s[j][r] - mx);
+            s[j][r] = e;
+            p += e;
+        }
+        const float l = omd::sum16(p);
+#pragma unroll
+        for (int j = 0; j < L / 16; j++) s[j][r] = omd::canon(s[j][r] / l);
+    }
+}
+
+// acc[jn] += A (16 rows, K = L) x B[L][D] where A comes from LDS in K layout (row stride LDA, rows a0 + t, k from 0)
+// and B is staged [L][D+4]; B's D/16 column blocks are interleaved (block jn holds columns DB*c + jn), so one lane
+// reads its DB values of a row at once.
+template <int D, int L, int LDA>
+__device__ __forceinline__ void mm_kA(floatx4 (&acc)[D / 16], const float *As, int a0, const float *Bs, int t,
+                                      int kl) {
+    constexpr int DB = D / 16, LDB = D + 4;
+#pragma unroll
+    for (int blk = 0; blk < L / 16; blk++) {
+        floatx4 a = *reinterpret_cast<const floatx4 *>(&As[(a0 + t) * LDA + 16 * blk + 4 * kl]);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float *brow = &Bs[(16 * blk + 4 * kl + u) * LDB + DB * t];
+            float bv[DB];
+            if constexpr (DB % 4 == 0) {
+#pragma unroll
+                for (int x = 0; x < DB; x += 4) {
+                    floatx4 w = *reinterpret_cast<const floatx4 *>(brow + x);
+                    bv[x] = w[0];
+                    bv[x + 1] = w[1];
+                    bv[x + 2] = w[2];
+                    bv[x + 3] = w[3];
+                }
+            } else {
+#pragma unroll
+                for (int x = 0; x < DB; x += 2) {
+                    float2 w = *reinterpret_cast<const float2 *>(brow + x);
+                    bv[x] = w.x;
+                    bv[x + 1] = w.y;
+                }
+            }
+#pragma unroll
+            for (int jn = 0; jn < DB; jn++) acc[jn] = mfma4(a[u], bv[jn], acc[jn]);
+        }
+    }
+}
+
+// Writes a 16-row result block (rows row0 + 4kl + r) with interleaved columns DB*t + jn, optionally accumulating.
+template <int D>
+__device__ __forceinline__ void store_rows(float *dst, int64_t ld, int row0, const floatx4 (&acc)[D / 16], int t,
+                                           int kl, int accumulate) {
+    constexpr int DB = D / 16;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float *p = dst + (int64_t)(row0 + 4 * kl + r) * ld + DB * t;
+#pragma unroll
+        for (int jn = 0; jn < DB; jn++) p[jn] = accumulate ? p[jn] + acc[jn][r] : acc[jn][r];
+    }
+}
+
+template <int D, int L>
+__global__ void __launch_bounds__(256) k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
+                                                  const float *__restrict__ v, int ld, const float *__restrict__ mask,
+                                                  int64_t mask_bstride, float *__restrict__ o, int ldo, float scale) {
+    constexpr int LDX = D + 4, LDP = L + 4;
+    __shared__ __attribute__((aligned(16))) float Qs[64 * LDX];
+    __shared__ __attribute__((aligned(16))) float Ks[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Vs[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Ps[64 * LDP];
+    const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int64_t row0 = (int64_t)b * L;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
+    const int q0 = 16 * w;  // this wavefront's first query within the block
+    float mv[4][L / 16];
+    load_mask<L>(mv, mask ? mask + b * mask_bstride + (int64_t)(qb * 64 + q0 + 4 * kl) * L : nullptr, t);
+    stage<D, 256>(Qs, q + (row0 + qb * 64) * ld + h * D, ld, 64);
+    stage<D, 256>(Ks, k + row0 * ld + h * D, ld, L);
+    stage<D, 256>(Vs, v + row0 * ld + h * D, ld, L);
+    __syncthreads();
+    floatx4 s[L / 16];
+    scores<D, L>(s, Qs, Ks, q0, t, kl);
+    softmax_rows<L>(s, mv, mask != nullptr, scale);
+    // P -> LDS as [query][key]; each wavefront reads back only its own 16 rows, so no barrier is needed.
+#pragma unroll
+    for (int j = 0; j < L / 16; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) Ps[(q0 + 4 * kl + r) * LDP + 16 * j + t] = s[j][r];
+    floatx4 oacc[D / 16];
+#pragma unroll
+    for (int jn = 0; jn < D / 16; jn++) oacc[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
+    mm_kA<D, L, LDP>(oacc, Ps, q0, Vs, t, kl);
+    store_rows<D>(o + (row0 + qb * 64) * ldo + h * D, ldo, q0, oacc, t, kl, 0);
+}
+
+template <int D, int L>
+__global__ void __launch_bounds__(L * 4) k_attn_bwd(const float *__restrict__ q, const float *__restrict__ k,
+                                                    const float *__restrict__ v, int ld, const float *__restrict__ mask,
+                                                    int64_t mask_bstride, const float *__restrict__ g, int ldg,
+                                                    float *dq, float *dk, float *dv, int ldd, float scale, int acc) {
+    constexpr int NTH = L * 4, LDX = D + 4, LDT = L + 4, NB = L / 16;
+    __shared__ __attribute__((aligned(16))) float Qs[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Ks[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Vs[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Gs[L * LDX];
+    __shared__ __attribute__((aligned(16))) float T[L * LDT];  // P^T, then dS^T: [key][query]
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int64_t row0 = (int64_t)b * L;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
+    const int q0 = 16 * w;  // this wavefront's queries; also its block of 16 keys for dK and dV
+    float mv[4][L / 16];
+    load_mask<L>(mv, mask ? mask + b * mask_bstride + (int64_t)(q0 + 4 * kl) * L : nullptr, t);
+    stage<D, NTH>(Qs, q + row0 * ld + h * D, ld, L);
+    stage<D, NTH>(Ks, k + row0 * ld + h * D, ld, L);
+    stage<D, NTH>(Vs, v + row0 * ld + h * D, ld, L);
+    stage<D, NTH>(Gs, g + row0 * ldg + h * D, ldg, L);
+    __syncthreads();
+    floatx4 s[NB];
+    scores<D, L>(s, Qs, Ks, q0, t, kl);
+    softmax_rows<L>(s, mv, mask != nullptr, scale);
+    floatx4 dp[NB];
+    scores<D, L>(dp, Gs, Vs, q0, t, kl);  // dP = dO V^T
+    // dS = P (dP - sum_k dP P) scale, the row sum in double (BackwardNn.cs:26-52 via AttentionBackward)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        double dot = 0.0;
+#pragma unroll
+        for (int j = 0; j < NB; j++) dot += (double)(dp[j][r] * s[j][r]);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 16);
+        const float df = (float)dot;
+#pragma unroll
+        for (int j = 0; j < NB; j++) dp[j][r] = (s[j][r] * (dp[j][r] - df)) * scale;
+    }
+    // P^T -> T (four consecutive queries per store)
+#pragma unroll
+    for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4 *>(&T[(16 * j + t) * LDT + q0 + 4 * kl]) = s[j];
+    __syncthreads();
+    floatx4 dva[D / 16];
+#pragma unroll
+    for (int jn = 0; jn < D / 16; jn++) dva[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
+    mm_kA<D, L, LDT>(dva, T, q0, Gs, t, kl);  // dV = P^T dO for keys q0..q0+15
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NB; j++) *reinterpret_cast<floatx4 *>(&T[(16 * j + t) * LDT + q0 + 4 * kl]) = dp[j];
+    __syncthreads();
+    floatx4 dka[D / 16];
+#pragma unroll
+    for (int jn = 0; jn < D / 16; jn++) dka[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
+    mm_kA<D, L, LDT>(dka, T, q0, Qs, t, kl);  // dK = dS^T Q for keys q0..q0+15
+    // dQ = dS K for queries q0..q0+15: A = dS[q][key] read column-wise from T = dS^T.
+    floatx4 dqa[D / 16];
+#pragma unroll
+    for (int jn = 0; jn < D / 16; jn++) dqa[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
+    {
+        constexpr int DB = D / 16;
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++)
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int key = 16 * blk + 4 * kl + u;
+                const float a = T[key * LDT + q0 + t];
+                const float *brow = &Ks[key * LDX + DB * t];
+                float bv[DB];
+#pragma unroll
+                for (int x = 0; x < DB; x++) bv[x] = brow[x];
+#pragma unroll
+                for (int jn = 0; jn < DB; jn++) dqa[jn] = mfma4(a, bv[jn], dqa[jn]);
+            }
+    }
+    if (dv) store_rows<D>(dv + row0 * ldd + h * D, ldd, q0, dva, t, kl, acc);
+    if (dk) store_rows<D>(dk + row0 * ldd + h * D, ldd, q0, dka, t, kl, acc);
+    if (dq) store_rows<D>(dq + row0 * ldd + h * D, ldd, q0, dqa, t, kl, acc);
+}
+
+bool fused_ok(const float *q, const float *k, const float *v, int ld, int ldo, int lq, int lk, int d) {
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    return d == 32 && lq == lk && (lq == 64 || lq == 128) && ld % 4 == 0 && ldo % 4 == 0 && al(q) && al(k) && al(v);
+}
+
+om_status check(om_ctx *ctx, const char *what, const void *q, const void *k, const void *v, int B, int H, int L,
+                int d, int ld, int ldo) {
+    OM_REQUIRE(ctx, q && k && v, "%s: NULL q/k/v", what);
+    OM_REQUIRE(ctx, B > 0 && H > 0 && L > 0 && d > 0 && d % 2 == 0,
+               "%s: needs [B,L,H*D] tensors with positive sizes and even D, got B=%d H=%d L=%d D=%d", what, B, H, L,
+               d);
+    OM_REQUIRE(ctx, ld >= H * d && ldo >= H * d, "%s: row strides %d / %d below H*D = %d", what, ld, ldo, H * d);
+    OM_REQUIRE(ctx, (int64_t)B * H * L <= INT32_MAX, "%s: too many rows", what);
+    return OM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+om_status om_attention_fwd_fused(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                 const float *mask, int mask_batched, float *o, int ld_o, int B, int H, int L, int d,
+                                 float scale) {
+    OM_CHECK_CTX(ctx);
+    om_status s = check(ctx, "om_attention_fwd_fused", q, k, v, B, H, L, d, ld_qkv, ld_o);
+    if (s) return s;
+    OM_REQUIRE(ctx, o, "om_attention_fwd_fused: NULL output");
+    if (scale == 0.0f || scale != scale) scale = 1.0f / sqrtf((float)d);
+    const int64_t mstride = (mask && mask_batched) ? (int64_t)L * L : 0;
+    if (fused_ok(q, k, v, ld_qkv, ld_o, L, L, d) && ((uintptr_t)o & 7) == 0) {
+        dim3 grid(L / 64, H, B);
+        if (L == 128)
+            hipLaunchKernelGGL((k_attn_fwd<32, 128>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o,
+                               ld_o, scale);
+        else
+            hipLaunchKernelGGL((k_attn_fwd<32, 64>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o,
+                               ld_o, scale);
+        return OM_LAUNCH_CHECK(ctx, "om_attention_fwd_fused");
+    }
+    float *p;
+    s = om::scratch2(ctx, sizeof(float) * (uint64_t)B * H * L * L, &p);
+    if (s) return s;
+    return om_attention_fwd_ld(ctx, q, k, v, ld_qkv, mask, mask_batched, o, ld_o, p, B, H, L, L, d, scale);
+}
+
+om_status om_attention_bwd_fused(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
+                                 const float *mask, int mask_batched, const float *g, int ld_g, float *dq, float *dk,
+                                 float *dv, int ld_d, int B, int H, int L, int d, float scale, int acc) {
+    OM_CHECK_CTX(ctx);
+    om_status s = check(ctx, "om_attention_bwd_fused", q, k, v, B, H, L, d, ld_qkv, ld_d);
+    if (s) return s;
+    OM_REQUIRE(ctx, g && ld_g >= H * d, "om_attention_bwd_fused: NULL gradient or short stride");
+    if (!dq && !dk && !dv) return OM_OK;
+    if (scale == 0.0f || scale != scale) scale = 1.0f / sqrtf((float)d);
+    const int64_t mstride = (mask && mask_batched) ? (int64_t)L * L : 0;
+    if (fused_ok(q, k, v, ld_qkv, ld_d, L, L, d) && ld_g % 4 == 0 && ((uintptr_t)g & 15) == 0) {
+        dim3 grid(H, B);
+        if (L == 128)
+            hipLaunchKernelGGL((k_attn_bwd<32, 128>), grid, dim3(512), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
+                               g, ld_g, dq, dk, dv, ld_d, scale, acc);
+        else
+            hipLaunchKernelGGL((k_attn_bwd<32, 64>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
+                               g, ld_g, dq, dk, dv, ld_d, scale, acc);
+        return OM_LAUNCH_CHECK(ctx, "om_attention_bwd_fused");
+    }
+    // Recompute P (as the reference does) with the GEMM path, then the unfused backward.
+    const uint64_t n = (uint64_t)B * H * L * L;
+    float *p;
+    s = om::scratch2(ctx, sizeof(float) * 2 * n, &p);
+    if (s) return s;
+    // S and P only (the forward entry point would also run O = P V).
+    {
+        omg::Params ps = omg::dense_params(L, L, d, nullptr, 0, nullptr, 0, p, L);
+        ps.batch_div = H;
+        ps.a = q;
+        ps.lda = ld_qkv;
+        ps.sa_outer = (int64_t)L * ld_qkv;
+        ps.sa_inner = d;
+        ps.b = k;
+        ps.ldb = ld_qkv;
+        ps.sb_outer = (int64_t)L * ld_qkv;
+        ps.sb_inner = d;
+        ps.sc_outer = (int64_t)H * L * L;
+        ps.sc_inner = (int64_t)L * L;
+        ps.alpha = scale;
+        ps.mask = mask;
+        ps.mask_outer_stride = mstride;
+        s = omg::launch_dense(ctx, ps, false, true, B * H, "attention scores (recompute)");
+        if (s) return s;
+        s = om_internal_softmax_rows(ctx, p, B * H * L, L);
+        if (s) return s;
+    }
+    return om_attention_bwd_ld(ctx, q, k, v, ld_qkv, p, g, ld_g, dq, dk, dv, ld_d, p + n, B, H, L, L, d, scale, acc);
+}
+
+}  // extern "C"

@@ -31,22 +31,28 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what) {
     return fail(ctx, e == hipErrorOutOfMemory ? OM_E_OOM : OM_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
-om_status scratch(om_ctx *ctx, uint64_t bytes, float **out) {
-    if (bytes <= ctx->scratch_bytes) {
-        *out = ctx->scratch;
+static om_status grow(om_ctx *ctx, float *&buf, uint64_t &have, uint64_t bytes, float **out, const char *what) {
+    if (bytes <= have) {
+        *out = buf;
         return OM_OK;
     }
     om_status s = check_hip(ctx, hipStreamSynchronize(ctx->stream), "scratch sync");
     if (s) return s;
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
-    ctx->scratch = nullptr;
-    ctx->scratch_bytes = 0;
+    if (buf) (void)hipFree(buf);
+    buf = nullptr;
+    have = 0;
     uint64_t want = bytes < (64ull << 20) ? (64ull << 20) : bytes + (bytes >> 2);
-    s = check_hip(ctx, hipMalloc(&ctx->scratch, want), "scratch alloc");
+    s = check_hip(ctx, hipMalloc(&buf, want), what);
     if (s) return s;
-    ctx->scratch_bytes = want;
-    *out = ctx->scratch;
+    have = want;
+    *out = buf;
     return OM_OK;
+}
+om_status scratch(om_ctx *ctx, uint64_t bytes, float **out) {
+    return grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out, "scratch alloc");
+}
+om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out) {
+    return grow(ctx, ctx->scratch2, ctx->scratch2_bytes, bytes, out, "scratch alloc");
 }
 
 }  // namespace om
@@ -100,6 +106,7 @@ om_status om_ctx_destroy(om_ctx *ctx) {
     for (auto &r : ctx->region)
         for (auto &s : r.slabs) (void)hipFree(s.base);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->scratch2) (void)hipFree(ctx->scratch2);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return OM_OK;

@@ -19,22 +19,10 @@ struct ReluGradF {
     __device__ float operator()(float g, float y) const { return y > 0.0f ? g : 0.0f; }
 };
 struct GeluF {
-    __device__ float operator()(float x, float) const {
-        float e, ope;
-        omd::erf_parts(x * 0.70710677f, e, ope);
-        float res = (0.5f * x) * ope;
-        if (x == -__int_as_float(0x7F800000)) res = -0.0f;
-        return omd::canon(x == x ? res : x);
-    }
+    __device__ float operator()(float x, float) const { return omd::gelu(x); }
 };
 struct GeluGradF {
-    __device__ float operator()(float g, float v) const {
-        float e, ope;
-        omd::erf_parts(v * 0.70710677f, e, ope);
-        float cdf = 0.5f * (1.0f + e);
-        float pdf = omd::exp_poly((-0.5f * v) * v) * 0.3989423f;
-        return omd::canon(g * (cdf + v * pdf));
-    }
+    __device__ float operator()(float g, float v) const { return omd::gelu_grad(g, v); }
 };
 struct AddF {
     __device__ float operator()(float a, float b) const { return a + b; }

@@ -42,16 +42,25 @@ __global__ void __launch_bounds__(NT) k_gemm(Params p) {
     run_k<BM, BN, BKT>(
         t, la, lb, [&](LA &l, int k0) { l.fetch(A, lda, M, kend, m0, k0); },
         [&](LB &l, int k0) { l.fetch(B, ldb, N, kend, n0, k0); }, kbeg, kend, As, Bs, wm0, wn0, lane);
-    store_tile(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
+    store_tile<decltype(t), true>(p, t, m0, n0, wm0, wn0, lane, C, p.ldc, mask, split);
 }
 
-// Adds the split-K partials in split order and applies the epilogue; four consecutive columns per thread.
+// Adds the split-K partials in split order and applies the epilogue; four consecutive columns per thread. A fused
+// bias gradient's per-split column sums are finished here too (in split order, in double).
 __global__ void k_splitk_reduce(Params p) {
     const int64_t total = (int64_t)p.m * p.n;
     const int nq = (p.n + 3) / 4;
     const int64_t quads = (int64_t)p.m * nq;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < quads; q += stride) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p.colsum_ws)
+        for (int64_t i = gid; i < p.m; i += stride) {
+            double t = 0.0;
+            for (int s = 0; s < p.splits; s++) t += p.colsum_ws[(int64_t)s * p.m + i];
+            float v = (float)t;
+            p.db[i] = p.db_acc ? p.db[i] + v : v;
+        }
+    for (int64_t q = gid; q < quads; q += stride) {
         int row = (int)(q / nq), col0 = (int)(q % nq) * 4;
         int64_t e = (int64_t)row * p.n + col0;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -67,13 +76,7 @@ __global__ void k_splitk_reduce(Params p) {
             for (int s = 0; s < p.splits; s++)
                 for (int u = 0; u < 4 && col0 + u < p.n; u++) v[u] += p.ws[(int64_t)s * total + e + u];
         }
-        for (int u = 0; u < 4 && col0 + u < p.n; u++) {
-            float x = v[u];
-            if (p.alpha != 1.0f) x = x * p.alpha;
-            if (p.bias) x = x + p.bias[p.bias_per_row ? row : col0 + u];
-            float *dst = p.c + (int64_t)row * p.ldc + col0 + u;
-            *dst = p.accumulate ? *dst + x : x;
-        }
+        for (int u = 0; u < 4 && col0 + u < p.n; u++) epilogue(p, p.c, p.ldc, nullptr, row, col0 + u, v[u]);
     }
 }
 
@@ -110,14 +113,44 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 #undef OMG_CASE
 }
 
-// Tile-exact set (om_gemm_x.hpp): NN, NT, TN.
-template <int BM, int BN, int BKT>
+// Tile-exact set (om_gemm_x.hpp): NN, NT, TN; GELU epilogue variants (NN / NT only) where G instantiates them.
+template <int BM, int BN, int BKT, bool G>
 static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
-    if (!ta && !tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, false, false>), dim3(total), dim3(NT), 0, st, p);
-    else if (!ta && tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, false, true>), dim3(total), dim3(NT), 0, st, p);
-    else if (ta && !tb) hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false>), dim3(total), dim3(NT), 0, st, p);
-    else return false;
+    const bool gelu = p.epi != EPI_NONE;
+    if (gelu && (!G || ta)) return false;
+#define OMG_L(K, NTH, TA_, TB_)                                                                                  \
+    if (gelu)                                                                                                    \
+        hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, G>), dim3(total), dim3(NTH), 0, st, p);                 \
+    else                                                                                                         \
+        hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, false>), dim3(total), dim3(NTH), 0, st, p);
+    if (!ta && !tb) {
+        OMG_L(k_gemm_x, NT, false, false)
+    } else if (!ta && tb) {
+        OMG_L(k_gemm_x, NT, false, true)
+    } else if (ta && !tb) {
+        hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false, false>), dim3(total), dim3(NT), 0, st, p);
+    } else {
+        return false;
+    }
+    return true;
+}
+// Eight-wavefront variant (om_gemm_x.hpp, k_gemm_x2).
+template <int BM, int BN, int BKT, bool G>
+static bool launch_x2(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+    const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
+    const bool gelu = p.epi != EPI_NONE;
+    if (gelu && (!G || ta)) return false;
+    if (!ta && !tb) {
+        OMG_L(k_gemm_x2, 2 * NT, false, false)
+    } else if (!ta && tb) {
+        OMG_L(k_gemm_x2, 2 * NT, false, true)
+    } else if (ta && !tb) {
+        hipLaunchKernelGGL((gx::k_gemm_x2<BM, BN, BKT, true, false, false>), dim3(total), dim3(2 * NT), 0, st, p);
+    } else {
+        return false;
+    }
+#undef OMG_L
     return true;
 }
 
@@ -127,29 +160,36 @@ struct XTile {
 const XTile kXTiles[] = {{64, 64, 32},  {64, 96, 32},   {96, 64, 32},  {64, 128, 32}, {128, 64, 32},
                          {128, 128, 32}, {64, 64, 64},  {64, 96, 64},  {128, 128, 64}};
 
+// Launches tile t; false when t (or its GELU variant) is not instantiated.
 static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
-#define OMG_X(BM, BN, BKT) \
-    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT>(p, batch, ta, tb, st);
-    OMG_X(64, 64, 32)
-    OMG_X(64, 96, 32)
-    OMG_X(96, 64, 32)
-    OMG_X(64, 128, 32)
-    OMG_X(128, 64, 32)
-    OMG_X(128, 128, 32)
-    OMG_X(64, 64, 64)
-    OMG_X(64, 96, 64)
-    OMG_X(128, 128, 64)
+    // bkt 33 / 65 select the eight-wavefront variant of the 32 / 64 chunk.
+    if (t.bkt == 33 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 32, true>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 64 && t.bn == 64) return launch_x2<64, 64, 32, true>(p, batch, ta, tb, st);
+    if (t.bkt == 65 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 64, false>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, false>(p, batch, ta, tb, st);
+#define OMG_X(BM, BN, BKT, G) \
+    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, G>(p, batch, ta, tb, st);
+    OMG_X(64, 64, 32, true)
+    OMG_X(64, 96, 32, true)
+    OMG_X(96, 64, 32, false)
+    OMG_X(64, 128, 32, false)
+    OMG_X(128, 64, 32, false)
+    OMG_X(128, 128, 32, false)
+    OMG_X(64, 64, 64, true)
+    OMG_X(64, 96, 64, false)
+    OMG_X(128, 128, 64, false)
 #undef OMG_X
     return false;
 }
 
 // Whether tile t covers the product exactly (full tiles, whole chunks per split, 32-bit in-tile offsets).
 static bool x_fits(const XTile &t, const Params &p, int splits, int k_split) {
-    if (p.m % t.bm || p.n % t.bn || p.k % t.bkt || k_split % t.bkt) return false;
+    const int ck = t.bkt & ~1;  // chunk depth (an odd bkt selects the eight-wavefront variant)
+    if (p.m % t.bm || p.n % t.bn || p.k % ck || k_split % ck) return false;
     if (splits > 1 && (int64_t)(splits - 1) * k_split >= p.k) return false;
     const int64_t ld = p.lda > p.ldb ? p.lda : p.ldb;
     const int rows = t.bm > t.bn ? t.bm : t.bn;
-    return ld * (rows > t.bkt ? rows : t.bkt) < (int64_t)1 << 31;
+    return ld * (rows > ck ? rows : ck) < (int64_t)1 << 31;
 }
 
 namespace {
@@ -166,13 +206,13 @@ const Tuned kTuned[] = {
     {4096, 384, 1536, false, true, 64, 96, 32, 1},    {4096, 1152, 384, false, true, 64, 96, 32, 1},
     {4096, 768, 768, false, true, 64, 64, 32, 1},     {4096, 3072, 768, false, true, 128, 128, 32, 1},
     {4096, 768, 3072, false, true, 64, 64, 32, 1},    {4096, 2304, 768, false, true, 64, 64, 32, 1},
-    // input gradient dx = g W (NN)
-    {4096, 384, 384, false, false, 64, 96, 32, 1},    {4096, 384, 1536, false, false, 64, 96, 32, 1},
-    {4096, 1536, 384, false, false, 64, 64, 64, 1},   {4096, 384, 1152, false, false, 64, 96, 32, 1},
+    // input gradient dx = g W (NN); bkt 33 = the eight-wavefront kernel with 32-deep chunks
+    {4096, 384, 384, false, false, 64, 96, 33, 1},    {4096, 384, 1536, false, false, 64, 96, 33, 1},
+    {4096, 1536, 384, false, false, 64, 64, 33, 1},   {4096, 384, 1152, false, false, 64, 96, 33, 1},
     {4096, 768, 768, false, false, 64, 64, 32, 1},    {4096, 768, 3072, false, false, 64, 64, 32, 1},
-    {4096, 3072, 768, false, false, 128, 128, 32, 1}, {4096, 768, 2304, false, false, 64, 64, 32, 1},
+    {4096, 3072, 768, false, false, 128, 128, 33, 1}, {4096, 768, 2304, false, false, 64, 64, 32, 1},
     // weight gradient dW = g^T x (TN), K = tokens
-    {384, 384, 4096, true, false, 64, 96, 32, 8},     {1536, 384, 4096, true, false, 64, 96, 32, 8},
+    {384, 384, 4096, true, false, 64, 96, 33, 8},     {1536, 384, 4096, true, false, 64, 96, 32, 8},
     {384, 1536, 4096, true, false, 64, 96, 32, 8},    {1152, 384, 4096, true, false, 64, 64, 32, 4},
     {768, 768, 4096, true, false, 64, 96, 32, 8},     {3072, 768, 4096, true, false, 64, 96, 32, 2},
     {768, 3072, 4096, true, false, 64, 96, 32, 2},    {2304, 768, 4096, true, false, 64, 96, 32, 2},
@@ -184,7 +224,7 @@ int split_len(int k, int splits, int bkt) { return ((k + splits - 1) / splits + 
 Choice with_splits(int bm, int bn, int bkt, int k, int splits) {
     Choice c{bm, bn, 1, k, bkt};
     if (splits > 1) {
-        c.k_split = split_len(k, splits, bkt);
+        c.k_split = split_len(k, splits, bkt & ~1);
         c.splits = (k + c.k_split - 1) / c.k_split;
         if (c.splits <= 1) c.k_split = k;
     }
@@ -250,7 +290,8 @@ Choice choose(int m, int n, int k, int batch, int cus) {
     return c;
 }
 
-om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what) {
+om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what, bool *colsum_fused) {
+    if (colsum_fused) *colsum_fused = false;
     if (p.m <= 0 || p.n <= 0 || batch <= 0) return OM_OK;
     p.batch = batch;
     bool vec = ((uintptr_t)p.a % 16 == 0) && ((uintptr_t)p.b % 16 == 0) && p.lda % 4 == 0 && p.ldb % 4 == 0 &&
@@ -260,18 +301,33 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     Choice c = p.k <= 0 ? Choice{64, 64, 1, 1, 16}
                         : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus)
                                 : choose(p.m, p.n, p.k, batch, ctx->num_cus));
+    if (fast && p.epi != EPI_NONE) {  // only some tiles carry the GELU epilogue
+        const bool ok = ((c.bkt == 32 || c.bkt == 33) && c.bm == 64 && (c.bn == 64 || c.bn == 96)) ||
+                        (c.bkt == 64 && c.bm == 64 && c.bn == 64);
+        if (!ok) c = with_splits(64, 64, 32, p.k, c.splits);
+    }
     bool use_x = fast && !x_disabled() && x_fits(XTile{c.bm, c.bn, c.bkt}, p, c.splits, c.k_split);
     if (fast && !use_x && c.bkt != 32) c = with_splits(c.bm, c.bn, 32, p.k, c.splits);  // guarded set: BK = 32
+    c.bkt = use_x ? c.bkt : 32;
     p.splits = c.splits;
     p.k_split = c.splits > 1 ? c.k_split : (p.k > 0 ? p.k : 1);
     p.ws = nullptr;
     p.xcd_remap = 1;
+    // A fused bias gradient needs a tile-exact TN launch whose row groups divide the workgroup.
+    const bool cs = p.db && use_x && ta && !tb && batch == 1 && ((c.bkt & 1) ? 2 * NT : NT) % c.bm == 0;
+    if (!cs) {
+        p.db = nullptr;
+        p.colsum_ws = nullptr;
+    }
     if (p.splits > 1) {
         float *ws;
-        om_status s = om::scratch(ctx, sizeof(float) * (uint64_t)p.splits * p.m * p.n, &ws);
+        const uint64_t cbytes = cs ? (sizeof(double) * (uint64_t)p.splits * p.m + 255) / 256 * 256 : 0;
+        om_status s = om::scratch(ctx, cbytes + sizeof(float) * (uint64_t)p.splits * p.m * p.n, &ws);
         if (s) return s;
-        p.ws = ws;
+        p.colsum_ws = cs ? reinterpret_cast<double *>(ws) : nullptr;
+        p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
     }
+    if (colsum_fused) *colsum_fused = cs;
     hipStream_t st = ctx->stream;
     bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st);
     if (launched) {
@@ -368,14 +424,51 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd dx");
         if (s) return s;
     }
+    bool db_done = false;
     if (dw) {
         omg::Params p = omg::dense_params(out, in, rows, g, out, x, in, dw, in);
         p.accumulate = acc_dw;
-        s = omg::launch_dense(ctx, p, true, false, 1, "om_linear_bwd dw");
+        p.db = db;  // the bias gradient rides along with dW when the kernel can sum g's columns
+        p.db_acc = acc_db;
+        s = omg::launch_dense(ctx, p, true, false, 1, "om_linear_bwd dw", &db_done);
         if (s) return s;
     }
-    if (db) s = om_colsum(ctx, g, db, rows, out, acc_db);
+    if (db && !db_done) s = om_colsum(ctx, g, db, rows, out, acc_db);
     return s;
+}
+
+om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,
+                              float *y, int rows, int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && y && resid && rows >= 0 && in > 0 && out > 0, "om_linear_fwd_resid: bad arguments");
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
+    p.bias = b;
+    p.resid = resid;
+    p.ldr = out;
+    return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd_resid");
+}
+
+om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *h, float *a, int rows,
+                             int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && h && a && rows >= 0 && in > 0 && out > 0, "om_linear_gelu_fwd: bad arguments");
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, h, out);
+    p.bias = b;
+    p.epi = omg::EPI_GELU;
+    p.out2 = a;
+    p.ld2 = out;
+    return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd");
+}
+
+om_status om_linear_bwd_dx_gelu(om_ctx *ctx, const float *g, const float *w, const float *h, float *dh, int rows,
+                                int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && w && h && dh && rows >= 0 && in > 0 && out > 0, "om_linear_bwd_dx_gelu: bad arguments");
+    omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dh, in);
+    p.epi = omg::EPI_GELU_GRAD;
+    p.aux = h;
+    p.ldaux = in;
+    return omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd_dx_gelu");
 }
 
 }  // extern "C"

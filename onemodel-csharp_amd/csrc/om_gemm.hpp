@@ -14,6 +14,9 @@ Choice choose(int m, int n, int k, int batch, int cus);
 Params dense_params(int m, int n, int k, const float *a, int64_t lda, const float *b, int64_t ldb, float *c,
                     int64_t ldc);
 // Launches a dense (optionally batched) product; adds the split-K reduce when the chooser splits K.
-om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what);
+// With p.db set on a weight-gradient product (ta, !tb), the bias gradient db (+)= column sums of A is fused into the
+// launch when the chosen kernel supports it; *colsum_fused reports whether it was (else p.db was ignored).
+om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what,
+                       bool *colsum_fused = nullptr);
 
 }  // namespace omg

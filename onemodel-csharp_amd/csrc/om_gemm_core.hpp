@@ -56,7 +56,44 @@ struct Params {
     // convolution geometry (gather loaders)
     int cin, h, w, cout, kh, kw, stride, pad, oh, ow;
     int xcd_remap;
+    // fused epilogue terms, applied after alpha, mask and bias (dense products only):
+    //   resid: v += resid[row * ldr + col] (a residual Add after the Linear);
+    //   epi EPI_GELU: C gets v (the pre-activation, which GELU's backward reads) and out2 gets gelu(v);
+    //   epi EPI_GELU_GRAD: C gets gelu_grad(v, aux[row * ldaux + col]) (GELU's backward of the product).
+    const float *resid;
+    int64_t ldr;
+    int epi;
+    float *out2;
+    int64_t ld2;
+    const float *aux;
+    int64_t ldaux;
+    // fused bias gradient of a weight-gradient product (A transposed, stored [k][m]): db[m] (+)= sum over k of A in
+    // double. The tile-exact kernels' first column of tiles sums its A chunks from LDS; with split K the per-split
+    // sums go to colsum_ws[split * m + row] and the split-K reduce finishes them.
+    double *colsum_ws;
+    float *db;
+    int db_acc;
 };
+
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2 };
+
+// The epilogue of one finished dot product v at (row, col): alpha, mask, bias, residual, GELU terms, then C. The
+// GELU polynomials are compiled only into the instantiations that can be asked for them (GELU = true): inlined
+// into every large-tile kernel they would raise register pressure enough to spill.
+template <bool GELU = true>
+__device__ __forceinline__ void epilogue(const Params &p, float *cbase, int64_t ldc, const float *mask, int row, int col,
+                                         float v) {
+    if (p.alpha != 1.0f) v = v * p.alpha;
+    if (mask) v = v + mask[(int64_t)row * p.n + col];
+    if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
+    if (p.resid) v = v + p.resid[(int64_t)row * p.ldr + col];
+    if constexpr (GELU) {
+        if (p.epi == EPI_GELU) p.out2[(int64_t)row * p.ld2 + col] = omd::gelu(v);
+        else if (p.epi == EPI_GELU_GRAD) v = omd::gelu_grad(v, p.aux[(int64_t)row * p.ldaux + col]);
+    }
+    float *dst = cbase + (int64_t)row * ldc + col;
+    *dst = p.accumulate ? *dst + v : v;
+}
 
 // ------------------------------------------------------------------------------------------------ loaders
 // A loader fills one LDS buffer for k in [k0, k0 + BKT) and rows in [r0, r0 + ROWS) of its logical operand (A: rows
@@ -209,7 +246,7 @@ __device__ __forceinline__ void tile_coords(const Params &p, int tiles_n, int ti
 }
 
 // Epilogue for one accumulator tile: writes C (or the split-K partial).
-template <class TL>
+template <class TL, bool GELU = false>
 __device__ __forceinline__ void store_tile(const Params &p, TL &t, int m0, int n0, int wm0, int wn0, int lane,
                                            float *cbase, int64_t ldc, const float *mask, int split) {
     const int col_l = lane & 15, row_l = (lane >> 4) * 4;
@@ -228,11 +265,7 @@ __device__ __forceinline__ void store_tile(const Params &p, TL &t, int m0, int n
                     p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
                     continue;
                 }
-                if (p.alpha != 1.0f) v = v * p.alpha;
-                if (mask) v = v + mask[(int64_t)row * p.n + col];
-                if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
-                float *dst = cbase + (int64_t)row * ldc + col;
-                *dst = p.accumulate ? *dst + v : v;
+                epilogue<GELU>(p, cbase, ldc, mask, row, col, v);
             }
         }
 }

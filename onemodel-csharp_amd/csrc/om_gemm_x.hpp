@@ -23,12 +23,14 @@
 namespace omg {
 namespace gx {
 
-// Exact loader of one operand chunk: ROWS x BKT values (KCONTIG: rows contiguous along k; else along the rows).
-template <int ROWS, int BKT, bool KCONTIG>
+// Exact loader of one operand chunk: ROWS x BKT values (KCONTIG: rows contiguous along k; else along the rows),
+// spread over NTH threads (a chunk that does not split evenly leaves whole wavefronts idle on the last load).
+template <int ROWS, int BKT, bool KCONTIG, int NTH = NT>
 struct Ld {
     static constexpr int TOT = ROWS * BKT / 4;
-    static_assert(TOT % NT == 0, "a chunk must split evenly over the workgroup");
-    static constexpr int NV = TOT / NT;
+    static_assert(TOT % 64 == 0, "a chunk must split into whole wavefronts");
+    static constexpr int NV = (TOT + NTH - 1) / NTH;
+    static constexpr bool RAGGED = TOT % NTH != 0;
     static constexpr int LDSZ = KCONTIG ? ROWS * (BKT + PAD) : BKT * (ROWS + PAD);
     const float *base;  // operand origin of this tile (row r0, k 0)
     int64_t ld;
@@ -38,7 +40,8 @@ struct Ld {
     __device__ __forceinline__ Ld(const float *b, int64_t ld_, int r0) : ld(ld_) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
-            int f = threadIdx.x + i * NT;
+            int f = threadIdx.x + i * NTH;
+            if (RAGGED && f >= TOT) f = TOT - 1;  // unused: the load and store below are skipped for it
             if constexpr (KCONTIG) {
                 int r = f / (BKT / 4), kq = (f % (BKT / 4)) * 4;
                 goff[i] = (int)(r * ld) + kq;
@@ -54,11 +57,15 @@ struct Ld {
     __device__ __forceinline__ void fetch(floatx4 (&v)[NV], int k0) const {
         const float *p = base + (KCONTIG ? (int64_t)k0 : (int64_t)k0 * ld);
 #pragma unroll
-        for (int i = 0; i < NV; i++) v[i] = *reinterpret_cast<const floatx4 *>(p + goff[i]);
+        for (int i = 0; i < NV; i++)
+            if (!RAGGED || i + 1 < NV || (int)threadIdx.x + i * NTH < TOT)
+                v[i] = *reinterpret_cast<const floatx4 *>(p + goff[i]);
     }
     __device__ __forceinline__ void put(const floatx4 (&v)[NV], float *T) const {
 #pragma unroll
-        for (int i = 0; i < NV; i++) *reinterpret_cast<floatx4 *>(T + soff[i]) = v[i];
+        for (int i = 0; i < NV; i++)
+            if (!RAGGED || i + 1 < NV || (int)threadIdx.x + i * NTH < TOT)
+                *reinterpret_cast<floatx4 *>(T + soff[i]) = v[i];
     }
 };
 
@@ -101,7 +108,40 @@ __device__ __forceinline__ void read_frag(float (&f)[4][TX], const float *T, int
     }
 }
 
-template <int BM, int BN, int BKT, bool TA, bool TB>
+// Fused bias gradient of a weight-gradient product: column sums of A (transposed, staged [BKT][BM+4] in LDS) over
+// the k rows of each chunk, in double. Thread x of NTH sums column x % BM over rows x / BM, x / BM + NTH / BM, ...;
+// colsum_finish combines the NTH / BM row groups in order and writes the tile's BM sums.
+template <int BM, int BKT, int NTH>
+struct ColSum {
+    static constexpr int RG = NTH / BM;
+    static_assert(NTH % BM == 0 && BKT % RG == 0, "column sums need whole row groups");
+    double s = 0.0;
+    __device__ __forceinline__ void add(const float *Ab) {
+        const int c = threadIdx.x % BM, rg = threadIdx.x / BM;
+#pragma unroll
+        for (int kk = rg; kk < BKT; kk += RG) s += (double)Ab[kk * (BM + PAD) + c];
+    }
+    // Uses `sh` (RG * BM doubles of LDS, free when called) and ends with a barrier.
+    __device__ __forceinline__ void finish(const Params &p, double *sh, int m0, int split) {
+        sh[threadIdx.x] = s;
+        __syncthreads();
+        if ((int)threadIdx.x < BM) {
+            double t = sh[threadIdx.x];
+#pragma unroll
+            for (int g = 1; g < RG; g++) t += sh[g * BM + threadIdx.x];
+            const int row = m0 + threadIdx.x;
+            if (p.splits > 1) {
+                p.colsum_ws[(int64_t)split * p.m + row] = t;
+            } else {
+                float v = (float)t;
+                p.db[row] = p.db_acc ? p.db[row] + v : v;
+            }
+        }
+        __syncthreads();
+    }
+};
+
+template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
 __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     constexpr bool AK = !TA, BKL = TB;  // operands in K layout
     constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
@@ -147,8 +187,14 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
     };
+    // Bias gradient: the first column of tiles of a TN product sums its A chunks (A is [k][m] in LDS).
+    constexpr bool CS_OK = TA && (NT % BM == 0) && (BKT % (NT / BM) == 0);
+    ColSum<CS_OK ? BM : 64, BKT, NT> cs;
+    const bool do_cs = CS_OK && p.db && tn == 0;
     // Blocks 0 .. NB-2 of the chunk in (Ab, Bb): the fragments of block b+1 are read while block b multiplies.
     auto body = [&](const float *Ab, const float *Bb) {
+        if constexpr (CS_OK)
+            if (do_cs) cs.add(Ab);
 #pragma unroll
         for (int blk = 0; blk + 1 < NB; blk++) {
             if (blk & 1) rd(fa0, fb0, Ab, Bb, blk + 1);
@@ -206,6 +252,11 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
         body(Al, Bl);
         mm(fa1, fb1);
     }
+    if constexpr (CS_OK)
+        if (p.db && tn == 0) {  // uniform over the workgroup
+            __syncthreads();
+            cs.finish(p, reinterpret_cast<double *>(As), m0, split);
+        }
 
     // Epilogue: output register r of MFMA block (i, j) on this lane is row rho = 4*kl + r, column l16 of the block.
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
@@ -224,11 +275,151 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
                     p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
                     continue;
                 }
-                if (p.alpha != 1.0f) v = v * p.alpha;
-                if (mask) v = v + mask[(int64_t)row * p.n + col];
-                if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
-                float *dst = C + (int64_t)row * p.ldc + col;
-                *dst = p.accumulate ? *dst + v : v;
+                epilogue<GELU>(p, C, p.ldc, mask, row, col, v);
+            }
+        }
+}
+
+// The same tile with eight wavefronts: two groups of four (2 x 2 over the tile, as above) split each chunk's 16-k
+// blocks between them (group g takes blocks g, g+2, ...), so every SIMD runs two wavefronts of the tile and one's LDS
+// and barrier waits hide behind the other's MFMAs. At the end group 1 hands its partial sums to group 0 through LDS
+// and group 0 adds them (in that fixed order) and runs the epilogue. For products with about one tile per CU.
+template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
+__global__ void __launch_bounds__(2 * NT) k_gemm_x2(Params p) {
+    constexpr int NTH = 2 * NT;
+    constexpr bool AK = !TA, BKL = TB;
+    constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
+    static_assert(NB % 2 == 0, "each group needs whole 16-k blocks");
+    using LA = Ld<BM, BKT, AK, NTH>;
+    using LB = Ld<BN, BKT, BKL, NTH>;
+    __shared__ __attribute__((aligned(16))) float Sh[2 * LA::LDSZ + 2 * LB::LDSZ];
+    static_assert(2 * (LA::LDSZ + LB::LDSZ) >= BM * BN, "the partial-sum exchange reuses the operand buffers");
+    float *As = Sh, *Bs = Sh + 2 * LA::LDSZ;
+
+    const int tiles_n = p.n / BN, tiles_m = p.m / BM;
+    int tm, tn, zz;
+    tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
+    if (zz >= p.batch * p.splits) return;
+    const int z = zz / p.splits, split = zz % p.splits;
+    const int outer = z / p.batch_div, inner = z % p.batch_div;
+    const float *A = p.a + outer * p.sa_outer + inner * p.sa_inner;
+    const float *B = p.b + outer * p.sb_outer + inner * p.sb_inner;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kbeg = split * p.k_split;
+    const int nk = (min(p.k, kbeg + p.k_split) - kbeg) / BKT;
+    const int lane = threadIdx.x & 63, wv = (threadIdx.x >> 6) & 3, kg = threadIdx.x >> 8;
+    const int l16 = lane & 15, kl = lane >> 4;
+    const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const LA la(A, p.lda, m0);
+    const LB lb(B, p.ldb, n0);
+    constexpr bool CS_OK = TA && (NTH % BM == 0) && (BKT % (NTH / BM) == 0);
+    ColSum<CS_OK ? BM : 64, BKT, NTH> cs;
+    const bool do_cs = CS_OK && p.db && tn == 0;
+    auto chunk = [&](const float *Ab, const float *Bb) {
+        if constexpr (CS_OK)
+            if (do_cs) cs.add(Ab);
+#pragma unroll
+        for (int blk = 0; blk < NB; blk += 2) {
+            float fa[4][TM], fb[4][TN];
+            read_frag<BM, BKT, TM, AK>(fa, Ab, blk + kg, wm0, l16, kl);
+            read_frag<BN, BKT, TN, BKL>(fb, Bb, blk + kg, wn0, l16, kl);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[s][i], fb[s][j], acc[i][j], 0, 0, 0);
+        }
+    };
+    if (nk > 0) {
+        floatx4 ra0[LA::NV], rb0[LB::NV], ra1[LA::NV], rb1[LB::NV];
+        const int klast = kbeg + (nk - 1) * BKT;
+        float *A0 = As, *A1 = As + LA::LDSZ, *B0 = Bs, *B1 = Bs + LB::LDSZ;
+        la.fetch(ra0, kbeg);
+        lb.fetch(rb0, kbeg);
+        la.fetch(ra1, min(kbeg + BKT, klast));
+        lb.fetch(rb1, min(kbeg + BKT, klast));
+        la.put(ra0, A0);
+        lb.put(rb0, B0);
+        __syncthreads();
+        int t = 0;
+        for (; t + 2 < nk; t += 2) {  // both halves always run (clamped loads), see k_gemm_x
+            la.fetch(ra0, min(kbeg + (t + 2) * BKT, klast));
+            lb.fetch(rb0, min(kbeg + (t + 2) * BKT, klast));
+            __builtin_amdgcn_sched_barrier(0);
+            chunk(A0, B0);
+            la.put(ra1, A1);
+            lb.put(rb1, B1);
+            __syncthreads();
+            la.fetch(ra1, min(kbeg + (t + 3) * BKT, klast));
+            lb.fetch(rb1, min(kbeg + (t + 3) * BKT, klast));
+            __builtin_amdgcn_sched_barrier(0);
+            chunk(A1, B1);
+            la.put(ra0, A0);
+            lb.put(rb0, B0);
+            __syncthreads();
+        }
+        const float *Al = A0, *Bl = B0;
+        if (nk - t == 2) {
+            chunk(A0, B0);
+            la.put(ra1, A1);
+            lb.put(rb1, B1);
+            __syncthreads();
+            Al = A1;
+            Bl = B1;
+        }
+        chunk(Al, Bl);
+    }
+    if constexpr (CS_OK)
+        if (p.db && tn == 0) {
+            __syncthreads();
+            cs.finish(p, reinterpret_cast<double *>(Sh), m0, split);
+        }
+    // Group 1's partial sums -> LDS (the operand buffers, after everyone is done with them) -> group 0.
+    __syncthreads();
+    float *X = Sh;  // [4 waves][TM*TN*4][64 lanes]
+    constexpr int PER = TM * TN * 4;
+    if (kg == 1) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) X[(wv * PER + (i * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[i][j][r] = acc[i][j][r] + X[(wv * PER + (i * TN + j) * 4 + r) * 64 + lane];
+
+    float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
+    const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int rho = 4 * kl + r;
+            const int row = m0 + wm0 + (AK ? i * 16 + rho : TM * rho + i);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int col = n0 + wn0 + (BKL ? j * 16 + l16 : TN * l16 + j);
+                float v = acc[i][j][r];
+                if (p.splits > 1) {
+                    p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
+                    continue;
+                }
+                epilogue<GELU>(p, C, p.ldc, mask, row, col, v);
             }
         }
 }

@@ -33,6 +33,9 @@ struct om_ctx {
     // Device scratch owned by the context (split-K partials, per-row statistics); grown on demand between steps.
     float *scratch = nullptr;
     uint64_t scratch_bytes = 0;
+    // Second slot for callers that launch GEMMs while holding their own scratch (attention's score recompute).
+    float *scratch2 = nullptr;
+    uint64_t scratch2_bytes = 0;
     int num_cus = 256;
 };
 
@@ -43,6 +46,8 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 // Returns device scratch of at least `bytes` (kept by the context; valid until the next call that grows it, which
 // first synchronises the stream so no in-flight kernel still reads the old buffer).
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
+// The same for the second slot (never used by the GEMM engine itself).
+om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
 // out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column; a second
 // (part2, out2) pair of the same shape is reduced in the same launch when given.
 om_status chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,
@@ -100,6 +105,26 @@ __device__ __forceinline__ double block_sum(double v, double *sh) {
 #pragma unroll
     for (int i = 0; i < NW; i++) t += sh[i];
     return t;
+}
+
+// The reference's canonical 16-partial sum (RowReduce.Sum16, Softmax.cs:139-179) over one row held by a 16-lane group:
+// lane t holds p[t] = sum of the row's elements j = t, t+16, ... in increasing j; the halving combine p[t]+p[t+8],
+// +4, +2, +1 runs as shuffles inside the group, so the bits equal the reference's; every lane gets the total.
+__device__ __forceinline__ float sum16(float p) {
+    p = p + __shfl_down(p, 8, 16);
+    p = p + __shfl_down(p, 4, 16);
+    p = p + __shfl_down(p, 2, 16);
+    p = p + __shfl_down(p, 1, 16);
+    return __shfl(p, 0, 16);
+}
+// Row maximum over a 16-lane group ignoring NaN (RowReduce.Max, Softmax.cs:181-212); exact, so order-free.
+__device__ __forceinline__ float max16(float v) {
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) {
+        float w = __shfl_xor(v, o, 16);
+        v = w > v ? w : v;
+    }
+    return v;
 }
 
 // The reference's fp32 polynomials (Transcendental.cs:39-263), restated with one IEEE rounding per operation; the
@@ -183,6 +208,23 @@ __device__ __forceinline__ void erf_parts(float x, float &erf, float &ope) {
     bool ok = x == x;
     erf = canon(ok ? erfSigned : x);
     ope = canon(ok ? (isSmall ? opeSmall : opeLarge) : x);
+}
+
+// GELU, erf form (Ops.Gelu, Ops.Nn.cs:86-112; Transcendental.GeluErf, Transcendental.cs:252): 0.5 x (1 + erf(x/sqrt2)).
+__device__ __forceinline__ float gelu(float x) {
+    float e, ope;
+    erf_parts(x * 0.70710677f, e, ope);
+    float res = (0.5f * x) * ope;
+    if (x == -__int_as_float(0x7F800000)) res = -0.0f;
+    return canon(x == x ? res : x);
+}
+// GeluGradBin (TrainElementwise.cs:59-85): g * (0.5 (1 + erf(x/sqrt2)) + x exp(-x^2/2) / sqrt(2 pi)).
+__device__ __forceinline__ float gelu_grad(float g, float v) {
+    float e, ope;
+    erf_parts(v * 0.70710677f, e, ope);
+    float cdf = 0.5f * (1.0f + e);
+    float pdf = exp_poly((-0.5f * v) * v) * 0.3989423f;
+    return canon(g * (cdf + v * pdf));
 }
 
 }  // namespace omd

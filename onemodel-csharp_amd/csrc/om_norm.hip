@@ -8,25 +8,8 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// The reference's canonical 16-partial sum (RowReduce.Sum16, Softmax.cs:139-179) over one row held by 16 lanes:
-// lane t accumulates elements j = t, t+16, ... in increasing j; the halving combine p[t]+p[t+8], +4, +2, +1 is done
-// with shuffles inside the 16-lane group, so the bits equal the reference's at every lane width.
-__device__ __forceinline__ float sum16_combine(float p) {
-    p = p + __shfl_down(p, 8, 16);
-    p = p + __shfl_down(p, 4, 16);
-    p = p + __shfl_down(p, 2, 16);
-    p = p + __shfl_down(p, 1, 16);
-    return __shfl(p, 0, 16);
-}
-// Row maximum ignoring NaN (RowReduce.Max, Softmax.cs:181-212); max is exact, so the order does not matter.
-__device__ __forceinline__ float max16(float v) {
-#pragma unroll
-    for (int o = 8; o > 0; o >>= 1) {
-        float w = __shfl_xor(v, o, 16);
-        v = w > v ? w : v;
-    }
-    return v;
-}
+using omd::max16;
+__device__ __forceinline__ float sum16_combine(float p) { return omd::sum16(p); }
 
 // LayerNorm forward: one row per 16-lane group (4 rows per wavefront). NormKernels.Rows (NormKernels.cs:79-127):
 // mean = Sum16(x)/n, ssq = Sum16((x-mean)^2), inv = 1/sqrt(ssq/n + eps), y = (((x-mean)*inv)*gamma)+beta.

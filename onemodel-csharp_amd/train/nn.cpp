@@ -92,6 +92,9 @@ Tensor MultiHeadAttention::operator()(const Tensor &x, const Tensor &mask) const
     // Layers.cs:497-516: q/k/v projections, split heads, attention, merge heads, output projection.
     return (*o)(attention_qkv(x, q->w, q->b, k->w, k->b, v->w, v->b, mask, heads));
 }
+Tensor MultiHeadAttention::residual(const Tensor &x, const Tensor &mask, const Tensor &resid) const {
+    return linear_residual(attention_qkv(x, q->w, q->b, k->w, k->b, v->w, v->b, mask, heads), o->w, o->b, resid);
+}
 
 // Post-norm TransformerEncoderLayer (Layers.cs:523-578).
 struct EncoderLayer : Module {
@@ -106,8 +109,10 @@ struct EncoderLayer : Module {
         norm2 = child("norm2", std::make_unique<LayerNorm>(width));
     }
     Tensor operator()(const Tensor &x, const Tensor &mask) const {
-        Tensor x1 = (*norm1)(add(x, (*attn)(x, mask)));
-        return (*norm2)(add(x1, (*ff2)(gelu((*ff1)(x1)))));
+        // norm1(x + attn(x)), then norm2(x1 + ff2(gelu(ff1(x1)))), with the residual Adds and GELU fused into the
+        // Linear launches
+        Tensor x1 = (*norm1)(attn->residual(x, mask, x));
+        return (*norm2)(ffn(x1, ff1->w, ff1->b, ff2->w, ff2->b, x1));
     }
 };
 // The C3 block: pre-norm, composed from the reference's pieces (children ln1, attn, ln2, ff1, ff2).
@@ -123,8 +128,9 @@ struct PreNormBlock : Module {
         ff2 = child("ff2", std::make_unique<Linear>(ff, width, g));
     }
     Tensor operator()(const Tensor &x, const Tensor &mask) const {
-        Tensor h = add(x, (*attn)((*ln1)(x), mask));
-        return add(h, (*ff2)(gelu((*ff1)((*ln2)(h)))));
+        // h = x + attn(ln1(x)); y = h + ff2(gelu(ff1(ln2(h)))), the Adds and GELU fused into the Linear launches
+        Tensor h = attn->residual((*ln1)(x), mask, x);
+        return ffn((*ln2)(h), ff1->w, ff1->b, ff2->w, ff2->b, h);
     }
 };
 

@@ -316,11 +316,11 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
         shape_error("The mask must be [" + std::to_string(B) + "," + std::to_string(L) + "," + std::to_string(L) +
                     "], not " + shape_str(mask->shape));
     Tensor o = make(q->shape);
-    float *p = dev().step_floats((int64_t)B * heads * L * L);
     const float *md = mask ? mask->data : nullptr;
-    OMT(om_attention_fwd(C(), q->data, k->data, v->data, md, 1, o->data, p, B, heads, L, L, D, 0.0f));
+    const int W = heads * D;
+    OMT(om_attention_fwd_fused(C(), q->data, k->data, v->data, W, md, 1, o->data, W, B, heads, L, D, 0.0f));
     if (tracked({&q, &k, &v}))
-        attach(o, "Attention", {q, k, v}, [p, B, heads, L, D](Engine &e, Record &r, const float *g) {
+        attach(o, "Attention", {q, k, v}, [md, B, heads, L, D, W](Engine &e, Record &r, const float *g) {
             int a[3];
             float *d[3];
             for (int i = 0; i < 3; i++) d[i] = e.dest(r, i, &a[i]);
@@ -331,10 +331,9 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
                 if (d[i] && a[i] != common) {
                     tmp[i] = dev().step_floats(r.inputs[i]->numel);
                 }
-            float *ds = dev().step_floats((int64_t)B * heads * L * L);
-            OMT(om_attention_bwd(C(), r.inputs[0]->data, r.inputs[1]->data, r.inputs[2]->data, p, g,
-                                 tmp[0] ? tmp[0] : d[0], tmp[1] ? tmp[1] : d[1], tmp[2] ? tmp[2] : d[2], ds, B, heads,
-                                 L, L, D, 0.0f, common));
+            OMT(om_attention_bwd_fused(C(), r.inputs[0]->data, r.inputs[1]->data, r.inputs[2]->data, W, md, 1, g, W,
+                                       tmp[0] ? tmp[0] : d[0], tmp[1] ? tmp[1] : d[1], tmp[2] ? tmp[2] : d[2], W, B,
+                                       heads, L, D, 0.0f, common));
             for (int i = 0; i < 3; i++)
                 if (tmp[i]) {
                     if (a[i]) OMT(om_axpy(C(), 1.0f, tmp[i], d[i], r.inputs[i]->numel));
@@ -342,6 +341,70 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
                 }
         });
     return o;
+}
+
+Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const Tensor &resid) {
+    if (w->shape.size() != 2 || x->shape.empty() || x->shape.back() != w->shape[1])
+        shape_error("Linear: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w->shape) + " ([out, in]).");
+    const int in = w->shape[1], out = w->shape[0];
+    const int rows = (int)(x->numel / in);
+    std::vector<int> ys = x->shape;
+    ys.back() = out;
+    if (resid->shape != ys) shape_error("Add: shapes " + shape_str(resid->shape) + " and " + shape_str(ys) + " differ.");
+    Tensor y = make(ys);
+    OMT(om_linear_fwd_resid(C(), x->data, w->data, b ? b->data : nullptr, resid->data, y->data, rows, in, out));
+    if (tracked({&x, &w, &b, &resid})) {
+        attach(y, "LinearAdd", {x, w, b, resid}, [rows, in, out](Engine &e, Record &r, const float *g) {
+            int ax, aw, ab = 0;
+            float *dx = e.dest(r, 0, &ax);
+            float *dw = e.dest(r, 1, &aw);
+            float *db = r.inputs[2] ? e.dest(r, 2, &ab) : nullptr;
+            OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw, ab));
+            if (r.needs(3)) e.emit_alias(r, 3, g);  // Add backward: the residual gets g unchanged
+        });
+    }
+    return y;
+}
+
+Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
+           const Tensor &resid) {
+    if (w1->shape.size() != 2 || w2->shape.size() != 2 || x->shape.empty() || x->shape.back() != w1->shape[1] ||
+        w2->shape[1] != w1->shape[0])
+        shape_error("FeedForward: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w1->shape) +
+                    " and " + shape_str(w2->shape));
+    const int d = w1->shape[1], f = w1->shape[0], o = w2->shape[0];
+    const int rows = (int)(x->numel / d);
+    std::vector<int> ys = x->shape;
+    ys.back() = o;
+    if (resid && resid->shape != ys)
+        shape_error("Add: shapes " + shape_str(resid->shape) + " and " + shape_str(ys) + " differ.");
+    float *h = dev().step_floats((int64_t)rows * f);  // pre-activation, read by GELU's backward
+    float *a = dev().step_floats((int64_t)rows * f);  // GELU output, read by Linear2's weight gradient
+    OMT(om_linear_gelu_fwd(C(), x->data, w1->data, b1 ? b1->data : nullptr, h, a, rows, d, f));
+    Tensor y = make(ys);
+    if (resid) OMT(om_linear_fwd_resid(C(), a, w2->data, b2 ? b2->data : nullptr, resid->data, y->data, rows, f, o));
+    else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
+    if (tracked({&x, &w1, &b1, &w2, &b2, &resid})) {
+        attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [h, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
+            int aw2, ab2 = 0;
+            float *dw2 = e.dest(r, 3, &aw2);
+            float *db2 = r.inputs[4] ? e.dest(r, 4, &ab2) : nullptr;
+            OMT(om_linear_bwd(C(), g, a, r.inputs[3]->data, nullptr, dw2, db2, rows, f, o, 0, aw2, ab2));
+            const bool below = r.needs(0) || r.needs(1) || r.needs(2);
+            if (below) {
+                float *dh = dev().step_floats((int64_t)rows * f);
+                OMT(om_linear_bwd_dx_gelu(C(), g, r.inputs[3]->data, h, dh, rows, f, o));
+                int ax, aw1, ab1 = 0;
+                float *dx = e.dest(r, 0, &ax);
+                float *dw1 = e.dest(r, 1, &aw1);
+                float *db1 = r.inputs[2] ? e.dest(r, 2, &ab1) : nullptr;
+                OMT(om_linear_bwd(C(), dh, r.inputs[0]->data, r.inputs[1]->data, dx, dw1, db1, rows, d, f, ax, aw1,
+                                  ab1));
+            }
+            if (r.needs(5)) e.emit_alias(r, 5, g);
+        });
+    }
+    return y;
 }
 
 Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const Tensor &wk, const Tensor &bk,
@@ -367,17 +430,15 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
     float *qkv = dev().step_floats((int64_t)rows * 3 * W);
     OMT(om_linear_fwd(C(), x->data, wq->data, bq->data, qkv, rows, w, 3 * w));
     Tensor o = make(x->shape);
-    float *p = dev().step_floats((int64_t)B * heads * L * L);
     const float *md = mask ? mask->data : nullptr;
-    OMT(om_attention_fwd_ld(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, o->data, w, p, B, heads, L, L, D, 0.0f));
+    OMT(om_attention_fwd_fused(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, o->data, w, B, heads, L, D, 0.0f));
     if (tracked({&x, &wq, &bq, &wk, &bk, &wv, &bv}))
         attach(o, "AttentionQKV", {x, wq, bq, wk, bk, wv, bv},
-               [qkv, p, B, L, heads, D, w, rows, WW](Engine &e, Record &r, const float *g) {
+               [qkv, md, B, L, heads, D, w, rows, WW](Engine &e, Record &r, const float *g) {
                    const int64_t W = w;
                    float *dqkv = dev().step_floats((int64_t)rows * 3 * W);
-                   float *ds = dev().step_floats((int64_t)B * heads * L * L);
-                   OMT(om_attention_bwd_ld(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, p, g, w, dqkv, dqkv + W,
-                                           dqkv + 2 * W, 3 * w, ds, B, heads, L, L, D, 0.0f, 0));
+                   OMT(om_attention_bwd_fused(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, g, w, dqkv, dqkv + W,
+                                              dqkv + 2 * W, 3 * w, B, heads, L, D, 0.0f, 0));
                    int ax, a[6];
                    float *dx = e.dest(r, 0, &ax);
                    float *d[6];

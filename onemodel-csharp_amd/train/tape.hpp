@@ -105,6 +105,13 @@ void settle_grads(const std::vector<Tensor> &leaves);
 // ------------------------------------------------------------------------------------------------ ops
 // Each records a backward record when an input requires a gradient (the reference's Ops.*).
 Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b);
+// resid + Linear(x) (Ops.Layers.cs:715-733 then Ops.Add): one launch forward, the residual's gradient is g itself.
+Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const Tensor &resid);
+// The feed-forward sub-block resid + Linear2(GELU(Linear1(x))) as one record (resid may be empty): forward is two
+// launches (Linear1 with GELU in its epilogue, Linear2 with the residual in its epilogue); backward is Linear2's dW
+// (with its bias gradient), the input gradient through GELU in one launch, then Linear1's backward.
+Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
+           const Tensor &resid);
 Tensor relu(const Tensor &x);
 Tensor gelu(const Tensor &x);
 Tensor add(const Tensor &a, const Tensor &b);
@@ -196,6 +203,8 @@ class MultiHeadAttention : public Module {
    public:
     MultiHeadAttention(int width, int heads, Generator &g);
     Tensor operator()(const Tensor &x, const Tensor &mask) const;
+    // resid + MultiHeadAttention(x): the residual Add fused into the output projection.
+    Tensor residual(const Tensor &x, const Tensor &mask, const Tensor &resid) const;
     Linear *q, *k, *v, *o;
     int heads;
 };

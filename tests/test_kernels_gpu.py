@@ -102,7 +102,8 @@ def test_gemm_rejects_bad_shapes(dev):
 
 
 # ------------------------------------------------------------------------------------------------ Linear
-@pytest.mark.parametrize("rows,inf,outf", [(64, 784, 256), (64, 256, 10), (4096, 384, 1536), (300, 37, 9)])
+@pytest.mark.parametrize("rows,inf,outf", [(64, 784, 256), (64, 256, 10), (4096, 384, 1536), (300, 37, 9),
+                                           (512, 256, 128), (4096, 1536, 384), (4096, 384, 1152)])
 def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     rng = np.random.default_rng(rows + inf + outf)
     x, w, b, g = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf), rnd(rng, rows, outf)
@@ -122,6 +123,46 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 1, 1, 1)
     assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
     assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
+
+
+@pytest.mark.parametrize("rows,inf,outf", [(4096, 384, 1536), (4096, 1536, 384), (256, 64, 192), (100, 36, 20)])
+def test_linear_fused_epilogues(dev, T, rows, inf, outf):
+    """om_linear_fwd_resid (Linear then the residual Add), om_linear_gelu_fwd (Linear then GELU, keeping the
+    pre-activation) and om_linear_bwd_dx_gelu (GELU's backward of g w): the GEMM part to the GEMM tolerance, the
+    fused element-wise steps bit for bit on the device's own GEMM results."""
+    rng = np.random.default_rng(rows + 3 * inf + outf)
+    x, w, b = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf)
+    resid, g = rnd(rng, rows, outf), rnd(rng, rows, outf)
+    lin = np.empty((rows, outf), np.float32)
+    T.lib().or_linear_fwd(T.fp(x), T.fp(w), T.fp(b), T.fp(lin), rows, inf, outf)
+    X, W, Bb, R = dev.put(x), dev.put(w), dev.put(b), dev.put(resid)
+    Y, H, A = dev.empty((rows, outf)), dev.empty((rows, outf)), dev.empty((rows, outf))
+    dev.call("om_linear_fwd_resid", X, W, Bb, R, Y, rows, inf, outf)
+    assert scaled(dev.get(Y), resid + lin) <= TOL
+    dev.call("om_linear_fwd", X, W, Bb, H, rows, inf, outf)
+    plain = dev.get(H)
+    assert np.array_equal(dev.get(Y), (resid + plain).astype(np.float32))  # Linear, then one rounded Add
+    dev.call("om_linear_gelu_fwd", X, W, Bb, H, A, rows, inf, outf)
+    h = dev.get(H)
+    assert scaled(h, lin) <= TOL
+    a_ref = np.empty_like(h)
+    T.lib().or_gelu_fwd(T.fp(h), T.fp(a_ref), C.c_int64(h.size))
+    assert np.array_equal(dev.get(A).view(np.uint32), a_ref.view(np.uint32))
+    # dh = GELU'(h) * (g w): g [rows, outf] against w [outf, inf] is the backward of a Linear(inf -> outf) whose
+    # input went through GELU; here h plays that input, so use a pre-activation of shape [rows, inf].
+    hin = rnd(rng, rows, inf, scale=2.0)
+    da = np.empty((rows, inf), np.float32)
+    T.lib().or_gemm(0, 0, rows, inf, outf, T.fp(g), outf, T.fp(w), inf, T.fp(da), inf, 0)
+    dh_ref = np.empty_like(da)
+    T.lib().or_gelu_bwd(T.fp(da), T.fp(hin), T.fp(dh_ref), C.c_int64(da.size))
+    G, HI, DH, DA = dev.put(g), dev.put(hin), dev.empty((rows, inf)), dev.empty((rows, inf))
+    dev.call("om_linear_bwd_dx_gelu", G, W, HI, DH, rows, inf, outf)
+    assert scaled(dev.get(DH), dh_ref) <= TOL
+    dev.call("om_linear_bwd", G, X, W, DA, None, None, rows, inf, outf, 0, 0, 0)
+    da_dev = dev.get(DA)
+    dh_exact = np.empty_like(da_dev)
+    T.lib().or_gelu_bwd(T.fp(da_dev), T.fp(hin), T.fp(dh_exact), C.c_int64(da_dev.size))
+    assert np.array_equal(dev.get(DH).view(np.uint32), dh_exact.view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------------ element-wise
@@ -311,6 +352,56 @@ def test_attention_packed_qkv_strides(dev, T, B, H, L, D):
     d = dev.get(DQKV)
     for i, ref in enumerate((dq, dk, dv)):
         assert scaled(heads(d[:, :, i * W:(i + 1) * W]), ref) <= TOL
+
+
+@pytest.mark.parametrize("B,H,L,D,masked,packed", [(4, 12, 128, 32, True, True), (3, 2, 64, 32, True, False),
+                                                     (2, 3, 128, 32, False, False), (2, 3, 40, 32, True, False),
+                                                     (1, 2, 128, 64, True, True)])
+def test_attention_fused_recompute(dev, T, B, H, L, D, masked, packed):
+    """om_attention_{fwd,bwd}_fused (no saved weights; the backward recomputes P): the fused kernels for D = 32 and
+    L in {64, 128}, the GEMM fallback otherwise; against the oracle, and accumulating into existing gradients."""
+    rng = np.random.default_rng(B * L + D + H)
+    W = H * D
+    ld = 3 * W if packed else W
+    qkv = rnd(rng, B, L, 3 * W)
+    g = rnd(rng, B, L, W)
+    mask = None
+    if masked:
+        lens = rng.integers(L // 2, L + 1, B)
+        mask = np.zeros((B, L, L), np.float32)
+        for b in range(B):
+            mask[b, :, lens[b]:] = -np.inf
+    heads = lambda a: np.ascontiguousarray(a.reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    parts = [qkv[:, :, i * W:(i + 1) * W] for i in range(3)]
+    tq, tk, tv = (heads(a) for a in parts)
+    tg = heads(g)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref = np.empty_like(tq)
+    mp = T.fp(mask) if masked else None
+    T.lib().or_attention_fwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(o_ref), B, H, L, L, D, C.c_float(scale))
+    dq, dk, dv = np.empty_like(tq), np.empty_like(tk), np.empty_like(tv)
+    T.lib().or_attention_bwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(tg), T.fp(dq), T.fp(dk), T.fp(dv), B, H, L, L,
+                             D, C.c_float(scale))
+    if packed:
+        QKV = dev.put(qkv)
+        qp = [QKV.data_ptr() + 4 * i * W for i in range(3)]
+        DQKV = dev.empty((B, L, 3 * W), fill=0.5)
+        dp = [DQKV.data_ptr() + 4 * i * W for i in range(3)]
+        got = lambda: [dev.get(DQKV)[:, :, i * W:(i + 1) * W] for i in range(3)]
+    else:
+        QS = [dev.put(np.ascontiguousarray(a)) for a in parts]
+        qp = [t.data_ptr() for t in QS]
+        DS = [dev.empty((B, L, W), fill=0.5) for _ in range(3)]
+        dp = [t.data_ptr() for t in DS]
+        got = lambda: [dev.get(t) for t in DS]
+    G, M = dev.put(g), (dev.put(mask) if masked else None)
+    O = dev.empty((B, L, W))
+    dev.call("om_attention_fwd_fused", qp[0], qp[1], qp[2], ld, M, 1, O, W, B, H, L, D, C.c_float(scale))
+    assert scaled(heads(dev.get(O)), o_ref) <= TOL
+    dev.call("om_attention_bwd_fused", qp[0], qp[1], qp[2], ld, M, 1, G, W, dp[0], dp[1], dp[2], ld, B, H, L, D,
+             C.c_float(scale), 1)
+    for gd, ref in zip(got(), (dq, dk, dv)):
+        assert scaled(heads(gd) - np.float32(0.5), ref) <= TOL
 
 
 # ------------------------------------------------------------------------------------------------ conv and pool
