@@ -141,6 +141,102 @@ struct ColSum {
     }
 };
 
+// Epilogue of a wavefront's TM x TN MFMA blocks: output register r of block (i, j) on this lane is row rho = 4*kl + r
+// and column l16 of the block, mapped back through the interleaving of R-layout operands. Every operand the epilogue
+// reads (bias, residual, GELU input, mask, the old C) is gathered into registers first, in runs of independent loads,
+// and the arithmetic follows in the reference's order: alpha, mask, bias, residual, GELU, then accumulate.
+template <int TM, int TN, bool AK, bool BKL, bool GELU>
+__device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&acc)[TM][TN], float *C,
+                                              const float *mask, int m0, int n0, int wm0, int wn0, int l16, int kl,
+                                              int split) {
+    int colv[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) colv[j] = n0 + wn0 + (BKL ? j * 16 + l16 : TN * l16 + j);
+    float bcol[TN];
+    if (p.splits == 1 && p.bias && !p.bias_per_row) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) bcol[j] = p.bias[colv[j]];
+    }
+    // One MFMA row block (i) at a time keeps the gathered operands to 4 x TN registers each.
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        int rowv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) rowv[r] = m0 + wm0 + (AK ? i * 16 + 4 * kl + r : TM * (4 * kl + r) + i);
+        if (p.splits > 1) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) p.ws[((int64_t)split * p.m + rowv[r]) * p.n + colv[j]] = acc[i][j][r];
+            continue;
+        }
+        float v[4][TN], t[4][TN];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) v[r][j] = acc[i][j][r];
+        auto gather = [&](const float *base, int64_t ld) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) t[r][j] = base[(int64_t)rowv[r] * ld + colv[j]];
+        };
+        if (p.alpha != 1.0f) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = v[r][j] * p.alpha;
+        }
+        if (mask) {
+            gather(mask, p.n);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = v[r][j] + t[r][j];
+        }
+        if (p.bias) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float br = p.bias_per_row ? p.bias[rowv[r]] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = v[r][j] + (p.bias_per_row ? br : bcol[j]);
+            }
+        }
+        if (p.resid) {
+            gather(p.resid, p.ldr);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = v[r][j] + t[r][j];
+        }
+        if constexpr (GELU) {
+            if (p.epi == EPI_GELU) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) p.out2[(int64_t)rowv[r] * p.ld2 + colv[j]] = omd::gelu(v[r][j]);
+            } else if (p.epi == EPI_GELU_GRAD) {
+                gather(p.aux, p.ldaux);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) v[r][j] = omd::gelu_grad(v[r][j], t[r][j]);
+            }
+        }
+        if (p.accumulate) {
+            gather(C, p.ldc);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = t[r][j] + v[r][j];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) C[(int64_t)rowv[r] * p.ldc + colv[j]] = v[r][j];
+    }
+}
+
 template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
 __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     constexpr bool AK = !TA, BKL = TB;  // operands in K layout
@@ -258,26 +354,9 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
             cs.finish(p, reinterpret_cast<double *>(As), m0, split);
         }
 
-    // Epilogue: output register r of MFMA block (i, j) on this lane is row rho = 4*kl + r, column l16 of the block.
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rho = 4 * kl + r;
-            const int row = m0 + wm0 + (AK ? i * 16 + rho : TM * rho + i);
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int col = n0 + wn0 + (BKL ? j * 16 + l16 : TN * l16 + j);
-                float v = acc[i][j][r];
-                if (p.splits > 1) {
-                    p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
-                    continue;
-                }
-                epilogue<GELU>(p, C, p.ldc, mask, row, col, v);
-            }
-        }
+    tile_epilogue<TM, TN, AK, BKL, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
 }
 
 // The same tile with eight wavefronts: two groups of four (2 x 2 over the tile, as above) split each chunk's 16-k
@@ -405,23 +484,7 @@ __global__ void __launch_bounds__(2 * NT) k_gemm_x2(Params p) {
 
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rho = 4 * kl + r;
-            const int row = m0 + wm0 + (AK ? i * 16 + rho : TM * rho + i);
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int col = n0 + wn0 + (BKL ? j * 16 + l16 : TN * l16 + j);
-                float v = acc[i][j][r];
-                if (p.splits > 1) {
-                    p.ws[((int64_t)split * p.m + row) * p.n + col] = v;
-                    continue;
-                }
-                epilogue<GELU>(p, C, p.ldc, mask, row, col, v);
-            }
-        }
+    tile_epilogue<TM, TN, AK, BKL, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
 }
 
 }  // namespace gx
