@@ -45,6 +45,14 @@ const char *om_last_error(om_ctx *ctx);
 void *om_ctx_stream(om_ctx *ctx);
 /* Version of this ABI (major * 100 + minor). */
 int om_abi_version(void);
+/* Overlap mode (off by default). When on, om_linear_bwd enqueues its weight and bias gradients on a second stream
+ * (default priority) that starts after everything already queued on the context's stream, so they run beside the
+ * rest of the backward; their results are complete for the context's stream after om_ctx_join, which om_ctx_sync,
+ * om_step_reset, om_upload, om_download, om_copy, om_zero, om_fill, om_adam_step and om_sgd_step perform first.
+ * Inputs g and x of such a call must not be overwritten before that join. No counterpart in the reference, whose
+ * CPU backward is sequential (Engine.cs:124-207); results do not depend on the mode. */
+om_status om_ctx_set_overlap(om_ctx *ctx, int enable);
+om_status om_ctx_join(om_ctx *ctx);
 
 /* ---------------------------------------------------------------------------------------------- arena */
 /* Device memory in two regions, in the spirit of the reference's buffer lifetimes (ActivationScope.cs:18-106,

@@ -31,6 +31,8 @@ _OM_SIGS = {
     "om_last_error": [vp],
     "om_ctx_stream": [vp],
     "om_abi_version": [],
+    "om_ctx_set_overlap": [vp, ci],
+    "om_ctx_join": [vp],
     "om_arena_reserve": [vp, u64, u64],
     "om_alloc": [vp, ci, u64, C.POINTER(vp)],
     "om_step_reset": [vp],

@@ -169,7 +169,7 @@ om_status om::chunk_final(om_ctx *ctx, const double *part, int chunks, int cols,
                           const double *part2, float *out2) {
     int waves = part2 ? 2 * cols : cols;
     hipLaunchKernelGGL(om_k_chunk_final, dim3(om::grid1d((int64_t)waves * 64, 256, 1 << 30)), dim3(256), 0,
-                       ctx->stream, part, out, part2, out2, chunks, cols, acc);
+                       om::cur_stream(ctx), part, out, part2, out2, chunks, cols, acc);
     return OM_LAUNCH_CHECK(ctx, "column reduction");
 }
 
@@ -373,7 +373,7 @@ om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, 
     if (s) return s;
     double *part = reinterpret_cast<double *>(scr);
     dim3 g1((cols + 63) / 64, chunks);
-    hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, ctx->stream, g, rows, cols, part);
+    hipLaunchKernelGGL(k_colsum_partial, g1, dim3(kBlock), 0, om::cur_stream(ctx), g, rows, cols, part);
     s = OM_LAUNCH_CHECK(ctx, "om_colsum");
     if (s) return s;
     return om::chunk_final(ctx, part, chunks, cols, db, accumulate);

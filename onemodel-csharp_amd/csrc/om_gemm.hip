@@ -328,7 +328,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
         p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
     }
     if (colsum_fused) *colsum_fused = cs;
-    hipStream_t st = ctx->stream;
+    hipStream_t st = om::cur_stream(ctx);
     bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st);
     if (launched) {
     } else if (fast) {
@@ -347,7 +347,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     }
     om_status s = OM_LAUNCH_CHECK(ctx, what);
     if (s || p.splits <= 1) return s;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, ctx->stream,
+    hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, st,
                        p);
     return OM_LAUNCH_CHECK(ctx, what);
 }
@@ -424,6 +424,13 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd dx");
         if (s) return s;
     }
+    // In overlap mode the weight and bias gradients go to the second stream: nothing downstream in the backward
+    // reads them, so they run beside the input-gradient chain until a join.
+    const bool aux = ctx->overlap && (dw || db);
+    if (aux) {
+        s = om::fork(ctx);
+        if (s) return s;
+    }
     bool db_done = false;
     if (dw) {
         omg::Params p = omg::dense_params(out, in, rows, g, out, x, in, dw, in);
@@ -431,9 +438,9 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         p.db = db;  // the bias gradient rides along with dW when the kernel can sum g's columns
         p.db_acc = acc_db;
         s = omg::launch_dense(ctx, p, true, false, 1, "om_linear_bwd dw", &db_done);
-        if (s) return s;
     }
-    if (db && !db_done) s = om_colsum(ctx, g, db, rows, out, acc_db);
+    if (!s && db && !db_done) s = om_colsum(ctx, g, db, rows, out, acc_db);
+    if (aux) om::unfork(ctx);
     return s;
 }
 

@@ -36,6 +36,16 @@ struct om_ctx {
     // Second slot for callers that launch GEMMs while holding their own scratch (attention's score recompute).
     float *scratch2 = nullptr;
     uint64_t scratch2_bytes = 0;
+    // Overlap mode (om_ctx_set_overlap): weight-gradient launches go to a second default-priority stream that forks
+    // from the main stream and is joined back before anything reads gradients. `active` routes the GEMM engine's
+    // launches (and its scratch slot) to that stream while a weight gradient is being enqueued.
+    bool overlap = false;
+    hipStream_t stream2 = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    bool aux_pending = false;
+    int active = 0;
+    float *scratch_aux = nullptr;
+    uint64_t scratch_aux_bytes = 0;
     int num_cus = 256;
 };
 
@@ -48,6 +58,14 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
 // The same for the second slot (never used by the GEMM engine itself).
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
+// The stream the GEMM engine launches on right now (the weight-gradient stream while ctx->active).
+inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->active ? ctx->stream2 : ctx->stream; }
+// Overlap mode: fork = the weight-gradient stream waits for everything queued so far on the main stream, and
+// becomes the active stream; unfork = back to the main stream; join = the main stream waits for the weight-gradient
+// stream (a no-op when nothing was queued there since the last join).
+om_status fork(om_ctx *ctx);
+void unfork(om_ctx *ctx);
+om_status join(om_ctx *ctx);
 // out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column; a second
 // (part2, out2) pair of the same shape is reduced in the same launch when given.
 om_status chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,

@@ -43,19 +43,20 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd(const float *__restrict__ x, 
 // The same computation with the block's 16 rows staged through LDS: global traffic is float4-coalesced and the
 // 16-lane strided Sum16 walks run on LDS (row stride cols+16 keeps the four rows of a wavefront on distinct banks);
 // y goes back out through LDS as well. Requires cols % 4 == 0 and cols <= kLnLdsMaxCols.
-constexpr int kLnRows = kBlock / 16;
 constexpr int kLnLdsMaxCols = 960;  // keeps dynamic LDS under 64 KB
-__global__ void __launch_bounds__(kBlock) k_ln_fwd_lds(const float *__restrict__ x, const float *__restrict__ gamma,
-                                                       const float *__restrict__ beta, float *__restrict__ y,
-                                                       float *__restrict__ mean_out, float *__restrict__ rstd_out,
-                                                       int rows, int cols, float eps) {
-    extern __shared__ float sh[];  // [kLnRows][cols + 16]
+template <int NTH>
+__global__ void __launch_bounds__(NTH) k_ln_fwd_lds(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                    const float *__restrict__ beta, float *__restrict__ y,
+                                                    float *__restrict__ mean_out, float *__restrict__ rstd_out,
+                                                    int rows, int cols, float eps) {
+    constexpr int NR = NTH / 16;  // rows per block, a 16-lane group each
+    extern __shared__ float sh[];  // [NR][cols + 16]
     const int ld = cols + 16, c4 = cols >> 2;
-    const int r0 = blockIdx.x * kLnRows;
-    const int nr = min(kLnRows, rows - r0);
+    const int r0 = blockIdx.x * NR;
+    const int nr = min(NR, rows - r0);
     const int n4 = nr * c4;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + (int64_t)r0 * cols);
-    for (int i = threadIdx.x; i < n4; i += kBlock) {
+    for (int i = threadIdx.x; i < n4; i += NTH) {
         int r = i / c4, q = i - r * c4;
         *reinterpret_cast<float4 *>(sh + r * ld + 4 * q) = x4[i];
     }
@@ -82,7 +83,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd_lds(const float *__restrict__
     }
     __syncthreads();
     float4 *y4 = reinterpret_cast<float4 *>(y + (int64_t)r0 * cols);
-    for (int i = threadIdx.x; i < n4; i += kBlock) {
+    for (int i = threadIdx.x; i < n4; i += NTH) {
         int r = i / c4, q = i - r * c4;
         y4[i] = *reinterpret_cast<const float4 *>(sh + r * ld + 4 * q);
     }
@@ -92,39 +93,50 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd_lds(const float *__restrict__
 // dx is written per row; the dgamma/dbeta column contributions are kept per lane in double and summed over the
 // block's waves in LDS (fixed order), giving partial[chunk][col] for the second pass.
 constexpr int kMaxPer = 16;
+// PER = column slots per lane (cols <= 64 * PER); the row walk is fully unrolled when cols == 64 * PER.
+template <int PER>
 __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, const float *__restrict__ x,
                                                    const float *__restrict__ gamma, const float *__restrict__ mean,
                                                    const float *__restrict__ rstd, float *__restrict__ dx,
                                                    double *__restrict__ part_g, double *__restrict__ part_b, int rows,
                                                    int cols, int rows_per_chunk, int acc_dx) {
-    __shared__ double lds[kBlock / 64][64 * kMaxPer];
+    __shared__ double lds[kBlock / 64][64 * PER];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
-    const int per = (cols + 63) >> 6;
-    double pg[kMaxPer], pb[kMaxPer];
+    const bool full = cols == 64 * PER;
+    double pg[PER], pb[PER];
+    float gam[PER];
 #pragma unroll
-    for (int i = 0; i < kMaxPer; i++) pg[i] = pb[i] = 0.0;
+    for (int i = 0; i < PER; i++) {
+        pg[i] = pb[i] = 0.0;
+        int j = lane + 64 * i;
+        gam[i] = (full || j < cols) ? gamma[j] : 0.0f;
+    }
     for (int r = r0 + w; r < r1; r += kBlock / 64) {
         const float *xr = x + (int64_t)r * cols;
         const float *gr = g + (int64_t)r * cols;
         float m = mean[r], s = rstd[r];
         double sum1 = 0.0, sum2 = 0.0;
-        float xh[kMaxPer], gv[kMaxPer];
+        float xh[PER], gv[PER];
 #pragma unroll
-        for (int i = 0; i < kMaxPer; i++) {
+        for (int i = 0; i < PER; i++) {
             int j = lane + 64 * i;
-            xh[i] = 0.0f;
-            gv[i] = 0.0f;
-            if (i < per && j < cols) {
-                float xhat = (xr[j] - m) * s;
-                float gg = gr[j];
-                float dxhat = gg * gamma[j];
+            const bool in = full || j < cols;
+            xh[i] = in ? xr[j] : 0.0f;
+            gv[i] = in ? gr[j] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            int j = lane + 64 * i;
+            if (full || j < cols) {
+                float xhat = (xh[i] - m) * s;
+                float gg = gv[i];
+                float dxhat = gg * gam[i];
                 sum1 += (double)dxhat;
                 sum2 += (double)(dxhat * xhat);
                 pg[i] += (double)(gg * xhat);
                 pb[i] += (double)gg;
                 xh[i] = xhat;
-                gv[i] = gg;
             }
         }
         sum1 = omd::wave_sum(sum1);
@@ -133,10 +145,10 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
             float m1 = (float)(sum1 / cols), m2 = (float)(sum2 / cols);
             float *dr = dx + (int64_t)r * cols;
 #pragma unroll
-            for (int i = 0; i < kMaxPer; i++) {
+            for (int i = 0; i < PER; i++) {
                 int j = lane + 64 * i;
-                if (i < per && j < cols) {
-                    float v = s * (((gv[i] * gamma[j]) - m1) - (xh[i] * m2));
+                if (full || j < cols) {
+                    float v = s * (((gv[i] * gam[i]) - m1) - (xh[i] * m2));
                     dr[j] = acc_dx ? dr[j] + v : v;
                 }
             }
@@ -148,8 +160,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
         if (!part) continue;
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kMaxPer; i++)
-            if (i < per) lds[w][lane + 64 * i] = pass == 0 ? pg[i] : pb[i];
+        for (int i = 0; i < PER; i++) lds[w][lane + 64 * i] = pass == 0 ? pg[i] : pb[i];
         __syncthreads();
         for (int j = threadIdx.x; j < cols; j += kBlock) {
             double t = 0.0;
@@ -363,9 +374,10 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
     if (rows == 0) return OM_OK;
     const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
     if (cols % 4 == 0 && cols <= kLnLdsMaxCols && aligned) {
-        const size_t lds = (size_t)kLnRows * (cols + 16) * sizeof(float);
-        hipLaunchKernelGGL(k_ln_fwd_lds, dim3((rows + kLnRows - 1) / kLnRows), dim3(kBlock), lds, ctx->stream, x,
-                           gamma, beta, y, mean, rstd, rows, cols, eps);
+        // Four rows per 64-thread block: many small blocks keep several in flight per CU.
+        const size_t lds = (size_t)4 * (cols + 16) * sizeof(float);
+        hipLaunchKernelGGL(k_ln_fwd_lds<64>, dim3((rows + 3) / 4), dim3(64), lds, ctx->stream, x, gamma, beta, y,
+                           mean, rstd, rows, cols, eps);
     } else {
         hipLaunchKernelGGL(k_ln_fwd, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma, beta, y,
                            mean, rstd, rows, cols, eps);
@@ -390,8 +402,17 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
         pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
     }
     if (cols <= 64 * kMaxPer) {
-        hipLaunchKernelGGL(k_ln_bwd, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, pg, pb,
-                           rows, cols, rpc, acc_dx);
+        const int per = (cols + 63) / 64;
+#define OM_LNB(P)                                                                                                   \
+    hipLaunchKernelGGL(k_ln_bwd<P>, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, pg, pb, \
+                       rows, cols, rpc, acc_dx)
+        if (per <= 2) OM_LNB(2);
+        else if (per <= 4) OM_LNB(4);
+        else if (per <= 6) OM_LNB(6);
+        else if (per <= 8) OM_LNB(8);
+        else if (per <= 12) OM_LNB(12);
+        else OM_LNB(16);
+#undef OM_LNB
     } else {
         if (dx)
             hipLaunchKernelGGL(k_ln_bwd_dx_wide, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g, x, gamma,

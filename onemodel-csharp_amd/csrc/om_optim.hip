@@ -99,6 +99,7 @@ om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v
                        float beta1, float beta2, float eps, float weight_decay, int decoupled, float step_size,
                        float sqrt_bc2) {
     OM_CHECK_CTX(ctx);
+    if (om::join(ctx)) return OM_E_DEVICE;  // the gradients may still be in flight on the weight-gradient stream
     OM_REQUIRE(ctx, n >= 0, "om_adam_step: negative length");
     if (n == 0) return OM_OK;
     OM_REQUIRE(ctx, p && g && m && v, "om_adam_step: NULL pointer");
@@ -125,6 +126,7 @@ om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v
 om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t n, float lr, float momentum,
                       float dampening, float weight_decay, int nesterov, int first) {
     OM_CHECK_CTX(ctx);
+    if (om::join(ctx)) return OM_E_DEVICE;  // the gradients may still be in flight on the weight-gradient stream
     OM_REQUIRE(ctx, n >= 0, "om_sgd_step: negative length");
     if (n == 0) return OM_OK;
     OM_REQUIRE(ctx, p && g, "om_sgd_step: NULL pointer");

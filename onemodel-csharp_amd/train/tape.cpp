@@ -1,6 +1,8 @@
 // The tape: device and step allocator, the reverse-mode engine, and the recording ops.
 #include "tape.hpp"
 
+#include <cstdlib>
+
 #include <cmath>
 #include <cstring>
 
@@ -25,6 +27,12 @@ Device::Device(int device) {
     om_status s = om_ctx_create(device, &ctx_);
     if (s != OM_OK) throw Error(s, std::string("om_ctx_create: ") + om_last_error(nullptr));
     check(ctx_, om_arena_reserve(ctx_, 0, 1ull << 30), "om_arena_reserve");
+    // OMT_OVERLAP=1 puts weight gradients on a second stream beside the input-gradient chain (joined by the
+    // optimizer, downloads and the step reset). Off by default: measured on MI355X at the C3 shapes, the two
+    // streams' GEMMs split the CUs between them and the input-gradient chain (the critical path) finishes later.
+    const char *ov = std::getenv("OMT_OVERLAP");
+    overlap_ = ov && ov[0] == '1';
+    check(ctx_, om_ctx_set_overlap(ctx_, overlap_ ? 1 : 0), "om_ctx_set_overlap");
 }
 Device::~Device() {
     if (ctx_) om_ctx_destroy(ctx_);
@@ -93,13 +101,20 @@ float *Engine::dest(Record &r, int i, int *acc) {
     if (!p.pending) {
         p.pending = dev().step_floats(x.numel);
         p.pending_borrowed = false;
+        holders_[p.pending] = 1;
         return p.pending;
     }
-    if (p.pending_borrowed) {  // copy-on-write: the buffer belongs to another record's gradient
-        float *nb = dev().step_floats(x.numel);
-        OMT(om_copy(C(), nb, p.pending, sizeof(float) * (uint64_t)x.numel));
-        p.pending = nb;
-        p.pending_borrowed = false;
+    if (p.pending_borrowed) {
+        if (sole_holder(p.pending)) {  // the lender is done with it: take it over
+            p.pending_borrowed = false;
+        } else {  // copy-on-write: the buffer is still another record's gradient
+            float *nb = dev().step_floats(x.numel);
+            OMT(om_copy(C(), nb, p.pending, sizeof(float) * (uint64_t)x.numel));
+            holders_[p.pending]--;
+            p.pending = nb;
+            holders_[nb] = 1;
+            p.pending_borrowed = false;
+        }
     }
     *acc = 1;  // Engine.AddInto (Engine.cs:331-344)
     return p.pending;
@@ -120,15 +135,19 @@ void Engine::emit_alias(Record &r, int i, const float *g) {
     if (!p.pending) {
         p.pending = const_cast<float *>(g);
         p.pending_borrowed = true;
+        holders_[g]++;
         return;
     }
-    if (p.pending_borrowed) {
+    if (p.pending_borrowed && !sole_holder(p.pending)) {
         float *nb = dev().step_floats(x.numel);
         OMT(om_add(C(), p.pending, g, nb, x.numel));
+        holders_[p.pending]--;
         p.pending = nb;
+        holders_[nb] = 1;
         p.pending_borrowed = false;
         return;
     }
+    p.pending_borrowed = false;
     OMT(om_axpy(C(), 1.0f, g, p.pending, x.numel));
 }
 
@@ -162,8 +181,10 @@ void Engine::run(const Tensor &root) {
             stack.pop_back();
         }
     }
+    holders_.clear();
     root->grad_fn->pending = g;
     root->grad_fn->pending_borrowed = false;
+    holders_[g] = 1;
     for (size_t i = order.size(); i-- > 0;) {
         Record *r = order[i];
         float *gi = r->pending;
@@ -171,7 +192,9 @@ void Engine::run(const Tensor &root) {
         if (!gi) continue;
         if (!r->rule) throw Error(OM_E_STATE, std::string("backward ran through a released ") + r->op + " record");
         r->rule(*this, *r, gi);
+        holders_[gi]--;  // this record is done with its gradient
     }
+    holders_.clear();
     // Release the records (BackwardRecord.Release): a second backward through this graph is an error.
     for (Record *r : order) {
         r->rule = nullptr;

@@ -11,6 +11,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "om.h"
@@ -73,9 +74,11 @@ class Device {
     void *persistent(uint64_t bytes);
     void step_reset();
     void sync();
+    bool overlap() const { return overlap_; }
 
    private:
     om_ctx *ctx_ = nullptr;
+    bool overlap_ = false;
 };
 
 Device &dev();            // the device of the current thread's model (set by Model)
@@ -95,6 +98,19 @@ class Engine {
     // be added to an existing gradient.
     void emit_alias(Record &r, int i, const float *g);
     void run(const Tensor &root);
+
+   private:
+    // How many records hold each gradient buffer as their pending gradient during a backward pass (the record
+    // running counts as a holder of its own gradient until its rule returns). A borrowed buffer whose only holder
+    // is the record about to write into it is written in place instead of being copied first.
+    std::unordered_map<const float *, int> holders_;
+    // In overlap mode a gradient buffer may still be read by a weight-gradient launch on the second stream, so
+    // it is never written in place once borrowed.
+    bool sole_holder(const float *b) const {
+        if (dev().overlap()) return false;
+        auto it = holders_.find(b);
+        return it != holders_.end() && it->second == 1;
+    }
 };
 
 void backward(const Tensor &root);  // Tensor.Backward() of a one-element tensor
