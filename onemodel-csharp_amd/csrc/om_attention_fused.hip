@@ -148,38 +148,111 @@ __device__ __forceinline__ void store_rows(float *dst, int64_t ld, int row0, con
     }
 }
 
+// Forward in the transposed form: S^T = K Q^T, so the MFMA result puts keys on (lane group kl, register r) and a
+// wavefront's 16 queries on the lane index t. Then
+//   - the row softmax of query t runs over this lane's 4 x L/16 values and the four lane groups; Sum16's partial
+//     p[key % 16] is this lane's register-r sum over the key blocks (key % 16 = 4 kl + r), so the halving combine
+//     p[i] + p[i+8], +4, +2, +1 is two cross-group shuffles (lanes +32, +16) and two in-register adds;
+//   - P^T in registers is exactly the B operand of O^T = V^T P^T (no LDS round trip), with V^T staged in LDS;
+//   - the mask of query t over keys 4 kl + r is four consecutive floats (one 16-byte load per key block).
+// One workgroup per batch item, head and 64 queries (four wavefronts of 16 queries).
 template <int D, int L>
 __global__ void __launch_bounds__(256) k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                   int64_t mask_bstride, float *__restrict__ o, int ldo, float scale) {
-    constexpr int LDX = D + 4, LDP = L + 4;
-    __shared__ __attribute__((aligned(16))) float Qs[64 * LDX];
-    __shared__ __attribute__((aligned(16))) float Ks[L * LDX];
-    __shared__ __attribute__((aligned(16))) float Vs[L * LDX];
-    __shared__ __attribute__((aligned(16))) float Ps[64 * LDP];
+    constexpr int LDK = D + 4, LDV = L + 4, NB = L / 16, DB = D / 16;
+    __shared__ __attribute__((aligned(16))) float Ks[L * LDK];  // [key][d]
+    __shared__ __attribute__((aligned(16))) float Vt[D * LDV];  // [d][key]
     const int qb = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int64_t row0 = (int64_t)b * L;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
-    const int q0 = 16 * w;  // this wavefront's first query within the block
-    float mv[4][L / 16];
-    load_mask<L>(mv, mask ? mask + b * mask_bstride + (int64_t)(qb * 64 + q0 + 4 * kl) * L : nullptr, t);
-    stage<D, 256>(Qs, q + (row0 + qb * 64) * ld + h * D, ld, 64);
+    const int qrow = qb * 64 + 16 * w + t;  // this lane's query
+    // Early loads: this lane's query fragment (B operand of S^T) and mask values.
+    floatx4 qf[DB];
+    const float *qg = q + (row0 + qrow) * ld + h * D;
+#pragma unroll
+    for (int blk = 0; blk < DB; blk++) qf[blk] = *reinterpret_cast<const floatx4 *>(qg + 16 * blk + 4 * kl);
+    floatx4 mv[NB];
+    if (mask) {
+        const float *mr = mask + b * mask_bstride + (int64_t)qrow * L + 4 * kl;
+#pragma unroll
+        for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
+    }
     stage<D, 256>(Ks, k + row0 * ld + h * D, ld, L);
-    stage<D, 256>(Vs, v + row0 * ld + h * D, ld, L);
+    {  // V^T: thread f takes key f % L and four d from f / L, so each store row is contiguous across the lanes
+        const float *vg = v + row0 * ld + h * D;
+        for (int f = threadIdx.x; f < L * (D / 4); f += 256) {
+            const int key = f % L, c = (f / L) * 4;
+            const floatx4 x = *reinterpret_cast<const floatx4 *>(vg + (int64_t)key * ld + c);
+#pragma unroll
+            for (int i = 0; i < 4; i++) Vt[(c + i) * LDV + key] = x[i];
+        }
+    }
     __syncthreads();
-    floatx4 s[L / 16];
-    scores<D, L>(s, Qs, Ks, q0, t, kl);
-    softmax_rows<L>(s, mv, mask != nullptr, scale);
-    // P -> LDS as [query][key]; each wavefront reads back only its own 16 rows, so no barrier is needed.
+    floatx4 s[NB];
 #pragma unroll
-    for (int j = 0; j < L / 16; j++)
+    for (int j = 0; j < NB; j++) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < 4; r++) Ps[(q0 + 4 * kl + r) * LDP + 16 * j + t] = s[j][r];
-    floatx4 oacc[D / 16];
+    for (int blk = 0; blk < DB; blk++)
 #pragma unroll
-    for (int jn = 0; jn < D / 16; jn++) oacc[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
-    mm_kA<D, L, LDP>(oacc, Ps, q0, Vs, t, kl);
-    store_rows<D>(o + (row0 + qb * 64) * ldo + h * D, ldo, q0, oacc, t, kl, 0);
+        for (int j = 0; j < NB; j++) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Ks[(16 * j + t) * LDK + 16 * blk + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[j] = mfma4(a[u], qf[blk][u], s[j]);
+        }
+    // Softmax over keys for query t.
+    float mx = -__int_as_float(0x7F800000);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float x = s[j][r] * scale;
+            if (mask) x = x + mv[j][r];
+            s[j][r] = x;
+            mx = x > mx ? x : mx;
+        }
+    {
+        float w2 = __shfl_xor(mx, 16, 64);
+        mx = w2 > mx ? w2 : mx;
+        w2 = __shfl_xor(mx, 32, 64);
+        mx = w2 > mx ? w2 : mx;
+    }
+    float pr[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float e = omd::exp_nonpos(s[j][r] - mx);
+            s[j][r] = e;
+            pr[r] += e;
+        }
+#pragma unroll
+    for (int r = 0; r < 4; r++) pr[r] = pr[r] + __shfl_down(pr[r], 32, 64);  // p[i] + p[i+8]  (kl + 2)
+#pragma unroll
+    for (int r = 0; r < 4; r++) pr[r] = pr[r] + __shfl_down(pr[r], 16, 64);  // p[i] + p[i+4]  (kl + 1)
+    pr[0] = pr[0] + pr[2];                                                   // p[i] + p[i+2]
+    pr[1] = pr[1] + pr[3];
+    pr[0] = pr[0] + pr[1];                                                   // p[0] + p[1]
+    const float l = __shfl(pr[0], t, 64);  // the total sits on lane t of group 0
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) s[j][r] = omd::canon(s[j][r] / l);
+    // O^T = V^T P^T
+    floatx4 oa[DB];
+#pragma unroll
+    for (int db = 0; db < DB; db++) {
+        oa[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Vt[(16 * db + t) * LDV + 16 * j + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) oa[db] = mfma4(a[u], s[j][u], oa[db]);
+        }
+    }
+    float *og = o + (row0 + qrow) * ldo + h * D;
+#pragma unroll
+    for (int db = 0; db < DB; db++) *reinterpret_cast<floatx4 *>(og + 16 * db + 4 * kl) = oa[db];
 }
 
 template <int D, int L>
@@ -291,7 +364,7 @@ om_status om_attention_fwd_fused(om_ctx *ctx, const float *q, const float *k, co
     OM_REQUIRE(ctx, o, "om_attention_fwd_fused: NULL output");
     if (scale == 0.0f || scale != scale) scale = 1.0f / sqrtf((float)d);
     const int64_t mstride = (mask && mask_batched) ? (int64_t)L * L : 0;
-    if (fused_ok(q, k, v, ld_qkv, ld_o, L, L, d) && ((uintptr_t)o & 7) == 0) {
+    if (fused_ok(q, k, v, ld_qkv, ld_o, L, L, d) && ((uintptr_t)o & 15) == 0 && ((uintptr_t)mask & 15) == 0) {
         dim3 grid(L / 64, H, B);
         if (L == 128)
             hipLaunchKernelGGL((k_attn_fwd<32, 128>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o,

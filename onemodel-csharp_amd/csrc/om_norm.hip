@@ -89,6 +89,48 @@ __global__ void __launch_bounds__(NTH) k_ln_fwd_lds(const float *__restrict__ x,
     }
 }
 
+// LayerNorm forward for a compile-time width (a multiple of 16): a 16-lane group per row, lane t holding elements
+// t, t+16, ... in registers. All of a row's loads (and gamma/beta, once per wavefront) are issued before any use, and
+// the Sum16 chains run on registers; the arithmetic is k_ln_fwd's, bit for bit.
+template <int COLS>
+__global__ void __launch_bounds__(kBlock) k_ln_fwd_w(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                     const float *__restrict__ beta, float *__restrict__ y,
+                                                     float *__restrict__ mean_out, float *__restrict__ rstd_out,
+                                                     int rows, float eps) {
+    constexpr int PER = COLS / 16;
+    const int row = (blockIdx.x * kBlock + threadIdx.x) >> 4, t = threadIdx.x & 15;
+    if (row >= rows) return;  // whole 16-lane groups leave together
+    const float *xr = x + (int64_t)row * COLS + t;
+    float v[PER], gm[PER], bt[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) v[k] = xr[16 * k];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        gm[k] = gamma[t + 16 * k];
+        bt[k] = beta[t + 16 * k];
+    }
+    const float n = (float)COLS;
+    float p = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) p += v[k];
+    const float mean = sum16_combine(p) / n;
+    p = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        float d = v[k] - mean;
+        p += d * d;
+    }
+    const float ssq = sum16_combine(p);
+    const float inv = 1.0f / sqrtf(ssq / n + eps);
+    if (t == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = inv;
+    }
+    float *yr = y + (int64_t)row * COLS + t;
+#pragma unroll
+    for (int k = 0; k < PER; k++) yr[16 * k] = omd::canon(((v[k] - mean) * inv) * gm[k] + bt[k]);
+}
+
 // LayerNorm backward (BackwardNn.cs:170-223), cols <= 64*kMaxPer: a wavefront per row, a block per chunk of rows.
 // dx is written per row; the dgamma/dbeta column contributions are kept per lane in double and summed over the
 // block's waves in LDS (fixed order), giving partial[chunk][col] for the second pass.
@@ -170,6 +212,88 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
         }
     }
 }
+// LayerNorm backward for a compile-time width (a multiple of 64): a wavefront per row, lane l holding columns
+// l, l+64, ...; each wavefront walks RPW consecutive rows with the next row's loads in flight while the current row
+// computes, and the workgroup's fp64 column partials of dgamma / dbeta go out once. Same arithmetic as k_ln_bwd.
+template <int COLS, int RPW, int NW>
+__global__ void __launch_bounds__(NW * 64) k_ln_bwd_w(const float *__restrict__ g, const float *__restrict__ x,
+                                                     const float *__restrict__ gamma, const float *__restrict__ mean,
+                                                     const float *__restrict__ rstd, float *__restrict__ dx,
+                                                     double *__restrict__ part_g, double *__restrict__ part_b,
+                                                     int rows, int acc_dx) {
+    constexpr int PER = COLS / 64;
+    __shared__ double lds[NW][COLS];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int rbase = (blockIdx.x * NW + w) * RPW;
+    double pg[PER], pb[PER];
+    float gam[PER];
+#pragma unroll
+    for (int c = 0; c < PER; c++) {
+        pg[c] = pb[c] = 0.0;
+        gam[c] = gamma[lane + 64 * c];
+    }
+    float xv[2][PER], gv[2][PER], mv[2], sv[2];
+    auto load = [&](int slot, int r) {
+        if (r < rows) {
+            const float *xr = x + (int64_t)r * COLS + lane, *gr = g + (int64_t)r * COLS + lane;
+#pragma unroll
+            for (int c = 0; c < PER; c++) {
+                xv[slot][c] = xr[64 * c];
+                gv[slot][c] = gr[64 * c];
+            }
+            mv[slot] = mean[r];
+            sv[slot] = rstd[r];
+        }
+    };
+    load(0, rbase);
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const int cur = i & 1, r = rbase + i;
+        if (i + 1 < RPW) load(cur ^ 1, r + 1);
+        if (r >= rows) break;
+        const float m = mv[cur], s = sv[cur];
+        double sum1 = 0.0, sum2 = 0.0;
+        float xh[PER];
+#pragma unroll
+        for (int c = 0; c < PER; c++) {
+            const float xhat = (xv[cur][c] - m) * s;
+            const float gg = gv[cur][c];
+            const float dxhat = gg * gam[c];
+            sum1 += (double)dxhat;
+            sum2 += (double)(dxhat * xhat);
+            pg[c] += (double)(gg * xhat);
+            pb[c] += (double)gg;
+            xh[c] = xhat;
+        }
+        sum1 = omd::wave_sum(sum1);
+        sum2 = omd::wave_sum(sum2);
+        if (dx) {
+            const float m1 = (float)(sum1 / COLS), m2 = (float)(sum2 / COLS);
+            float *dr = dx + (int64_t)r * COLS + lane;
+#pragma unroll
+            for (int c = 0; c < PER; c++) {
+                const float v = s * (((gv[cur][c] * gam[c]) - m1) - (xh[c] * m2));
+                dr[64 * c] = acc_dx ? dr[64 * c] + v : v;
+            }
+        }
+    }
+    if (!part_g && !part_b) return;
+    for (int pass = 0; pass < 2; pass++) {
+        double *part = pass == 0 ? part_g : part_b;
+        if (!part) continue;
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < PER; c++) lds[w][lane + 64 * c] = pass == 0 ? pg[c] : pb[c];
+        __syncthreads();
+        for (int j = threadIdx.x; j < COLS; j += NW * 64) {
+            double t = 0.0;
+#pragma unroll
+            for (int q = 0; q < NW; q++) t += lds[q][j];
+            part[(int64_t)blockIdx.x * COLS + j] = t;
+        }
+    }
+}
+
 // Generic (any width) LayerNorm backward for dx only: a wavefront per row, columns strided.
 __global__ void __launch_bounds__(kBlock) k_ln_bwd_dx_wide(const float *__restrict__ g, const float *__restrict__ x,
                                                            const float *__restrict__ gamma,
@@ -373,7 +497,14 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
     OM_REQUIRE(ctx, x && gamma && beta && y && rows >= 0 && cols > 0, "om_layernorm_fwd: bad arguments");
     if (rows == 0) return OM_OK;
     const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
-    if (cols % 4 == 0 && cols <= kLnLdsMaxCols && aligned) {
+    if (cols == 384 || cols == 768) {
+        if (cols == 384)
+            hipLaunchKernelGGL(k_ln_fwd_w<384>, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma,
+                               beta, y, mean, rstd, rows, eps);
+        else
+            hipLaunchKernelGGL(k_ln_fwd_w<768>, dim3(rows_grid(rows, 16)), dim3(kBlock), 0, ctx->stream, x, gamma,
+                               beta, y, mean, rstd, rows, eps);
+    } else if (cols % 4 == 0 && cols <= kLnLdsMaxCols && aligned) {
         // Four rows per 64-thread block: many small blocks keep several in flight per CU.
         const size_t lds = (size_t)4 * (cols + 16) * sizeof(float);
         hipLaunchKernelGGL(k_ln_fwd_lds<64>, dim3((rows + 3) / 4), dim3(64), lds, ctx->stream, x, gamma, beta, y,
@@ -390,7 +521,8 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
                            int acc_params) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
-    const int rpc = 8;  // rows per block: 512 blocks for 4096 rows
+    const bool wide_fixed = cols == 384 || cols == 768;
+    const int rpc = wide_fixed ? 16 : 8;  // rows per block: 256 (fixed widths) or 512 blocks for 4096 rows
     int chunks = (rows + rpc - 1) / rpc;
     bool params = dgamma || dbeta;
     double *pg = nullptr, *pb = nullptr;
@@ -401,7 +533,16 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
         pg = dgamma ? reinterpret_cast<double *>(scr) : nullptr;
         pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
     }
-    if (cols <= 64 * kMaxPer) {
+    if (wide_fixed) {
+        // 16 wavefronts of one row each per block: every row's loads are in flight at once, and the block's 16
+        // rows share one set of fp64 column partials.
+        if (cols == 384)
+            hipLaunchKernelGGL((k_ln_bwd_w<384, 1, 16>), dim3(chunks), dim3(1024), 0, ctx->stream, g, x, gamma, mean,
+                               rstd, dx, pg, pb, rows, acc_dx);
+        else
+            hipLaunchKernelGGL((k_ln_bwd_w<768, 1, 16>), dim3(chunks), dim3(1024), 0, ctx->stream, g, x, gamma, mean,
+                               rstd, dx, pg, pb, rows, acc_dx);
+    } else if (cols <= 64 * kMaxPer) {
         const int per = (cols + 63) / 64;
 #define OM_LNB(P)                                                                                                   \
     hipLaunchKernelGGL(k_ln_bwd<P>, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, pg, pb, \

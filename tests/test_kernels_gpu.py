@@ -219,7 +219,8 @@ def test_add_sub_mul_axpy_mean(dev, T):
 
 
 # ------------------------------------------------------------------------------------------------ norms and softmax
-@pytest.mark.parametrize("rows,cols", [(4096, 384), (512, 768), (7, 1536), (33, 2000), (17, 12), (9, 10), (40, 960)])
+@pytest.mark.parametrize("rows,cols", [(4096, 384), (512, 768), (7, 1536), (33, 2000), (17, 12), (9, 10), (40, 960),
+                                       (37, 384), (21, 768)])
 def test_layernorm(dev, T, rows, cols):
     rng = np.random.default_rng(rows + cols)
     x, g = rnd(rng, rows, cols, scale=2.0) + 0.5, rnd(rng, rows, cols)
