@@ -139,6 +139,61 @@ def time_adamw(pkg, model, ev, reps: int = 50):
             "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
 
 
+def time_row_kernels(pkg, model, ev, reps: int = 50):
+    """The C3 step's LayerNorm forward/backward (4096 x 384, om_layernorm_bwd including its fp64 column-sum final)
+    and fused attention forward/backward (B 32, H 12, L 128, D 32, padding mask), on random data, HIP events on the
+    model's stream. LayerNorm is priced in algorithmic HBM bytes (forward 8 B/elem + 8 B/row + 8 B/col, backward
+    12 B/elem + 8 B/row + 12 B/col), attention in MFMA flops (forward 2 products, backward 5, of 2 B H L^2 D)."""
+    import numpy as np
+    L = pkg.load_hip()
+    ctx = model.ctx
+    st = L.om_ctx_stream(ctx)
+    out = {}
+    R, Cc = 4096, 384
+    x, g = _dev_rand(L, ctx, R * Cc, 1.0, 5), _dev_rand(L, ctx, R * Cc, 1.0, 6)
+    gam, bet = _dev_rand(L, ctx, Cc, 0.1, 7), _dev_rand(L, ctx, Cc, 0.1, 8)
+    y, dx = _dev_buf(L, ctx, R * Cc, 0.0), _dev_buf(L, ctx, R * Cc, 0.0)
+    mu, rs = _dev_buf(L, ctx, R, 0.0), _dev_buf(L, ctx, R, 0.0)
+    dg, db = _dev_buf(L, ctx, Cc, 0.0), _dev_buf(L, ctx, Cc, 0.0)
+    fwd = lambda: L.om_layernorm_fwd(ctx, x, gam, bet, y, mu, rs, R, Cc, C.c_float(1e-5))
+    bwd = lambda: L.om_layernorm_bwd(ctx, g, x, gam, mu, rs, dx, dg, db, R, Cc, 0, 0)
+    for name, f, nbytes in (("layernorm_fwd", fwd, 8 * R * Cc + 8 * R + 8 * Cc),
+                            ("layernorm_bwd", bwd, 12 * R * Cc + 8 * R + 12 * Cc)):
+        for _ in range(3):
+            assert f() == 0
+        ms = ev.time(st, f, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"bound": "hbm", "kernel": f"om_{name} 4096x384", "achieved": round(gbs, 1), "peak": HBM_PEAK,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
+    B, H, Ls, D = 32, 12, 128, 32
+    W = H * D
+    qkv = _dev_rand(L, ctx, B * Ls * 3 * W, 1.0, 9)
+    go = _dev_rand(L, ctx, B * Ls * W, 1.0, 10)
+    rng = np.random.default_rng(11)
+    mask = np.zeros((B, Ls, Ls), np.float32)
+    for b in range(B):
+        mask[b, :, rng.integers(64, 129):] = -np.inf
+    M = C.c_void_p()
+    assert L.om_alloc(ctx, 0, mask.nbytes, C.byref(M)) == 0
+    assert L.om_upload(ctx, M, mask.ctypes.data_as(C.c_void_p), mask.nbytes) == 0
+    o, dqkv = _dev_buf(L, ctx, B * Ls * W, 0.0), _dev_buf(L, ctx, B * Ls * 3 * W, 0.0)
+    off = lambda p, i: C.c_void_p(p.value + 4 * i * W)
+    sc = C.c_float(0.0)
+    afwd = lambda: L.om_attention_fwd_fused(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, o, W, B, H, Ls, D, sc)
+    abwd = lambda: L.om_attention_bwd_fused(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, go, W, dqkv,
+                                            off(dqkv, 1), off(dqkv, 2), 3 * W, B, H, Ls, D, sc, 0)
+    unit = 2.0 * B * H * Ls * Ls * D
+    for name, f, flops in (("attention_fwd", afwd, 2 * unit), ("attention_bwd", abwd, 5 * unit)):
+        for _ in range(3):
+            assert f() == 0
+        ms = ev.time(st, f, reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"bound": "mfma", "kernel": f"om_{name}_fused B32 H12 L128 D32 masked", "achieved": round(tf, 2),
+                     "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK, 4),
+                     "ms_per_launch": round(ms, 5)}
+    return out
+
+
 COPY_PROBE_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dominant_kernel_traffic.json")
 
@@ -231,7 +286,7 @@ def main():
     if not a.no_kernels:
         ev = HipEvents()
         out["roofline"] = time_dominant_kernel(pkg, model, ev)
-        out["kernels"] = {"adamw": time_adamw(pkg, model, ev)}
+        out["kernels"] = {"adamw": time_adamw(pkg, model, ev), **time_row_kernels(pkg, model, ev)}
     if not a.no_cpu:
         cb = cpu_baseline(a.config, a.cpu_seconds)
         cb["gpu_over_cpu"] = round(sps / cb["value"], 1)

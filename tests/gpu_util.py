@@ -1,5 +1,11 @@
 """Helpers for the GPU tests: load the package (its directory name has a hyphen), a library context, and device
-buffers. torch is used only to own device memory; every computation under test runs in lib/libom_hip.so."""
+buffers.
+
+Device buffers come from the HIP runtime that lib/libom_hip.so itself links (/opt/rocm's libamdhip64), reached
+through ctypes: no second GPU runtime is loaded into the test process (torch's wheel ships its own copies of the HIP
+and HSA runtimes, and two runtimes in one process cannot both open the device). Every computation under test runs in
+lib/libom_hip.so.
+"""
 import ctypes as C
 import importlib.util
 import os
@@ -22,32 +28,81 @@ def load_pkg():
     return m
 
 
+_HIP = None
+
+
+def hip():
+    """The HIP runtime libom_hip.so is linked against (already loaded with it, so the same instance)."""
+    global _HIP
+    if _HIP is None:
+        load_pkg().load_hip()
+        h = C.CDLL("libamdhip64.so.7")
+        h.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        h.hipFree.argtypes = [C.c_void_p]
+        h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        h.hipDeviceSynchronize.argtypes = []
+        _HIP = h
+    return _HIP
+
+
+H2D, D2H = 1, 2
+
+
+class DevBuf:
+    """A device allocation with a shape and dtype; `data_ptr()` is what the ABI calls take."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self._p = C.c_void_p()
+        st = hip().hipMalloc(C.byref(self._p), max(self.nbytes, 4))
+        if st != 0:
+            raise RuntimeError(f"hipMalloc({self.nbytes}) failed: {st}")
+
+    def data_ptr(self):
+        return self._p.value
+
+    def __del__(self):
+        try:
+            if self._p:
+                hip().hipDeviceSynchronize()
+                hip().hipFree(self._p)
+                self._p = C.c_void_p()
+        except Exception:
+            pass
+
+
 class Dev:
-    """Device buffers from torch plus the library context; `sync()` orders torch's stream and the library's."""
+    """Device buffers plus the library context."""
 
     def __init__(self):
-        import torch
-        self.torch = torch
         self.pkg = load_pkg()
         self.ctx = self.pkg.Context(0)
+        self.hip = hip()
 
     def put(self, a):
-        t = self.torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
-        self.torch.cuda.synchronize()
-        return t
+        a = np.ascontiguousarray(a)
+        b = DevBuf(a.shape, a.dtype)
+        if b.nbytes:
+            st = self.hip.hipMemcpy(b.data_ptr(), a.ctypes.data, b.nbytes, H2D)
+            if st != 0:
+                raise RuntimeError(f"hipMemcpy H2D failed: {st}")
+        return b
 
     def empty(self, shape, dtype=np.float32, fill=None):
-        td = {np.float32: self.torch.float32, np.int32: self.torch.int32}[dtype]
-        t = self.torch.empty(tuple(shape), dtype=td, device="cuda")
         if fill is not None:
-            t.fill_(fill)
-        self.torch.cuda.synchronize()
-        return t
+            return self.put(np.full(tuple(shape), fill, dtype))
+        return DevBuf(shape, dtype)
 
-    def get(self, t):
+    def get(self, b):
         self.ctx.sync()
-        self.torch.cuda.synchronize()
-        return t.cpu().numpy()
+        out = np.empty(b.shape, b.dtype)
+        if b.nbytes:
+            st = self.hip.hipMemcpy(out.ctypes.data, b.data_ptr(), b.nbytes, D2H)
+            if st != 0:
+                raise RuntimeError(f"hipMemcpy D2H failed: {st}")
+        return out
 
     def call(self, name, *args):
         conv = [a.data_ptr() if hasattr(a, "data_ptr") else a for a in args]
