@@ -139,6 +139,33 @@ def time_adamw(pkg, model, ev, reps: int = 50):
             "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
 
 
+def time_clip(pkg, model, ev, reps: int = 50):
+    """GradClip.ClipNorm on the device over C5's parameter count (28.36M gradients, one segment): the norm alone
+    (partials + final, 4 algorithmic bytes per gradient) and norm + in-place scaling (4 + 8 bytes per gradient)."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    n = 28_358_409
+    g = _dev_rand(L, ctx, n, 1e-3, 12)
+    slot = _dev_buf(L, ctx, 2, 0.0)
+    ptrs, lens = (C.c_void_p * 1)(g.value), (C.c_int64 * 1)(n)
+    coef = C.c_void_p(slot.value + 4)
+    out = {}
+    for name, in_place, per in (("clip_grad_norm", 0, 4.0), ("clip_grad_norm_scale", 1, 12.0)):
+        def launch(in_place=in_place):
+            st = L.om_clip_grad_norm(ctx, 1, C.cast(ptrs, C.c_void_p), C.cast(lens, C.c_void_p), C.c_float(0.5), 0,
+                                     in_place, slot, coef)
+            if st != 0:
+                raise RuntimeError(L.om_last_error(ctx).decode())
+        for _ in range(3):
+            launch()
+        ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
+        gbs = per * n / (ms * 1e-3) / 1e9
+        out[name] = {"bound": "hbm", "kernel": f"om_clip_grad_norm (C5 arena, 28.36M grads, "
+                     f"{'norm and in-place scale' if in_place else 'norm only'})", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
+    return out
+
+
 def time_row_kernels(pkg, model, ev, reps: int = 50):
     """The C3 step's LayerNorm forward/backward (4096 x 384, om_layernorm_bwd including its fp64 column-sum final)
     and fused attention forward/backward (B 32, H 12, L 128, D 32, padding mask), on random data, HIP events on the
@@ -286,7 +313,8 @@ def main():
     if not a.no_kernels:
         ev = HipEvents()
         out["roofline"] = time_dominant_kernel(pkg, model, ev)
-        out["kernels"] = {"adamw": time_adamw(pkg, model, ev), **time_row_kernels(pkg, model, ev)}
+        out["kernels"] = {"adamw": time_adamw(pkg, model, ev), **time_row_kernels(pkg, model, ev),
+                          **time_clip(pkg, model, ev)}
     if not a.no_cpu:
         cb = cpu_baseline(a.config, a.cpu_seconds)
         cb["gpu_over_cpu"] = round(sps / cb["value"], 1)

@@ -48,7 +48,8 @@ int om_abi_version(void);
 /* Overlap mode (off by default). When on, om_linear_bwd enqueues its weight and bias gradients on a second stream
  * (default priority) that starts after everything already queued on the context's stream, so they run beside the
  * rest of the backward; their results are complete for the context's stream after om_ctx_join, which om_ctx_sync,
- * om_step_reset, om_upload, om_download, om_copy, om_zero, om_fill, om_adam_step and om_sgd_step perform first.
+ * om_step_reset, om_upload, om_download, om_copy, om_zero, om_fill, om_adam_step(_scaled), om_sgd_step and
+ * om_clip_grad_norm/value perform first.
  * Inputs g and x of such a call must not be overwritten before that join. No counterpart in the reference, whose
  * CPU backward is sequential (Engine.cs:124-207); results do not depend on the mode. */
 om_status om_ctx_set_overlap(om_ctx *ctx, int enable);
@@ -249,10 +250,33 @@ om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v
                        float sqrt_bc2);
 /* Host helper: Adam.IntPow + BeginStep in double for step t (1-based). */
 void om_adam_scalars(float lr, float beta1, float beta2, int64_t t, float *step_size, float *sqrt_bc2);
+/* om_adam_step with GradClip.ClipNorm's scaling folded into the read of g: grad_scale is a device float (the coef
+ * om_clip_grad_norm wrote) and every gradient element is used as g * c when c < 1, unchanged otherwise — the same
+ * float product the reference's in-place scaling (Schedules.cs:70-76) stores before Adam reads it, so the update is
+ * bit-identical to clip-then-step; the gradient buffer itself is left unscaled (one fewer pass over it). */
+om_status om_adam_step_scaled(om_ctx *ctx, float *p, const float *g, float *m, float *v, float *vmax, int64_t n,
+                              float lr, float beta1, float beta2, float eps, float weight_decay, int decoupled,
+                              float step_size, float sqrt_bc2, const float *grad_scale);
 /* Sgd.Update (Optimizers.cs, class Sgd) over n contiguous elements; buf may be NULL (no momentum); first != 0 on
  * the parameter's first step (the momentum buffer starts from the gradient). */
 om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t n, float lr, float momentum,
                       float dampening, float weight_decay, int nesterov, int first);
+
+/* ---------------------------------------------------------------------------------------------- gradient clipping */
+/* GradClip.ClipNorm (Schedules.cs:22-100) over `count` gradient segments: grads[i] (device) holds lens[i] floats;
+ * a NULL or empty segment is skipped, as a parameter without a gradient is (pass a row-sparse gradient's values).
+ * The norm is the L2 norm (squares summed in fp64; the device sums in a fixed tree that depends only on the
+ * segment lengths, within count·2^-53 relative of the reference's serial sum) or, with infinity_norm, the largest
+ * |g| (a NaN wins). When the norm is finite and coef = (float)(max_norm / (norm + 1e-6)) < 1, every element becomes
+ * g * coef. Asynchronous: the norm is written as float to *total (device, may be NULL) — om_download it to read the
+ * value ClipNorm returns — and the coefficient to *coef (device, may be NULL; 1 when the norm is not finite).
+ * scale_in_place = 0 leaves the gradients unscaled for om_adam_step_scaled (coef required then).
+ * max_norm must be positive (OM_E_ARG, the reference's ArgumentOutOfRangeException). */
+om_status om_clip_grad_norm(om_ctx *ctx, int count, float *const *grads, const int64_t *lens, float max_norm,
+                            int infinity_norm, int scale_in_place, float *total, float *coef);
+/* GradClip.ClipValue (Schedules.cs:119-149): every element clamped to [-clip_value, clip_value], NaN stays NaN;
+ * bit-exact. clip_value must not be negative (OM_E_ARG). */
+om_status om_clip_grad_value(om_ctx *ctx, int count, float *const *grads, const int64_t *lens, float clip_value);
 
 #ifdef __cplusplus
 }

@@ -64,6 +64,48 @@ om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel);
  * Generator): kind 0 = uniform [lo, hi), 1 = benchmark normal, 2 = ints in [lo, hi). */
 void omt_generate(uint64_t seed, int kind, float lo, float hi, void *out, int64_t n);
 
+/* ------------------------------------------------------------------------------------------ learning rate */
+/* Optimizer.LearningRate (Optimizers.cs:30-60): the rate the next step uses. */
+float omt_lr(omt_model *m);
+om_status omt_set_lr(omt_model *m, float lr);
+
+/* LrSchedule and its subclasses (Schedules.cs:151-422): pure functions of the step count, IEEE double in the
+ * reference's order, so rates are the reference's bit for bit. Arguments the reference rejects with
+ * ArgumentOutOfRangeException return OM_E_ARG (message: omt_last_error(NULL)). Host only, no device. */
+typedef struct omt_lr_schedule omt_lr_schedule;
+om_status omt_lr_constant(float lr, omt_lr_schedule **out);                                     /* ConstantLr */
+om_status omt_lr_step(float base_lr, int64_t step_size, float gamma, omt_lr_schedule **out);    /* StepLr */
+om_status omt_lr_cosine(float base_lr, int64_t total_steps, float min_lr, omt_lr_schedule **out); /* CosineLr */
+/* WarmupLr over a copy of `after` (the caller keeps and frees its own). */
+om_status omt_lr_warmup(const omt_lr_schedule *after, int64_t warmup_steps, float start_factor,
+                        omt_lr_schedule **out);
+om_status omt_lr_warmup_cosine(float base_lr, int64_t warmup_steps, int64_t total_steps, float floor_fraction,
+                               omt_lr_schedule **out);                                          /* WarmupCosineLr */
+om_status omt_lr_onecycle(float max_lr, int64_t total_steps, float pct_start, float div_factor,
+                          float final_div_factor, omt_lr_schedule **out);                       /* OneCycleLr */
+void omt_lr_free(omt_lr_schedule *s);
+/* LrSchedule.LrAt(step); NaN for a NULL schedule. */
+float omt_lr_at(const omt_lr_schedule *s, int64_t step);
+/* LrSchedule.Cos: cos(pi * t) for t in [0, 1] (clamped), from + - * / only. */
+double omt_lr_cos(double t);
+/* LrSchedule.Apply before every optimizer step of the model: the rate becomes s(step count). The model keeps a
+ * copy; NULL detaches (the rate then stays where it is). */
+om_status omt_set_lr_schedule(omt_model *m, const omt_lr_schedule *s);
+
+/* ------------------------------------------------------------------------------------------ gradient clipping */
+/* GradClip.ClipNorm(model.Parameters(), max_norm, infinity_norm) (Schedules.cs:22-100) on the gradients now in the
+ * arena, in place, on the device (om_clip_grad_norm). *norm (host, may be NULL) receives the norm ClipNorm returns;
+ * asking for it waits for the device. */
+om_status omt_clip_grad_norm(omt_model *m, float max_norm, int infinity_norm, float *norm);
+/* GradClip.ClipValue(model.Parameters(), clip_value) (Schedules.cs:119-149), in place on the device. */
+om_status omt_clip_grad_value(omt_model *m, float clip_value);
+/* Makes omt_step run ClipNorm between the backward and the optimizer step (max_norm 0 switches it off). The scaling
+ * is folded into AdamW's read of the gradients (om_adam_step_scaled), so the step's parameters and moments equal
+ * backward + omt_clip_grad_norm + omt_optimizer_step bit for bit while the gradients stay unscaled. */
+om_status omt_set_clip(omt_model *m, float max_norm, int infinity_norm);
+/* The norm the last clipped omt_step computed (waits for the device; NaN before the first one). */
+om_status omt_last_grad_norm(omt_model *m, float *norm);
+
 #ifdef __cplusplus
 }
 #endif

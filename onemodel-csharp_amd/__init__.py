@@ -87,7 +87,10 @@ _OM_SIGS = {
     "om_ctc_bwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci],
     "om_adam_step": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32],
     "om_adam_scalars": [f32, f32, f32, i64, C.POINTER(f32), C.POINTER(f32)],
+    "om_adam_step_scaled": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32, vp],
     "om_sgd_step": [vp, vp, vp, vp, i64, f32, f32, f32, f32, ci, ci],
+    "om_clip_grad_norm": [vp, ci, vp, vp, f32, ci, ci, vp, vp],
+    "om_clip_grad_value": [vp, ci, vp, vp, f32],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None}
 
@@ -145,6 +148,22 @@ _OMT_SIGS = {
     "omt_input_read": ([vp, ci, vp, i64], i32),
     "omt_input_grad": ([vp, ci, vp, i64], i32),
     "omt_generate": ([u64, ci, f32, f32, vp, i64], None),
+    "omt_lr": ([vp], f32),
+    "omt_set_lr": ([vp, f32], i32),
+    "omt_lr_constant": ([f32, C.POINTER(vp)], i32),
+    "omt_lr_step": ([f32, i64, f32, C.POINTER(vp)], i32),
+    "omt_lr_cosine": ([f32, i64, f32, C.POINTER(vp)], i32),
+    "omt_lr_warmup": ([vp, i64, f32, C.POINTER(vp)], i32),
+    "omt_lr_warmup_cosine": ([f32, i64, i64, f32, C.POINTER(vp)], i32),
+    "omt_lr_onecycle": ([f32, i64, f32, f32, f32, C.POINTER(vp)], i32),
+    "omt_lr_free": ([vp], None),
+    "omt_lr_at": ([vp, i64], f32),
+    "omt_lr_cos": ([C.c_double], C.c_double),
+    "omt_set_lr_schedule": ([vp, vp], i32),
+    "omt_clip_grad_norm": ([vp, f32, ci, C.POINTER(f32)], i32),
+    "omt_clip_grad_value": ([vp, f32], i32),
+    "omt_set_clip": ([vp, f32, ci], i32),
+    "omt_last_grad_norm": ([vp, C.POINTER(f32)], i32),
 }
 _TRAIN = None
 
@@ -257,6 +276,38 @@ class Model:
     def step_count(self):
         return self.L.omt_step_count(self.h)
 
+    @property
+    def lr(self) -> float:
+        return self.L.omt_lr(self.h)
+
+    @lr.setter
+    def lr(self, value: float):
+        self._check(self.L.omt_set_lr(self.h, value), "omt_set_lr")
+
+    def set_schedule(self, schedule):
+        """LrSchedule.Apply before every optimizer step (None detaches)."""
+        self._check(self.L.omt_set_lr_schedule(self.h, schedule.h if schedule is not None else None),
+                    "omt_set_lr_schedule")
+
+    def clip_grad_norm(self, max_norm: float, infinity_norm: bool = False) -> float:
+        """GradClip.ClipNorm over Parameters() on the device, in place; returns the norm."""
+        v = f32()
+        self._check(self.L.omt_clip_grad_norm(self.h, max_norm, int(infinity_norm), C.byref(v)),
+                    "omt_clip_grad_norm")
+        return v.value
+
+    def clip_grad_value(self, clip_value: float):
+        self._check(self.L.omt_clip_grad_value(self.h, clip_value), "omt_clip_grad_value")
+
+    def set_clip(self, max_norm: float, infinity_norm: bool = False):
+        """ClipNorm inside step() (folded into AdamW); 0 switches it off."""
+        self._check(self.L.omt_set_clip(self.h, max_norm, int(infinity_norm)), "omt_set_clip")
+
+    def last_grad_norm(self) -> float:
+        v = f32()
+        self._check(self.L.omt_last_grad_norm(self.h, C.byref(v)), "omt_last_grad_norm")
+        return v.value
+
     def close(self):
         if getattr(self, "h", None):
             self.L.omt_destroy(self.h)
@@ -265,6 +316,54 @@ class Model:
     def __del__(self):
         try:
             self.close()
+        except Exception:
+            pass
+
+
+class LrSchedule:
+    """A learning-rate schedule of libom_train.so (include/om_train.h): `LrSchedule.constant(...)`, `.step(...)`,
+    `.cosine(...)`, `.warmup(inner, ...)`, `.warmup_cosine(...)`, `.onecycle(...)`; `lr_at(step)` is LrAt."""
+
+    def __init__(self, make, *args):
+        self.L = load_train()
+        h = vp()
+        st = getattr(self.L, make)(*args, C.byref(h))
+        if st != 0:
+            raise OmError(f"{make} failed ({st}): {self.L.omt_last_error(None).decode()}")
+        self.h = h
+
+    @classmethod
+    def constant(cls, lr):
+        return cls("omt_lr_constant", lr)
+
+    @classmethod
+    def step(cls, base_lr, step_size, gamma=0.1):
+        return cls("omt_lr_step", base_lr, step_size, gamma)
+
+    @classmethod
+    def cosine(cls, base_lr, total_steps, min_lr=0.0):
+        return cls("omt_lr_cosine", base_lr, total_steps, min_lr)
+
+    @classmethod
+    def warmup(cls, after, warmup_steps, start_factor=0.0):
+        return cls("omt_lr_warmup", after.h, warmup_steps, start_factor)
+
+    @classmethod
+    def warmup_cosine(cls, base_lr, warmup_steps, total_steps, floor_fraction=0.0):
+        return cls("omt_lr_warmup_cosine", base_lr, warmup_steps, total_steps, floor_fraction)
+
+    @classmethod
+    def onecycle(cls, max_lr, total_steps, pct_start=0.3, div_factor=25.0, final_div_factor=1e4):
+        return cls("omt_lr_onecycle", max_lr, total_steps, pct_start, div_factor, final_div_factor)
+
+    def lr_at(self, step: int) -> float:
+        return self.L.omt_lr_at(self.h, step)
+
+    def __del__(self):
+        try:
+            if self.h:
+                self.L.omt_lr_free(self.h)
+                self.h = None
         except Exception:
             pass
 

@@ -36,9 +36,14 @@ __device__ __forceinline__ void adam_one(float &p, float g, float &m, float &v, 
     p = pi - (a.step_size * mi) / denom;
 }
 
+// gs (may be NULL): a device-side gradient coefficient, applied as g * c when c < 1 — GradClip.ClipNorm's in-place
+// scaling (Schedules.cs:70-76) folded into the update's read of g, with the same single float rounding.
 __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const float *__restrict__ g,
                                                  float *__restrict__ m, float *__restrict__ v,
-                                                 float *__restrict__ vmax, int64_t n, AdamArgs a) {
+                                                 float *__restrict__ vmax, int64_t n, AdamArgs a,
+                                                 const float *__restrict__ gs) {
+    const float c = gs ? *gs : 1.0f;
+    const bool sc = c < 1.0f;
     int64_t stride = (int64_t)gridDim.x * kBlock;
     int64_t n4 = (vmax == nullptr) ? (n >> 2) : 0;
     float4 *p4 = reinterpret_cast<float4 *>(p);
@@ -47,6 +52,12 @@ __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const fl
     float4 *v4 = reinterpret_cast<float4 *>(v);
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
         float4 pp = p4[i], gg = g4[i], mm = m4[i], vv = v4[i];
+        if (sc) {
+            gg.x = gg.x * c;
+            gg.y = gg.y * c;
+            gg.z = gg.z * c;
+            gg.w = gg.w * c;
+        }
         adam_one(pp.x, gg.x, mm.x, vv.x, nullptr, a);
         adam_one(pp.y, gg.y, mm.y, vv.y, nullptr, a);
         adam_one(pp.z, gg.z, mm.z, vv.z, nullptr, a);
@@ -56,7 +67,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const fl
         v4[i] = vv;
     }
     for (int64_t i = (n4 << 2) + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-        adam_one(p[i], g[i], m[i], v[i], vmax ? vmax + i : nullptr, a);
+        adam_one(p[i], sc ? g[i] * c : g[i], m[i], v[i], vmax ? vmax + i : nullptr, a);
 }
 
 __global__ void __launch_bounds__(kBlock) k_sgd(float *__restrict__ p, const float *__restrict__ g,
@@ -95,16 +106,17 @@ void om_adam_scalars(float lr, float beta1, float beta2, int64_t t, float *step_
     if (sqrt_bc2) *sqrt_bc2 = (float)std::sqrt(bc2);
 }
 
-om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v, float *vmax, int64_t n, float lr,
-                       float beta1, float beta2, float eps, float weight_decay, int decoupled, float step_size,
-                       float sqrt_bc2) {
+static om_status adam_launch(om_ctx *ctx, const char *what, float *p, const float *g, float *m, float *v,
+                             float *vmax, int64_t n, float lr, float beta1, float beta2, float eps,
+                             float weight_decay, int decoupled, float step_size, float sqrt_bc2,
+                             const float *grad_scale) {
     OM_CHECK_CTX(ctx);
     if (om::join(ctx)) return OM_E_DEVICE;  // the gradients may still be in flight on the weight-gradient stream
-    OM_REQUIRE(ctx, n >= 0, "om_adam_step: negative length");
+    OM_REQUIRE(ctx, n >= 0, "%s: negative length", what);
     if (n == 0) return OM_OK;
-    OM_REQUIRE(ctx, p && g && m && v, "om_adam_step: NULL pointer");
+    OM_REQUIRE(ctx, p && g && m && v, "%s: NULL pointer", what);
     OM_REQUIRE(ctx, ((uintptr_t)p | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) % 16 == 0,
-               "om_adam_step: p, g, m, v must be 16-byte aligned");
+               "%s: p, g, m, v must be 16-byte aligned", what);
     AdamArgs a;
     a.lr = lr;
     a.b1 = beta1;
@@ -119,8 +131,24 @@ om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v
     a.decoupled = decoupled;
     // Enough waves to cover HBM latency on 256 CUs, grid-stride beyond that.
     unsigned grid = om::grid1d((n + 3) / 4, kBlock, (int64_t)ctx->num_cus * 8);
-    hipLaunchKernelGGL(k_adam, dim3(grid), dim3(kBlock), 0, ctx->stream, p, g, m, v, vmax, n, a);
-    return OM_LAUNCH_CHECK(ctx, "om_adam_step");
+    hipLaunchKernelGGL(k_adam, dim3(grid), dim3(kBlock), 0, ctx->stream, p, g, m, v, vmax, n, a, grad_scale);
+    return OM_LAUNCH_CHECK(ctx, what);
+}
+
+om_status om_adam_step(om_ctx *ctx, float *p, const float *g, float *m, float *v, float *vmax, int64_t n, float lr,
+                       float beta1, float beta2, float eps, float weight_decay, int decoupled, float step_size,
+                       float sqrt_bc2) {
+    return adam_launch(ctx, "om_adam_step", p, g, m, v, vmax, n, lr, beta1, beta2, eps, weight_decay, decoupled,
+                       step_size, sqrt_bc2, nullptr);
+}
+
+om_status om_adam_step_scaled(om_ctx *ctx, float *p, const float *g, float *m, float *v, float *vmax, int64_t n,
+                              float lr, float beta1, float beta2, float eps, float weight_decay, int decoupled,
+                              float step_size, float sqrt_bc2, const float *grad_scale) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, grad_scale, "om_adam_step_scaled: grad_scale is NULL");
+    return adam_launch(ctx, "om_adam_step_scaled", p, g, m, v, vmax, n, lr, beta1, beta2, eps, weight_decay,
+                       decoupled, step_size, sqrt_bc2, grad_scale);
 }
 
 om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t n, float lr, float momentum,

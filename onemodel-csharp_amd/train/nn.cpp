@@ -4,6 +4,7 @@
 #include <map>
 
 #include "om_train.h"
+#include "schedules.hpp"
 #include "tape.hpp"
 
 namespace omt {
@@ -161,6 +162,10 @@ struct omt_model {
     // AdamW hyper-parameters
     float lr = 1e-3f, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, wd = 0.01f;
     int64_t step_count = 0;
+    std::unique_ptr<LrSchedule> schedule;  // LrSchedule.Apply before every step when set
+    float clip_max = 0.0f;                 // ClipNorm inside omt_step when > 0
+    int clip_inf = 0;
+    float *clip_buf = nullptr;             // device: [norm, coefficient] of the last ClipNorm
     std::string err;
 
     Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
@@ -256,6 +261,8 @@ struct omt_model {
             t->grad = gb + offset[i];
             leaves.insert(leaves.begin() + (long)i, t);
         }
+        clip_buf = (float *)device->persistent(16);
+        check(c, om_fill(c, clip_buf, std::nanf(""), 4), "clip slot");
         check(c, om_upload(c, pb, host.data(), bytes), "upload params");
         check(c, om_zero(c, gb, bytes), "zero grads");
         check(c, om_zero(c, mb, bytes), "zero m");
@@ -263,16 +270,12 @@ struct omt_model {
         device->sync();
     }
 
-    // AdamW.Step (Optimizers.cs:184-219, 501-589): BeginStep scalars on the host, then one fused update per run of
-    // consecutive parameters that have gradients (a parameter without one is skipped, as in the reference).
-    void optimizer_step() {
-        settle_grads(leaves);
-        float ss, sq;
-        om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
-        om_ctx *c = device->ctx();
-        // Runs of physically consecutive parameters with gradients (the alignment gaps between them are zero in
-        // every block, and Adam keeps a zero parameter with a zero gradient and zero moments at zero).
+    // Runs of physically consecutive parameters that have gradients, as (first element, length) in the arena: the
+    // alignment gaps between them are zero in every block, and every per-element operation here (Adam, clipping)
+    // keeps a zero parameter with a zero gradient and zero moments at zero and adds nothing to a norm.
+    std::vector<std::pair<int64_t, int64_t>> live_runs() const {
         auto live = [&](size_t q) { return params[phys[q]].second->grad_exists && params[phys[q]].second->requires_grad; };
+        std::vector<std::pair<int64_t, int64_t>> runs;
         size_t i = 0;
         while (i < phys.size()) {
             if (!live(i)) {
@@ -281,13 +284,62 @@ struct omt_model {
             }
             size_t j = i;
             while (j + 1 < phys.size() && live(j + 1)) j++;
-            int64_t beg = offset[phys[i]], end = offset[phys[j]] + params[phys[j]].second->numel;
-            check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, end - beg, lr, beta1, beta2, eps,
-                                  wd, 1, ss, sq),
-                  "om_adam_step");
+            const int64_t beg = offset[phys[i]], end = offset[phys[j]] + params[phys[j]].second->numel;
+            runs.emplace_back(beg, end - beg);
             i = j + 1;
         }
+        return runs;
+    }
+
+    // AdamW.Step (Optimizers.cs:184-219, 501-589): LrSchedule.Apply when a schedule is attached, the rate check,
+    // BeginStep scalars on the host, then one fused update per run of parameters that have gradients (a parameter
+    // without one is skipped, as in the reference). grad_scale: ClipNorm's device coefficient, folded into the read
+    // of g (om_adam_step_scaled), or NULL.
+    void optimizer_step(const float *grad_scale = nullptr) {
+        settle_grads(leaves);
+        if (schedule) lr = schedule->lr_at(step_count);
+        if (!std::isfinite(lr) || lr < 0.0f) throw Error(OM_E_ARG, "learning rate must be finite and not negative");
+        float ss, sq;
+        om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
+        om_ctx *c = device->ctx();
+        for (auto [beg, n] : live_runs()) {
+            if (grad_scale)
+                check(c, om_adam_step_scaled(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, n, lr, beta1, beta2,
+                                             eps, wd, 1, ss, sq, grad_scale),
+                      "om_adam_step_scaled");
+            else
+                check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, n, lr, beta1, beta2, eps,
+                                      wd, 1, ss, sq),
+                      "om_adam_step");
+        }
         step_count++;
+    }
+
+    // GradClip.ClipNorm / ClipValue over Parameters() (Schedules.cs:22-149) on the device; the norm and the
+    // coefficient land in clip_buf. in_place = false leaves the gradients for optimizer_step(clip_buf + 1).
+    void clip_norm(float max_norm, int infinity_norm, bool in_place) {
+        settle_grads(leaves);
+        std::vector<float *> ptrs;
+        std::vector<int64_t> lens;
+        for (auto [beg, n] : live_runs()) {
+            ptrs.push_back(gb + beg);
+            lens.push_back(n);
+        }
+        om_ctx *c = device->ctx();
+        check(c, om_clip_grad_norm(c, (int)ptrs.size(), ptrs.data(), lens.data(), max_norm, infinity_norm,
+                                   in_place ? 1 : 0, clip_buf, clip_buf + 1),
+              "om_clip_grad_norm");
+    }
+    void clip_value(float bound) {
+        settle_grads(leaves);
+        std::vector<float *> ptrs;
+        std::vector<int64_t> lens;
+        for (auto [beg, n] : live_runs()) {
+            ptrs.push_back(gb + beg);
+            lens.push_back(n);
+        }
+        om_ctx *c = device->ctx();
+        check(c, om_clip_grad_value(c, (int)ptrs.size(), ptrs.data(), lens.data(), bound), "om_clip_grad_value");
     }
 
     float forward_backward() {
@@ -304,7 +356,12 @@ struct omt_model {
         zero_grad(leaves);
         Tensor loss = loss_fn(*this);
         backward(loss);
-        optimizer_step();
+        if (clip_max > 0.0f) {
+            clip_norm(clip_max, clip_inf, false);
+            optimizer_step(clip_buf + 1);
+        } else {
+            optimizer_step();
+        }
         float v = 0.0f;
         check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
         return v;
@@ -438,6 +495,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
 
 // ------------------------------------------------------------------------------------------------ C ABI
 static std::string g_create_err;
+void omt::set_global_error(const std::string &msg) { g_create_err = msg; }
 
 template <class F>
 static om_status guard(omt_model *m, F f) {
@@ -493,6 +551,50 @@ void omt_destroy(omt_model *m) {
 }
 
 const char *omt_last_error(omt_model *m) { return m ? m->err.c_str() : g_create_err.c_str(); }
+
+float omt_lr(omt_model *m) { return m ? m->lr : std::nanf(""); }
+om_status omt_set_lr(omt_model *m, float lr) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        if (!std::isfinite(lr) || lr < 0.0f) throw Error(OM_E_ARG, "omt_set_lr: rate must be finite and not negative");
+        m->lr = lr;
+    });
+}
+om_status omt_set_lr_schedule(omt_model *m, const omt_lr_schedule *s) {
+    if (!m) return OM_E_ARG;
+    m->schedule = (s && s->s) ? s->s->clone() : nullptr;
+    return OM_OK;
+}
+om_status omt_clip_grad_norm(omt_model *m, float max_norm, int infinity_norm, float *norm) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        if (!(max_norm > 0.0f)) throw Error(OM_E_ARG, "ClipNorm: the maximum norm must be positive");
+        m->clip_norm(max_norm, infinity_norm, true);
+        if (norm)
+            check(m->device->ctx(), om_download(m->device->ctx(), norm, m->clip_buf, sizeof(float)), "norm readback");
+    });
+}
+om_status omt_clip_grad_value(omt_model *m, float clip_value) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        if (!(clip_value >= 0.0f)) throw Error(OM_E_ARG, "ClipValue: the bound must not be negative");
+        m->clip_value(clip_value);
+    });
+}
+om_status omt_set_clip(omt_model *m, float max_norm, int infinity_norm) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        if (!(max_norm >= 0.0f)) throw Error(OM_E_ARG, "omt_set_clip: max_norm must be positive (or 0 to switch off)");
+        m->clip_max = max_norm;
+        m->clip_inf = infinity_norm;
+    });
+}
+om_status omt_last_grad_norm(omt_model *m, float *norm) {
+    if (!m || !norm) return OM_E_ARG;
+    return guard(m, [&] {
+        check(m->device->ctx(), om_download(m->device->ctx(), norm, m->clip_buf, sizeof(float)), "norm readback");
+    });
+}
 
 om_status omt_step(omt_model *m, float *loss) {
     if (!m) return OM_E_ARG;

@@ -907,3 +907,50 @@ EXPORT void or_sgd_update(float *p, const float *grad, float *buf, int64_t n, fl
         p[i] -= lr * g;
     }
 }
+
+/* ------------------------------------------------------------------------------------------------ gradient clipping */
+/* GradClip.ClipNorm (Schedules.cs:22-100), serially as the reference runs it: squares (double)g*g summed in one double
+ * accumulator in segment then element order (L2), or the running largest |g| where a larger value or a NaN replaces
+ * it (infinity); the norm is the square root (L2) or the accumulator; nothing is scaled when it is not finite,
+ * otherwise coef = (float)(max_norm / (norm + 1e-6)) and every element becomes g * coef when coef < 1. NULL or empty
+ * segments are skipped. Returns the norm as float; *coef_out (may be NULL) gets coef, or 1 for a non-finite norm. */
+EXPORT float or_clip_norm(float *const *grads, const int64_t *lens, int count, float max_norm, int inf,
+                          float *coef_out) {
+    double acc = 0.0;
+    for (int i = 0; i < count; i++) {
+        if (!grads[i] || lens[i] <= 0) continue;
+        const float *s = grads[i];
+        for (int64_t j = 0; j < lens[i]; j++) {
+            if (inf) {
+                double a = fabs((double)s[j]);
+                if (a > acc || isnan(a)) acc = a;
+            } else {
+                acc += (double)s[j] * s[j];
+            }
+        }
+    }
+    double norm = inf ? acc : sqrt(acc);
+    float total = (float)norm;
+    if (!isfinite(norm)) {
+        if (coef_out) *coef_out = 1.0f;
+        return total;
+    }
+    float coef = (float)((double)max_norm / (norm + 1e-6));
+    if (coef < 1.0f)
+        for (int i = 0; i < count; i++) {
+            if (!grads[i] || lens[i] <= 0) continue;
+            for (int64_t j = 0; j < lens[i]; j++) grads[i][j] *= coef;
+        }
+    if (coef_out) *coef_out = coef;
+    return total;
+}
+/* GradClip.ClipValue (Schedules.cs:119-149): v > c ? c : v < -c ? -c : v, so NaN stays NaN. */
+EXPORT void or_clip_value(float *const *grads, const int64_t *lens, int count, float c) {
+    for (int i = 0; i < count; i++) {
+        if (!grads[i] || lens[i] <= 0) continue;
+        for (int64_t j = 0; j < lens[i]; j++) {
+            float v = grads[i][j];
+            grads[i][j] = v > c ? c : v < -c ? -c : v;
+        }
+    }
+}

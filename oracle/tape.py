@@ -45,6 +45,12 @@ def lib():
         L.or_ctc_logadd.argtypes = [ctypes.c_double, ctypes.c_double]
         L.or_sum_all.restype = ctypes.c_float
         L.or_nll_fwd.restype = ctypes.c_float
+        L.or_clip_norm.restype = ctypes.c_float
+        L.or_clip_norm.argtypes = [ctypes.POINTER(F32P), ctypes.POINTER(ctypes.c_int64), ctypes.c_int,
+                                   ctypes.c_float, ctypes.c_int, F32P]
+        L.or_clip_value.restype = None
+        L.or_clip_value.argtypes = [ctypes.POINTER(F32P), ctypes.POINTER(ctypes.c_int64), ctypes.c_int,
+                                    ctypes.c_float]
         _LIB = L
     return _LIB
 
@@ -594,3 +600,40 @@ class Sgd:
 
     def zero_grad(self):
         zero_grad(self.params)
+
+
+# ----------------------------------------------------------------------------------------------------- gradient clipping
+def _grad_table(params):
+    """Pointer and length tables over the gradients of `params` (a parameter without one gets a NULL entry, which
+    the clip functions skip, as GradClip does). Gradients are made float32 C-contiguous in place first."""
+    ptrs, lens = (F32P * len(params))(), (ctypes.c_int64 * len(params))()
+    for i, p in enumerate(params):
+        if p.grad is None:
+            lens[i] = 0
+            continue
+        p.grad = c32(p.grad)
+        ptrs[i] = fp(p.grad)
+        lens[i] = p.grad.size
+    return ptrs, lens
+
+
+def clip_grad_norm(params, max_norm, infinity_norm=False):
+    """GradClip.ClipNorm (Schedules.cs:22-100) in place over the parameters' gradients; returns (norm as float32,
+    coefficient: the scale applied when below 1, or 1 for a non-finite norm)."""
+    if not max_norm > 0:
+        raise ValueError("the maximum norm must be positive")
+    params = list(params)
+    ptrs, lens = _grad_table(params)
+    coef = ctypes.c_float()
+    total = lib().or_clip_norm(ptrs, lens, len(params), ctypes.c_float(max_norm), int(infinity_norm),
+                               ctypes.byref(coef))
+    return np.float32(total), np.float32(coef.value)
+
+
+def clip_grad_value(params, clip_value):
+    """GradClip.ClipValue (Schedules.cs:119-149) in place."""
+    if not clip_value >= 0:
+        raise ValueError("the bound must not be negative")
+    params = list(params)
+    ptrs, lens = _grad_table(params)
+    lib().or_clip_value(ptrs, lens, len(params), ctypes.c_float(clip_value))
