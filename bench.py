@@ -60,12 +60,14 @@ class HipEvents:
         self.hip.hipEventDestroy.argtypes = [C.c_void_p]
 
     def time(self, stream, fn, reps: int) -> float:
-        """Average milliseconds of fn() over reps launches, measured between two events on `stream`."""
+        """Average milliseconds of fn() over reps launches, measured between two events on `stream`. fn may be a
+        list of launches over distinct buffer sets, called in turn (see MALL_BYTES)."""
+        fns = fn if isinstance(fn, (list, tuple)) else [fn]
         e0, e1 = C.c_void_p(), C.c_void_p()
         assert self.hip.hipEventCreate(C.byref(e0)) == 0 and self.hip.hipEventCreate(C.byref(e1)) == 0
         self.hip.hipEventRecord(e0, stream)
-        for _ in range(reps):
-            fn()
+        for i in range(reps):
+            fns[i % len(fns)]()
         self.hip.hipEventRecord(e1, stream)
         self.hip.hipEventSynchronize(e1)
         ms = C.c_float()
@@ -73,6 +75,17 @@ class HipEvents:
         self.hip.hipEventDestroy(e0)
         self.hip.hipEventDestroy(e1)
         return ms.value / reps
+
+
+# MI355X keeps a 256 MB Infinity Cache (MALL) in front of HBM. A kernel timed over and over on one working set
+# smaller than that reads it from the cache, not from HBM, and can show more than the HBM peak. The HBM-priced
+# timings below therefore cycle through enough distinct buffer sets that every launch finds its operands evicted:
+# sets = ceil(2 * MALL_BYTES / bytes per set).
+MALL_BYTES = 256 << 20
+
+
+def _sets(bytes_per_set: int) -> int:
+    return max(1, -(-2 * MALL_BYTES // bytes_per_set))
 
 
 def _dev_buf(L, ctx, n, value):
@@ -123,17 +136,17 @@ def time_adamw(pkg, model, ev, reps: int = 50):
     L = pkg.load_hip()
     ctx = model.ctx
     n = 28_358_409
-    p, g = _dev_rand(L, ctx, n + 3, 0.05, 3), _dev_rand(L, ctx, n + 3, 1e-3, 4)
-    m, v = _dev_buf(L, ctx, n + 3, 0.0), _dev_buf(L, ctx, n + 3, 0.0)
     ss, sq = C.c_float(), C.c_float()
     L.om_adam_scalars(1e-3, 0.9, 0.999, 1, C.byref(ss), C.byref(sq))
-
-    def launch():
-        L.om_adam_step(ctx, p, g, m, v, None, n, 1e-3, 0.9, 0.999, 1e-8, 0.01, 1, ss, sq)
-
-    for _ in range(3):
-        launch()
-    ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
+    launches = []
+    for k in range(_sets(16 * n)):
+        p, g = _dev_rand(L, ctx, n + 3, 0.05, 3 + 100 * k), _dev_rand(L, ctx, n + 3, 1e-3, 4 + 100 * k)
+        m, v = _dev_buf(L, ctx, n + 3, 0.0), _dev_buf(L, ctx, n + 3, 0.0)
+        launches.append(lambda p=p, g=g, m=m, v=v: L.om_adam_step(ctx, p, g, m, v, None, n, 1e-3, 0.9, 0.999, 1e-8,
+                                                                  0.01, 1, ss, sq))
+    for f in launches:
+        f()
+    ms = ev.time(L.om_ctx_stream(ctx), launches, reps)
     gbs = 28.0 * n / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "kernel": "om_adam_step (C5 arena, 28.36M params)", "achieved": round(gbs, 1),
             "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
@@ -141,24 +154,30 @@ def time_adamw(pkg, model, ev, reps: int = 50):
 
 def time_clip(pkg, model, ev, reps: int = 50):
     """GradClip.ClipNorm on the device over C5's parameter count (28.36M gradients, one segment): the norm alone
-    (partials + final, 4 algorithmic bytes per gradient) and norm + in-place scaling (4 + 8 bytes per gradient)."""
+    (partials + final: g read once, 4 algorithmic bytes per gradient) and norm + in-place scaling (g read and written
+    once, 8 bytes per gradient; the scaling pass's second read of g comes from the Infinity Cache when the gradients
+    fit in it, as C5's 113 MB do)."""
     L = pkg.load_hip()
     ctx = model.ctx
     n = 28_358_409
-    g = _dev_rand(L, ctx, n, 1e-3, 12)
     slot = _dev_buf(L, ctx, 2, 0.0)
-    ptrs, lens = (C.c_void_p * 1)(g.value), (C.c_int64 * 1)(n)
     coef = C.c_void_p(slot.value + 4)
+    tables = []
+    for k in range(_sets(4 * n)):
+        g = _dev_rand(L, ctx, n, 1e-3, 12 + k)
+        tables.append(((C.c_void_p * 1)(g.value), (C.c_int64 * 1)(n)))
     out = {}
-    for name, in_place, per in (("clip_grad_norm", 0, 4.0), ("clip_grad_norm_scale", 1, 12.0)):
-        def launch(in_place=in_place):
-            st = L.om_clip_grad_norm(ctx, 1, C.cast(ptrs, C.c_void_p), C.cast(lens, C.c_void_p), C.c_float(0.5), 0,
-                                     in_place, slot, coef)
+    for name, in_place, per in (("clip_grad_norm", 0, 4.0), ("clip_grad_norm_scale", 1, 8.0)):
+        def launch(ptrs, lens, in_place=in_place):
+            # max_norm below every set's norm, so the in-place variant always runs its scaling pass
+            st = L.om_clip_grad_norm(ctx, 1, C.cast(ptrs, C.c_void_p), C.cast(lens, C.c_void_p), C.c_float(1e-3),
+                                     0, in_place, slot, coef)
             if st != 0:
                 raise RuntimeError(L.om_last_error(ctx).decode())
-        for _ in range(3):
-            launch()
-        ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
+        launches = [lambda t=t: launch(*t) for t in tables]
+        for f in launches:
+            f()
+        ms = ev.time(L.om_ctx_stream(ctx), launches, reps)
         gbs = per * n / (ms * 1e-3) / 1e9
         out[name] = {"bound": "hbm", "kernel": f"om_clip_grad_norm (C5 arena, 28.36M grads, "
                      f"{'norm and in-place scale' if in_place else 'norm only'})", "achieved": round(gbs, 1),
@@ -167,9 +186,9 @@ def time_clip(pkg, model, ev, reps: int = 50):
 
 
 def time_row_kernels(pkg, model, ev, reps: int = 50):
-    """The C3 step's LayerNorm forward/backward (4096 x 384, om_layernorm_bwd including its fp64 column-sum final)
-    and fused attention forward/backward (B 32, H 12, L 128, D 32, padding mask), on random data, HIP events on the
-    model's stream. LayerNorm is priced in algorithmic HBM bytes (forward 8 B/elem + 8 B/row + 8 B/col, backward
+    """The C3 step's LayerNorm forward/backward (4096 x 384, om_layernorm_bwd including its fp64 column-sum final;
+    cycling through buffer sets larger than the Infinity Cache) and fused attention forward/backward (B 32, H 12,
+    L 128, D 32, padding mask), on random data, HIP events on the model's stream. LayerNorm is priced in algorithmic HBM bytes (forward 8 B/elem + 8 B/row + 8 B/col, backward
     12 B/elem + 8 B/row + 12 B/col), attention in MFMA flops (forward 2 products, backward 5, of 2 B H L^2 D)."""
     import numpy as np
     L = pkg.load_hip()
@@ -177,18 +196,24 @@ def time_row_kernels(pkg, model, ev, reps: int = 50):
     st = L.om_ctx_stream(ctx)
     out = {}
     R, Cc = 4096, 384
-    x, g = _dev_rand(L, ctx, R * Cc, 1.0, 5), _dev_rand(L, ctx, R * Cc, 1.0, 6)
     gam, bet = _dev_rand(L, ctx, Cc, 0.1, 7), _dev_rand(L, ctx, Cc, 0.1, 8)
-    y, dx = _dev_buf(L, ctx, R * Cc, 0.0), _dev_buf(L, ctx, R * Cc, 0.0)
-    mu, rs = _dev_buf(L, ctx, R, 0.0), _dev_buf(L, ctx, R, 0.0)
     dg, db = _dev_buf(L, ctx, Cc, 0.0), _dev_buf(L, ctx, Cc, 0.0)
-    fwd = lambda: L.om_layernorm_fwd(ctx, x, gam, bet, y, mu, rs, R, Cc, C.c_float(1e-5))
-    bwd = lambda: L.om_layernorm_bwd(ctx, g, x, gam, mu, rs, dx, dg, db, R, Cc, 0, 0)
-    for name, f, nbytes in (("layernorm_fwd", fwd, 8 * R * Cc + 8 * R + 8 * Cc),
-                            ("layernorm_bwd", bwd, 12 * R * Cc + 8 * R + 12 * Cc)):
-        for _ in range(3):
+    fwds, bwds = [], []
+    for k in range(_sets(16 * R * Cc)):
+        x, g = _dev_rand(L, ctx, R * Cc, 1.0, 5 + 100 * k), _dev_rand(L, ctx, R * Cc, 1.0, 6 + 100 * k)
+        y, dx = _dev_buf(L, ctx, R * Cc, 0.0), _dev_buf(L, ctx, R * Cc, 0.0)
+        mu, rs = _dev_buf(L, ctx, R, 0.0), _dev_buf(L, ctx, R, 0.0)
+        fwds.append(lambda x=x, y=y, mu=mu, rs=rs: L.om_layernorm_fwd(ctx, x, gam, bet, y, mu, rs, R, Cc,
+                                                                      C.c_float(1e-5)))
+        bwds.append(lambda x=x, g=g, dx=dx, mu=mu, rs=rs: L.om_layernorm_bwd(ctx, g, x, gam, mu, rs, dx, dg, db, R,
+                                                                             Cc, 0, 0))
+    for f in fwds:
+        assert f() == 0  # statistics for the backward
+    for name, fs, nbytes in (("layernorm_fwd", fwds, 8 * R * Cc + 8 * R + 8 * Cc),
+                             ("layernorm_bwd", bwds, 12 * R * Cc + 8 * R + 12 * Cc)):
+        for f in fs:
             assert f() == 0
-        ms = ev.time(st, f, reps)
+        ms = ev.time(st, fs, reps)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[name] = {"bound": "hbm", "kernel": f"om_{name} 4096x384", "achieved": round(gbs, 1), "peak": HBM_PEAK,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}

@@ -225,6 +225,43 @@ om_status om_maxpool_fwd(om_ctx *ctx, const float *x, float *y, int32_t *idx, in
                          int KW, int SH, int SW, int PH, int PW);
 om_status om_maxpool_bwd(om_ctx *ctx, const float *g, const int32_t *idx, float *dx, int N, int C, int H, int W,
                          int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW, int accumulate);
+/* Ops.AvgPool2d (Ops.Layers.cs:405-455) over `planes` = N*C planes of H x W: each output is its window's in-order
+ * float sum divided by the window size (counting the zero padding when count_include_pad, else only real pixels);
+ * and AvgPoolBackward (BackwardNn.cs:464-492), each input pixel gathering its windows' shares in the reference's
+ * scatter order. Both bit-exact. Padding at most half the window. */
+om_status om_avgpool2d_fwd(om_ctx *ctx, const float *x, float *y, int planes, int H, int W, int KH, int KW, int SH,
+                           int SW, int PH, int PW, int count_include_pad);
+om_status om_avgpool2d_bwd(om_ctx *ctx, const float *g, float *dx, int planes, int H, int W, int KH, int KW, int SH,
+                           int SW, int PH, int PW, int count_include_pad, int accumulate);
+
+/* ---------------------------------------------------------------------------------------------- normalisation, lookup */
+/* Ops.BatchNorm2d (Ops.Layers.cs:158-246) over x [N, C, plane]. training != 0: batch mean and biased variance in
+ * fp64, saved mean/inv = 1/sqrtf(var + eps) per channel, running statistics updated in place with the unbiased
+ * variance: r = (float)((1 - momentum) * r + momentum * stat); training == 0: mean/inv from the running statistics.
+ * y = ((x - mean) * inv) * gamma + beta. */
+om_status om_batchnorm2d_fwd(om_ctx *ctx, const float *x, const float *gamma, const float *beta, float *running_mean,
+                             float *running_var, float *y, float *mean, float *inv, int N, int C, int plane,
+                             int training, float momentum, float eps);
+/* BatchNormBackward (BackwardNn.cs:244-307) from the saved mean/inv: fp64 per-channel sums of g*xhat and g; dx may
+ * be NULL; dgamma/dbeta may be NULL. */
+om_status om_batchnorm2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                             const float *inv, float *dx, float *dgamma, float *dbeta, int N, int C, int plane,
+                             int training, int acc_dx, int acc_params);
+/* Ops.Embedding, dense (Ops.Layers.cs:549-600): y[i] = table[ids[i]] for n_ids int32 ids in [0, rows) (an id out of
+ * range reads nothing and gives NaN; the host validates ids before they are uploaded); and EmbeddingBackward's
+ * dense branch (BackwardNn.cs:521-540): dtable row r = the sum of g rows of the positions holding r, in increasing
+ * position order (rows never looked up, and padding_index, get 0). Bit-exact. */
+om_status om_embedding_fwd(om_ctx *ctx, const float *table, const int32_t *ids, float *y, int64_t n_ids, int dim,
+                           int rows);
+om_status om_embedding_bwd(om_ctx *ctx, const float *g, const int32_t *ids, float *dtable, int64_t n_ids, int dim,
+                           int rows, int padding_index, int accumulate);
+/* Dropout.Forward in training mode (Layers.cs:341-368): y = x * mask with mask[i] = 1/(1-p) when
+ * (Mix(Mix(seed + draw*G) + (i+1)*G) >> 40) / 2^24 >= p and 0 otherwise (SplitMix64's Mix, G = 0x9E3779B97F4A7C15,
+ * draw = the module's count of masks drawn before this one). The backward (the Mul rule, dx = g * mask) recomputes
+ * the mask from (seed, draw) instead of reading a stored one. p in [0, 1). Bit-exact. */
+om_status om_dropout_fwd(om_ctx *ctx, const float *x, float *y, int64_t n, float p, uint64_t seed, int64_t draw);
+om_status om_dropout_bwd(om_ctx *ctx, const float *g, float *dx, int64_t n, float p, uint64_t seed, int64_t draw,
+                         int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- CTC */
 /* Ops.CtcLoss (CtcLoss.cs:40-153) in double with the reference's exp/ln/logadd (Ctc.cs:515-616); reduction

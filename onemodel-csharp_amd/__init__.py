@@ -90,6 +90,14 @@ _OM_SIGS = {
     "om_adam_step_scaled": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32, vp],
     "om_sgd_step": [vp, vp, vp, vp, i64, f32, f32, f32, f32, ci, ci],
     "om_clip_grad_norm": [vp, ci, vp, vp, f32, ci, ci, vp, vp],
+    "om_avgpool2d_fwd": [vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci],
+    "om_avgpool2d_bwd": [vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci],
+    "om_batchnorm2d_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, f32, f32],
+    "om_batchnorm2d_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci],
+    "om_embedding_fwd": [vp, vp, vp, vp, i64, ci, ci],
+    "om_embedding_bwd": [vp, vp, vp, vp, i64, ci, ci, ci, ci],
+    "om_dropout_fwd": [vp, vp, vp, i64, f32, u64, i64],
+    "om_dropout_bwd": [vp, vp, vp, i64, f32, u64, i64, ci],
     "om_clip_grad_value": [vp, ci, vp, vp, f32],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None}

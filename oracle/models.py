@@ -315,3 +315,130 @@ def mlp_curve(o, steps=None):
         T.backward(loss)
         opt.step()
     return np.array(losses, np.float32), {k: v.data for k, v in P.items()}
+
+
+# ----------------------------------------------------------------------------------------------------------- curves
+class BatchNorm2d(Module):
+    """BatchNorm2d (Layers.cs:119-160): weight 1, bias 0, running mean 0 / variance 1 (buffers), momentum 0.1,
+    eps 1e-5, training mode."""
+
+    def __init__(self, c):
+        super().__init__()
+        self.weight = self.param("weight", np.ones(c, np.float32))
+        self.bias = self.param("bias", np.zeros(c, np.float32))
+        self.running_mean = np.zeros(c, np.float32)
+        self.running_var = np.ones(c, np.float32)
+
+    def __call__(self, x):
+        return T.batch_norm2d(x, self.weight, self.bias, self.running_mean, self.running_var)
+
+
+class Seq(Module):
+    """Sequential (Layers.cs:581-640): children named by position; entries without parameters are plain callables."""
+
+    def __init__(self, *layers):
+        super().__init__()
+        self.layers = layers
+        for i, l in enumerate(layers):
+            if isinstance(l, Module):
+                self.child(str(i), l)
+
+    def __call__(self, x):
+        for l in self.layers:
+            x = l(x)
+        return x
+
+
+class EncoderClassifier(Module):
+    """The encoder classifier of the reference's training-curve test (TrainCase.cs:9-38): Embedding, post-norm
+    encoder layers, mean over the sequence, Linear head."""
+
+    def __init__(self, vocab, width, heads, ff, layers, classes, g):
+        super().__init__()
+        b = 1.7320508
+        self.emb = self.param("emb.weight", g.uniform(-b, b, (vocab, width)))
+        self.layers = [self.child(f"layer{i}", TransformerEncoderLayer(width, heads, ff, g)) for i in range(layers)]
+        self.cls = self.child("cls", Linear(width, classes, g))
+
+    def __call__(self, ids):
+        x = T.embedding(self.emb, ids)
+        for l in self.layers:
+            x = l(x)
+        return self.cls(T.mean_axis(x, 1))
+
+
+def _load(model, o, mapping):
+    named = dict(model.named_parameters())
+    for p, k in mapping:
+        named[p].data[...] = o["in." + k].reshape(named[p].data.shape)
+
+
+CNN_MAP = [("0.weight", "c1w"), ("0.bias", "c1b"), ("1.weight", "bn1g"), ("1.bias", "bn1b"), ("4.weight", "c2w"),
+           ("4.bias", "c2b"), ("5.weight", "bn2g"), ("5.bias", "bn2b"), ("9.weight", "fcw"), ("9.bias", "fcb")]
+
+
+def encoder_map(layers=2):
+    m = [("emb.weight", "emb")]
+    for i in range(layers):
+        for q in "qkvo":
+            m += [(f"layer{i}.attn.{q}.weight", f"l{i}.w{q}"), (f"layer{i}.attn.{q}.bias", f"l{i}.b{q}")]
+        m += [(f"layer{i}.norm1.weight", f"l{i}.ln1g"), (f"layer{i}.norm1.bias", f"l{i}.ln1b"),
+              (f"layer{i}.ff1.weight", f"l{i}.w1"), (f"layer{i}.ff1.bias", f"l{i}.b1"),
+              (f"layer{i}.ff2.weight", f"l{i}.w2"), (f"layer{i}.ff2.bias", f"l{i}.b2"),
+              (f"layer{i}.norm2.weight", f"l{i}.ln2g"), (f"layer{i}.norm2.bias", f"l{i}.ln2b")]
+    return m + [("cls.weight", "clsw"), ("cls.bias", "clsb")]
+
+
+def cnn_curve(o, steps=None):
+    """TrainCase.Cnn (TrainCase.cs:145-183): conv-BN-ReLU-maxpool-conv-BN-ReLU-avgpool-flatten-linear, CE,
+    AdamW(3e-3, wd 0.01) with CosineLr(3e-3, steps) applied before each step and ClipNorm(0.5) after each backward.
+    Returns (losses, gradient norms, final parameters by name, running statistics)."""
+    from . import schedules as S
+    g = T.Generator(2)
+    bn1, bn2 = BatchNorm2d(4), BatchNorm2d(8)
+    model = Seq(Conv2d(1, 4, 3, g, padding=1), bn1, T.relu, lambda x: T.max_pool2d(x, 2, 2)[0],
+                Conv2d(4, 8, 3, g, padding=1), bn2, T.relu, lambda x: T.avg_pool2d(x, 2),
+                lambda x: T.reshape(x, (x.shape[0], -1)), Linear(72, 5, g))
+    _load(model, o, CNN_MAP)
+    n = o["in.order"].shape[0] if steps is None else steps
+    params = model.parameters()
+    opt = T.AdamW(params, lr=3e-3, wd=0.01)
+    sched = S.Cosine(3e-3, o["in.order"].shape[0])
+    x, y, order = o["in.x"], o["in.y"], o["in.order"].astype(np.int64)
+    losses, norms = [], []
+    for i in range(n):
+        idx = order[i]
+        loss = T.cross_entropy(model(T.Tensor(np.ascontiguousarray(x[idx]))), y[idx].astype(np.int32))
+        losses.append(float(loss.data))
+        T.zero_grad(params)
+        T.backward(loss)
+        norms.append(float(T.clip_grad_norm(params, 0.5)[0]))
+        opt.lr = float(sched.lr_at(opt.step_count))
+        opt.step()
+    stats = {"rm1": bn1.running_mean, "rv1": bn1.running_var, "rm2": bn2.running_mean, "rv2": bn2.running_var}
+    return (np.array(losses, np.float32), np.array(norms, np.float32),
+            {k: t.data for k, t in model.named_parameters()}, stats)
+
+
+def encoder_curve(o, steps=None):
+    """TrainCase.Encoder (TrainCase.cs:185-237): EncoderClassifier(vocab 11, width 16, heads 2, ff 32, 2 layers,
+    2 classes), CE, Adam(2e-3) with WarmupLr(ConstantLr(2e-3), 10, 0.1) applied before each step. Returns (losses,
+    final parameters by name)."""
+    from . import schedules as S
+    model = EncoderClassifier(11, 16, 2, 32, 2, 2, T.Generator(3))
+    _load(model, o, encoder_map())
+    params = model.parameters()
+    opt = T.AdamW(params, lr=2e-3, wd=0.0, decoupled=False)
+    sched = S.Warmup(S.Constant(2e-3), 10, 0.1)
+    ids, y, order = o["in.ids"].astype(np.int32), o["in.y"], o["in.order"].astype(np.int64)
+    n = order.shape[0] if steps is None else steps
+    losses = []
+    for i in range(n):
+        idx = order[i]
+        loss = T.cross_entropy(model(np.ascontiguousarray(ids[idx])), y[idx].astype(np.int32))
+        losses.append(float(loss.data))
+        T.zero_grad(params)
+        T.backward(loss)
+        opt.lr = float(sched.lr_at(opt.step_count))
+        opt.step()
+    return np.array(losses, np.float32), {k: t.data for k, t in model.named_parameters()}

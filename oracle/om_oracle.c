@@ -954,3 +954,23 @@ EXPORT void or_clip_value(float *const *grads, const int64_t *lens, int count, f
         }
     }
 }
+
+/* ------------------------------------------------------------------------------------------------ dropout */
+/* Dropout.Forward in training mode (Layers.cs:341-368): stream = Mix(seed + draw * G); element i keeps iff
+ * (Mix(stream + (i + 1) * G) >> 40) * 2^-24 >= p, and out = in * (keep ? 1/(1-p) : 0) (Ops.Mul; the backward's Mul rule
+ * is the same product with g). Mix is SplitMix64's output function (Generator.cs:41-47). */
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+EXPORT void or_dropout(const float *in, float *out, int64_t n, float p, uint64_t seed, int64_t draw) {
+    const uint64_t G = 0x9E3779B97F4A7C15ull;
+    uint64_t stream = mix64(seed + (uint64_t)draw * G);
+    float scale = 1.0f / (1.0f - p);
+    for (int64_t i = 0; i < n; i++) {
+        uint64_t bits = mix64(stream + (uint64_t)(i + 1) * G);
+        float u = (float)(bits >> 40) * (1.0f / 16777216.0f);
+        out[i] = in[i] * (u >= p ? scale : 0.0f);
+    }
+}

@@ -519,6 +519,24 @@ def embedding(table: Tensor, ids: np.ndarray, pad=-1) -> Tensor:
     return _attach(y, [table], rule)
 
 
+def dropout(x: Tensor, p: float, seed: int, draw: int) -> Tensor:
+    """Dropout.Forward in training mode (Layers.cs:341-368) as Ops.Mul(x, mask), backward g * mask; the caller keeps
+    the module's draw counter. p == 0 returns x itself, as the reference does."""
+    if p == 0.0:
+        return x
+    xv = c32(x.data)
+    y = np.empty_like(xv)
+    lib().or_dropout(fp(xv), fp(y), ctypes.c_int64(xv.size), ctypes.c_float(p), ctypes.c_uint64(seed),
+                     ctypes.c_int64(draw))
+
+    def rule(g):
+        dx = np.empty_like(xv)
+        lib().or_dropout(fp(c32(g)), fp(dx), ctypes.c_int64(xv.size), ctypes.c_float(p), ctypes.c_uint64(seed),
+                         ctypes.c_int64(draw))
+        return [dx]
+    return _attach(y, [x], rule)
+
+
 CTC_NONE, CTC_MEAN, CTC_SUM = 0, 1, 2
 
 

@@ -365,3 +365,67 @@ def test_fd_ctc(oracle):
             out = T.ctc_loss(T.log_softmax(t[0]), [1, 2, 2, 3, 1, 1], [7, 6, 4], [2, 3, 1], 0, red)
             return out if out.data.ndim else T.reshape(out, (1,))
         gradcheck(T, f, [z])
+
+
+def test_cnn_training_curve(oracle):
+    """TrainingCurveTests.ConvNetAdamWCosineClipMatchesTorch (TrainingCurveTests.cs:100-124): losses and final
+    parameters 1e-3, gradient norms 1e-3 relative with clipping engaged, running variance 1e-3; the zero-gradient
+    conv biases in front of batch norm (0.bias, 4.bias) are noise, as the reference reports them."""
+    from oracle import models
+    o = load_golden("training_cnn")
+    losses, norms, final, stats = models.cnn_curve(o)
+    want = o["out.loss"]
+    assert np.max(np.abs(losses.astype(np.float64) - want) / np.abs(want)) <= 1e-3
+    for p, k in models.CNN_MAP:
+        if p in ("0.bias", "4.bias"):
+            continue
+        assert scaled(final[p], o["out." + k]) <= 1e-3, p
+    wn = o["out.gradnorm"]
+    assert np.max(np.abs(norms.astype(np.float64) - wn) / wn) < 1e-3
+    assert int(np.sum(wn > 0.5)) > 5
+    assert scaled(stats["rv2"], o["out.rv2"]) < 1e-3
+    assert losses[-1] < losses[0]
+
+
+def test_encoder_training_curve(oracle):
+    """TrainingCurveTests.TransformerAdamWarmupMatchesTorch (TrainingCurveTests.cs:126-128): losses and final
+    parameters 1e-3 (the attention key biases, zero-gradient in theory, reported apart)."""
+    from oracle import models
+    o = load_golden("training_encoder")
+    losses, final = models.encoder_curve(o)
+    want = o["out.loss"]
+    assert np.max(np.abs(losses.astype(np.float64) - want) / np.abs(want)) <= 1e-3
+    for p, k in models.encoder_map():
+        if p.endswith("attn.k.bias"):
+            continue
+        assert scaled(final[p], o["out." + k]) <= 1e-3, p
+    assert losses[-1] < losses[0]
+
+
+def test_dropout_mask_is_the_generator_stream(oracle):
+    """Dropout's mask (Layers.cs:341-368) is the pinned SplitMix64 Generator read from state Mix(seed + draw*G):
+    element i keeps iff that generator's (i+1)-th NextSingle is >= p; plus the reference's own properties
+    (ModuleAndLossTests.cs:62-100): about p dropped, kept values scaled by exactly 1/(1-p), draws give new masks."""
+    T = oracle
+    G = 0x9E3779B97F4A7C15
+    M = (1 << 64) - 1
+    n, p = 1000, 0.3
+    x = np.ones(n, np.float32)
+    masks = []
+    for draw in (0, 1, 5):
+        y = T.dropout(T.Tensor(x), p, 42, draw).data
+        stream = T.Generator((42 + draw * G - G) & M).next_u64()  # = Mix(seed + draw*G)
+        u = T.Generator(stream).uniform(0.0, 1.0, (n,))
+        keep = u >= np.float32(p)
+        assert np.array_equal(y != 0, keep)
+        assert np.all(y[keep] == np.float32(1.0) / np.float32(1.0 - np.float32(p)))
+        masks.append(keep)
+        if draw == 0:
+            assert 240 <= int(np.sum(~keep)) <= 360
+    assert not np.array_equal(masks[0], masks[1])
+    # backward: g * mask with the same mask (DropoutBackwardUsesTheMask)
+    X = T.Tensor(np.full(64, 2.0, np.float32), requires_grad=True)
+    Y = T.dropout(X, 0.5, 7, 0)
+    T.backward(T.sum_all(Y))
+    assert np.array_equal(X.grad, np.where(Y.data == 0, 0.0, 2.0).astype(np.float32))
+    assert T.dropout(X, 0.0, 7, 0) is X
