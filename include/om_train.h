@@ -30,7 +30,11 @@ typedef struct {
 /* Builds configuration `cfg` (1 = MLP 784-256-10, 2 = conv block, 3 = MiniLM-shaped pre-LN block, 4 = CRNN + CTC,
  * 5 = BERT-base-shaped 4-layer stack) on `device`: parameters from the SplitMix64 generator in registration order
  * (Kaiming-uniform +-1/sqrt(fan_in), LayerNorm 1/0), synthetic inputs from seed 20261201 + 100*cfg + index, and an
- * AdamW(lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0.01) over the parameter arena. */
+ * AdamW(lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0.01) over the parameter arena.
+ * Configurations 6-8 are the models of the reference's training-curve tests (TrainCase.cs:114-237), whose batches
+ * the caller supplies each step with omt_input_write: 6 = MLP 20-32-4 with SGD(0.05, momentum 0.9, wd 1e-4);
+ * 7 = conv/BatchNorm/pool net with AdamW(3e-3, wd 0.01), CosineLr(3e-3, 60) and ClipNorm(0.5) inside omt_step;
+ * 8 = Embedding + 2 post-norm encoder layers + mean + Linear with Adam(2e-3) and WarmupLr(ConstantLr(2e-3), 10, 0.1). */
 om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out);
 void omt_destroy(omt_model *m);
 const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */
@@ -59,6 +63,25 @@ om_status omt_input_info(omt_model *m, int i, char *name, int name_cap, int *is_
 om_status omt_input_read(omt_model *m, int i, void *host, int64_t numel);
 /* Gradient of an input that requires one (C2's image), after a backward. */
 om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel);
+/* Replaces input i with numel host values (float, or int32 for an int input, which must lie in the range the
+ * model accepts: labels below the class count, ids below the vocabulary), uploaded on the model's stream ahead of
+ * the next step: the per-step batch of a training loop (TrainCase.cs:77-96 builds its batches on the host). */
+om_status omt_input_write(omt_model *m, int i, const void *host, int64_t numel);
+
+/* Named float state buffers that are not parameters (NnModule.RegisterBuffer, NnModule.cs:54-65): BatchNorm2d's
+ * running_mean and running_var, in named_buffers() order ("1.running_mean", ...). */
+int omt_buffer_count(omt_model *m);
+om_status omt_buffer_info(omt_model *m, int i, char *name, int name_cap, int64_t *numel);
+om_status omt_buffer_read(omt_model *m, int i, float *host, int64_t numel);
+om_status omt_buffer_write(omt_model *m, int i, const float *host, int64_t numel);
+
+/* Replaces the model's optimizer with a new one over Parameters() (fresh state: zero moments and momentum buffers,
+ * step count 0): kind 0 = Sgd(lr, momentum, dampening, weight_decay, nesterov) (Optimizers.cs:270-330), 1 = Adam
+ * (L2 weight decay added to g), 2 = AdamW (decoupled decay) (Optimizers.cs:374-608), with betas, eps and amsgrad.
+ * Arguments the reference rejects return OM_E_ARG. Configurations 1-5 default to AdamW(1e-3, 0.9, 0.999, 1e-8, 0.01);
+ * 6-8 to the optimizers of the reference's training-curve cases (omt_config_create). */
+om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float beta2, float eps, float weight_decay,
+                            float momentum, float dampening, int nesterov, int amsgrad);
 
 /* Host helper with no device: the SplitMix64 generator of the tape (for cross-checks against the reference's
  * Generator): kind 0 = uniform [lo, hi), 1 = benchmark normal, 2 = ints in [lo, hi). */

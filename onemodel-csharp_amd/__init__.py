@@ -156,6 +156,12 @@ _OMT_SIGS = {
     "omt_input_read": ([vp, ci, vp, i64], i32),
     "omt_input_grad": ([vp, ci, vp, i64], i32),
     "omt_generate": ([u64, ci, f32, f32, vp, i64], None),
+    "omt_input_write": ([vp, ci, vp, i64], i32),
+    "omt_buffer_count": ([vp], ci),
+    "omt_buffer_info": ([vp, ci, C.c_char_p, ci, C.POINTER(i64)], i32),
+    "omt_buffer_read": ([vp, ci, vp, i64], i32),
+    "omt_buffer_write": ([vp, ci, vp, i64], i32),
+    "omt_set_optimizer": ([vp, ci, f32, f32, f32, f32, f32, f32, f32, ci, ci], i32),
     "omt_lr": ([vp], f32),
     "omt_set_lr": ([vp, f32], i32),
     "omt_lr_constant": ([f32, C.POINTER(vp)], i32),
@@ -271,6 +277,40 @@ class Model:
             self._check(self.L.omt_input_read(self.h, i, a.ctypes.data, a.size), "omt_input_read")
             out[name.value.decode()] = a
         return out
+
+    def write_input(self, name, values):
+        """Uploads a new value for a named input (the next step's batch)."""
+        np = self.np
+        names = [self._input_name(i) for i in range(self.L.omt_input_count(self.h))]
+        i = names.index(name)
+        a = np.ascontiguousarray(values)
+        a = a.astype(np.int32 if a.dtype.kind in "iu" else np.float32, copy=False)
+        self._check(self.L.omt_input_write(self.h, i, a.ctypes.data, a.size), "omt_input_write")
+
+    def _input_name(self, i):
+        name = C.create_string_buffer(64)
+        self._check(self.L.omt_input_info(self.h, i, name, 64, None, None, None), "omt_input_info")
+        return name.value.decode()
+
+    def buffers(self):
+        """{name: numpy array} of the model's state buffers (BatchNorm running statistics)."""
+        np = self.np
+        out = {}
+        for i in range(self.L.omt_buffer_count(self.h)):
+            name = C.create_string_buffer(256)
+            n = i64()
+            self._check(self.L.omt_buffer_info(self.h, i, name, 256, C.byref(n)), "omt_buffer_info")
+            a = np.empty(n.value, np.float32)
+            self._check(self.L.omt_buffer_read(self.h, i, a.ctypes.data, a.size), "omt_buffer_read")
+            out[name.value.decode()] = a
+        return out
+
+    def set_optimizer(self, kind, lr, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.0, momentum=0.0,
+                      dampening=0.0, nesterov=False, amsgrad=False):
+        """kind: "sgd", "adam" or "adamw" (a fresh optimizer over Parameters())."""
+        k = {"sgd": 0, "adam": 1, "adamw": 2}[kind]
+        self._check(self.L.omt_set_optimizer(self.h, k, lr, beta1, beta2, eps, weight_decay, momentum, dampening,
+                                             int(nesterov), int(amsgrad)), "omt_set_optimizer")
 
     def input_grad(self, name):
         np = self.np

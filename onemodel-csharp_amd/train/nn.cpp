@@ -1,4 +1,5 @@
 // Modules, the parameter arena, optimizers, the benchmark configurations and the C ABI of include/om_train.h.
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -50,6 +51,18 @@ void Module::named_parameters(std::vector<std::pair<std::string, Tensor>> &out, 
     for (auto &p : params_) out.emplace_back(prefix + p.first, p.second);
     for (auto &c : children_) c.second->named_parameters(out, prefix + c.first + ".");
 }
+float *Module::buffer(const std::string &name, const std::vector<float> &init) {
+    const uint64_t bytes = sizeof(float) * (init.empty() ? 1 : init.size());
+    float *d = (float *)dev().persistent(bytes);
+    if (!init.empty()) check(dev().ctx(), om_upload(dev().ctx(), d, init.data(), bytes), "buffer upload");
+    buffers_.emplace_back(name, std::make_pair(d, (int64_t)init.size()));
+    return d;
+}
+void Module::named_buffers(std::vector<std::pair<std::string, std::pair<float *, int64_t>>> &out,
+                           const std::string &prefix) const {
+    for (auto &b : buffers_) out.emplace_back(prefix + b.first, b.second);
+    for (auto &c : children_) c.second->named_buffers(out, prefix + c.first + ".");
+}
 void Module::colocation_groups(std::vector<std::vector<Tensor>> &out) const {
     for (auto &g : colocate_) out.push_back(g);
     for (auto &c : children_) c.second->colocation_groups(out);
@@ -75,6 +88,22 @@ Conv2d::Conv2d(int cin, int cout, int k, Generator &g, int padding, int stride_)
     g.fill_uniform(-bd, bd, bv);
     w = param("weight", {cout, cin, k, k}, std::move(wv));
     b = param("bias", {cout}, std::move(bv));
+}
+BatchNorm2d::BatchNorm2d(int c, float momentum_, float eps_) : momentum(momentum_), eps(eps_) {
+    if (c < 1) throw Error(OM_E_ARG, "BatchNorm2d needs at least one channel");
+    w = param("weight", {c}, std::vector<float>(c, 1.0f));
+    b = param("bias", {c}, std::vector<float>(c, 0.0f));
+    rm = buffer("running_mean", std::vector<float>(c, 0.0f));
+    rv = buffer("running_var", std::vector<float>(c, 1.0f));
+}
+Embedding::Embedding(int count, int width, Generator &g, int padding_index) : pad(padding_index) {
+    if (count < 1 || width < 1) throw Error(OM_E_ARG, "Embedding needs at least one id and one column");
+    std::vector<float> v((size_t)count * width);
+    g.fill_uniform(-1.7320508f, 1.7320508f, v);  // Init.Uniform(g, sqrt(3), count, width), Layers.cs:11-21
+    w = param("weight", {count, width}, std::move(v));
+}
+Dropout::Dropout(float p_, uint64_t seed_) : p(p_), seed(seed_) {
+    if (!(p >= 0.0f && p < 1.0f)) throw Error(OM_E_ARG, "Dropout probability must be in [0, 1).");
 }
 LayerNorm::LayerNorm(int n, float eps_) : eps(eps_) {
     w = param("weight", {n}, std::vector<float>(n, 1.0f));  // Layers.cs:255-262
@@ -146,7 +175,14 @@ struct Input {
     std::vector<float> hf;       // host copy (float inputs)
     std::vector<int32_t> hi;     // host copy (int inputs)
     bool is_int = false;
+    int32_t lo = INT32_MIN, hi_bound = INT32_MAX;  // int inputs: the values the model accepts, [lo, hi_bound)
+    void set_range(int32_t l, int32_t h) {
+        lo = l;
+        hi_bound = h;
+    }
 };
+
+enum { OPT_SGD = 0, OPT_ADAM = 1, OPT_ADAMW = 2 };
 
 struct omt_model {
     std::unique_ptr<Device> device;
@@ -158,9 +194,16 @@ struct omt_model {
     int64_t total = 0;
     float *pb = nullptr, *gb = nullptr, *mb = nullptr, *vb = nullptr;
     std::vector<Input> inputs;
+    std::vector<std::pair<std::string, std::pair<float *, int64_t>>> buffers;  // named_buffers() order
     std::function<Tensor(omt_model &)> loss_fn;
-    // AdamW hyper-parameters
+    // Optimizer (Optimizers.cs): kind OPT_SGD, OPT_ADAM (L2 weight decay) or OPT_ADAMW (decoupled); the benchmark
+    // configurations use AdamW(lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0.01).
+    int opt_kind = OPT_ADAMW;
     float lr = 1e-3f, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, wd = 0.01f;
+    float momentum = 0.0f, dampening = 0.0f;
+    bool nesterov = false, amsgrad = false;
+    float *vmaxb = nullptr;            // AMSGrad's running maximum of v (allocated when first asked for)
+    std::vector<char> sgd_started;     // per parameter: its momentum buffer holds a value (Sgd starts it from g)
     int64_t step_count = 0;
     std::unique_ptr<LrSchedule> schedule;  // LrSchedule.Apply before every step when set
     float clip_max = 0.0f;                 // ClipNorm inside omt_step when > 0
@@ -211,6 +254,7 @@ struct omt_model {
     // gradients, first and second moments; uploads the initial values once.
     void finalize(std::vector<std::vector<float>> &&init) {
         root->named_parameters(params);
+        root->named_buffers(buffers);
         std::vector<std::vector<Tensor>> groups;
         root->colocation_groups(groups);
         // Physical order: Parameters() order, except that a colocation group is placed whole where its first member
@@ -261,6 +305,7 @@ struct omt_model {
             t->grad = gb + offset[i];
             leaves.insert(leaves.begin() + (long)i, t);
         }
+        sgd_started.assign(params.size(), 0);
         clip_buf = (float *)device->persistent(16);
         check(c, om_fill(c, clip_buf, std::nanf(""), 4), "clip slot");
         check(c, om_upload(c, pb, host.data(), bytes), "upload params");
@@ -291,28 +336,96 @@ struct omt_model {
         return runs;
     }
 
-    // AdamW.Step (Optimizers.cs:184-219, 501-589): LrSchedule.Apply when a schedule is attached, the rate check,
-    // BeginStep scalars on the host, then one fused update per run of parameters that have gradients (a parameter
-    // without one is skipped, as in the reference). grad_scale: ClipNorm's device coefficient, folded into the read
-    // of g (om_adam_step_scaled), or NULL.
+    // Optimizer.Step (Optimizers.cs:184-219): LrSchedule.Apply when a schedule is attached, the rate check, then
+    // one fused update per run of parameters that have gradients (a parameter without one is skipped, as in the
+    // reference). Adam/AdamW: BeginStep scalars on the host (Optimizers.cs:501-508), UpdateRange on the device;
+    // grad_scale is ClipNorm's device coefficient folded into the read of g (om_adam_step_scaled), or NULL.
+    // SGD (class Sgd): runs are split where the momentum buffers' started state changes.
     void optimizer_step(const float *grad_scale = nullptr) {
         settle_grads(leaves);
         if (schedule) lr = schedule->lr_at(step_count);
         if (!std::isfinite(lr) || lr < 0.0f) throw Error(OM_E_ARG, "learning rate must be finite and not negative");
+        om_ctx *c = device->ctx();
+        if (opt_kind == OPT_SGD) {
+            if (grad_scale) throw Error(OM_E_STATE, "SGD takes in-place clipped gradients");
+            sgd_step();
+            step_count++;
+            return;
+        }
         float ss, sq;
         om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
-        om_ctx *c = device->ctx();
+        const int dec = opt_kind == OPT_ADAMW ? 1 : 0;
         for (auto [beg, n] : live_runs()) {
+            float *vm = amsgrad ? vmaxb + beg : nullptr;
             if (grad_scale)
-                check(c, om_adam_step_scaled(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, n, lr, beta1, beta2,
-                                             eps, wd, 1, ss, sq, grad_scale),
+                check(c, om_adam_step_scaled(c, pb + beg, gb + beg, mb + beg, vb + beg, vm, n, lr, beta1, beta2, eps,
+                                             wd, dec, ss, sq, grad_scale),
                       "om_adam_step_scaled");
             else
-                check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, nullptr, n, lr, beta1, beta2, eps,
-                                      wd, 1, ss, sq),
+                check(c, om_adam_step(c, pb + beg, gb + beg, mb + beg, vb + beg, vm, n, lr, beta1, beta2, eps, wd,
+                                      dec, ss, sq),
                       "om_adam_step");
         }
         step_count++;
+    }
+    void sgd_step() {
+        om_ctx *c = device->ctx();
+        const bool buf = momentum != 0.0f;
+        size_t i = 0;
+        while (i < phys.size()) {
+            const Tensor &t = params[phys[i]].second;
+            if (!(t->grad_exists && t->requires_grad)) {
+                i++;
+                continue;
+            }
+            const bool first = buf && !sgd_started[phys[i]];
+            size_t j = i;
+            while (j + 1 < phys.size()) {
+                const Tensor &u = params[phys[j + 1]].second;
+                if (!(u->grad_exists && u->requires_grad) || (buf && !sgd_started[phys[j + 1]]) != first) break;
+                j++;
+            }
+            const int64_t beg = offset[phys[i]], n = offset[phys[j]] + params[phys[j]].second->numel - beg;
+            check(c, om_sgd_step(c, pb + beg, gb + beg, buf ? mb + beg : nullptr, n, lr, momentum, dampening, wd,
+                                 nesterov ? 1 : 0, first ? 1 : 0),
+                  "om_sgd_step");
+            for (size_t q = i; q <= j; q++) sgd_started[phys[q]] = 1;
+            i = j + 1;
+        }
+    }
+    // A new optimizer over Parameters() (its state starts empty: moments and momentum buffers zero, step count 0).
+    void set_optimizer(int kind, float lr_, float b1, float b2, float eps_, float wd_, float mom, float damp,
+                       bool nest, bool ams) {
+        auto finite_nonneg = [](float v) { return std::isfinite(v) && v >= 0.0f; };
+        if (kind != OPT_SGD && kind != OPT_ADAM && kind != OPT_ADAMW) throw Error(OM_E_ARG, "unknown optimizer kind");
+        if (!finite_nonneg(lr_) || !finite_nonneg(wd_)) throw Error(OM_E_ARG, "rate and weight decay must be finite and not negative");
+        if (kind == OPT_SGD) {
+            if (!finite_nonneg(mom) || !finite_nonneg(damp)) throw Error(OM_E_ARG, "momentum and dampening must be finite and not negative");
+            if (nest && (mom <= 0.0f || damp != 0.0f))
+                throw Error(OM_E_ARG, "Nesterov momentum needs a positive momentum and zero dampening");
+        } else {
+            if (!(b1 >= 0.0f && b1 < 1.0f) || !(b2 >= 0.0f && b2 < 1.0f)) throw Error(OM_E_ARG, "betas must be in [0, 1)");
+            if (!(eps_ > 0.0f) || !std::isfinite(eps_)) throw Error(OM_E_ARG, "epsilon must be positive and finite");
+        }
+        opt_kind = kind;
+        lr = lr_;
+        beta1 = b1;
+        beta2 = b2;
+        eps = eps_;
+        wd = wd_;
+        momentum = kind == OPT_SGD ? mom : 0.0f;
+        dampening = kind == OPT_SGD ? damp : 0.0f;
+        nesterov = kind == OPT_SGD && nest;
+        amsgrad = kind != OPT_SGD && ams;
+        om_ctx *c = device->ctx();
+        const uint64_t bytes = sizeof(float) * (uint64_t)(total > 0 ? total : 4);
+        if (amsgrad && !vmaxb) vmaxb = (float *)device->persistent(bytes);
+        check(c, om_zero(c, mb, bytes), "zero moments");
+        check(c, om_zero(c, vb, bytes), "zero moments");
+        if (vmaxb) check(c, om_zero(c, vmaxb, bytes), "zero moments");
+        sgd_started.assign(params.size(), 0);
+        step_count = 0;
+        device->sync();
     }
 
     // GradClip.ClipNorm / ClipValue over Parameters() (Schedules.cs:22-149) on the device; the norm and the
@@ -357,8 +470,10 @@ struct omt_model {
         Tensor loss = loss_fn(*this);
         backward(loss);
         if (clip_max > 0.0f) {
-            clip_norm(clip_max, clip_inf, false);
-            optimizer_step(clip_buf + 1);
+            // Adam/AdamW read the coefficient in their update; SGD gets the gradients scaled in place
+            const bool fold = opt_kind != OPT_SGD;
+            clip_norm(clip_max, clip_inf, !fold);
+            optimizer_step(fold ? clip_buf + 1 : nullptr);
         } else {
             optimizer_step();
         }
@@ -488,6 +603,95 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
             for (EncoderLayer *l : mp->layers) h = (*l)(h, nullptr);
             return cross_entropy(reshape((*mp->head)(h), {B * L, 9}), s.input("labels").t);
         };
+    } else if (cfg == 6) {
+        // TrainCase.Mlp (TrainCase.cs:114-143): Linear(20,32) - ReLU - Linear(32,4), CE, SGD(0.05, momentum 0.9,
+        // weight decay 1e-4); the batches come from the caller (omt_input_write) each step.
+        const int B = pick(sc.batch, 32);
+        Generator gm(1);
+        struct Mlp : Module {
+            Linear *l1, *l2;
+        };
+        auto m = std::make_unique<Mlp>();
+        m->l1 = m->child("0", std::make_unique<Linear>(20, 32, gm));
+        m->l2 = m->child("2", std::make_unique<Linear>(32, 4, gm));
+        Mlp *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, 20}, std::vector<float>((size_t)B * 20, 0.0f), false);
+        M.add_int_input("labels", {B}, std::vector<int32_t>(B, 0)).set_range(0, 4);
+        M.loss_fn = [mp](omt_model &s) {
+            return cross_entropy((*mp->l2)(relu((*mp->l1)(s.input("x").t))), s.input("labels").t);
+        };
+        M.opt_kind = OPT_SGD;
+        M.lr = 0.05f;
+        M.momentum = 0.9f;
+        M.wd = 1e-4f;
+    } else if (cfg == 7) {
+        // TrainCase.Cnn (TrainCase.cs:145-183): Conv(1,4,3,p1) BN ReLU MaxPool(2) Conv(4,8,3,p1) BN ReLU AvgPool(2)
+        // Flatten Linear(72,5), CE, AdamW(3e-3, wd 0.01), CosineLr(3e-3, 60) and ClipNorm(0.5) every step.
+        const int B = pick(sc.batch, 8);
+        Generator gm(2);
+        struct Cnn : Module {
+            Conv2d *c1, *c2;
+            BatchNorm2d *bn1, *bn2;
+            Linear *fc;
+        };
+        auto m = std::make_unique<Cnn>();
+        m->c1 = m->child("0", std::make_unique<Conv2d>(1, 4, 3, gm, 1));
+        m->bn1 = m->child("1", std::make_unique<BatchNorm2d>(4));
+        m->c2 = m->child("4", std::make_unique<Conv2d>(4, 8, 3, gm, 1));
+        m->bn2 = m->child("5", std::make_unique<BatchNorm2d>(8));
+        m->fc = m->child("9", std::make_unique<Linear>(72, 5, gm));
+        Cnn *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, 1, 12, 12}, std::vector<float>((size_t)B * 144, 0.0f), false);
+        M.add_int_input("labels", {B}, std::vector<int32_t>(B, 0)).set_range(0, 5);
+        M.loss_fn = [mp, B](omt_model &s) {
+            Tensor h = max_pool2d(relu((*mp->bn1)((*mp->c1)(s.input("x").t))), 2, 2, 2, 2);
+            h = avg_pool2d(relu((*mp->bn2)((*mp->c2)(h))), 2, 2, 0);
+            return cross_entropy((*mp->fc)(reshape(h, {B, 72})), s.input("labels").t);
+        };
+        M.opt_kind = OPT_ADAMW;
+        M.lr = 3e-3f;
+        M.wd = 0.01f;
+        omt_lr_schedule *cs = nullptr;
+        check(nullptr, omt_lr_cosine(3e-3f, 60, 0.0f, &cs), "CosineLr");
+        M.schedule = std::move(cs->s);
+        omt_lr_free(cs);
+        M.clip_max = 0.5f;
+    } else if (cfg == 8) {
+        // TrainCase.Encoder (TrainCase.cs:185-237): EncoderClassifier(vocab 11, width 16, 2 heads, FFN 32, 2 post-norm
+        // layers, 2 classes) = Embedding, layers, Mean over the sequence, Linear; CE; Adam(2e-3);
+        // WarmupLr(ConstantLr(2e-3), 10, 0.1).
+        const int B = pick(sc.batch, 16), L = pick(sc.seq, 6), NL = pick(sc.layers, 2);
+        Generator gm(3);
+        struct Classifier : Module {
+            Embedding *emb;
+            std::vector<EncoderLayer *> layers;
+            Linear *cls;
+        };
+        auto m = std::make_unique<Classifier>();
+        m->emb = m->child("emb", std::make_unique<Embedding>(11, 16, gm));
+        for (int i = 0; i < NL; i++)
+            m->layers.push_back(m->child("layer" + std::to_string(i), std::make_unique<EncoderLayer>(16, 2, 32, gm)));
+        m->cls = m->child("cls", std::make_unique<Linear>(16, 2, gm));
+        Classifier *mp = m.get();
+        M.root = std::move(m);
+        M.add_int_input("ids", {B, L}, std::vector<int32_t>((size_t)B * L, 0)).set_range(0, 11);
+        M.add_int_input("labels", {B}, std::vector<int32_t>(B, 0)).set_range(0, 2);
+        M.loss_fn = [mp](omt_model &s) {
+            Tensor h = (*mp->emb)(s.input("ids").t);
+            for (EncoderLayer *l : mp->layers) h = (*l)(h, nullptr);
+            return cross_entropy((*mp->cls)(mean_axis(h, 1)), s.input("labels").t);
+        };
+        M.opt_kind = OPT_ADAM;
+        M.lr = 2e-3f;
+        M.wd = 0.0f;
+        omt_lr_schedule *cs = nullptr, *ws = nullptr;
+        check(nullptr, omt_lr_constant(2e-3f, &cs), "ConstantLr");
+        check(nullptr, omt_lr_warmup(cs, 10, 0.1f, &ws), "WarmupLr");
+        M.schedule = std::move(ws->s);
+        omt_lr_free(ws);
+        omt_lr_free(cs);
     } else {
         throw Error(OM_E_ARG, "unknown configuration " + std::to_string(cfg));
     }
@@ -656,6 +860,42 @@ om_status omt_param_write(omt_model *m, int i, int which, const float *host, int
 }
 int64_t omt_step_count(omt_model *m) { return m ? m->step_count : -1; }
 
+om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float beta2, float eps, float weight_decay,
+                            float momentum, float dampening, int nesterov, int amsgrad) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        m->set_optimizer(kind, lr, beta1, beta2, eps, weight_decay, momentum, dampening, nesterov != 0, amsgrad != 0);
+    });
+}
+
+int omt_buffer_count(omt_model *m) { return m ? (int)m->buffers.size() : 0; }
+om_status omt_buffer_info(omt_model *m, int i, char *name, int cap, int64_t *numel) {
+    if (!m || i < 0 || i >= (int)m->buffers.size()) return OM_E_ARG;
+    if (name && cap > 0) {
+        std::strncpy(name, m->buffers[i].first.c_str(), (size_t)cap - 1);
+        name[cap - 1] = 0;
+    }
+    if (numel) *numel = m->buffers[i].second.second;
+    return OM_OK;
+}
+om_status omt_buffer_read(omt_model *m, int i, float *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->buffers.size() || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        if (numel != m->buffers[i].second.second) throw Error(OM_E_ARG, "omt_buffer_read: wrong element count");
+        check(m->device->ctx(), om_download(m->device->ctx(), host, m->buffers[i].second.first,
+                                            sizeof(float) * (uint64_t)numel), "download");
+    });
+}
+om_status omt_buffer_write(omt_model *m, int i, const float *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->buffers.size() || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        if (numel != m->buffers[i].second.second) throw Error(OM_E_ARG, "omt_buffer_write: wrong element count");
+        check(m->device->ctx(), om_upload(m->device->ctx(), m->buffers[i].second.first, host,
+                                          sizeof(float) * (uint64_t)numel), "upload");
+        m->device->sync();
+    });
+}
+
 int omt_input_count(omt_model *m) { return m ? (int)m->inputs.size() : 0; }
 om_status omt_input_info(omt_model *m, int i, char *name, int cap, int *is_int, int *ndim, int32_t *dims) {
     if (!m || i < 0 || i >= (int)m->inputs.size()) return OM_E_ARG;
@@ -677,6 +917,27 @@ om_status omt_input_read(omt_model *m, int i, void *host, int64_t numel) {
     if (in.is_int) std::memcpy(host, in.hi.data(), sizeof(int32_t) * (size_t)numel);
     else std::memcpy(host, in.hf.data(), sizeof(float) * (size_t)numel);
     return OM_OK;
+}
+om_status omt_input_write(omt_model *m, int i, const void *host, int64_t numel) {
+    if (!m || i < 0 || i >= (int)m->inputs.size() || !host) return OM_E_ARG;
+    return guard(m, [&] {
+        Input &in = m->inputs[i];
+        if (numel != in.t->numel) throw Error(OM_E_ARG, "omt_input_write: wrong element count for " + in.name);
+        if (in.is_int) {
+            const int32_t *v = static_cast<const int32_t *>(host);
+            for (int64_t k = 0; k < numel; k++)
+                if (v[k] < in.lo || v[k] >= in.hi_bound)
+                    throw Error(OM_E_ARG, "omt_input_write: " + in.name + "[" + std::to_string(k) + "] = " +
+                                              std::to_string(v[k]) + " is out of range");
+            std::memcpy(in.hi.data(), v, sizeof(int32_t) * (size_t)numel);
+            check(m->device->ctx(), om_upload(m->device->ctx(), in.t->idata, v, sizeof(int32_t) * (uint64_t)numel),
+                  "upload");
+        } else {
+            std::memcpy(in.hf.data(), host, sizeof(float) * (size_t)numel);
+            check(m->device->ctx(), om_upload(m->device->ctx(), in.t->data, host, sizeof(float) * (uint64_t)numel),
+                  "upload");
+        }
+    });
 }
 om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel) {
     if (!m || i < 0 || i >= (int)m->inputs.size() || !host) return OM_E_ARG;

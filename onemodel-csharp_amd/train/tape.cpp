@@ -687,4 +687,79 @@ Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std
     return loss;
 }
 
+Tensor avg_pool2d(const Tensor &x, int k, int s, int p, bool count_include_pad) {
+    if (x->shape.size() != 4) shape_error("AvgPool2d needs an (N,C,H,W) input, not " + shape_str(x->shape));
+    const int N = x->shape[0], Cc = x->shape[1], H = x->shape[2], W = x->shape[3];
+    const int OH = (H + 2 * p - k) / s + 1, OW = (W + 2 * p - k) / s + 1;
+    Tensor y = make({N, Cc, OH, OW});
+    const int cip = count_include_pad ? 1 : 0;
+    OMT(om_avgpool2d_fwd(C(), x->data, y->data, N * Cc, H, W, k, k, s, s, p, p, cip));
+    if (tracked({&x}))
+        attach(y, "AvgPool2d", {x}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_avgpool2d_bwd(C(), g, dx, N * Cc, H, W, k, k, s, s, p, p, cip, a));
+        });
+    return y;
+}
+
+Tensor batch_norm2d(const Tensor &x, const Tensor &gamma, const Tensor &beta, float *running_mean,
+                    float *running_var, bool training, float momentum, float eps) {
+    if (x->shape.size() != 4) shape_error("BatchNorm2d needs an (N,C,H,W) input, not " + shape_str(x->shape));
+    const int N = x->shape[0], Cc = x->shape[1], plane = x->shape[2] * x->shape[3];
+    if (gamma->numel != Cc || beta->numel != Cc)
+        shape_error("BatchNorm2d over " + std::to_string(Cc) + " channels needs per-channel tensors");
+    Tensor y = make(x->shape);
+    float *mean = dev().step_floats(Cc), *inv = dev().step_floats(Cc);
+    const int tr = training ? 1 : 0;
+    OMT(om_batchnorm2d_fwd(C(), x->data, gamma->data, beta->data, running_mean, running_var, y->data, mean, inv, N,
+                           Cc, plane, tr, momentum, eps));
+    if (tracked({&x, &gamma, &beta}))
+        attach(y, "BatchNorm", {x, gamma, beta}, [=](Engine &e, Record &r, const float *g) {
+            int ax, ag, ab;
+            float *dx = e.dest(r, 0, &ax), *dg = e.dest(r, 1, &ag), *db = e.dest(r, 2, &ab);
+            const float *xd = r.inputs[0]->data, *gd = r.inputs[1]->data;
+            if (!dg || !db || ag == ab) {
+                OMT(om_batchnorm2d_bwd(C(), g, xd, gd, mean, inv, dx, dg, db, N, Cc, plane, tr, ax, dg ? ag : ab));
+            } else {  // the two parameter gradients need different accumulation: one launch each
+                OMT(om_batchnorm2d_bwd(C(), g, xd, gd, mean, inv, dx, dg, nullptr, N, Cc, plane, tr, ax, ag));
+                OMT(om_batchnorm2d_bwd(C(), g, xd, gd, mean, inv, nullptr, nullptr, db, N, Cc, plane, tr, 0, ab));
+            }
+        });
+    return y;
+}
+
+Tensor embedding(const Tensor &table, const Tensor &ids, int padding_index) {
+    if (table->shape.size() != 2 || !ids->idata)
+        shape_error("Embedding needs a [count, width] table and Int32 ids, not " + shape_str(table->shape));
+    const int rows = table->shape[0], dim = table->shape[1];
+    std::vector<int> ys = ids->shape;
+    ys.push_back(dim);
+    Tensor y = make(ys);
+    const int64_t n = ids->numel;
+    OMT(om_embedding_fwd(C(), table->data, ids->idata, y->data, n, dim, rows));
+    if (tracked({&table})) {
+        const int32_t *id = ids->idata;
+        attach(y, "Embedding", {table}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dt = e.dest(r, 0, &a);
+            OMT(om_embedding_bwd(C(), g, id, dt, n, dim, rows, padding_index, a));
+        });
+    }
+    return y;
+}
+
+Tensor dropout(const Tensor &x, float p, uint64_t seed, int64_t draw) {
+    Tensor y = make(x->shape);
+    const int64_t n = x->numel;
+    OMT(om_dropout_fwd(C(), x->data, y->data, n, p, seed, draw));
+    if (tracked({&x}))
+        attach(y, "Mul", {x}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            OMT(om_dropout_bwd(C(), g, dx, n, p, seed, draw, a));
+        });
+    return y;
+}
+
 }  // namespace omt

@@ -152,6 +152,15 @@ Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int
 Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw);
 Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std::vector<int32_t> &in_len,
                 const std::vector<int32_t> &tgt_len, int blank, int reduction);
+// Ops.AvgPool2d (Ops.Layers.cs:405-455), square window k, stride s, padding p.
+Tensor avg_pool2d(const Tensor &x, int k, int s, int p, bool count_include_pad = true);
+// Ops.BatchNorm2d (Ops.Layers.cs:158-246) with the module's running statistics (device, [C], updated in training).
+Tensor batch_norm2d(const Tensor &x, const Tensor &gamma, const Tensor &beta, float *running_mean,
+                    float *running_var, bool training, float momentum, float eps);
+// Ops.Embedding, dense gradient (Ops.Layers.cs:549-600): ids is an Int32 tensor; the result is ids.shape + [dim].
+Tensor embedding(const Tensor &table, const Tensor &ids, int padding_index);
+// Dropout.Forward in training mode (Layers.cs:341-368) for mask number `draw` of the stream `seed`.
+Tensor dropout(const Tensor &x, float p, uint64_t seed, int64_t draw);
 
 // ------------------------------------------------------------------------------------------------ modules
 // SplitMix64 (Generator.cs:10-48).
@@ -181,6 +190,11 @@ class Module {
         return p;
     }
     void named_parameters(std::vector<std::pair<std::string, Tensor>> &out, const std::string &prefix = "") const;
+    // A float state buffer that is not a parameter (RegisterBuffer, NnModule.cs:54-65): device memory in the
+    // persistent region, initialised from `init`; listed by named_buffers in the same prefix order.
+    float *buffer(const std::string &name, const std::vector<float> &init);
+    void named_buffers(std::vector<std::pair<std::string, std::pair<float *, int64_t>>> &out,
+                       const std::string &prefix = "") const;
     // Asks the arena to place these parameters back to back, in this order (values, gradients and moments alike),
     // so one kernel can treat them as one tensor. Parameters() order is unchanged.
     void colocate(std::vector<Tensor> group) { colocate_.push_back(std::move(group)); }
@@ -190,6 +204,7 @@ class Module {
 
    private:
     std::vector<std::pair<std::string, Tensor>> params_;
+    std::vector<std::pair<std::string, std::pair<float *, int64_t>>> buffers_;
     std::vector<std::pair<std::string, std::unique_ptr<Module>>> children_;
     std::vector<std::vector<float>> init_;  // host values until the parameters are laid out in device memory
     std::vector<std::vector<Tensor>> colocate_;
@@ -207,6 +222,37 @@ class Conv2d : public Module {
     Tensor operator()(const Tensor &x) const { return conv2d(x, w, b, stride, pad); }
     Tensor w, b;
     int stride, pad;
+};
+// BatchNorm2d (Layers.cs:202-238): weight 1, bias 0; buffers running_mean 0 and running_var 1.
+class BatchNorm2d : public Module {
+   public:
+    explicit BatchNorm2d(int c, float momentum = 0.1f, float eps = 1e-5f);
+    Tensor operator()(const Tensor &x) const { return batch_norm2d(x, w, b, rm, rv, training, momentum, eps); }
+    Tensor w, b;
+    float *rm, *rv;
+    float momentum, eps;
+    bool training = true;
+};
+// Embedding (Layers.cs:268-308): weight U(-sqrt(3), sqrt(3)) in row-major order, dense gradient.
+class Embedding : public Module {
+   public:
+    Embedding(int count, int width, Generator &g, int padding_index = -1);
+    Tensor operator()(const Tensor &ids) const { return embedding(w, ids, pad); }
+    Tensor w;
+    int pad;
+};
+// Dropout (Layers.cs:310-368): the mask stream is a pure function of (seed, masks drawn so far, index).
+class Dropout : public Module {
+   public:
+    Dropout(float p, uint64_t seed);
+    Tensor operator()(const Tensor &x) {
+        if (!training || p == 0.0f) return x;
+        return dropout(x, p, seed, draws++);
+    }
+    float p;
+    uint64_t seed;
+    int64_t draws = 0;
+    bool training = true;
 };
 class LayerNorm : public Module {
    public:

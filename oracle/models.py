@@ -319,7 +319,7 @@ def mlp_curve(o, steps=None):
 
 # ----------------------------------------------------------------------------------------------------------- curves
 class BatchNorm2d(Module):
-    """BatchNorm2d (Layers.cs:119-160): weight 1, bias 0, running mean 0 / variance 1 (buffers), momentum 0.1,
+    """BatchNorm2d (Layers.cs:202-238): weight 1, bias 0, running mean 0 / variance 1 (buffers), momentum 0.1,
     eps 1e-5, training mode."""
 
     def __init__(self, c):
