@@ -34,7 +34,8 @@ typedef struct {
  * Configurations 6-8 are the models of the reference's training-curve tests (TrainCase.cs:114-237), whose batches
  * the caller supplies each step with omt_input_write: 6 = MLP 20-32-4 with SGD(0.05, momentum 0.9, wd 1e-4);
  * 7 = conv/BatchNorm/pool net with AdamW(3e-3, wd 0.01), CosineLr(3e-3, 60) and ClipNorm(0.5) inside omt_step;
- * 8 = Embedding + 2 post-norm encoder layers + mean + Linear with Adam(2e-3) and WarmupLr(ConstantLr(2e-3), 10, 0.1). */
+ * 8 = Embedding + 2 post-norm encoder layers + mean + Linear with Adam(2e-3) and WarmupLr(ConstantLr(2e-3), 10, 0.1);
+ * 9 = configuration 8 with dropout 0.1 after attention and feed-forward in every layer (seeds 77 + 2i, 78 + 2i). */
 om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out);
 void omt_destroy(omt_model *m);
 const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */
@@ -82,6 +83,40 @@ om_status omt_buffer_write(omt_model *m, int i, const float *host, int64_t numel
  * 6-8 to the optimizers of the reference's training-curve cases (omt_config_create). */
 om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float beta2, float eps, float weight_decay,
                             float momentum, float dampening, int nesterov, int amsgrad);
+
+/* ------------------------------------------------------------------------------------------ checkpoints */
+/* Checkpoint errors (CheckpointErrorKind, Checkpoint.cs:11-24), returned by the calls below. */
+enum {
+    OMT_E_CKPT_BAD_HEADER = 16,        /* header missing, malformed or inconsistent with the file length */
+    OMT_E_CKPT_BAD_MANIFEST = 17,      /* manifest not the expected JSON, or a field missing or out of range */
+    OMT_E_CKPT_BAD_TENSOR = 18,        /* a tensor entry outside the data region or sized unlike its shape */
+    OMT_E_CKPT_MISMATCH = 19,          /* well-formed but not the model's (or optimizer's) state */
+    OMT_E_CKPT_UNSUPPORTED_STREAM = 20 /* not a regular, seekable file */
+};
+/* Checkpoint.Save (Checkpoint.cs:55-138): the ONEMCKPT file of the model's StateDict (parameters and buffers per
+ * module, then children) and, with with_optimizer, the optimizer's kind, step count, hyper-parameters (float bit
+ * patterns) and state tensors; n_extra integer values by key (written in key order). Written to path + ".tmp",
+ * then renamed. The same state always writes the same bytes. */
+om_status omt_checkpoint_save(omt_model *m, const char *path, int with_optimizer, int n_extra,
+                              const char *const *extra_keys, const int64_t *extra_values);
+/* Checkpoint.Load (Checkpoint.cs:151-331): checks the whole file against the model (and, with with_optimizer, its
+ * optimizer: kind, fixed settings, state shapes) before changing anything, then restores parameters, buffers,
+ * optimizer state, rate, weight decay and step count. *had_optimizer (may be NULL) says whether the file holds
+ * optimizer state; a file without it fails with OMT_E_CKPT_MISMATCH when with_optimizer is set. */
+om_status omt_checkpoint_load(omt_model *m, const char *path, int with_optimizer, int *had_optimizer);
+/* The extra values of the last checkpoint loaded, in key order. */
+int omt_checkpoint_extra_count(omt_model *m);
+om_status omt_checkpoint_extra(omt_model *m, int i, char *key, int key_cap, int64_t *value);
+/* Host only, no device: checks a checkpoint file against a model-state target given as (name, dtype 0 = f32,
+ * 1 = i32, 2 = i64, shape) entries in state order, exactly as a model-only omt_checkpoint_load would, and returns
+ * its status (message: omt_last_error(NULL)). For tools that vet a file before a device is involved. */
+typedef struct {
+    const char *name;
+    int32_t dtype;
+    int32_t ndim;
+    const int32_t *dims;
+} omt_tensor_spec;
+om_status omt_checkpoint_check(const char *path, const omt_tensor_spec *model, int n_model);
 
 /* Host helper with no device: the SplitMix64 generator of the tape (for cross-checks against the reference's
  * Generator): kind 0 = uniform [lo, hi), 1 = benchmark normal, 2 = ints in [lo, hi). */

@@ -162,6 +162,11 @@ _OMT_SIGS = {
     "omt_buffer_read": ([vp, ci, vp, i64], i32),
     "omt_buffer_write": ([vp, ci, vp, i64], i32),
     "omt_set_optimizer": ([vp, ci, f32, f32, f32, f32, f32, f32, f32, ci, ci], i32),
+    "omt_checkpoint_save": ([vp, C.c_char_p, ci, ci, C.POINTER(C.c_char_p), C.POINTER(i64)], i32),
+    "omt_checkpoint_load": ([vp, C.c_char_p, ci, C.POINTER(ci)], i32),
+    "omt_checkpoint_extra_count": ([vp], ci),
+    "omt_checkpoint_extra": ([vp, ci, C.c_char_p, ci, C.POINTER(i64)], i32),
+    "omt_checkpoint_check": ([C.c_char_p, vp, ci], i32),
     "omt_lr": ([vp], f32),
     "omt_set_lr": ([vp, f32], i32),
     "omt_lr_constant": ([f32, C.POINTER(vp)], i32),
@@ -324,6 +329,29 @@ class Model:
     def step_count(self):
         return self.L.omt_step_count(self.h)
 
+    def save_checkpoint(self, path, optimizer=True, extra=None):
+        """Checkpoint.Save of the model (and its optimizer); extra: {key: int}."""
+        extra = extra or {}
+        keys = (C.c_char_p * max(len(extra), 1))(*[k.encode() for k in extra])
+        vals = (i64 * max(len(extra), 1))(*extra.values())
+        self._check(self.L.omt_checkpoint_save(self.h, os.fsencode(path), int(optimizer), len(extra), keys, vals),
+                    "omt_checkpoint_save")
+
+    def load_checkpoint(self, path, optimizer=True):
+        """Checkpoint.Load; returns (had_optimizer, extra). Raises CheckpointError with the failed check's kind."""
+        had = ci()
+        st = self.L.omt_checkpoint_load(self.h, os.fsencode(path), int(optimizer), C.byref(had))
+        if st in CKPT_KINDS:
+            raise CheckpointError(CKPT_KINDS[st], self.L.omt_last_error(self.h).decode())
+        self._check(st, "omt_checkpoint_load")
+        extra = {}
+        for i in range(self.L.omt_checkpoint_extra_count(self.h)):
+            k = C.create_string_buffer(256)
+            v = i64()
+            self._check(self.L.omt_checkpoint_extra(self.h, i, k, 256, C.byref(v)), "omt_checkpoint_extra")
+            extra[k.value.decode()] = v.value
+        return bool(had.value), extra
+
     @property
     def lr(self) -> float:
         return self.L.omt_lr(self.h)
@@ -366,6 +394,39 @@ class Model:
             self.close()
         except Exception:
             pass
+
+
+CKPT_KINDS = {16: "BadHeader", 17: "BadManifest", 18: "BadTensor", 19: "Mismatch", 20: "UnsupportedStream"}
+
+
+class CheckpointError(OmError):
+    """A checkpoint that is malformed or does not fit (CheckpointException); `kind` names the failed check."""
+
+    def __init__(self, kind, message):
+        super().__init__(f"{kind}: {message}")
+        self.kind = kind
+
+
+class omt_tensor_spec(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", i32), ("ndim", i32), ("dims", C.POINTER(i32))]
+
+
+def checkpoint_check(path, target):
+    """Checks a checkpoint file against a model-state target [(name, "f32"|"i32"|"i64", shape)] on the host (no
+    device), as a model-only load would; raises CheckpointError with the failed check's kind."""
+    L = load_train()
+    dt = {"f32": 0, "i32": 1, "i64": 2}
+    keep = []
+    specs = (omt_tensor_spec * max(len(target), 1))()
+    for i, (name, dtype, shape) in enumerate(target):
+        dims = (i32 * max(len(shape), 1))(*shape)
+        keep.append(dims)
+        specs[i] = omt_tensor_spec(name.encode(), dt[dtype], len(shape), dims)
+    st = L.omt_checkpoint_check(os.fsencode(path), C.cast(specs, vp), len(target))
+    if st in CKPT_KINDS:
+        raise CheckpointError(CKPT_KINDS[st], L.omt_last_error(None).decode())
+    if st != 0:
+        raise OmError(f"omt_checkpoint_check failed ({st}): {L.omt_last_error(None).decode()}")
 
 
 class LrSchedule:

@@ -4,6 +4,7 @@
 #include <cstring>
 #include <map>
 
+#include "checkpoint.hpp"
 #include "om_train.h"
 #include "schedules.hpp"
 #include "tape.hpp"
@@ -55,13 +56,26 @@ float *Module::buffer(const std::string &name, const std::vector<float> &init) {
     const uint64_t bytes = sizeof(float) * (init.empty() ? 1 : init.size());
     float *d = (float *)dev().persistent(bytes);
     if (!init.empty()) check(dev().ctx(), om_upload(dev().ctx(), d, init.data(), bytes), "buffer upload");
-    buffers_.emplace_back(name, std::make_pair(d, (int64_t)init.size()));
+    BufferRef r;
+    r.dev = d;
+    r.numel = (int64_t)init.size();
+    buffers_.emplace_back(name, r);
     return d;
 }
-void Module::named_buffers(std::vector<std::pair<std::string, std::pair<float *, int64_t>>> &out,
-                           const std::string &prefix) const {
+void Module::buffer_i64(const std::string &name, int64_t *host) {
+    BufferRef r;
+    r.host = host;
+    r.numel = 1;
+    buffers_.emplace_back(name, r);
+}
+void Module::named_buffers(std::vector<std::pair<std::string, BufferRef>> &out, const std::string &prefix) const {
     for (auto &b : buffers_) out.emplace_back(prefix + b.first, b.second);
     for (auto &c : children_) c.second->named_buffers(out, prefix + c.first + ".");
+}
+void Module::state(std::vector<StateRef> &out, const std::string &prefix) const {
+    for (auto &p : params_) out.push_back({prefix + p.first, p.second, {}});
+    for (auto &b : buffers_) out.push_back({prefix + b.first, nullptr, b.second});
+    for (auto &c : children_) c.second->state(out, prefix + c.first + ".");
 }
 void Module::colocation_groups(std::vector<std::vector<Tensor>> &out) const {
     for (auto &g : colocate_) out.push_back(g);
@@ -104,6 +118,7 @@ Embedding::Embedding(int count, int width, Generator &g, int padding_index) : pa
 }
 Dropout::Dropout(float p_, uint64_t seed_) : p(p_), seed(seed_) {
     if (!(p >= 0.0f && p < 1.0f)) throw Error(OM_E_ARG, "Dropout probability must be in [0, 1).");
+    buffer_i64("draws", &draws);
 }
 LayerNorm::LayerNorm(int n, float eps_) : eps(eps_) {
     w = param("weight", {n}, std::vector<float>(n, 1.0f));  // Layers.cs:255-262
@@ -131,14 +146,23 @@ struct EncoderLayer : Module {
     MultiHeadAttention *attn;
     LayerNorm *norm1, *norm2;
     Linear *ff1, *ff2;
-    EncoderLayer(int width, int heads, int ff, Generator &g) {
+    Dropout *drop1 = nullptr, *drop2 = nullptr;  // only when dropout > 0 (seeds s and s + 1)
+    EncoderLayer(int width, int heads, int ff, Generator &g, float dropout = 0.0f, uint64_t dropout_seed = 0) {
         attn = child("attn", std::make_unique<MultiHeadAttention>(width, heads, g));
         norm1 = child("norm1", std::make_unique<LayerNorm>(width));
         ff1 = child("ff1", std::make_unique<Linear>(width, ff, g));
         ff2 = child("ff2", std::make_unique<Linear>(ff, width, g));
         norm2 = child("norm2", std::make_unique<LayerNorm>(width));
+        if (dropout > 0.0f) {
+            drop1 = child("drop1", std::make_unique<Dropout>(dropout, dropout_seed));
+            drop2 = child("drop2", std::make_unique<Dropout>(dropout, dropout_seed + 1));
+        }
     }
     Tensor operator()(const Tensor &x, const Tensor &mask) const {
+        if (drop1) {  // norm1(x + drop1(attn(x))), norm2(x1 + drop2(ff2(gelu(ff1(x1)))))
+            Tensor x1 = (*norm1)(add(x, (*drop1)((*attn)(x, mask))));
+            return (*norm2)(add(x1, (*drop2)(ffn(x1, ff1->w, ff1->b, ff2->w, ff2->b, nullptr))));
+        }
         // norm1(x + attn(x)), then norm2(x1 + ff2(gelu(ff1(x1)))), with the residual Adds and GELU fused into the
         // Linear launches
         Tensor x1 = (*norm1)(attn->residual(x, mask, x));
@@ -194,7 +218,7 @@ struct omt_model {
     int64_t total = 0;
     float *pb = nullptr, *gb = nullptr, *mb = nullptr, *vb = nullptr;
     std::vector<Input> inputs;
-    std::vector<std::pair<std::string, std::pair<float *, int64_t>>> buffers;  // named_buffers() order
+    std::vector<std::pair<std::string, Module::BufferRef>> buffers;  // float buffers, named_buffers() order
     std::function<Tensor(omt_model &)> loss_fn;
     // Optimizer (Optimizers.cs): kind OPT_SGD, OPT_ADAM (L2 weight decay) or OPT_ADAMW (decoupled); the benchmark
     // configurations use AdamW(lr 1e-3, betas 0.9/0.999, eps 1e-8, wd 0.01).
@@ -209,6 +233,7 @@ struct omt_model {
     float clip_max = 0.0f;                 // ClipNorm inside omt_step when > 0
     int clip_inf = 0;
     float *clip_buf = nullptr;             // device: [norm, coefficient] of the last ClipNorm
+    std::map<std::string, int64_t> ckpt_extra;  // the extra values of the last checkpoint loaded
     std::string err;
 
     Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
@@ -254,7 +279,12 @@ struct omt_model {
     // gradients, first and second moments; uploads the initial values once.
     void finalize(std::vector<std::vector<float>> &&init) {
         root->named_parameters(params);
-        root->named_buffers(buffers);
+        {
+            std::vector<std::pair<std::string, Module::BufferRef>> all;
+            root->named_buffers(all);
+            for (auto &b : all)
+                if (b.second.dev) buffers.push_back(b);
+        }
         std::vector<std::vector<Tensor>> groups;
         root->colocation_groups(groups);
         // Physical order: Parameters() order, except that a colocation group is placed whole where its first member
@@ -464,6 +494,193 @@ struct omt_model {
         check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
         return v;
     }
+    // ---------------------------------------------------------------------------------------------- checkpoints
+    // The model's StateDict as checkpoint tensors (names, types, shapes), and the optimizer's kind, hyper-parameters
+    // and StateTensors (Sgd: "initialized" Int32 flags then "momentum_buffer.i"; Adam/AdamW: "exp_avg.i",
+    // "exp_avg_sq.i", and "max_exp_avg_sq.i" with AMSGrad; Optimizers.cs:88-160, 300-315, 440-470).
+    std::vector<Module::StateRef> state_refs() const {
+        std::vector<Module::StateRef> st;
+        root->state(st);
+        return st;
+    }
+    int param_index(const Tensor &t) const {
+        for (size_t i = 0; i < params.size(); i++)
+            if (params[i].second == t) return (int)i;
+        throw Error(OM_E_STATE, "state tensor is not a parameter of the model");
+    }
+    std::vector<ckpt::Tensor> model_specs(const std::vector<Module::StateRef> &st) const {
+        std::vector<ckpt::Tensor> out;
+        for (const auto &r : st) {
+            ckpt::Tensor t;
+            t.name = r.name;
+            if (r.param) {
+                t.dims = r.param->shape;
+            } else if (r.buf.host) {
+                t.dtype = ckpt::I64;
+                t.dims = {1};
+            } else {
+                t.dims = {(int)r.buf.numel};
+            }
+            out.push_back(std::move(t));
+        }
+        return out;
+    }
+    ckpt::Optimizer optimizer_spec() const {
+        ckpt::Optimizer o;
+        o.step = step_count;
+        auto slot = [&](const char *nm) {
+            for (size_t i = 0; i < params.size(); i++) {
+                ckpt::Tensor t;
+                t.name = std::string(nm) + "." + std::to_string(i);
+                t.dims = params[i].second->shape;
+                o.state.push_back(t);
+                o.param_dims.push_back(t.dims);
+            }
+        };
+        if (opt_kind == OPT_SGD) {
+            o.kind = "sgd";
+            o.hyper = {{"lr", lr}, {"momentum", momentum}, {"dampening", dampening}, {"weight_decay", wd},
+                       {"nesterov", nesterov ? 1.0f : 0.0f}};
+            ckpt::Tensor f;
+            f.name = "initialized";
+            f.dtype = ckpt::I32;
+            f.dims = {(int)params.size()};
+            o.state.push_back(f);
+            o.param_dims.push_back({});
+            if (momentum != 0.0f) slot("momentum_buffer");
+        } else {
+            o.kind = opt_kind == OPT_ADAMW ? "adamw" : "adam";
+            o.hyper = {{"lr", lr}, {"beta1", beta1}, {"beta2", beta2}, {"epsilon", eps}, {"weight_decay", wd},
+                       {"amsgrad", amsgrad ? 1.0f : 0.0f}};
+            slot("exp_avg");
+            slot("exp_avg_sq");
+            if (amsgrad) slot("max_exp_avg_sq");
+        }
+        return o;
+    }
+    std::vector<float> host_block(float *block) const {
+        std::vector<float> h((size_t)(total > 0 ? total : 4));
+        check(device->ctx(), om_download(device->ctx(), h.data(), block, sizeof(float) * h.size()), "download");
+        return h;
+    }
+    // Checkpoint.Save (Checkpoint.cs:80-138): one download per arena block, then the file in StateDict order.
+    void save_checkpoint(const std::string &path, bool with_opt, const std::map<std::string, int64_t> &extra) {
+        const auto st = state_refs();
+        std::vector<ckpt::Tensor> model = model_specs(st);
+        const std::vector<float> ph = host_block(pb);
+        std::vector<std::vector<float>> bufs(st.size());
+        for (size_t i = 0; i < st.size(); i++) {
+            if (st[i].param) {
+                model[i].data = ph.data() + offset[param_index(st[i].param)];
+            } else if (st[i].buf.host) {
+                model[i].data = st[i].buf.host;
+            } else {
+                bufs[i].resize((size_t)st[i].buf.numel);
+                check(device->ctx(), om_download(device->ctx(), bufs[i].data(), st[i].buf.dev,
+                                                 sizeof(float) * bufs[i].size()), "download");
+                model[i].data = bufs[i].data();
+            }
+        }
+        ckpt::Optimizer o;
+        std::vector<float> mh, vh, xh;
+        std::vector<int32_t> flags;
+        if (with_opt) {
+            o = optimizer_spec();
+            mh = host_block(mb);
+            if (opt_kind != OPT_SGD) vh = host_block(vb);
+            if (amsgrad) xh = host_block(vmaxb);
+            size_t k = 0;
+            const size_t P = params.size();
+            if (opt_kind == OPT_SGD) {
+                flags.assign(sgd_started.begin(), sgd_started.end());
+                o.state[k++].data = flags.data();
+                if (momentum != 0.0f)
+                    for (size_t i = 0; i < P; i++) o.state[k++].data = mh.data() + offset[i];
+            } else {
+                for (size_t i = 0; i < P; i++) o.state[k++].data = mh.data() + offset[i];
+                for (size_t i = 0; i < P; i++) o.state[k++].data = vh.data() + offset[i];
+                if (amsgrad)
+                    for (size_t i = 0; i < P; i++) o.state[k++].data = xh.data() + offset[i];
+            }
+        }
+        ckpt::save(path, model, with_opt ? &o : nullptr, extra);
+    }
+    // Optimizer.SetHyperParameters' checks (Optimizers.cs:320-330, 470-480): the fixed settings must equal the
+    // target's, the rate and the weight decay must be finite and not negative.
+    static std::string settings_ok(const std::map<std::string, float> &h, const ckpt::Optimizer &o) {
+        auto rate_ok = [](float v) { return std::isfinite(v) && v >= 0.0f; };
+        auto target = [&](const char *n) {
+            for (auto &p : o.hyper)
+                if (p.first == n) return p.second;
+            return 0.0f;
+        };
+        if (o.kind == "sgd") {
+            if (h.at("momentum") != target("momentum") || h.at("dampening") != target("dampening") ||
+                (h.at("nesterov") != 0.0f) != (target("nesterov") != 0.0f))
+                return "The saved momentum, dampening or nesterov setting differs from this optimizer's.";
+        } else if (h.at("beta1") != target("beta1") || h.at("beta2") != target("beta2") ||
+                   h.at("epsilon") != target("epsilon") || (h.at("amsgrad") != 0.0f) != (target("amsgrad") != 0.0f)) {
+            return "The saved betas, epsilon or amsgrad setting differ from this optimizer's.";
+        }
+        if (!rate_ok(h.at("lr")) || !rate_ok(h.at("weight_decay"))) return "Value must be finite and not negative.";
+        return "";
+    }
+    // Checkpoint.Load (Checkpoint.cs:151-331): everything is checked before the model changes; then one upload per
+    // arena block and per buffer.
+    bool load_checkpoint(const std::string &path, bool with_opt) {
+        const auto st = state_refs();
+        const std::vector<ckpt::Tensor> model = model_specs(st);
+        ckpt::Optimizer o;
+        if (with_opt) o = optimizer_spec();
+        ckpt::Loaded L = ckpt::load(path, model, with_opt ? &o : nullptr, &settings_ok);
+        om_ctx *c = device->ctx();
+        std::vector<float> ph = host_block(pb);
+        for (size_t i = 0; i < st.size(); i++) {
+            const std::vector<char> &b = L.model[i];
+            if (st[i].param) {
+                std::memcpy(ph.data() + offset[param_index(st[i].param)], b.data(), b.size());
+            } else if (st[i].buf.host) {
+                std::memcpy(st[i].buf.host, b.data(), sizeof(int64_t));
+            } else {
+                check(c, om_upload(c, st[i].buf.dev, b.data(), b.size()), "upload");
+            }
+        }
+        check(c, om_upload(c, pb, ph.data(), sizeof(float) * ph.size()), "upload");
+        if (with_opt) {
+            const size_t P = params.size();
+            std::vector<float> mh(ph.size(), 0.0f), vh(ph.size(), 0.0f), xh;
+            if (amsgrad) xh.assign(ph.size(), 0.0f);
+            auto put = [&](std::vector<float> &blk, size_t i, const std::vector<char> &b) {
+                if (!b.empty()) std::memcpy(blk.data() + offset[i], b.data(), b.size());  // [0]: zero state
+            };
+            size_t k = 0;
+            if (opt_kind == OPT_SGD) {
+                const std::vector<char> &f = L.state[k++];
+                for (size_t i = 0; i < P; i++) {
+                    int32_t v;
+                    std::memcpy(&v, f.data() + 4 * i, 4);
+                    sgd_started[i] = v != 0;
+                }
+                if (momentum != 0.0f)
+                    for (size_t i = 0; i < P; i++) put(mh, i, L.state[k++]);
+            } else {
+                for (size_t i = 0; i < P; i++) put(mh, i, L.state[k++]);
+                for (size_t i = 0; i < P; i++) put(vh, i, L.state[k++]);
+                if (amsgrad)
+                    for (size_t i = 0; i < P; i++) put(xh, i, L.state[k++]);
+            }
+            check(c, om_upload(c, mb, mh.data(), sizeof(float) * mh.size()), "upload");
+            check(c, om_upload(c, vb, vh.data(), sizeof(float) * vh.size()), "upload");
+            if (amsgrad) check(c, om_upload(c, vmaxb, xh.data(), sizeof(float) * xh.size()), "upload");
+            lr = L.hyper.at("lr");
+            wd = L.hyper.at("weight_decay");
+            step_count = L.step;
+        }
+        ckpt_extra = L.extra;
+        device->sync();
+        return L.had_optimizer;
+    }
+
     float step() {
         device->step_reset();
         zero_grad(leaves);
@@ -658,11 +875,13 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.schedule = std::move(cs->s);
         omt_lr_free(cs);
         M.clip_max = 0.5f;
-    } else if (cfg == 8) {
+    } else if (cfg == 8 || cfg == 9) {
         // TrainCase.Encoder (TrainCase.cs:185-237): EncoderClassifier(vocab 11, width 16, 2 heads, FFN 32, 2 post-norm
         // layers, 2 classes) = Embedding, layers, Mean over the sequence, Linear; CE; Adam(2e-3);
-        // WarmupLr(ConstantLr(2e-3), 10, 0.1).
+        // WarmupLr(ConstantLr(2e-3), 10, 0.1). Configuration 9 is the same with dropout 0.1 in every layer (seed 77,
+        // layer i's two streams 77 + 2i and 78 + 2i; CheckpointTests.cs:21-30).
         const int B = pick(sc.batch, 16), L = pick(sc.seq, 6), NL = pick(sc.layers, 2);
+        const float drop = cfg == 9 ? 0.1f : 0.0f;
         Generator gm(3);
         struct Classifier : Module {
             Embedding *emb;
@@ -672,7 +891,8 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         auto m = std::make_unique<Classifier>();
         m->emb = m->child("emb", std::make_unique<Embedding>(11, 16, gm));
         for (int i = 0; i < NL; i++)
-            m->layers.push_back(m->child("layer" + std::to_string(i), std::make_unique<EncoderLayer>(16, 2, 32, gm)));
+            m->layers.push_back(m->child("layer" + std::to_string(i),
+                                         std::make_unique<EncoderLayer>(16, 2, 32, gm, drop, 77ull + 2ull * i)));
         m->cls = m->child("cls", std::make_unique<Linear>(16, 2, gm));
         Classifier *mp = m.get();
         M.root = std::move(m);
@@ -711,6 +931,10 @@ static om_status guard(omt_model *m, F f) {
         if (m) m->err = e.what();
         else g_create_err = e.what();
         return e.code;
+    } catch (const ckpt::Failure &e) {
+        if (m) m->err = e.what();
+        else g_create_err = e.what();
+        return OMT_E_CKPT_BAD_HEADER + (int)e.kind;
     } catch (const std::exception &e) {
         if (m) m->err = e.what();
         else g_create_err = e.what();
@@ -860,6 +1084,55 @@ om_status omt_param_write(omt_model *m, int i, int which, const float *host, int
 }
 int64_t omt_step_count(omt_model *m) { return m ? m->step_count : -1; }
 
+om_status omt_checkpoint_save(omt_model *m, const char *path, int with_optimizer, int n_extra,
+                              const char *const *extra_keys, const int64_t *extra_values) {
+    if (!m || !path || !*path || n_extra < 0 || (n_extra > 0 && (!extra_keys || !extra_values))) return OM_E_ARG;
+    return guard(m, [&] {
+        std::map<std::string, int64_t> extra;
+        for (int i = 0; i < n_extra; i++) {
+            if (!extra_keys[i]) throw Error(OM_E_ARG, "omt_checkpoint_save: NULL extra key");
+            extra[extra_keys[i]] = extra_values[i];
+        }
+        m->save_checkpoint(path, with_optimizer != 0, extra);
+    });
+}
+om_status omt_checkpoint_load(omt_model *m, const char *path, int with_optimizer, int *had_optimizer) {
+    if (!m || !path || !*path) return OM_E_ARG;
+    return guard(m, [&] {
+        const bool had = m->load_checkpoint(path, with_optimizer != 0);
+        if (had_optimizer) *had_optimizer = had ? 1 : 0;
+    });
+}
+int omt_checkpoint_extra_count(omt_model *m) { return m ? (int)m->ckpt_extra.size() : 0; }
+om_status omt_checkpoint_extra(omt_model *m, int i, char *key, int cap, int64_t *value) {
+    if (!m || i < 0 || i >= (int)m->ckpt_extra.size()) return OM_E_ARG;
+    auto it = m->ckpt_extra.begin();
+    std::advance(it, i);
+    if (key && cap > 0) {
+        std::strncpy(key, it->first.c_str(), (size_t)cap - 1);
+        key[cap - 1] = 0;
+    }
+    if (value) *value = it->second;
+    return OM_OK;
+}
+om_status omt_checkpoint_check(const char *path, const omt_tensor_spec *model, int n_model) {
+    if (!path || n_model < 0 || (n_model > 0 && !model)) return OM_E_ARG;
+    return guard(nullptr, [&] {
+        std::vector<ckpt::Tensor> target;
+        for (int i = 0; i < n_model; i++) {
+            ckpt::Tensor t;
+            if (!model[i].name || model[i].dtype < 0 || model[i].dtype > 2 || model[i].ndim < 0 ||
+                (model[i].ndim > 0 && !model[i].dims))
+                throw Error(OM_E_ARG, "omt_checkpoint_check: bad target entry " + std::to_string(i));
+            t.name = model[i].name;
+            t.dtype = (ckpt::DType)model[i].dtype;
+            t.dims.assign(model[i].dims, model[i].dims + model[i].ndim);
+            target.push_back(std::move(t));
+        }
+        ckpt::load(path, target, nullptr);
+    });
+}
+
 om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float beta2, float eps, float weight_decay,
                             float momentum, float dampening, int nesterov, int amsgrad) {
     if (!m) return OM_E_ARG;
@@ -875,22 +1148,22 @@ om_status omt_buffer_info(omt_model *m, int i, char *name, int cap, int64_t *num
         std::strncpy(name, m->buffers[i].first.c_str(), (size_t)cap - 1);
         name[cap - 1] = 0;
     }
-    if (numel) *numel = m->buffers[i].second.second;
+    if (numel) *numel = m->buffers[i].second.numel;
     return OM_OK;
 }
 om_status omt_buffer_read(omt_model *m, int i, float *host, int64_t numel) {
     if (!m || i < 0 || i >= (int)m->buffers.size() || !host) return OM_E_ARG;
     return guard(m, [&] {
-        if (numel != m->buffers[i].second.second) throw Error(OM_E_ARG, "omt_buffer_read: wrong element count");
-        check(m->device->ctx(), om_download(m->device->ctx(), host, m->buffers[i].second.first,
+        if (numel != m->buffers[i].second.numel) throw Error(OM_E_ARG, "omt_buffer_read: wrong element count");
+        check(m->device->ctx(), om_download(m->device->ctx(), host, m->buffers[i].second.dev,
                                             sizeof(float) * (uint64_t)numel), "download");
     });
 }
 om_status omt_buffer_write(omt_model *m, int i, const float *host, int64_t numel) {
     if (!m || i < 0 || i >= (int)m->buffers.size() || !host) return OM_E_ARG;
     return guard(m, [&] {
-        if (numel != m->buffers[i].second.second) throw Error(OM_E_ARG, "omt_buffer_write: wrong element count");
-        check(m->device->ctx(), om_upload(m->device->ctx(), m->buffers[i].second.first, host,
+        if (numel != m->buffers[i].second.numel) throw Error(OM_E_ARG, "omt_buffer_write: wrong element count");
+        check(m->device->ctx(), om_upload(m->device->ctx(), m->buffers[i].second.dev, host,
                                           sizeof(float) * (uint64_t)numel), "upload");
         m->device->sync();
     });

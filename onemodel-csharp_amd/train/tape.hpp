@@ -191,10 +191,24 @@ class Module {
     }
     void named_parameters(std::vector<std::pair<std::string, Tensor>> &out, const std::string &prefix = "") const;
     // A float state buffer that is not a parameter (RegisterBuffer, NnModule.cs:54-65): device memory in the
-    // persistent region, initialised from `init`; listed by named_buffers in the same prefix order.
+    // persistent region, initialised from `init`.
     float *buffer(const std::string &name, const std::vector<float> &init);
-    void named_buffers(std::vector<std::pair<std::string, std::pair<float *, int64_t>>> &out,
-                       const std::string &prefix = "") const;
+    // An Int64 [1] buffer kept on the host (Dropout's count of masks drawn).
+    void buffer_i64(const std::string &name, int64_t *host);
+    struct BufferRef {
+        float *dev = nullptr;      // float buffer in device memory
+        int64_t *host = nullptr;   // or an Int64 [1] buffer on the host
+        int64_t numel = 0;
+    };
+    void named_buffers(std::vector<std::pair<std::string, BufferRef>> &out, const std::string &prefix = "") const;
+    // StateDict order (NnModule.cs:281-311): per module its own parameters, its own buffers, then its children.
+    // Each entry is a parameter (tensor set) or a buffer.
+    struct StateRef {
+        std::string name;
+        Tensor param;
+        BufferRef buf;
+    };
+    void state(std::vector<StateRef> &out, const std::string &prefix = "") const;
     // Asks the arena to place these parameters back to back, in this order (values, gradients and moments alike),
     // so one kernel can treat them as one tensor. Parameters() order is unchanged.
     void colocate(std::vector<Tensor> group) { colocate_.push_back(std::move(group)); }
@@ -204,7 +218,7 @@ class Module {
 
    private:
     std::vector<std::pair<std::string, Tensor>> params_;
-    std::vector<std::pair<std::string, std::pair<float *, int64_t>>> buffers_;
+    std::vector<std::pair<std::string, BufferRef>> buffers_;
     std::vector<std::pair<std::string, std::unique_ptr<Module>>> children_;
     std::vector<std::vector<float>> init_;  // host values until the parameters are laid out in device memory
     std::vector<std::vector<Tensor>> colocate_;
@@ -244,7 +258,7 @@ class Embedding : public Module {
 // Dropout (Layers.cs:310-368): the mask stream is a pure function of (seed, masks drawn so far, index).
 class Dropout : public Module {
    public:
-    Dropout(float p, uint64_t seed);
+    Dropout(float p, uint64_t seed);  // registers the buffer "draws" (Int64 [1])
     Tensor operator()(const Tensor &x) {
         if (!training || p == 0.0f) return x;
         return dropout(x, p, seed, draws++);
