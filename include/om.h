@@ -75,6 +75,25 @@ om_status om_copy(om_ctx *ctx, void *dst_device, const void *src_device, uint64_
 om_status om_zero(om_ctx *ctx, void *dst_device, uint64_t bytes);
 om_status om_fill(om_ctx *ctx, float *dst, float value, int64_t n);
 
+/* ---------------------------------------------------------------------------------------------- staging */
+/* Host data staging for the per-step batches a DataLoader builds (DataLoader.cs:35-90, Batching.cs:129-200 produce
+ * them on the host): a ring of `slots` slots, each a pinned host buffer and a device buffer of slot_bytes, and a
+ * copy stream of default priority. The producer writes a batch straight into the pinned buffer that
+ * om_stager_begin returns (it waits for that buffer's previous upload to have read it), om_stager_commit queues the
+ * upload behind the previous use of the slot's device buffer and returns the device address, om_stager_acquire
+ * makes the context's stream wait for the upload before the step's launches, and om_stager_release, after the
+ * step's last launch, frees the device buffer for the slot's next upload. The upload of batch k+1 thus runs under
+ * step k. A slot can be begun again only after its batch was released (OM_E_STATE otherwise). No counterpart in
+ * the reference's CPU path, whose batches are used where they are built. */
+typedef struct om_stager om_stager;
+om_status om_stager_create(om_ctx *ctx, uint64_t slot_bytes, int slots, om_stager **out);
+om_status om_stager_destroy(om_stager *s);
+uint64_t om_stager_slot_bytes(const om_stager *s);
+om_status om_stager_begin(om_stager *s, void **host, int *slot);
+om_status om_stager_commit(om_stager *s, int slot, uint64_t bytes, void **device);
+om_status om_stager_acquire(om_stager *s, int slot);
+om_status om_stager_release(om_stager *s, int slot);
+
 /* ---------------------------------------------------------------------------------------------- GEMM */
 /* C[m,n] = op(A)[m,k] * op(B)[k,n] (+ bias[n]) on fp32 MFMA, for `batch` independent products. Row-major operands
  * with leading dimensions lda/ldb/ldc; trans_a means A is stored [k,m], trans_b means B is stored [n,k].

@@ -69,6 +69,19 @@ om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel);
  * the next step: the per-step batch of a training loop (TrainCase.cs:77-96 builds its batches on the host). */
 om_status omt_input_write(omt_model *m, int i, const void *host, int64_t numel);
 
+/* Staged batches (om_stager, include/om.h): a batch packs the model's inputs in input order, input i at byte
+ * `offset` (256-byte aligned) with `bytes` bytes (float32 or int32 elements). omt_batch_begin hands out a pinned
+ * host buffer of omt_batch_bytes to fill in place; omt_batch_commit checks the int inputs' ranges and queues the
+ * upload on the copy stream; the next omt_step / omt_forward_backward takes the oldest committed batch as its
+ * inputs (after its upload) and releases it after its last launch, so committing batch k+1 before running step k
+ * overlaps its upload with step k. Up to 3 batches may wait. Without a committed batch a step reads the inputs as
+ * last written by omt_input_write (which a staged batch does not change). */
+uint64_t omt_batch_bytes(omt_model *m);
+om_status omt_batch_layout(omt_model *m, int i, uint64_t *offset, uint64_t *bytes);
+om_status omt_batch_begin(omt_model *m, void **host);
+om_status omt_batch_commit(omt_model *m);
+int omt_batch_queued(omt_model *m);
+
 /* Named float state buffers that are not parameters (NnModule.RegisterBuffer, NnModule.cs:54-65): BatchNorm2d's
  * running_mean and running_var, in named_buffers() order ("1.running_mean", ...). */
 int omt_buffer_count(omt_model *m);

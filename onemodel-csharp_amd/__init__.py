@@ -90,6 +90,13 @@ _OM_SIGS = {
     "om_adam_step_scaled": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32, vp],
     "om_sgd_step": [vp, vp, vp, vp, i64, f32, f32, f32, f32, ci, ci],
     "om_clip_grad_norm": [vp, ci, vp, vp, f32, ci, ci, vp, vp],
+    "om_stager_create": [vp, u64, ci, C.POINTER(vp)],
+    "om_stager_destroy": [vp],
+    "om_stager_slot_bytes": [vp],
+    "om_stager_begin": [vp, C.POINTER(vp), C.POINTER(ci)],
+    "om_stager_commit": [vp, ci, u64, C.POINTER(vp)],
+    "om_stager_acquire": [vp, ci],
+    "om_stager_release": [vp, ci],
     "om_avgpool2d_fwd": [vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci],
     "om_avgpool2d_bwd": [vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci, ci],
     "om_batchnorm2d_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, f32, f32],
@@ -100,7 +107,8 @@ _OM_SIGS = {
     "om_dropout_bwd": [vp, vp, vp, i64, f32, u64, i64, ci],
     "om_clip_grad_value": [vp, ci, vp, vp, f32],
 }
-_RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None}
+_RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
+            "om_stager_slot_bytes": u64}
 
 _HIP = None
 
@@ -157,6 +165,11 @@ _OMT_SIGS = {
     "omt_input_grad": ([vp, ci, vp, i64], i32),
     "omt_generate": ([u64, ci, f32, f32, vp, i64], None),
     "omt_input_write": ([vp, ci, vp, i64], i32),
+    "omt_batch_bytes": ([vp], u64),
+    "omt_batch_layout": ([vp, ci, C.POINTER(u64), C.POINTER(u64)], i32),
+    "omt_batch_begin": ([vp, C.POINTER(vp)], i32),
+    "omt_batch_commit": ([vp], i32),
+    "omt_batch_queued": ([vp], ci),
     "omt_buffer_count": ([vp], ci),
     "omt_buffer_info": ([vp, ci, C.c_char_p, ci, C.POINTER(i64)], i32),
     "omt_buffer_read": ([vp, ci, vp, i64], i32),
@@ -291,6 +304,26 @@ class Model:
         a = np.ascontiguousarray(values)
         a = a.astype(np.int32 if a.dtype.kind in "iu" else np.float32, copy=False)
         self._check(self.L.omt_input_write(self.h, i, a.ctypes.data, a.size), "omt_input_write")
+
+    def stage_batch(self, values):
+        """Writes a batch {input name: array} into the next pinned staging slot and commits its upload (the next
+        step consumes it); inputs not named keep the slot's previous contents."""
+        np = self.np
+        host = vp()
+        self._check(self.L.omt_batch_begin(self.h, C.byref(host)), "omt_batch_begin")
+        try:
+            names = [self._input_name(i) for i in range(self.L.omt_input_count(self.h))]
+            for name, v in values.items():
+                i = names.index(name)
+                off, nb = u64(), u64()
+                self._check(self.L.omt_batch_layout(self.h, i, C.byref(off), C.byref(nb)), "omt_batch_layout")
+                a = np.ascontiguousarray(v)
+                a = a.astype(np.int32 if a.dtype.kind in "iu" else np.float32, copy=False)
+                if a.nbytes != nb.value:
+                    raise OmError(f"stage_batch: {name} has {a.nbytes} bytes, the model expects {nb.value}")
+                C.memmove(host.value + off.value, a.ctypes.data, a.nbytes)
+        finally:
+            self._check(self.L.omt_batch_commit(self.h), "omt_batch_commit")
 
     def _input_name(self, i):
         name = C.create_string_buffer(64)

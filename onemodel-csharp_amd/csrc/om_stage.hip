@@ -1,0 +1,151 @@
+// Host data staging: batches travel from the producer to HBM through a ring of pinned host slots, uploaded on a
+// copy stream while the previous step computes.
+//
+// A slot is a pinned host buffer (hipHostMalloc) and a device buffer of the same size. The producer fills the host
+// side in place (om_stager_begin hands out the pointer once the slot's previous upload has read it), om_stager_commit
+// queues the upload on the copy stream behind the event that marks the slot's previous device copy consumed, the
+// step makes the context's stream wait for the upload (om_stager_acquire) and marks the device copy consumed after
+// its last launch (om_stager_release). Upload k+1 then runs on the DMA engines under step k. Both streams have the
+// default priority.
+#include "om_internal.hpp"
+
+struct om_stager {
+    om_ctx *ctx = nullptr;
+    uint64_t slot_bytes = 0;
+    int slots = 0;
+    int next = 0;
+    hipStream_t copy = nullptr;
+    std::vector<char *> host;
+    std::vector<char *> dev;
+    std::vector<hipEvent_t> uploaded, consumed;
+    std::vector<char> upload_pending, consume_pending, begun, in_use;
+};
+
+namespace {
+
+om_status destroy(om_stager *s) {
+    om_status st = OM_OK;
+    if (s->copy && hipStreamSynchronize(s->copy) != hipSuccess) st = OM_E_DEVICE;
+    if (s->ctx && s->ctx->stream && hipStreamSynchronize(s->ctx->stream) != hipSuccess) st = OM_E_DEVICE;
+    for (char *p : s->host)
+        if (p) (void)hipHostFree(p);
+    for (char *p : s->dev)
+        if (p) (void)hipFree(p);
+    for (hipEvent_t e : s->uploaded)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : s->consumed)
+        if (e) (void)hipEventDestroy(e);
+    if (s->copy) (void)hipStreamDestroy(s->copy);
+    delete s;
+    return st;
+}
+
+bool valid_slot(const om_stager *s, int slot) { return s && slot >= 0 && slot < s->slots; }
+
+}  // namespace
+
+extern "C" {
+
+om_status om_stager_create(om_ctx *ctx, uint64_t slot_bytes, int slots, om_stager **out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, out, "om_stager_create: out is NULL");
+    *out = nullptr;
+    OM_REQUIRE(ctx, slot_bytes > 0 && slots >= 2 && slots <= 64, "om_stager_create: need slot_bytes > 0 and 2..64 slots");
+    om_stager *s = new om_stager;
+    s->ctx = ctx;
+    s->slot_bytes = slot_bytes;
+    s->slots = slots;
+    s->host.assign(slots, nullptr);
+    s->dev.assign(slots, nullptr);
+    s->uploaded.assign(slots, nullptr);
+    s->consumed.assign(slots, nullptr);
+    s->upload_pending.assign(slots, 0);
+    s->consume_pending.assign(slots, 0);
+    s->begun.assign(slots, 0);
+    s->in_use.assign(slots, 0);
+    hipError_t e = hipStreamCreateWithFlags(&s->copy, hipStreamNonBlocking);
+    for (int i = 0; e == hipSuccess && i < slots; i++) {
+        e = hipHostMalloc((void **)&s->host[i], slot_bytes, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc((void **)&s->dev[i], slot_bytes);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&s->uploaded[i], hipEventDisableTiming);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&s->consumed[i], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+        destroy(s);
+        return om::check_hip(ctx, e, "om_stager_create");
+    }
+    *out = s;
+    return OM_OK;
+}
+
+om_status om_stager_destroy(om_stager *s) {
+    if (!s) return OM_OK;
+    return destroy(s);
+}
+
+uint64_t om_stager_slot_bytes(const om_stager *s) { return s ? s->slot_bytes : 0; }
+
+om_status om_stager_begin(om_stager *s, void **host, int *slot) {
+    if (!s) return OM_E_ARG;
+    om_ctx *ctx = s->ctx;
+    OM_REQUIRE(ctx, host && slot, "om_stager_begin: NULL output");
+    const int k = s->next;
+    OM_REQUIRE(ctx, !s->begun[k], "om_stager_begin: slot %d is still being filled (commit it first)", k);
+    if (s->in_use[k])
+        return om::fail(ctx, OM_E_STATE, "om_stager_begin: all %d slots hold batches not yet released", s->slots);
+    // The pinned buffer is free once its previous upload has read it.
+    if (s->upload_pending[k]) {
+        om_status st = om::check_hip(ctx, hipEventSynchronize(s->uploaded[k]), "om_stager_begin wait");
+        if (st) return st;
+        s->upload_pending[k] = 0;
+    }
+    s->begun[k] = 1;
+    s->next = (k + 1) % s->slots;
+    *host = s->host[k];
+    *slot = k;
+    return OM_OK;
+}
+
+om_status om_stager_commit(om_stager *s, int slot, uint64_t bytes, void **device) {
+    if (!valid_slot(s, slot)) return OM_E_ARG;
+    om_ctx *ctx = s->ctx;
+    OM_REQUIRE(ctx, s->begun[slot], "om_stager_commit: slot %d was not begun", slot);
+    OM_REQUIRE(ctx, bytes <= s->slot_bytes, "om_stager_commit: %llu bytes exceed the slot size %llu",
+               (unsigned long long)bytes, (unsigned long long)s->slot_bytes);
+    // The device buffer is free once the step that read it has finished.
+    if (s->consume_pending[slot]) {
+        om_status st = om::check_hip(ctx, hipStreamWaitEvent(s->copy, s->consumed[slot], 0), "om_stager_commit wait");
+        if (st) return st;
+        s->consume_pending[slot] = 0;
+    }
+    if (bytes) {
+        om_status st = om::check_hip(
+            ctx, hipMemcpyAsync(s->dev[slot], s->host[slot], bytes, hipMemcpyHostToDevice, s->copy), "om_stager_commit");
+        if (st) return st;
+    }
+    om_status st = om::check_hip(ctx, hipEventRecord(s->uploaded[slot], s->copy), "om_stager_commit record");
+    if (st) return st;
+    s->upload_pending[slot] = 1;
+    s->begun[slot] = 0;
+    s->in_use[slot] = 1;
+    if (device) *device = s->dev[slot];
+    return OM_OK;
+}
+
+om_status om_stager_acquire(om_stager *s, int slot) {
+    if (!valid_slot(s, slot)) return OM_E_ARG;
+    return om::check_hip(s->ctx, hipStreamWaitEvent(s->ctx->stream, s->uploaded[slot], 0), "om_stager_acquire");
+}
+
+om_status om_stager_release(om_stager *s, int slot) {
+    if (!valid_slot(s, slot)) return OM_E_ARG;
+    om_ctx *ctx = s->ctx;
+    if (om::join(ctx)) return OM_E_DEVICE;  // weight-gradient launches on the second stream may read the inputs
+    om_status st = om::check_hip(ctx, hipEventRecord(s->consumed[slot], ctx->stream), "om_stager_release");
+    if (st) return st;
+    s->consume_pending[slot] = 1;
+    s->in_use[slot] = 0;
+    return OM_OK;
+}
+
+}  // extern "C"

@@ -2,6 +2,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <deque>
 #include <map>
 
 #include "checkpoint.hpp"
@@ -200,6 +201,8 @@ struct Input {
     std::vector<int32_t> hi;     // host copy (int inputs)
     bool is_int = false;
     int32_t lo = INT32_MIN, hi_bound = INT32_MAX;  // int inputs: the values the model accepts, [lo, hi_bound)
+    float *home_data = nullptr;                    // the input's own device buffer (a staged batch replaces it
+    int32_t *home_idata = nullptr;                 // for one step)
     void set_range(int32_t l, int32_t h) {
         lo = l;
         hi_bound = h;
@@ -234,6 +237,21 @@ struct omt_model {
     int clip_inf = 0;
     float *clip_buf = nullptr;             // device: [norm, coefficient] of the last ClipNorm
     std::map<std::string, int64_t> ckpt_extra;  // the extra values of the last checkpoint loaded
+    // Host data staging: a batch packs the inputs in input order, each 256-byte aligned; committed batches wait in
+    // `staged` until a step consumes the oldest.
+    static constexpr int kStageSlots = 3;
+    om_stager *stager = nullptr;
+    std::vector<uint64_t> batch_off;
+    uint64_t batch_bytes = 0;
+    int begun_slot = -1;
+    char *begun_host = nullptr;
+    struct Staged {
+        int slot;
+        char *dev;
+        std::vector<std::vector<int32_t>> ints;  // host copies of the int inputs (CTC reads its lengths on the host)
+    };
+    std::deque<Staged> staged;
+    int active_slot = -1;
     std::string err;
 
     Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
@@ -243,6 +261,7 @@ struct omt_model {
         in.t->shape = std::move(shape);
         in.t->numel = numel_of(in.t->shape);
         in.t->data = (float *)device->persistent(sizeof(float) * (uint64_t)in.t->numel);
+        in.home_data = in.t->data;
         in.t->name = name;
         check(device->ctx(), om_upload(device->ctx(), in.t->data, host.data(), sizeof(float) * host.size()), "upload");
         if (requires_grad) {
@@ -262,6 +281,7 @@ struct omt_model {
         in.t->shape = std::move(shape);
         in.t->numel = numel_of(in.t->shape);
         in.t->idata = (int32_t *)device->persistent(sizeof(int32_t) * (uint64_t)(in.t->numel > 0 ? in.t->numel : 1));
+        in.home_idata = in.t->idata;
         in.t->name = name;
         check(device->ctx(), om_upload(device->ctx(), in.t->idata, host.data(), sizeof(int32_t) * host.size()),
               "upload");
@@ -485,11 +505,89 @@ struct omt_model {
         check(c, om_clip_grad_value(c, (int)ptrs.size(), ptrs.data(), lens.data(), bound), "om_clip_grad_value");
     }
 
+    void batch_layout() {
+        batch_off.clear();
+        uint64_t off = 0;
+        for (const Input &in : inputs) {
+            batch_off.push_back(off);
+            const uint64_t b = (uint64_t)in.t->numel * 4;
+            off = (off + b + 255) & ~uint64_t(255);
+        }
+        batch_bytes = off > 0 ? off : 256;
+    }
+    void batch_begin(void **host) {
+        if (begun_slot >= 0) throw Error(OM_E_STATE, "omt_batch_begin: the previous batch was not committed");
+        if ((int)staged.size() >= kStageSlots)
+            throw Error(OM_E_STATE, "omt_batch_begin: " + std::to_string(kStageSlots) + " batches already wait for a step");
+        om_ctx *c = device->ctx();
+        if (!stager) {
+            batch_layout();
+            check(c, om_stager_create(c, batch_bytes, kStageSlots, &stager), "om_stager_create");
+        }
+        void *h = nullptr;
+        int slot = -1;
+        check(c, om_stager_begin(stager, &h, &slot), "om_stager_begin");
+        begun_slot = slot;
+        begun_host = (char *)h;
+        *host = h;
+    }
+    void batch_commit() {
+        if (begun_slot < 0) throw Error(OM_E_STATE, "omt_batch_commit: no batch was begun");
+        Staged st;
+        st.slot = begun_slot;
+        for (size_t i = 0; i < inputs.size(); i++) {
+            const Input &in = inputs[i];
+            if (!in.is_int) continue;
+            const int32_t *v = reinterpret_cast<const int32_t *>(begun_host + batch_off[i]);
+            for (int64_t k = 0; k < in.t->numel; k++)
+                if (v[k] < in.lo || v[k] >= in.hi_bound)
+                    throw Error(OM_E_ARG, "omt_batch_commit: " + in.name + "[" + std::to_string(k) + "] = " +
+                                              std::to_string(v[k]) + " is out of range");
+            st.ints.emplace_back(v, v + in.t->numel);
+        }
+        void *d = nullptr;
+        check(device->ctx(), om_stager_commit(stager, begun_slot, batch_bytes, &d), "om_stager_commit");
+        st.dev = (char *)d;
+        begun_slot = -1;
+        begun_host = nullptr;
+        staged.push_back(std::move(st));
+    }
+    // At the start of a step: the oldest committed batch becomes the inputs (the stream waits for its upload).
+    void take_batch() {
+        if (staged.empty()) return;
+        Staged st = std::move(staged.front());
+        staged.pop_front();
+        check(device->ctx(), om_stager_acquire(stager, st.slot), "om_stager_acquire");
+        size_t k = 0;
+        for (size_t i = 0; i < inputs.size(); i++) {
+            Input &in = inputs[i];
+            if (in.is_int) {
+                in.t->idata = reinterpret_cast<int32_t *>(st.dev + batch_off[i]);
+                in.hi = std::move(st.ints[k++]);
+            } else {
+                in.t->data = reinterpret_cast<float *>(st.dev + batch_off[i]);
+            }
+        }
+        active_slot = st.slot;
+    }
+    // After the step's last launch: the slot's device copy is released and the inputs point home again.
+    void return_batch() {
+        if (active_slot < 0) return;
+        check(device->ctx(), om_stager_release(stager, active_slot), "om_stager_release");
+        active_slot = -1;
+        for (Input &in : inputs) {
+            if (in.is_int) in.t->idata = in.home_idata;
+            else in.t->data = in.home_data;
+        }
+    }
+
     float forward_backward() {
         device->step_reset();
+        take_batch();
         zero_grad(leaves);
         Tensor loss = loss_fn(*this);
         backward(loss);
+        return_batch();
         float v = 0.0f;
         check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
         return v;
@@ -683,9 +781,11 @@ struct omt_model {
 
     float step() {
         device->step_reset();
+        take_batch();
         zero_grad(leaves);
         Tensor loss = loss_fn(*this);
         backward(loss);
+        return_batch();
         if (clip_max > 0.0f) {
             // Adam/AdamW read the coefficient in their update; SGD gets the gradients scaled in place
             const bool fold = opt_kind != OPT_SGD;
@@ -969,6 +1069,7 @@ om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_mod
 void omt_destroy(omt_model *m) {
     if (!m) return;
     set_dev(m->device.get());
+    if (m->stager) om_stager_destroy(m->stager);
     m->root.reset();
     m->params.clear();
     m->leaves.clear();
@@ -1140,6 +1241,28 @@ om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float
         m->set_optimizer(kind, lr, beta1, beta2, eps, weight_decay, momentum, dampening, nesterov != 0, amsgrad != 0);
     });
 }
+
+uint64_t omt_batch_bytes(omt_model *m) {
+    if (!m) return 0;
+    if (m->batch_off.empty()) m->batch_layout();
+    return m->batch_bytes;
+}
+om_status omt_batch_layout(omt_model *m, int i, uint64_t *offset, uint64_t *bytes) {
+    if (!m || i < 0 || i >= (int)m->inputs.size()) return OM_E_ARG;
+    if (m->batch_off.empty()) m->batch_layout();
+    if (offset) *offset = m->batch_off[i];
+    if (bytes) *bytes = (uint64_t)m->inputs[i].t->numel * 4;
+    return OM_OK;
+}
+om_status omt_batch_begin(omt_model *m, void **host) {
+    if (!m || !host) return OM_E_ARG;
+    return guard(m, [&] { m->batch_begin(host); });
+}
+om_status omt_batch_commit(omt_model *m) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] { m->batch_commit(); });
+}
+int omt_batch_queued(omt_model *m) { return m ? (int)m->staged.size() : 0; }
 
 int omt_buffer_count(omt_model *m) { return m ? (int)m->buffers.size() : 0; }
 om_status omt_buffer_info(omt_model *m, int i, char *name, int cap, int64_t *numel) {

@@ -1,0 +1,135 @@
+"""Host data staging (om_stager_*, omt_batch_*), on the GPU.
+
+A run fed through pinned staging slots, each batch committed one step ahead so its upload overlaps the previous
+step, must equal the same run fed with omt_input_write bit for bit; the slot protocol refuses a fourth waiting
+batch, a slot not yet released, and out-of-range labels, and never changes the data it carries.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def pkg():
+    from gpu_util import load_pkg
+    return load_pkg()
+
+
+def cnn_batches(n):
+    o = load_golden("training_cnn")
+    out = []
+    for i in range(n):
+        idx = o["in.order"][i].astype(int)
+        out.append({"x": o["in.x"][idx], "labels": o["in.y"][idx].astype(np.int32)})
+    return out
+
+
+def state(m):
+    return [m.read_param(i, w).view(np.uint32).copy() for i in range(len(m.params())) for w in (0, 2, 3)]
+
+
+def test_staged_run_equals_written_run(pkg):
+    batches = cnn_batches(10)
+    a, b = pkg.Model(7), pkg.Model(7)
+    try:
+        la = []
+        for bt in batches:
+            for k, v in bt.items():
+                a.write_input(k, v)
+            la.append(a.step())
+        lb = []
+        b.stage_batch(batches[0])
+        for i in range(len(batches)):
+            if i + 1 < len(batches):
+                b.stage_batch(batches[i + 1])  # committed before step i runs: its upload overlaps step i
+            lb.append(b.step())
+        assert pkg.load_train().omt_batch_queued(b.h) == 0
+        assert np.array_equal(np.array(la, np.float32).view(np.uint32), np.array(lb, np.float32).view(np.uint32))
+        for x, y in zip(state(a), state(b)):
+            assert np.array_equal(x, y)
+        bufs_a, bufs_b = a.buffers(), b.buffers()
+        for k in bufs_a:
+            assert np.array_equal(bufs_a[k].view(np.uint32), bufs_b[k].view(np.uint32)), k
+    finally:
+        a.close()
+        b.close()
+
+
+def test_staged_c3_batch_equals_resident_inputs(pkg):
+    """The benchmark block with its own inputs staged each step: the same losses as the resident inputs."""
+    a, b = pkg.Model(3, batch=4), pkg.Model(3, batch=4)
+    try:
+        ins = b.inputs()
+        la = [a.step() for _ in range(3)]
+        lb = []
+        b.stage_batch(ins)
+        for i in range(3):
+            if i < 2:
+                b.stage_batch(ins)
+            lb.append(b.step())
+        assert np.array_equal(np.array(la, np.float32).view(np.uint32), np.array(lb, np.float32).view(np.uint32))
+    finally:
+        a.close()
+        b.close()
+
+
+def test_queue_limit_and_range_checks(pkg):
+    m = pkg.Model(7)
+    try:
+        bt = cnn_batches(4)
+        for i in range(3):
+            m.stage_batch(bt[i])
+        L = pkg.load_train()
+        host = C.c_void_p()
+        assert L.omt_batch_begin(m.h, C.byref(host)) == 4  # OM_E_STATE: three batches already wait
+        m.step()
+        bad = dict(bt[3])
+        bad["labels"] = np.full(8, 5, np.int32)  # five classes: 5 is out of range
+        with pytest.raises(pkg.OmError):
+            m.stage_batch(bad)
+        assert L.omt_batch_queued(m.h) == 2
+        m.step()
+        m.step()
+        assert L.omt_batch_queued(m.h) == 0
+    finally:
+        m.close()
+
+
+def test_stager_protocol_carries_data_unchanged(pkg):
+    from gpu_util import Dev
+    d = Dev()
+    L = d.ctx.L
+    s = C.c_void_p()
+    n = 1 << 20
+    d.call("om_stager_create", C.c_uint64(4 * n), 2, C.byref(s))
+    try:
+        assert L.om_stager_slot_bytes(s) == 4 * n
+        out = d.empty((n,))
+        rng = np.random.default_rng(0)
+        for it in range(5):
+            host, slot = C.c_void_p(), C.c_int()
+            assert L.om_stager_begin(s, C.byref(host), C.byref(slot)) == 0
+            assert slot.value == it % 2
+            a = rng.standard_normal(n).astype(np.float32)
+            C.memmove(host.value, a.ctypes.data, a.nbytes)
+            dev = C.c_void_p()
+            assert L.om_stager_commit(s, slot, C.c_uint64(a.nbytes), C.byref(dev)) == 0
+            assert L.om_stager_acquire(s, slot) == 0
+            d.call("om_copy", out, dev, C.c_uint64(a.nbytes))
+            assert L.om_stager_release(s, slot) == 0
+            assert np.array_equal(d.get(out).view(np.uint32), a.view(np.uint32))
+        # a slot whose batch is not released cannot be begun again
+        host, slot = C.c_void_p(), C.c_int()
+        for _ in range(2):
+            assert L.om_stager_begin(s, C.byref(host), C.byref(slot)) == 0
+            assert L.om_stager_commit(s, slot, C.c_uint64(16), None) == 0
+        assert L.om_stager_begin(s, C.byref(host), C.byref(slot)) == 4
+        assert L.om_stager_commit(s, 0, C.c_uint64(8 * n), None) != 0  # more than a slot holds
+    finally:
+        L.om_stager_destroy(s)
+        d.ctx.close()
