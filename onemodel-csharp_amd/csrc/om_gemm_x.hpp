@@ -11,7 +11,7 @@
 //     written to LDS, which gives each load about two chunks of MFMA time to land;
 //   - LDS is double-buffered, one barrier per chunk;
 //   - inside a chunk, the fragments of 16-k block b+1 are read from LDS while the MFMAs of block b issue.
-// Operand layouts in LDS are those of om_gemm_core.hpp (K layout [rows][BKT+4], R layout [BKT][rows+4]). For an
+// Operand layouts in LDS: K layout [rows][BKT] with XOR-swizzled float4 chunks (kaddr), R layout [BKT][rows+4]. For an
 // R-layout operand the wavefront's 16-row (or 16-column) MFMA blocks are interleaved: block i of a wavefront's TX
 // blocks covers rows {TX*c + i}, so the TX fragments a lane needs for one k sit side by side and arrive in one wide
 // LDS read (b64 / b96 / b128) instead of TX separate ones; the epilogue maps rows and columns back accordingly, and
@@ -23,6 +23,20 @@
 namespace omg {
 namespace gx {
 
+// K layout in LDS: row r keeps its BKT values with stride BKT (no pad), its float4 chunks permuted by an XOR with
+// kswz(r). A 16-lane phase of the b128 stores (two rows of 8 chunks at BKT 32, one row of 16 chunks at BKT 64) and
+// of the fragment reads (16 rows, one chunk each) then covers 16 distinct 4-bank groups of the 64 LDS banks; the
+// padded layout [rows][BKT + 4] let the two rows of a store phase overlap on four banks.
+template <int BKT>
+__device__ __forceinline__ int kswz(int r) {
+    static_assert(BKT == 32 || BKT == 64, "K-layout swizzle is defined for 32- and 64-wide chunks");
+    return BKT == 32 ? ((r >> 1) & 7) : (r & 15);
+}
+template <int BKT>
+__device__ __forceinline__ int kaddr(int r, int chunk) {
+    return r * BKT + 4 * (chunk ^ kswz<BKT>(r));
+}
+
 // Exact loader of one operand chunk: ROWS x BKT values (KCONTIG: rows contiguous along k; else along the rows),
 // spread over NTH threads (a chunk that does not split evenly leaves whole wavefronts idle on the last load).
 template <int ROWS, int BKT, bool KCONTIG, int NTH = NT>
@@ -31,7 +45,7 @@ struct Ld {
     static_assert(TOT % 64 == 0, "a chunk must split into whole wavefronts");
     static constexpr int NV = (TOT + NTH - 1) / NTH;
     static constexpr bool RAGGED = TOT % NTH != 0;
-    static constexpr int LDSZ = KCONTIG ? ROWS * (BKT + PAD) : BKT * (ROWS + PAD);
+    static constexpr int LDSZ = KCONTIG ? ROWS * BKT : BKT * (ROWS + PAD);
     const float *base;  // operand origin of this tile (row r0, k 0)
     int64_t ld;
     int goff[NV];  // per-load element offset from (r0, k0)
@@ -45,7 +59,7 @@ struct Ld {
             if constexpr (KCONTIG) {
                 int r = f / (BKT / 4), kq = (f % (BKT / 4)) * 4;
                 goff[i] = (int)(r * ld) + kq;
-                soff[i] = r * (BKT + PAD) + kq;
+                soff[i] = kaddr<BKT>(r, kq >> 2);
             } else {
                 int kk = f / (ROWS / 4), rq = (f % (ROWS / 4)) * 4;
                 goff[i] = (int)(kk * ld) + rq;
@@ -76,7 +90,7 @@ __device__ __forceinline__ void read_frag(float (&f)[4][TX], const float *T, int
     if constexpr (KL) {
 #pragma unroll
         for (int x = 0; x < TX; x++) {
-            floatx4 v = *reinterpret_cast<const floatx4 *>(&T[(w0 + x * 16 + l16) * (BKT + PAD) + blk * 16 + kl * 4]);
+            floatx4 v = *reinterpret_cast<const floatx4 *>(&T[kaddr<BKT>(w0 + x * 16 + l16, blk * 4 + kl)]);
 #pragma unroll
             for (int s = 0; s < 4; s++) f[s][x] = v[s];
         }
