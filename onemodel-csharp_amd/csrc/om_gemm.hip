@@ -80,6 +80,42 @@ __global__ void k_splitk_reduce(Params p) {
     }
 }
 
+// The same reduction for n % 4 == 0 and a split count known at compile time: a thread per float4 of C issues the S
+// loads of its partials before adding them in split order (0 + p0 + p1 + ...), so the result is k_splitk_reduce's.
+template <int S>
+__global__ void k_splitk_reduce_s(Params p) {
+    const int64_t total = (int64_t)p.m * p.n;
+    const int nq = p.n / 4;
+    const int64_t quads = (int64_t)p.m * nq;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p.colsum_ws)
+        for (int64_t i = gid; i < p.m; i += stride) {
+            double t = 0.0;
+#pragma unroll
+            for (int s = 0; s < S; s++) t += p.colsum_ws[(int64_t)s * p.m + i];
+            float v = (float)t;
+            p.db[i] = p.db_acc ? p.db[i] + v : v;
+        }
+    for (int64_t q = gid; q < quads; q += stride) {
+        const int row = (int)(q / nq), col0 = (int)(q % nq) * 4;
+        const float *src = p.ws + (int64_t)row * p.n + col0;
+        float4 t[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) t[s] = *reinterpret_cast<const float4 *>(src + s * total);
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            v[0] += t[s].x;
+            v[1] += t[s].y;
+            v[2] += t[s].z;
+            v[3] += t[s].w;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) epilogue(p, p.c, p.ldc, nullptr, row, col0 + u, v[u]);
+    }
+}
+
 template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
 static void launch_t(const Params &p, int batch, hipStream_t st) {
     int64_t tiles = (int64_t)((p.m + BM - 1) / BM) * ((p.n + BN - 1) / BN);
@@ -347,8 +383,17 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     }
     om_status s = OM_LAUNCH_CHECK(ctx, what);
     if (s || p.splits <= 1) return s;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, st,
-                       p);
+    if (p.n % 4 == 0 && (p.splits == 2 || p.splits == 4 || p.splits == 8 || p.splits == 16)) {
+        const int64_t quads = (int64_t)p.m * (p.n / 4);
+        const dim3 grid(om::grid1d(quads > p.m ? quads : p.m, 256, 4096));
+        if (p.splits == 2) hipLaunchKernelGGL(k_splitk_reduce_s<2>, grid, dim3(256), 0, st, p);
+        else if (p.splits == 4) hipLaunchKernelGGL(k_splitk_reduce_s<4>, grid, dim3(256), 0, st, p);
+        else if (p.splits == 8) hipLaunchKernelGGL(k_splitk_reduce_s<8>, grid, dim3(256), 0, st, p);
+        else hipLaunchKernelGGL(k_splitk_reduce_s<16>, grid, dim3(256), 0, st, p);
+    } else {
+        hipLaunchKernelGGL(k_splitk_reduce, dim3(om::grid1d((int64_t)p.m * p.n, 256, 4096)), dim3(256), 0, st,
+                           p);
+    }
     return OM_LAUNCH_CHECK(ctx, what);
 }
 
