@@ -4,7 +4,7 @@
  * This is the boundary a host tape binds (the reference's C# tape through [LibraryImport], or this repository's C++
  * tape in onemodel-csharp_amd/train). Every entry point:
  *   - takes plain device pointers (float*, int32_t*) and sizes; no C++ or framework types cross the ABI;
- *   - is asynchronous on the context's HIP stream; only om_download and om_ctx_sync block;
+ *   - is asynchronous on the context's HIP stream; only om_download, om_readback_wait and om_ctx_sync block;
  *   - returns om_status (OM_OK = 0) and leaves a message in om_last_error(ctx) on failure;
  *   - validates shapes and pointers on the host before launching, so a kernel never sees a shape it does not handle;
  *   - is deterministic: tiling, split-K and reduction orders depend only on the shape.
@@ -93,6 +93,18 @@ om_status om_stager_begin(om_stager *s, void **host, int *slot);
 om_status om_stager_commit(om_stager *s, int slot, uint64_t bytes, void **device);
 om_status om_stager_acquire(om_stager *s, int slot);
 om_status om_stager_release(om_stager *s, int slot);
+
+/* Readback of a small device value (a step's loss) without waiting for the rest of the stream: om_readback_post
+ * queues a copy of `bytes` from device memory into a pinned host buffer on the context's stream, ordered after the
+ * work already queued there (not after the weight-gradient stream), and om_readback_wait blocks only until that
+ * copy has landed, then copies it to dst. Launches queued between the two keep the device busy while the host
+ * returns with the value. No counterpart in the reference's CPU path, where the loss is a host float as soon as the
+ * forward has run: its training step reads it there, before Backward and Step (TrainCase.cs:117-127). */
+typedef struct om_readback om_readback;
+om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out);
+om_status om_readback_destroy(om_readback *r);
+om_status om_readback_post(om_readback *r, const void *src_device, uint64_t bytes);
+om_status om_readback_wait(om_readback *r, void *dst_host, uint64_t bytes);
 
 /* ---------------------------------------------------------------------------------------------- GEMM */
 /* C[m,n] = op(A)[m,k] * op(B)[k,n] (+ bias[n]) on fp32 MFMA, for `batch` independent products. Row-major operands

@@ -40,7 +40,10 @@ om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_mod
 void omt_destroy(omt_model *m);
 const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */
 
-/* One training step: ZeroGrad, forward, loss.Backward(), optimizer.Step(); *loss is read back at the end. */
+/* One training step: ZeroGrad, forward, loss.Backward(), optimizer.Step(). *loss is the forward's loss, read where
+ * the reference's step reads it (TrainCase.cs:117-127): the call returns once that value has landed on the host,
+ * with the backward and the update queued behind it on the model's stream (omt_ctx). Every later call that touches
+ * the model's memory is ordered after them; om_ctx_sync(omt_ctx(m)) waits for them. */
 om_status omt_step(omt_model *m, float *loss);
 /* ZeroGrad, forward and backward only (gradients are left in the arena). */
 om_status omt_forward_backward(omt_model *m, float *loss);

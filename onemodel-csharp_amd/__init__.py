@@ -91,6 +91,10 @@ _OM_SIGS = {
     "om_sgd_step": [vp, vp, vp, vp, i64, f32, f32, f32, f32, ci, ci],
     "om_clip_grad_norm": [vp, ci, vp, vp, f32, ci, ci, vp, vp],
     "om_stager_create": [vp, u64, ci, C.POINTER(vp)],
+    "om_readback_create": [vp, u64, C.POINTER(vp)],
+    "om_readback_destroy": [vp],
+    "om_readback_post": [vp, vp, u64],
+    "om_readback_wait": [vp, vp, u64],
     "om_stager_destroy": [vp],
     "om_stager_slot_bytes": [vp],
     "om_stager_begin": [vp, C.POINTER(vp), C.POINTER(ci)],

@@ -7,6 +7,8 @@
 // step makes the context's stream wait for the upload (om_stager_acquire) and marks the device copy consumed after
 // its last launch (om_stager_release). Upload k+1 then runs on the DMA engines under step k. Both streams have the
 // default priority.
+#include <cstring>
+
 #include "om_internal.hpp"
 
 struct om_stager {
@@ -145,6 +147,81 @@ om_status om_stager_release(om_stager *s, int slot) {
     if (st) return st;
     s->consume_pending[slot] = 1;
     s->in_use[slot] = 0;
+    return OM_OK;
+}
+
+}  // extern "C"
+
+// Readback: a pinned host buffer the context's stream copies a small device value into, and an event recorded after
+// the copy. The host waits for that event only, so launches queued after the post keep running while it returns.
+struct om_readback {
+    om_ctx *ctx = nullptr;
+    uint64_t bytes = 0;
+    char *host = nullptr;
+    hipEvent_t landed = nullptr;
+    uint64_t posted = 0;  // bytes of the last post, 0 before the first
+};
+
+extern "C" {
+
+om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, out, "om_readback_create: out is NULL");
+    *out = nullptr;
+    OM_REQUIRE(ctx, bytes > 0 && bytes <= (1u << 20), "om_readback_create: need 1 .. 1 MiB, got %llu",
+               (unsigned long long)bytes);
+    om_readback *r = new om_readback;
+    r->ctx = ctx;
+    r->bytes = bytes;
+    hipError_t e = hipHostMalloc((void **)&r->host, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&r->landed, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        if (r->host) (void)hipHostFree(r->host);
+        delete r;
+        return om::check_hip(ctx, e, "om_readback_create");
+    }
+    *out = r;
+    return OM_OK;
+}
+
+om_status om_readback_destroy(om_readback *r) {
+    if (!r) return OM_OK;
+    om_status st = OM_OK;
+    if (r->posted && hipEventSynchronize(r->landed) != hipSuccess) st = OM_E_DEVICE;
+    (void)hipEventDestroy(r->landed);
+    (void)hipHostFree(r->host);
+    delete r;
+    return st;
+}
+
+om_status om_readback_post(om_readback *r, const void *src, uint64_t bytes) {
+    if (!r) return OM_E_ARG;
+    om_ctx *ctx = r->ctx;
+    OM_REQUIRE(ctx, src && bytes > 0 && bytes <= r->bytes, "om_readback_post: need a source and 1 .. %llu bytes",
+               (unsigned long long)r->bytes);
+    // The pinned buffer may still be the target of the previous post.
+    if (r->posted) {
+        om_status st = om::check_hip(ctx, hipEventSynchronize(r->landed), "om_readback_post wait");
+        if (st) return st;
+    }
+    om_status st = om::check_hip(ctx, hipMemcpyAsync(r->host, src, bytes, hipMemcpyDeviceToHost, ctx->stream),
+                                 "om_readback_post");
+    if (st) return st;
+    st = om::check_hip(ctx, hipEventRecord(r->landed, ctx->stream), "om_readback_post record");
+    if (st) return st;
+    r->posted = bytes;
+    return OM_OK;
+}
+
+om_status om_readback_wait(om_readback *r, void *dst, uint64_t bytes) {
+    if (!r) return OM_E_ARG;
+    om_ctx *ctx = r->ctx;
+    if (!r->posted) return om::fail(ctx, OM_E_STATE, "om_readback_wait: nothing was posted");
+    OM_REQUIRE(ctx, dst && bytes <= r->posted, "om_readback_wait: need a destination and at most %llu bytes",
+               (unsigned long long)r->posted);
+    om_status st = om::check_hip(ctx, hipEventSynchronize(r->landed), "om_readback_wait");
+    if (st) return st;
+    memcpy(dst, r->host, bytes);
     return OM_OK;
 }
 

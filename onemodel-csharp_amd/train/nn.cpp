@@ -241,6 +241,7 @@ struct omt_model {
     // `staged` until a step consumes the oldest.
     static constexpr int kStageSlots = 3;
     om_stager *stager = nullptr;
+    om_readback *loss_rb = nullptr;  // the step's loss, read back while the backward and update still run
     std::vector<uint64_t> batch_off;
     uint64_t batch_bytes = 0;
     int begun_slot = -1;
@@ -779,11 +780,17 @@ struct omt_model {
         return L.had_optimizer;
     }
 
+    // One step. The loss is read back as the reference's step reads it, right after the forward (TrainCase.cs:
+    // 117-127): its copy is queued behind the forward and the host waits for that copy alone, after queueing the
+    // backward and the update, so those still run while the caller gets the value and queues the next step. Later
+    // work on the context's stream is ordered after them.
     float step() {
         device->step_reset();
         take_batch();
         zero_grad(leaves);
         Tensor loss = loss_fn(*this);
+        if (!loss_rb) check(device->ctx(), om_readback_create(device->ctx(), sizeof(float), &loss_rb), "readback");
+        check(device->ctx(), om_readback_post(loss_rb, loss->data, sizeof(float)), "loss readback");
         backward(loss);
         return_batch();
         if (clip_max > 0.0f) {
@@ -795,7 +802,7 @@ struct omt_model {
             optimizer_step();
         }
         float v = 0.0f;
-        check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
+        check(device->ctx(), om_readback_wait(loss_rb, &v, sizeof(float)), "loss readback");
         return v;
     }
 };
@@ -1070,6 +1077,7 @@ void omt_destroy(omt_model *m) {
     if (!m) return;
     set_dev(m->device.get());
     if (m->stager) om_stager_destroy(m->stager);
+    if (m->loss_rb) om_readback_destroy(m->loss_rb);
     m->root.reset();
     m->params.clear();
     m->leaves.clear();

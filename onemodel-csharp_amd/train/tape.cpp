@@ -52,6 +52,14 @@ void *Device::persistent(uint64_t bytes) {
     check(ctx_, om_alloc(ctx_, OM_REGION_PERSISTENT, bytes, &p), "om_alloc");
     return p;
 }
+const float *Device::one() {
+    if (!one_) {
+        float *p = static_cast<float *>(persistent(sizeof(float)));
+        check(ctx_, om_fill(ctx_, p, 1.0f, 1), "om_fill");
+        one_ = p;
+    }
+    return one_;
+}
 void Device::step_reset() { check(ctx_, om_step_reset(ctx_), "om_step_reset"); }
 void Device::sync() { check(ctx_, om_ctx_sync(ctx_), "om_ctx_sync"); }
 
@@ -152,8 +160,9 @@ void Engine::emit_alias(Record &r, int i, const float *g) {
 }
 
 void Engine::run(const Tensor &root) {
-    float *g = dev().step_floats(1);
-    OMT(om_fill(C(), g, 1.0f, 1));
+    // The seed gradient dL/dL = 1 is the device's persistent one; it is held as a borrowed buffer that is never
+    // anyone's sole holding, so every gradient that would be added into it is copied first.
+    float *g = const_cast<float *>(dev().one());
     if (root->is_leaf()) {
         Record tmp;
         tmp.inputs = {root};
@@ -183,8 +192,8 @@ void Engine::run(const Tensor &root) {
     }
     holders_.clear();
     root->grad_fn->pending = g;
-    root->grad_fn->pending_borrowed = false;
-    holders_[g] = 1;
+    root->grad_fn->pending_borrowed = true;
+    holders_[g] = 1 << 30;
     for (size_t i = order.size(); i-- > 0;) {
         Record *r = order[i];
         float *gi = r->pending;

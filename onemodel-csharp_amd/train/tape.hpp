@@ -72,6 +72,8 @@ class Device {
     float *step_floats(int64_t n);
     int32_t *step_ints(int64_t n);
     void *persistent(uint64_t bytes);
+    // A persistent 1.0f: the seed gradient of every backward pass (written once, never written again).
+    const float *one();
     void step_reset();
     void sync();
     bool overlap() const { return overlap_; }
@@ -79,6 +81,7 @@ class Device {
    private:
     om_ctx *ctx_ = nullptr;
     bool overlap_ = false;
+    float *one_ = nullptr;
 };
 
 Device &dev();            // the device of the current thread's model (set by Model)

@@ -133,3 +133,44 @@ def test_stager_protocol_carries_data_unchanged(pkg):
     finally:
         L.om_stager_destroy(s)
         d.ctx.close()
+
+
+def test_readback_takes_the_value_at_its_place_in_the_stream(pkg):
+    """om_readback_post copies the value as the stream has it at the post; work queued after it (here a fill of the
+    same buffer) does not change what om_readback_wait returns, and the next post sees the fill."""
+    from gpu_util import Dev
+    d = Dev()
+    L = d.ctx.L
+    r = C.c_void_p()
+    d.call("om_readback_create", C.c_uint64(64), C.byref(r))
+    try:
+        a = np.arange(16, dtype=np.float32) * 0.5 - 3.0
+        src = d.put(a)
+        assert L.om_readback_post(r, src.data_ptr(), C.c_uint64(64)) == 0
+        d.call("om_fill", src, C.c_float(7.0), C.c_int64(16))
+        out = np.zeros(16, np.float32)
+        assert L.om_readback_wait(r, out.ctypes.data, C.c_uint64(64)) == 0
+        assert np.array_equal(out.view(np.uint32), a.view(np.uint32))
+        assert L.om_readback_post(r, src.data_ptr(), C.c_uint64(8)) == 0
+        two = np.zeros(2, np.float32)
+        assert L.om_readback_wait(r, two.ctypes.data, C.c_uint64(8)) == 0
+        assert np.array_equal(two, np.full(2, 7.0, np.float32))
+        assert L.om_readback_wait(r, out.ctypes.data, C.c_uint64(16)) != 0  # more than the last post carried
+        assert L.om_readback_post(r, src.data_ptr(), C.c_uint64(128)) != 0  # more than the buffer holds
+    finally:
+        L.om_readback_destroy(r)
+        d.ctx.close()
+
+
+def test_readback_wait_before_any_post_is_refused(pkg):
+    from gpu_util import Dev
+    d = Dev()
+    L = d.ctx.L
+    r = C.c_void_p()
+    d.call("om_readback_create", C.c_uint64(4), C.byref(r))
+    try:
+        v = np.zeros(1, np.float32)
+        assert L.om_readback_wait(r, v.ctypes.data, C.c_uint64(4)) == 4  # OM_E_STATE
+    finally:
+        L.om_readback_destroy(r)
+        d.ctx.close()
