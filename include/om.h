@@ -144,6 +144,14 @@ om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const 
  * h and dh [rows, in]. */
 om_status om_linear_bwd_dx_gelu(om_ctx *ctx, const float *g, const float *w, const float *h, float *dh, int rows,
                                 int in, int out);
+/* The same pair with GELU's slope saved in place of the pre-activation: the forward writes a = gelu(h) and
+ * s = 0.5 (1 + erf(h/sqrt2)) + h exp(-h^2/2) / sqrt(2 pi) (the factor GeluGradBin multiplies by, TrainElementwise.cs:
+ * 59-85, rounded as there) from one erf evaluation; the backward is then dh = (g w) * s, bit for bit the
+ * om_linear_bwd_dx_gelu result, with no transcendental left in its epilogue. a and s are [rows, out]. */
+om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, const float *b, float *a, float *s,
+                                   int rows, int in, int out);
+om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,
+                                 int in, int out);
 /* Bias gradient alone: db[n] (+)= (float) sum over rows of g[row, n] in double (BackwardOps.SumTo). */
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate);
 

@@ -512,6 +512,30 @@ om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const 
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd");
 }
 
+om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, const float *b, float *a, float *s,
+                                   int rows, int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && a && s && a != s && rows >= 0 && in > 0 && out > 0,
+               "om_linear_gelu_fwd_slope: bad arguments");
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, a, out);
+    p.bias = b;
+    p.epi = omg::EPI_GELU_SLOPE;
+    p.out2 = s;
+    p.ld2 = out;
+    return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd_slope");
+}
+
+om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,
+                                 int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && w && s && dh && rows >= 0 && in > 0 && out > 0, "om_linear_bwd_dx_slope: bad arguments");
+    omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dh, in);
+    p.epi = omg::EPI_MUL_AUX;
+    p.aux = s;
+    p.ldaux = in;
+    return omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd_dx_slope");
+}
+
 om_status om_linear_bwd_dx_gelu(om_ctx *ctx, const float *g, const float *w, const float *h, float *dh, int rows,
                                 int in, int out) {
     OM_CHECK_CTX(ctx);

@@ -60,6 +60,8 @@ struct Params {
     //   resid: v += resid[row * ldr + col] (a residual Add after the Linear);
     //   epi EPI_GELU: C gets v (the pre-activation, which GELU's backward reads) and out2 gets gelu(v);
     //   epi EPI_GELU_GRAD: C gets gelu_grad(v, aux[row * ldaux + col]) (GELU's backward of the product).
+    //   epi EPI_GELU_SLOPE: C gets gelu(v) and out2 gets GELU's slope at v (all GELU's backward needs);
+    //   epi EPI_MUL_AUX: C gets v * aux[row * ldaux + col] (GELU's backward of the product, given that slope).
     const float *resid;
     int64_t ldr;
     int epi;
@@ -75,7 +77,7 @@ struct Params {
     int db_acc;
 };
 
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2 };
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4 };
 
 // The epilogue of one finished dot product v at (row, col): alpha, mask, bias, residual, GELU terms, then C. The
 // GELU polynomials are compiled only into the instantiations that can be asked for them (GELU = true): inlined
@@ -88,8 +90,18 @@ __device__ __forceinline__ void epilogue(const Params &p, float *cbase, int64_t 
     if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
     if (p.resid) v = v + p.resid[(int64_t)row * p.ldr + col];
     if constexpr (GELU) {
-        if (p.epi == EPI_GELU) p.out2[(int64_t)row * p.ld2 + col] = omd::gelu(v);
-        else if (p.epi == EPI_GELU_GRAD) v = omd::gelu_grad(v, p.aux[(int64_t)row * p.ldaux + col]);
+        if (p.epi == EPI_GELU) {
+            p.out2[(int64_t)row * p.ld2 + col] = omd::gelu(v);
+        } else if (p.epi == EPI_GELU_GRAD) {
+            v = omd::gelu_grad(v, p.aux[(int64_t)row * p.ldaux + col]);
+        } else if (p.epi == EPI_GELU_SLOPE) {
+            float a, s;
+            omd::gelu_and_slope(v, a, s);
+            p.out2[(int64_t)row * p.ld2 + col] = s;
+            v = a;
+        } else if (p.epi == EPI_MUL_AUX) {
+            v = omd::canon(v * p.aux[(int64_t)row * p.ldaux + col]);
+        }
     }
     float *dst = cbase + (int64_t)row * ldc + col;
     *dst = p.accumulate ? *dst + v : v;

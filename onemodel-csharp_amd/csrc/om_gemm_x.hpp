@@ -235,6 +235,22 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
                 for (int r = 0; r < 4; r++)
 #pragma unroll
                     for (int j = 0; j < TN; j++) v[r][j] = omd::gelu_grad(v[r][j], t[r][j]);
+            } else if (p.epi == EPI_GELU_SLOPE) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        float a, s;
+                        omd::gelu_and_slope(v[r][j], a, s);
+                        p.out2[(int64_t)rowv[r] * p.ld2 + colv[j]] = s;
+                        v[r][j] = a;
+                    }
+            } else if (p.epi == EPI_MUL_AUX) {
+                gather(p.aux, p.ldaux);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) v[r][j] = omd::canon(v[r][j] * t[r][j]);
             }
         }
         if (p.accumulate) {

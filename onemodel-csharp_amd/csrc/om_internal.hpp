@@ -236,13 +236,27 @@ __device__ __forceinline__ float gelu(float x) {
     if (x == -__int_as_float(0x7F800000)) res = -0.0f;
     return canon(x == x ? res : x);
 }
-// GeluGradBin (TrainElementwise.cs:59-85): g * (0.5 (1 + erf(x/sqrt2)) + x exp(-x^2/2) / sqrt(2 pi)).
+// GELU's slope at v, the factor GeluGradBin multiplies the incoming gradient by (TrainElementwise.cs:59-85):
+// 0.5 (1 + erf(v/sqrt2)) + v exp(-v^2/2) / sqrt(2 pi), rounded as the reference rounds it, from erf_parts' erf.
+__device__ __forceinline__ float slope_from_erf(float v, float e) {
+    float cdf = 0.5f * (1.0f + e);
+    float pdf = exp_poly((-0.5f * v) * v) * 0.3989423f;
+    return cdf + v * pdf;
+}
+// GeluGradBin: g * slope(v). A slope saved by the forward and multiplied in later gives the same bits.
 __device__ __forceinline__ float gelu_grad(float g, float v) {
     float e, ope;
     erf_parts(v * 0.70710677f, e, ope);
-    float cdf = 0.5f * (1.0f + e);
-    float pdf = exp_poly((-0.5f * v) * v) * 0.3989423f;
-    return canon(g * (cdf + v * pdf));
+    return canon(g * slope_from_erf(v, e));
+}
+// gelu(x) and its slope from one erf evaluation.
+__device__ __forceinline__ void gelu_and_slope(float x, float &a, float &s) {
+    float e, ope;
+    erf_parts(x * 0.70710677f, e, ope);
+    float res = (0.5f * x) * ope;
+    if (x == -__int_as_float(0x7F800000)) res = -0.0f;
+    a = canon(x == x ? res : x);
+    s = slope_from_erf(x, e);
 }
 
 }  // namespace omd

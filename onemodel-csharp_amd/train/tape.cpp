@@ -410,14 +410,14 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
     ys.back() = o;
     if (resid && resid->shape != ys)
         shape_error("Add: shapes " + shape_str(resid->shape) + " and " + shape_str(ys) + " differ.");
-    float *h = dev().step_floats((int64_t)rows * f);  // pre-activation, read by GELU's backward
-    float *a = dev().step_floats((int64_t)rows * f);  // GELU output, read by Linear2's weight gradient
-    OMT(om_linear_gelu_fwd(C(), x->data, w1->data, b1 ? b1->data : nullptr, h, a, rows, d, f));
+    float *a = dev().step_floats((int64_t)rows * f);   // GELU output, read by Linear2's weight gradient
+    float *sl = dev().step_floats((int64_t)rows * f);  // GELU's slope at the pre-activation, all its backward needs
+    OMT(om_linear_gelu_fwd_slope(C(), x->data, w1->data, b1 ? b1->data : nullptr, a, sl, rows, d, f));
     Tensor y = make(ys);
     if (resid) OMT(om_linear_fwd_resid(C(), a, w2->data, b2 ? b2->data : nullptr, resid->data, y->data, rows, f, o));
     else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
     if (tracked({&x, &w1, &b1, &w2, &b2, &resid})) {
-        attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [h, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
+        attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [sl, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
             int aw2, ab2 = 0;
             float *dw2 = e.dest(r, 3, &aw2);
             float *db2 = r.inputs[4] ? e.dest(r, 4, &ab2) : nullptr;
@@ -425,7 +425,7 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
             const bool below = r.needs(0) || r.needs(1) || r.needs(2);
             if (below) {
                 float *dh = dev().step_floats((int64_t)rows * f);
-                OMT(om_linear_bwd_dx_gelu(C(), g, r.inputs[3]->data, h, dh, rows, f, o));
+                OMT(om_linear_bwd_dx_slope(C(), g, r.inputs[3]->data, sl, dh, rows, f, o));
                 int ax, aw1, ab1 = 0;
                 float *dx = e.dest(r, 0, &ax);
                 float *dw1 = e.dest(r, 1, &aw1);

@@ -163,6 +163,19 @@ def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     dh_exact = np.empty_like(da_dev)
     T.lib().or_gelu_bwd(T.fp(da_dev), T.fp(hin), T.fp(dh_exact), C.c_int64(da_dev.size))
     assert np.array_equal(dev.get(DH).view(np.uint32), dh_exact.view(np.uint32))
+    # The slope pair: the forward's a equals om_linear_gelu_fwd's, its s is GELU's slope at h (GeluGradBin with a unit
+    # gradient), and the backward from a saved slope equals om_linear_bwd_dx_gelu bit for bit.
+    A2, S = dev.empty((rows, outf)), dev.empty((rows, outf))
+    dev.call("om_linear_gelu_fwd_slope", X, W, Bb, A2, S, rows, inf, outf)
+    assert np.array_equal(dev.get(A2).view(np.uint32), dev.get(A).view(np.uint32))
+    s_ref = np.empty_like(h)
+    T.lib().or_gelu_bwd(T.fp(np.ones_like(h)), T.fp(h), T.fp(s_ref), C.c_int64(h.size))
+    assert np.array_equal(dev.get(S).view(np.uint32), s_ref.view(np.uint32))
+    s_in = np.empty_like(hin)
+    T.lib().or_gelu_bwd(T.fp(np.ones_like(hin)), T.fp(hin), T.fp(s_in), C.c_int64(hin.size))
+    SI, DH2 = dev.put(s_in), dev.empty((rows, inf))
+    dev.call("om_linear_bwd_dx_slope", G, W, SI, DH2, rows, inf, outf)
+    assert np.array_equal(dev.get(DH2).view(np.uint32), dev.get(DH).view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------------ element-wise
