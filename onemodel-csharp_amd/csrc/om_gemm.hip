@@ -253,6 +253,12 @@ const Tuned kTuned[] = {
     {768, 768, 4096, true, false, 64, 96, 32, 8},     {3072, 768, 4096, true, false, 64, 96, 32, 2},
     {768, 3072, 4096, true, false, 64, 96, 32, 2},    {2304, 768, 4096, true, false, 64, 96, 32, 2},
 };
+// The same for products with a GELU epilogue (GELU and its slope in the forward, the slope product in the input
+// gradient), whose element-wise tail shifts the best tile.
+const Tuned kTunedEpi[] = {
+    {4096, 1536, 384, false, true, 64, 64, 32, 1},
+    {4096, 1536, 384, false, false, 64, 96, 33, 1},
+};
 
 // K length of one split: k / splits rounded up to whole chunks.
 int split_len(int k, int splits, int bkt) { return ((k + splits - 1) / splits + bkt - 1) / bkt * bkt; }
@@ -288,9 +294,13 @@ bool x_disabled() {
 //     slices of at least 256 k, with tiles x splits near three workgroups per CU (64 x 96 tiles when N allows);
 //   - otherwise 64 x 96 when N is a multiple of 96 and its tiles fit in one round of the CUs (4096 x 384 becomes
 //     exactly 256 tiles: one per CU), else 64 x 64 (occupancy 4, best once there are several tiles per CU).
-Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus) {
+Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bool epi) {
     Choice best{64, 64, 1, k, 32};
     if (env_override(best, k)) return best;
+    if (batch == 1 && epi)
+        for (const Tuned &t : kTunedEpi)
+            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
+                return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
     if (batch == 1)
         for (const Tuned &t : kTuned)
             if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
@@ -335,7 +345,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     bool fast = vec && !(ta && tb) && p.k > 0 && p.m > 32 && p.n > 32 && p.m % 4 == 0 && p.n % 4 == 0 &&
                 p.k % 4 == 0;
     Choice c = p.k <= 0 ? Choice{64, 64, 1, 1, 16}
-                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus)
+                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus, p.epi != EPI_NONE)
                                 : choose(p.m, p.n, p.k, batch, ctx->num_cus));
     if (fast && p.epi != EPI_NONE) {  // only some tiles carry the GELU epilogue
         const bool ok = ((c.bkt == 32 || c.bkt == 33) && c.bm == 64 && (c.bn == 64 || c.bn == 96)) ||

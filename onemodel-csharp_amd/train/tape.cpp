@@ -99,9 +99,12 @@ float *Engine::dest(Record &r, int i, int *acc) {
     if (i >= (int)r.inputs.size() || !r.needs(i)) return nullptr;
     TensorImpl &x = *r.inputs[i];
     if (x.is_leaf()) {
-        // AccumulateLeaf (Engine.cs:292-328): the first gradient creates Grad, later ones add into it.
+        // AccumulateLeaf (Engine.cs:292-328): the first gradient creates Grad, later ones add into it. A gradient
+        // added into must be complete on the main stream: in overlap mode its earlier part may come from a launch
+        // on the second stream.
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
         *acc = x.grad_live ? 1 : 0;
+        if (x.grad_live) OMT(om_ctx_join(C()));
         x.grad_live = x.grad_exists = true;
         return x.grad;
     }
@@ -134,8 +137,12 @@ void Engine::emit_alias(Record &r, int i, const float *g) {
     uint64_t bytes = sizeof(float) * (uint64_t)x.numel;
     if (x.is_leaf()) {
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
-        if (x.grad_live) OMT(om_axpy(C(), 1.0f, g, x.grad, x.numel));
-        else OMT(om_copy(C(), x.grad, g, bytes));
+        if (x.grad_live) {
+            OMT(om_ctx_join(C()));
+            OMT(om_axpy(C(), 1.0f, g, x.grad, x.numel));
+        } else {
+            OMT(om_copy(C(), x.grad, g, bytes));
+        }
         x.grad_live = x.grad_exists = true;
         return;
     }
