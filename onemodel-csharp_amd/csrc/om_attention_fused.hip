@@ -32,15 +32,29 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Copies `rows` rows of D floats (global stride ld) into LDS rows of stride D + 4.
-template <int D, int NTH>
-__device__ __forceinline__ void stage(float *dst, const float *src, int64_t ld, int rows) {
-    constexpr int Q4 = D / 4;
-    for (int f = threadIdx.x; f < rows * Q4; f += NTH) {
-        int r = f / Q4, c = (f % Q4) * 4;
-        *reinterpret_cast<floatx4 *>(&dst[r * (D + 4) + c]) = *reinterpret_cast<const floatx4 *>(src + r * ld + c);
+// Staging of ROWS rows of D floats (global stride ld) into LDS rows of stride D + 4, in two steps: load() issues all
+// of this thread's global loads into registers, store() writes them to LDS. Callers issue the loads of every operand
+// before the first store, so the loads' latencies overlap instead of following one another.
+template <int D, int NTH, int ROWS>
+struct Stage {
+    static constexpr int Q4 = D / 4, TOT = ROWS * Q4, PER = (TOT + NTH - 1) / NTH;
+    floatx4 v[PER];
+    __device__ __forceinline__ void load(const float *src, int64_t ld) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int f = (int)threadIdx.x + i * NTH;
+            if (TOT % NTH == 0 || f < TOT)
+                v[i] = *reinterpret_cast<const floatx4 *>(src + (int64_t)(f / Q4) * ld + (f % Q4) * 4);
+        }
     }
-}
+    __device__ __forceinline__ void store(float *dst) const {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int f = (int)threadIdx.x + i * NTH;
+            if (TOT % NTH == 0 || f < TOT) *reinterpret_cast<floatx4 *>(&dst[(f / Q4) * (D + 4) + (f % Q4) * 4]) = v[i];
+        }
+    }
+};
 
 // S = scale * X Y^T (+ mask) for the 16 rows x0.. of X against all L rows of Y (both staged [rows][D+4]):
 // s[j] holds columns 16j.. in the MFMA result layout (lane t, group kl, register r = row 4kl+r, column 16j+t).
@@ -178,15 +192,25 @@ __global__ void __launch_bounds__(256) k_attn_fwd(const float *__restrict__ q, c
 #pragma unroll
         for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
     }
-    stage<D, 256>(Ks, k + row0 * ld + h * D, ld, L);
-    {  // V^T: thread f takes key f % L and four d from f / L, so each store row is contiguous across the lanes
-        const float *vg = v + row0 * ld + h * D;
-        for (int f = threadIdx.x; f < L * (D / 4); f += 256) {
-            const int key = f % L, c = (f / L) * 4;
-            const floatx4 x = *reinterpret_cast<const floatx4 *>(vg + (int64_t)key * ld + c);
+    // K rows and V^T, all loads first. V^T: thread f takes key f % L and four d from f / L, so each store row is
+    // contiguous across the lanes.
+    Stage<D, 256, L> ks;
+    ks.load(k + row0 * ld + h * D, ld);
+    constexpr int VPER = L * (D / 4) / 256;
+    static_assert(L * (D / 4) % 256 == 0, "V^T staging covers whole rounds of the workgroup");
+    floatx4 vx[VPER];
+    const float *vg = v + row0 * ld + h * D;
 #pragma unroll
-            for (int i = 0; i < 4; i++) Vt[(c + i) * LDV + key] = x[i];
-        }
+    for (int i = 0; i < VPER; i++) {
+        const int f = (int)threadIdx.x + i * 256, key = f % L, c = (f / L) * 4;
+        vx[i] = *reinterpret_cast<const floatx4 *>(vg + (int64_t)key * ld + c);
+    }
+    ks.store(Ks);
+#pragma unroll
+    for (int i = 0; i < VPER; i++) {
+        const int f = (int)threadIdx.x + i * 256, key = f % L, c = (f / L) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) Vt[(c + e) * LDV + key] = vx[i][e];
     }
     __syncthreads();
     floatx4 s[NB];
@@ -272,10 +296,17 @@ __global__ void __launch_bounds__(L * 4) k_attn_bwd(const float *__restrict__ q,
     const int q0 = 16 * w;  // this wavefront's queries; also its block of 16 keys for dK and dV
     float mv[4][L / 16];
     load_mask<L>(mv, mask ? mask + b * mask_bstride + (int64_t)(q0 + 4 * kl) * L : nullptr, t);
-    stage<D, NTH>(Qs, q + row0 * ld + h * D, ld, L);
-    stage<D, NTH>(Ks, k + row0 * ld + h * D, ld, L);
-    stage<D, NTH>(Vs, v + row0 * ld + h * D, ld, L);
-    stage<D, NTH>(Gs, g + row0 * ldg + h * D, ldg, L);
+    {  // all four operands' loads in flight before the first LDS store
+        Stage<D, NTH, L> sq, sk, sv, sg;
+        sq.load(q + row0 * ld + h * D, ld);
+        sk.load(k + row0 * ld + h * D, ld);
+        sv.load(v + row0 * ld + h * D, ld);
+        sg.load(g + row0 * ldg + h * D, ldg);
+        sq.store(Qs);
+        sk.store(Ks);
+        sv.store(Vs);
+        sg.store(Gs);
+    }
     __syncthreads();
     floatx4 s[NB];
     scores<D, L>(s, Qs, Ks, q0, t, kl);
