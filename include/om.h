@@ -152,6 +152,21 @@ om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, 
                                    int rows, int in, int out);
 om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,
                                  int in, int out);
+/* Weight (and bias) gradients of several Linear layers whose inputs share the row count, in one launch: item i gets
+ * dw_i (+)= g_i^T x_i ([out_i, in_i], g_i [rows, out_i], x_i [rows, in_i]) and db_i (+)= fp64 column sums of g_i,
+ * the MatMul and SumTo rules of om_linear_bwd (BackwardOps.cs:69-82, 201-269). Up to four items whose sizes are
+ * multiples of 64 share one tile-exact launch and one split-K reduce (their tiles fill the device together instead
+ * of each launch ramping up and down alone); other calls run the items one by one through om_linear_bwd. Either
+ * way each item's result is a GEMM of the library within its tolerance; the grouped launch fixes its tile and split
+ * from the group, so its bits may differ from a lone om_linear_bwd of the same item. dw or db may be NULL. */
+typedef struct {
+    const float *g;
+    const float *x;
+    float *dw;
+    float *db;
+    int32_t in, out, acc_dw, acc_db;
+} om_linear_dw;
+om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *items, int rows);
 /* Bias gradient alone: db[n] (+)= (float) sum over rows of g[row, n] in double (BackwardOps.SumTo). */
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate);
 

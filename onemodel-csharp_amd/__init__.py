@@ -50,6 +50,7 @@ _OM_SIGS = {
     "om_linear_bwd_dx_gelu": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_gelu_fwd_slope": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd_dx_slope": [vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_linear_bwd_dw_group": [vp, ci, vp, ci],
     "om_colsum": [vp, vp, vp, ci, ci, ci],
     "om_relu_fwd": [vp, vp, vp, i64],
     "om_relu_bwd": [vp, vp, vp, vp, i64, ci],
@@ -146,6 +147,11 @@ def load_hip():
 
 def om_symbols():
     return list(_OM_SIGS)
+
+
+class om_linear_dw(C.Structure):
+    _fields_ = [("g", vp), ("x", vp), ("dw", vp), ("db", vp), ("in_", i32), ("out", i32), ("acc_dw", i32),
+                ("acc_db", i32)]
 
 
 class omt_scale(C.Structure):

@@ -83,36 +83,60 @@ __global__ void k_splitk_reduce(Params p) {
 // The same reduction for n % 4 == 0 and a split count known at compile time: a thread per float4 of C issues the S
 // loads of its partials before adding them in split order (0 + p0 + p1 + ...), so the result is k_splitk_reduce's.
 template <int S>
-__global__ void k_splitk_reduce_s(Params p) {
-    const int64_t total = (int64_t)p.m * p.n;
+__device__ __forceinline__ void reduce_bias_row(const Params &p, int i) {
+    double t = 0.0;
+#pragma unroll
+    for (int s = 0; s < S; s++) t += p.colsum_ws[(int64_t)s * p.m + i];
+    float v = (float)t;
+    p.db[i] = p.db_acc ? p.db[i] + v : v;
+}
+template <int S>
+__device__ __forceinline__ void reduce_quad(const Params &p, int64_t q) {
     const int nq = p.n / 4;
-    const int64_t quads = (int64_t)p.m * nq;
+    const int row = (int)(q / nq), col0 = (int)(q % nq) * 4;
+    const float *src = p.ws + (int64_t)row * p.n + col0;
+    const int64_t total = (int64_t)p.m * p.n;
+    float4 t[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) t[s] = *reinterpret_cast<const float4 *>(src + s * total);
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        v[0] += t[s].x;
+        v[1] += t[s].y;
+        v[2] += t[s].z;
+        v[3] += t[s].w;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) epilogue(p, p.c, p.ldc, nullptr, row, col0 + u, v[u]);
+}
+template <int S>
+__global__ void k_splitk_reduce_s(Params p) {
+    const int64_t quads = (int64_t)p.m * (p.n / 4);
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p.colsum_ws)
-        for (int64_t i = gid; i < p.m; i += stride) {
-            double t = 0.0;
+        for (int64_t i = gid; i < p.m; i += stride) reduce_bias_row<S>(p, (int)i);
+    for (int64_t q = gid; q < quads; q += stride) reduce_quad<S>(p, q);
+}
+// The reduce of a grouped weight-gradient launch: the same per-row and per-quad work over every product in turn.
+template <int S>
+__global__ void k_splitk_reduce_group(GroupParams g) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t r = gid; r < g.rstart[g.count]; r += stride) {
+        int i = 0;
 #pragma unroll
-            for (int s = 0; s < S; s++) t += p.colsum_ws[(int64_t)s * p.m + i];
-            float v = (float)t;
-            p.db[i] = p.db_acc ? p.db[i] + v : v;
-        }
-    for (int64_t q = gid; q < quads; q += stride) {
-        const int row = (int)(q / nq), col0 = (int)(q % nq) * 4;
-        const float *src = p.ws + (int64_t)row * p.n + col0;
-        float4 t[S];
+        for (int j = 1; j < kMaxGroup; j++)
+            if (j < g.count && r >= g.rstart[j]) i = j;
+        reduce_bias_row<S>(g.p[i], (int)(r - g.rstart[i]));
+    }
+    for (int64_t q = gid; q < g.qstart[g.count]; q += stride) {
+        int i = 0;
 #pragma unroll
-        for (int s = 0; s < S; s++) t[s] = *reinterpret_cast<const float4 *>(src + s * total);
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            v[0] += t[s].x;
-            v[1] += t[s].y;
-            v[2] += t[s].z;
-            v[3] += t[s].w;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) epilogue(p, p.c, p.ldc, nullptr, row, col0 + u, v[u]);
+        for (int j = 1; j < kMaxGroup; j++)
+            if (j < g.count && q >= g.qstart[j]) i = j;
+        reduce_quad<S>(g.p[i], q - g.qstart[i]);
     }
 }
 
@@ -407,6 +431,93 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     return OM_LAUNCH_CHECK(ctx, what);
 }
 
+// Weight gradients dw_i (+)= g_i^T x_i of 2..kMaxGroup products sharing K = rows, with fused bias gradients, in one
+// tile-exact launch (and one split-K reduce). Returns false, launching nothing, when the products do not fit it:
+// then the caller runs them one by one. The tile is 64 x 96 when every product's width allows it, else 64 x 64; the
+// K split is the smallest power of two giving about three workgroups per CU. Each product's arithmetic is that of
+// k_gemm_x at that tile and split.
+static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int rows, om_status *st) {
+    *st = OM_OK;
+    if (count < 2 || count > kMaxGroup || rows <= 0 || x_disabled()) return false;
+    bool n96 = true;
+    for (int i = 0; i < count; i++) {
+        const om_linear_dw &d = it[i];
+        auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+        if (!d.dw || d.out % 64 || d.in % 64 || !al(d.g) || !al(d.x) || !al(d.dw)) return false;
+        if (d.in % 96) n96 = false;
+    }
+    const int bn = n96 ? 96 : 64;
+    int64_t tiles = 0;
+    for (int i = 0; i < count; i++) tiles += (int64_t)(it[i].out / 64) * (it[i].in / bn);
+    int splits = 1;
+    while (splits < 16 && tiles * splits < 3 * (int64_t)ctx->num_cus && rows % (2 * splits * 32) == 0 &&
+           rows / (2 * splits) >= 256)
+        splits *= 2;
+    if (rows % (splits * 32)) return false;
+    const int k_split = rows / splits;
+    GroupParams g{};
+    g.count = count;
+    uint64_t ws_floats = 0, cs_doubles = 0;
+    for (int i = 0; i < count; i++) {
+        const om_linear_dw &d = it[i];
+        Params p = dense_params(d.out, d.in, rows, d.g, d.out, d.x, d.in, d.dw, d.in);
+        p.accumulate = d.acc_dw;
+        p.db = d.db;
+        p.db_acc = d.acc_db;
+        p.batch = 1;
+        p.splits = splits;
+        p.k_split = k_split;
+        if (!x_fits(XTile{64, bn, 32}, p, splits, k_split)) return false;
+        ws_floats += splits > 1 ? (uint64_t)splits * d.out * d.in : 0;
+        cs_doubles += splits > 1 && d.db ? (uint64_t)splits * d.out : 0;
+        g.p[i] = p;
+    }
+    if (splits > 1) {
+        const uint64_t cbytes = (sizeof(double) * cs_doubles + 255) / 256 * 256;
+        float *ws;
+        *st = om::scratch(ctx, cbytes + sizeof(float) * ws_floats, &ws);
+        if (*st) return true;
+        double *cs = reinterpret_cast<double *>(ws);
+        float *w = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
+        for (int i = 0; i < count; i++) {
+            Params &p = g.p[i];
+            p.ws = w;
+            w += (uint64_t)splits * p.m * p.n;
+            if (p.db) {
+                p.colsum_ws = cs;
+                cs += (uint64_t)splits * p.m;
+            }
+        }
+    }
+    g.start[0] = 0;
+    g.qstart[0] = 0;
+    g.rstart[0] = 0;
+    for (int i = 0; i < count; i++) {
+        const Params &p = g.p[i];
+        g.start[i + 1] = g.start[i] + (p.m / 64) * (p.n / bn) * splits;
+        g.qstart[i + 1] = g.qstart[i] + (int64_t)p.m * (p.n / 4);
+        g.rstart[i + 1] = g.rstart[i] + (splits > 1 && p.db ? p.m : 0);
+    }
+    for (int i = count; i < kMaxGroup; i++) {
+        g.start[i + 1] = g.start[count];
+        g.qstart[i + 1] = g.qstart[count];
+        g.rstart[i + 1] = g.rstart[count];
+    }
+    hipStream_t stream = om::cur_stream(ctx);
+    if (bn == 96) hipLaunchKernelGGL((gx::k_gemm_x_tn_group<64, 96, 32>), dim3(g.start[count]), dim3(NT), 0, stream, g);
+    else hipLaunchKernelGGL((gx::k_gemm_x_tn_group<64, 64, 32>), dim3(g.start[count]), dim3(NT), 0, stream, g);
+    *st = OM_LAUNCH_CHECK(ctx, "om_linear_bwd_dw_group");
+    if (*st || splits == 1) return true;
+    const int64_t units = g.qstart[count] > g.rstart[count] ? g.qstart[count] : g.rstart[count];
+    const dim3 grid(om::grid1d(units, 256, 4096));
+    if (splits == 2) hipLaunchKernelGGL(k_splitk_reduce_group<2>, grid, dim3(256), 0, stream, g);
+    else if (splits == 4) hipLaunchKernelGGL(k_splitk_reduce_group<4>, grid, dim3(256), 0, stream, g);
+    else if (splits == 8) hipLaunchKernelGGL(k_splitk_reduce_group<8>, grid, dim3(256), 0, stream, g);
+    else hipLaunchKernelGGL(k_splitk_reduce_group<16>, grid, dim3(256), 0, stream, g);
+    *st = OM_LAUNCH_CHECK(ctx, "om_linear_bwd_dw_group reduce");
+    return true;
+}
+
 Params dense_params(int m, int n, int k, const float *a, int64_t lda, const float *b, int64_t ldb, float *c,
                     int64_t ldc) {
     Params p{};
@@ -533,6 +644,26 @@ om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, 
     p.out2 = s;
     p.ld2 = out;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd_slope");
+}
+
+om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *items, int rows) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, count >= 0 && (count == 0 || items) && rows >= 0, "om_linear_bwd_dw_group: bad arguments");
+    for (int i = 0; i < count; i++)
+        OM_REQUIRE(ctx, items[i].g && items[i].x && items[i].in > 0 && items[i].out > 0,
+                   "om_linear_bwd_dw_group: item %d has a NULL input or a non-positive size", i);
+    om_status s = OM_OK;
+    // In overlap mode the grouped launch goes to the weight-gradient stream, like om_linear_bwd's dW.
+    if (ctx->overlap && (s = om::fork(ctx))) return s;
+    const bool grouped = omg::launch_dw_group(ctx, count, items, rows, &s);
+    if (ctx->overlap) om::unfork(ctx);
+    if (grouped) return s;
+    for (int i = 0; i < count && !s; i++) {
+        const om_linear_dw &d = items[i];
+        if (d.dw || d.db)
+            s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw, d.acc_db);
+    }
+    return s;
 }
 
 om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,

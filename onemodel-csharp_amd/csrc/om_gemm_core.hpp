@@ -79,6 +79,18 @@ struct Params {
 
 enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4 };
 
+// Several products launched together (the grouped weight-gradient kernel and its reduce): product i owns workgroups
+// [start[i], start[i+1]) of the GEMM launch, float4 quads [qstart[i], qstart[i+1]) and bias rows
+// [rstart[i], rstart[i+1]) of the reduce.
+constexpr int kMaxGroup = 4;
+struct GroupParams {
+    Params p[kMaxGroup];
+    int start[kMaxGroup + 1];
+    int64_t qstart[kMaxGroup + 1];
+    int rstart[kMaxGroup + 1];
+    int count;
+};
+
 // The epilogue of one finished dot product v at (row, col): alpha, mask, bias, residual, GELU terms, then C. The
 // GELU polynomials are compiled only into the instantiations that can be asked for them (GELU = true): inlined
 // into every large-tile kernel they would raise register pressure enough to spill.

@@ -267,8 +267,10 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
     }
 }
 
-template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
-__global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
+// One tile (tm, tn) of batch-and-split index zz, by one workgroup of NT threads: the body of k_gemm_x and of the
+// grouped weight-gradient kernel.
+template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU>
+__device__ __forceinline__ void gemm_x_tile(const Params &p, int tm, int tn, int zz) {
     constexpr bool AK = !TA, BKL = TB;  // operands in K layout
     constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
     using LA = Ld<BM, BKT, AK>;
@@ -276,9 +278,6 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     __shared__ __attribute__((aligned(16))) float As[2 * LA::LDSZ];
     __shared__ __attribute__((aligned(16))) float Bs[2 * LB::LDSZ];
 
-    const int tiles_n = p.n / BN, tiles_m = p.m / BM;
-    int tm, tn, zz;
-    tile_coords(p, tiles_n, tiles_m, tm, tn, zz);
     if (zz >= p.batch * p.splits) return;
     const int z = zz / p.splits, split = zz % p.splits;
     const int outer = z / p.batch_div, inner = z % p.batch_div;
@@ -387,6 +386,30 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
     tile_epilogue<TM, TN, AK, BKL, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
+}
+
+template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
+__global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
+    int tm, tn, zz;
+    tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
+    gemm_x_tile<BM, BN, BKT, TA, TB, GELU>(p, tm, tn, zz);
+}
+
+// Weight gradients of several products in one launch (om_linear_bwd_dw_group): product i owns the workgroups
+// [start[i], start[i+1]) of the XCD-remapped grid, each a (tile, split) of its own Params, run by the same tile body.
+template <int BM, int BN, int BKT>
+__global__ void __launch_bounds__(NT) k_gemm_x_tn_group(GroupParams g) {
+    int lin = blockIdx.x;
+    const int total = gridDim.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxGroup; j++)
+        if (j < g.count && lin >= g.start[j]) i = j;
+    const Params &p = g.p[i];
+    const int local = lin - g.start[i], tiles_n = p.n / BN, tiles_m = p.m / BM;
+    const int rest = local / tiles_n;
+    gemm_x_tile<BM, BN, BKT, true, false, false>(p, rest % tiles_m, local % tiles_n, rest / tiles_m);
 }
 
 // The same tile with eight wavefronts: two groups of four (2 x 2 over the tile, as above) split each chunk's 16-k

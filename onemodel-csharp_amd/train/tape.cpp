@@ -425,10 +425,14 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
     else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
     if (tracked({&x, &w1, &b1, &w2, &b2, &resid})) {
         attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [sl, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
+            // The input-gradient chain first (dh = (g W2) * GELU's slope, then dx = dh W1), then both layers' weight
+            // and bias gradients in one grouped launch.
             int aw2, ab2 = 0;
             float *dw2 = e.dest(r, 3, &aw2);
             float *db2 = r.inputs[4] ? e.dest(r, 4, &ab2) : nullptr;
-            OMT(om_linear_bwd(C(), g, a, r.inputs[3]->data, nullptr, dw2, db2, rows, f, o, 0, aw2, ab2));
+            om_linear_dw items[2];
+            int n = 0;
+            if (dw2 || db2) items[n++] = om_linear_dw{g, a, dw2, db2, f, o, aw2, ab2};
             const bool below = r.needs(0) || r.needs(1) || r.needs(2);
             if (below) {
                 float *dh = dev().step_floats((int64_t)rows * f);
@@ -437,9 +441,12 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
                 float *dx = e.dest(r, 0, &ax);
                 float *dw1 = e.dest(r, 1, &aw1);
                 float *db1 = r.inputs[2] ? e.dest(r, 2, &ab1) : nullptr;
-                OMT(om_linear_bwd(C(), dh, r.inputs[0]->data, r.inputs[1]->data, dx, dw1, db1, rows, d, f, ax, aw1,
-                                  ab1));
+                if (dx)
+                    OMT(om_linear_bwd(C(), dh, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, d, f,
+                                      ax, 0, 0));
+                if (dw1 || db1) items[n++] = om_linear_dw{dh, r.inputs[0]->data, dw1, db1, d, f, aw1, ab1};
             }
+            if (n) OMT(om_linear_bwd_dw_group(C(), n, items, rows));
             if (r.needs(5)) e.emit_alias(r, 5, g);
         });
     }

@@ -125,6 +125,43 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
 
 
+@pytest.mark.parametrize("rows,shapes", [
+    (4096, [(384, 1536), (1536, 384)]),                # the FFN pair (in, out): one grouped launch, 64 x 96 tiles
+    (4096, [(384, 384), (384, 1152), (384, 384)]),     # attention-shaped: three products, 64 x 96 tiles
+    (512, [(64, 192), (128, 64)]),                     # 64 x 64 tiles, few splits
+    (100, [(20, 36), (36, 20)]),                       # ragged: item by item through om_linear_bwd
+], ids=["ffn-pair", "attention-triple", "small-64", "ragged"])
+def test_linear_dw_group(dev, T, rows, shapes):
+    """om_linear_bwd_dw_group: every item's dW and db to the GEMM tolerance against the oracle (the last item of
+    each group without a bias gradient), then a second call accumulating into the same leaves."""
+    rng = np.random.default_rng(rows + len(shapes))
+    Item = dev.pkg.om_linear_dw
+    refs, bufs, items = [], [], (Item * len(shapes))()
+    for i, (inf, outf) in enumerate(shapes):
+        x, g = rnd(rng, rows, inf), rnd(rng, rows, outf)
+        w = rnd(rng, outf, inf, scale=0.1)
+        dx_r, dw_r, db_r = np.empty_like(x), np.empty_like(w), np.empty(outf, np.float32)
+        T.lib().or_linear_bwd(T.fp(g), T.fp(x), T.fp(w), T.fp(dx_r), T.fp(dw_r), T.fp(db_r), rows, inf, outf)
+        X, G, DW = dev.put(x), dev.put(g), dev.empty((outf, inf), fill=7.0)
+        DB = dev.empty((outf,), fill=7.0) if i + 1 < len(shapes) else None
+        bufs.append((X, G, DW, DB))
+        refs.append((dw_r, db_r))
+        items[i] = Item(G.data_ptr(), X.data_ptr(), DW.data_ptr(), DB.data_ptr() if DB is not None else None, inf,
+                        outf, 0, 0)
+    dev.call("om_linear_bwd_dw_group", len(shapes), C.cast(items, C.c_void_p), rows)
+    for (X, G, DW, DB), (dw_r, db_r) in zip(bufs, refs):
+        assert scaled(dev.get(DW), dw_r) <= TOL
+        if DB is not None:
+            assert scaled(dev.get(DB), db_r) <= 1e-7
+    for i in range(len(shapes)):
+        items[i].acc_dw = items[i].acc_db = 1
+    dev.call("om_linear_bwd_dw_group", len(shapes), C.cast(items, C.c_void_p), rows)
+    for (X, G, DW, DB), (dw_r, db_r) in zip(bufs, refs):
+        assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
+        if DB is not None:
+            assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
+
+
 @pytest.mark.parametrize("rows,inf,outf", [(4096, 384, 1536), (4096, 1536, 384), (256, 64, 192), (100, 36, 20)])
 def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     """om_linear_fwd_resid (Linear then the residual Add), om_linear_gelu_fwd (Linear then GELU, keeping the
