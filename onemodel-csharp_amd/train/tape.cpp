@@ -94,6 +94,30 @@ static std::string shape_str(const std::vector<int> &s) {
 [[noreturn]] static void shape_error(const std::string &m) { throw Error(OM_E_ARG, m); }
 
 // ------------------------------------------------------------------------------------------------ engine
+void Engine::queue_dw(const om_linear_dw &item, int rows) {
+    if (!item.dw && !item.db) return;
+    if (!dw_queue_.empty() && (rows != dw_rows_ || dw_queue_.size() == 4)) flush_dw();
+    dw_queue_.push_back(item);
+    dw_rows_ = rows;
+    holders_[item.g]++;
+    if (item.dw) {
+        const char *b = reinterpret_cast<const char *>(item.dw);
+        dw_ranges_.emplace_back(b, b + sizeof(float) * (uint64_t)item.in * item.out);
+    }
+    if (item.db) {
+        const char *b = reinterpret_cast<const char *>(item.db);
+        dw_ranges_.emplace_back(b, b + sizeof(float) * (uint64_t)item.out);
+    }
+}
+
+void Engine::flush_dw() {
+    if (dw_queue_.empty()) return;
+    OMT(om_linear_bwd_dw_group(C(), (int)dw_queue_.size(), dw_queue_.data(), dw_rows_));
+    for (const om_linear_dw &it : dw_queue_) holders_[it.g]--;
+    dw_queue_.clear();
+    dw_ranges_.clear();
+}
+
 float *Engine::dest(Record &r, int i, int *acc) {
     *acc = 0;
     if (i >= (int)r.inputs.size() || !r.needs(i)) return nullptr;
@@ -103,6 +127,7 @@ float *Engine::dest(Record &r, int i, int *acc) {
         // added into must be complete on the main stream: in overlap mode its earlier part may come from a launch
         // on the second stream.
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
+        if (queued_leaf(x.grad)) flush_dw();  // a queued launch writes this gradient first
         *acc = x.grad_live ? 1 : 0;
         if (x.grad_live) OMT(om_ctx_join(C()));
         x.grad_live = x.grad_exists = true;
@@ -137,6 +162,7 @@ void Engine::emit_alias(Record &r, int i, const float *g) {
     uint64_t bytes = sizeof(float) * (uint64_t)x.numel;
     if (x.is_leaf()) {
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
+        if (queued_leaf(x.grad)) flush_dw();  // a queued launch writes this gradient first
         if (x.grad_live) {
             OMT(om_ctx_join(C()));
             OMT(om_axpy(C(), 1.0f, g, x.grad, x.numel));
@@ -210,6 +236,7 @@ void Engine::run(const Tensor &root) {
         r->rule(*this, *r, gi);
         holders_[gi]--;  // this record is done with its gradient
     }
+    flush_dw();
     holders_.clear();
     // Release the records (BackwardRecord.Release): a second backward through this graph is an error.
     for (Record *r : order) {
@@ -269,9 +296,11 @@ Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
         attach(y, "Linear", ins, [rows, in, out](Engine &e, Record &r, const float *g) {
             int ax, aw, ab = 0;
             float *dx = e.dest(r, 0, &ax);
+            if (dx) OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, in, out,
+                                      ax, 0, 0));
             float *dw = e.dest(r, 1, &aw);
             float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
-            OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw, ab));
+            e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
         });
     }
     return y;
@@ -396,9 +425,11 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
         attach(y, "LinearAdd", {x, w, b, resid}, [rows, in, out](Engine &e, Record &r, const float *g) {
             int ax, aw, ab = 0;
             float *dx = e.dest(r, 0, &ax);
+            if (dx) OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, in, out,
+                                      ax, 0, 0));
             float *dw = e.dest(r, 1, &aw);
             float *db = r.inputs[2] ? e.dest(r, 2, &ab) : nullptr;
-            OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw, ab));
+            e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
             if (r.needs(3)) e.emit_alias(r, 3, g);  // Add backward: the residual gets g unchanged
         });
     }
@@ -425,8 +456,8 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
     else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
     if (tracked({&x, &w1, &b1, &w2, &b2, &resid})) {
         attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [sl, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
-            // The input-gradient chain first (dh = (g W2) * GELU's slope, then dx = dh W1), then both layers' weight
-            // and bias gradients in one grouped launch.
+            // The input-gradient chain (dh = (g W2) * GELU's slope, then dx = dh W1); both layers' weight and bias
+            // gradients are queued for a grouped launch.
             int aw2, ab2 = 0;
             float *dw2 = e.dest(r, 3, &aw2);
             float *db2 = r.inputs[4] ? e.dest(r, 4, &ab2) : nullptr;
@@ -446,7 +477,7 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
                                       ax, 0, 0));
                 if (dw1 || db1) items[n++] = om_linear_dw{dh, r.inputs[0]->data, dw1, db1, d, f, aw1, ab1};
             }
-            if (n) OMT(om_linear_bwd_dw_group(C(), n, items, rows));
+            for (int i = 0; i < n; i++) e.queue_dw(items[i], rows);
             if (r.needs(5)) e.emit_alias(r, 5, g);
         });
     }
@@ -499,6 +530,13 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
                    const bool any_w = d[0] || d[2] || d[4], any_b = d[1] || d[3] || d[5];
                    float *dw = !any_w ? nullptr : dw_direct ? d[0] : dev().step_floats(3 * WW);
                    float *db = !any_b ? nullptr : db_direct ? d[1] : dev().step_floats(3 * W);
+                   if ((!any_w || dw_direct) && (!any_b || db_direct)) {
+                       // the packed leaves' gradients directly: the input gradient now, dW and db queued
+                       if (dx) OMT(om_linear_bwd(C(), dqkv, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr,
+                                                 rows, w, 3 * w, ax, 0, 0));
+                       e.queue_dw(om_linear_dw{dqkv, r.inputs[0]->data, dw, db, w, 3 * w, a[0], a[1]}, rows);
+                       return;
+                   }
                    OMT(om_linear_bwd(C(), dqkv, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, w, 3 * w, ax,
                                      dw_direct ? a[0] : 0, db_direct ? a[1] : 0));
                    for (int i = 0; i < 6; i++) {

@@ -100,9 +100,26 @@ class Engine {
     // Hands the incoming gradient itself on to input i (EmitAliased, Engine.cs:245-249): no copy unless it has to
     // be added to an existing gradient.
     void emit_alias(Record &r, int i, const float *g);
+    // Queues a Linear layer's weight and bias gradients (dw (+)= g^T x, db (+)= column sums of g); queued items of
+    // the same row count are launched together (om_linear_bwd_dw_group), up to four at a time, when the queue is
+    // full, when another gradient is about to be added into one of their leaf gradients, and when the pass ends.
+    // Until then g stays pinned: it counts as held, so no record writes into it in place.
+    void queue_dw(const om_linear_dw &item, int rows);
+    void flush_dw();
     void run(const Tensor &root);
 
    private:
+    std::vector<om_linear_dw> dw_queue_;
+    int dw_rows_ = 0;
+    // Leaf gradient ranges [begin, end) a queued item writes.
+    std::vector<std::pair<const char *, const char *>> dw_ranges_;
+    bool queued_leaf(const float *p) const {
+        const char *c = reinterpret_cast<const char *>(p);
+        for (const auto &r : dw_ranges_)
+            if (c >= r.first && c < r.second) return true;
+        return false;
+    }
+
     // How many records hold each gradient buffer as their pending gradient during a backward pass (the record
     // running counts as a holder of its own gradient until its rule returns). A borrowed buffer whose only holder
     // is the record about to write into it is written in place instead of being copied first.
