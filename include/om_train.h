@@ -35,7 +35,9 @@ typedef struct {
  * the caller supplies each step with omt_input_write: 6 = MLP 20-32-4 with SGD(0.05, momentum 0.9, wd 1e-4);
  * 7 = conv/BatchNorm/pool net with AdamW(3e-3, wd 0.01), CosineLr(3e-3, 60) and ClipNorm(0.5) inside omt_step;
  * 8 = Embedding + 2 post-norm encoder layers + mean + Linear with Adam(2e-3) and WarmupLr(ConstantLr(2e-3), 10, 0.1);
- * 9 = configuration 8 with dropout 0.1 after attention and feed-forward in every layer (seeds 77 + 2i, 78 + 2i). */
+ * 9 = configuration 8 with dropout 0.1 after attention and feed-forward in every layer (seeds 77 + 2i, 78 + 2i);
+ * 10 = MLP 64-128-[128]-[128]-64 whose middle Linear is applied twice, so its gradient sums two uses
+ * (BackwardEngineTests.cs:13-25 at layer level), CE, AdamW(1e-3, wd 0.01), batch 256. */
 om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out);
 void omt_destroy(omt_model *m);
 const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */

@@ -1019,6 +1019,27 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.schedule = std::move(ws->s);
         omt_lr_free(ws);
         omt_lr_free(cs);
+    } else if (cfg == 10) {
+        // A weight applied twice (the layer-level form of the reference's DiamondGraphSumsBothPaths,
+        // BackwardEngineTests.cs:13-25): Linear(64,128) - ReLU - T - ReLU - T - ReLU - Linear(128,64), T one
+        // Linear(128,128) whose gradient is the sum of both uses (AccumulateLeaf, Engine.cs:292-328), CE, AdamW.
+        const int B = pick(sc.batch, 256);
+        struct Tied : Module {
+            Linear *l1, *t, *l2;
+        };
+        auto m = std::make_unique<Tied>();
+        m->l1 = m->child("0", std::make_unique<Linear>(64, 128, g));
+        m->t = m->child("1", std::make_unique<Linear>(128, 128, g));
+        m->l2 = m->child("2", std::make_unique<Linear>(128, 64, g));
+        Tied *mp = m.get();
+        M.root = std::move(m);
+        M.add_input("x", {B, 64}, normal(10, 1, (int64_t)B * 64), false);
+        M.add_int_input("labels", {B}, ints(10, 2, B, 0, 64));
+        M.loss_fn = [mp](omt_model &s) {
+            Tensor h = relu((*mp->l1)(s.input("x").t));
+            h = relu((*mp->t)(relu((*mp->t)(h))));
+            return cross_entropy((*mp->l2)(h), s.input("labels").t);
+        };
     } else {
         throw Error(OM_E_ARG, "unknown configuration " + std::to_string(cfg));
     }

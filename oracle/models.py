@@ -168,7 +168,7 @@ def padding_mask(lengths, L):
 
 
 def make_config(cfg: int, scale: dict | None = None) -> Config:
-    """Builds config `cfg` (1..5). `scale` shrinks sizes for fast parity tests (keys: batch, seq, layers, hw)."""
+    """Builds config `cfg` (1..5, or 10: a Linear applied twice). `scale` shrinks sizes for fast parity tests (keys: batch, seq, layers, hw)."""
     s = scale or {}
     g = T.Generator(cfg_seed(cfg, 0))
     if cfg == 1:
@@ -245,6 +245,19 @@ def make_config(cfg: int, scale: dict | None = None) -> Config:
                 h = layer(h)
             return T.cross_entropy(T.reshape(head(h), (B * L, 9)), y)
         return Config(5, model, loss, {"x": x, "labels": y})
+    if cfg == 10:  # one Linear applied twice: its gradient sums both uses (BackwardEngineTests.cs:13-25)
+        B = s.get("batch", 256)
+        model = Module()
+        l1 = model.child("0", Linear(64, 128, g))
+        t = model.child("1", Linear(128, 128, g))
+        l2 = model.child("2", Linear(128, 64, g))
+        x = T.Tensor(T.Generator(cfg_seed(10, 1)).normal((B, 64)))
+        y = T.Generator(cfg_seed(10, 2)).ints(0, 64, (B,))
+
+        def loss(c):
+            h = T.relu(l1(x))
+            return T.cross_entropy(l2(T.relu(t(T.relu(t(h))))), y)
+        return Config(10, model, loss, {"x": x, "labels": y})
     raise ValueError(cfg)
 
 

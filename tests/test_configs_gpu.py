@@ -24,6 +24,7 @@ CASES = [
     (3, {}),
     (4, {"batch": 8}),
     (5, {"batch": 1, "layers": 2}),
+    (10, {}),  # a weight used twice: its queued gradient is launched before the second use adds into it
 ]
 
 
