@@ -95,9 +95,10 @@ om_status om_stager_acquire(om_stager *s, int slot);
 om_status om_stager_release(om_stager *s, int slot);
 
 /* Readback of a small device value (a step's loss) without waiting for the rest of the stream: om_readback_post
- * queues a copy of `bytes` from device memory into a pinned host buffer on the context's stream, ordered after the
- * work already queued there (not after the weight-gradient stream), and om_readback_wait blocks only until that
- * copy has landed, then copies it to dst. Launches queued between the two keep the device busy while the host
+ * queues a copy of `bytes` (at most 64 KiB) from device memory into a pinned host buffer, a one-workgroup kernel on
+ * the context's stream writing through the buffer's device mapping and then a sequence number, ordered after the
+ * work already queued there (not after the weight-gradient stream); om_readback_wait polls that number, so it blocks
+ * only until the copy has landed (and reports a stream error meanwhile), then copies the value to dst. Launches queued between the two keep the device busy while the host
  * returns with the value. No counterpart in the reference's CPU path, where the loss is a host float as soon as the
  * forward has run: its training step reads it there, before Backward and Step (TrainCase.cs:117-127). */
 typedef struct om_readback om_readback;

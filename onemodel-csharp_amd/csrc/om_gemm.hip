@@ -433,9 +433,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
 
 // Weight gradients dw_i (+)= g_i^T x_i of 2..kMaxGroup products sharing K = rows, with fused bias gradients, in one
 // tile-exact launch (and one split-K reduce). Returns false, launching nothing, when the products do not fit it:
-// then the caller runs them one by one. The tile is 64 x 96 when every product's width allows it, else 64 x 64; the
-// K split is the smallest power of two giving about three workgroups per CU. Each product's arithmetic is that of
-// k_gemm_x at that tile and split.
+// then the caller runs them one by one. Each product's arithmetic is that of k_gemm_x at the group's tile and split.
 static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int rows, om_status *st) {
     *st = OM_OK;
     if (count < 2 || count > kMaxGroup || rows <= 0 || x_disabled()) return false;
@@ -446,14 +444,23 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
         if (!d.dw || d.out % 64 || d.in % 64 || !al(d.g) || !al(d.x) || !al(d.dw)) return false;
         if (d.in % 96) n96 = false;
     }
-    const int bn = n96 ? 96 : 64;
+    // 64 x 64 tiles, split until there are about six workgroups per CU (measured on the four C3 weight gradients:
+    // 148 us at 64 x 64 with 4 splits against 152 us for the best 64 x 96 choice, 8 splits).
+    int bn = 64;
     int64_t tiles = 0;
     for (int i = 0; i < count; i++) tiles += (int64_t)(it[i].out / 64) * (it[i].in / bn);
     int splits = 1;
-    while (splits < 16 && tiles * splits < 3 * (int64_t)ctx->num_cus && rows % (2 * splits * 32) == 0 &&
+    while (splits < 16 && tiles * splits < 6 * (int64_t)ctx->num_cus && rows % (2 * splits * 32) == 0 &&
            rows / (2 * splits) >= 256)
         splits *= 2;
-    if (rows % (splits * 32)) return false;
+    Choice forced{};
+    if (env_override(forced, rows)) {  // OM_GEMM_X="64,bn,32,splits" for measurements
+        if (forced.bm != 64 || forced.bkt != 32 || (forced.bn != 64 && forced.bn != 96) || (forced.bn == 96 && !n96))
+            return false;
+        bn = forced.bn;
+        splits = forced.splits;
+    }
+    if (splits < 1 || (splits & (splits - 1)) || splits > 16 || rows % (splits * 32)) return false;
     const int k_split = rows / splits;
     GroupParams g{};
     g.count = count;

@@ -7,6 +7,7 @@
 // step makes the context's stream wait for the upload (om_stager_acquire) and marks the device copy consumed after
 // its last launch (om_stager_release). Upload k+1 then runs on the DMA engines under step k. Both streams have the
 // default priority.
+#include <atomic>
 #include <cstring>
 
 #include "om_internal.hpp"
@@ -152,15 +153,53 @@ om_status om_stager_release(om_stager *s, int slot) {
 
 }  // extern "C"
 
-// Readback: a pinned host buffer the context's stream copies a small device value into, and an event recorded after
-// the copy. The host waits for that event only, so launches queued after the post keep running while it returns.
+// Readback: a pinned host buffer that a one-workgroup kernel on the context's stream writes a device value into,
+// through the buffer's device mapping, followed by a sequence number. The host polls that number instead of
+// waiting on an event: an event's marker on the stream makes the queue drain before the next launch, which left the
+// device idle for several microseconds in the middle of every training step. Launches queued after the post keep
+// running while the host returns with the value.
 struct om_readback {
     om_ctx *ctx = nullptr;
     uint64_t bytes = 0;
-    char *host = nullptr;
-    hipEvent_t landed = nullptr;
-    uint64_t posted = 0;  // bytes of the last post, 0 before the first
+    char *host = nullptr;      // [data, rounded up to 8 bytes][uint64 sequence]
+    char *host_dev = nullptr;  // the same buffer as the device addresses it
+    uint64_t seq = 0;          // sequence number of the last post
+    uint64_t posted = 0;       // bytes of the last post, 0 before the first
 };
+
+namespace {
+
+constexpr uint64_t kReadbackMax = 64 << 10;
+
+// Copies n bytes to dst, then, once every thread's stores are visible system-wide, writes seq after the data.
+__global__ void __launch_bounds__(256) k_readback(char *__restrict__ dst, const char *__restrict__ src, uint64_t n,
+                                                  uint64_t *seq_at, uint64_t seq) {
+    for (uint64_t i = threadIdx.x; i < n; i += 256) dst[i] = src[i];
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) *reinterpret_cast<volatile uint64_t *>(seq_at) = seq;
+}
+
+volatile uint64_t *seq_host(const om_readback *r) {
+    return reinterpret_cast<volatile uint64_t *>(r->host + (r->bytes + 7) / 8 * 8);
+}
+
+// Waits until the last post's sequence number has landed. Every 256 polls it asks the stream: an error is reported,
+// and a stream that has finished everything must have written the number.
+om_status await(om_readback *r) {
+    om_ctx *ctx = r->ctx;
+    for (uint64_t n = 1; *seq_host(r) != r->seq; n++) {
+        if (n % 256) continue;
+        hipError_t e = hipStreamQuery(ctx->stream);
+        if (e == hipErrorNotReady) continue;
+        if (e != hipSuccess) return om::check_hip(ctx, e, "om_readback_wait");
+        if (*seq_host(r) != r->seq) return om::fail(ctx, OM_E_DEVICE, "om_readback_wait: the copy did not land");
+    }
+    std::atomic_thread_fence(std::memory_order_acquire);
+    return OM_OK;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -168,18 +207,20 @@ om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, out, "om_readback_create: out is NULL");
     *out = nullptr;
-    OM_REQUIRE(ctx, bytes > 0 && bytes <= (1u << 20), "om_readback_create: need 1 .. 1 MiB, got %llu",
+    OM_REQUIRE(ctx, bytes > 0 && bytes <= kReadbackMax, "om_readback_create: need 1 .. 64 KiB, got %llu",
                (unsigned long long)bytes);
     om_readback *r = new om_readback;
     r->ctx = ctx;
     r->bytes = bytes;
-    hipError_t e = hipHostMalloc((void **)&r->host, bytes, hipHostMallocDefault);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&r->landed, hipEventDisableTiming);
+    const uint64_t total = (bytes + 7) / 8 * 8 + sizeof(uint64_t);
+    hipError_t e = hipHostMalloc((void **)&r->host, total, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void **)&r->host_dev, r->host, 0);
     if (e != hipSuccess) {
         if (r->host) (void)hipHostFree(r->host);
         delete r;
         return om::check_hip(ctx, e, "om_readback_create");
     }
+    memset(r->host, 0, total);
     *out = r;
     return OM_OK;
 }
@@ -187,8 +228,7 @@ om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out) {
 om_status om_readback_destroy(om_readback *r) {
     if (!r) return OM_OK;
     om_status st = OM_OK;
-    if (r->posted && hipEventSynchronize(r->landed) != hipSuccess) st = OM_E_DEVICE;
-    (void)hipEventDestroy(r->landed);
+    if (r->posted && hipStreamSynchronize(r->ctx->stream) != hipSuccess) st = OM_E_DEVICE;
     (void)hipHostFree(r->host);
     delete r;
     return st;
@@ -201,14 +241,15 @@ om_status om_readback_post(om_readback *r, const void *src, uint64_t bytes) {
                (unsigned long long)r->bytes);
     // The pinned buffer may still be the target of the previous post.
     if (r->posted) {
-        om_status st = om::check_hip(ctx, hipEventSynchronize(r->landed), "om_readback_post wait");
+        om_status st = await(r);
         if (st) return st;
     }
-    om_status st = om::check_hip(ctx, hipMemcpyAsync(r->host, src, bytes, hipMemcpyDeviceToHost, ctx->stream),
-                                 "om_readback_post");
+    const uint64_t seq = r->seq + 1;
+    hipLaunchKernelGGL(k_readback, dim3(1), dim3(256), 0, ctx->stream, r->host_dev, static_cast<const char *>(src),
+                       bytes, reinterpret_cast<uint64_t *>(r->host_dev + (r->bytes + 7) / 8 * 8), seq);
+    om_status st = OM_LAUNCH_CHECK(ctx, "om_readback_post");
     if (st) return st;
-    st = om::check_hip(ctx, hipEventRecord(r->landed, ctx->stream), "om_readback_post record");
-    if (st) return st;
+    r->seq = seq;
     r->posted = bytes;
     return OM_OK;
 }
@@ -219,7 +260,7 @@ om_status om_readback_wait(om_readback *r, void *dst, uint64_t bytes) {
     if (!r->posted) return om::fail(ctx, OM_E_STATE, "om_readback_wait: nothing was posted");
     OM_REQUIRE(ctx, dst && bytes <= r->posted, "om_readback_wait: need a destination and at most %llu bytes",
                (unsigned long long)r->posted);
-    om_status st = om::check_hip(ctx, hipEventSynchronize(r->landed), "om_readback_wait");
+    om_status st = await(r);
     if (st) return st;
     memcpy(dst, r->host, bytes);
     return OM_OK;

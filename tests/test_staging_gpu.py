@@ -144,6 +144,12 @@ def test_readback_takes_the_value_at_its_place_in_the_stream(pkg):
     r = C.c_void_p()
     d.call("om_readback_create", C.c_uint64(64), C.byref(r))
     try:
+        for k in range(3):  # successive posts of one buffer (the sequence number moves on each time)
+            src = d.put(np.full(16, float(k), np.float32))
+            assert L.om_readback_post(r, src.data_ptr(), C.c_uint64(64)) == 0
+            got = np.zeros(16, np.float32)
+            assert L.om_readback_wait(r, got.ctypes.data, C.c_uint64(64)) == 0
+            assert np.array_equal(got, np.full(16, float(k), np.float32))
         a = np.arange(16, dtype=np.float32) * 0.5 - 3.0
         src = d.put(a)
         assert L.om_readback_post(r, src.data_ptr(), C.c_uint64(64)) == 0
@@ -171,6 +177,9 @@ def test_readback_wait_before_any_post_is_refused(pkg):
     try:
         v = np.zeros(1, np.float32)
         assert L.om_readback_wait(r, v.ctypes.data, C.c_uint64(4)) == 4  # OM_E_STATE
+        big = C.c_void_p()
+        assert L.om_readback_create(d.ctx.h, C.c_uint64((64 << 10) + 1), C.byref(big)) == 1  # beyond 64 KiB
+        assert not big.value
     finally:
         L.om_readback_destroy(r)
         d.ctx.close()
