@@ -106,26 +106,52 @@ def _dev_rand(L, ctx, n, scale, seed):
     return p
 
 
+# The four Linear layers of the C3 block as (in, out): FFN 1536 -> 384 and 384 -> 1536, attention output 384 -> 384,
+# packed q|k|v 384 -> 1152; their weight gradients share K = 4096 tokens.
+DOMINANT_ROWS = 4096
+DOMINANT_SHAPES = [(1536, 384), (384, 1536), (384, 384), (384, 1152)]
+
+
 def time_dominant_kernel(pkg, model, ev, reps: int = 50):
-    """The largest GEMM of the C3 step (the FFN weight gradient dW = g^T x, [1536, 384] over K = 4096 tokens: one
-    om_gemm call = the MFMA kernel plus its split-K reduce) on random operands, timed with HIP events on the model's
-    stream."""
+    """The largest launch of the C3 step: the grouped weight and bias gradients of the block's four Linear layers (one
+    om_linear_bwd_dw_group call = the MFMA kernel plus its split-K reduce), on random operands rotated through buffer
+    sets larger than the MALL together, timed with HIP events on the model's stream."""
+    import numpy as np
     L = pkg.load_hip()
     ctx = model.ctx
-    M, N, K = 1536, 384, 4096
-    g, x, dw = _dev_rand(L, ctx, K * M, 1e-3, 1), _dev_rand(L, ctx, K * N, 1.0, 2), _dev_buf(L, ctx, M * N, 0.0)
+    rows, shapes = DOMINANT_ROWS, DOMINANT_SHAPES
+    Item = pkg.om_linear_dw
+    per_set = 4 * sum(rows * (i + o) + i * o + o for i, o in shapes)
+    rng = np.random.default_rng(7)
+    xs = {i: rng.standard_normal(rows * i).astype(np.float32) for i in sorted({i for i, _ in shapes})}
+    gs = {o: (rng.standard_normal(rows * o) * 1e-3).astype(np.float32) for o in sorted({o for _, o in shapes})}
 
-    def launch():
-        st = L.om_gemm(ctx, 1, 0, M, N, K, g, M, x, N, dw, N, None, 0, None)
-        if st != 0:
-            raise RuntimeError(L.om_last_error(ctx).decode())
+    def up(a):
+        p = C.c_void_p()
+        assert L.om_alloc(ctx, 0, 4 * a.size, C.byref(p)) == 0, L.om_last_error(ctx)
+        assert L.om_upload(ctx, p, a.ctypes.data_as(C.c_void_p), 4 * a.size) == 0, L.om_last_error(ctx)
+        return p
 
-    for _ in range(5):
-        launch()
-    ms = ev.time(L.om_ctx_stream(ctx), launch, reps)
-    flops = 2.0 * M * N * K
+    keep, launches = [], []
+    for _ in range(_sets(per_set)):
+        items = (Item * len(shapes))()
+        for j, (i, o) in enumerate(shapes):
+            g, x = up(gs[o]), up(xs[i])
+            dw, db = _dev_buf(L, ctx, o * i, 0.0), _dev_buf(L, ctx, o, 0.0)
+            items[j] = Item(g.value, x.value, dw.value, db.value, i, o, 0, 0)
+        keep.append(items)
+
+        def launch(items=items):
+            if L.om_linear_bwd_dw_group(ctx, len(shapes), C.cast(items, C.c_void_p), rows) != 0:
+                raise RuntimeError(L.om_last_error(ctx).decode())
+        launches.append(launch)
+    for f in launches:
+        f()
+    ms = ev.time(L.om_ctx_stream(ctx), launches, reps)
+    flops = sum(2.0 * rows * i * o for i, o in shapes)
     achieved = flops / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "kernel": "om_gemm TN (FFN dW = g^T x, 1536x384, K=4096) incl. split-K reduce",
+    return {"bound": "mfma", "kernel": "om_linear_bwd_dw_group: the C3 block's four weight gradients (1536x384, "
+            "384x1536, 384x384, 384x1152; K = 4096) with fused bias gradients, incl. split-K reduce",
             "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK, 4), "traffic": measured_traffic(), "ms_per_launch": round(ms, 5),
             "flops_per_launch": flops}
@@ -283,8 +309,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dominant_kernel_traffic.json")
 
 
 def pmc_probe(pkg, model):
-    """Launches, in order, three plain device copies of COPY_PROBE_BYTES, three dominant-kernel GEMMs and three AdamW
-    steps, and nothing else, so that a `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE) run over this mode reads the
+    """Launches, in order, three plain device copies of COPY_PROBE_BYTES, three dominant launches (grouped weight
+    gradients) and three AdamW steps, and nothing else, so that a `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE) run over this mode reads the
     counters of a copy of known size beside those of the kernels it scales."""
     L = pkg.load_hip()
     ctx = model.ctx
