@@ -214,6 +214,12 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
 om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
                            const float *rstd, float *dx, float *dgamma, float *dbeta, int rows, int cols, int acc_dx,
                            int acc_params);
+/* The same with the input gradient's earlier part passed in: dx = dx_add + (this layer's dx), one rounding, into a
+ * buffer other than dx_add — the AddInto of a residual gradient (Engine.cs:331-344) without first copying the
+ * residual's buffer, which may still be read by a queued launch. */
+om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                               const float *rstd, const float *dx_add, float *dx, float *dgamma, float *dbeta, int rows,
+                               int cols, int acc_params);
 
 /* ---------------------------------------------------------------------------------------------- softmax family */
 /* Softmax.Rows (Softmax.cs:27-133) and its backward (BackwardNn.cs:26-52). */

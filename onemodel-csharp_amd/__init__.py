@@ -70,6 +70,7 @@ _OM_SIGS = {
     "om_mean_all_bwd": [vp, vp, vp, i64, ci],
     "om_layernorm_fwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, f32],
     "om_layernorm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci],
+    "om_layernorm_bwd_add": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci],
     "om_softmax_fwd": [vp, vp, vp, ci, ci],
     "om_softmax_bwd": [vp, vp, vp, vp, ci, ci, ci],
     "om_logsoftmax_fwd": [vp, vp, vp, ci, ci],

@@ -139,9 +139,9 @@ constexpr int kMaxPer = 16;
 template <int PER>
 __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, const float *__restrict__ x,
                                                    const float *__restrict__ gamma, const float *__restrict__ mean,
-                                                   const float *__restrict__ rstd, float *__restrict__ dx,
+                                                   const float *__restrict__ rstd, float *dx, const float *dxin,
                                                    double *__restrict__ part_g, double *__restrict__ part_b, int rows,
-                                                   int cols, int rows_per_chunk, int acc_dx) {
+                                                   int cols, int rows_per_chunk) {
     __shared__ double lds[kBlock / 64][64 * PER];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
@@ -186,12 +186,13 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
         if (dx) {
             float m1 = (float)(sum1 / cols), m2 = (float)(sum2 / cols);
             float *dr = dx + (int64_t)r * cols;
+            const float *di = dxin ? dxin + (int64_t)r * cols : nullptr;
 #pragma unroll
             for (int i = 0; i < PER; i++) {
                 int j = lane + 64 * i;
                 if (full || j < cols) {
                     float v = s * (((gv[i] * gam[i]) - m1) - (xh[i] * m2));
-                    dr[j] = acc_dx ? dr[j] + v : v;
+                    dr[j] = di ? di[j] + v : v;
                 }
             }
         }
@@ -218,9 +219,9 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
 template <int COLS, int RPW, int NW>
 __global__ void __launch_bounds__(NW * 64) k_ln_bwd_w(const float *__restrict__ g, const float *__restrict__ x,
                                                      const float *__restrict__ gamma, const float *__restrict__ mean,
-                                                     const float *__restrict__ rstd, float *__restrict__ dx,
+                                                     const float *__restrict__ rstd, float *dx, const float *dxin,
                                                      double *__restrict__ part_g, double *__restrict__ part_b,
-                                                     int rows, int acc_dx) {
+                                                     int rows) {
     constexpr int PER = COLS / 64;
     __shared__ double lds[NW][COLS];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -270,10 +271,11 @@ __global__ void __launch_bounds__(NW * 64) k_ln_bwd_w(const float *__restrict__ 
         if (dx) {
             const float m1 = (float)(sum1 / COLS), m2 = (float)(sum2 / COLS);
             float *dr = dx + (int64_t)r * COLS + lane;
+            const float *di = dxin ? dxin + (int64_t)r * COLS + lane : nullptr;
 #pragma unroll
             for (int c = 0; c < PER; c++) {
                 const float v = s * (((gv[cur][c] * gam[c]) - m1) - (xh[c] * m2));
-                dr[64 * c] = acc_dx ? dr[64 * c] + v : v;
+                dr[64 * c] = di ? di[64 * c] + v : v;
             }
         }
     }
@@ -298,8 +300,8 @@ __global__ void __launch_bounds__(NW * 64) k_ln_bwd_w(const float *__restrict__ 
 __global__ void __launch_bounds__(kBlock) k_ln_bwd_dx_wide(const float *__restrict__ g, const float *__restrict__ x,
                                                            const float *__restrict__ gamma,
                                                            const float *__restrict__ mean,
-                                                           const float *__restrict__ rstd, float *__restrict__ dx,
-                                                           int rows, int cols, int acc_dx) {
+                                                           const float *__restrict__ rstd, float *dx,
+                                                           const float *dxin, int rows, int cols) {
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *xr = x + (int64_t)r * cols, *gr = g + (int64_t)r * cols;
@@ -314,10 +316,11 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd_dx_wide(const float *__restri
     sum2 = omd::wave_sum(sum2);
     float m1 = (float)(sum1 / cols), m2 = (float)(sum2 / cols);
     float *dr = dx + (int64_t)r * cols;
+    const float *di = dxin ? dxin + (int64_t)r * cols : nullptr;
     for (int j = lane; j < cols; j += 64) {
         float xhat = (xr[j] - m) * s;
         float v = s * (((gr[j] * gamma[j]) - m1) - (xhat * m2));
-        dr[j] = acc_dx ? dr[j] + v : v;
+        dr[j] = di ? di[j] + v : v;
     }
 }
 // Generic column partials of g*xhat and g for wide rows: one thread per column per chunk of rows.
@@ -516,11 +519,12 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
     return OM_LAUNCH_CHECK(ctx, "om_layernorm_fwd");
 }
 
-om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
-                           const float *rstd, float *dx, float *dgamma, float *dbeta, int rows, int cols, int acc_dx,
-                           int acc_params) {
-    OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
+}  // extern "C"
+
+// dx = dxin + v when dxin is given (dxin == dx for accumulation), else dx = v.
+static om_status ln_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                        const float *rstd, float *dx, const float *dxin, float *dgamma, float *dbeta, int rows,
+                        int cols, int acc_params) {
     const bool wide_fixed = cols == 384 || cols == 768;
     const int rpc = wide_fixed ? 16 : 8;  // rows per block: 256 (fixed widths) or 512 blocks for 4096 rows
     int chunks = (rows + rpc - 1) / rpc;
@@ -538,15 +542,15 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
         // rows share one set of fp64 column partials.
         if (cols == 384)
             hipLaunchKernelGGL((k_ln_bwd_w<384, 1, 16>), dim3(chunks), dim3(1024), 0, ctx->stream, g, x, gamma, mean,
-                               rstd, dx, pg, pb, rows, acc_dx);
+                               rstd, dx, dxin, pg, pb, rows);
         else
             hipLaunchKernelGGL((k_ln_bwd_w<768, 1, 16>), dim3(chunks), dim3(1024), 0, ctx->stream, g, x, gamma, mean,
-                               rstd, dx, pg, pb, rows, acc_dx);
+                               rstd, dx, dxin, pg, pb, rows);
     } else if (cols <= 64 * kMaxPer) {
         const int per = (cols + 63) / 64;
 #define OM_LNB(P)                                                                                                   \
-    hipLaunchKernelGGL(k_ln_bwd<P>, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, pg, pb, \
-                       rows, cols, rpc, acc_dx)
+    hipLaunchKernelGGL(k_ln_bwd<P>, dim3(chunks), dim3(kBlock), 0, ctx->stream, g, x, gamma, mean, rstd, dx, dxin, pg, \
+                       pb, rows, cols, rpc)
         if (per <= 2) OM_LNB(2);
         else if (per <= 4) OM_LNB(4);
         else if (per <= 6) OM_LNB(6);
@@ -557,7 +561,7 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
     } else {
         if (dx)
             hipLaunchKernelGGL(k_ln_bwd_dx_wide, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, g, x, gamma,
-                               mean, rstd, dx, rows, cols, acc_dx);
+                               mean, rstd, dx, dxin, rows, cols);
         if (params)
             hipLaunchKernelGGL(k_ln_param_partial_wide, dim3((cols + kBlock - 1) / kBlock, chunks), dim3(kBlock), 0,
                                ctx->stream, g, x, mean, rstd, pg, pb, rows, cols, rpc);
@@ -568,6 +572,25 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
     if (dgamma) return om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params);
     if (dbeta) return om::chunk_final(ctx, pb, chunks, cols, dbeta, acc_params);
     return OM_OK;
+}
+
+extern "C" {
+
+om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                           const float *rstd, float *dx, float *dgamma, float *dbeta, int rows, int cols, int acc_dx,
+                           int acc_params) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
+    return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, acc_dx && dx ? dx : nullptr, dgamma, dbeta, rows, cols, acc_params);
+}
+
+om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                               const float *rstd, const float *dx_add, float *dx, float *dgamma, float *dbeta, int rows,
+                               int cols, int acc_params) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && dx_add && dx && rows > 0 && cols > 0,
+               "om_layernorm_bwd_add: bad arguments");
+    return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, dx_add, dgamma, dbeta, rows, cols, acc_params);
 }
 
 om_status om_softmax_fwd(om_ctx *ctx, const float *x, float *y, int rows, int cols) {

@@ -156,6 +156,25 @@ float *Engine::dest(Record &r, int i, int *acc) {
     return p.pending;
 }
 
+float *Engine::dest_add(Record &r, int i, int *acc, const float **addend) {
+    *addend = nullptr;
+    if (i < (int)r.inputs.size() && r.needs(i) && !r.inputs[i]->is_leaf()) {
+        Record &p = *r.inputs[i]->grad_fn;
+        if (p.pending && p.pending_borrowed && !sole_holder(p.pending)) {
+            // the borrowed gradient goes in as the addend; the result lands in a fresh buffer of this record's own
+            float *nb = dev().step_floats(r.inputs[i]->numel);
+            *addend = p.pending;
+            holders_[p.pending]--;
+            p.pending = nb;
+            holders_[nb] = 1;
+            p.pending_borrowed = false;
+            *acc = 0;
+            return nb;
+        }
+    }
+    return dest(r, i, acc);
+}
+
 void Engine::emit_alias(Record &r, int i, const float *g) {
     if (i >= (int)r.inputs.size() || !r.needs(i)) return;
     TensorImpl &x = *r.inputs[i];
@@ -361,7 +380,8 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
     if (rec)
         attach(y, "LayerNorm", {x, gamma, beta}, [rows, cols, mean, rstd](Engine &e, Record &r, const float *g) {
             int ax, ag, ab;
-            float *dx = e.dest(r, 0, &ax);
+            const float *dx_add = nullptr;
+            float *dx = e.dest_add(r, 0, &ax, &dx_add);
             float *dg = e.dest(r, 1, &ag);
             float *db = e.dest(r, 2, &ab);
             if (dg && db && ag != ab) {  // keep one accumulate flag for the pair: materialise the other's zeros
@@ -369,8 +389,12 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
                 if (!ab) OMT(om_zero(C(), db, sizeof(float) * cols));
                 ag = ab = 1;
             }
-            OMT(om_layernorm_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx, dg, db, rows, cols, ax,
-                                 dg ? ag : ab));
+            if (dx_add)
+                OMT(om_layernorm_bwd_add(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx_add, dx, dg, db,
+                                         rows, cols, dg ? ag : ab));
+            else
+                OMT(om_layernorm_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx, dg, db, rows, cols,
+                                     ax, dg ? ag : ab));
         });
     return y;
 }

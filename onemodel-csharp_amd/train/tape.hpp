@@ -97,6 +97,10 @@ class Engine {
     // Destination for a freshly computed gradient of input i: the producer's pending buffer or the leaf's gradient,
     // with *acc telling the kernel to add (C = C + v) instead of overwrite. nullptr when the input needs no gradient.
     float *dest(Record &r, int i, int *acc);
+    // The same for kernels that can add an existing gradient themselves (out = addend + v): where dest would copy a
+    // borrowed gradient still held elsewhere before adding into the copy, this returns a fresh buffer and hands the
+    // borrowed one over as *addend (else *addend is NULL and the result is dest's).
+    float *dest_add(Record &r, int i, int *acc, const float **addend);
     // Hands the incoming gradient itself on to input i (EmitAliased, Engine.cs:245-249): no copy unless it has to
     // be added to an existing gradient.
     void emit_alias(Record &r, int i, const float *g);

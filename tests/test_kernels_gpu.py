@@ -288,6 +288,14 @@ def test_layernorm(dev, T, rows, cols):
     dev.call("om_layernorm_bwd", G, X, GA, MU, IV, DX, DG, DB, rows, cols, 0, 0)
     assert scaled(dev.get(DX), dx) <= 1e-6
     assert scaled(dev.get(DG), dg) <= 1e-7 and scaled(dev.get(DB), db) <= 1e-7
+    # dx accumulated into an existing gradient equals dx written beside it from that gradient as an addend
+    prev = rnd(rng, rows, cols)
+    ACC, ADD, OUT = dev.put(prev), dev.put(prev), dev.empty(x.shape, fill=np.nan)
+    dev.call("om_layernorm_bwd", G, X, GA, MU, IV, ACC, None, None, rows, cols, 1, 0)
+    dev.call("om_layernorm_bwd_add", G, X, GA, MU, IV, ADD, OUT, None, None, rows, cols, 0)
+    assert np.array_equal(dev.get(OUT).view(np.uint32), dev.get(ACC).view(np.uint32))
+    assert np.array_equal(dev.get(ADD), prev)  # the addend is only read
+    assert scaled(dev.get(OUT), prev + dx) <= 1e-6
 
 
 @pytest.mark.parametrize("rows,cols", [(1000, 128), (300, 512), (17, 37)])
