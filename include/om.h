@@ -168,6 +168,18 @@ typedef struct {
     int32_t in, out, acc_dw, acc_db;
 } om_linear_dw;
 om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *items, int rows);
+/* Two-stage column sums finished later: out[c] (+)= (float) of the fp64 sum over k < chunks of part[k * cols + c]
+ * (lanes add every 64th chunk in increasing order, then a fixed butterfly: om_layernorm_bwd's own final order). */
+typedef struct {
+    const double *part;
+    float *out;
+    int32_t chunks, cols, acc;
+} om_column_sum;
+/* All parameter gradients a backward pass leaves to the end in one go: the Linear weight gradients of
+ * om_linear_bwd_dw_group and up to 8 column sums (the dgamma/dbeta partials of om_layernorm_bwd_partials), the
+ * column sums riding in the weight gradients' reduce launch. */
+om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, int rows, int n_cs,
+                               const om_column_sum *cs);
 /* Bias gradient alone: db[n] (+)= (float) sum over rows of g[row, n] in double (BackwardOps.SumTo). */
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate);
 
@@ -220,6 +232,13 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
 om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
                                const float *rstd, const float *dx_add, float *dx, float *dgamma, float *dbeta, int rows,
                                int cols, int acc_params);
+/* LayerNorm backward leaving dgamma/dbeta as fp64 partials: dx as om_layernorm_bwd (dx = dx_add + v when dx_add is
+ * given, else accumulated when acc_dx, else written; dx may be NULL), and part_g / part_b (either may be NULL), each
+ * [om_layernorm_bwd_chunks(rows, cols)][cols], to be finished by om_param_grads_group's column sums. */
+int om_layernorm_bwd_chunks(int rows, int cols);
+om_status om_layernorm_bwd_partials(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                                    const float *rstd, const float *dx_add, float *dx, int acc_dx, double *part_g,
+                                    double *part_b, int rows, int cols);
 
 /* ---------------------------------------------------------------------------------------------- softmax family */
 /* Softmax.Rows (Softmax.cs:27-133) and its backward (BackwardNn.cs:26-52). */

@@ -51,6 +51,7 @@ _OM_SIGS = {
     "om_linear_gelu_fwd_slope": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd_dx_slope": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd_dw_group": [vp, ci, vp, ci],
+    "om_param_grads_group": [vp, ci, vp, ci, ci, vp],
     "om_colsum": [vp, vp, vp, ci, ci, ci],
     "om_relu_fwd": [vp, vp, vp, i64],
     "om_relu_bwd": [vp, vp, vp, vp, i64, ci],
@@ -71,6 +72,8 @@ _OM_SIGS = {
     "om_layernorm_fwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, f32],
     "om_layernorm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci],
     "om_layernorm_bwd_add": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_layernorm_bwd_chunks": [ci, ci],
+    "om_layernorm_bwd_partials": [vp, vp, vp, vp, vp, vp, vp, vp, ci, vp, vp, ci, ci],
     "om_softmax_fwd": [vp, vp, vp, ci, ci],
     "om_softmax_bwd": [vp, vp, vp, vp, ci, ci, ci],
     "om_logsoftmax_fwd": [vp, vp, vp, ci, ci],
@@ -116,6 +119,7 @@ _OM_SIGS = {
     "om_clip_grad_value": [vp, ci, vp, vp, f32],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
+            "om_layernorm_bwd_chunks": ci,
             "om_stager_slot_bytes": u64}
 
 _HIP = None
@@ -153,6 +157,10 @@ def om_symbols():
 class om_linear_dw(C.Structure):
     _fields_ = [("g", vp), ("x", vp), ("dw", vp), ("db", vp), ("in_", i32), ("out", i32), ("acc_dw", i32),
                 ("acc_db", i32)]
+
+
+class om_column_sum(C.Structure):
+    _fields_ = [("part", vp), ("out", vp), ("chunks", i32), ("cols", i32), ("acc", i32)]
 
 
 class omt_scale(C.Structure):

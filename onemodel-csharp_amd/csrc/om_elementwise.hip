@@ -156,13 +156,7 @@ __global__ void __launch_bounds__(256) om_k_chunk_final(const double *__restrict
         src = part2;
         dst = out2;
     }
-    double s = 0.0;
-    for (int c = lane; c < chunks; c += 64) s += src[(int64_t)c * cols + col];
-    s = omd::wave_sum(s);
-    if (lane == 0) {
-        float v = (float)s;
-        dst[col] = acc ? dst[col] + v : v;
-    }
+    omd::column_sum_wave(src, dst, chunks, cols, col, acc, lane);
 }
 
 om_status om::chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,

@@ -138,6 +138,16 @@ __global__ void k_splitk_reduce_group(GroupParams g) {
             if (j < g.count && q >= g.qstart[j]) i = j;
         reduce_quad<S>(g.p[i], q - g.qstart[i]);
     }
+    // column sums, a wavefront per column (the loop bound is uniform over each wavefront)
+    const int lane = threadIdx.x & 63;
+    for (int64_t w = gid >> 6; w < g.cstart[g.ncs]; w += stride >> 6) {
+        int i = 0;
+#pragma unroll
+        for (int j = 1; j < kMaxColSums; j++)
+            if (j < g.ncs && w >= g.cstart[j]) i = j;
+        const ColSumItem &c = g.cs[i];
+        omd::column_sum_wave(c.part, c.out, c.chunks, c.cols, (int)(w - g.cstart[i]), c.acc, lane);
+    }
 }
 
 template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
@@ -434,7 +444,33 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
 // Weight gradients dw_i (+)= g_i^T x_i of 2..kMaxGroup products sharing K = rows, with fused bias gradients, in one
 // tile-exact launch (and one split-K reduce). Returns false, launching nothing, when the products do not fit it:
 // then the caller runs them one by one. Each product's arithmetic is that of k_gemm_x at the group's tile and split.
-static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int rows, om_status *st) {
+// Fills the column-sum items of g (prefix counts in wavefronts, one per column).
+static void set_column_sums(GroupParams &g, int ncs, const om_column_sum *cs) {
+    g.ncs = ncs;
+    g.cstart[0] = 0;
+    for (int j = 0; j < ncs; j++) {
+        g.cs[j] = ColSumItem{cs[j].part, cs[j].out, cs[j].chunks, cs[j].cols, cs[j].acc};
+        g.cstart[j + 1] = g.cstart[j] + cs[j].cols;
+    }
+    for (int j = ncs; j < kMaxColSums; j++) g.cstart[j + 1] = g.cstart[ncs];
+}
+
+// The grouped reduce: split-K partials (S splits) of g's products, their fused bias sums and g's column sums.
+static om_status launch_group_reduce(om_ctx *ctx, const GroupParams &g, int splits, hipStream_t stream) {
+    int64_t units = g.qstart[g.count] > g.rstart[g.count] ? g.qstart[g.count] : g.rstart[g.count];
+    if (64 * (int64_t)g.cstart[g.ncs] > units) units = 64 * (int64_t)g.cstart[g.ncs];
+    if (units == 0) return OM_OK;
+    const dim3 grid(om::grid1d(units, 256, 4096));
+    if (splits <= 1) hipLaunchKernelGGL(k_splitk_reduce_group<1>, grid, dim3(256), 0, stream, g);
+    else if (splits == 2) hipLaunchKernelGGL(k_splitk_reduce_group<2>, grid, dim3(256), 0, stream, g);
+    else if (splits == 4) hipLaunchKernelGGL(k_splitk_reduce_group<4>, grid, dim3(256), 0, stream, g);
+    else if (splits == 8) hipLaunchKernelGGL(k_splitk_reduce_group<8>, grid, dim3(256), 0, stream, g);
+    else hipLaunchKernelGGL(k_splitk_reduce_group<16>, grid, dim3(256), 0, stream, g);
+    return OM_LAUNCH_CHECK(ctx, "grouped reduce");
+}
+
+static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int rows, int ncs, const om_column_sum *cs,
+                            om_status *st) {
     *st = OM_OK;
     if (count < 2 || count > kMaxGroup || rows <= 0 || x_disabled()) return false;
     bool n96 = true;
@@ -513,15 +549,14 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
     hipStream_t stream = om::cur_stream(ctx);
     if (bn == 96) hipLaunchKernelGGL((gx::k_gemm_x_tn_group<64, 96, 32>), dim3(g.start[count]), dim3(NT), 0, stream, g);
     else hipLaunchKernelGGL((gx::k_gemm_x_tn_group<64, 64, 32>), dim3(g.start[count]), dim3(NT), 0, stream, g);
-    *st = OM_LAUNCH_CHECK(ctx, "om_linear_bwd_dw_group");
-    if (*st || splits == 1) return true;
-    const int64_t units = g.qstart[count] > g.rstart[count] ? g.qstart[count] : g.rstart[count];
-    const dim3 grid(om::grid1d(units, 256, 4096));
-    if (splits == 2) hipLaunchKernelGGL(k_splitk_reduce_group<2>, grid, dim3(256), 0, stream, g);
-    else if (splits == 4) hipLaunchKernelGGL(k_splitk_reduce_group<4>, grid, dim3(256), 0, stream, g);
-    else if (splits == 8) hipLaunchKernelGGL(k_splitk_reduce_group<8>, grid, dim3(256), 0, stream, g);
-    else hipLaunchKernelGGL(k_splitk_reduce_group<16>, grid, dim3(256), 0, stream, g);
-    *st = OM_LAUNCH_CHECK(ctx, "om_linear_bwd_dw_group reduce");
+    *st = OM_LAUNCH_CHECK(ctx, "om_param_grads_group");
+    if (*st) return true;
+    if (splits == 1) {  // the products are complete: only the column sums are left
+        g.count = 0;
+        for (int i = 0; i <= kMaxGroup; i++) g.qstart[i] = g.rstart[i] = 0;
+    }
+    set_column_sums(g, ncs, cs);
+    *st = launch_group_reduce(ctx, g, splits, stream);
     return true;
 }
 
@@ -653,24 +688,41 @@ om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, 
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd_slope");
 }
 
-om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *items, int rows) {
+om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, int rows, int n_cs,
+                               const om_column_sum *cs) {
     OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, count >= 0 && (count == 0 || items) && rows >= 0, "om_linear_bwd_dw_group: bad arguments");
-    for (int i = 0; i < count; i++)
-        OM_REQUIRE(ctx, items[i].g && items[i].x && items[i].in > 0 && items[i].out > 0,
-                   "om_linear_bwd_dw_group: item %d has a NULL input or a non-positive size", i);
+    OM_REQUIRE(ctx, n_dw >= 0 && (n_dw == 0 || dw) && rows >= 0 && n_cs >= 0 && n_cs <= omg::kMaxColSums &&
+                        (n_cs == 0 || cs),
+               "om_param_grads_group: bad arguments (at most %d column sums)", omg::kMaxColSums);
+    for (int i = 0; i < n_dw; i++)
+        OM_REQUIRE(ctx, dw[i].g && dw[i].x && dw[i].in > 0 && dw[i].out > 0,
+                   "om_param_grads_group: weight item %d has a NULL input or a non-positive size", i);
+    for (int j = 0; j < n_cs; j++)
+        OM_REQUIRE(ctx, cs[j].part && cs[j].out && cs[j].chunks > 0 && cs[j].cols > 0,
+                   "om_param_grads_group: column-sum item %d has a NULL pointer or a non-positive size", j);
     om_status s = OM_OK;
-    // In overlap mode the grouped launch goes to the weight-gradient stream, like om_linear_bwd's dW.
+    // In overlap mode the grouped launches go to the weight-gradient stream, like om_linear_bwd's dW.
     if (ctx->overlap && (s = om::fork(ctx))) return s;
-    const bool grouped = omg::launch_dw_group(ctx, count, items, rows, &s);
-    if (ctx->overlap) om::unfork(ctx);
-    if (grouped) return s;
-    for (int i = 0; i < count && !s; i++) {
-        const om_linear_dw &d = items[i];
-        if (d.dw || d.db)
-            s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw, d.acc_db);
+    const bool grouped = omg::launch_dw_group(ctx, n_dw, dw, rows, n_cs, cs, &s);
+    if (!grouped) {
+        for (int i = 0; i < n_dw && !s; i++) {
+            const om_linear_dw &d = dw[i];
+            if (d.dw || d.db)
+                s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw,
+                                  d.acc_db);
+        }
+        if (!s && n_cs) {
+            omg::GroupParams g{};
+            omg::set_column_sums(g, n_cs, cs);
+            s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
+        }
     }
+    if (ctx->overlap) om::unfork(ctx);
     return s;
+}
+
+om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *items, int rows) {
+    return om_param_grads_group(ctx, count, items, rows, 0, nullptr);
 }
 
 om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,

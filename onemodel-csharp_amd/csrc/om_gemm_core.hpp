@@ -82,13 +82,24 @@ enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MU
 // Several products launched together (the grouped weight-gradient kernel and its reduce): product i owns workgroups
 // [start[i], start[i+1]) of the GEMM launch, float4 quads [qstart[i], qstart[i+1]) and bias rows
 // [rstart[i], rstart[i+1]) of the reduce.
+// The reduce also finishes up to kMaxColSums two-stage column sums (LayerNorm's dgamma/dbeta partials): item j owns
+// the wavefronts [cstart[j], cstart[j+1]) of the reduce grid, one per column.
 constexpr int kMaxGroup = 4;
+constexpr int kMaxColSums = 8;
+struct ColSumItem {
+    const double *part;
+    float *out;
+    int chunks, cols, acc;
+};
 struct GroupParams {
     Params p[kMaxGroup];
     int start[kMaxGroup + 1];
     int64_t qstart[kMaxGroup + 1];
     int rstart[kMaxGroup + 1];
     int count;
+    ColSumItem cs[kMaxColSums];
+    int cstart[kMaxColSums + 1];
+    int ncs;
 };
 
 // The epilogue of one finished dot product v at (row, col): alpha, mask, bias, residual, GELU terms, then C. The

@@ -145,6 +145,19 @@ __device__ __forceinline__ float max16(float v) {
     return v;
 }
 
+// One column of a two-stage column reduction, by one wavefront: lanes add the chunk partials c = lane, lane + 64, ...
+// of part[c * cols + col] in increasing c, then the fixed butterfly; lane 0 writes out[col] (+)= the float of the sum.
+__device__ __forceinline__ void column_sum_wave(const double *part, float *out, int chunks, int cols, int col, int acc,
+                                                int lane) {
+    double s = 0.0;
+    for (int c = lane; c < chunks; c += 64) s += part[(int64_t)c * cols + col];
+    s = wave_sum(s);
+    if (lane == 0) {
+        float v = (float)s;
+        out[col] = acc ? out[col] + v : v;
+    }
+}
+
 // The reference's fp32 polynomials (Transcendental.cs:39-263), restated with one IEEE rounding per operation; the
 // library is built with -ffp-contract=off so no multiply-add is fused behind our back.
 __device__ __forceinline__ float exp_poly(float x) {

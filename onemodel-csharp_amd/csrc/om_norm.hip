@@ -522,21 +522,18 @@ om_status om_layernorm_fwd(om_ctx *ctx, const float *x, const float *gamma, cons
 }  // extern "C"
 
 // dx = dxin + v when dxin is given (dxin == dx for accumulation), else dx = v.
-static om_status ln_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
-                        const float *rstd, float *dx, const float *dxin, float *dgamma, float *dbeta, int rows,
-                        int cols, int acc_params) {
+// Rows per chunk of the fp64 column partials: 16 for the fixed widths (256 chunks at 4096 rows), else 8.
+static int ln_rows_per_chunk(int cols) { return cols == 384 || cols == 768 ? 16 : 8; }
+
+// The backward's main launch(es): dx (dx = dxin + v when dxin is given, dxin == dx to accumulate) and the per-chunk
+// partials pg / pb of dgamma / dbeta (either may be NULL).
+static om_status ln_bwd_main(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                             const float *rstd, float *dx, const float *dxin, double *pg, double *pb, int rows,
+                             int cols) {
     const bool wide_fixed = cols == 384 || cols == 768;
-    const int rpc = wide_fixed ? 16 : 8;  // rows per block: 256 (fixed widths) or 512 blocks for 4096 rows
-    int chunks = (rows + rpc - 1) / rpc;
-    bool params = dgamma || dbeta;
-    double *pg = nullptr, *pb = nullptr;
-    if (params) {
-        float *scr;
-        om_status s = om::scratch(ctx, sizeof(double) * 2ull * chunks * cols, &scr);
-        if (s) return s;
-        pg = dgamma ? reinterpret_cast<double *>(scr) : nullptr;
-        pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
-    }
+    const int rpc = ln_rows_per_chunk(cols);
+    const int chunks = (rows + rpc - 1) / rpc;
+    const bool params = pg || pb;
     if (wide_fixed) {
         // 16 wavefronts of one row each per block: every row's loads are in flight at once, and the block's 16
         // rows share one set of fp64 column partials.
@@ -566,7 +563,23 @@ static om_status ln_bwd(om_ctx *ctx, const float *g, const float *x, const float
             hipLaunchKernelGGL(k_ln_param_partial_wide, dim3((cols + kBlock - 1) / kBlock, chunks), dim3(kBlock), 0,
                                ctx->stream, g, x, mean, rstd, pg, pb, rows, cols, rpc);
     }
-    om_status s = OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
+    return OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
+}
+
+static om_status ln_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                        const float *rstd, float *dx, const float *dxin, float *dgamma, float *dbeta, int rows,
+                        int cols, int acc_params) {
+    const int rpc = ln_rows_per_chunk(cols);
+    const int chunks = (rows + rpc - 1) / rpc;
+    double *pg = nullptr, *pb = nullptr;
+    if (dgamma || dbeta) {
+        float *scr;
+        om_status s = om::scratch(ctx, sizeof(double) * 2ull * chunks * cols, &scr);
+        if (s) return s;
+        pg = dgamma ? reinterpret_cast<double *>(scr) : nullptr;
+        pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
+    }
+    om_status s = ln_bwd_main(ctx, g, x, gamma, mean, rstd, dx, dxin, pg, pb, rows, cols);
     if (s) return s;
     if (dgamma && dbeta) return om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params, pb, dbeta);
     if (dgamma) return om::chunk_final(ctx, pg, chunks, cols, dgamma, acc_params);
@@ -582,6 +595,22 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
     return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, acc_dx && dx ? dx : nullptr, dgamma, dbeta, rows, cols, acc_params);
+}
+
+int om_layernorm_bwd_chunks(int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    const int rpc = ln_rows_per_chunk(cols);
+    return (rows + rpc - 1) / rpc;
+}
+
+om_status om_layernorm_bwd_partials(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
+                                    const float *rstd, const float *dx_add, float *dx, int acc_dx, double *part_g,
+                                    double *part_b, int rows, int cols) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0 && (!dx_add || dx),
+               "om_layernorm_bwd_partials: bad arguments");
+    return ln_bwd_main(ctx, g, x, gamma, mean, rstd, dx, dx_add ? dx_add : (acc_dx && dx ? dx : nullptr), part_g, part_b,
+                       rows, cols);
 }
 
 om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,

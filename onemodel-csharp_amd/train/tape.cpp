@@ -110,11 +110,20 @@ void Engine::queue_dw(const om_linear_dw &item, int rows) {
     }
 }
 
+void Engine::queue_colsum(const om_column_sum &item) {
+    if (cs_queue_.size() == 8) flush_dw();
+    cs_queue_.push_back(item);
+    const char *b = reinterpret_cast<const char *>(item.out);
+    dw_ranges_.emplace_back(b, b + sizeof(float) * (uint64_t)item.cols);
+}
+
 void Engine::flush_dw() {
-    if (dw_queue_.empty()) return;
-    OMT(om_linear_bwd_dw_group(C(), (int)dw_queue_.size(), dw_queue_.data(), dw_rows_));
+    if (dw_queue_.empty() && cs_queue_.empty()) return;
+    OMT(om_param_grads_group(C(), (int)dw_queue_.size(), dw_queue_.data(), dw_rows_, (int)cs_queue_.size(),
+                             cs_queue_.data()));
     for (const om_linear_dw &it : dw_queue_) holders_[it.g]--;
     dw_queue_.clear();
+    cs_queue_.clear();
     dw_ranges_.clear();
 }
 
@@ -379,22 +388,21 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
     OMT(om_layernorm_fwd(C(), x->data, gamma->data, beta->data, y->data, mean, rstd, rows, cols, eps));
     if (rec)
         attach(y, "LayerNorm", {x, gamma, beta}, [rows, cols, mean, rstd](Engine &e, Record &r, const float *g) {
+            // dx now; dgamma / dbeta as fp64 partials in step memory whose column sums are queued with the weight
+            // gradients (om_param_grads_group)
             int ax, ag, ab;
             const float *dx_add = nullptr;
             float *dx = e.dest_add(r, 0, &ax, &dx_add);
             float *dg = e.dest(r, 1, &ag);
             float *db = e.dest(r, 2, &ab);
-            if (dg && db && ag != ab) {  // keep one accumulate flag for the pair: materialise the other's zeros
-                if (!ag) OMT(om_zero(C(), dg, sizeof(float) * cols));
-                if (!ab) OMT(om_zero(C(), db, sizeof(float) * cols));
-                ag = ab = 1;
-            }
-            if (dx_add)
-                OMT(om_layernorm_bwd_add(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx_add, dx, dg, db,
-                                         rows, cols, dg ? ag : ab));
-            else
-                OMT(om_layernorm_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx, dg, db, rows, cols,
-                                     ax, dg ? ag : ab));
+            const int chunks = om_layernorm_bwd_chunks(rows, cols);
+            auto partials = [&]() { return reinterpret_cast<double *>(dev().step_floats(2 * (int64_t)chunks * cols)); };
+            double *pg = dg ? partials() : nullptr;
+            double *pb = db ? partials() : nullptr;
+            OMT(om_layernorm_bwd_partials(C(), g, r.inputs[0]->data, r.inputs[1]->data, mean, rstd, dx_add, dx, ax, pg,
+                                          pb, rows, cols));
+            if (dg) e.queue_colsum(om_column_sum{pg, dg, chunks, cols, ag});
+            if (db) e.queue_colsum(om_column_sum{pb, db, chunks, cols, ab});
         });
     return y;
 }

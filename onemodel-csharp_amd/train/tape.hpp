@@ -109,11 +109,15 @@ class Engine {
     // full, when another gradient is about to be added into one of their leaf gradients, and when the pass ends.
     // Until then g stays pinned: it counts as held, so no record writes into it in place.
     void queue_dw(const om_linear_dw &item, int rows);
+    // Queues a two-stage column sum (LayerNorm's dgamma / dbeta partials in step memory), launched with the weight
+    // gradients (om_param_grads_group).
+    void queue_colsum(const om_column_sum &item);
     void flush_dw();
     void run(const Tensor &root);
 
    private:
     std::vector<om_linear_dw> dw_queue_;
+    std::vector<om_column_sum> cs_queue_;
     int dw_rows_ = 0;
     // Leaf gradient ranges [begin, end) a queued item writes.
     std::vector<std::pair<const char *, const char *>> dw_ranges_;

@@ -155,7 +155,12 @@ def test_linear_dw_group(dev, T, rows, shapes):
             assert scaled(dev.get(DB), db_r) <= 1e-7
     for i in range(len(shapes)):
         items[i].acc_dw = items[i].acc_db = 1
-    dev.call("om_linear_bwd_dw_group", len(shapes), C.cast(items, C.c_void_p), rows)
+    # the second call through om_param_grads_group, with a column sum riding in the same launches
+    part = rng.standard_normal((9, 70))
+    P, OUT = dev.put(part), dev.empty((70,))
+    cs = (dev.pkg.om_column_sum * 1)(dev.pkg.om_column_sum(P.data_ptr(), OUT.data_ptr(), 9, 70, 0))
+    dev.call("om_param_grads_group", len(shapes), C.cast(items, C.c_void_p), rows, 1, C.cast(cs, C.c_void_p))
+    assert scaled(dev.get(OUT), part.sum(axis=0).astype(np.float32)) <= 1e-7
     for (X, G, DW, DB), (dw_r, db_r) in zip(bufs, refs):
         assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
         if DB is not None:
@@ -296,6 +301,18 @@ def test_layernorm(dev, T, rows, cols):
     assert np.array_equal(dev.get(OUT).view(np.uint32), dev.get(ACC).view(np.uint32))
     assert np.array_equal(dev.get(ADD), prev)  # the addend is only read
     assert scaled(dev.get(OUT), prev + dx) <= 1e-6
+    # partials now, column sums later through om_param_grads_group: the same bits as om_layernorm_bwd
+    L = dev.ctx.L
+    chunks = L.om_layernorm_bwd_chunks(rows, cols)
+    PG, PB = dev.empty((chunks, cols), np.float64), dev.empty((chunks, cols), np.float64)
+    DX2, DG2, DB2 = dev.empty(x.shape), dev.empty((cols,), fill=3.0), dev.empty((cols,), fill=3.0)
+    dev.call("om_layernorm_bwd_partials", G, X, GA, MU, IV, None, DX2, 0, PG, PB, rows, cols)
+    items = (dev.pkg.om_column_sum * 2)(dev.pkg.om_column_sum(PG.data_ptr(), DG2.data_ptr(), chunks, cols, 0),
+                                        dev.pkg.om_column_sum(PB.data_ptr(), DB2.data_ptr(), chunks, cols, 1))
+    dev.call("om_param_grads_group", 0, None, 0, 2, C.cast(items, C.c_void_p))
+    assert np.array_equal(dev.get(DX2).view(np.uint32), dev.get(DX).view(np.uint32))
+    assert np.array_equal(dev.get(DG2).view(np.uint32), dev.get(DG).view(np.uint32))
+    assert np.array_equal(dev.get(DB2), (dev.get(DB) + np.float32(3.0)).astype(np.float32))  # accumulated
 
 
 @pytest.mark.parametrize("rows,cols", [(1000, 128), (300, 512), (17, 37)])
