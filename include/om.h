@@ -206,6 +206,10 @@ om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int3
  * target is saved, *loss (device) = (float)(sum in double of fl(diff*diff) / n). The backward is the chain's rounding
  * order: t = (g / (float)n) * diff, dpred = t + t (the two Mul emissions added, Engine.AddInto). */
 om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n);
+/* The same, also writing dpred_unit = the backward's dpred for a unit upstream gradient (g = 1: t = (1 / (float)n) *
+ * diff, t + t), so a loss that is the root of the backward needs no separate gradient launch. */
+om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
+                          float *dpred_unit, int64_t n);
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- reductions */

@@ -229,16 +229,22 @@ __global__ void __launch_bounds__(kBlock) k_permute(const float *__restrict__ x,
 }
 
 // MSE: diff and per-block double partial sums of fl(diff*diff); a final pass adds the partials in block order.
+// With unit != NULL it also writes the gradient for a unit upstream gradient, k_mse_bwd's arithmetic with g = 1.
 __global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict__ p, const float *__restrict__ t,
                                                         float *__restrict__ diff, int64_t n,
-                                                        double *__restrict__ part) {
+                                                        double *__restrict__ part, float *__restrict__ unit) {
     __shared__ double sh[kBlock / 64];
+    const float dsq = 1.0f / (float)n;
     double acc = 0.0;
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float d = p[i] - t[i];
         diff[i] = d;
         acc += (double)(d * d);
+        if (unit) {
+            float u = dsq * d;
+            unit[i] = u + u;
+        }
     }
     double s = omd::block_sum<kBlock / 64>(acc, sh);
     if (threadIdx.x == 0) part[blockIdx.x] = s;
@@ -282,17 +288,29 @@ om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int3
     return OM_LAUNCH_CHECK(ctx, "om_permute");
 }
 
-om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n) {
-    OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, pred && target && diff && loss && n > 0, "om_mse_fwd: bad arguments");
+static om_status mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, float *unit,
+                         int64_t n) {
     float *scr;
     om_status s = om::scratch(ctx, sizeof(double) * kSumBlocks, &scr);
     if (s) return s;
     double *part = reinterpret_cast<double *>(scr);
     int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
-    hipLaunchKernelGGL(k_mse_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, pred, target, diff, n, part);
+    hipLaunchKernelGGL(k_mse_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, pred, target, diff, n, part, unit);
     hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, loss, (double)n);
     return OM_LAUNCH_CHECK(ctx, "om_mse_fwd");
+}
+
+om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, pred && target && diff && loss && n > 0, "om_mse_fwd: bad arguments");
+    return mse_fwd(ctx, pred, target, diff, loss, nullptr, n);
+}
+
+om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
+                          float *dpred_unit, int64_t n) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, pred && target && diff && loss && dpred_unit && n > 0, "om_mse_fwd_unit: bad arguments");
+    return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n);
 }
 
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate) {

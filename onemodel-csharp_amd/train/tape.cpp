@@ -689,12 +689,21 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     const int64_t n = pred->numel;
     float *diff = dev().step_floats(n);
     Tensor loss = make({});
-    OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
-    if (tracked({&pred, &target}))
-        attach(loss, "Mse", {pred, target}, [diff, n](Engine &e, Record &r, const float *g) {
-            int a;
-            float *dp = e.dest(r, 0, &a);
-            if (dp) OMT(om_mse_bwd(C(), g, diff, dp, n, a));
+    const bool rec = tracked({&pred, &target});
+    // the gradient for a unit upstream gradient comes with the forward: the loss is normally the backward's root,
+    // whose seed gradient is exactly that unit
+    float *unit = rec && pred->requires_grad ? dev().step_floats(n) : nullptr;
+    if (unit) OMT(om_mse_fwd_unit(C(), pred->data, target->data, diff, loss->data, unit, n));
+    else OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
+    if (rec)
+        attach(loss, "Mse", {pred, target}, [diff, unit, n](Engine &e, Record &r, const float *g) {
+            if (unit && g == dev().one()) {
+                e.emit_alias(r, 0, unit);
+            } else {
+                int a;
+                float *dp = e.dest(r, 0, &a);
+                if (dp) OMT(om_mse_bwd(C(), g, diff, dp, n, a));
+            }
             if (r.needs(1)) {  // Sub backward negates the second input's gradient
                 float *t = dev().step_floats(n);
                 OMT(om_mse_bwd(C(), g, diff, t, n, 0));

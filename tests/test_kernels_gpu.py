@@ -273,6 +273,30 @@ def test_add_sub_mul_axpy_mean(dev, T):
     assert np.all(dev.get(D) == np.float32(0.75) / np.float32(x2.size))
 
 
+def test_mse_and_its_unit_gradient(dev, T):
+    """om_mse_fwd / om_mse_bwd against the oracle's Losses.Mse chain, and om_mse_fwd_unit's gradient for a unit
+    upstream gradient equal to om_mse_bwd with g = 1 bit for bit."""
+    from oracle import tape as OT
+    rng = np.random.default_rng(21)
+    pred, tgt = rnd(rng, 4096, 384), rnd(rng, 4096, 384)
+    n = pred.size
+    P, TG = dev.put(pred), dev.put(tgt)
+    D, LOSS, D2, LOSS2, UNIT = (dev.empty(pred.shape), dev.empty((1,)), dev.empty(pred.shape), dev.empty((1,)),
+                                dev.empty(pred.shape))
+    dev.call("om_mse_fwd", P, TG, D, LOSS, C.c_int64(n))
+    dev.call("om_mse_fwd_unit", P, TG, D2, LOSS2, UNIT, C.c_int64(n))
+    assert np.array_equal(dev.get(LOSS), dev.get(LOSS2)) and np.array_equal(dev.get(D), dev.get(D2))
+    ONE, DP = dev.put(np.ones(1, np.float32)), dev.empty(pred.shape)
+    dev.call("om_mse_bwd", ONE, D, DP, C.c_int64(n), 0)
+    assert np.array_equal(dev.get(UNIT).view(np.uint32), dev.get(DP).view(np.uint32))
+    tp = OT.Tensor(pred.copy(), True)
+    loss = OT.mse(tp, OT.Tensor(tgt.copy()))
+    OT.backward(loss)
+    ref = float(loss.data.reshape(-1)[0])
+    assert abs(float(dev.get(LOSS)[0]) - ref) <= 1e-6 * abs(ref)
+    assert scaled(dev.get(UNIT), tp.grad) <= 1e-6
+
+
 # ------------------------------------------------------------------------------------------------ norms and softmax
 @pytest.mark.parametrize("rows,cols", [(4096, 384), (512, 768), (7, 1536), (33, 2000), (17, 12), (9, 10), (40, 960),
                                        (37, 384), (21, 768)])
