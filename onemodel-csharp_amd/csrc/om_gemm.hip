@@ -183,9 +183,16 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 #undef OMG_CASE
 }
 
+// OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for comparisons); otherwise NT tiles with
+// 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
+static bool dma_disabled() {
+    static const char *s = std::getenv("OM_GEMM_DMA");
+    return s && s[0] == '0';
+}
+
 // Tile-exact set (om_gemm_x.hpp): NN, NT, TN; GELU epilogue variants (NN / NT only) where G instantiates them.
 template <int BM, int BN, int BKT, bool G>
-static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
     const bool gelu = p.epi != EPI_NONE;
     if (gelu && (!G || ta)) return false;
@@ -197,6 +204,18 @@ static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t s
     if (!ta && !tb) {
         OMG_L(k_gemm_x, NT, false, false)
     } else if (!ta && tb) {
+        // Both operands K-contiguous: chunks load straight into LDS, when the grid fits in one round of the CUs at
+        // the occupancy the three LDS stages allow (C3: the 256-tile products gain 7-8 %, the 768-tile q|k|v
+        // projection would lose 14 % to a second round). Not for the GELU epilogues, whose element-wise tail hides
+        // better behind the register-staged kernel's higher occupancy (75 against 81 us for the C3 FFN product).
+        if constexpr (BKT == 32) {
+            constexpr int lds = 4 * (64 + 3 * (BM + BN) * BKT);
+            const unsigned per_cu = (160u << 10) / lds;
+            if (!gelu && !dma_disabled() && total <= per_cu * (unsigned)cus) {
+                hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, false>), dim3(total), dim3(NT), 0, st, p);
+                return true;
+            }
+        }
         OMG_L(k_gemm_x, NT, false, true)
     } else if (ta && !tb) {
         hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false, false>), dim3(total), dim3(NT), 0, st, p);
@@ -231,14 +250,14 @@ const XTile kXTiles[] = {{64, 64, 32},  {64, 96, 32},   {96, 64, 32},  {64, 128,
                          {128, 128, 32}, {64, 64, 64},  {64, 96, 64},  {128, 128, 64}};
 
 // Launches tile t; false when t (or its GELU variant) is not instantiated.
-static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
+static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
     // bkt 33 / 65 select the eight-wavefront variant of the 32 / 64 chunk.
     if (t.bkt == 33 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 32, true>(p, batch, ta, tb, st);
     if (t.bkt == 33 && t.bm == 64 && t.bn == 64) return launch_x2<64, 64, 32, true>(p, batch, ta, tb, st);
     if (t.bkt == 65 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 64, false>(p, batch, ta, tb, st);
     if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, false>(p, batch, ta, tb, st);
 #define OMG_X(BM, BN, BKT, G) \
-    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, G>(p, batch, ta, tb, st);
+    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, G>(p, batch, ta, tb, st, cus);
     OMG_X(64, 64, 32, true)
     OMG_X(64, 96, 32, true)
     OMG_X(96, 64, 32, false)
@@ -409,7 +428,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     }
     if (colsum_fused) *colsum_fused = cs;
     hipStream_t st = om::cur_stream(ctx);
-    bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st);
+    bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st, ctx->num_cus);
     if (launched) {
     } else if (fast) {
         if (c.bm == 128 && c.bn == 192) launch_fast<128, 192>(p, batch, ta, tb, st);

@@ -395,6 +395,128 @@ __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     gemm_x_tile<BM, BN, BKT, TA, TB, GELU>(p, tm, tn, zz);
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Tile-exact product with both operands K-contiguous (A [m][k], B [n][k]: every Linear forward) whose chunks travel
+// from global memory straight into LDS: `global_load_lds_dwordx4` writes each lane's 16 bytes at M0 + 16 * lane, so a
+// wavefront instruction fills 64 consecutive float4 slots of the swizzled K layout, and each lane loads the global
+// float4 that belongs in its slot. Three LDS stages form a ring: chunk t sits in stage t % 3, and the loads of chunk
+// t + 2 are issued right after the barrier that opens chunk t, so every chunk has two chunks of MFMA time to land,
+// with no staging registers and no LDS writes of our own. The loads are inline assembly with explicit waits: the
+// compiler tracks such loads only as a whole and would otherwise wait for all of them (vmcnt(0)) before the first
+// LDS read of every chunk. Before the barrier opening chunk t each wavefront waits until only chunk t+1's loads may
+// still be in flight (vmcnt counts in issue order) and until its own LDS reads are done (lgkmcnt(0)); the barrier
+// then also tells every wavefront that all others have finished reading the stage the new loads will overwrite
+// (chunk t-1's). No load is in flight at the end.
+// Arithmetic, order and epilogue are k_gemm_x's, so the results are bit for bit those of k_gemm_x at the same tile.
+// One operand's part of a chunk: wavefront w issues instructions q = 4 j + w, each filling slots [64 q, 64 q + 64)
+// of the stage. `src` is this lane's row pointer for j = 0 (row r0 = (64 w + lane) / CH); each further j moves 4 * 64
+// slots = 256 / CH rows down. `lds` is the stage's LDS byte address plus this wavefront's first instruction, a
+// wavefront-uniform value.
+template <int ROWS, int BKT>
+__device__ __forceinline__ void dma_chunk(const float *src, int64_t ld, unsigned lds) {
+    constexpr int INSTR = ROWS * (BKT / 4) / 64;  // wavefront instructions per stage and operand
+    static_assert(INSTR % 4 == 0, "each of the four wavefronts issues whole instructions");
+    constexpr int CH = BKT / 4;  // float4 chunks per row
+#pragma unroll
+    for (int j = 0; j < INSTR / 4; j++) {
+        const float *g = src + (int64_t)j * (256 / CH) * ld;
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds + j * 4096u)
+                     : "memory", "m0");
+    }
+}
+
+template <int BM, int BN, int BKT, bool GELU>
+__device__ __forceinline__ void gemm_xd_tile(const Params &p, int tm, int tn, int zz) {
+    constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
+    constexpr int SA = BM * BKT, SB = BN * BKT, STAGE = SA + SB;
+    constexpr int PER = (BM + BN) * (BKT / 4) / 64 / 4;  // loads per wavefront and chunk
+    static_assert(PER <= 63, "vmcnt holds at most 63");
+    // 64 floats of pad ahead of the stages: no stage starts at LDS address 0
+    __shared__ __attribute__((aligned(16))) float S[64 + 3 * STAGE];
+
+    if (zz >= p.batch * p.splits) return;
+    const int z = zz / p.splits, split = zz % p.splits;
+    const int outer = z / p.batch_div, inner = z % p.batch_div;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const float *A = p.a + outer * p.sa_outer + inner * p.sa_inner + (int64_t)m0 * p.lda;
+    const float *B = p.b + outer * p.sb_outer + inner * p.sb_inner + (int64_t)n0 * p.ldb;
+    const int kbeg = split * p.k_split;
+    const int nk = (min(p.k, kbeg + p.k_split) - kbeg) / BKT;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
+    const int wm0 = (wv >> 1) * (BM / 2), wn0 = (wv & 1) * (BN / 2);
+
+    floatx4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // This lane's source rows for the first instruction (slot 64 w + lane of the stage), with the swizzle that puts
+    // the float4 chunk of column group c into slot column c ^ kswz(r); rows 256 / CH apart share the swizzle.
+    constexpr int CH = BKT / 4;
+    static_assert((256 / CH) % 16 == 0, "the swizzle repeats every 16 rows");
+    const int slot0 = wv * 64 + lane, r0 = slot0 / CH, c0 = (slot0 % CH) ^ kswz<BKT>(r0);
+    const float *srcA = A + (int64_t)r0 * p.lda + kbeg + 4 * c0;
+    const float *srcB = B + (int64_t)r0 * p.ldb + kbeg + 4 * c0;
+    const unsigned wave = __builtin_amdgcn_readfirstlane(wv);
+    const unsigned lds0 = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void *)(S + 64) + wave * 1024u;
+    auto issue = [&](int t, int st) {
+        const unsigned base = lds0 + (unsigned)(st * STAGE) * 4u;
+        dma_chunk<BM, BKT>(srcA + t * BKT, p.lda, base);
+        dma_chunk<BN, BKT>(srcB + t * BKT, p.ldb, base + SA * 4u);
+    };
+    auto compute = [&](int st) {
+        const float *Ab = S + 64 + st * STAGE, *Bb = Ab + SA;
+#pragma unroll
+        for (int blk = 0; blk < NB; blk++) {
+            floatx4 fa[TM], fb[TN];
+#pragma unroll
+            for (int x = 0; x < TM; x++)
+                fa[x] = *reinterpret_cast<const floatx4 *>(&Ab[kaddr<BKT>(wm0 + x * 16 + l16, blk * 4 + kl)]);
+#pragma unroll
+            for (int x = 0; x < TN; x++)
+                fb[x] = *reinterpret_cast<const floatx4 *>(&Bb[kaddr<BKT>(wn0 + x * 16 + l16, blk * 4 + kl)]);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        }
+    };
+    // lgkmcnt(0) too: this wavefront's LDS reads of the previous chunk must be complete before the barrier, since
+    // after it other wavefronts load into that stage (the compiler may leave reads in flight past the barrier asm).
+    auto step = [&](int t, int st) {
+        if (t + 1 < nk) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(PER) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        if (t + 2 < nk) issue(t + 2, st == 0 ? 2 : st - 1);
+        compute(st);
+    };
+    if (nk > 0) issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    int t = 0;
+    for (; t + 3 <= nk; t += 3) {  // unrolled by three so every stage index is a constant
+        step(t, 0);
+        step(t + 1, 1);
+        step(t + 2, 2);
+    }
+    if (t < nk) step(t, 0);
+    if (t + 1 < nk) step(t + 1, 1);
+
+    float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
+    const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
+    tile_epilogue<TM, TN, true, true, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
+}
+
+template <int BM, int BN, int BKT, bool GELU = false>
+__global__ void __launch_bounds__(NT) k_gemm_xd(Params p) {
+    int tm, tn, zz;
+    tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
+    gemm_xd_tile<BM, BN, BKT, GELU>(p, tm, tn, zz);
+}
+
 // Weight gradients of several products in one launch (om_linear_bwd_dw_group): product i owns the workgroups
 // [start[i], start[i+1]) of the XCD-remapped grid, each a (tile, split) of its own Params, run by the same tile body.
 template <int BM, int BN, int BKT>
