@@ -417,6 +417,9 @@ __device__ __forceinline__ void dma_chunk(const float *src, int64_t ld, unsigned
     constexpr int INSTR = ROWS * (BKT / 4) / 64;  // wavefront instructions per stage and operand
     static_assert(INSTR % 4 == 0, "each of the four wavefronts issues whole instructions");
     constexpr int CH = BKT / 4;  // float4 chunks per row
+    // m0 is a reserved register: the compiler warns that it does not keep a value of its own in m0 across this
+    // statement. That is safe here because nothing else in these kernels reads m0 (no LDS-direct or
+    // relative-indexing instructions in their assembly), so each load's m0 is the one set just before it.
 #pragma unroll
     for (int j = 0; j < INSTR / 4; j++) {
         const float *g = src + (int64_t)j * (256 / CH) * ld;
