@@ -210,6 +210,12 @@ om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float 
  * diff, t + t), so a loss that is the root of the backward needs no separate gradient launch. */
 om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n);
+/* The same (dpred_unit may be NULL) with the loss also posted to rb, as om_readback_post(rb, loss, 4) would post
+ * it, by the launch that finishes the loss's sum (which then writes the value to the pinned buffer, fences, and
+ * writes the sequence number). No counterpart in the reference (whose loss is a host float after the forward): it
+ * spares the loss's own readback launch. Waits for rb's previous post like om_readback_post. */
+om_status om_mse_fwd_post(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
+                          float *dpred_unit, int64_t n, om_readback *rb);
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- reductions */

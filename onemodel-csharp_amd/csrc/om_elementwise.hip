@@ -109,12 +109,27 @@ __global__ void __launch_bounds__(kBlock) k_sum_partial(const float *__restrict_
     double t = omd::block_sum<kBlock / 64>(acc, sh);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
+// Optionally also posts the result to a readback buffer as k_readback does: the value, a system-scope fence, then
+// the sequence number.
+struct PostTo {
+    char *dst;
+    uint64_t *seq_at;
+    uint64_t seq;
+};
 __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ part, int np, float *__restrict__ out,
-                                                  double divisor) {
+                                                  double divisor, PostTo post) {
     double acc = 0.0;
     for (int i = threadIdx.x; i < np; i += 64) acc += part[i];
     acc = omd::wave_sum(acc);
-    if (threadIdx.x == 0) out[0] = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;
+    if (threadIdx.x == 0) {
+        const float v = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;
+        out[0] = v;
+        if (post.dst) {
+            *reinterpret_cast<float *>(post.dst) = v;
+            __threadfence_system();
+            *reinterpret_cast<volatile uint64_t *>(post.seq_at) = post.seq;
+        }
+    }
 }
 
 // Column sums of a [rows, cols] matrix in double. Stage 1: a block covers 64 columns (one per lane, coalesced
@@ -289,28 +304,42 @@ om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int3
 }
 
 static om_status mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, float *unit,
-                         int64_t n) {
+                         int64_t n, om_readback *rb) {
     float *scr;
     om_status s = om::scratch(ctx, sizeof(double) * kSumBlocks, &scr);
     if (s) return s;
     double *part = reinterpret_cast<double *>(scr);
-    int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
+    const int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
+    PostTo post{nullptr, nullptr, 0};
+    if (rb) {
+        s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq);
+        if (s) return s;
+    }
     hipLaunchKernelGGL(k_mse_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, pred, target, diff, n, part, unit);
-    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, loss, (double)n);
-    return OM_LAUNCH_CHECK(ctx, "om_mse_fwd");
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, loss, (double)n, post);
+    s = OM_LAUNCH_CHECK(ctx, "om_mse_fwd");
+    if (s == OM_OK && rb) om::readback_posted(rb, post.seq, sizeof(float));
+    return s;
 }
 
 om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, pred && target && diff && loss && n > 0, "om_mse_fwd: bad arguments");
-    return mse_fwd(ctx, pred, target, diff, loss, nullptr, n);
+    return mse_fwd(ctx, pred, target, diff, loss, nullptr, n, nullptr);
 }
 
 om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, pred && target && diff && loss && dpred_unit && n > 0, "om_mse_fwd_unit: bad arguments");
-    return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n);
+    return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n, nullptr);
+}
+
+om_status om_mse_fwd_post(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
+                          float *dpred_unit, int64_t n, om_readback *rb) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, pred && target && diff && loss && n > 0 && rb, "om_mse_fwd_post: bad arguments");
+    return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n, rb);
 }
 
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate) {
@@ -371,7 +400,8 @@ om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mea
     double *part = reinterpret_cast<double *>(scr);
     int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
     hipLaunchKernelGGL(k_sum_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, x, n, part);
-    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, out, mean ? (double)n : 0.0);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, out, mean ? (double)n : 0.0,
+                       PostTo{nullptr, nullptr, 0});
     return OM_LAUNCH_CHECK(ctx, "om_sum_all");
 }
 

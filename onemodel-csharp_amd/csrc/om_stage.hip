@@ -201,6 +201,29 @@ om_status await(om_readback *r) {
 
 }  // namespace
 
+namespace om {
+
+om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq) {
+    OM_REQUIRE(ctx, r && r->ctx == ctx, "readback post: the readback belongs to another context");
+    OM_REQUIRE(ctx, bytes > 0 && bytes <= r->bytes, "readback post: need 1 .. %llu bytes", (unsigned long long)r->bytes);
+    // The pinned buffer may still be the target of the previous post.
+    if (r->posted) {
+        om_status st = await(r);
+        if (st) return st;
+    }
+    *dst = r->host_dev;
+    *seq_at = reinterpret_cast<uint64_t *>(r->host_dev + (r->bytes + 7) / 8 * 8);
+    *seq = r->seq + 1;
+    return OM_OK;
+}
+
+void readback_posted(om_readback *r, uint64_t seq, uint64_t bytes) {
+    r->seq = seq;
+    r->posted = bytes;
+}
+
+}  // namespace om
+
 extern "C" {
 
 om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out) {
@@ -237,20 +260,16 @@ om_status om_readback_destroy(om_readback *r) {
 om_status om_readback_post(om_readback *r, const void *src, uint64_t bytes) {
     if (!r) return OM_E_ARG;
     om_ctx *ctx = r->ctx;
-    OM_REQUIRE(ctx, src && bytes > 0 && bytes <= r->bytes, "om_readback_post: need a source and 1 .. %llu bytes",
-               (unsigned long long)r->bytes);
-    // The pinned buffer may still be the target of the previous post.
-    if (r->posted) {
-        om_status st = await(r);
-        if (st) return st;
-    }
-    const uint64_t seq = r->seq + 1;
-    hipLaunchKernelGGL(k_readback, dim3(1), dim3(256), 0, ctx->stream, r->host_dev, static_cast<const char *>(src),
-                       bytes, reinterpret_cast<uint64_t *>(r->host_dev + (r->bytes + 7) / 8 * 8), seq);
-    om_status st = OM_LAUNCH_CHECK(ctx, "om_readback_post");
+    OM_REQUIRE(ctx, src, "om_readback_post: NULL source");
+    char *dst;
+    uint64_t *seq_at, seq;
+    om_status st = om::readback_target(ctx, r, bytes, &dst, &seq_at, &seq);
     if (st) return st;
-    r->seq = seq;
-    r->posted = bytes;
+    hipLaunchKernelGGL(k_readback, dim3(1), dim3(256), 0, ctx->stream, dst, static_cast<const char *>(src), bytes,
+                       seq_at, seq);
+    st = OM_LAUNCH_CHECK(ctx, "om_readback_post");
+    if (st) return st;
+    om::readback_posted(r, seq, bytes);
     return OM_OK;
 }
 

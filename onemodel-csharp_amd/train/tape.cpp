@@ -693,8 +693,14 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     // the gradient for a unit upstream gradient comes with the forward: the loss is normally the backward's root,
     // whose seed gradient is exactly that unit
     float *unit = rec && pred->requires_grad ? dev().step_floats(n) : nullptr;
-    if (unit) OMT(om_mse_fwd_unit(C(), pred->data, target->data, diff, loss->data, unit, n));
-    else OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
+    if (om_readback *rb = dev().take_loss_post()) {
+        OMT(om_mse_fwd_post(C(), pred->data, target->data, diff, loss->data, unit, n, rb));
+        dev().set_loss_posted(loss->data);
+    } else if (unit) {
+        OMT(om_mse_fwd_unit(C(), pred->data, target->data, diff, loss->data, unit, n));
+    } else {
+        OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
+    }
     if (rec)
         attach(loss, "Mse", {pred, target}, [diff, unit, n](Engine &e, Record &r, const float *g) {
             if (unit && g == dev().one()) {

@@ -77,11 +77,27 @@ class Device {
     void step_reset();
     void sync();
     bool overlap() const { return overlap_; }
+    // Loss readback folded into the loss's own launch: arm_loss_post(rb) offers rb to the next loss op that can post
+    // its value itself (MSE); that op takes it (take_loss_post) and reports what it posted (loss_posted), so the
+    // step posts the loss separately only when the offer was not taken for that very tensor.
+    void arm_loss_post(om_readback *rb) {
+        loss_rb_ = rb;
+        loss_posted_ = nullptr;
+    }
+    om_readback *take_loss_post() {
+        om_readback *r = loss_rb_;
+        loss_rb_ = nullptr;
+        return r;
+    }
+    void set_loss_posted(const float *p) { loss_posted_ = p; }
+    const float *loss_posted() const { return loss_posted_; }
 
    private:
     om_ctx *ctx_ = nullptr;
     bool overlap_ = false;
     float *one_ = nullptr;
+    om_readback *loss_rb_ = nullptr;
+    const float *loss_posted_ = nullptr;
 };
 
 Device &dev();            // the device of the current thread's model (set by Model)

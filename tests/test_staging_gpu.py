@@ -183,3 +183,49 @@ def test_readback_wait_before_any_post_is_refused(pkg):
     finally:
         L.om_readback_destroy(r)
         d.ctx.close()
+
+
+def test_mse_posts_its_loss_from_its_own_launch(pkg):
+    """om_mse_fwd_post: the loss, diff and unit gradient of om_mse_fwd_unit bit for bit, and the same loss landed in
+    the readback buffer with no readback launch of its own; over sizes from one workgroup to the grid-stride range,
+    posts in a row, and a readback of another context refused."""
+    from gpu_util import Dev
+    d = Dev()
+    L = d.ctx.L
+    r = C.c_void_p()
+    d.call("om_readback_create", C.c_uint64(4), C.byref(r))
+    rng = np.random.default_rng(5)
+    try:
+        for n in (1, 255, 256, 1000, 65536, 1572864, 262144 * 4 + 17):
+            pred = rng.standard_normal(n).astype(np.float32)
+            tgt = rng.standard_normal(n).astype(np.float32)
+            P, TG = d.put(pred), d.put(tgt)
+            D1, L1, U1 = d.empty((n,)), d.empty((1,)), d.empty((n,))
+            D2, L2, U2 = d.empty((n,)), d.empty((1,)), d.empty((n,))
+            d.call("om_mse_fwd_unit", P, TG, D1, L1, U1, C.c_int64(n))
+            d.call("om_mse_fwd_post", P, TG, D2, L2, U2, C.c_int64(n), r)
+            got = np.zeros(1, np.float32)
+            assert L.om_readback_wait(r, got.ctypes.data, C.c_uint64(4)) == 0
+            loss = d.get(L1)
+            assert np.array_equal(d.get(L2).view(np.uint32), loss.view(np.uint32)), n
+            assert np.array_equal(got.view(np.uint32), loss.view(np.uint32)), n
+            assert np.array_equal(d.get(D2), d.get(D1)) and np.array_equal(d.get(U2), d.get(U1))
+            ref = np.mean((pred.astype(np.float64) - tgt) ** 2)
+            assert abs(float(loss[0]) - ref) <= 1e-6 * ref, n
+        # without a unit gradient, and two posts back to back: the second waits for the first's copy
+        pred = rng.standard_normal(4096).astype(np.float32)
+        P, TG, DD, LA, LB = d.put(pred), d.put(np.zeros(4096, np.float32)), d.empty((4096,)), d.empty((1,)), d.empty((1,))
+        d.call("om_mse_fwd_post", P, TG, DD, LA, None, C.c_int64(4096), r)
+        d.call("om_mse_fwd_post", TG, TG, DD, LB, None, C.c_int64(4096), r)
+        got = np.zeros(1, np.float32)
+        assert L.om_readback_wait(r, got.ctypes.data, C.c_uint64(4)) == 0
+        assert got[0] == 0.0 and d.get(LB)[0] == 0.0
+        assert abs(float(d.get(LA)[0]) - np.mean(pred.astype(np.float64) ** 2)) <= 1e-6
+        other = Dev()
+        try:
+            assert other.status("om_mse_fwd_post", P, TG, DD, LA, None, C.c_int64(4096), r) != 0
+        finally:
+            other.ctx.close()
+    finally:
+        L.om_readback_destroy(r)
+        d.ctx.close()
