@@ -366,6 +366,128 @@ __global__ void __launch_bounds__(L * 4) k_attn_bwd(const float *__restrict__ q,
     if (dq) store_rows<D>(dq + row0 * ldd + h * D, ldd, q0, dqa, t, kl, acc);
 }
 
+// Backward with P^T and dS^T staged a quarter at a time (32 queries by all keys) in the LDS that V held, so a
+// workgroup needs only Q, K, V and dO in LDS (74 KB at L = 128: two workgroups per CU, one round for C3's 384).
+// The row phase is k_attn_bwd's (each wavefront: S, P, dP and dS for its 16 queries, in registers). Then, per
+// quarter r of the queries (those of wavefronts 2r and 2r+1): those two wavefronts write their P^T columns, every
+// wavefront adds the quarter's terms to dV for its 16 keys; the same with dS^T for dK, while four wavefronts each
+// take one 16 x 16 block of the quarter's dQ over all keys. Every sum runs over the same index sequence as in
+// k_attn_bwd (queries, or keys, in increasing order, one MFMA chain), so the results are bit for bit its results.
+// Each workgroup's own path is longer (eight barrier rounds): the launcher takes this kernel only when the
+// (head, batch) pairs outnumber the CUs.
+template <int D, int L>
+__global__ void __launch_bounds__(L * 4, 2) k_attn_bwd_q(const float *__restrict__ q, const float *__restrict__ k,
+                                                         const float *__restrict__ v, int ld,
+                                                         const float *__restrict__ mask, int64_t mask_bstride,
+                                                         const float *__restrict__ g, int ldg, float *dq, float *dk,
+                                                         float *dv, int ldd, float scale, int acc) {
+    constexpr int NTH = L * 4, LDX = D + 4, NB = L / 16, NW = L / 16, QT = 32, LDT = QT + 4, DB = D / 16;
+    static_assert(D == 32, "the quarter's dQ is four 16 x 16 blocks");
+    static_assert(QT * LDT <= L * LDX / 1 && L * LDT <= L * LDX, "a quarter of P^T fits where V was");
+    __shared__ __attribute__((aligned(16))) float Qs[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Ks[L * LDX];
+    __shared__ __attribute__((aligned(16))) float Vs[L * LDX];  // V, then a quarter of P^T or dS^T: [key][32 queries]
+    __shared__ __attribute__((aligned(16))) float Gs[L * LDX];
+    float *T = Vs;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int64_t row0 = (int64_t)b * L;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
+    const int q0 = 16 * w;  // this wavefront's queries; also its block of 16 keys for dK and dV
+    {
+        float mv[4][L / 16];
+        load_mask<L>(mv, mask ? mask + b * mask_bstride + (int64_t)(q0 + 4 * kl) * L : nullptr, t);
+        {
+            Stage<D, NTH, L> sq, sk, sv, sg;
+            sq.load(q + row0 * ld + h * D, ld);
+            sk.load(k + row0 * ld + h * D, ld);
+            sv.load(v + row0 * ld + h * D, ld);
+            sg.load(g + row0 * ldg + h * D, ldg);
+            sq.store(Qs);
+            sk.store(Ks);
+            sv.store(Vs);
+            sg.store(Gs);
+        }
+        __syncthreads();
+        floatx4 s[NB];
+        scores<D, L>(s, Qs, Ks, q0, t, kl);
+        softmax_rows<L>(s, mv, mask != nullptr, scale);
+        floatx4 dp[NB];
+        scores<D, L>(dp, Gs, Vs, q0, t, kl);  // dP = dO V^T
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            double dot = 0.0;
+#pragma unroll
+            for (int j = 0; j < NB; j++) dot += (double)(dp[j][r] * s[j][r]);
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 16);
+            const float df = (float)dot;
+#pragma unroll
+            for (int j = 0; j < NB; j++) dp[j][r] = (s[j][r] * (dp[j][r] - df)) * scale;
+        }
+        __syncthreads();  // V is read; its LDS now takes the quarters
+
+        // acc[jn] += A (16 keys a0.., k = the quarter's 32 queries from T) x B (rows qb0.. of Bs, interleaved d)
+        auto quarter_mm = [&](floatx4(&accv)[DB], const float *Bs, int qb0) {
+#pragma unroll
+            for (int blk = 0; blk < QT / 16; blk++) {
+                floatx4 a = *reinterpret_cast<const floatx4 *>(&T[(q0 + t) * LDT + 16 * blk + 4 * kl]);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float *brow = &Bs[(qb0 + 16 * blk + 4 * kl + u) * LDX + DB * t];
+                    float2 w2 = *reinterpret_cast<const float2 *>(brow);
+                    accv[0] = mfma4(a[u], w2.x, accv[0]);
+                    accv[1] = mfma4(a[u], w2.y, accv[1]);
+                }
+            }
+        };
+        floatx4 dva[DB], dka[DB];
+#pragma unroll
+        for (int jn = 0; jn < DB; jn++) dva[jn] = dka[jn] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // dV = P^T dO, a quarter of the queries at a time
+#pragma unroll
+        for (int r = 0; r < NW / 2; r++) {
+            if ((w >> 1) == r) {
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    *reinterpret_cast<floatx4 *>(&T[(16 * j + t) * LDT + 16 * (w & 1) + 4 * kl]) = s[j];
+            }
+            __syncthreads();
+            quarter_mm(dva, Gs, QT * r);
+            __syncthreads();
+        }
+        // dK = dS^T Q and dQ = dS K, the same way
+#pragma unroll
+        for (int r = 0; r < NW / 2; r++) {
+            if ((w >> 1) == r) {
+#pragma unroll
+                for (int j = 0; j < NB; j++)
+                    *reinterpret_cast<floatx4 *>(&T[(16 * j + t) * LDT + 16 * (w & 1) + 4 * kl]) = dp[j];
+            }
+            __syncthreads();
+            quarter_mm(dka, Qs, QT * r);
+            // the quarter's dQ: block (qb, db) of four, over all keys in increasing order
+            const bool mine = NW == 4 || (w >> 2) == (r & 1);
+            if (dq && mine) {
+                const int blkq = w & 3, qb = blkq >> 1, db = blkq & 1;
+                floatx4 qa = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int blk = 0; blk < NB; blk++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int key = 16 * blk + 4 * kl + u;
+                        qa = mfma4(T[key * LDT + 16 * qb + t], Ks[key * LDX + 16 * db + t], qa);
+                    }
+                float *dst = dq + (row0 + QT * r + 16 * qb + 4 * kl) * ldd + h * D + 16 * db + t;
+#pragma unroll
+                for (int e = 0; e < 4; e++) dst[e * ldd] = acc ? dst[e * ldd] + qa[e] : qa[e];
+            }
+            __syncthreads();
+        }
+        if (dv) store_rows<D>(dv + row0 * ldd + h * D, ldd, q0, dva, t, kl, acc);
+        if (dk) store_rows<D>(dk + row0 * ldd + h * D, ldd, q0, dka, t, kl, acc);
+    }
+}
+
 bool fused_ok(const float *q, const float *k, const float *v, int ld, int ldo, int lq, int lk, int d) {
     auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
     return d == 32 && lq == lk && (lq == 64 || lq == 128) && ld % 4 == 0 && ldo % 4 == 0 && al(q) && al(k) && al(v);
@@ -423,6 +545,18 @@ om_status om_attention_bwd_fused(om_ctx *ctx, const float *q, const float *k, co
     const int64_t mstride = (mask && mask_batched) ? (int64_t)L * L : 0;
     if (fused_ok(q, k, v, ld_qkv, ld_d, L, L, d) && ld_g % 4 == 0 && ((uintptr_t)g & 15) == 0) {
         dim3 grid(H, B);
+        // More (head, batch) pairs than CUs: the quarter-staged kernel fits two per CU, one round instead of two
+        // (C3: 46 against 48 us); fewer: one round either way, and k_attn_bwd's shorter path per workgroup wins.
+        // The results are the same bits.
+        if ((int64_t)B * H > ctx->num_cus) {
+            if (L == 128)
+                hipLaunchKernelGGL((k_attn_bwd_q<32, 128>), grid, dim3(512), 0, ctx->stream, q, k, v, ld_qkv, mask,
+                                   mstride, g, ld_g, dq, dk, dv, ld_d, scale, acc);
+            else
+                hipLaunchKernelGGL((k_attn_bwd_q<32, 64>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask,
+                                   mstride, g, ld_g, dq, dk, dv, ld_d, scale, acc);
+            return OM_LAUNCH_CHECK(ctx, "om_attention_bwd_fused");
+        }
         if (L == 128)
             hipLaunchKernelGGL((k_attn_bwd<32, 128>), grid, dim3(512), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
                                g, ld_g, dq, dk, dv, ld_d, scale, acc);

@@ -456,7 +456,8 @@ def test_attention_packed_qkv_strides(dev, T, B, H, L, D):
 
 @pytest.mark.parametrize("B,H,L,D,masked,packed", [(4, 12, 128, 32, True, True), (3, 2, 64, 32, True, False),
                                                      (2, 3, 128, 32, False, False), (2, 3, 40, 32, True, False),
-                                                     (1, 2, 128, 64, True, True)])
+                                                     (1, 2, 128, 64, True, True), (24, 12, 128, 32, True, True),
+                                                     (24, 12, 64, 32, False, False)])
 def test_attention_fused_recompute(dev, T, B, H, L, D, masked, packed):
     """om_attention_{fwd,bwd}_fused (no saved weights; the backward recomputes P): the fused kernels for D = 32 and
     L in {64, 128}, the GEMM fallback otherwise; against the oracle, and accumulating into existing gradients."""
@@ -502,6 +503,33 @@ def test_attention_fused_recompute(dev, T, B, H, L, D, masked, packed):
              C.c_float(scale), 1)
     for gd, ref in zip(got(), (dq, dk, dv)):
         assert scaled(heads(gd) - np.float32(0.5), ref) <= TOL
+
+
+@pytest.mark.parametrize("L,masked", [(128, True), (128, False), (64, True)])
+def test_attention_bwd_kernels_agree(dev, L, masked):
+    """The backward's two fused kernels give the same bits: 24 x 12 (head, batch) pairs run the quarter-staged
+    kernel (more pairs than CUs), each half of the batch alone the one-pass kernel; same inputs, accumulating into
+    the same initial gradients."""
+    B, H, D = 24, 12, 32
+    W = H * D
+    rng = np.random.default_rng(L + masked)
+    qkv, g = rnd(rng, B, L, 3 * W), rnd(rng, B, L, W)
+    mask = np.where(rng.random((B, L, L)) < 0.15, -1e9, 0.0).astype(np.float32) if masked else None
+    init = rnd(rng, B, L, 3 * W)
+    QKV, G, M = dev.put(qkv), dev.put(g), (dev.put(mask) if masked else None)
+    outs = []
+    for halves in (1, 2):
+        D3 = dev.put(init)
+        bh = B // halves
+        for i in range(halves):
+            off = i * bh * L
+            q = QKV.data_ptr() + 4 * off * 3 * W
+            m = (M.data_ptr() + 4 * i * bh * L * L) if masked else None
+            dq = D3.data_ptr() + 4 * off * 3 * W
+            dev.call("om_attention_bwd_fused", q, q + 4 * W, q + 8 * W, 3 * W, m, 1, G.data_ptr() + 4 * off * W, W,
+                     dq, dq + 4 * W, dq + 8 * W, 3 * W, bh, H, L, D, C.c_float(0.0), 1)
+        outs.append(dev.get(D3))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------------ conv and pool
