@@ -325,6 +325,78 @@ def pmc_probe(pkg, model):
     L.om_ctx_sync(ctx)
 
 
+# The dense products of one C3 step, as (name, m, n, k, ta, tb): C[m,n] = op(A) op(B) with A [m,k] (or [k,m] when ta)
+# and B [k,n] (or [n,k] when tb).
+C3_PRODUCTS = [("q|k|v projection", 4096, 1152, 384, 0, 1), ("attention output", 4096, 384, 384, 0, 1),
+               ("FFN 384->1536", 4096, 1536, 384, 0, 1), ("FFN 1536->384", 4096, 384, 1536, 0, 1),
+               ("dX FFN 1536->384", 4096, 1536, 384, 0, 0), ("dX FFN 384->1536", 4096, 384, 1536, 0, 0),
+               ("dX attention output", 4096, 384, 384, 0, 0), ("dX q|k|v", 4096, 384, 1152, 0, 0)]
+
+
+def vendor_gemm(reps: int = 30):
+    """This library's products at the C3 shapes beside torch.mm in fp32 (hipBLASLt / rocBLAS), same random operands,
+    warm, HIP events on each side's stream: a calibration of the GEMM engine against the vendor library. The weight
+    gradients are compared as the C3 step runs them: the library's one grouped launch (with its reduce and bias
+    sums) against four torch.mm calls (without bias sums). Prints a markdown table."""
+    import numpy as np
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    pkg = load_pkg()
+    L = pkg.load_hip()
+    ctx = C.c_void_p()
+    assert L.om_ctx_create(0, C.byref(ctx)) == 0
+    ev = HipEvents()
+    dev = torch.device("cuda")
+    tev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def torch_time(f):
+        for _ in range(3):
+            f()
+        e0, e1 = tev(), tev()
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    rows = ["| product | m x n x k | this library us | TFLOP/s | torch.mm us | TFLOP/s |", "|---|---|---:|---:|---:|---:|"]
+    big = 4096 * 1536
+    a, b, c = _dev_rand(L, ctx, big, 0.1, 1), _dev_rand(L, ctx, big, 0.1, 2), _dev_buf(L, ctx, big, 0.0)
+    for name, m, n, k, ta, tb in C3_PRODUCTS:
+        lda, ldb = (m if ta else k), (k if tb else n)
+        f = lambda: L.om_gemm(ctx, ta, tb, m, n, k, a, lda, b, ldb, c, n, None, 0, None)
+        for _ in range(3):
+            assert f() == 0, L.om_last_error(ctx)
+        ms = ev.time(L.om_ctx_stream(ctx), f, reps)
+        A = torch.randn(k, m, device=dev).t() if ta else torch.randn(m, k, device=dev)
+        B = torch.randn(n, k, device=dev).t() if tb else torch.randn(k, n, device=dev)
+        tm = torch_time(lambda: torch.mm(A, B))
+        fl = 2.0 * m * n * k
+        rows.append(f"| {name} | {m} x {n} x {k} | {ms * 1e3:.1f} | {fl / ms / 1e9:.1f} | {tm * 1e3:.1f} | "
+                    f"{fl / tm / 1e9:.1f} |")
+    items = (pkg.om_linear_dw * 4)()
+    for i, (inf, outf) in enumerate(DOMINANT_SHAPES):
+        g, x = _dev_rand(L, ctx, DOMINANT_ROWS * outf, 0.1, 10 + i), _dev_rand(L, ctx, DOMINANT_ROWS * inf, 0.1, 20 + i)
+        dw, db = _dev_buf(L, ctx, outf * inf, 0.0), _dev_buf(L, ctx, outf, 0.0)
+        items[i] = pkg.om_linear_dw(g.value, x.value, dw.value, db.value, inf, outf, 0, 0)
+    f = lambda: L.om_linear_bwd_dw_group(ctx, 4, C.cast(items, C.c_void_p), DOMINANT_ROWS)
+    for _ in range(3):
+        assert f() == 0, L.om_last_error(ctx)
+    ms = ev.time(L.om_ctx_stream(ctx), f, reps)
+    ts = [(torch.randn(DOMINANT_ROWS, outf, device=dev), torch.randn(DOMINANT_ROWS, inf, device=dev))
+          for inf, outf in DOMINANT_SHAPES]
+    tm = torch_time(lambda: [torch.mm(g.t(), x) for g, x in ts])
+    fl = sum(2.0 * DOMINANT_ROWS * i * o for i, o in DOMINANT_SHAPES)
+    rows.append(f"| the four weight gradients (dW = g^T x, K = 4096) | 1536x384, 384x1536, 384x384, 1152x384 | "
+                f"{ms * 1e3:.1f} | {fl / ms / 1e9:.1f} | {tm * 1e3:.1f} | {fl / tm / 1e9:.1f} |")
+    A, B = torch.randn(8192, 8192, device=dev), torch.randn(8192, 8192, device=dev)
+    tm = torch_time(lambda: torch.mm(A, B))
+    rows.append(f"| (large square, torch only) | 8192 x 8192 x 8192 | | | {tm * 1e3:.1f} | {2.0 * 8192 ** 3 / tm / 1e9:.1f} |")
+    L.om_ctx_destroy(ctx)
+    print("\n".join(rows))
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed counter summary (two rocprofv3 --pmc runs of
     `bench.py --pmc-probe`, each counter scaled by its reading for the known-size copy), or None without one."""
@@ -365,10 +437,15 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches a counter run needs (no timing line)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only the C3 products beside torch.mm (hipBLASLt / rocBLAS), as a markdown table")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    if a.vendor_gemm:
+        vendor_gemm()
+        return
     pkg = load_pkg()
     model = pkg.Model(a.config)
     if a.pmc_probe:
