@@ -327,10 +327,10 @@ def pmc_probe(pkg, model):
 
 # The dense products of one C3 step, as (name, m, n, k, ta, tb): C[m,n] = op(A) op(B) with A [m,k] (or [k,m] when ta)
 # and B [k,n] (or [n,k] when tb).
-C3_PRODUCTS = [("q|k|v projection", 4096, 1152, 384, 0, 1), ("attention output", 4096, 384, 384, 0, 1),
+C3_PRODUCTS = [("q, k, v projection", 4096, 1152, 384, 0, 1), ("attention output", 4096, 384, 384, 0, 1),
                ("FFN 384->1536", 4096, 1536, 384, 0, 1), ("FFN 1536->384", 4096, 384, 1536, 0, 1),
                ("dX FFN 1536->384", 4096, 1536, 384, 0, 0), ("dX FFN 384->1536", 4096, 384, 1536, 0, 0),
-               ("dX attention output", 4096, 384, 384, 0, 0), ("dX q|k|v", 4096, 384, 1152, 0, 0)]
+               ("dX attention output", 4096, 384, 384, 0, 0), ("dX q, k, v", 4096, 384, 1152, 0, 0)]
 
 
 def vendor_gemm(reps: int = 30):
