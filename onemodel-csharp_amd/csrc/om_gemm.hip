@@ -107,6 +107,19 @@ __device__ __forceinline__ void reduce_quad(const Params &p, int64_t q) {
         v[2] += t[s].z;
         v[3] += t[s].w;
     }
+    // A plain epilogue (every weight gradient) writes the quad as one float4, with the same arithmetic.
+    const bool plain = p.alpha == 1.0f && !p.bias && !p.resid && p.epi == EPI_NONE && p.ldc % 4 == 0 &&
+                       ((uintptr_t)p.c & 15) == 0;
+    if (plain) {
+        float4 *dst = reinterpret_cast<float4 *>(p.c + (int64_t)row * p.ldc + col0);
+        float4 o = make_float4(v[0], v[1], v[2], v[3]);
+        if (p.accumulate) {
+            const float4 c = *dst;
+            o = make_float4(c.x + v[0], c.y + v[1], c.z + v[2], c.w + v[3]);
+        }
+        *dst = o;
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < 4; u++) epilogue(p, p.c, p.ldc, nullptr, row, col0 + u, v[u]);
 }
