@@ -1,6 +1,6 @@
 """Kernel-level parity of lib/libom_hip.so against the CPU oracle (oracle/om_oracle.c), on the GPU.
 
-Bars: floating-point results within 1e-5 scaled error (max|a-b|/max|ref|, the
+Bars (the benchmark's stated parity bar): floating-point results within 1e-5 scaled error (max|a-b|/max|ref|, the
 reference's metric, AutogradModelTests.cs:20-30); integer work (pool indices) and the optimizer update bit-exact;
 kernels that restate the reference's fixed-order arithmetic (LayerNorm forward, softmax rows, GELU, CTC) are checked
 bit-for-bit as well.
