@@ -207,10 +207,11 @@ om_status om_permute(om_ctx *ctx, const float *x, float *y, int ndim, const int3
  * order: t = (g / (float)n) * diff, dpred = t + t (the two Mul emissions added, Engine.AddInto). */
 om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss, int64_t n);
 /* The same, also writing dpred_unit = the backward's dpred for a unit upstream gradient (g = 1: t = (1 / (float)n) *
- * diff, t + t), so a loss that is the root of the backward needs no separate gradient launch. */
+ * diff, t + t), so a loss that is the root of the backward needs no separate gradient launch. diff may be NULL (not
+ * written): a caller that needs it later only off that path recomputes it with om_sub. */
 om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n);
-/* The same (dpred_unit may be NULL) with the loss also posted to rb, as om_readback_post(rb, loss, 4) would post
+/* The same (dpred_unit or diff may be NULL, not both) with the loss also posted to rb, as om_readback_post(rb, loss, 4) would post
  * it, by the launch that finishes the loss's sum (which then writes the value to the pinned buffer, fences, and
  * writes the sequence number). No counterpart in the reference (whose loss is a host float after the forward): it
  * spares the loss's own readback launch. Waits for rb's previous post like om_readback_post. */

@@ -243,8 +243,8 @@ __global__ void __launch_bounds__(kBlock) k_permute(const float *__restrict__ x,
     }
 }
 
-// MSE: diff and per-block double partial sums of fl(diff*diff); a final pass adds the partials in block order.
-// With unit != NULL it also writes the gradient for a unit upstream gradient, k_mse_bwd's arithmetic with g = 1.
+// MSE: diff (unless NULL) and per-block double partial sums of fl(diff*diff); a final pass adds the partials in block
+// order. With unit != NULL it also writes the gradient for a unit upstream gradient, k_mse_bwd's arithmetic with g = 1.
 __global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict__ p, const float *__restrict__ t,
                                                         float *__restrict__ diff, int64_t n,
                                                         double *__restrict__ part, float *__restrict__ unit) {
@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict_
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float d = p[i] - t[i];
-        diff[i] = d;
+        if (diff) diff[i] = d;
         acc += (double)(d * d);
         if (unit) {
             float u = dsq * d;
@@ -331,14 +331,14 @@ om_status om_mse_fwd(om_ctx *ctx, const float *pred, const float *target, float 
 om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n) {
     OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, pred && target && diff && loss && dpred_unit && n > 0, "om_mse_fwd_unit: bad arguments");
+    OM_REQUIRE(ctx, pred && target && loss && dpred_unit && n > 0, "om_mse_fwd_unit: bad arguments");
     return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n, nullptr);
 }
 
 om_status om_mse_fwd_post(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n, om_readback *rb) {
     OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, pred && target && diff && loss && n > 0 && rb, "om_mse_fwd_post: bad arguments");
+    OM_REQUIRE(ctx, pred && target && loss && n > 0 && rb && (diff || dpred_unit), "om_mse_fwd_post: bad arguments");
     return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n, rb);
 }
 

@@ -687,12 +687,13 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     if (pred->shape != target->shape)
         shape_error("Mse: shapes " + shape_str(pred->shape) + " and " + shape_str(target->shape) + " differ.");
     const int64_t n = pred->numel;
-    float *diff = dev().step_floats(n);
     Tensor loss = make({});
     const bool rec = tracked({&pred, &target});
     // the gradient for a unit upstream gradient comes with the forward: the loss is normally the backward's root,
-    // whose seed gradient is exactly that unit
+    // whose seed gradient is exactly that unit. diff is then kept only when the target needs a gradient; another
+    // upstream gradient recomputes it (om_sub, the forward's own subtraction)
     float *unit = rec && pred->requires_grad ? dev().step_floats(n) : nullptr;
+    float *diff = !unit || target->requires_grad ? dev().step_floats(n) : nullptr;
     if (om_readback *rb = dev().take_loss_post()) {
         OMT(om_mse_fwd_post(C(), pred->data, target->data, diff, loss->data, unit, n, rb));
         dev().set_loss_posted(loss->data);
@@ -703,16 +704,22 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     }
     if (rec)
         attach(loss, "Mse", {pred, target}, [diff, unit, n](Engine &e, Record &r, const float *g) {
+            const float *d = diff;
+            if (!d && (g != dev().one() || r.needs(1))) {
+                float *t = dev().step_floats(n);
+                OMT(om_sub(C(), r.inputs[0]->data, r.inputs[1]->data, t, n));
+                d = t;
+            }
             if (unit && g == dev().one()) {
                 e.emit_alias(r, 0, unit);
             } else {
                 int a;
                 float *dp = e.dest(r, 0, &a);
-                if (dp) OMT(om_mse_bwd(C(), g, diff, dp, n, a));
+                if (dp) OMT(om_mse_bwd(C(), g, d, dp, n, a));
             }
             if (r.needs(1)) {  // Sub backward negates the second input's gradient
                 float *t = dev().step_floats(n);
-                OMT(om_mse_bwd(C(), g, diff, t, n, 0));
+                OMT(om_mse_bwd(C(), g, d, t, n, 0));
                 int b;
                 float *dt = e.dest(r, 1, &b);
                 if (b) OMT(om_axpy(C(), -1.0f, t, dt, n));

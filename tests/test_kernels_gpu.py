@@ -289,6 +289,12 @@ def test_mse_and_its_unit_gradient(dev, T):
     ONE, DP = dev.put(np.ones(1, np.float32)), dev.empty(pred.shape)
     dev.call("om_mse_bwd", ONE, D, DP, C.c_int64(n), 0)
     assert np.array_equal(dev.get(UNIT).view(np.uint32), dev.get(DP).view(np.uint32))
+    # without diff (NULL: not written), the same loss and unit gradient; om_sub restates the skipped diff
+    LOSS3, UNIT3, D3 = dev.empty((1,)), dev.empty(pred.shape), dev.empty(pred.shape)
+    dev.call("om_mse_fwd_unit", P, TG, None, LOSS3, UNIT3, C.c_int64(n))
+    assert np.array_equal(dev.get(LOSS3), dev.get(LOSS)) and np.array_equal(dev.get(UNIT3), dev.get(UNIT))
+    dev.call("om_sub", P, TG, D3, C.c_int64(n))
+    assert np.array_equal(dev.get(D3).view(np.uint32), dev.get(D).view(np.uint32))
     tp = OT.Tensor(pred.copy(), True)
     loss = OT.mse(tp, OT.Tensor(tgt.copy()))
     OT.backward(loss)
