@@ -64,13 +64,13 @@ inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->active ? ctx->str
 // becomes the active stream; unfork = back to the main stream; join = the main stream waits for the weight-gradient
 // stream (a no-op when nothing was queued there since the last join).
 om_status fork(om_ctx *ctx);
+void unfork(om_ctx *ctx);
+om_status join(om_ctx *ctx);
 // A readback post written by another entry point's kernel: checks that r belongs to ctx and holds `bytes`, waits for
 // the previous post's copy (the pinned buffer is reused), and returns the device addresses of the buffer and of its
 // sequence word with the sequence number the post carries; readback_posted records the launched post.
 om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq);
 void readback_posted(om_readback *r, uint64_t seq, uint64_t bytes);
-void unfork(om_ctx *ctx);
-om_status join(om_ctx *ctx);
 // out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column; a second
 // (part2, out2) pair of the same shape is reduced in the same launch when given.
 om_status chunk_final(om_ctx *ctx, const double *part, int chunks, int cols, float *out, int acc,

@@ -790,8 +790,15 @@ struct omt_model {
         zero_grad(leaves);
         if (!loss_rb) check(device->ctx(), om_readback_create(device->ctx(), sizeof(float), &loss_rb), "readback");
         device->arm_loss_post(loss_rb);  // a loss op that posts its own value takes it (MSE)
-        Tensor loss = loss_fn(*this);
-        device->take_loss_post();
+        struct Disarm {  // the offer ends with the loss function, also when it throws
+            Device *d;
+            ~Disarm() { d->take_loss_post(); }
+        };
+        Tensor loss;
+        {
+            Disarm disarm{device.get()};
+            loss = loss_fn(*this);
+        }
         if (device->loss_posted() != loss->data)
             check(device->ctx(), om_readback_post(loss_rb, loss->data, sizeof(float)), "loss readback");
         backward(loss);
