@@ -226,6 +226,15 @@ def test_mse_posts_its_loss_from_its_own_launch(pkg):
             assert other.status("om_mse_fwd_post", P, TG, DD, LA, None, C.c_int64(4096), r) != 0
         finally:
             other.ctx.close()
+        # refused: no readback, neither diff nor a unit gradient, an empty input; om_mse_fwd_unit without its unit
+        assert d.status("om_mse_fwd_post", P, TG, DD, LA, None, C.c_int64(4096), None) != 0
+        assert d.status("om_mse_fwd_post", P, TG, None, LA, None, C.c_int64(4096), r) != 0
+        assert d.status("om_mse_fwd_post", P, TG, DD, LA, None, C.c_int64(0), r) != 0
+        assert d.status("om_mse_fwd_unit", P, TG, DD, LA, None, C.c_int64(4096)) != 0
+        # the readback still works after the refusals
+        d.call("om_mse_fwd_post", P, TG, None, LA, DD, C.c_int64(4096), r)
+        assert L.om_readback_wait(r, got.ctypes.data, C.c_uint64(4)) == 0
+        assert got.view(np.uint32)[0] == d.get(LA).view(np.uint32)[0]
     finally:
         L.om_readback_destroy(r)
         d.ctx.close()
