@@ -45,15 +45,6 @@ const char *om_last_error(om_ctx *ctx);
 void *om_ctx_stream(om_ctx *ctx);
 /* Version of this ABI (major * 100 + minor). */
 int om_abi_version(void);
-/* Overlap mode (off by default). When on, om_linear_bwd enqueues its weight and bias gradients on a second stream
- * (default priority) that starts after everything already queued on the context's stream, so they run beside the
- * rest of the backward; their results are complete for the context's stream after om_ctx_join, which om_ctx_sync,
- * om_step_reset, om_upload, om_download, om_copy, om_zero, om_fill, om_adam_step(_scaled), om_sgd_step and
- * om_clip_grad_norm/value perform first.
- * Inputs g and x of such a call must not be overwritten before that join. No counterpart in the reference, whose
- * CPU backward is sequential (Engine.cs:124-207); results do not depend on the mode. */
-om_status om_ctx_set_overlap(om_ctx *ctx, int enable);
-om_status om_ctx_join(om_ctx *ctx);
 
 /* ---------------------------------------------------------------------------------------------- arena */
 /* Device memory in two regions, in the spirit of the reference's buffer lifetimes (ActivationScope.cs:18-106,
@@ -97,7 +88,7 @@ om_status om_stager_release(om_stager *s, int slot);
 /* Readback of a small device value (a step's loss) without waiting for the rest of the stream: om_readback_post
  * queues a copy of `bytes` (at most 64 KiB) from device memory into a pinned host buffer, a one-workgroup kernel on
  * the context's stream writing through the buffer's device mapping and then a sequence number, ordered after the
- * work already queued there (not after the weight-gradient stream); om_readback_wait polls that number, so it blocks
+ * work already queued there; om_readback_wait polls that number, so it blocks
  * only until the copy has landed (and reports a stream error meanwhile), then copies the value to dst. Launches queued between the two keep the device busy while the host
  * returns with the value. No counterpart in the reference's CPU path, where the loss is a host float as soon as the
  * forward has run: its training step reads it there, before Backward and Step (TrainCase.cs:117-127). */
@@ -356,15 +347,19 @@ om_status om_dropout_bwd(om_ctx *ctx, const float *g, float *dx, int64_t n, floa
 
 /* ---------------------------------------------------------------------------------------------- CTC */
 /* Ops.CtcLoss (CtcLoss.cs:40-153) in double with the reference's exp/ln/logadd (Ctc.cs:515-616); reduction
- * 0 = None ([B] losses), 1 = Mean, 2 = Sum (a scalar). Inputs are validated on the host from the host copies of the
- * lengths and targets. `lp` is [T,B,C] on the device; targets/in_len/tgt_len are device copies of the host arrays.
- * om_ctc_bwd = CtcBackward (BackwardRecurrent.cs:253-296): dlp[t,b,c] (+)= -scale * exp(...), g on the device. */
+ * 0 = None ([B] losses), 1 = Mean, 2 = Sum (a scalar). Both entry points validate on the host, from the host copies
+ * of the lengths and targets, everything the kernels index with (input lengths within [0, T], target lengths summing
+ * to n_targets, labels in [0, C) and not the blank, blank in [0, C)) and size their scratch from the host target
+ * lengths. `lp` is [T,B,C] on the device; targets/in_len/tgt_len are device copies that must hold the same values as
+ * the host arrays. om_ctc_bwd = CtcBackward (BackwardRecurrent.cs:253-296): dlp[t,b,c] (+)= -scale * exp(...), g on
+ * the device. */
 om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
                      const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
                      const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
                      int zero_infinity, float *loss);
 om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
-                     const int32_t *tgt_len, const float *g, float *dlp, int max_tgt_len, int T, int B, int C,
+                     const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                     const int32_t *h_targets, int n_targets, const float *g, float *dlp, int T, int B, int C,
                      int blank, int reduction, int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- optimizer */

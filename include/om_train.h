@@ -49,6 +49,16 @@ const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors *
 om_status omt_step(omt_model *m, float *loss);
 /* ZeroGrad, forward and backward only (gradients are left in the arena). */
 om_status omt_forward_backward(omt_model *m, float *loss);
+/* The same two halves as separate calls, for callers that act between them: omt_forward runs ZeroGrad and the
+ * forward, reads the loss and keeps the graph (and the step's staged batch); omt_backward runs loss.Backward() over
+ * it (Tensor.Backward, Engine.cs:21-207). Records are released by the backward, so a second omt_backward on the same
+ * forward fails with OM_E_STATE (Engine.cs:136-141). A tensor the graph saved that was written in place since the
+ * forward (omt_param_write of a value, omt_input_write, omt_optimizer_step, omt_checkpoint_load) makes omt_backward
+ * fail with OMT_E_TENSOR_VERSION before any gradient is written for its record (SavedTensor.Unpack, Autograd.cs:
+ * 222-237). The next omt_forward / omt_step drops the graph. */
+enum { OMT_E_TENSOR_VERSION = 21 /* TensorVersionException (Autograd.cs:188-191) */ };
+om_status omt_forward(omt_model *m, float *loss);
+om_status omt_backward(omt_model *m);
 /* optimizer.Step() alone, on the gradients currently in the arena. */
 om_status omt_optimizer_step(omt_model *m);
 /* The model's om_ctx (its stream orders every launch of the step). */

@@ -31,8 +31,6 @@ _OM_SIGS = {
     "om_last_error": [vp],
     "om_ctx_stream": [vp],
     "om_abi_version": [],
-    "om_ctx_set_overlap": [vp, ci],
-    "om_ctx_join": [vp],
     "om_arena_reserve": [vp, u64, u64],
     "om_alloc": [vp, ci, u64, C.POINTER(vp)],
     "om_step_reset": [vp],
@@ -93,7 +91,7 @@ _OM_SIGS = {
     "om_maxpool_fwd": [vp, vp, vp, vp] + [ci] * 10,
     "om_maxpool_bwd": [vp, vp, vp, vp] + [ci] * 12 + [ci],
     "om_ctc_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, vp],
-    "om_ctc_bwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci],
+    "om_ctc_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci],
     "om_adam_step": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32],
     "om_adam_scalars": [f32, f32, f32, i64, C.POINTER(f32), C.POINTER(f32)],
     "om_adam_step_scaled": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32, vp],
@@ -128,7 +126,11 @@ _HIP = None
 
 
 class OmError(RuntimeError):
-    pass
+    """A failed library call; `code` is its status (OM_E_* / OMT_E_*) when there was one."""
+
+    def __init__(self, message, code=None):
+        super().__init__(message)
+        self.code = code
 
 
 def lib_path(name: str = "libom_hip.so") -> str:
@@ -175,6 +177,8 @@ _OMT_SIGS = {
     "omt_last_error": ([vp], C.c_char_p),
     "omt_step": ([vp, C.POINTER(f32)], i32),
     "omt_forward_backward": ([vp, C.POINTER(f32)], i32),
+    "omt_forward": ([vp, C.POINTER(f32)], i32),
+    "omt_backward": ([vp], i32),
     "omt_optimizer_step": ([vp], i32),
     "omt_ctx": ([vp], vp),
     "omt_param_count": ([vp], ci),
@@ -263,7 +267,7 @@ class Model:
 
     def _check(self, st, what):
         if st != 0:
-            raise OmError(f"{what} failed ({st}): {self.L.omt_last_error(self.h).decode()}")
+            raise OmError(f"{what} failed ({st}): {self.L.omt_last_error(self.h).decode()}", st)
 
     def step(self) -> float:
         v = f32()
@@ -274,6 +278,16 @@ class Model:
         v = f32()
         self._check(self.L.omt_forward_backward(self.h, C.byref(v)), "omt_forward_backward")
         return v.value
+
+    def forward(self) -> float:
+        """ZeroGrad + forward; the graph is kept for backward()."""
+        v = f32()
+        self._check(self.L.omt_forward(self.h, C.byref(v)), "omt_forward")
+        return v.value
+
+    def backward(self):
+        """loss.Backward() over the last forward()'s graph (released afterwards)."""
+        self._check(self.L.omt_backward(self.h), "omt_backward")
 
     def optimizer_step(self):
         self._check(self.L.omt_optimizer_step(self.h), "omt_optimizer_step")
@@ -547,7 +561,7 @@ class Context:
     def call(self, name, *args):
         st = getattr(self.L, name)(self.h, *args)
         if st != 0:
-            raise OmError(f"{name} failed ({st}): {self.L.om_last_error(self.h).decode()}")
+            raise OmError(f"{name} failed ({st}): {self.L.om_last_error(self.h).decode()}", st)
 
     @property
     def stream(self) -> int:

@@ -198,7 +198,6 @@ extern "C" {
 om_status om_clip_grad_norm(om_ctx *ctx, int count, float *const *grads, const int64_t *lens, float max_norm,
                             int infinity_norm, int scale_in_place, float *total, float *coef) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;  // gradients may still be in flight on the weight-gradient stream
     OM_REQUIRE(ctx, max_norm > 0.0f, "om_clip_grad_norm: the maximum norm must be positive (got %g)", (double)max_norm);
     OM_REQUIRE(ctx, scale_in_place || coef, "om_clip_grad_norm: coef is required when scale_in_place is 0");
     std::vector<Segs> segs;
@@ -235,7 +234,6 @@ om_status om_clip_grad_norm(om_ctx *ctx, int count, float *const *grads, const i
 
 om_status om_clip_grad_value(om_ctx *ctx, int count, float *const *grads, const int64_t *lens, float clip_value) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     OM_REQUIRE(ctx, clip_value >= 0.0f, "om_clip_grad_value: the bound must not be negative (got %g)",
                (double)clip_value);
     std::vector<Segs> segs;

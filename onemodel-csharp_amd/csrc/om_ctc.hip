@@ -195,6 +195,36 @@ __global__ void __launch_bounds__(kBlock) k_ctc_bwd(const float *__restrict__ lp
     }
 }
 
+// The host-side checks both entry points run on the host copies of the lengths and labels (CtcLoss.cs:40-153 raises
+// the same conditions); on success *max_ext is the longest extended label sequence, 2 * max(tgt_len) + 1. The
+// kernels index lp, dlp and their scratch with the device copies, which the caller keeps equal to these.
+om_status check_args(om_ctx *ctx, const char *who, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                     const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
+                     int *max_ext) {
+    OM_REQUIRE(ctx, h_in_len && h_tgt_len && (h_targets || n_targets == 0) && n_targets >= 0,
+               "%s: the host lengths and targets are required", who);
+    OM_REQUIRE(ctx, T >= 0 && B > 0 && C > 0, "%s: CtcLoss needs log-probabilities [T,B,C]", who);
+    OM_REQUIRE(ctx, (unsigned)blank < (unsigned)C, "%s: The blank index %d is outside [0, %d).", who, blank, C);
+    OM_REQUIRE(ctx, reduction >= 0 && reduction <= 2, "%s: bad reduction %d", who, reduction);
+    int64_t total = 0;
+    int ext = 1;
+    for (int b = 0; b < B; b++) {
+        OM_REQUIRE(ctx, (unsigned)h_in_len[b] <= (unsigned)T,
+                   "%s: Input length %d of sequence %d is outside [0, %d].", who, h_in_len[b], b, T);
+        OM_REQUIRE(ctx, h_tgt_len[b] >= 0 && h_tgt_len[b] <= (1 << 20),
+                   "%s: Target length %d of sequence %d is negative or too long.", who, h_tgt_len[b], b);
+        total += h_tgt_len[b];
+        ext = 2 * h_tgt_len[b] + 1 > ext ? 2 * h_tgt_len[b] + 1 : ext;
+    }
+    OM_REQUIRE(ctx, total == n_targets, "%s: The target lengths sum to %lld but %d labels were given.", who,
+               (long long)total, n_targets);
+    for (int i = 0; i < n_targets; i++)
+        OM_REQUIRE(ctx, (unsigned)h_targets[i] < (unsigned)C && h_targets[i] != blank,
+                   "%s: Target label %d must be in [0, %d) and differ from the blank %d.", who, h_targets[i], C, blank);
+    *max_ext = ext;
+    return OM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -204,27 +234,11 @@ om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
                      const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
                      int zero_infinity, float *loss) {
     OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && loss && h_in_len && h_tgt_len && (h_targets || n_targets == 0),
-               "om_ctc_fwd: NULL pointer");
-    OM_REQUIRE(ctx, T >= 0 && B > 0 && C > 0, "om_ctc_fwd: CtcLoss needs log-probabilities [T,B,C]");
-    OM_REQUIRE(ctx, (unsigned)blank < (unsigned)C, "om_ctc_fwd: The blank index %d is outside [0, %d).", blank, C);
-    OM_REQUIRE(ctx, reduction >= 0 && reduction <= 2, "om_ctc_fwd: bad reduction %d", reduction);
-    int64_t total = 0;
-    for (int b = 0; b < B; b++) {
-        OM_REQUIRE(ctx, (unsigned)h_in_len[b] <= (unsigned)T,
-                   "om_ctc_fwd: Input length %d of sequence %d is outside [0, %d].", h_in_len[b], b, T);
-        OM_REQUIRE(ctx, h_tgt_len[b] >= 0, "om_ctc_fwd: Target length %d of sequence %d is negative.", h_tgt_len[b], b);
-        total += h_tgt_len[b];
-    }
-    OM_REQUIRE(ctx, total == n_targets, "om_ctc_fwd: The target lengths sum to %lld but %d labels were given.",
-               (long long)total, n_targets);
-    for (int i = 0; i < n_targets; i++)
-        OM_REQUIRE(ctx, (unsigned)h_targets[i] < (unsigned)C && h_targets[i] != blank,
-                   "om_ctc_fwd: Target label %d must be in [0, %d) and differ from the blank %d.", h_targets[i], C,
-                   blank);
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && loss, "om_ctc_fwd: NULL pointer");
     int max_ext = 1;
-    for (int b = 0; b < B; b++) max_ext = 2 * h_tgt_len[b] + 1 > max_ext ? 2 * h_tgt_len[b] + 1 : max_ext;
-    om_status s;
+    om_status s = check_args(ctx, "om_ctc_fwd", h_in_len, h_tgt_len, h_targets, n_targets, T, B, C, blank, reduction,
+                             &max_ext);
+    if (s) return s;
     float *scr;
     uint64_t need = sizeof(double) * ((uint64_t)B * (T > 0 ? T : 1) * max_ext + B);
     s = om::scratch(ctx, need, &scr);
@@ -239,13 +253,15 @@ om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
 }
 
 om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
-                     const int32_t *tgt_len, const float *g, float *dlp, int max_tgt_len, int T, int B, int C,
+                     const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                     const int32_t *h_targets, int n_targets, const float *g, float *dlp, int T, int B, int C,
                      int blank, int reduction, int accumulate) {
     OM_CHECK_CTX(ctx);
-    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && g && dlp && T >= 0 && B > 0 && C > 0 && max_tgt_len >= 0,
-               "om_ctc_bwd: bad arguments");
-    const int max_ext = 2 * max_tgt_len + 1;
-    om_status s;
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && g && dlp, "om_ctc_bwd: NULL pointer");
+    int max_ext = 1;
+    om_status s = check_args(ctx, "om_ctc_bwd", h_in_len, h_tgt_len, h_targets, n_targets, T, B, C, blank, reduction,
+                             &max_ext);
+    if (s) return s;
     float *scr;
     uint64_t tt = T > 0 ? T : 1;
     s = om::scratch(ctx, sizeof(double) * 2ull * B * tt * max_ext, &scr);

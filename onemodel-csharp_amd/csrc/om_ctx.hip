@@ -36,13 +36,9 @@ static om_status grow(om_ctx *ctx, float *&buf, uint64_t &have, uint64_t bytes, 
         *out = buf;
         return OM_OK;
     }
-    // No kernel on either stream may still use the old buffer.
+    // No kernel may still use the old buffer.
     om_status s = check_hip(ctx, hipStreamSynchronize(ctx->stream), "scratch sync");
     if (s) return s;
-    if (ctx->stream2) {
-        s = check_hip(ctx, hipStreamSynchronize(ctx->stream2), "scratch sync");
-        if (s) return s;
-    }
     if (buf) (void)hipFree(buf);
     buf = nullptr;
     have = 0;
@@ -54,27 +50,7 @@ static om_status grow(om_ctx *ctx, float *&buf, uint64_t &have, uint64_t bytes, 
     return OM_OK;
 }
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out) {
-    if (ctx->active) return grow(ctx, ctx->scratch_aux, ctx->scratch_aux_bytes, bytes, out, "scratch alloc");
     return grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out, "scratch alloc");
-}
-om_status fork(om_ctx *ctx) {
-    om_status s = check_hip(ctx, hipEventRecord(ctx->ev_fork, ctx->stream), "fork record");
-    if (s) return s;
-    s = check_hip(ctx, hipStreamWaitEvent(ctx->stream2, ctx->ev_fork, 0), "fork wait");
-    if (s) return s;
-    ctx->active = 1;
-    ctx->aux_pending = true;
-    return OM_OK;
-}
-void unfork(om_ctx *ctx) { ctx->active = 0; }
-om_status join(om_ctx *ctx) {
-    if (!ctx->aux_pending) return OM_OK;
-    om_status s = check_hip(ctx, hipEventRecord(ctx->ev_join, ctx->stream2), "join record");
-    if (s) return s;
-    s = check_hip(ctx, hipStreamWaitEvent(ctx->stream, ctx->ev_join, 0), "join wait");
-    if (s) return s;
-    ctx->aux_pending = false;
-    return OM_OK;
 }
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out) {
     return grow(ctx, ctx->scratch2, ctx->scratch2_bytes, bytes, out, "scratch alloc");
@@ -130,13 +106,8 @@ om_status om_ctx_destroy(om_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     for (auto &r : ctx->region)
         for (auto &s : r.slabs) (void)hipFree(s.base);
-    if (ctx->stream2) (void)hipStreamSynchronize(ctx->stream2);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->scratch2) (void)hipFree(ctx->scratch2);
-    if (ctx->scratch_aux) (void)hipFree(ctx->scratch_aux);
-    if (ctx->ev_fork) (void)hipEventDestroy(ctx->ev_fork);
-    if (ctx->ev_join) (void)hipEventDestroy(ctx->ev_join);
-    if (ctx->stream2) (void)hipStreamDestroy(ctx->stream2);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return OM_OK;
@@ -144,33 +115,7 @@ om_status om_ctx_destroy(om_ctx *ctx) {
 
 om_status om_ctx_sync(om_ctx *ctx) {
     OM_CHECK_CTX(ctx);
-    om_status s = om::join(ctx);
-    if (s) return s;
     return om::check_hip(ctx, hipStreamSynchronize(ctx->stream), "om_ctx_sync");
-}
-
-om_status om_ctx_set_overlap(om_ctx *ctx, int enable) {
-    OM_CHECK_CTX(ctx);
-    if (enable && !ctx->stream2) {
-        // Default priority, like the main stream.
-        om_status s = om::check_hip(ctx, hipStreamCreateWithFlags(&ctx->stream2, hipStreamNonBlocking), "stream2");
-        if (s) return s;
-        s = om::check_hip(ctx, hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming), "fork event");
-        if (s) return s;
-        s = om::check_hip(ctx, hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming), "join event");
-        if (s) return s;
-    }
-    if (!enable) {
-        om_status s = om::join(ctx);
-        if (s) return s;
-    }
-    ctx->overlap = enable != 0;
-    return OM_OK;
-}
-
-om_status om_ctx_join(om_ctx *ctx) {
-    OM_CHECK_CTX(ctx);
-    return om::join(ctx);
 }
 
 const char *om_last_error(om_ctx *ctx) {
@@ -231,8 +176,6 @@ om_status om_alloc(om_ctx *ctx, int region, uint64_t bytes, void **out) {
 
 om_status om_step_reset(om_ctx *ctx) {
     OM_CHECK_CTX(ctx);
-    om_status s = om::join(ctx);  // later launches reuse the memory: nothing on the second stream may still read it
-    if (s) return s;
     om_region &r = ctx->region[OM_REGION_STEP];
     r.cur = 0;
     r.off = 0;
@@ -252,7 +195,6 @@ om_status om_arena_stats(om_ctx *ctx, int region, uint64_t *used, uint64_t *rese
 
 om_status om_upload(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst && src, "om_upload: NULL pointer");
     // Pageable host memory: the copy is staged by the runtime and completes before the call returns.
@@ -261,7 +203,6 @@ om_status om_upload(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
 
 om_status om_download(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst && src, "om_download: NULL pointer");
     om_status s = om::check_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "om_download");
@@ -271,7 +212,6 @@ om_status om_download(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
 
 om_status om_copy(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst && src, "om_copy: NULL pointer");
     return om::check_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "om_copy");
@@ -292,7 +232,6 @@ __global__ void k_zero_bytes(unsigned char *__restrict__ d, int64_t n) {
 
 extern "C" om_status om_fill(om_ctx *ctx, float *dst, float value, int64_t n) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     if (n <= 0) return OM_OK;
     OM_REQUIRE(ctx, dst, "om_fill: NULL pointer");
     hipLaunchKernelGGL(k_fill, dim3(om::grid1d(n, 256, 8192)), dim3(256), 0, ctx->stream, dst, value, n);
@@ -301,7 +240,6 @@ extern "C" om_status om_fill(om_ctx *ctx, float *dst, float value, int64_t n) {
 
 extern "C" om_status om_zero(om_ctx *ctx, void *dst, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst, "om_zero: NULL pointer");
     if ((bytes & 3) == 0 && ((uintptr_t)dst & 3) == 0) return om_fill(ctx, (float *)dst, 0.0f, (int64_t)(bytes >> 2));

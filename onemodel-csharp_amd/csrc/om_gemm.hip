@@ -664,13 +664,6 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd dx");
         if (s) return s;
     }
-    // In overlap mode the weight and bias gradients go to the second stream: nothing downstream in the backward
-    // reads them, so they run beside the input-gradient chain until a join.
-    const bool aux = ctx->overlap && (dw || db);
-    if (aux) {
-        s = om::fork(ctx);
-        if (s) return s;
-    }
     bool db_done = false;
     if (dw) {
         omg::Params p = omg::dense_params(out, in, rows, g, out, x, in, dw, in);
@@ -680,7 +673,6 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = omg::launch_dense(ctx, p, true, false, 1, "om_linear_bwd dw", &db_done);
     }
     if (!s && db && !db_done) s = om_colsum(ctx, g, db, rows, out, acc_db);
-    if (aux) om::unfork(ctx);
     return s;
 }
 
@@ -733,8 +725,6 @@ om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, in
         OM_REQUIRE(ctx, cs[j].part && cs[j].out && cs[j].chunks > 0 && cs[j].cols > 0,
                    "om_param_grads_group: column-sum item %d has a NULL pointer or a non-positive size", j);
     om_status s = OM_OK;
-    // In overlap mode the grouped launches go to the weight-gradient stream, like om_linear_bwd's dW.
-    if (ctx->overlap && (s = om::fork(ctx))) return s;
     const bool grouped = omg::launch_dw_group(ctx, n_dw, dw, rows, n_cs, cs, &s);
     if (!grouped) {
         for (int i = 0; i < n_dw && !s; i++) {
@@ -749,7 +739,6 @@ om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, in
             s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
         }
     }
-    if (ctx->overlap) om::unfork(ctx);
     return s;
 }
 

@@ -36,16 +36,6 @@ struct om_ctx {
     // Second slot for callers that launch GEMMs while holding their own scratch (attention's score recompute).
     float *scratch2 = nullptr;
     uint64_t scratch2_bytes = 0;
-    // Overlap mode (om_ctx_set_overlap): weight-gradient launches go to a second default-priority stream that forks
-    // from the main stream and is joined back before anything reads gradients. `active` routes the GEMM engine's
-    // launches (and its scratch slot) to that stream while a weight gradient is being enqueued.
-    bool overlap = false;
-    hipStream_t stream2 = nullptr;
-    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-    bool aux_pending = false;
-    int active = 0;
-    float *scratch_aux = nullptr;
-    uint64_t scratch_aux_bytes = 0;
     int num_cus = 256;
 };
 
@@ -58,14 +48,8 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
 // The same for the second slot (never used by the GEMM engine itself).
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
-// The stream the GEMM engine launches on right now (the weight-gradient stream while ctx->active).
-inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->active ? ctx->stream2 : ctx->stream; }
-// Overlap mode: fork = the weight-gradient stream waits for everything queued so far on the main stream, and
-// becomes the active stream; unfork = back to the main stream; join = the main stream waits for the weight-gradient
-// stream (a no-op when nothing was queued there since the last join).
-om_status fork(om_ctx *ctx);
-void unfork(om_ctx *ctx);
-om_status join(om_ctx *ctx);
+// The stream every launch of the context goes to.
+inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->stream; }
 // A readback post written by another entry point's kernel: checks that r belongs to ctx and holds `bytes`, waits for
 // the previous post's copy (the pinned buffer is reused), and returns the device addresses of the buffer and of its
 // sequence word with the sequence number the post carries; readback_posted records the launched post.

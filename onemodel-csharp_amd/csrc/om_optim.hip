@@ -111,7 +111,6 @@ static om_status adam_launch(om_ctx *ctx, const char *what, float *p, const floa
                              float weight_decay, int decoupled, float step_size, float sqrt_bc2,
                              const float *grad_scale) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;  // the gradients may still be in flight on the weight-gradient stream
     OM_REQUIRE(ctx, n >= 0, "%s: negative length", what);
     if (n == 0) return OM_OK;
     OM_REQUIRE(ctx, p && g && m && v, "%s: NULL pointer", what);
@@ -154,7 +153,6 @@ om_status om_adam_step_scaled(om_ctx *ctx, float *p, const float *g, float *m, f
 om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t n, float lr, float momentum,
                       float dampening, float weight_decay, int nesterov, int first) {
     OM_CHECK_CTX(ctx);
-    if (om::join(ctx)) return OM_E_DEVICE;  // the gradients may still be in flight on the weight-gradient stream
     OM_REQUIRE(ctx, n >= 0, "om_sgd_step: negative length");
     if (n == 0) return OM_OK;
     OM_REQUIRE(ctx, p && g, "om_sgd_step: NULL pointer");

@@ -143,7 +143,6 @@ om_status om_stager_acquire(om_stager *s, int slot) {
 om_status om_stager_release(om_stager *s, int slot) {
     if (!valid_slot(s, slot)) return OM_E_ARG;
     om_ctx *ctx = s->ctx;
-    if (om::join(ctx)) return OM_E_DEVICE;  // weight-gradient launches on the second stream may read the inputs
     om_status st = om::check_hip(ctx, hipEventRecord(s->consumed[slot], ctx->stream), "om_stager_release");
     if (st) return st;
     s->consume_pending[slot] = 1;

@@ -253,6 +253,9 @@ struct omt_model {
     };
     std::deque<Staged> staged;
     int active_slot = -1;
+    // The loss of the last omt_forward, kept for omt_backward; its records are released by that backward, so a second
+    // omt_backward runs through a released graph (Engine.cs:136-141). Dropped at the next step's start.
+    Tensor graph_loss;
     std::string err;
 
     Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
@@ -394,6 +397,10 @@ struct omt_model {
     // SGD (class Sgd): runs are split where the momentum buffers' started state changes.
     void optimizer_step(const float *grad_scale = nullptr) {
         settle_grads(leaves);
+        // the update writes the parameters in place (Tensor.MutableData in Optimizer.Step): a graph that saved one
+        // of them can no longer run backward
+        for (auto &p : params)
+            if (p.second->grad_exists && p.second->requires_grad) touch(p.second);
         if (schedule) lr = schedule->lr_at(step_count);
         if (!std::isfinite(lr) || lr < 0.0f) throw Error(OM_E_ARG, "learning rate must be finite and not negative");
         om_ctx *c = device->ctx();
@@ -571,27 +578,77 @@ struct omt_model {
         }
         active_slot = st.slot;
     }
-    // After the step's last launch: the slot's device copy is released and the inputs point home again.
+    // After the step's last launch: the slot's device copy is released and the inputs point home again. The inputs
+    // point home even when the release fails.
     void return_batch() {
         if (active_slot < 0) return;
-        check(device->ctx(), om_stager_release(stager, active_slot), "om_stager_release");
+        const int slot = active_slot;
         active_slot = -1;
         for (Input &in : inputs) {
             if (in.is_int) in.t->idata = in.home_idata;
             else in.t->data = in.home_data;
         }
+        check(device->ctx(), om_stager_release(stager, slot), "om_stager_release");
+    }
+    // Returns the step's batch when the scope ends, also when the step throws (a failed step must not keep its
+    // staging slot, or the ring runs dry after a few failures). keep() hands the batch on to a later backward.
+    struct BatchScope {
+        omt_model *m;
+        bool armed = true;
+        ~BatchScope() {
+            if (!armed) return;
+            try {
+                m->return_batch();
+            } catch (...) {  // the step's own error is the one reported
+            }
+        }
+        void keep() { armed = false; }
+        void done() {  // returns the batch now, reporting a failure
+            armed = false;
+            m->return_batch();
+        }
+    };
+    // The start of every step: a batch still held by an omt_forward that no backward followed is returned, the
+    // previous graph is dropped, step memory is rewound (ActivationScope.Dispose), the next batch is taken and the
+    // gradients are zeroed (Optimizer.ZeroGrad).
+    void begin_step() {
+        graph_loss.reset();
+        return_batch();
+        device->step_reset();
+        take_batch();
     }
 
     float forward_backward() {
-        device->step_reset();
-        take_batch();
+        begin_step();
+        BatchScope batch{this};
         zero_grad(leaves);
         Tensor loss = loss_fn(*this);
         backward(loss);
-        return_batch();
+        batch.done();
         float v = 0.0f;
         check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
         return v;
+    }
+    // ZeroGrad and the forward alone; the graph and the batch are kept for backward_pass().
+    float forward() {
+        begin_step();
+        BatchScope batch{this};
+        zero_grad(leaves);
+        Tensor loss = loss_fn(*this);
+        float v = 0.0f;
+        check(device->ctx(), om_download(device->ctx(), &v, loss->data, sizeof(float)), "loss readback");
+        graph_loss = loss;
+        batch.keep();
+        return v;
+    }
+    // loss.Backward() of the last forward(). Its records are released afterwards, so a second call fails as the
+    // reference's second Backward does; a saved tensor written in place since the forward fails with
+    // TensorVersionException's code. The batch goes back either way.
+    void backward_pass() {
+        if (!graph_loss) throw Error(OM_E_STATE, "omt_backward: no forward pass to run backward through");
+        BatchScope batch{this};
+        backward(graph_loss);
+        batch.done();
     }
     // ---------------------------------------------------------------------------------------------- checkpoints
     // The model's StateDict as checkpoint tensors (names, types, shapes), and the optimizer's kind, hyper-parameters
@@ -745,6 +802,7 @@ struct omt_model {
             }
         }
         check(c, om_upload(c, pb, ph.data(), sizeof(float) * ph.size()), "upload");
+        for (auto &p : params) touch(p.second);
         if (with_opt) {
             const size_t P = params.size();
             std::vector<float> mh(ph.size(), 0.0f), vh(ph.size(), 0.0f), xh;
@@ -785,8 +843,8 @@ struct omt_model {
     // backward and the update, so those still run while the caller gets the value and queues the next step. Later
     // work on the context's stream is ordered after them.
     float step() {
-        device->step_reset();
-        take_batch();
+        begin_step();
+        BatchScope batch{this};
         zero_grad(leaves);
         if (!loss_rb) check(device->ctx(), om_readback_create(device->ctx(), sizeof(float), &loss_rb), "readback");
         device->arm_loss_post(loss_rb);  // a loss op that posts its own value takes it (MSE)
@@ -802,7 +860,7 @@ struct omt_model {
         if (device->loss_posted() != loss->data)
             check(device->ctx(), om_readback_post(loss_rb, loss->data, sizeof(float)), "loss readback");
         backward(loss);
-        return_batch();
+        batch.done();
         if (clip_max > 0.0f) {
             // Adam/AdamW read the coefficient in their update; SGD gets the gradients scaled in place
             const bool fold = opt_kind != OPT_SGD;
@@ -1179,6 +1237,20 @@ om_status omt_forward_backward(omt_model *m, float *loss) {
         if (loss) *loss = v;
     });
 }
+om_status omt_forward(omt_model *m, float *loss) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        float v = m->forward();
+        if (loss) *loss = v;
+    });
+}
+om_status omt_backward(omt_model *m) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        m->backward_pass();
+        settle_grads(m->leaves);
+    });
+}
 om_status omt_optimizer_step(omt_model *m) {
     if (!m) return OM_E_ARG;
     return guard(m, [&] {
@@ -1219,6 +1291,7 @@ om_status omt_param_write(omt_model *m, int i, int which, const float *host, int
         if (numel != m->params[i].second->numel) throw Error(OM_E_ARG, "omt_param_write: wrong element count");
         check(m->device->ctx(), om_upload(m->device->ctx(), param_block(m, which) + m->offset[i], host,
                                           sizeof(float) * (uint64_t)numel), "upload");
+        if (which == 0) touch(m->params[i].second);
         m->device->sync();
     });
 }
@@ -1372,6 +1445,7 @@ om_status omt_input_write(omt_model *m, int i, const void *host, int64_t numel) 
             check(m->device->ctx(), om_upload(m->device->ctx(), in.t->data, host, sizeof(float) * (uint64_t)numel),
                   "upload");
         }
+        touch(in.t);
     });
 }
 om_status omt_input_grad(omt_model *m, int i, float *host, int64_t numel) {

@@ -27,12 +27,6 @@ Device::Device(int device) {
     om_status s = om_ctx_create(device, &ctx_);
     if (s != OM_OK) throw Error(s, std::string("om_ctx_create: ") + om_last_error(nullptr));
     check(ctx_, om_arena_reserve(ctx_, 0, 1ull << 30), "om_arena_reserve");
-    // OMT_OVERLAP=1 puts weight gradients on a second stream beside the input-gradient chain (joined by the
-    // optimizer, downloads and the step reset). Off by default: measured on MI355X at the C3 shapes, the two
-    // streams' GEMMs split the CUs between them and the input-gradient chain (the critical path) finishes later.
-    const char *ov = std::getenv("OMT_OVERLAP");
-    overlap_ = ov && ov[0] == '1';
-    check(ctx_, om_ctx_set_overlap(ctx_, overlap_ ? 1 : 0), "om_ctx_set_overlap");
 }
 Device::~Device() {
     if (ctx_) om_ctx_destroy(ctx_);
@@ -94,6 +88,13 @@ static std::string shape_str(const std::vector<int> &s) {
 [[noreturn]] static void shape_error(const std::string &m) { throw Error(OM_E_ARG, m); }
 
 // ------------------------------------------------------------------------------------------------ engine
+void Record::unpack_check() const {
+    for (const auto &s : saved)
+        if (*s.first != s.second)
+            throw Error(kErrTensorVersion, "A tensor saved for the backward pass was modified in place (saved at version " +
+                                               std::to_string(s.second) + ", now " + std::to_string(*s.first) + ").");
+}
+
 void Engine::queue_dw(const om_linear_dw &item, int rows) {
     if (!item.dw && !item.db) return;
     if (!dw_queue_.empty() && (rows != dw_rows_ || dw_queue_.size() == 4)) flush_dw();
@@ -132,13 +133,10 @@ float *Engine::dest(Record &r, int i, int *acc) {
     if (i >= (int)r.inputs.size() || !r.needs(i)) return nullptr;
     TensorImpl &x = *r.inputs[i];
     if (x.is_leaf()) {
-        // AccumulateLeaf (Engine.cs:292-328): the first gradient creates Grad, later ones add into it. A gradient
-        // added into must be complete on the main stream: in overlap mode its earlier part may come from a launch
-        // on the second stream.
+        // AccumulateLeaf (Engine.cs:292-328): the first gradient creates Grad, later ones add into it.
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
         if (queued_leaf(x.grad)) flush_dw();  // a queued launch writes this gradient first
         *acc = x.grad_live ? 1 : 0;
-        if (x.grad_live) OMT(om_ctx_join(C()));
         x.grad_live = x.grad_exists = true;
         return x.grad;
     }
@@ -192,7 +190,6 @@ void Engine::emit_alias(Record &r, int i, const float *g) {
         if (!x.grad) throw Error(OM_E_STATE, "leaf " + x.name + " requires a gradient but has no gradient buffer");
         if (queued_leaf(x.grad)) flush_dw();  // a queued launch writes this gradient first
         if (x.grad_live) {
-            OMT(om_ctx_join(C()));
             OMT(om_axpy(C(), 1.0f, g, x.grad, x.numel));
         } else {
             OMT(om_copy(C(), x.grad, g, bytes));
@@ -239,6 +236,9 @@ void Engine::run(const Tensor &root) {
     while (!stack.empty()) {
         Record *rec = stack.back().first;
         size_t next = stack.back().second;
+        if (rec->released)
+            throw Error(OM_E_STATE,
+                        "Backward ran through a graph whose saved tensors were already freed by an earlier backward.");
         if (next < rec->inputs.size()) {
             stack.back().second = next + 1;
             const Tensor &x = rec->inputs[next];
@@ -260,7 +260,7 @@ void Engine::run(const Tensor &root) {
         float *gi = r->pending;
         r->pending = nullptr;
         if (!gi) continue;
-        if (!r->rule) throw Error(OM_E_STATE, std::string("backward ran through a released ") + r->op + " record");
+        r->unpack_check();  // SavedTensor.Unpack's version check, before the rule reads anything
         r->rule(*this, *r, gi);
         holders_[gi]--;  // this record is done with its gradient
     }
@@ -270,6 +270,8 @@ void Engine::run(const Tensor &root) {
     for (Record *r : order) {
         r->rule = nullptr;
         r->inputs.clear();
+        r->saved.clear();
+        r->released = true;
     }
 }
 
@@ -298,13 +300,17 @@ static bool tracked(std::initializer_list<const Tensor *> xs) {
         if (*x && (*x)->requires_grad) return true;
     return false;
 }
+// Records `op` on `out`. `saved` lists the tensors the rule reads (the reference's rec.Save slots); the output
+// itself may be among them (Relu and LogSoftmax save their result).
 static void attach(const Tensor &out, const char *op, std::vector<Tensor> inputs,
-                   std::function<void(Engine &, Record &, const float *)> rule) {
+                   std::function<void(Engine &, Record &, const float *)> rule,
+                   std::initializer_list<Tensor> saved = {}) {
     auto r = std::make_shared<Record>();
     r->op = op;
     r->inputs = std::move(inputs);
     r->rule = std::move(rule);
     r->out_numel = out->numel;
+    for (const Tensor &t : saved) r->save(t);
     out->requires_grad = true;
     out->grad_fn = r;
 }
@@ -329,7 +335,7 @@ Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
             float *dw = e.dest(r, 1, &aw);
             float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
             e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
-        });
+        }, {x, w});
     }
     return y;
 }
@@ -344,7 +350,7 @@ Tensor relu(const Tensor &x) {
             int a;
             float *dx = e.dest(r, 0, &a);
             OMT(om_relu_bwd(C(), g, yd, dx, n, a));
-        });
+        }, {y});
     }
     return y;
 }
@@ -358,7 +364,7 @@ Tensor gelu(const Tensor &x) {
             int a;
             float *dx = e.dest(r, 0, &a);
             OMT(om_gelu_bwd(C(), g, r.inputs[0]->data, dx, n, a));
-        });
+        }, {x});
     }
     return y;
 }
@@ -403,7 +409,7 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
                                           pb, rows, cols));
             if (dg) e.queue_colsum(om_column_sum{pg, dg, chunks, cols, ag});
             if (db) e.queue_colsum(om_column_sum{pb, db, chunks, cols, ab});
-        });
+        }, {x, gamma});
     return y;
 }
 
@@ -439,7 +445,7 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
                     if (a[i]) OMT(om_axpy(C(), 1.0f, tmp[i], d[i], r.inputs[i]->numel));
                     else OMT(om_copy(C(), d[i], tmp[i], sizeof(float) * (uint64_t)r.inputs[i]->numel));
                 }
-        });
+        }, {q, k, v, mask});
     return o;
 }
 
@@ -463,7 +469,7 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
             float *db = r.inputs[2] ? e.dest(r, 2, &ab) : nullptr;
             e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
             if (r.needs(3)) e.emit_alias(r, 3, g);  // Add backward: the residual gets g unchanged
-        });
+        }, {x, w});
     }
     return y;
 }
@@ -511,7 +517,7 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
             }
             for (int i = 0; i < n; i++) e.queue_dw(items[i], rows);
             if (r.needs(5)) e.emit_alias(r, 5, g);
-        });
+        }, {x, w1, w2});
     }
     return y;
 }
@@ -579,7 +585,7 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
                        if (a[i]) OMT(om_axpy(C(), 1.0f, src, d[i], n));
                        else OMT(om_copy(C(), d[i], src, sizeof(float) * (uint64_t)n));
                    }
-               });
+               }, {x, wq, wk, wv, mask});
     return o;
 }
 
@@ -596,8 +602,9 @@ Tensor reshape(const Tensor &x, const std::vector<int> &shape) {
     auto y = std::make_shared<TensorImpl>();
     y->shape = s;
     y->numel = x->numel;
-    y->data = x->data;  // a view: same memory
+    y->data = x->data;  // a view: same memory, same version counter
     y->idata = x->idata;
+    y->version = x->version;
     if (tracked({&x})) attach(y, "Reshape", {x}, [](Engine &e, Record &r, const float *g) { e.emit_alias(r, 0, g); });
     return y;
 }
@@ -657,7 +664,7 @@ Tensor log_softmax(const Tensor &x) {
             int a;
             float *dx = e.dest(r, 0, &a);
             OMT(om_logsoftmax_bwd(C(), g, yd, dx, rows, cols, a));
-        });
+        }, {y});
     }
     return y;
 }
@@ -678,7 +685,7 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels) {
             int a;
             float *dz = e.dest(r, 0, &a);
             OMT(om_xent_bwd(C(), g, lp, tg, dz, rows, cols, 1, -100, a));
-        });
+        }, {labels});
     }
     return loss;
 }
@@ -753,7 +760,7 @@ Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int
             }
             OMT(om_conv2d_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, N, Cin, H, W, Cout, KH, KW,
                               stride, pad, ax, dw ? aw : ab));
-        });
+        }, {x, w});
     }
     return y;
 }
@@ -791,13 +798,12 @@ Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std
     OMT(om_ctc_fwd(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(), (int)targets.size(), T,
                    B, Cc, blank, reduction, 0, loss->data));
     if (tracked({&lp})) {
-        int maxl = 0;
-        for (int32_t l : tgt_len) maxl = l > maxl ? l : maxl;
         attach(loss, "CtcLoss", {lp}, [=](Engine &e, Record &r, const float *g) {
             int a;
             float *d = e.dest(r, 0, &a);
-            OMT(om_ctc_bwd(C(), r.inputs[0]->data, dt, dil, dtl, g, d, maxl, T, B, Cc, blank, reduction, a));
-        });
+            OMT(om_ctc_bwd(C(), r.inputs[0]->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
+                           (int)targets.size(), g, d, T, B, Cc, blank, reduction, a));
+        }, {lp});
     }
     return loss;
 }
@@ -840,7 +846,7 @@ Tensor batch_norm2d(const Tensor &x, const Tensor &gamma, const Tensor &beta, fl
                 OMT(om_batchnorm2d_bwd(C(), g, xd, gd, mean, inv, dx, dg, nullptr, N, Cc, plane, tr, ax, ag));
                 OMT(om_batchnorm2d_bwd(C(), g, xd, gd, mean, inv, nullptr, nullptr, db, N, Cc, plane, tr, 0, ab));
             }
-        });
+        }, {x, gamma});
     return y;
 }
 
@@ -859,7 +865,7 @@ Tensor embedding(const Tensor &table, const Tensor &ids, int padding_index) {
             int a;
             float *dt = e.dest(r, 0, &a);
             OMT(om_embedding_bwd(C(), g, id, dt, n, dim, rows, padding_index, a));
-        });
+        }, {ids});
     }
     return y;
 }

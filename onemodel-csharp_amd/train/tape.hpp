@@ -45,8 +45,18 @@ struct TensorImpl {
     bool grad_exists = false;
     bool grad_live = false;
     std::string name;
+    // The storage's version counter (Tensor.Version, Tensor.cs:190-191; TensorBuffer.Version): views share it, and
+    // every in-place write to the storage raises it (touch), so a record that saved the tensor notices.
+    std::shared_ptr<int64_t> version = std::make_shared<int64_t>(0);
     bool is_leaf() const { return !grad_fn; }
 };
+// An in-place write to t's storage (Tensor.MutableData, Tensor.cs:292-309): raises its version.
+inline void touch(const Tensor &t) {
+    if (t) ++*t->version;
+}
+// The tape's error code for TensorVersionException (Autograd.cs:188-191): a tensor saved for the backward pass was
+// modified in place. The om_train.h ABI reports it as OMT_E_TENSOR_VERSION.
+constexpr int kErrTensorVersion = 21;
 
 class Engine;
 // A backward record (BackwardRecord.cs:17-150): inputs in order and the rule that turns the output gradient into
@@ -60,6 +70,15 @@ struct Record {
     bool pending_borrowed = false;  // aliases another gradient; copy before writing into it
     int64_t out_numel = 0;
     uint64_t mark = 0;
+    // Set when a backward pass has run through the record and freed what it saved (BackwardRecord.Release).
+    bool released = false;
+    // The tensors the rule reads, each with its storage version at the time it was saved (SavedTensor,
+    // Autograd.cs:197-237); unpack_check() fails if any was written in place since.
+    std::vector<std::pair<std::shared_ptr<int64_t>, int64_t>> saved;
+    void save(const Tensor &t) {
+        if (t) saved.emplace_back(t->version, *t->version);
+    }
+    void unpack_check() const;
     bool needs(int i) const { return inputs[i] && inputs[i]->requires_grad; }
 };
 
@@ -76,7 +95,6 @@ class Device {
     const float *one();
     void step_reset();
     void sync();
-    bool overlap() const { return overlap_; }
     // Loss readback folded into the loss's own launch: arm_loss_post(rb) offers rb to the next loss op that can post
     // its value itself (MSE); that op takes it (take_loss_post) and reports what it posted (loss_posted), so the
     // step posts the loss separately only when the offer was not taken for that very tensor.
@@ -94,7 +112,6 @@ class Device {
 
    private:
     om_ctx *ctx_ = nullptr;
-    bool overlap_ = false;
     float *one_ = nullptr;
     om_readback *loss_rb_ = nullptr;
     const float *loss_posted_ = nullptr;
@@ -148,10 +165,7 @@ class Engine {
     // running counts as a holder of its own gradient until its rule returns). A borrowed buffer whose only holder
     // is the record about to write into it is written in place instead of being copied first.
     std::unordered_map<const float *, int> holders_;
-    // In overlap mode a gradient buffer may still be read by a weight-gradient launch on the second stream, so
-    // it is never written in place once borrowed.
     bool sole_holder(const float *b) const {
-        if (dev().overlap()) return false;
         auto it = holders_.find(b);
         return it != holders_.end() && it->second == 1;
     }

@@ -8,7 +8,9 @@ bias, are checked as noise as the reference's own tests do, AutogradModelTests.c
 the device's gradients must equal the oracle's update of the same gradients bit for bit; and after the step every
 parameter must agree to 1e-5 scaled on the elements whose gradient sign the two computations agree on — a gradient
 that rounding noise can flip gets a +-lr Adam step either way (TrainingCurveTests.cs:49-66 reports those separately).
-Sizes are scaled down where the CPU oracle would take minutes; C3, the benchmark's workload, runs at full size.
+Every configuration runs at its full benchmark size (C2 batch 32, C4 batch 32, C5 batch 8 with its four layers), so
+the tile, split-K and reduction choices only full sizes take are checked against the oracle; reduced sizes are kept
+as extra cases of the smaller shapes' paths.
 """
 import numpy as np
 import pytest
@@ -20,10 +22,13 @@ pytestmark = pytest.mark.gpu
 CASES = [
     (1, {}),
     (2, {"batch": 4}),
+    (2, {}),
     (3, {"batch": 4}),
     (3, {}),
     (4, {"batch": 8}),
+    (4, {}),
     (5, {"batch": 1, "layers": 2}),
+    (5, {}),
     (10, {}),  # a weight used twice: its queued gradient is launched before the second use adds into it
 ]
 

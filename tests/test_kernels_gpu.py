@@ -54,7 +54,10 @@ def test_mfma_fragment_layout(dev):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("m,n,k", [(64, 64, 64), (37, 53, 29), (256, 384, 384), (5, 300, 1000), (384, 384, 4096),
-                                   (130, 10, 257)])
+                                   (130, 10, 257),
+                                   # C5's products: the FFN pair and the 768-wide projections over 4096 tokens, and
+                                   # the weight-gradient shapes with K = 4096 (the tuned table's C5 rows)
+                                   (4096, 3072, 768), (4096, 768, 3072), (4096, 768, 768), (3072, 768, 4096)])
 def test_gemm_parity(dev, T, ta, tb, m, n, k):
     rng = np.random.default_rng(m * 1000 + n + k)
     A = rnd(rng, *((k, m) if ta else (m, k)))
@@ -103,7 +106,10 @@ def test_gemm_rejects_bad_shapes(dev):
 
 # ------------------------------------------------------------------------------------------------ Linear
 @pytest.mark.parametrize("rows,inf,outf", [(64, 784, 256), (64, 256, 10), (4096, 384, 1536), (300, 37, 9),
-                                           (512, 256, 128), (4096, 1536, 384), (4096, 384, 1152)])
+                                           (512, 256, 128), (4096, 1536, 384), (4096, 384, 1152),
+                                           # C5 at full size: FFN pair, attention output, packed q|k|v, token head
+                                           (4096, 768, 3072), (4096, 3072, 768), (4096, 768, 768), (4096, 768, 2304),
+                                           (4096, 768, 9)])
 def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     rng = np.random.default_rng(rows + inf + outf)
     x, w, b, g = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf), rnd(rng, rows, outf)
@@ -130,7 +136,9 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     (4096, [(384, 384), (384, 1152), (384, 384)]),     # attention-shaped: three products, 64 x 96 tiles
     (512, [(64, 192), (128, 64)]),                     # 64 x 64 tiles, few splits
     (100, [(20, 36), (36, 20)]),                       # ragged: item by item through om_linear_bwd
-], ids=["ffn-pair", "attention-triple", "small-64", "ragged"])
+    (4096, [(768, 3072), (3072, 768), (768, 768), (768, 2304)]),  # C5's four weight gradients of one layer
+    (4096, [(768, 768)]),                              # C5's attention output alone
+], ids=["ffn-pair", "attention-triple", "small-64", "ragged", "c5-layer", "c5-single"])
 def test_linear_dw_group(dev, T, rows, shapes):
     """om_linear_bwd_dw_group: every item's dW and db to the GEMM tolerance against the oracle (the last item of
     each group without a bias gradient), then a second call accumulating into the same leaves."""
@@ -167,7 +175,8 @@ def test_linear_dw_group(dev, T, rows, shapes):
             assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
 
 
-@pytest.mark.parametrize("rows,inf,outf", [(4096, 384, 1536), (4096, 1536, 384), (256, 64, 192), (100, 36, 20)])
+@pytest.mark.parametrize("rows,inf,outf", [(4096, 384, 1536), (4096, 1536, 384), (256, 64, 192), (100, 36, 20),
+                                           (4096, 768, 3072), (4096, 3072, 768), (4096, 768, 768)])
 def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     """om_linear_fwd_resid (Linear then the residual Add), om_linear_gelu_fwd (Linear then GELU, keeping the
     pre-activation) and om_linear_bwd_dx_gelu (GELU's backward of g w): the GEMM part to the GEMM tolerance, the
@@ -200,11 +209,19 @@ def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     G, HI, DH, DA = dev.put(g), dev.put(hin), dev.empty((rows, inf)), dev.empty((rows, inf))
     dev.call("om_linear_bwd_dx_gelu", G, W, HI, DH, rows, inf, outf)
     assert scaled(dev.get(DH), dh_ref) <= TOL
-    dev.call("om_linear_bwd", G, X, W, DA, None, None, rows, inf, outf, 0, 0, 0)
+    # GeluGradBin applied to the epilogue kernel's own product: om_linear_bwd_dx_slope with a unit slope yields that
+    # product exactly (x * 1 = x) from the tile every epilogue launch of this shape takes. A plain om_linear_bwd may
+    # take a tile that carries no epilogue (the eight-wavefront 128 x 128 one at 4096 x 3072 x 768), whose partial
+    # sums combine in another order, so it is held to the GEMM tolerance only.
+    ONES = dev.put(np.ones((rows, inf), np.float32))
+    dev.call("om_linear_bwd_dx_slope", G, W, ONES, DA, rows, inf, outf)
     da_dev = dev.get(DA)
+    assert scaled(da_dev, da) <= TOL
     dh_exact = np.empty_like(da_dev)
     T.lib().or_gelu_bwd(T.fp(da_dev), T.fp(hin), T.fp(dh_exact), C.c_int64(da_dev.size))
     assert np.array_equal(dev.get(DH).view(np.uint32), dh_exact.view(np.uint32))
+    dev.call("om_linear_bwd", G, X, W, DA, None, None, rows, inf, outf, 0, 0, 0)
+    assert scaled(dev.get(DA), da) <= TOL
     # The slope pair: the forward's a equals om_linear_gelu_fwd's, its s is GELU's slope at h (GeluGradBin with a unit
     # gradient), and the backward from a saved slope equals om_linear_bwd_dx_gelu bit for bit.
     A2, S = dev.empty((rows, outf)), dev.empty((rows, outf))
@@ -541,7 +558,12 @@ def test_attention_bwd_kernels_agree(dev, L, masked):
 # ------------------------------------------------------------------------------------------------ conv and pool
 @pytest.mark.parametrize("N,Cin,H,W,Cout,K,S,P", [(2, 64, 14, 14, 64, 3, 1, 1), (2, 1, 32, 128, 32, 3, 1, 1),
                                                   (3, 32, 16, 64, 64, 3, 1, 1), (2, 5, 9, 11, 7, 3, 2, 1),
-                                                  (1, 128, 4, 32, 256, 3, 1, 1)])
+                                                  (1, 128, 4, 32, 256, 3, 1, 1),
+                                                  # C2 at full size: dW reduces over 32 images x 3136 pixels
+                                                  (32, 64, 56, 56, 64, 3, 1, 1),
+                                                  # C4's four stages at full batch
+                                                  (32, 1, 32, 128, 32, 3, 1, 1), (32, 32, 16, 64, 64, 3, 1, 1),
+                                                  (32, 64, 8, 32, 128, 3, 1, 1), (32, 128, 4, 32, 256, 3, 1, 1)])
 def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     rng = np.random.default_rng(N * Cin + Cout)
     x, w, b = rnd(rng, N, Cin, H, W), rnd(rng, Cout, Cin, K, K, scale=0.2), rnd(rng, Cout)
@@ -615,7 +637,7 @@ def test_ctc_bit_exact(dev, T, red):
             dev.put(gin), dev.empty(lp.shape, fill=123.0)
         hil, htl, htg = (a.ctypes.data_as(C.c_void_p) for a in (il, tl, tg))
         dev.call("om_ctc_fwd", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L)
-        dev.call("om_ctc_bwd", LP, TG, IL, TL, GIN, D, int(tl.max()), Tn, B, Cc, 0, red, 0)
+        dev.call("om_ctc_bwd", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D, Tn, B, Cc, 0, red, 0)
         got = dev.get(L)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
         assert np.array_equal(dev.get(D).view(np.uint32), dref.view(np.uint32)), name
@@ -628,6 +650,41 @@ def test_ctc_rejects_bad_targets(dev):
     st = dev.status("om_ctc_fwd", lp, dev.put(tg), dev.put(il), dev.put(tl), il.ctypes.data_as(C.c_void_p),
                     tl.ctypes.data_as(C.c_void_p), tg.ctypes.data_as(C.c_void_p), 1, 3, 1, 4, 0, 1, 0, lp)
     assert st == 1 and b"differ from the blank" in dev.ctx.L.om_last_error(dev.ctx.h)
+
+
+def test_ctc_bwd_rejects_what_it_would_index_with(dev):
+    """om_ctc_bwd checks the host copies of the lengths and labels before it launches anything: an input length past
+    T, target lengths that do not sum to the labels given, a label outside [0, C) or equal to the blank, and a blank
+    outside [0, C) are refused with OM_E_ARG (each would make the kernel read lp or write dlp and its scratch out of
+    bounds), and dlp is left untouched."""
+    Tn, B, Cc = 4, 2, 5
+    lp = dev.empty((Tn, B, Cc), fill=-1.0)
+    g = dev.put(np.ones(1, np.float32))
+    dlp = dev.empty((Tn, B, Cc), fill=7.0)
+
+    def call(il, tl, tg, blank=0):
+        il, tl, tg = (np.asarray(a, np.int32) for a in (il, tl, tg))
+        st = dev.status("om_ctc_bwd", lp, dev.put(tg if tg.size else np.zeros(1, np.int32)), dev.put(il),
+                        dev.put(tl), il.ctypes.data_as(C.c_void_p), tl.ctypes.data_as(C.c_void_p),
+                        tg.ctypes.data_as(C.c_void_p), int(tg.size), g, dlp, Tn, B, Cc, blank, 1, 0)
+        return st, dev.ctx.L.om_last_error(dev.ctx.h)
+
+    cases = [
+        (([5, 4], [1, 1], [1, 2]), b"Input length 5"),             # past T
+        (([4, 4], [2, 1], [1, 2]), b"sum to 3 but 2 labels"),      # more labels claimed than given
+        (([4, 4], [1, 1], [1, 5]), b"Target label 5"),             # label == C
+        (([4, 4], [1, 1], [0, 2]), b"differ from the blank"),      # the blank as a label
+        (([4, -1], [1, 1], [1, 2]), b"Input length -1"),           # negative input length
+        (([4, 4], [1, -1], [1]), b"Target length -1"),             # negative target length
+    ]
+    for args, msg in cases:
+        st, err = call(*args)
+        assert st == 1 and msg in err, (args, st, err)
+    st, err = call([4, 4], [1, 1], [1, 2], blank=5)
+    assert st == 1 and b"blank index 5" in err
+    assert np.all(dev.get(dlp) == 7.0)
+    st, _ = call([4, 4], [1, 1], [1, 2])  # the same call with valid arguments runs
+    assert st == 0
 
 
 # ------------------------------------------------------------------------------------------------ optimizers
