@@ -340,6 +340,22 @@ def mean_axis(x: Tensor, axis: int) -> Tensor:
     return _attach(y, [x], rule)
 
 
+def softmax(x: Tensor) -> Tensor:
+    """Ops.Softmax over the last axis (Ops.Layers.cs:17-39; Softmax.Rows, Softmax.cs:27-133), backward
+    BackwardNn.cs:26-52 (dx = y * (g - (float) fp64 sum of g*y), the record saving the output)."""
+    xv = c32(x.data)
+    cols = xv.shape[-1]
+    rows = xv.size // cols
+    y = np.empty_like(xv)
+    lib().or_softmax_rows(fp(xv), fp(y), rows, cols)
+
+    def rule(g):
+        dx = np.empty_like(xv)
+        lib().or_softmax_bwd(fp(c32(g)), fp(y), fp(dx), rows, cols)
+        return [dx]
+    return _attach(y, [x], rule)
+
+
 def log_softmax(x: Tensor) -> Tensor:
     """Ops.LogSoftmax over the last axis (Ops.Layers.cs:47-96), backward BackwardNn.cs:54-80."""
     xv = c32(x.data)

@@ -331,6 +331,51 @@ def test_fd_layernorm_gelu_linear(oracle):
     gradcheck(T, lambda t: T.gelu(T.linear(T.layer_norm(t[0], t[3], t[4]), t[1], t[2])), [x, w, b, gm, bt])
 
 
+def test_fd_softmax(oracle):
+    """The standalone softmax backward (or_softmax_bwd, BackwardNn.cs:26-52) against central differences, on rows
+    of moderate and of wide-ranging logits."""
+    T = oracle
+    rng = np.random.default_rng(12)
+    gradcheck(T, lambda t: T.softmax(t[0]), [rng.standard_normal((4, 7)).astype(np.float32)])
+    gradcheck(T, lambda t: T.softmax(t[0]), [(3 * rng.standard_normal((2, 3, 5))).astype(np.float32)], seed=3)
+
+
+def test_softmax_backward_closed_forms(oracle):
+    """What the mathematics fixes for dx = J^T g with J = diag(y) - y y^T, each failing a plausible slip:
+    - a one-hot row (y = e_k exactly) has J = 0, so dx = 0 whatever g is (a dropped factor y, or g*(y - dot) with
+      the operands swapped, leaves g_k or g_k (1 - g_k) there);
+    - a uniform row (y = 1/n) gives dx = (g - mean(g)) / n (a wrong sign or a missing 1/n fails);
+    - every row of dx sums to zero, since sum_j y_j (g_j - y.g) = y.g (1 - sum_j y_j) (a wrong index in the dot
+      product, e.g. summing g alone, breaks it), within the rounding of y.g and of the n products."""
+    T = oracle
+    rng = np.random.default_rng(13)
+    n = 9
+    # one-hot rows: a gap of 200 makes every other exp underflow to exactly 0 in float32
+    x = np.full((4, n), -200.0, np.float32)
+    for r in range(4):
+        x[r, (2 * r + 1) % n] = 0.0
+    t = T.Tensor(x.copy(), requires_grad=True)
+    g = rng.standard_normal((4, n)).astype(np.float32)
+    T.backward(T.sum_all(T.mul(T.softmax(t), T.Tensor(g))))
+    assert np.array_equal(T.softmax(T.Tensor(x)).data, (x == 0).astype(np.float32))
+    assert np.all(t.grad == 0.0)
+    # uniform rows
+    x = np.tile(rng.standard_normal((5, 1)).astype(np.float32), (1, n))
+    t = T.Tensor(x.copy(), requires_grad=True)
+    g = rng.standard_normal((5, n)).astype(np.float32)
+    T.backward(T.sum_all(T.mul(T.softmax(t), T.Tensor(g))))
+    expect = (g.astype(np.float64) - g.astype(np.float64).mean(1, keepdims=True)) / n
+    assert np.max(np.abs(t.grad - expect)) <= 4 * np.finfo(np.float32).eps * np.max(np.abs(g)) / n
+    # rows of dx sum to zero
+    x = (2 * rng.standard_normal((16, 33))).astype(np.float32)
+    t = T.Tensor(x.copy(), requires_grad=True)
+    g = rng.standard_normal((16, 33)).astype(np.float32)
+    T.backward(T.sum_all(T.mul(T.softmax(t), T.Tensor(g))))
+    y = T.softmax(T.Tensor(x)).data.astype(np.float64)
+    bound = 4 * 33 * np.finfo(np.float32).eps * np.max(np.abs(g), axis=1) * np.max(y, axis=1)
+    assert np.all(np.abs(t.grad.astype(np.float64).sum(1)) <= bound)
+
+
 def test_fd_attention_masked(oracle):
     T = oracle
     rng = np.random.default_rng(6)
