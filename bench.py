@@ -59,6 +59,28 @@ class HipEvents:
         self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
         self.hip.hipEventDestroy.argtypes = [C.c_void_p]
 
+    def per_step(self, stream, fn, reps: int) -> list:
+        """Milliseconds of each of reps calls of fn(), between events recorded on `stream` after each call: the
+        device time from the end of one call's queued work to the end of the next one's."""
+        evs = []
+        for _ in range(reps + 1):
+            e = C.c_void_p()
+            assert self.hip.hipEventCreate(C.byref(e)) == 0
+            evs.append(e)
+        self.hip.hipEventRecord(evs[0], stream)
+        for i in range(reps):
+            fn()
+            self.hip.hipEventRecord(evs[i + 1], stream)
+        self.hip.hipEventSynchronize(evs[-1])
+        out = []
+        for i in range(reps):
+            ms = C.c_float()
+            self.hip.hipEventElapsedTime(C.byref(ms), evs[i], evs[i + 1])
+            out.append(ms.value)
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+        return out
+
     def time(self, stream, fn, reps: int) -> float:
         """Average milliseconds of fn() over reps launches, measured between two events on `stream`. fn may be a
         list of launches over distinct buffer sets, called in turn (see MALL_BYTES)."""
@@ -408,23 +430,66 @@ def measured_traffic():
         return None
 
 
+def cpu_model() -> str:
+    """The host CPU's model name as `lscpu` reports it (from /proc/cpuinfo when lscpu is absent)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _omp_threads(n: int):
+    """Sets the OpenMP thread count of the oracle library's runtime (libgomp, already loaded with it)."""
+    try:
+        C.CDLL("libgomp.so.1").omp_set_num_threads(C.c_int(n))
+    except OSError:
+        pass
+
+
+def _cpu_run(oc, seconds: float, min_steps: int):
+    oc.step()  # warm-up (page-in, thread pool)
+    times = []
+    t0 = time.perf_counter()
+    while True:
+        t = time.perf_counter()
+        oc.step()
+        times.append(time.perf_counter() - t)
+        if len(times) >= min_steps and time.perf_counter() - t0 >= seconds:
+            break
+    times.sort()
+    return len(times), sum(times), times[len(times) // 2]
+
+
 def cpu_baseline(cfg: int, seconds: float):
-    """The oracle's step (C restatement of the reference CPU path) on this host's cores: as many steps as fit in
-    about `seconds` (at least one), at the benchmark's full size."""
+    """The oracle's step (C restatement of the reference CPU path) on this host's cores, at the benchmark's full
+    size: with all the threads OpenMP is given (OMP_NUM_THREADS, else the core count) for about `seconds`, and on one
+    thread for about half as long; each reports the median step time of its sample (at least two steps)."""
     from oracle import models
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     oc = models.make_config(cfg)
-    oc.step()  # warm-up (page-in, thread pool)
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oc.step()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(n / el, 4), "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full-size C{cfg} steps (ZeroGrad+fwd+bwd+AdamW) of oracle/om_oracle.c via oracle/tape.py, "
-                      f"{el:.1f} s, OpenMP {threads} threads"}
+    _omp_threads(threads)
+    n, tot, med = _cpu_run(oc, seconds, 2)
+    _omp_threads(1)
+    n1, tot1, med1 = _cpu_run(oc, seconds / 2, 2)
+    _omp_threads(threads)
+    return {"value": round(1.0 / med, 4), "unit": "steps/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(), "nproc": os.cpu_count(),
+            "one_core": {"value": round(1.0 / med1, 4), "unit": "steps/s", "cores": 1,
+                         "sample": f"{n1} steps, {tot1:.1f} s"},
+            "sample": f"median of {n} full-size C{cfg} steps (ZeroGrad+fwd+bwd+AdamW) of oracle/om_oracle.c via "
+                      f"oracle/tape.py, {tot:.1f} s, OpenMP {threads} threads"}
 
 
 def main():
@@ -458,16 +523,22 @@ def main():
     t0 = time.perf_counter()
     loss = None
     for _ in range(a.steps):
-        loss = model.step()  # each step ends with the loss readback (a stream synchronisation)
+        loss = model.step()  # each step returns once its loss has landed on the host
     pkg.load_hip().om_ctx_sync(model.ctx)
     el = time.perf_counter() - t0
     sps = a.steps / el
+    # per-step device times: HIP events on the model's stream after each step, over at least 50 further steps
+    # (a separate pass, so the events do not touch the timed window above)
+    per = sorted(HipEvents().per_step(pkg.load_hip().om_ctx_stream(model.ctx), model.step, max(50, a.steps)))
+    q = lambda f: per[min(len(per) - 1, int(f * len(per)))]
     desc, batch, seq = WORKLOADS[a.config]
     out = {
         "metric": METRIC, "value": round(sps, 3), "unit": "steps/s", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(1000.0 * el / a.steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
         "config": {"workload": desc, "global_batch": batch, "seq_len": seq, "parallelism": "none (1 GPU)"},
+        "step_ms": {"median": round(q(0.5), 4), "p10": round(q(0.1), 4), "p90": round(q(0.9), 4), "n": len(per),
+                    "median_steps_per_s": round(1000.0 / q(0.5), 3), "timing": "hipEvent per step"},
         "final_loss": loss,
     }
     if a.config == 3:
