@@ -234,6 +234,17 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
 om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
                                const float *rstd, const float *dx_add, float *dx, float *dgamma, float *dbeta, int rows,
                                int cols, int acc_params);
+/* om_layernorm_bwd without any device allocation, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. The dgamma/dbeta fp64
+ * partials (2 * ceil(rows / r) * cols doubles, r = 16 rows per chunk when cols is 384 or 768, else 8) go to one fixed
+ * device array of OM_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; larger shapes are refused with
+ * OM_E_ARG before anything is launched. The partials are rewritten by every call, so nothing has to start at zero;
+ * calls that overlap on one GPU (contexts on other streams or threads) share the array and race. Results are
+ * om_layernorm_bwd's, bit for bit. */
+#define OM_NOALLOC_SCRATCH_BYTES (8u << 20)
+om_status om_layernorm_bwd_noalloc(om_ctx *ctx, const float *g, const float *x, const float *gamma,
+                                   const float *mean, const float *rstd, float *dx, float *dgamma, float *dbeta,
+                                   int rows, int cols, int acc_dx, int acc_params);
 /* LayerNorm backward leaving dgamma/dbeta as fp64 partials: dx as om_layernorm_bwd (dx = dx_add + v when dx_add is
  * given, else accumulated when acc_dx, else written; dx may be NULL), and part_g / part_b (either may be NULL), each
  * [om_layernorm_bwd_chunks(rows, cols)][cols], to be finished by om_param_grads_group's column sums. */

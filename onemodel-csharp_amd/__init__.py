@@ -117,6 +117,7 @@ _OM_SIGS = {
     "om_dropout_fwd": [vp, vp, vp, i64, f32, u64, i64],
     "om_dropout_bwd": [vp, vp, vp, i64, f32, u64, i64, ci],
     "om_clip_grad_value": [vp, ci, vp, vp, f32],
+    "om_layernorm_bwd_noalloc": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
             "om_layernorm_bwd_chunks": ci,

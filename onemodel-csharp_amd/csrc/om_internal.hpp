@@ -36,6 +36,9 @@ struct om_ctx {
     // Second slot for callers that launch GEMMs while holding their own scratch (attention's score recompute).
     float *scratch2 = nullptr;
     uint64_t scratch2_bytes = 0;
+    // Device address of the fixed scratch array the allocation-free entry point uses on this context's device
+    // (looked up once per device at context creation; NULL if that failed).
+    void *noalloc_scratch = nullptr;
     int num_cus = 256;
 };
 
@@ -48,6 +51,9 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
 // The same for the second slot (never used by the GEMM engine itself).
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
+// Sets ctx->noalloc_scratch to the device address of the fixed scratch array on ctx->device (the current device),
+// looking it up on the first call for that device only.
+om_status noalloc_init(om_ctx *ctx);
 // The stream every launch of the context goes to.
 inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->stream; }
 // A readback post written by another entry point's kernel: checks that r belongs to ctx and holds `bytes`, waits for

@@ -4,6 +4,8 @@
 // pass.
 #include "om_internal.hpp"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -566,18 +568,50 @@ static om_status ln_bwd_main(om_ctx *ctx, const float *g, const float *x, const 
     return OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
 }
 
+// Fixed device scratch for om_layernorm_bwd_noalloc's fp64 dgamma / dbeta partials (2 * chunks * cols doubles), one
+// copy per GPU for the life of the process. Host code never passes this name to a kernel: it is a host-side stand-in;
+// kernels get the device address that noalloc_init looks up per device.
+static __device__ __align__(256) unsigned char ln_scratch[OM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_ln_scratch_mu;
+void *g_ln_scratch_at[kMaxDevices];  // per device: ln_scratch's device address, once looked up
+}  // namespace
+
+om_status om::noalloc_init(om_ctx *ctx) {
+    ctx->noalloc_scratch = nullptr;
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return om::fail(ctx, OM_E_DEVICE, "allocation-free scratch: device %d is beyond %d", ctx->device, kMaxDevices);
+    std::lock_guard<std::mutex> g(g_ln_scratch_mu);
+    if (!g_ln_scratch_at[ctx->device]) {
+        void *p = nullptr;  // ctx->device is current (om_ctx_create set it)
+        om_status s = om::check_hip(ctx, hipGetSymbolAddress(&p, HIP_SYMBOL(ln_scratch)), "hipGetSymbolAddress");
+        if (s) return s;
+        g_ln_scratch_at[ctx->device] = p;
+    }
+    ctx->noalloc_scratch = g_ln_scratch_at[ctx->device];
+    return OM_OK;
+}
+
+// fixed: the partials' device memory when the caller provides it (the allocation-free entry point), else NULL and
+// the context's scratch is used.
 static om_status ln_bwd(om_ctx *ctx, const float *g, const float *x, const float *gamma, const float *mean,
                         const float *rstd, float *dx, const float *dxin, float *dgamma, float *dbeta, int rows,
-                        int cols, int acc_params) {
+                        int cols, int acc_params, double *fixed = nullptr) {
     const int rpc = ln_rows_per_chunk(cols);
     const int chunks = (rows + rpc - 1) / rpc;
     double *pg = nullptr, *pb = nullptr;
     if (dgamma || dbeta) {
-        float *scr;
-        om_status s = om::scratch(ctx, sizeof(double) * 2ull * chunks * cols, &scr);
-        if (s) return s;
-        pg = dgamma ? reinterpret_cast<double *>(scr) : nullptr;
-        pb = dbeta ? reinterpret_cast<double *>(scr) + (size_t)chunks * cols : nullptr;
+        double *base = fixed;
+        if (!base) {
+            float *scr;
+            om_status s = om::scratch(ctx, sizeof(double) * 2ull * chunks * cols, &scr);
+            if (s) return s;
+            base = reinterpret_cast<double *>(scr);
+        }
+        pg = dgamma ? base : nullptr;
+        pb = dbeta ? base + (size_t)chunks * cols : nullptr;
     }
     om_status s = ln_bwd_main(ctx, g, x, gamma, mean, rstd, dx, dxin, pg, pb, rows, cols);
     if (s) return s;
@@ -595,6 +629,25 @@ om_status om_layernorm_bwd(om_ctx *ctx, const float *g, const float *x, const fl
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0, "om_layernorm_bwd: bad arguments");
     return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, acc_dx && dx ? dx : nullptr, dgamma, dbeta, rows, cols, acc_params);
+}
+
+om_status om_layernorm_bwd_noalloc(om_ctx *ctx, const float *g, const float *x, const float *gamma,
+                                   const float *mean, const float *rstd, float *dx, float *dgamma, float *dbeta,
+                                   int rows, int cols, int acc_dx, int acc_params) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && gamma && mean && rstd && rows > 0 && cols > 0,
+               "om_layernorm_bwd_noalloc: bad arguments");
+    const int rpc = ln_rows_per_chunk(cols);
+    const uint64_t chunks = ((uint64_t)rows + rpc - 1) / rpc;
+    const uint64_t need = (dgamma || dbeta) ? sizeof(double) * 2ull * chunks * (uint64_t)cols : 0;
+    OM_REQUIRE(ctx, need <= (uint64_t)OM_NOALLOC_SCRATCH_BYTES,
+               "om_layernorm_bwd_noalloc: %d x %d needs %llu bytes of dgamma/dbeta partials, more than the %llu of "
+               "its fixed scratch",
+               rows, cols, (unsigned long long)need, (unsigned long long)OM_NOALLOC_SCRATCH_BYTES);
+    if (need && !ctx->noalloc_scratch)
+        return om::fail(ctx, OM_E_STATE, "om_layernorm_bwd_noalloc: the fixed scratch has no device address here");
+    return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, acc_dx && dx ? dx : nullptr, dgamma, dbeta, rows, cols,
+                  acc_params, static_cast<double *>(ctx->noalloc_scratch));
 }
 
 int om_layernorm_bwd_chunks(int rows, int cols) {
