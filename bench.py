@@ -309,18 +309,106 @@ def time_row_kernels(pkg, model, ev, reps: int = 50):
     assert L.om_alloc(ctx, 0, mask.nbytes, C.byref(M)) == 0
     assert L.om_upload(ctx, M, mask.ctypes.data_as(C.c_void_p), mask.nbytes) == 0
     o, dqkv = _dev_buf(L, ctx, B * Ls * W, 0.0), _dev_buf(L, ctx, B * Ls * 3 * W, 0.0)
+    stats = _dev_buf(L, ctx, 2 * B * H * Ls, 0.0)
     off = lambda p, i: C.c_void_p(p.value + 4 * i * W)
     sc = C.c_float(0.0)
-    afwd = lambda: L.om_attention_fwd_fused(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, o, W, B, H, Ls, D, sc)
-    abwd = lambda: L.om_attention_bwd_fused(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, go, W, dqkv,
-                                            off(dqkv, 1), off(dqkv, 2), 3 * W, B, H, Ls, D, sc, 0)
+    # the entry points the tape calls (at this shape they run the whole-row kernels)
+    afwd = lambda: L.om_attention_fwd_flash(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, o, W, stats, B, H, Ls,
+                                            D, sc)
+    abwd = lambda: L.om_attention_bwd_flash(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, M, 1, o, W, stats, go, W,
+                                            dqkv, off(dqkv, 1), off(dqkv, 2), 3 * W, B, H, Ls, D, sc, 0)
     unit = 2.0 * B * H * Ls * Ls * D
     for name, f, flops in (("attention_fwd", afwd, 2 * unit), ("attention_bwd", abwd, 5 * unit)):
         for _ in range(3):
             assert f() == 0
         ms = ev.time(st, f, reps)
         tf = flops / (ms * 1e-3) / 1e12
-        out[name] = {"bound": "mfma", "kernel": f"om_{name}_fused B32 H12 L128 D32 masked", "achieved": round(tf, 2),
+        out[name] = {"bound": "mfma", "kernel": f"om_{name}_flash B32 H12 L128 D32 masked (whole-row kernels)",
+                     "achieved": round(tf, 2),
+                     "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK, 4),
+                     "ms_per_launch": round(ms, 5)}
+    return out
+
+
+def time_conv(pkg, model, ev, reps: int = 20):
+    """C2's convolution (Conv2d 3x3, stride 1, padding 1, 64 -> 64 channels on 32 x 64 x 56 x 56) as the step runs it:
+    the forward (om_conv2d_fwd with bias), the input gradient alone and the weight + bias gradients alone
+    (om_conv2d_bwd with the other outputs NULL), each 2 N Cout Hout Wout Cin k^2 = 7.40 GFLOP, on random data,
+    HIP events on the model's stream."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    N, Ci, H, W, Co, K = 32, 64, 56, 56, 64, 3
+    x, g = _dev_rand(L, ctx, N * Ci * H * W, 1.0, 31), _dev_rand(L, ctx, N * Co * H * W, 1e-2, 32)
+    w, b = _dev_rand(L, ctx, Co * Ci * K * K, 0.05, 33), _dev_rand(L, ctx, Co, 0.1, 34)
+    y, dx = _dev_buf(L, ctx, N * Co * H * W, 0.0), _dev_buf(L, ctx, N * Ci * H * W, 0.0)
+    dw, db = _dev_buf(L, ctx, Co * Ci * K * K, 0.0), _dev_buf(L, ctx, Co, 0.0)
+    geo = (N, Ci, H, W, Co, K, K, 1, 1)
+    runs = (("conv_fwd", lambda: L.om_conv2d_fwd(ctx, x, w, b, y, *geo)),
+            ("conv_dx", lambda: L.om_conv2d_bwd(ctx, g, x, w, dx, None, None, *geo, 0, 0)),
+            ("conv_dw", lambda: L.om_conv2d_bwd(ctx, g, x, w, None, dw, db, *geo, 0, 0)))
+    flops = 2.0 * N * Co * H * W * Ci * K * K
+    out = {}
+    for name, f in runs:
+        for _ in range(3):
+            assert f() == 0, L.om_last_error(ctx)
+        ms = ev.time(L.om_ctx_stream(ctx), f, reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"bound": "mfma", "kernel": f"om_conv2d ({name[5:]}) C2: 32x64x56x56, 64->64, 3x3 p1",
+                     "achieved": round(tf, 2), "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s",
+                     "frac": round(tf / FP32_MFMA_PEAK, 4), "ms_per_launch": round(ms, 5)}
+    return out
+
+
+def time_c5_rows(pkg, model, ev, reps: int = 20):
+    """C5's LayerNorm forward / backward (4096 x 768, buffer sets cycled past the Infinity Cache) and attention forward
+    / backward through the fused entry points (B 8, H 12, L 512, D 64, no mask), priced as time_row_kernels prices
+    the C3 shapes."""
+    L = pkg.load_hip()
+    ctx = model.ctx
+    st = L.om_ctx_stream(ctx)
+    out = {}
+    R, Cc = 4096, 768
+    gam, bet = _dev_rand(L, ctx, Cc, 0.1, 41), _dev_rand(L, ctx, Cc, 0.1, 42)
+    dg, db = _dev_buf(L, ctx, Cc, 0.0), _dev_buf(L, ctx, Cc, 0.0)
+    fwds, bwds = [], []
+    for k in range(_sets(16 * R * Cc)):
+        x, g = _dev_rand(L, ctx, R * Cc, 1.0, 43 + 100 * k), _dev_rand(L, ctx, R * Cc, 1.0, 44 + 100 * k)
+        y, dx = _dev_buf(L, ctx, R * Cc, 0.0), _dev_buf(L, ctx, R * Cc, 0.0)
+        mu, rs = _dev_buf(L, ctx, R, 0.0), _dev_buf(L, ctx, R, 0.0)
+        fwds.append(lambda x=x, y=y, mu=mu, rs=rs: L.om_layernorm_fwd(ctx, x, gam, bet, y, mu, rs, R, Cc,
+                                                                      C.c_float(1e-5)))
+        bwds.append(lambda x=x, g=g, dx=dx, mu=mu, rs=rs: L.om_layernorm_bwd(ctx, g, x, gam, mu, rs, dx, dg, db, R,
+                                                                             Cc, 0, 0))
+    for f in fwds:
+        assert f() == 0
+    for name, fs, nbytes in (("c5_layernorm_fwd", fwds, 8 * R * Cc + 8 * R + 8 * Cc),
+                             ("c5_layernorm_bwd", bwds, 12 * R * Cc + 8 * R + 12 * Cc)):
+        for f in fs:
+            assert f() == 0
+        ms = ev.time(st, fs, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"bound": "hbm", "kernel": f"om_{name[3:]} 4096x768", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK, "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "ms_per_launch": round(ms, 5)}
+    B, H, Ls, D = 8, 12, 512, 64
+    W = H * D
+    qkv = _dev_rand(L, ctx, B * Ls * 3 * W, 1.0, 45)
+    go = _dev_rand(L, ctx, B * Ls * W, 1.0, 46)
+    o, dqkv = _dev_buf(L, ctx, B * Ls * W, 0.0), _dev_buf(L, ctx, B * Ls * 3 * W, 0.0)
+    stats = _dev_buf(L, ctx, 2 * B * H * Ls, 0.0)
+    off = lambda p, i: C.c_void_p(p.value + 4 * i * W)
+    sc = C.c_float(0.0)
+    afwd = lambda: L.om_attention_fwd_flash(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, None, 0, o, W, stats, B, H,
+                                            Ls, D, sc)
+    abwd = lambda: L.om_attention_bwd_flash(ctx, qkv, off(qkv, 1), off(qkv, 2), 3 * W, None, 0, o, W, stats, go, W,
+                                            dqkv, off(dqkv, 1), off(dqkv, 2), 3 * W, B, H, Ls, D, sc, 0)
+    unit = 2.0 * B * H * Ls * Ls * D
+    for name, f, flops in (("c5_attention_fwd", afwd, 2 * unit), ("c5_attention_bwd", abwd, 5 * unit)):
+        for _ in range(3):
+            assert f() == 0, L.om_last_error(ctx)
+        ms = ev.time(st, f, reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"bound": "mfma", "kernel": f"om_{name[3:]}_flash B8 H12 L512 D64 (streaming kernels; the "
+                     f"backward's 5 products priced, its delta pre-pass and dQ reduce included)", "achieved": round(tf, 2),
                      "peak": FP32_MFMA_PEAK, "unit": "TFLOP/s", "frac": round(tf / FP32_MFMA_PEAK, 4),
                      "ms_per_launch": round(ms, 5)}
     return out
@@ -458,8 +546,9 @@ def _omp_threads(n: int):
         pass
 
 
-def _cpu_run(oc, seconds: float, min_steps: int):
-    oc.step()  # warm-up (page-in, thread pool)
+def _cpu_run(oc, seconds: float, min_steps: int, warm: bool = True):
+    if warm:
+        oc.step()  # warm-up (page-in, thread pool)
     times = []
     t0 = time.perf_counter()
     while True:
@@ -475,19 +564,31 @@ def _cpu_run(oc, seconds: float, min_steps: int):
 def cpu_baseline(cfg: int, seconds: float):
     """The oracle's step (C restatement of the reference CPU path) on this host's cores, at the benchmark's full
     size: with all the threads OpenMP is given (OMP_NUM_THREADS, else the core count) for about `seconds`, and on one
-    thread for about half as long; each reports the median step time of its sample (at least two steps)."""
+    thread for about half as long; each reports the median step time of its sample (at least two steps). Where one
+    full step on one thread would not fit that budget (C5), the one-thread sample runs the same model at a smaller
+    batch and scales its step time by the batch ratio (the step's work is linear in the batch)."""
     from oracle import models
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     oc = models.make_config(cfg)
     _omp_threads(threads)
     n, tot, med = _cpu_run(oc, seconds, 2)
     _omp_threads(1)
-    n1, tot1, med1 = _cpu_run(oc, seconds / 2, 2)
+    full = WORKLOADS[cfg][1]
+    b = full
+    while b > 1 and med * threads * b / full > seconds / 4:  # a generous guess of one thread's step time
+        b //= 2
+    if b == full:
+        n1, tot1, med1 = _cpu_run(oc, seconds / 2, 2, warm=False)
+        one_sample = f"{n1} full-size steps, {tot1:.1f} s"
+    else:
+        n1, tot1, med1 = _cpu_run(models.make_config(cfg, {"batch": b}), seconds / 2, 1, warm=False)
+        one_sample = (f"{n1} steps at batch {b} of {full}, {tot1:.1f} s; the median step time scaled by {full // b} "
+                      f"to the full batch")
+        med1 *= full / b
     _omp_threads(threads)
     return {"value": round(1.0 / med, 4), "unit": "steps/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(), "nproc": os.cpu_count(),
-            "one_core": {"value": round(1.0 / med1, 4), "unit": "steps/s", "cores": 1,
-                         "sample": f"{n1} steps, {tot1:.1f} s"},
+            "one_core": {"value": round(1.0 / med1, 4), "unit": "steps/s", "cores": 1, "sample": one_sample},
             "sample": f"median of {n} full-size C{cfg} steps (ZeroGrad+fwd+bwd+AdamW) of oracle/om_oracle.c via "
                       f"oracle/tape.py, {tot:.1f} s, OpenMP {threads} threads"}
 
@@ -547,7 +648,7 @@ def main():
         ev = HipEvents()
         out["roofline"] = time_dominant_kernel(pkg, model, ev)
         out["kernels"] = {"adamw": time_adamw(pkg, model, ev), **time_row_kernels(pkg, model, ev),
-                          **time_clip(pkg, model, ev)}
+                          **time_clip(pkg, model, ev), **time_conv(pkg, model, ev), **time_c5_rows(pkg, model, ev)}
     if not a.no_cpu:
         cb = cpu_baseline(a.config, a.cpu_seconds)
         cb["gpu_over_cpu"] = round(sps / cb["value"], 1)

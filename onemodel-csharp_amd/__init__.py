@@ -118,6 +118,8 @@ _OM_SIGS = {
     "om_dropout_bwd": [vp, vp, vp, i64, f32, u64, i64, ci],
     "om_clip_grad_value": [vp, ci, vp, vp, f32],
     "om_layernorm_bwd_noalloc": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci],
+    "om_attention_fwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, ci, ci, ci, ci, f32],
+    "om_attention_bwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
             "om_layernorm_bwd_chunks": ci,

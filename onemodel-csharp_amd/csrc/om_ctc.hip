@@ -140,58 +140,96 @@ __global__ void k_ctc_reduce(const double *__restrict__ per, const int32_t *__re
     if (reduction != 0) loss[0] = (float)(reduction == 1 ? sum / B : sum);
 }
 
-// CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence: recompute alpha, run beta backwards in t, and for every
-// class accumulate logadd(alpha + beta) over its positions in increasing s.
-__global__ void __launch_bounds__(kBlock) k_ctc_bwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
-                                                    const int32_t *__restrict__ in_len,
-                                                    const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
-                                                    float *__restrict__ dlp, int T, int B,
-                                                    int C, int blank, int reduction, int max_ext, int acc,
-                                                    double *__restrict__ ws) {
-    __shared__ double nll;
+// CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence, in two phases. First the alpha recursion (recomputed, as
+// the reference recomputes it) and the beta recursion run side by side on two wavefronts, alpha forward and beta
+// backward in t, one barrier per step (each lane owns extended positions s, s + 64, ...). Then every (t, class)
+// entry of the gradient is independent: the workgroup's threads take them in turn, and each accumulates
+// logadd(alpha + beta) over the class's positions in increasing s, exactly the reference's order, so the values are
+// those of the sequential loop bit for bit.
+constexpr int kBwdBlock = 256;
+__global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
+                                                       const int32_t *__restrict__ in_len,
+                                                       const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
+                                                       float *__restrict__ dlp, int T, int B, int C, int blank,
+                                                       int reduction, int max_ext, int acc, double *__restrict__ ws) {
+    __shared__ double nll_s;
     const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
-    int b = blockIdx.x;
-    int len = in_len[b], L = tgt_len[b];
+    const int b = blockIdx.x;
+    const int len = in_len[b], L = tgt_len[b];
     int off = 0;
     for (int i = 0; i < b; i++) off += tgt_len[i];
     const int32_t *tgt = targets + off;
-    int tt = T > 0 ? T : 1;
+    const int tt = T > 0 ? T : 1;
     double *alpha = ws + (int64_t)b * 2 * tt * max_ext;
     double *beta = alpha + (int64_t)tt * max_ext;
-    // dlp for this sequence starts from zero (or the existing gradient when accumulating).
-    if (!acc)
-        for (int i = threadIdx.x; i < T * C; i += blockDim.x) dlp[((int64_t)(i / C) * B + b) * C + i % C] = 0.0f;
-    alpha_pass(lp, B, C, b, len, tgt, L, blank, alpha, &nll);
-    if (len == 0 || (isinf(nll) && nll > 0)) return;
-    double scale = reduction == 0 ? (double)g[b] : (double)g[0];
-    if (reduction == 1) scale = scale / (double)(L > 1 ? L : 1) / (double)B;
     const int ext = 2 * L + 1;
-    for (int t = len - 1; t >= 0; t--) {
-        for (int s = threadIdx.x; s < ext; s += blockDim.x) {
-            double v;
-            if (t == len - 1) {
-                v = s >= ext - 2 ? 0.0 : NEG;
-            } else {
-                v = beta[(t + 1) * ext + s];
-                if (s + 1 < ext) v = ctc_logadd(v, beta[(t + 1) * ext + s + 1]);
-                if (s + 2 < ext && can_skip(tgt, s + 2)) v = ctc_logadd(v, beta[(t + 1) * ext + s + 2]);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int i = 0; i < len; i++) {
+        if (wave == 0) {
+            const int t = i;
+            for (int s = lane; s < ext; s += 64) {
+                double a;
+                if (t == 0) {
+                    a = s <= 1 ? 0.0 : NEG;
+                } else {
+                    a = alpha[(t - 1) * ext + s];
+                    if (s >= 1) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 1]);
+                    if (can_skip(tgt, s)) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 2]);
+                }
+                alpha[t * ext + s] =
+                    is_neg_inf(a) ? NEG : a + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
             }
-            beta[t * ext + s] = is_neg_inf(v) ? NEG : v + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+        } else if (wave == 1) {
+            const int t = len - 1 - i;
+            for (int s = lane; s < ext; s += 64) {
+                double v;
+                if (t == len - 1) {
+                    v = s >= ext - 2 ? 0.0 : NEG;
+                } else {
+                    v = beta[(t + 1) * ext + s];
+                    if (s + 1 < ext) v = ctc_logadd(v, beta[(t + 1) * ext + s + 1]);
+                    if (s + 2 < ext && can_skip(tgt, s + 2)) v = ctc_logadd(v, beta[(t + 1) * ext + s + 2]);
+                }
+                beta[t * ext + s] =
+                    is_neg_inf(v) ? NEG : v + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+            }
         }
         __syncthreads();
-        for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    }
+    if (threadIdx.x == 0) {
+        double nll;
+        if (len == 0) {
+            nll = L == 0 ? 0.0 : __longlong_as_double(0x7FF0000000000000LL);
+        } else {
+            double p = alpha[(len - 1) * ext + ext - 1];
+            if (ext >= 2) p = ctc_logadd(p, alpha[(len - 1) * ext + ext - 2]);
+            nll = is_neg_inf(p) ? __longlong_as_double(0x7FF0000000000000LL) : -p;
+        }
+        nll_s = nll;
+    }
+    __syncthreads();
+    const double nll = nll_s;
+    // +inf (an impossible alignment) and an empty input give a zero gradient (CtcBackward, BackwardRecurrent.cs)
+    const bool none = len == 0 || (isinf(nll) && nll > 0);
+    double scale = reduction == 0 ? (double)g[b] : (double)g[0];
+    if (reduction == 1) scale = scale / (double)(L > 1 ? L : 1) / (double)B;
+    for (int idx = threadIdx.x; idx < T * C; idx += blockDim.x) {
+        const int t = idx / C, c = idx - t * C;
+        float *d = dlp + ((int64_t)t * B + b) * C + c;
+        float v = acc ? *d : 0.0f;
+        if (!none && t < len) {
             double a = NEG;
             for (int s = 0; s < ext; s++) {
                 if (label_at(tgt, blank, s) != c) continue;
                 double ab = alpha[t * ext + s] + beta[t * ext + s];
                 if (!is_neg_inf(ab) && ab == ab) a = ctc_logadd(a, ab);
             }
-            if (is_neg_inf(a)) continue;
-            double l = (double)lp[((int64_t)t * B + b) * C + c];
-            float *d = dlp + ((int64_t)t * B + b) * C + c;
-            *d = *d + (float)(-scale * ctc_exp(a - l + nll));
+            if (!is_neg_inf(a)) {
+                double l = (double)lp[((int64_t)t * B + b) * C + c];
+                v = v + (float)(-scale * ctc_exp(a - l + nll));
+            }
         }
-        __syncthreads();
+        *d = v;
     }
 }
 
@@ -266,7 +304,7 @@ om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
     uint64_t tt = T > 0 ? T : 1;
     s = om::scratch(ctx, sizeof(double) * 2ull * B * tt * max_ext, &scr);
     if (s) return s;
-    hipLaunchKernelGGL(k_ctc_bwd, dim3(B), dim3(kBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, g, dlp, T, B, C,
+    hipLaunchKernelGGL(k_ctc_bwd, dim3(B), dim3(kBwdBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, g, dlp, T, B, C,
                        blank, reduction, max_ext, accumulate, reinterpret_cast<double *>(scr));
     return OM_LAUNCH_CHECK(ctx, "om_ctc_bwd");
 }

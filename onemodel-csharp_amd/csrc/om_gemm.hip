@@ -373,6 +373,13 @@ Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bo
                 return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
     const bool n96 = n % 96 == 0 && m >= 64;
     int64_t tiles = (int64_t)((m + 63) / 64) * (n96 ? n / 96 : (n + 63) / 64) * batch;
+    // A handful of tiles over a long-enough K (an MLP's first layer: 4 tiles over K = 784) leaves most CUs idle:
+    // split K into slices of at least 128 k until there are about as many workgroups as CUs / 2.
+    if (batch == 1 && 8 * tiles <= cus && k >= 512) {
+        int s = 1;
+        while (s < 16 && k / (2 * s) >= 128 && tiles * 2 * s <= cus / 2) s *= 2;
+        if (s > 1) return with_splits(64, 64, 32, k, s);
+    }
     if (batch == 1 && tiles < 2 * cus && k >= 1024) {
         double want = 3.0 * cus / (double)tiles;
         int s = 1;
@@ -384,14 +391,17 @@ Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bo
     return best;
 }
 
+// Thin products (one side at most 32: a classifier head's weight gradient, 9 x 768 over K = 4096 tokens) take the
+// 128 x 32 / 32 x 128 tiles; like the square ones they split a long K when their tiles leave CUs idle (slices of at
+// least 256 k, or 128 k when K is short).
 Choice choose(int m, int n, int k, int batch, int cus) {
-    if (n <= 32) return Choice{128, 32, 1, k, 16};
-    if (m <= 32) return Choice{32, 128, 1, k, 16};
     Choice c{64, 64, 1, k, 16};
-    int64_t tiles = (int64_t)((m + 63) / 64) * ((n + 63) / 64) * batch;
-    if (batch == 1 && tiles < cus && k >= 1024) {
+    if (n <= 32) c = Choice{128, 32, 1, k, 16};
+    else if (m <= 32) c = Choice{32, 128, 1, k, 16};
+    int64_t tiles = (int64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * batch;
+    if (batch == 1 && tiles < cus && k >= 512) {
         int want = (int)((cus + tiles - 1) / tiles);
-        int maxs = k / 256;
+        int maxs = k >= 1024 ? k / 256 : k / 128;
         int s = want < maxs ? want : maxs;
         if (s > 1) {
             int ks = ((k + s - 1) / s + 15) / 16 * 16;

@@ -424,9 +424,11 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
     Tensor o = make(q->shape);
     const float *md = mask ? mask->data : nullptr;
     const int W = heads * D;
-    OMT(om_attention_fwd_fused(C(), q->data, k->data, v->data, W, md, 1, o->data, W, B, heads, L, D, 0.0f));
+    float *st = dev().step_floats(2 * (int64_t)B * heads * L);  // per-query softmax statistics for the backward
+    OMT(om_attention_fwd_flash(C(), q->data, k->data, v->data, W, md, 1, o->data, W, st, B, heads, L, D, 0.0f));
+    const float *od = o->data;
     if (tracked({&q, &k, &v}))
-        attach(o, "Attention", {q, k, v}, [md, B, heads, L, D, W](Engine &e, Record &r, const float *g) {
+        attach(o, "Attention", {q, k, v}, [md, st, od, B, heads, L, D, W](Engine &e, Record &r, const float *g) {
             int a[3];
             float *d[3];
             for (int i = 0; i < 3; i++) d[i] = e.dest(r, i, &a[i]);
@@ -437,9 +439,9 @@ Tensor attention_heads(const Tensor &q, const Tensor &k, const Tensor &v, const 
                 if (d[i] && a[i] != common) {
                     tmp[i] = dev().step_floats(r.inputs[i]->numel);
                 }
-            OMT(om_attention_bwd_fused(C(), r.inputs[0]->data, r.inputs[1]->data, r.inputs[2]->data, W, md, 1, g, W,
-                                       tmp[0] ? tmp[0] : d[0], tmp[1] ? tmp[1] : d[1], tmp[2] ? tmp[2] : d[2], W, B,
-                                       heads, L, D, 0.0f, common));
+            OMT(om_attention_bwd_flash(C(), r.inputs[0]->data, r.inputs[1]->data, r.inputs[2]->data, W, md, 1, od, W,
+                                       st, g, W, tmp[0] ? tmp[0] : d[0], tmp[1] ? tmp[1] : d[1],
+                                       tmp[2] ? tmp[2] : d[2], W, B, heads, L, D, 0.0f, common));
             for (int i = 0; i < 3; i++)
                 if (tmp[i]) {
                     if (a[i]) OMT(om_axpy(C(), 1.0f, tmp[i], d[i], r.inputs[i]->numel));
@@ -546,14 +548,16 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
     OMT(om_linear_fwd(C(), x->data, wq->data, bq->data, qkv, rows, w, 3 * w));
     Tensor o = make(x->shape);
     const float *md = mask ? mask->data : nullptr;
-    OMT(om_attention_fwd_fused(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, o->data, w, B, heads, L, D, 0.0f));
+    float *st = dev().step_floats(2 * (int64_t)B * heads * L);  // per-query softmax statistics for the backward
+    OMT(om_attention_fwd_flash(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, o->data, w, st, B, heads, L, D, 0.0f));
+    const float *od = o->data;
     if (tracked({&x, &wq, &bq, &wk, &bk, &wv, &bv}))
         attach(o, "AttentionQKV", {x, wq, bq, wk, bk, wv, bv},
-               [qkv, md, B, L, heads, D, w, rows, WW](Engine &e, Record &r, const float *g) {
+               [qkv, md, st, od, B, L, heads, D, w, rows, WW](Engine &e, Record &r, const float *g) {
                    const int64_t W = w;
                    float *dqkv = dev().step_floats((int64_t)rows * 3 * W);
-                   OMT(om_attention_bwd_fused(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, g, w, dqkv, dqkv + W,
-                                              dqkv + 2 * W, 3 * w, B, heads, L, D, 0.0f, 0));
+                   OMT(om_attention_bwd_flash(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, od, w, st, g, w, dqkv,
+                                              dqkv + W, dqkv + 2 * W, 3 * w, B, heads, L, D, 0.0f, 0));
                    int ax, a[6];
                    float *dx = e.dest(r, 0, &ax);
                    float *d[6];

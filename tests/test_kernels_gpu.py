@@ -528,6 +528,79 @@ def test_attention_fused_recompute(dev, T, B, H, L, D, masked, packed):
         assert scaled(heads(gd) - np.float32(0.5), ref) <= TOL
 
 
+@pytest.mark.parametrize("B,H,L,D,masked,packed,acc", [
+    (8, 12, 512, 64, False, True, 0),   # C5 at full size: the packed q|k|v projection, no mask
+    (2, 3, 128, 64, True, False, 1),
+    (2, 4, 256, 32, True, True, 1),     # D = 32 beyond the whole-row kernels' 128
+    (1, 2, 64, 64, True, True, 0),      # one chunk
+    (3, 2, 192, 64, True, False, 1),    # three chunks, padding masks of different lengths
+], ids=["c5", "L128-d64", "L256-d32", "L64-d64", "L192-d64"])
+def test_attention_flash(dev, T, B, H, L, D, masked, packed, acc):
+    """om_attention_{fwd,bwd}_flash (keys, then queries streamed through the workgroup; the forward's row statistics
+    feed the backward; dQ summed over key blocks in a fixed order) against the oracle's reference attention: O and
+    dQ, dK, dV within 1e-5 scaled, accumulating into existing gradients when asked; the forward's statistics are each
+    row's maximum logit (log2 units) and inverse sum; and two runs give the same bits."""
+    rng = np.random.default_rng(B * L + D + H + 7)
+    W = H * D
+    ld = 3 * W if packed else W
+    qkv = rnd(rng, B, L, 3 * W)
+    g = rnd(rng, B, L, W)
+    mask = None
+    if masked:
+        lens = rng.integers(L // 2, L + 1, B)
+        mask = np.zeros((B, L, L), np.float32)
+        for b in range(B):
+            mask[b, :, lens[b]:] = -np.inf
+    heads = lambda a: np.ascontiguousarray(a.reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    parts = [qkv[:, :, i * W:(i + 1) * W] for i in range(3)]
+    tq, tk, tv = (heads(a) for a in parts)
+    tg = heads(g)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref = np.empty_like(tq)
+    mp = T.fp(mask) if masked else None
+    T.lib().or_attention_fwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(o_ref), B, H, L, L, D, C.c_float(scale))
+    dq, dk, dv = np.empty_like(tq), np.empty_like(tk), np.empty_like(tv)
+    T.lib().or_attention_bwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(tg), T.fp(dq), T.fp(dk), T.fp(dv), B, H, L, L,
+                             D, C.c_float(scale))
+    base = 0.5 if acc else 0.0
+    if packed:
+        QKV = dev.put(qkv)
+        qp = [QKV.data_ptr() + 4 * i * W for i in range(3)]
+        DQKV = dev.empty((B, L, 3 * W), fill=base)
+        dp = [DQKV.data_ptr() + 4 * i * W for i in range(3)]
+        got = lambda: [dev.get(DQKV)[:, :, i * W:(i + 1) * W] for i in range(3)]
+    else:
+        QS = [dev.put(np.ascontiguousarray(a)) for a in parts]
+        qp = [t.data_ptr() for t in QS]
+        DS = [dev.empty((B, L, W), fill=base) for _ in range(3)]
+        dp = [t.data_ptr() for t in DS]
+        got = lambda: [dev.get(t) for t in DS]
+    G, M = dev.put(g), (dev.put(mask) if masked else None)
+    O, ST = dev.empty((B, L, W)), dev.empty((2, B, H, L))
+    dev.call("om_attention_fwd_flash", qp[0], qp[1], qp[2], ld, M, 1, O, W, ST, B, H, L, D, C.c_float(scale))
+    o_dev = dev.get(O)
+    assert scaled(heads(o_dev), o_ref) <= TOL
+    # the statistics: row maximum of x = S scale log2(e) + mask log2(e), and 1 / sum of 2^(x - max)
+    st = dev.get(ST)
+    x = (np.matmul(tq.astype(np.float64), tk.astype(np.float64).transpose(0, 1, 3, 2)) * scale
+         + (mask[:, None].astype(np.float64) if masked else 0.0)) * np.log2(np.e)
+    mx = x.max(-1)
+    assert np.max(np.abs(st[0] - mx)) <= 1e-5 * max(1.0, float(np.max(np.abs(mx))))
+    assert np.max(np.abs(st[1] * np.exp2(x - mx[..., None]).sum(-1) - 1.0)) <= 1e-5
+    runs = []
+    for rep in range(2):
+        if rep:
+            for t_ in ([DQKV] if packed else DS):
+                dev.call("om_fill", t_, C.c_float(base), C.c_int64(t_.nbytes // 4))
+        dev.call("om_attention_bwd_flash", qp[0], qp[1], qp[2], ld, M, 1, O, W, ST, G, W, dp[0], dp[1], dp[2], ld, B,
+                 H, L, D, C.c_float(scale), acc)
+        runs.append([a.copy() for a in got()])
+    for gd, ref in zip(runs[0], (dq, dk, dv)):
+        assert scaled(heads(gd) - np.float32(base), ref) <= TOL
+    for a, b in zip(runs[0], runs[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("L,masked", [(128, True), (128, False), (64, True)])
 def test_attention_bwd_kernels_agree(dev, L, masked):
     """The backward's two fused kernels give the same bits: 24 x 12 (head, batch) pairs run the quarter-staged
