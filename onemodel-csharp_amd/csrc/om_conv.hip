@@ -9,7 +9,22 @@
 // materialised; Wt is W with (ci) and (co) swapped, a small per-call transpose.
 #include "om_gemm.hpp"
 
+#include <cstdlib>
+
+// 3x3, stride 1, padding 1 kernels (om_conv3.hip); each returns false when the shape is not one it takes.
+bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin, int H,
+                  int W, int Cout, int acc, om_status *st, bool flip_weights);
+bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, int Cin, int H, int W, int Cout,
+                 int acc, om_status *st);
+
 namespace {
+
+// The 3x3 / stride 1 / padding 1 geometry the staged kernels take (OM_CONV3=0 keeps every shape on k_conv, for
+// comparisons).
+bool conv3_geometry(int KH, int KW, int stride, int pad) {
+    static const char *s = std::getenv("OM_CONV3");
+    return KH == 3 && KW == 3 && stride == 1 && pad == 1 && !(s && s[0] == '0');
+}
 
 using namespace omg;
 
@@ -380,6 +395,8 @@ om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float
     om_status s = conv_check(ctx, "om_conv2d_fwd", N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
     if (s) return s;
     OM_REQUIRE(ctx, x && w && y, "om_conv2d_fwd: NULL pointer");
+    if (conv3_geometry(KH, KW, stride, pad) && om_conv3_fwd(ctx, x, w, bias, y, N, Cin, H, W, Cout, 0, &s, false))
+        return s;
     Params p = conv_params(N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
     p.m = Cout;
     p.n = OH * OW;
@@ -422,6 +439,15 @@ om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float
                            acc_params);
         s = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd db");
         if (s) return s;
+    }
+    const bool c3 = conv3_geometry(KH, KW, stride, pad);
+    if (dw && c3 && om_conv3_dw(ctx, g, x, dw, N, Cin, H, W, Cout, acc_params, &s)) {
+        if (s) return s;
+        dw = nullptr;  // done
+    }
+    if (dx && c3 && om_conv3_fwd(ctx, g, w, nullptr, dx, N, Cout, H, W, Cin, acc_dx, &s, true)) {
+        if (s) return s;
+        dx = nullptr;  // done
     }
     if (dw) {
         Params p = conv_params(N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);

@@ -636,7 +636,11 @@ def test_attention_bwd_kernels_agree(dev, L, masked):
                                                   (32, 64, 56, 56, 64, 3, 1, 1),
                                                   # C4's four stages at full batch
                                                   (32, 1, 32, 128, 32, 3, 1, 1), (32, 32, 16, 64, 64, 3, 1, 1),
-                                                  (32, 64, 8, 32, 128, 3, 1, 1), (32, 128, 4, 32, 256, 3, 1, 1)])
+                                                  (32, 64, 8, 32, 128, 3, 1, 1), (32, 128, 4, 32, 256, 3, 1, 1),
+                                                  # the staged 3x3 kernels at widths that are not multiples of 16,
+                                                  # images smaller than a tile, and both channel blocks
+                                                  (3, 16, 7, 12, 32, 3, 1, 1), (2, 32, 9, 20, 64, 3, 1, 1),
+                                                  (2, 48, 5, 36, 96, 3, 1, 1)])
 def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     rng = np.random.default_rng(N * Cin + Cout)
     x, w, b = rnd(rng, N, Cin, H, W), rnd(rng, Cout, Cin, K, K, scale=0.2), rnd(rng, Cout)
@@ -654,6 +658,14 @@ def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     assert scaled(dev.get(DX), dx) <= TOL
     assert scaled(dev.get(DW), dw) <= TOL
     assert scaled(dev.get(DB), db) <= 1e-7
+    # accumulating into the existing gradients, and the same bits on a second run
+    first = [dev.get(t).copy() for t in (DX, DW, DB)]
+    dev.call("om_conv2d_bwd", G, X, Wd, DX, DW, DB, N, Cin, H, W, Cout, K, K, S, P, 1, 1)
+    assert scaled(dev.get(DX), dx + dx) <= TOL
+    assert scaled(dev.get(DW), dw + dw) <= TOL
+    dev.call("om_conv2d_bwd", G, X, Wd, DX, DW, DB, N, Cin, H, W, Cout, K, K, S, P, 0, 0)
+    for a, t in zip(first, (DX, DW, DB)):
+        assert np.array_equal(a.view(np.uint32), dev.get(t).view(np.uint32))
 
 
 @pytest.mark.parametrize("shape,k,s", [((2, 3, 8, 12), (2, 2), (2, 2)), ((2, 4, 8, 6), (2, 1), (2, 1)),
