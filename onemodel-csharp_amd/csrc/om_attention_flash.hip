@@ -177,6 +177,125 @@ __global__ void __launch_bounds__(256) k_flash_fwd(const float *__restrict__ q, 
     }
 }
 
+// Forward for rows that fit a workgroup whole (L = 64 or 128): the streaming forward's arithmetic in one pass over
+// all L keys, so there is no running rescale. One workgroup per batch item, head and 64 queries (a wavefront per 16
+// queries); K and V^T of the (batch, head) staged in LDS, S^T = K Q^T with this lane's query on the lane index t,
+// E = 2^(x - max) in the registers that hold S^T, which are the B operand of O^T = V^T E^T, and O = O^T / l. The
+// statistics are the streaming forward's (m in log2 units, 1/l), so either backward can follow either forward.
+template <int D, int L>
+__global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, const float *__restrict__ k,
+                                                  const float *__restrict__ v, int ld, const float *__restrict__ mask,
+                                                  int64_t mask_bstride, float *__restrict__ o, int ldo,
+                                                  float *__restrict__ stat_m, float *__restrict__ stat_r, int H,
+                                                  float c) {
+    constexpr int DB = D / 16, NB = L / 16, LDK = D + 4, LDV = L + 4, Q4 = D / 4, PER = L * Q4 / 256;
+    static_assert(L * Q4 % 256 == 0, "K and V are whole rounds of the workgroup");
+    __shared__ __attribute__((aligned(16))) float Ks[L * LDK];  // [key][d]
+    __shared__ __attribute__((aligned(16))) float Vt[D * LDV];  // [d][key]
+    int qb, h, b;
+    block_coords(L / 64, H, qb, h, b);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
+    const int qrow = qb * 64 + 16 * w + t;  // this lane's query
+    const int64_t row0 = (int64_t)b * L;
+    floatx4 qf[DB];  // B operand of S^T = K Q^T: Q[qrow][16 blk + 4 kl + u]
+    const float *qg = q + (row0 + qrow) * ld + h * D;
+#pragma unroll
+    for (int blk = 0; blk < DB; blk++) qf[blk] = *reinterpret_cast<const floatx4 *>(qg + 16 * blk + 4 * kl);
+    floatx4 mv[NB];  // mask of query t over keys 16 j + 4 kl + r
+    if (mask) {
+        const float *mr = mask + b * mask_bstride + (int64_t)qrow * L + 4 * kl;
+#pragma unroll
+        for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
+    }
+    // K rows: thread f takes row f / Q4, four d from (f % Q4) * 4. V^T: key f % L, four d from (f / L) * 4, so each
+    // LDS store row of V^T is contiguous across the lanes; V's loads are issued once K is in LDS and arrive while
+    // S^T and the softmax run.
+    const float *kg = k + row0 * ld + h * D, *vg = v + row0 * ld + h * D;
+    floatx4 kx[PER], vx[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int f = (int)threadIdx.x + 256 * i;
+        kx[i] = *reinterpret_cast<const floatx4 *>(kg + (int64_t)(f / Q4) * ld + (f % Q4) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int f = (int)threadIdx.x + 256 * i;
+        *reinterpret_cast<floatx4 *>(&Ks[(f / Q4) * LDK + (f % Q4) * 4]) = kx[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int f = (int)threadIdx.x + 256 * i;
+        vx[i] = *reinterpret_cast<const floatx4 *>(vg + (int64_t)(f % L) * ld + (f / L) * 4);
+    }
+    floatx4 s[NB];  // S^T[key 16 j + 4 kl + r][query t]
+#pragma unroll
+    for (int j = 0; j < NB; j++) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int blk = 0; blk < DB; blk++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Ks[(16 * j + t) * LDK + 16 * blk + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) s[j] = mfma4(a[u], qf[blk][u], s[j]);
+        }
+    float mx = -__int_as_float(0x7F800000);
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float x = __builtin_fmaf(s[j][r], c, mask ? mv[j][r] * kLog2e : 0.0f);
+            s[j][r] = x;
+            mx = x > mx ? x : mx;
+        }
+    {
+        float o2 = __shfl_xor(mx, 16, 64);
+        mx = o2 > mx ? o2 : mx;
+        o2 = __shfl_xor(mx, 32, 64);
+        mx = o2 > mx ? o2 : mx;
+    }
+    const float mu = mx == -__int_as_float(0x7F800000) ? 0.0f : mx;  // a fully masked row: l = 0, O = NaN
+    float ps = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float e = exp2_hw(s[j][r] - mu);
+            s[j][r] = e;
+            ps += e;
+        }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int f = (int)threadIdx.x + 256 * i;
+        const int key = f % L, d0 = (f / L) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; e++) Vt[(d0 + e) * LDV + key] = vx[i][e];
+    }
+    __syncthreads();
+    floatx4 oa[DB];  // O^T[16 db + 4 kl + r][query t], unnormalised
+#pragma unroll
+    for (int db = 0; db < DB; db++) {
+        oa[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Vt[(16 * db + t) * LDV + 16 * j + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) oa[db] = mfma4(a[u], s[j][u], oa[db]);
+        }
+    }
+    const float rl = 1.0f / ps;
+    float *og = o + (row0 + qrow) * ldo + h * D;
+#pragma unroll
+    for (int db = 0; db < DB; db++) *reinterpret_cast<floatx4 *>(og + 16 * db + 4 * kl) = oa[db] * rl;
+    if (kl == 0) {
+        const int64_t sr = ((int64_t)b * H + h) * L + qrow;
+        stat_m[sr] = mx;
+        stat_r[sr] = rl;
+    }
+}
+
 // delta[(b H + h) L + l] = (float) sum over d, in double, of dO * O for every query row (16 lanes per row).
 template <int D>
 __global__ void __launch_bounds__(256) k_flash_delta(const float *__restrict__ g, int ldg, const float *__restrict__ o,
@@ -348,6 +467,205 @@ __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ 
     }
 }
 
+// Backward for rows that fit a workgroup whole (D = 32, L = 64 or 128): the streaming backward's arithmetic with
+// all L queries in one pass. One workgroup per batch item, head and 64 keys (a wavefront per 16 keys), so a
+// (batch, head) pair is L / 64 workgroups and the 384 pairs of a C3 step fill the chip evenly (three workgroups per
+// CU). In order:
+//   1. Q and dO rows (all L queries), this block's K rows, the queries' m and 1/l into LDS; this lane's K and V row
+//      fragments into registers (the B operands of S = Q K^T and dP = dO V^T);
+//   2. delta = rowsum(dO * O) per query, a product per element summed in double over d;
+//   3. per block of 16 queries: S and dP on MFMA, P = 2^(x - m) / l, dS = P (dP - delta) scale, and at once
+//      dV^T += dO^T P and dK^T += Q^T dS, whose B operands are the P and dS registers just computed (the A operands
+//      read dO and Q two d at a time: row t of dV^T's A is d = 2t + db, so a lane's outputs are eight consecutive d);
+//      dS stays in registers;
+//   4. dS into LDS over Q and dO ([query][key]), then dQ = dS K over this block's 64 keys for two blocks of 16
+//      queries per wavefront: the final dQ when L = 64, else a partial summed by k_flash_dq_reduce.
+template <int L>
+__global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q, const float *__restrict__ k,
+                                                     const float *__restrict__ v, int ld, const float *__restrict__ mask,
+                                                     int64_t mask_bstride, const float *__restrict__ g, int ldg,
+                                                     const float *__restrict__ o, int ldo,
+                                                     const float *__restrict__ stat_m, const float *__restrict__ stat_r,
+                                                     float *dk, float *dv, float *dq, int ldd,
+                                                     float *__restrict__ dq_part, int H, float c, float scale,
+                                                     int acc) {
+    constexpr int D = 32, LDX = D + 4, NQB = L / 16, Q4 = D / 4, PERQ = L * Q4 / 256, PERK = kChunk * Q4 / 256;
+    constexpr int TPQ = 256 / L, DPT = D / TPQ;  // threads per query and d per thread for delta
+    static_assert(L == 64 || L == 128, "whole rows of 64 or 128 queries");
+    static_assert(L * LDSC <= 2 * L * LDX, "dS [L][68] fits where Q and dO were");
+    __shared__ __attribute__((aligned(16))) float QG[2 * L * LDX];  // Q [q][d] and dO [q][d]; later dS [q][key]
+    __shared__ __attribute__((aligned(16))) float Ks[kChunk * LDX];  // this block's K [key][d]
+    __shared__ __attribute__((aligned(16))) float St[3][L];          // m, 1/l, delta of every query
+    float *Qs = QG, *Gs = QG + L * LDX;
+    int kb, h, b;
+    block_coords(L / kChunk, H, kb, h, b);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
+    const int64_t row0 = (int64_t)b * L, bh = (int64_t)b * H + h;
+    const int key0 = kb * kChunk, mykey = key0 + 16 * w + t;  // this lane's key in S = Q K^T
+    floatx4 kf[2], vf[2];
+    {
+        const float *kr = k + (row0 + mykey) * ld + h * D, *vr = v + (row0 + mykey) * ld + h * D;
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            kf[blk] = *reinterpret_cast<const floatx4 *>(kr + 16 * blk + 4 * kl);
+            vf[blk] = *reinterpret_cast<const floatx4 *>(vr + 16 * blk + 4 * kl);
+        }
+    }
+    // 1. every load first, then the LDS stores
+    const int tid = threadIdx.x;
+    floatx4 qx[PERQ], gx[PERQ], kx[PERK], ox[DPT / 4];
+    const float *qg = q + row0 * ld + h * D, *gg = g + row0 * ldg + h * D;
+#pragma unroll
+    for (int i = 0; i < PERQ; i++) {
+        const int f = tid + 256 * i;
+        qx[i] = *reinterpret_cast<const floatx4 *>(qg + (int64_t)(f / Q4) * ld + (f % Q4) * 4);
+        gx[i] = *reinterpret_cast<const floatx4 *>(gg + (int64_t)(f / Q4) * ldg + (f % Q4) * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < PERK; i++) {
+        const int f = tid + 256 * i;
+        kx[i] = *reinterpret_cast<const floatx4 *>(k + (row0 + key0 + f / Q4) * ld + h * D + (f % Q4) * 4);
+    }
+    const int dq_q = tid / TPQ, dq_d0 = (tid % TPQ) * DPT;  // delta: this thread's query and first d
+    {
+        const float *orow = o + (row0 + dq_q) * ldo + h * D + dq_d0;
+#pragma unroll
+        for (int e = 0; e < DPT / 4; e++) ox[e] = *reinterpret_cast<const floatx4 *>(orow + 4 * e);
+    }
+    float stv = 0.0f;
+    if (tid < 2 * L) stv = (tid < L ? stat_m : stat_r)[bh * L + tid % L];
+#pragma unroll
+    for (int i = 0; i < PERQ; i++) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<floatx4 *>(&Qs[(f / Q4) * LDX + (f % Q4) * 4]) = qx[i];
+        *reinterpret_cast<floatx4 *>(&Gs[(f / Q4) * LDX + (f % Q4) * 4]) = gx[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PERK; i++) {
+        const int f = tid + 256 * i;
+        *reinterpret_cast<floatx4 *>(&Ks[(f / Q4) * LDX + (f % Q4) * 4]) = kx[i];
+    }
+    if (tid < 2 * L) St[tid / L][tid % L] = stv;
+    __syncthreads();
+    // 2. delta
+    {
+        double dot = 0.0;
+#pragma unroll
+        for (int e = 0; e < DPT / 4; e++) {
+            const floatx4 gv = *reinterpret_cast<const floatx4 *>(&Gs[dq_q * LDX + dq_d0 + 4 * e]);
+#pragma unroll
+            for (int x = 0; x < 4; x++) dot += (double)(gv[x] * ox[e][x]);
+        }
+#pragma unroll
+        for (int off = 1; off < TPQ; off <<= 1) dot += __shfl_xor(dot, off, 64);
+        if (tid % TPQ == 0) St[2][dq_q] = (float)dot;
+    }
+    __syncthreads();
+    // 3. S, dP, P, dS per block of 16 queries; dV^T and dK^T accumulate over all L queries. The mask values of block
+    // i + 1 (this lane's key at queries 16 (i + 1) + 4 kl + r) are loaded while block i runs.
+    const float *mbase = mask ? mask + b * mask_bstride + mykey : nullptr;
+    float mkc[4], mkn[4];
+    auto mask_load = [&](float(&dst)[4], int i) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) dst[r] = mbase ? mbase[(int64_t)(16 * i + 4 * kl + r) * L] : 0.0f;
+    };
+    mask_load(mkc, 0);
+    floatx4 dsv[NQB];
+    floatx4 dvt[2], dkt[2];  // [d = 2 (4 kl + r) + db][key t]
+#pragma unroll
+    for (int db = 0; db < 2; db++) dvt[db] = dkt[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NQB; i++) {
+        if (i + 1 < NQB) mask_load(mkn, i + 1);
+        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Qs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
+            const floatx4 ga = *reinterpret_cast<const floatx4 *>(&Gs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                s = mfma4(a[u], kf[blk][u], s);
+                dp = mfma4(ga[u], vf[blk][u], dp);
+            }
+        }
+        const floatx4 mq = *reinterpret_cast<const floatx4 *>(&St[0][16 * i + 4 * kl]);
+        const floatx4 rq = *reinterpret_cast<const floatx4 *>(&St[1][16 * i + 4 * kl]);
+        const floatx4 dl = *reinterpret_cast<const floatx4 *>(&St[2][16 * i + 4 * kl]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = exp2_hw(__builtin_fmaf(s[r], c, mkc[r] * kLog2e) - mq[r]) * rq[r];
+            s[r] = p;
+            dp[r] = (p * (dp[r] - dl[r])) * scale;
+            mkc[r] = mkn[r];
+        }
+        dsv[i] = dp;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int qq = 16 * i + 4 * kl + u;
+            const float2 gv = *reinterpret_cast<const float2 *>(&Gs[qq * LDX + 2 * t]);
+            const float2 qv = *reinterpret_cast<const float2 *>(&Qs[qq * LDX + 2 * t]);
+            dvt[0] = mfma4(gv.x, s[u], dvt[0]);
+            dvt[1] = mfma4(gv.y, s[u], dvt[1]);
+            dkt[0] = mfma4(qv.x, dp[u], dkt[0]);
+            dkt[1] = mfma4(qv.y, dp[u], dkt[1]);
+        }
+    }
+    __syncthreads();  // every wavefront is done with Q and dO
+    // 4. dS [query][key of this block] over Q and dO, then dQ for query blocks w, w + 4, ...
+    float *dS = QG;
+#pragma unroll
+    for (int i = 0; i < NQB; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) dS[(16 * i + 4 * kl + r) * LDSC + 16 * w + t] = dsv[i][r];
+    __syncthreads();
+    if (dq) {
+#pragma unroll
+        for (int i = w; i < NQB; i += 4) {
+            floatx4 qa[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int kb2 = 0; kb2 < 4; kb2++) {
+                const floatx4 a = *reinterpret_cast<const floatx4 *>(&dS[(16 * i + t) * LDSC + 16 * kb2 + 4 * kl]);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float2 kv = *reinterpret_cast<const float2 *>(&Ks[(16 * kb2 + 4 * kl + u) * LDX + 2 * t]);
+                    qa[0] = mfma4(a[u], kv.x, qa[0]);
+                    qa[1] = mfma4(a[u], kv.y, qa[1]);
+                }
+            }
+            // rows 16 i + 4 kl + r, d = 2 t and 2 t + 1
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int qq = 16 * i + 4 * kl + r;
+                const float2 val = make_float2(qa[0][r], qa[1][r]);
+                if (dq_part) {
+                    *reinterpret_cast<float2 *>(dq_part + ((int64_t)kb * gridDim.x / (L / kChunk) * L + bh * L + qq) *
+                                                              D + 2 * t) = val;
+                } else {
+                    float2 *p = reinterpret_cast<float2 *>(dq + (row0 + qq) * ldd + h * D + 2 * t);
+                    *p = acc ? make_float2(p->x + val.x, p->y + val.y) : val;
+                }
+            }
+        }
+    }
+    // dV and dK rows of this lane's key: d = 8 kl + 2 r + db
+    const int64_t orow = (row0 + mykey) * ldd + h * D + 8 * kl;
+    floatx4 lo, hi;
+    if (dv) {
+        lo = floatx4{dvt[0][0], dvt[1][0], dvt[0][1], dvt[1][1]};
+        hi = floatx4{dvt[0][2], dvt[1][2], dvt[0][3], dvt[1][3]};
+        floatx4 *p = reinterpret_cast<floatx4 *>(dv + orow);
+        p[0] = acc ? p[0] + lo : lo;
+        p[1] = acc ? p[1] + hi : hi;
+    }
+    if (dk) {
+        lo = floatx4{dkt[0][0], dkt[1][0], dkt[0][1], dkt[1][1]};
+        hi = floatx4{dkt[0][2], dkt[1][2], dkt[0][3], dkt[1][3]};
+        floatx4 *p = reinterpret_cast<floatx4 *>(dk + orow);
+        p[0] = acc ? p[0] + lo : lo;
+        p[1] = acc ? p[1] + hi : hi;
+    }
+}
+
 // dq[b, l, h, :] (+)= the sum over key blocks 0, 1, ... of the partials, in that order: a thread per four floats.
 template <int D>
 __global__ void __launch_bounds__(256) k_flash_dq_reduce(const float *__restrict__ part, int nkb, int64_t rows,
@@ -366,18 +684,26 @@ __global__ void __launch_bounds__(256) k_flash_dq_reduce(const float *__restrict
 
 bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-// Comparison runs: OM_ATTN_FLASH=1 sends the shapes the whole-row kernels of om_attention_fused.hip take (D = 32,
-// L <= 128) through the streaming kernels too.
-bool force_flash() {
-    static const char *s = std::getenv("OM_ATTN_FLASH");
-    return s && s[0] == '1';
+// Kernels for D = 32 and L = 64 or 128, where a workgroup holds whole rows. By default the whole-row forward with
+// statistics (k_rows_fwd) and the streaming backward. Comparison runs: OM_ATTN_PATH=exact runs the pair of
+// om_attention_fused.hip instead (the reference's exact softmax recompute, no statistics), OM_ATTN_PATH=stream the
+// streaming forward too.
+enum ShortPath { kRows, kExact, kStream };
+ShortPath short_path() {
+    static const ShortPath p = [] {
+        const char *s = std::getenv("OM_ATTN_PATH");
+        if (s && s[0] == 'e') return kExact;
+        if (s && s[0] == 's') return kStream;
+        return kRows;
+    }();
+    return p;
 }
+bool short_rows(int L, int d) { return d == 32 && (L == 64 || L == 128); }
 
-// Shapes the streaming kernels take: D of 32 or 64, L a positive multiple of 64, 16-byte aligned rows; D = 32 with
-// L <= 128 goes to the whole-row kernels.
+// Shapes the statistics kernels take: D of 32 or 64, L a positive multiple of 64, 16-byte aligned rows.
 bool flash_fwd_ok(const float *q, const float *k, const float *v, int ld, const float *mask, const float *o, int ldo,
                   int L, int d) {
-    if (d == 32 && L <= 128 && !force_flash()) return false;
+    if (short_rows(L, d) && short_path() == kExact) return false;
     return (d == 32 || d == 64) && L >= kChunk && L % kChunk == 0 && ld % 4 == 0 && ldo % 4 == 0 && al16(q) &&
            al16(k) && al16(v) && al16(o) && al16(mask);
 }
@@ -410,7 +736,14 @@ om_status om_attention_fwd_flash(om_ctx *ctx, const float *q, const float *k, co
     const int64_t n = (int64_t)B * H * L;
     const dim3 grid((unsigned)((int64_t)B * H * (L / kChunk)));
     const float c = scale * kLog2e;
-    if (d == 64)
+    if (short_rows(L, d) && short_path() == kRows) {
+        if (L == 128)
+            hipLaunchKernelGGL((k_rows_fwd<32, 128>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
+                               o, ld_o, stats, stats + n, H, c);
+        else
+            hipLaunchKernelGGL((k_rows_fwd<32, 64>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
+                               o, ld_o, stats, stats + n, H, c);
+    } else if (d == 64)
         hipLaunchKernelGGL(k_flash_fwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o,
                            stats, stats + n, H, L, c);
     else
@@ -437,14 +770,31 @@ om_status om_attention_bwd_flash(om_ctx *ctx, const float *q, const float *k, co
     const int64_t mstride = (mask && mask_batched) ? (int64_t)L * L : 0;
     const int64_t n = (int64_t)B * H * L;
     const int nb = L / kChunk;
+    const float c = scale * kLog2e;
+    const dim3 grid((unsigned)((int64_t)B * H * nb));
     float *scr;
+    if (short_rows(L, d) && short_path() == kRows) {
+        float *part = nullptr;
+        if (dq && nb > 1) {
+            s = om::scratch2(ctx, sizeof(float) * (uint64_t)nb * n * d, &part);
+            if (s) return s;
+        }
+        if (L == 128)
+            hipLaunchKernelGGL(k_rows_bwd<128>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g,
+                               ld_g, o, ld_o, stats, stats + n, dk, dv, dq, ld_d, part, H, c, scale, acc);
+        else
+            hipLaunchKernelGGL(k_rows_bwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g,
+                               ld_g, o, ld_o, stats, stats + n, dk, dv, dq, ld_d, part, H, c, scale, acc);
+        if (part)
+            hipLaunchKernelGGL(k_flash_dq_reduce<32>, dim3((unsigned)((n * 8 + 255) / 256)), dim3(256), 0,
+                               ctx->stream, part, nb, n, dq, ld_d, H, L, acc);
+        return OM_LAUNCH_CHECK(ctx, "om_attention_bwd_flash");
+    }
     const uint64_t part_floats = dq ? (uint64_t)nb * n * d : 0;
     s = om::scratch2(ctx, sizeof(float) * ((uint64_t)n + 64 + part_floats), &scr);
     if (s) return s;
     float *delta = scr, *part = dq ? scr + ((n + 63) / 64) * 64 : nullptr;
     const unsigned rows_grid = (unsigned)((n * 16 + 255) / 256);
-    const dim3 grid((unsigned)((int64_t)B * H * nb));
-    const float c = scale * kLog2e;
     if (d == 64) {
         hipLaunchKernelGGL(k_flash_delta<64>, dim3(rows_grid), dim3(256), 0, ctx->stream, g, ld_g, o, ld_o, delta, H,
                            L, n);

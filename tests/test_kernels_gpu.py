@@ -534,10 +534,14 @@ def test_attention_fused_recompute(dev, T, B, H, L, D, masked, packed):
     (2, 4, 256, 32, True, True, 1),     # D = 32 beyond the whole-row kernels' 128
     (1, 2, 64, 64, True, True, 0),      # one chunk
     (3, 2, 192, 64, True, False, 1),    # three chunks, padding masks of different lengths
-], ids=["c5", "L128-d64", "L256-d32", "L64-d64", "L192-d64"])
+    (32, 12, 128, 32, True, True, 0),   # C3 at full size: the whole-row kernels, two key blocks per (batch, head)
+    (3, 2, 128, 32, False, False, 1),   # whole rows, no mask, accumulating
+    (2, 3, 64, 32, True, True, 1),      # whole rows of 64: one key block, dQ written without a reduce
+], ids=["c5", "L128-d64", "L256-d32", "L64-d64", "L192-d64", "c3", "L128-d32", "L64-d32"])
 def test_attention_flash(dev, T, B, H, L, D, masked, packed, acc):
-    """om_attention_{fwd,bwd}_flash (keys, then queries streamed through the workgroup; the forward's row statistics
-    feed the backward; dQ summed over key blocks in a fixed order) against the oracle's reference attention: O and
+    """om_attention_{fwd,bwd}_flash (keys, then queries streamed through the workgroup, or whole rows of 64 or 128 at
+    D = 32; the forward's row statistics feed the backward; dQ summed over key blocks in a fixed order) against the
+    oracle's reference attention: O and
     dQ, dK, dV within 1e-5 scaled, accumulating into existing gradients when asked; the forward's statistics are each
     row's maximum logit (log2 units) and inverse sum; and two runs give the same bits."""
     rng = np.random.default_rng(B * L + D + H + 7)
