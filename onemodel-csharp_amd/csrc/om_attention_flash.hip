@@ -201,11 +201,14 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
     const float *qg = q + (row0 + qrow) * ld + h * D;
 #pragma unroll
     for (int blk = 0; blk < DB; blk++) qf[blk] = *reinterpret_cast<const floatx4 *>(qg + 16 * blk + 4 * kl);
-    floatx4 mv[NB];  // mask of query t over keys 16 j + 4 kl + r
+    floatx4 mv[NB];  // mask of query t over keys 16 j + 4 kl + r (scaled to log2 units below)
     if (mask) {
         const float *mr = mask + b * mask_bstride + (int64_t)qrow * L + 4 * kl;
 #pragma unroll
         for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NB; j++) mv[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     // K rows: thread f takes row f / Q4, four d from (f % Q4) * 4. V^T: key f % L, four d from (f / L) * 4, so each
     // LDS store row of V^T is contiguous across the lanes; V's loads are issued once K is in LDS and arrive while
@@ -244,16 +247,12 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
     for (int j = 0; j < NB; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float x = __builtin_fmaf(s[j][r], c, mask ? mv[j][r] * kLog2e : 0.0f);
+            const float x = __builtin_fmaf(s[j][r], c, mv[j][r] * kLog2e);
             s[j][r] = x;
-            mx = x > mx ? x : mx;
+            mx = fmaxf(mx, x);  // NaN scores are skipped, as by x > mx ? x : mx
         }
-    {
-        float o2 = __shfl_xor(mx, 16, 64);
-        mx = o2 > mx ? o2 : mx;
-        o2 = __shfl_xor(mx, 32, 64);
-        mx = o2 > mx ? o2 : mx;
-    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float mu = mx == -__int_as_float(0x7F800000) ? 0.0f : mx;  // a fully masked row: l = 0, O = NaN
     float ps = 0.0f;
 #pragma unroll

@@ -212,14 +212,24 @@ __global__ void __launch_bounds__(NT) k_conv(Params p) {
     }
 }
 
-// dW = sum over slots (image-major, then K split) in order; one thread per weight.
-__global__ void k_conv_dw_reduce(const float *__restrict__ ws, int slots, int64_t total, float *__restrict__ dw,
-                                 int acc) {
-    int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
-        float v = 0.0f;
-        for (int s = 0; s < slots; s++) v += ws[(int64_t)s * total + e];
-        dw[e] = acc ? dw[e] + v : v;
+// dW = the sum over slots (image-major, then K split): a workgroup takes 64 consecutive weights (one per lane) and its
+// four wavefronts the four quarters of the slot range, each in slot order, added in order at the end.
+__global__ void __launch_bounds__(256) k_conv_dw_reduce(const float *__restrict__ ws, int slots, int64_t total,
+                                                        float *__restrict__ dw, int acc) {
+    __shared__ float qs[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int k0 = (int)((int64_t)slots * w / 4), k1 = (int)((int64_t)slots * (w + 1) / 4);
+    float v = 0.0f;
+    if (e < total) {
+#pragma unroll 8
+        for (int s = k0; s < k1; s++) v += ws[(int64_t)s * total + e];
+    }
+    qs[w][lane] = v;
+    __syncthreads();
+    if (w == 0 && e < total) {
+        const float t = ((qs[0][lane] + qs[1][lane]) + qs[2][lane]) + qs[3][lane];
+        dw[e] = acc ? dw[e] + t : t;
     }
 }
 // Wt[ci][co*KK + r] = W[co][ci][r]
@@ -243,13 +253,17 @@ __global__ void k_conv_db_planes(const float *__restrict__ g, int planes, int pl
     acc = omd::wave_sum(acc);
     if (lane == 0) part[wv] = acc;
 }
+// A wavefront per output channel: lane l adds the planes of images l, l + 64, ... in order, then the fixed butterfly.
 __global__ void k_conv_db_final(const double *__restrict__ part, int n, int cout, float *__restrict__ db, int acc) {
-    int co = blockIdx.x * blockDim.x + threadIdx.x;
-    if (co >= cout) return;
+    const int co = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6), lane = threadIdx.x & 63;
+    if (co >= cout) return;  // whole wavefronts leave together
     double s = 0.0;
-    for (int i = 0; i < n; i++) s += part[(int64_t)i * cout + co];
-    float v = (float)s;
-    db[co] = acc ? db[co] + v : v;
+    for (int i = lane; i < n; i += 64) s += part[(int64_t)i * cout + co];
+    s = omd::wave_sum(s);
+    if (lane == 0) {
+        const float v = (float)s;
+        db[co] = acc ? db[co] + v : v;
+    }
 }
 
 template <int MODE>
@@ -435,8 +449,8 @@ om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float
         double *part = reinterpret_cast<double *>(scr);
         hipLaunchKernelGGL(k_conv_db_planes, dim3(om::grid1d((int64_t)N * Cout * 64, 256, 1 << 30)), dim3(256), 0,
                            ctx->stream, g, N * Cout, P, part);
-        hipLaunchKernelGGL(k_conv_db_final, dim3((Cout + 255) / 256), dim3(256), 0, ctx->stream, part, N, Cout, db,
-                           acc_params);
+        hipLaunchKernelGGL(k_conv_db_final, dim3((unsigned)((Cout + 3) / 4)), dim3(256), 0, ctx->stream, part, N, Cout,
+                           db, acc_params);
         s = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd db");
         if (s) return s;
     }
@@ -478,7 +492,7 @@ om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float
         p.ws = ws;
         bool vec = ((uintptr_t)g % 16 == 0) && P % 4 == 0;
         launch_conv<2>(p, bm, bn, vec, ctx->stream);
-        hipLaunchKernelGGL(k_conv_dw_reduce, dim3(om::grid1d((int64_t)Cout * Kc, 256, 4096)), dim3(256), 0,
+        hipLaunchKernelGGL(k_conv_dw_reduce, dim3((unsigned)(((int64_t)Cout * Kc + 63) / 64)), dim3(256), 0,
                            ctx->stream, ws, slots, (int64_t)Cout * Kc, dw, acc_params);
         s = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
         if (s) return s;

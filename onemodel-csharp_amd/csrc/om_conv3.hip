@@ -97,18 +97,22 @@ __device__ __forceinline__ void zero_halo(float *dst, int chans, int W, int R, i
 }
 
 // out[n][co][p] (+)= bias[co] + sum_{tap, ci} wr[co][tap][ci] in[n][ci][p + shift(tap)], BM output channels per
-// workgroup. in is [N][cin][H][W], out [N][cout][H][W], wr [cout][9][cin].
+// workgroup. in is [N][cin][H][W], out [N][cout][H][W], wr [cout][9][cin]. With nsplit > 1 (few tiles: small images)
+// the input channels are cut into nsplit runs of cps chunks, one per workgroup, each writing its partial sums to
+// ws[split] ([N][cout][H][W], no bias); k_conv3_sum adds them in split order.
 template <int BM, int NS>
 __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict__ in, const float *__restrict__ wr,
                                                         const float *__restrict__ bias, float *out, int cin, int cout,
-                                                        int H, int W, int R, int ps, int ntile, int acc) {
+                                                        int H, int W, int R, int ps, int ntile, int acc, int N,
+                                                        int nsplit, int cps, float *__restrict__ ws) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
     constexpr int MB = BM / 16, NWI = (9 * BM * 2 + kThreads - 1) / kThreads;
     float *Ws = lds;                   // [9][BM][kWLd]
     float *Xs = lds + 9 * BM * kWLd;   // [kFwdCk][ps]
     const int P = H * W, rs = W + 8, ncb = cout / BM;
     const int lin = xcd_lin();
-    const int tile = lin % ntile, cb = (lin / ntile) % ncb, n = lin / ntile / ncb;
+    const int tile = lin % ntile, cb = (lin / ntile) % ncb, n = (lin / ntile / ncb) % N, split = lin / ntile / ncb / N;
+    const int c_beg = split * cps * kFwdCk, c_end = min(cin, c_beg + cps * kFwdCk);
     const int p0 = tile * kFwdPx, co0 = cb * BM, oy0 = p0 / W;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
     int boff[2];
@@ -141,15 +145,15 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
             if (wlo[i] >= 0) wv4[i] = *reinterpret_cast<const floatx4 *>(wr + wgo[i] + c0);
         xs.load(inn + (int64_t)c0 * P, H, W, oy0);
     };
-    load(0);
-    for (int c0 = 0; c0 < cin; c0 += kFwdCk) {
+    load(c_beg);
+    for (int c0 = c_beg; c0 < c_end; c0 += kFwdCk) {
         __syncthreads();  // the previous chunk's reads are done
 #pragma unroll
         for (int i = 0; i < NWI; i++)
             if (wlo[i] >= 0) *reinterpret_cast<floatx4 *>(Ws + wlo[i]) = wv4[i];
         xs.store(Xs);
         __syncthreads();
-        if (c0 + kFwdCk < cin) load(c0 + kFwdCk);  // in flight while this chunk computes
+        if (c0 + kFwdCk < c_end) load(c0 + kFwdCk);  // in flight while this chunk computes
 #pragma unroll
         for (int tap = 0; tap < 9; tap++) {
             const int toff = (tap / 3) * rs + tap % 3;
@@ -170,6 +174,18 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
         }
     }
     // lane (t, kl), register r: channel co0 + 16 i + 4 kl + r, pixel p0 + 32 w + 16 j + t
+    if (nsplit > 1) {
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float *orow = ws + (((int64_t)split * N + n) * cout + co0 + 16 * i + 4 * kl + r) * P;
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    if (pv[j]) orow[p0 + 32 * w + 16 * j + t] = accv[i][j][r];
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -185,6 +201,17 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
                 orow[p] = acc ? orow[p] + v : v;
             }
         }
+}
+
+// out (+)= the sum of the nsplit partials in split order, plus bias[co] (the unsplit kernel's arithmetic order).
+__global__ void k_conv3_sum(const float *__restrict__ ws, int nsplit, int64_t total, int P, int cout,
+                            const float *__restrict__ bias, float *out, int acc) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        float v = ws[e];
+        for (int s = 1; s < nsplit; s++) v += ws[(int64_t)s * total + e];
+        if (bias) v = v + bias[(e / P) % cout];
+        out[e] = acc ? out[e] + v : v;
+    }
 }
 
 // wr[co][tap][ci] = W[co][ci][tap] (forward); with flip, wr[ci][tap][co] = W[co][ci][8 - tap] (dX).
@@ -270,18 +297,82 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
             part[(((int64_t)slot * cout + co0 + 16 * w + 4 * kl + r) * 9 + tap) * cin + ci0 + t] = accv[tap][r];
 }
 
-// dW[co][ci][tap] (+)= sum over slots 0, 1, ... of part[slot][co][tap][ci], in that order.
-__global__ void k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout, int cin, float *dw, int acc) {
+// dW[co][ci][tap] (+)= the sum over slots of part[slot][co][tap][ci]: a workgroup takes 64 consecutive elements (one
+// per lane) and its four wavefronts the four quarters of the slot range, each summed in slot order; the quarters are
+// then added in order, so the result depends only on the shape. (Many slots per element: one thread walking them all
+// would keep too few loads in flight.)
+__global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout, int cin,
+                                                         float *dw, int acc) {
+    __shared__ float qs[4][64];
     const int64_t total = (int64_t)cout * 9 * cin;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-        float s = part[e];
-        for (int k = 1; k < slots; k++) s += part[(int64_t)k * total + e];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int k0 = (int)((int64_t)slots * w / 4), k1 = (int)((int64_t)slots * (w + 1) / 4);
+    float s = 0.0f;
+    if (e < total) {
+#pragma unroll 8
+        for (int k = k0; k < k1; k++) s += part[(int64_t)k * total + e];
+    }
+    qs[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && e < total) {
+        const float v = ((qs[0][lane] + qs[1][lane]) + qs[2][lane]) + qs[3][lane];
         const int ci = (int)(e % cin);
         const int64_t ct = e / cin;
         const int tap = (int)(ct % 9), co = (int)(ct / 9);
         float *d = dw + ((int64_t)co * cin + ci) * 9 + tap;
-        *d = acc ? *d + s : s;
+        *d = acc ? *d + v : v;
     }
+}
+
+// dW of a convolution with one input channel (the first layer of an image model): dW[co][0][tap] = sum over images
+// and pixels of g[n][co][p] x[n][0][p + shift(tap)], 9 * cout weights over N * H * W pixels. A workgroup takes one
+// image's band of `br` rows: the band's input rows with their halo go to LDS (zeros outside the image), wavefront w
+// takes output channels 8 w .. 8 w + 7 and lane j the band's pixels j, j + 64, ..., multiplying each pixel's nine
+// staged inputs by its eight g values (72 running sums per lane, in pixel order). The lanes' sums combine through the
+// fixed butterfly into part[block][co][tap]; k_conv3_dw_reduce adds the blocks in order.
+__global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ g, const float *__restrict__ x,
+                                                      float *__restrict__ part, int cout, int H, int W, int br,
+                                                      int nbands) {
+    extern __shared__ float xs[];  // [br + 2][W + 2]
+    const int n = blockIdx.x / nbands, y0 = (blockIdx.x % nbands) * br, rows = min(br, H - y0), xw = W + 2;
+    for (int f = threadIdx.x; f < (br + 2) * xw; f += blockDim.x) {
+        const int r = f / xw, c = f - r * xw, iy = y0 - 1 + r, ix = c - 1;
+        xs[f] = (r < rows + 2 && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+                    ? x[((int64_t)n * H + iy) * W + ix]
+                    : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, co0 = 8 * (threadIdx.x >> 6);
+    const int64_t P = (int64_t)H * W;
+    const float *gn = g + ((int64_t)n * cout + co0) * P + (int64_t)y0 * W;
+    float acc[8][9];
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int tap = 0; tap < 9; tap++) acc[k][tap] = 0.0f;
+    const int np = rows * W;
+    for (int q = lane; q < np; q += 64) {
+        const int r = q / W, c = q - r * W;
+        float xv[9];
+#pragma unroll
+        for (int tap = 0; tap < 9; tap++) xv[tap] = xs[(r + tap / 3) * xw + c + tap % 3];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float gv = gn[k * P + q];
+#pragma unroll
+            for (int tap = 0; tap < 9; tap++) acc[k][tap] = acc[k][tap] + gv * xv[tap];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+#pragma unroll
+        for (int tap = 0; tap < 9; tap++) {
+            float v = acc[k][tap];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+            if (lane == 0) part[((int64_t)blockIdx.x * cout + co0 + k) * 9 + tap] = v;
+        }
 }
 
 // Rows of the staged input a run of `px` flattened output pixels can touch, halo included, and the LDS plane stride
@@ -326,15 +417,34 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
         hipLaunchKernelGGL(k_conv3_wt, dim3(om::grid1d(nw, 256, 1024)), dim3(256), 0, ctx->stream, w, wr, Cout, Cin, 0);
     const int ntile = (P + kFwdPx - 1) / kFwdPx;
     const size_t lds = sizeof(float) * (9 * (size_t)BM * kWLd + (size_t)kFwdCk * ps);
-    const dim3 grid((unsigned)((int64_t)ntile * (Cout / BM) * N));
+    const int64_t tiles = (int64_t)ntile * (Cout / BM) * N;
+    // Fewer tiles than two per CU (small images): split the input channels, at least two chunks per split.
+    const int chunks = Cin / kFwdCk;
+    int nsplit = 1, cps = chunks;
+    if (tiles < 2 * ctx->num_cus && chunks >= 4) {
+        int want = (int)((2 * ctx->num_cus + tiles - 1) / tiles);
+        if (want > chunks / 2) want = chunks / 2;
+        cps = (chunks + want - 1) / want;
+        nsplit = (chunks + cps - 1) / cps;
+    }
+    float *ws = nullptr;
+    const int64_t total = (int64_t)N * Cout * P;
+    if (nsplit > 1) {
+        *st = om::scratch2(ctx, sizeof(float) * (uint64_t)nsplit * total, &ws);
+        if (*st) return true;
+    }
+    const dim3 grid((unsigned)(tiles * nsplit));
 #define OMC3(BM_, NS_)                                                                                             \
     if (BM == BM_ && ns == NS_) {                                                                                  \
         hipLaunchKernelGGL((k_conv3_fwd<BM_, NS_>), grid, dim3(kThreads), lds, ctx->stream, x, wr, bias, y, Cin, Cout, \
-                           H, W, R, ps, ntile, acc);                                                               \
+                           H, W, R, ps, ntile, acc, N, nsplit, cps, ws);                                           \
     }
     OMC3(64, 1) OMC3(64, 2) OMC3(64, 3) OMC3(64, 4) OMC3(64, 6) OMC3(64, 8)
     OMC3(32, 1) OMC3(32, 2) OMC3(32, 3) OMC3(32, 4) OMC3(32, 6) OMC3(32, 8)
 #undef OMC3
+    if (nsplit > 1)
+        hipLaunchKernelGGL(k_conv3_sum, dim3(om::grid1d(total, 256, 4096)), dim3(256), 0, ctx->stream, ws, nsplit,
+                           total, P, Cout, bias, y, acc);
     *st = OM_LAUNCH_CHECK(ctx, flip_weights ? "om_conv2d_bwd dx" : "om_conv2d_fwd");
     return true;
 }
@@ -343,6 +453,25 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, 
                  int acc, om_status *st) {
     *st = OM_OK;
     const int P = H * W;
+    if (Cin == 1 && Cout % 8 == 0 && Cout <= 128 && (int64_t)N * Cout * P <= INT32_MAX && (W + 2) * 4 <= 16384) {
+        // bands of rows: about two workgroups per CU over the images, the band's input under 64 KB of LDS
+        const int want = (int)((2LL * ctx->num_cus + N - 1) / N);
+        int nb = want < H ? want : H;
+        int br = (H + nb - 1) / nb;
+        while (br > 1 && (int64_t)(br + 2) * (W + 2) * 4 > 65536) br = (br + 1) / 2;
+        nb = (H + br - 1) / br;
+        const int blocks = N * nb;
+        float *part;
+        *st = om::scratch(ctx, sizeof(float) * (uint64_t)blocks * Cout * 9, &part);
+        if (*st) return true;
+        const size_t lds = sizeof(float) * (size_t)(br + 2) * (W + 2);
+        hipLaunchKernelGGL(k_conv3_dw_c1, dim3((unsigned)blocks), dim3(64 * (Cout / 8)), lds, ctx->stream, g, x, part,
+                           Cout, H, W, br, nb);
+        hipLaunchKernelGGL(k_conv3_dw_reduce, dim3((unsigned)((Cout * 9 + 63) / 64)), dim3(256), 0, ctx->stream,
+                           part, blocks, Cout, 1, dw, acc);
+        *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
+        return true;
+    }
     if (Cin % kDwCi || Cout % kDwCo || W % 4 || (int64_t)N * Cout * P > INT32_MAX || (int64_t)N * Cin * P > INT32_MAX)
         return false;
     int R, ps;
@@ -368,7 +497,7 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, 
     OMW3(1) OMW3(2) OMW3(3) OMW3(4) OMW3(6) OMW3(8)
 #undef OMW3
     const int64_t total = (int64_t)Cout * 9 * Cin;
-    hipLaunchKernelGGL(k_conv3_dw_reduce, dim3(om::grid1d(total, 256, 2048)), dim3(256), 0, ctx->stream, part, slots,
+    hipLaunchKernelGGL(k_conv3_dw_reduce, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, ctx->stream, part, slots,
                        Cout, Cin, dw, acc);
     *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
     return true;

@@ -2,7 +2,9 @@
 // CtcBackward, BackwardRecurrent.cs:253-296), with the reference's own fixed exp/ln/logadd (Ctc.cs:515-616).
 //
 // One workgroup per sequence. The recursions are sequential in t; within a step every extended-label position s is
-// independent, so threads own positions and meet at a barrier per step. Each value is computed by exactly the
+// independent, so threads own positions and meet at a barrier per step. The alpha (and beta) tables live in LDS when
+// they fit (T x (2L + 1) doubles each, up to 32 KB), so a step's reads of the previous one stay on chip; longer
+// sequences keep them in device scratch. Each value is computed by exactly the
 // operations of the reference in the same order (no contraction: -ffp-contract=off), so the loss, the alignment
 // sums and the gradient are bit-identical to the CPU recursions.
 #include "om_internal.hpp"
@@ -12,6 +14,7 @@
 namespace {
 
 constexpr int kBlock = 64;
+constexpr uint64_t kLdsTable = 32768;  // bytes of one alpha or beta table kept in LDS
 
 __device__ double ctc_exp(double x) {
     if (!(x > -700.0)) return 0.0;
@@ -80,24 +83,88 @@ __device__ __forceinline__ bool can_skip(const int32_t *tgt, int s) {
     return s >= 2 && (s & 1) == 1 && tgt[s >> 1] != tgt[(s >> 1) - 1];
 }
 
-// alpha[t*ext + s] for t < len (CtcLossMath.Alpha); returns nll via *nll_out from thread 0.
+// One lane's extended positions s = lane + 64 k (k < NPL) for a recursion: their labels and skip flags, read from
+// the targets once, and the log-probabilities of the current and the next time step (the next one's loads are issued
+// before the current step's arithmetic, so their latency hides behind it). BETA selects the backward recursion (the
+// skip is the one into s + 2, the steps run down from len - 1).
+template <int NPL, bool BETA>
+struct RecLane {
+    int s[NPL], lab[NPL];
+    bool ok[NPL], sk[NPL];
+    float cur[NPL], nxt[NPL];
+    __device__ __forceinline__ void init(const int32_t *tgt, int blank, int ext, int lane) {
+#pragma unroll
+        for (int k = 0; k < NPL; k++) {
+            s[k] = lane + 64 * k;
+            ok[k] = s[k] < ext;
+            lab[k] = ok[k] ? label_at(tgt, blank, s[k]) : 0;
+            sk[k] = ok[k] && (BETA ? (s[k] + 2 < ext && can_skip(tgt, s[k] + 2)) : can_skip(tgt, s[k]));
+        }
+    }
+    __device__ __forceinline__ void fetch(float (&dst)[NPL], const float *lp, int B, int C, int b, int t) {
+#pragma unroll
+        for (int k = 0; k < NPL; k++) dst[k] = ok[k] ? lp[((int64_t)t * B + b) * C + lab[k]] : 0.0f;
+    }
+    // Step t of the recursion into table[t * ext + s] from row `from` (t - 1 for alpha, t + 1 for beta), with the
+    // reference's operations in its order.
+    __device__ __forceinline__ void step(double *table, int ext, int t, bool first) {
+        const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
+        const double *prev = table + (BETA ? t + 1 : t - 1) * ext;
+#pragma unroll
+        for (int k = 0; k < NPL; k++) {
+            if (!ok[k]) continue;
+            const int p = s[k];
+            double a;
+            if (first) {
+                a = BETA ? (p >= ext - 2 ? 0.0 : NEG) : (p <= 1 ? 0.0 : NEG);
+            } else if (BETA) {
+                a = prev[p];
+                if (p + 1 < ext) a = ctc_logadd(a, prev[p + 1]);
+                if (sk[k]) a = ctc_logadd(a, prev[p + 2]);
+            } else {
+                a = prev[p];
+                if (p >= 1) a = ctc_logadd(a, prev[p - 1]);
+                if (sk[k]) a = ctc_logadd(a, prev[p - 2]);
+            }
+            table[t * ext + p] = is_neg_inf(a) ? NEG : a + (double)cur[k];
+        }
+    }
+};
+
+// alpha[t*ext + s] for t < len (CtcLossMath.Alpha) by the 64 threads of the workgroup; returns nll via *nll_out from
+// thread 0. NPL positions per lane (ext <= 64 NPL); NPL = 0 walks any ext without the per-lane state.
+template <int NPL>
 __device__ void alpha_pass(const float *lp, int B, int C, int b, int len, const int32_t *tgt, int L, int blank,
                            double *alpha, double *nll_out) {
     const int ext = 2 * L + 1;
     const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
-    for (int t = 0; t < len; t++) {
-        for (int s = threadIdx.x; s < ext; s += blockDim.x) {
-            double a;
-            if (t == 0) {
-                a = s <= 1 ? 0.0 : NEG;
-            } else {
-                a = alpha[(t - 1) * ext + s];
-                if (s >= 1) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 1]);
-                if (can_skip(tgt, s)) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 2]);
-            }
-            alpha[t * ext + s] = is_neg_inf(a) ? NEG : a + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+    if constexpr (NPL > 0) {
+        RecLane<NPL, false> rl;
+        rl.init(tgt, blank, ext, threadIdx.x);
+        if (len > 0) rl.fetch(rl.cur, lp, B, C, b, 0);
+        for (int t = 0; t < len; t++) {
+            if (t + 1 < len) rl.fetch(rl.nxt, lp, B, C, b, t + 1);
+            rl.step(alpha, ext, t, t == 0);
+#pragma unroll
+            for (int k = 0; k < NPL; k++) rl.cur[k] = rl.nxt[k];
+            __syncthreads();
         }
-        __syncthreads();
+    } else {
+        for (int t = 0; t < len; t++) {
+            for (int s = threadIdx.x; s < ext; s += blockDim.x) {
+                double a;
+                if (t == 0) {
+                    a = s <= 1 ? 0.0 : NEG;
+                } else {
+                    a = alpha[(t - 1) * ext + s];
+                    if (s >= 1) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 1]);
+                    if (can_skip(tgt, s)) a = ctc_logadd(a, alpha[(t - 1) * ext + s - 2]);
+                }
+                alpha[t * ext + s] =
+                    is_neg_inf(a) ? NEG : a + (double)lp[((int64_t)t * B + b) * C + label_at(tgt, blank, s)];
+            }
+            __syncthreads();
+        }
     }
     if (threadIdx.x == 0) {
         double nll;
@@ -117,13 +184,18 @@ __global__ void __launch_bounds__(kBlock) k_ctc_fwd(const float *__restrict__ lp
                                                     const int32_t *__restrict__ in_len,
                                                     const int32_t *__restrict__ tgt_len, int T, int B, int C, int blank,
                                                     int max_ext, double *__restrict__ alpha_ws,
-                                                    double *__restrict__ per) {
+                                                    double *__restrict__ per, int in_lds) {
     __shared__ double nll;
+    extern __shared__ double tables[];
     int b = blockIdx.x;
     int off = 0;
     for (int i = 0; i < b; i++) off += tgt_len[i];
-    double *alpha = alpha_ws + (int64_t)b * (T > 0 ? T : 1) * max_ext;
-    alpha_pass(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
+    double *alpha = in_lds ? tables : alpha_ws + (int64_t)b * (T > 0 ? T : 1) * max_ext;
+    const int ext = 2 * tgt_len[b] + 1;
+    if (ext <= 64) alpha_pass<1>(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
+    else if (ext <= 128) alpha_pass<2>(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
+    else if (ext <= 256) alpha_pass<4>(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
+    else alpha_pass<0>(lp, B, C, b, in_len[b], targets + off, tgt_len[b], blank, alpha, &nll);
     if (threadIdx.x == 0) per[b] = nll;
 }
 // Reduction in sequence order (CtcLoss.cs:98-125).
@@ -140,6 +212,37 @@ __global__ void k_ctc_reduce(const double *__restrict__ per, const int32_t *__re
     if (reduction != 0) loss[0] = (float)(reduction == 1 ? sum / B : sum);
 }
 
+// The alpha (wavefront 0, t up) and beta (wavefront 1, t down) recursions of one sequence side by side, one barrier
+// per step for the whole workgroup.
+template <int NPL>
+__device__ void recursions(const float *lp, int B, int C, int b, int len, const int32_t *tgt, int blank, int ext,
+                           double *alpha, double *beta, int wave, int lane) {
+    RecLane<NPL, false> ra;
+    RecLane<NPL, true> rb;
+    if (wave == 0) {
+        ra.init(tgt, blank, ext, lane);
+        if (len > 0) ra.fetch(ra.cur, lp, B, C, b, 0);
+    } else if (wave == 1) {
+        rb.init(tgt, blank, ext, lane);
+        if (len > 0) rb.fetch(rb.cur, lp, B, C, b, len - 1);
+    }
+    for (int i = 0; i < len; i++) {
+        if (wave == 0) {
+            if (i + 1 < len) ra.fetch(ra.nxt, lp, B, C, b, i + 1);
+            ra.step(alpha, ext, i, i == 0);
+#pragma unroll
+            for (int k = 0; k < NPL; k++) ra.cur[k] = ra.nxt[k];
+        } else if (wave == 1) {
+            const int t = len - 1 - i;
+            if (t > 0) rb.fetch(rb.nxt, lp, B, C, b, t - 1);
+            rb.step(beta, ext, t, i == 0);
+#pragma unroll
+            for (int k = 0; k < NPL; k++) rb.cur[k] = rb.nxt[k];
+        }
+        __syncthreads();
+    }
+}
+
 // CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence, in two phases. First the alpha recursion (recomputed, as
 // the reference recomputes it) and the beta recursion run side by side on two wavefronts, alpha forward and beta
 // backward in t, one barrier per step (each lane owns extended positions s, s + 64, ...). Then every (t, class)
@@ -151,8 +254,10 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
                                                        const int32_t *__restrict__ in_len,
                                                        const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
                                                        float *__restrict__ dlp, int T, int B, int C, int blank,
-                                                       int reduction, int max_ext, int acc, double *__restrict__ ws) {
+                                                       int reduction, int max_ext, int acc, double *__restrict__ ws,
+                                                       int in_lds) {
     __shared__ double nll_s;
+    extern __shared__ double tables[];
     const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
     const int b = blockIdx.x;
     const int len = in_len[b], L = tgt_len[b];
@@ -160,11 +265,14 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
     for (int i = 0; i < b; i++) off += tgt_len[i];
     const int32_t *tgt = targets + off;
     const int tt = T > 0 ? T : 1;
-    double *alpha = ws + (int64_t)b * 2 * tt * max_ext;
+    double *alpha = in_lds ? tables : ws + (int64_t)b * 2 * tt * max_ext;
     double *beta = alpha + (int64_t)tt * max_ext;
     const int ext = 2 * L + 1;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int i = 0; i < len; i++) {
+    if (ext <= 64) recursions<1>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
+    else if (ext <= 128) recursions<2>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
+    else if (ext <= 256) recursions<4>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
+    else for (int i = 0; i < len; i++) {
         if (wave == 0) {
             const int t = i;
             for (int s = lane; s < ext; s += 64) {
@@ -278,13 +386,15 @@ om_status om_ctc_fwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
                              &max_ext);
     if (s) return s;
     float *scr;
-    uint64_t need = sizeof(double) * ((uint64_t)B * (T > 0 ? T : 1) * max_ext + B);
+    const uint64_t table = sizeof(double) * (uint64_t)(T > 0 ? T : 1) * max_ext;
+    const bool in_lds = table <= kLdsTable;
+    uint64_t need = sizeof(double) * B + (in_lds ? 0 : table * B);
     s = om::scratch(ctx, need, &scr);
     if (s) return s;
-    double *alpha = reinterpret_cast<double *>(scr);
-    double *per = alpha + (uint64_t)B * (T > 0 ? T : 1) * max_ext;
-    hipLaunchKernelGGL(k_ctc_fwd, dim3(B), dim3(kBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, T, B, C, blank,
-                       max_ext, alpha, per);
+    double *per = reinterpret_cast<double *>(scr);
+    double *alpha = in_lds ? nullptr : per + B;
+    hipLaunchKernelGGL(k_ctc_fwd, dim3(B), dim3(kBlock), in_lds ? table : 0, ctx->stream, lp, targets, in_len, tgt_len,
+                       T, B, C, blank, max_ext, alpha, per, in_lds ? 1 : 0);
     hipLaunchKernelGGL(k_ctc_reduce, dim3(1), dim3(64), 0, ctx->stream, per, tgt_len, B, reduction, zero_infinity,
                        loss);
     return OM_LAUNCH_CHECK(ctx, "om_ctc_fwd");
@@ -300,12 +410,17 @@ om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
     om_status s = check_args(ctx, "om_ctc_bwd", h_in_len, h_tgt_len, h_targets, n_targets, T, B, C, blank, reduction,
                              &max_ext);
     if (s) return s;
-    float *scr;
+    float *scr = nullptr;
     uint64_t tt = T > 0 ? T : 1;
-    s = om::scratch(ctx, sizeof(double) * 2ull * B * tt * max_ext, &scr);
-    if (s) return s;
-    hipLaunchKernelGGL(k_ctc_bwd, dim3(B), dim3(kBwdBlock), 0, ctx->stream, lp, targets, in_len, tgt_len, g, dlp, T, B, C,
-                       blank, reduction, max_ext, accumulate, reinterpret_cast<double *>(scr));
+    const uint64_t table = sizeof(double) * tt * max_ext;  // one of the two tables
+    const bool in_lds = table <= kLdsTable;
+    if (!in_lds) {
+        s = om::scratch(ctx, 2 * table * B, &scr);
+        if (s) return s;
+    }
+    hipLaunchKernelGGL(k_ctc_bwd, dim3(B), dim3(kBwdBlock), in_lds ? 2 * table : 0, ctx->stream, lp, targets, in_len,
+                       tgt_len, g, dlp, T, B, C, blank, reduction, max_ext, accumulate,
+                       reinterpret_cast<double *>(scr), in_lds ? 1 : 0);
     return OM_LAUNCH_CHECK(ctx, "om_ctc_bwd");
 }
 

@@ -348,6 +348,15 @@ bool env_override(Choice &c, int k) {
     c = with_splits(bm, bn, bk, k, sp);
     return true;
 }
+// Tile order of the grouped weight gradients: bands of OM_GROUP_BAND tile rows walked column by column (0:
+// row-major), for comparison runs.
+int group_band() {
+    static const int b = [] {
+        const char *s = std::getenv("OM_GROUP_BAND");
+        return s && *s ? atoi(s) : 0;
+    }();
+    return b;
+}
 bool x_disabled() {
     static const char *s = std::getenv("OM_GEMM_X");
     return s && !strcmp(s, "off");
@@ -373,11 +382,12 @@ Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bo
                 return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
     const bool n96 = n % 96 == 0 && m >= 64;
     int64_t tiles = (int64_t)((m + 63) / 64) * (n96 ? n / 96 : (n + 63) / 64) * batch;
-    // A handful of tiles over a long-enough K (an MLP's first layer: 4 tiles over K = 784) leaves most CUs idle:
-    // split K into slices of at least 128 k until there are about as many workgroups as CUs / 2.
-    if (batch == 1 && 8 * tiles <= cus && k >= 512) {
+    // A handful of tiles over a long-enough K (an MLP's first layer: 4 tiles over K = 784) leaves most CUs idle, and
+    // each workgroup's chunks then follow one another at memory latency: split K into slices of at least 64 k until
+    // there are about as many workgroups as CUs / 2.
+    if (batch == 1 && 8 * tiles <= cus && k >= 256) {
         int s = 1;
-        while (s < 16 && k / (2 * s) >= 128 && tiles * 2 * s <= cus / 2) s *= 2;
+        while (s < 16 && k / (2 * s) >= 64 && tiles * 2 * s <= cus / 2) s *= 2;
         if (s > 1) return with_splits(64, 64, 32, k, s);
     }
     if (batch == 1 && tiles < 2 * cus && k >= 1024) {
@@ -392,16 +402,17 @@ Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bo
 }
 
 // Thin products (one side at most 32: a classifier head's weight gradient, 9 x 768 over K = 4096 tokens) take the
-// 128 x 32 / 32 x 128 tiles; like the square ones they split a long K when their tiles leave CUs idle (slices of at
-// least 256 k, or 128 k when K is short).
+// 128 x 32 / 32 x 128 tiles. Products with fewer tiles than CUs (the classifier heads, small batches) split K into
+// slices of at least 32 k, up to about one workgroup per CU: their time is the chain of chunk loads each workgroup
+// waits for, not arithmetic.
 Choice choose(int m, int n, int k, int batch, int cus) {
     Choice c{64, 64, 1, k, 16};
     if (n <= 32) c = Choice{128, 32, 1, k, 16};
     else if (m <= 32) c = Choice{32, 128, 1, k, 16};
     int64_t tiles = (int64_t)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn) * batch;
-    if (batch == 1 && tiles < cus && k >= 512) {
+    if (batch == 1 && tiles < cus && k >= 64) {
         int want = (int)((cus + tiles - 1) / tiles);
-        int maxs = k >= 1024 ? k / 256 : k / 128;
+        int maxs = k / 32;
         int s = want < maxs ? want : maxs;
         if (s > 1) {
             int ks = ((k + s - 1) / s + 15) / 16 * 16;
@@ -542,6 +553,7 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
     const int k_split = rows / splits;
     GroupParams g{};
     g.count = count;
+    g.band = group_band();
     uint64_t ws_floats = 0, cs_doubles = 0;
     for (int i = 0; i < count; i++) {
         const om_linear_dw &d = it[i];

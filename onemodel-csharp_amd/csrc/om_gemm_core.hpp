@@ -100,6 +100,7 @@ struct GroupParams {
     ColSumItem cs[kMaxColSums];
     int cstart[kMaxColSums + 1];
     int ncs;
+    int band;  // tile order inside a (product, split): bands of `band` tile rows walked column by column; 0: row-major
 };
 
 // The epilogue of one finished dot product v at (row, col): alpha, mask, bias, residual, GELU terms, then C. The

@@ -533,6 +533,16 @@ __global__ void __launch_bounds__(NT) k_gemm_x_tn_group(GroupParams g) {
         if (j < g.count && lin >= g.start[j]) i = j;
     const Params &p = g.p[i];
     const int local = lin - g.start[i], tiles_n = p.n / BN, tiles_m = p.m / BM;
+    if (g.band > 0) {
+        // Within a split: bands of `band` tile rows (the last band may be shorter), each walked one tile column at a
+        // time with the band's rows fastest, so the workgroups that run together on one XCD share few operand slabs.
+        const int per = tiles_m * tiles_n, split = local / per, idx = local % per;
+        const int bh = g.band < tiles_m ? g.band : tiles_m;
+        const int band = idx / (bh * tiles_n), r0 = band * bh, rows = min(bh, tiles_m - r0);
+        const int within = idx - r0 * tiles_n;
+        gemm_x_tile<BM, BN, BKT, true, false, false>(p, r0 + within % rows, within / rows, split);
+        return;
+    }
     const int rest = local / tiles_n;
     gemm_x_tile<BM, BN, BKT, true, false, false>(p, rest % tiles_m, local % tiles_n, rest / tiles_m);
 }

@@ -203,6 +203,7 @@ struct Input {
     int32_t lo = INT32_MIN, hi_bound = INT32_MAX;  // int inputs: the values the model accepts, [lo, hi_bound)
     float *home_data = nullptr;                    // the input's own device buffer (a staged batch replaces it
     int32_t *home_idata = nullptr;                 // for one step)
+    std::vector<int32_t> home_hi;                  // int inputs: the own host copy while a staged batch is active
     void set_range(int32_t l, int32_t h) {
         lo = l;
         hi_bound = h;
@@ -571,6 +572,7 @@ struct omt_model {
             Input &in = inputs[i];
             if (in.is_int) {
                 in.t->idata = reinterpret_cast<int32_t *>(st.dev + batch_off[i]);
+                in.home_hi = std::move(in.hi);
                 in.hi = std::move(st.ints[k++]);
             } else {
                 in.t->data = reinterpret_cast<float *>(st.dev + batch_off[i]);
@@ -585,8 +587,12 @@ struct omt_model {
         const int slot = active_slot;
         active_slot = -1;
         for (Input &in : inputs) {
-            if (in.is_int) in.t->idata = in.home_idata;
-            else in.t->data = in.home_data;
+            if (in.is_int) {
+                in.t->idata = in.home_idata;
+                in.hi = std::move(in.home_hi);  // the host copy matches the device buffer it points at again
+            } else {
+                in.t->data = in.home_data;
+            }
         }
         check(device->ctx(), om_stager_release(stager, slot), "om_stager_release");
     }
@@ -974,7 +980,8 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
             Tensor f = mean_axis(h, 2);        // [B, 256, T]
             Tensor seq = permute(f, {2, 0, 1});  // [T, B, 256]
             Tensor lp = log_softmax((*mp->head)(seq));
-            return ctc_loss(lp, s.input("labels").hi, s.input("in_len").hi, s.input("tgt_len").hi, 0, 1);
+            const Input &lb = s.input("labels"), &il = s.input("in_len"), &tl = s.input("tgt_len");
+            return ctc_loss(lp, lb.hi, il.hi, tl.hi, 0, 1, lb.t, il.t, tl.t);
         };
     } else if (cfg == 5) {
         const int B = pick(sc.batch, 8), L = pick(sc.seq, 512), NL = pick(sc.layers, 4), D = 768, H = 12, F = 3072;

@@ -787,17 +787,22 @@ Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw) {
 }
 
 Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std::vector<int32_t> &in_len,
-                const std::vector<int32_t> &tgt_len, int blank, int reduction) {
+                const std::vector<int32_t> &tgt_len, int blank, int reduction, const Tensor &d_targets,
+                const Tensor &d_in_len, const Tensor &d_tgt_len) {
     if (lp->shape.size() != 3) shape_error("CtcLoss needs log-probabilities [T,B,C], not " + shape_str(lp->shape));
     const int T = lp->shape[0], B = lp->shape[1], Cc = lp->shape[2];
     if ((int)in_len.size() != B || (int)tgt_len.size() != B)
         shape_error("Expected " + std::to_string(B) + " input and target lengths");
-    int32_t *dt = dev().step_ints((int64_t)targets.size());
-    int32_t *dil = dev().step_ints(B);
-    int32_t *dtl = dev().step_ints(B);
-    OMT(om_upload(C(), dt, targets.data(), sizeof(int32_t) * targets.size()));
-    OMT(om_upload(C(), dil, in_len.data(), sizeof(int32_t) * (uint64_t)B));
-    OMT(om_upload(C(), dtl, tgt_len.data(), sizeof(int32_t) * (uint64_t)B));
+    const int32_t *dt = d_targets ? d_targets->idata : nullptr, *dil = d_in_len ? d_in_len->idata : nullptr,
+                  *dtl = d_tgt_len ? d_tgt_len->idata : nullptr;
+    auto upload = [&](const std::vector<int32_t> &h) {
+        int32_t *d = dev().step_ints((int64_t)h.size());
+        OMT(om_upload(C(), d, h.data(), sizeof(int32_t) * h.size()));
+        return d;
+    };
+    if (!dt) dt = upload(targets);
+    if (!dil) dil = upload(in_len);
+    if (!dtl) dtl = upload(tgt_len);
     Tensor loss = reduction == 0 ? make({B}) : make({});
     OMT(om_ctc_fwd(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(), (int)targets.size(), T,
                    B, Cc, blank, reduction, 0, loss->data));
@@ -807,7 +812,7 @@ Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std
             float *d = e.dest(r, 0, &a);
             OMT(om_ctc_bwd(C(), r.inputs[0]->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
                            (int)targets.size(), g, d, T, B, Cc, blank, reduction, a));
-        }, {lp});
+        }, {lp, d_targets, d_in_len, d_tgt_len});
     }
     return loss;
 }

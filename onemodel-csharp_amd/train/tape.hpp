@@ -208,8 +208,12 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels);  // Losses.Cro
 Tensor mse(const Tensor &pred, const Tensor &target);              // Losses.Mse: Mean((pred-target)^2)
 Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad);
 Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw);
+// The int arrays on the host; d_* are optional int tensors holding the same values on the device (a model's int
+// inputs keep such a copy), which spare the step three uploads from pageable memory. They are saved for the backward
+// like any tensor it reads, so an in-place write between forward and backward fails that backward.
 Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std::vector<int32_t> &in_len,
-                const std::vector<int32_t> &tgt_len, int blank, int reduction);
+                const std::vector<int32_t> &tgt_len, int blank, int reduction, const Tensor &d_targets = nullptr,
+                const Tensor &d_in_len = nullptr, const Tensor &d_tgt_len = nullptr);
 // Ops.AvgPool2d (Ops.Layers.cs:405-455), square window k, stride s, padding p.
 Tensor avg_pool2d(const Tensor &x, int k, int s, int p, bool count_include_pad = true);
 // Ops.BatchNorm2d (Ops.Layers.cs:158-246) with the module's running statistics (device, [C], updated in training).

@@ -710,6 +710,15 @@ def ctc_cases():
     tl[1] = 5
     labels = rng.integers(1, Cc, int(tl.sum())).astype(np.int32)
     yield "c4", lp, labels, il, tl
+    # long sequences: T x (2 L + 1) doubles beyond what the kernels keep in LDS (4096), so alpha and beta live in
+    # device scratch
+    Tn, B, Cc = 160, 3, 12
+    z = rng.standard_normal((Tn, B, Cc)).astype(np.float32)
+    lp = (z - np.log(np.exp(z.astype(np.float64)).sum(-1, keepdims=True))).astype(np.float32)
+    tl = np.array([30, 12, 40], np.int32)
+    il = np.array([Tn, 100, Tn], np.int32)
+    labels = rng.integers(1, Cc, int(tl.sum())).astype(np.int32)
+    yield "long", lp, labels, il, tl
 
 
 @pytest.mark.parametrize("red", [0, 1, 2])

@@ -70,6 +70,24 @@ def test_saved_tensor_written_in_place_fails_the_backward(pkg, how):
         m.close()
 
 
+def test_ctc_labels_written_between_forward_and_backward(pkg):
+    """The CTC loss reads the model's label and length inputs from their device copies, and saves them for the
+    backward like the log-probabilities: rewriting the labels between forward and backward fails that backward."""
+    m = pkg.Model(4, batch=4)
+    try:
+        ins = m.inputs()
+        m.forward()
+        m.write_input("labels", ins["labels"])
+        with pytest.raises(pkg.OmError) as e:
+            m.backward()
+        assert e.value.code == OMT_E_TENSOR_VERSION
+        a = m.forward_backward()
+        b = m.forward_backward()
+        assert a == b
+    finally:
+        m.close()
+
+
 def test_write_to_an_unsaved_tensor_is_not_a_version_error(pkg):
     """The first layer's bias enters through Add, which saves nothing (BackwardOps.cs Add rule), so rewriting it
     between forward and backward is allowed, as in the reference."""
