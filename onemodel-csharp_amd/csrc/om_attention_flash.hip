@@ -470,9 +470,10 @@ __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ 
 // all L queries in one pass. One workgroup per batch item, head and 64 keys (a wavefront per 16 keys), so a
 // (batch, head) pair is L / 64 workgroups and the 384 pairs of a C3 step fill the chip evenly (three workgroups per
 // CU). In order:
-//   1. Q and dO rows (all L queries), this block's K rows, the queries' m and 1/l into LDS; this lane's K and V row
-//      fragments into registers (the B operands of S = Q K^T and dP = dO V^T);
-//   2. delta = rowsum(dO * O) per query, a product per element summed in double over d;
+//   1. this block's K rows, the queries' m and 1/l and the first 64 queries' Q and dO rows into LDS; this lane's K and
+//      V row fragments into registers (the B operands of S = Q K^T and dP = dO V^T);
+//   2. per phase of 64 queries (the next phase's Q, dO and O rows load meanwhile): delta = rowsum(dO * O) of its
+//      queries, a product per element summed in double over d, then
 //   3. per block of 16 queries: S and dP on MFMA, P = 2^(x - m) / l, dS = P (dP - delta) scale, and at once
 //      dV^T += dO^T P and dK^T += Q^T dS, whose B operands are the P and dS registers just computed (the A operands
 //      read dO and Q two d at a time: row t of dV^T's A is d = 2t + db, so a lane's outputs are eight consecutive d);
@@ -488,8 +489,9 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
                                                      float *dk, float *dv, float *dq, int ldd,
                                                      float *__restrict__ dq_part, int H, float c, float scale,
                                                      int acc) {
-    constexpr int D = 32, LDX = D + 4, NQB = L / 16, Q4 = D / 4, PERQ = L * Q4 / 256, PERK = kChunk * Q4 / 256;
-    constexpr int TPQ = 256 / L, DPT = D / TPQ;  // threads per query and d per thread for delta
+    constexpr int D = 32, LDX = D + 4, NQB = L / 16, Q4 = D / 4, PERK = kChunk * Q4 / 256;
+    constexpr int RP = 64, NPH = L / RP, PERP = RP * Q4 / 256;  // queries per phase, phases, float4 per thread
+    constexpr int TPQ = 256 / RP, DPT = D / TPQ;  // threads per query and d per thread for delta
     static_assert(L == 64 || L == 128, "whole rows of 64 or 128 queries");
     static_assert(L * LDSC <= 2 * L * LDX, "dS [L][68] fits where Q and dO were");
     __shared__ __attribute__((aligned(16))) float QG[2 * L * LDX];  // Q [q][d] and dO [q][d]; later dS [q][key]
@@ -510,35 +512,54 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
             vf[blk] = *reinterpret_cast<const floatx4 *>(vr + 16 * blk + 4 * kl);
         }
     }
-    // 1. every load first, then the LDS stores
+    // 1. This block's K rows, the statistics and the first phase's rows (queries 0 .. 63: Q, dO, and O for delta)
+    // into LDS; each later phase's rows load while the previous phase computes.
     const int tid = threadIdx.x;
-    floatx4 qx[PERQ], gx[PERQ], kx[PERK], ox[DPT / 4];
+    floatx4 qx[PERP], gx[PERP], kx[PERK], ox[DPT / 4];
     const float *qg = q + row0 * ld + h * D, *gg = g + row0 * ldg + h * D;
+    const int dq_q = tid / TPQ, dq_d0 = (tid % TPQ) * DPT;  // delta: this thread's query in a phase, first d
+    auto load_rows = [&](int ph) {
 #pragma unroll
-    for (int i = 0; i < PERQ; i++) {
-        const int f = tid + 256 * i;
-        qx[i] = *reinterpret_cast<const floatx4 *>(qg + (int64_t)(f / Q4) * ld + (f % Q4) * 4);
-        gx[i] = *reinterpret_cast<const floatx4 *>(gg + (int64_t)(f / Q4) * ldg + (f % Q4) * 4);
-    }
+        for (int i = 0; i < PERP; i++) {
+            const int f = tid + 256 * i, row = ph * RP + f / Q4;
+            qx[i] = *reinterpret_cast<const floatx4 *>(qg + (int64_t)row * ld + (f % Q4) * 4);
+            gx[i] = *reinterpret_cast<const floatx4 *>(gg + (int64_t)row * ldg + (f % Q4) * 4);
+        }
+        const float *orow = o + (row0 + ph * RP + dq_q) * ldo + h * D + dq_d0;
+#pragma unroll
+        for (int e = 0; e < DPT / 4; e++) ox[e] = *reinterpret_cast<const floatx4 *>(orow + 4 * e);
+    };
+    auto store_rows = [&](int ph) {
+#pragma unroll
+        for (int i = 0; i < PERP; i++) {
+            const int f = tid + 256 * i, row = ph * RP + f / Q4;
+            *reinterpret_cast<floatx4 *>(&Qs[row * LDX + (f % Q4) * 4]) = qx[i];
+            *reinterpret_cast<floatx4 *>(&Gs[row * LDX + (f % Q4) * 4]) = gx[i];
+        }
+    };
+    // delta = rowsum(dO * O) of the phase's queries, each a product per element summed in double over d
+    auto delta = [&](int ph) {
+        const int qq = ph * RP + dq_q;
+        double dot = 0.0;
+#pragma unroll
+        for (int e = 0; e < DPT / 4; e++) {
+            const floatx4 gv = *reinterpret_cast<const floatx4 *>(&Gs[qq * LDX + dq_d0 + 4 * e]);
+#pragma unroll
+            for (int x = 0; x < 4; x++) dot += (double)(gv[x] * ox[e][x]);
+        }
+#pragma unroll
+        for (int off = 1; off < TPQ; off <<= 1) dot += __shfl_xor(dot, off, 64);
+        if (tid % TPQ == 0) St[2][qq] = (float)dot;
+    };
+    load_rows(0);
 #pragma unroll
     for (int i = 0; i < PERK; i++) {
         const int f = tid + 256 * i;
         kx[i] = *reinterpret_cast<const floatx4 *>(k + (row0 + key0 + f / Q4) * ld + h * D + (f % Q4) * 4);
     }
-    const int dq_q = tid / TPQ, dq_d0 = (tid % TPQ) * DPT;  // delta: this thread's query and first d
-    {
-        const float *orow = o + (row0 + dq_q) * ldo + h * D + dq_d0;
-#pragma unroll
-        for (int e = 0; e < DPT / 4; e++) ox[e] = *reinterpret_cast<const floatx4 *>(orow + 4 * e);
-    }
     float stv = 0.0f;
     if (tid < 2 * L) stv = (tid < L ? stat_m : stat_r)[bh * L + tid % L];
-#pragma unroll
-    for (int i = 0; i < PERQ; i++) {
-        const int f = tid + 256 * i;
-        *reinterpret_cast<floatx4 *>(&Qs[(f / Q4) * LDX + (f % Q4) * 4]) = qx[i];
-        *reinterpret_cast<floatx4 *>(&Gs[(f / Q4) * LDX + (f % Q4) * 4]) = gx[i];
-    }
+    store_rows(0);
 #pragma unroll
     for (int i = 0; i < PERK; i++) {
         const int f = tid + 256 * i;
@@ -546,22 +567,9 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
     }
     if (tid < 2 * L) St[tid / L][tid % L] = stv;
     __syncthreads();
-    // 2. delta
-    {
-        double dot = 0.0;
-#pragma unroll
-        for (int e = 0; e < DPT / 4; e++) {
-            const floatx4 gv = *reinterpret_cast<const floatx4 *>(&Gs[dq_q * LDX + dq_d0 + 4 * e]);
-#pragma unroll
-            for (int x = 0; x < 4; x++) dot += (double)(gv[x] * ox[e][x]);
-        }
-#pragma unroll
-        for (int off = 1; off < TPQ; off <<= 1) dot += __shfl_xor(dot, off, 64);
-        if (tid % TPQ == 0) St[2][dq_q] = (float)dot;
-    }
-    __syncthreads();
-    // 3. S, dP, P, dS per block of 16 queries; dV^T and dK^T accumulate over all L queries. The mask values of block
-    // i + 1 (this lane's key at queries 16 (i + 1) + 4 kl + r) are loaded while block i runs.
+    // 2, 3. Per phase: delta of its queries; then per block of 16 queries S, dP, P, dS, with dV^T and dK^T accumulating
+    // over all L queries. The mask values of block i + 1 (this lane's key at queries 16 (i + 1) + 4 kl + r) load while
+    // block i runs.
     const float *mbase = mask ? mask + b * mask_bstride + mykey : nullptr;
     float mkc[4], mkn[4];
     auto mask_load = [&](float(&dst)[4], int i) {
@@ -574,39 +582,50 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
 #pragma unroll
     for (int db = 0; db < 2; db++) dvt[db] = dkt[db] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < NQB; i++) {
-        if (i + 1 < NQB) mask_load(mkn, i + 1);
-        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int ph = 0; ph < NPH; ph++) {
+        delta(ph);
+        __syncthreads();
+        if (ph + 1 < NPH) load_rows(ph + 1);  // in flight during this phase's blocks
 #pragma unroll
-        for (int blk = 0; blk < 2; blk++) {
-            const floatx4 a = *reinterpret_cast<const floatx4 *>(&Qs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
-            const floatx4 ga = *reinterpret_cast<const floatx4 *>(&Gs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
+        for (int ii = 0; ii < RP / 16; ii++) {
+            const int i = ph * (RP / 16) + ii;
+            if (i + 1 < NQB) mask_load(mkn, i + 1);
+            floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int blk = 0; blk < 2; blk++) {
+                const floatx4 a = *reinterpret_cast<const floatx4 *>(&Qs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
+                const floatx4 ga = *reinterpret_cast<const floatx4 *>(&Gs[(16 * i + t) * LDX + 16 * blk + 4 * kl]);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    s = mfma4(a[u], kf[blk][u], s);
+                    dp = mfma4(ga[u], vf[blk][u], dp);
+                }
+            }
+            const floatx4 mq = *reinterpret_cast<const floatx4 *>(&St[0][16 * i + 4 * kl]);
+            const floatx4 rq = *reinterpret_cast<const floatx4 *>(&St[1][16 * i + 4 * kl]);
+            const floatx4 dl = *reinterpret_cast<const floatx4 *>(&St[2][16 * i + 4 * kl]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float p = exp2_hw(__builtin_fmaf(s[r], c, mkc[r] * kLog2e) - mq[r]) * rq[r];
+                s[r] = p;
+                dp[r] = (p * (dp[r] - dl[r])) * scale;
+                mkc[r] = mkn[r];
+            }
+            dsv[i] = dp;
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                s = mfma4(a[u], kf[blk][u], s);
-                dp = mfma4(ga[u], vf[blk][u], dp);
+                const int qq = 16 * i + 4 * kl + u;
+                const float2 gv = *reinterpret_cast<const float2 *>(&Gs[qq * LDX + 2 * t]);
+                const float2 qv = *reinterpret_cast<const float2 *>(&Qs[qq * LDX + 2 * t]);
+                dvt[0] = mfma4(gv.x, s[u], dvt[0]);
+                dvt[1] = mfma4(gv.y, s[u], dvt[1]);
+                dkt[0] = mfma4(qv.x, dp[u], dkt[0]);
+                dkt[1] = mfma4(qv.y, dp[u], dkt[1]);
             }
         }
-        const floatx4 mq = *reinterpret_cast<const floatx4 *>(&St[0][16 * i + 4 * kl]);
-        const floatx4 rq = *reinterpret_cast<const floatx4 *>(&St[1][16 * i + 4 * kl]);
-        const floatx4 dl = *reinterpret_cast<const floatx4 *>(&St[2][16 * i + 4 * kl]);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float p = exp2_hw(__builtin_fmaf(s[r], c, mkc[r] * kLog2e) - mq[r]) * rq[r];
-            s[r] = p;
-            dp[r] = (p * (dp[r] - dl[r])) * scale;
-            mkc[r] = mkn[r];
-        }
-        dsv[i] = dp;
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int qq = 16 * i + 4 * kl + u;
-            const float2 gv = *reinterpret_cast<const float2 *>(&Gs[qq * LDX + 2 * t]);
-            const float2 qv = *reinterpret_cast<const float2 *>(&Qs[qq * LDX + 2 * t]);
-            dvt[0] = mfma4(gv.x, s[u], dvt[0]);
-            dvt[1] = mfma4(gv.y, s[u], dvt[1]);
-            dkt[0] = mfma4(qv.x, dp[u], dkt[0]);
-            dkt[1] = mfma4(qv.y, dp[u], dkt[1]);
+        if (ph + 1 < NPH) {
+            store_rows(ph + 1);  // rows no block of this phase reads
+            __syncthreads();
         }
     }
     __syncthreads();  // every wavefront is done with Q and dO
