@@ -303,15 +303,15 @@ om_status om_attention_fwd_fused(om_ctx *ctx, const float *q, const float *k, co
 om_status om_attention_bwd_fused(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
                                  const float *mask, int mask_batched, const float *g, int ld_g, float *dq, float *dk,
                                  float *dv, int ld_d, int B, int H, int L, int d, float scale, int acc);
-/* The same pair for longer sequences, with the forward's row statistics kept for the backward (the reference keeps
- * nothing and recomputes, BackwardNn.cs:636-701): the forward streams keys through the workgroup in chunks of 64
- * (online softmax) and writes O and stats (2 * B * H * L floats: each query's row maximum, in log2 units, then the
- * inverse row sum); the backward streams queries, recomputes P = 2^(x - max) / sum from the statistics, takes
+/* The same pair with the forward's row statistics kept for the backward (the reference keeps nothing and
+ * recomputes, BackwardNn.cs:636-701): the forward writes O and stats (2 * B * H * L floats: each query's row maximum,
+ * in log2 units, then the inverse row sum); the backward recomputes P = 2^(x - max) / sum from the statistics, takes
  * delta = rowsum(dO * O) from the forward's output o, and never writes a [B, H, L, L] tensor (dQ partials per block
- * of 64 keys go through context scratch and are summed in key-block order, so results are deterministic). Taken for
- * D in {32, 64} and L a multiple of 64 with 16-byte aligned rows, except D = 32 with L <= 128, which the whole-row
- * kernels of the _fused entry points handle; other shapes run those entry points instead (the forward then leaves
- * stats unwritten and the backward recomputes). Results agree with the reference within its fp32 sums (1e-5). */
+ * of 64 keys go through context scratch and are summed in key-block order, so results are deterministic). For D = 32
+ * and L in {64, 128} the kernels hold whole rows; for D in {32, 64} and longer L (a multiple of 64) they stream keys
+ * (forward, online softmax) and queries (backward) through the workgroup in chunks of 64. Rows must be 16-byte
+ * aligned; other shapes run the _fused entry points instead (the forward then leaves stats unwritten and the
+ * backward recomputes). Results agree with the reference within its fp32 sums (1e-5). */
 om_status om_attention_fwd_flash(om_ctx *ctx, const float *q, const float *k, const float *v, int ld_qkv,
                                  const float *mask, int mask_batched, float *o, int ld_o, float *stats, int B, int H,
                                  int L, int d, float scale);
