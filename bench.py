@@ -611,6 +611,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="time the step without step graphs only")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches a counter run needs (no timing line)")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only the C3 products beside torch.mm (hipBLASLt / rocBLAS), as a markdown table")
@@ -627,15 +628,31 @@ def main():
         pmc_probe(pkg, model)
         model.close()
         return
-    for _ in range(a.warmup):
-        model.step()
-    pkg.load_hip().om_ctx_sync(model.ctx)
-    t0 = time.perf_counter()
-    loss = None
-    for _ in range(a.steps):
-        loss = model.step()  # each step returns once its loss has landed on the host
-    pkg.load_hip().om_ctx_sync(model.ctx)
-    el = time.perf_counter() - t0
+    def timed_window():
+        for _ in range(a.warmup):
+            model.step()
+        pkg.load_hip().om_ctx_sync(model.ctx)
+        t0 = time.perf_counter()
+        last = None
+        for _ in range(a.steps):
+            last = model.step()  # each step returns once its loss has landed on the host
+        pkg.load_hip().om_ctx_sync(model.ctx)
+        return time.perf_counter() - t0, last
+
+    # The step as the tape runs it launch by launch, then (unless --no-graph) the same step recorded once into a
+    # HIP graph and replayed (omt_set_step_graph; bit-identical results): the headline is the graph's rate.
+    el_eager, loss = timed_window()
+    el, el_graph = el_eager, None
+    if not a.no_graph:
+        model.set_step_graph(True)
+        el_graph, loss_g = timed_window()
+        if not model.step_graph_ready:
+            raise SystemExit(f"bench.py: C{a.config} did not run from a step graph")
+        if el_graph < el_eager:
+            el, loss = el_graph, loss_g
+        else:
+            model.set_step_graph(False)
+    graphed = el_graph is not None and el == el_graph
     sps = a.steps / el
     # per-step device times: HIP events on the model's stream after each step, over at least 50 further steps
     # (a separate pass, so the events do not touch the timed window above)
@@ -650,6 +667,12 @@ def main():
         "step_ms": {"median": round(q(0.5), 4), "p10": round(q(0.1), 4), "p90": round(q(0.9), 4), "n": len(per),
                     "median_steps_per_s": round(1000.0 / q(0.5), 3), "timing": "hipEvent per step"},
         "final_loss": loss,
+        "mode": "step graph" if graphed else "eager",
+        "modes": {"eager": round(a.steps / el_eager, 3),
+                  "step_graph": round(a.steps / el_graph, 3) if el_graph else None,
+                  "note": "steps/s of the same step launched kernel by kernel from the host tape (eager) and "
+                          "replayed from a recorded HIP graph (omt_set_step_graph); the results are bit-identical, "
+                          "value is the faster of the two"},
     }
     if a.config == 3:
         out["pcie_inclusive"] = time_staged(pkg, model, a.steps)

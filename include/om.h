@@ -98,6 +98,36 @@ om_status om_readback_destroy(om_readback *r);
 om_status om_readback_post(om_readback *r, const void *src_device, uint64_t bytes);
 om_status om_readback_wait(om_readback *r, void *dst_host, uint64_t bytes);
 
+/* ---------------------------------------------------------------------------------------------- step graphs */
+/* A training step as one HIP graph: between om_graph_capture_begin and om_graph_capture_end the launches a caller
+ * queues on the context's stream are recorded instead of run, and om_graph_launch replays them as one submission
+ * (a step of small launches is bound by the host's per-launch cost otherwise).
+ * Recorded launches keep the arguments they were recorded with (pointers, sizes, flags), except the values that
+ * change from step to step, which the graph's kernels read from device memory that the graph's first node fills
+ * from the om_step_values given to each om_graph_launch: the rate and Adam's two bias-correction scalars of
+ * om_adam_step / om_adam_step_scaled (their by-value lr, step_size and sqrt_bc2 are ignored inside a capture, and
+ * 1 - lr * weight_decay is formed on the device with the same float rounding), and the sequence number of the
+ * capture's one readback post (om_readback_post or om_mse_fwd_post; om_graph_launch advances the readback as a
+ * post would, so om_readback_wait works as after an eager post). A caller captures again whenever anything else
+ * it passed would change.
+ * Inside a capture, calls that would wait for the device or read host memory when the graph runs fail with
+ * OM_E_STATE and leave the capture unusable (abort it): om_upload, om_download, om_ctx_sync, om_sgd_step (its rate
+ * and first-step flag are host values), the stager calls, a second readback object, and growth of the context's
+ * scratch (run one step outside a capture first, so scratch and arena have their steady size).
+ * om_graph_launch waits, if need be, until the previous launch of the same graph has read its values.
+ * No counterpart in the reference, whose step runs on the CPU (TrainCase.cs:114-127). */
+typedef struct om_graph om_graph;
+typedef struct {
+    float lr, step_size, sqrt_bc2; /* as passed to om_adam_step for the step (om_adam_scalars) */
+} om_step_values;
+om_status om_graph_capture_begin(om_ctx *ctx);
+om_status om_graph_capture_end(om_ctx *ctx, om_graph **out);
+/* Ends a capture without a graph (after a failed call inside it); the stream runs launches again. */
+om_status om_graph_capture_abort(om_ctx *ctx);
+om_status om_graph_launch(om_graph *g, const om_step_values *v);
+/* Waits for the graph's launches, then frees it. */
+om_status om_graph_destroy(om_graph *g);
+
 /* ---------------------------------------------------------------------------------------------- GEMM */
 /* C[m,n] = op(A)[m,k] * op(B)[k,n] (+ bias[n]) on fp32 MFMA, for `batch` independent products. Row-major operands
  * with leading dimensions lda/ldb/ldc; trans_a means A is stored [k,m], trans_b means B is stored [n,k].

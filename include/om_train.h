@@ -47,6 +47,16 @@ const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors *
  * with the backward and the update queued behind it on the model's stream (omt_ctx). Every later call that touches
  * the model's memory is ordered after them; om_ctx_sync(omt_ctx(m)) waits for them. */
 om_status omt_step(omt_model *m, float *loss);
+/* Step graphs (om_graph_*, include/om.h) for omt_step: with `on`, the next omt_step runs as usual, the one after it
+ * is recorded into a HIP graph and launched, and later ones replay that graph, with only the host-side effects of
+ * a step (rate from the schedule, step count, parameter versions) done on the host; results are bit-identical to
+ * omt_step without graphs. The graph is dropped and recorded again after omt_set_optimizer, omt_set_clip,
+ * omt_checkpoint_load, omt_batch_commit (staged steps run without a graph), and omt_input_write of an input whose
+ * host copy the step reads (configuration 4's lengths and labels). SGD and dropout models always run without one.
+ * No counterpart in the reference (its step runs on the CPU); for callers whose step is bound by launch overhead. */
+om_status omt_set_step_graph(omt_model *m, int on);
+/* 1 when the next omt_step will replay a recorded graph. */
+int omt_step_graph_ready(omt_model *m);
 /* ZeroGrad, forward and backward only (gradients are left in the arena). */
 om_status omt_forward_backward(omt_model *m, float *loss);
 /* The same two halves as separate calls, for callers that act between them: omt_forward runs ZeroGrad and the

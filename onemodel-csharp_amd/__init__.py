@@ -102,6 +102,11 @@ _OM_SIGS = {
     "om_readback_destroy": [vp],
     "om_readback_post": [vp, vp, u64],
     "om_readback_wait": [vp, vp, u64],
+    "om_graph_capture_begin": [vp],
+    "om_graph_capture_end": [vp, C.POINTER(vp)],
+    "om_graph_capture_abort": [vp],
+    "om_graph_launch": [vp, vp],
+    "om_graph_destroy": [vp],
     "om_stager_destroy": [vp],
     "om_stager_slot_bytes": [vp],
     "om_stager_begin": [vp, C.POINTER(vp), C.POINTER(ci)],
@@ -179,6 +184,8 @@ _OMT_SIGS = {
     "omt_destroy": ([vp], None),
     "omt_last_error": ([vp], C.c_char_p),
     "omt_step": ([vp, C.POINTER(f32)], i32),
+    "omt_set_step_graph": ([vp, ci], i32),
+    "omt_step_graph_ready": ([vp], ci),
     "omt_forward_backward": ([vp, C.POINTER(f32)], i32),
     "omt_forward": ([vp, C.POINTER(f32)], i32),
     "omt_backward": ([vp], i32),
@@ -276,6 +283,15 @@ class Model:
         v = f32()
         self._check(self.L.omt_step(self.h, C.byref(v)), "omt_step")
         return v.value
+
+    def set_step_graph(self, on: bool = True):
+        """Runs later step() calls from a recorded HIP graph of the step (omt_set_step_graph)."""
+        self._check(self.L.omt_set_step_graph(self.h, int(bool(on))), "omt_set_step_graph")
+
+    @property
+    def step_graph_ready(self) -> bool:
+        """True when the next step() replays a recorded graph."""
+        return bool(self.L.omt_step_graph_ready(self.h))
 
     def forward_backward(self) -> float:
         v = f32()

@@ -1,6 +1,7 @@
 // Context, arena and host<->device copies of libom_hip.so.
 #include "om_internal.hpp"
 
+#include <atomic>
 #include <cstring>
 #include <mutex>
 
@@ -31,11 +32,19 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what) {
     return fail(ctx, e == hipErrorOutOfMemory ? OM_E_OOM : OM_E_DEVICE, "%s: %s", what, hipGetErrorString(e));
 }
 
+om_status refuse_in_capture(om_ctx *ctx, const char *what) {
+    if (!ctx->cap) return OM_OK;
+    return fail(ctx, OM_E_STATE, "%s: not possible inside a step-graph capture (it would wait for the device or read "
+                "host memory when the graph runs)", what);
+}
+
 static om_status grow(om_ctx *ctx, float *&buf, uint64_t &have, uint64_t bytes, float **out, const char *what) {
     if (bytes <= have) {
         *out = buf;
         return OM_OK;
     }
+    // Growth synchronises the stream, which a capture cannot hold; a step run once outside the capture has grown it.
+    if (om_status s = refuse_in_capture(ctx, "context scratch growth")) return s;
     // No kernel may still use the old buffer.
     om_status s = check_hip(ctx, hipStreamSynchronize(ctx->stream), "scratch sync");
     if (s) return s;
@@ -69,7 +78,7 @@ static om_status add_slab(om_ctx *ctx, om_region &r, uint64_t bytes) {
 
 extern "C" {
 
-int om_abi_version(void) { return 100; }
+int om_abi_version(void) { return 101; }
 
 om_status om_ctx_create(int device, om_ctx **out) {
     if (!out) return om::fail(nullptr, OM_E_ARG, "om_ctx_create: out is NULL");
@@ -106,6 +115,7 @@ om_status om_ctx_create(int device, om_ctx **out) {
 om_status om_ctx_destroy(om_ctx *ctx) {
     OM_CHECK_CTX(ctx);
     (void)hipSetDevice(ctx->device);
+    if (ctx->cap) (void)om_graph_capture_abort(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     for (auto &r : ctx->region)
         for (auto &s : r.slabs) (void)hipFree(s.base);
@@ -118,6 +128,7 @@ om_status om_ctx_destroy(om_ctx *ctx) {
 
 om_status om_ctx_sync(om_ctx *ctx) {
     OM_CHECK_CTX(ctx);
+    if (om_status s = om::refuse_in_capture(ctx, "om_ctx_sync")) return s;
     return om::check_hip(ctx, hipStreamSynchronize(ctx->stream), "om_ctx_sync");
 }
 
@@ -200,6 +211,7 @@ om_status om_upload(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst && src, "om_upload: NULL pointer");
+    if (om_status s = om::refuse_in_capture(ctx, "om_upload")) return s;
     // Pageable host memory: the copy is staged by the runtime and completes before the call returns.
     return om::check_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "om_upload");
 }
@@ -208,6 +220,7 @@ om_status om_download(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
     OM_CHECK_CTX(ctx);
     if (bytes == 0) return OM_OK;
     OM_REQUIRE(ctx, dst && src, "om_download: NULL pointer");
+    if (om_status s = om::refuse_in_capture(ctx, "om_download")) return s;
     om_status s = om::check_hip(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "om_download");
     if (s) return s;
     return om::check_hip(ctx, hipStreamSynchronize(ctx->stream), "om_download sync");
@@ -250,3 +263,151 @@ extern "C" om_status om_zero(om_ctx *ctx, void *dst, uint64_t bytes) {
                        (unsigned char *)dst, (int64_t)bytes);
     return OM_LAUNCH_CHECK(ctx, "om_zero");
 }
+
+// ------------------------------------------------------------------------------------------------ step graphs
+namespace {
+
+// The graph's first node: copies the values the host wrote for this launch into device memory for the later nodes,
+// then tells the host the entry may be overwritten (the launch number into the ack word). The entry is read as two
+// 16-byte loads (one PCIe round trip; the memory is fine-grained, so nothing is cached on the way), and the ack is
+// stored only after both have returned (s_waitcnt on every counter), so the host never overwrites an entry that is
+// still being read. No system-scope fence: the later nodes read `dev` in stream order, and the host needs only the
+// ack word itself.
+__global__ void k_step_begin(const om_step_block *entry, om_step_block *dev, uint64_t *ack) {
+    if (threadIdx.x != 0) return;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(entry);
+    const u32x4 lo = __builtin_nontemporal_load(src), hi = __builtin_nontemporal_load(src + 1);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(dev);
+    dst[0] = lo;
+    dst[1] = hi;
+    __builtin_amdgcn_s_waitcnt(0);
+    const uint64_t id = (uint64_t)hi.z | ((uint64_t)hi.w << 32);  // om_step_block::id
+    __hip_atomic_store(ack, id, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+om_step_block *entry_of(om_graph *g) { return reinterpret_cast<om_step_block *>(g->host); }
+volatile uint64_t *ack_of(om_graph *g) { return reinterpret_cast<volatile uint64_t *>(g->host + sizeof(om_step_block)); }
+
+void free_graph(om_graph *g) {
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    if (g->dev) (void)hipFree(g->dev);
+    if (g->host) (void)hipHostFree(g->host);
+    delete g;
+}
+
+}  // namespace
+
+extern "C" {
+
+om_status om_graph_capture_begin(om_ctx *ctx) {
+    OM_CHECK_CTX(ctx);
+    if (ctx->cap) return om::fail(ctx, OM_E_STATE, "om_graph_capture_begin: a capture is already running");
+    om_graph *g = new om_graph;
+    g->ctx = ctx;
+    // Fine-grained (coherent) pinned memory: the first node reads what the host wrote just before the launch, and
+    // the host polls the ack the node writes, with no cache in between.
+    hipError_t e = hipHostMalloc((void **)&g->host, 64, hipHostMallocCoherent);
+    if (e == hipSuccess) e = hipMalloc((void **)&g->dev, sizeof(om_step_block));
+    if (e != hipSuccess) {
+        free_graph(g);
+        return om::check_hip(ctx, e, "om_graph_capture_begin");
+    }
+    std::memset(g->host, 0, 64);
+    e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+        free_graph(g);
+        return om::check_hip(ctx, e, "om_graph_capture_begin");
+    }
+    ctx->cap = g;
+    hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(64), 0, ctx->stream, (const om_step_block *)g->host, g->dev,
+                       (uint64_t *)(g->host + sizeof(om_step_block)));
+    om_status s = OM_LAUNCH_CHECK(ctx, "om_graph_capture_begin");
+    if (s) {
+        std::string msg = ctx->err;
+        (void)om_graph_capture_abort(ctx);
+        ctx->err = msg;
+    }
+    return s;
+}
+
+om_status om_graph_capture_abort(om_ctx *ctx) {
+    OM_CHECK_CTX(ctx);
+    om_graph *g = ctx->cap;
+    if (!g) return OM_OK;
+    ctx->cap = nullptr;
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(ctx->stream, &partial);
+    if (partial) (void)hipGraphDestroy(partial);
+    (void)hipGetLastError();
+    free_graph(g);
+    return OM_OK;
+}
+
+om_status om_graph_capture_end(om_ctx *ctx, om_graph **out) {
+    OM_CHECK_CTX(ctx);
+    if (!ctx->cap) return om::fail(ctx, OM_E_STATE, "om_graph_capture_end: no capture is running");
+    if (!out) {
+        (void)om_graph_capture_abort(ctx);
+        return om::fail(ctx, OM_E_ARG, "om_graph_capture_end: out is NULL");
+    }
+    *out = nullptr;
+    om_graph *g = ctx->cap;
+    ctx->cap = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        free_graph(g);
+        return om::check_hip(ctx, e, "om_graph_capture_end");
+    }
+    *out = g;
+    return OM_OK;
+}
+
+om_status om_graph_launch(om_graph *g, const om_step_values *v) {
+    if (!g || !v) return OM_E_ARG;
+    om_ctx *ctx = g->ctx;
+    if (ctx->cap) return om::fail(ctx, OM_E_STATE, "om_graph_launch: a capture is running on the stream");
+    // The entry is reused: the previous launch's first node must have read it (it normally has: the host waited for
+    // that launch's loss, which comes later in the graph).
+    for (uint64_t n = 1; *ack_of(g) != g->launches; n++) {
+        if (n % 256) continue;
+        hipError_t e = hipStreamQuery(ctx->stream);
+        if (e == hipErrorNotReady) continue;
+        if (e != hipSuccess) return om::check_hip(ctx, e, "om_graph_launch");
+        if (*ack_of(g) != g->launches) return om::fail(ctx, OM_E_DEVICE, "om_graph_launch: the previous launch did not start");
+    }
+    uint64_t seq = 0;
+    if (g->rb) {
+        // The readback's previous post (eager or graph) must have landed before its buffer is written again.
+        char *dst;
+        uint64_t *seq_at;
+        const uint64_t *seq_dev;
+        om_status s = om::readback_target(ctx, g->rb, g->rb_bytes, &dst, &seq_at, &seq, &seq_dev);
+        if (s) return s;
+    }
+    om_step_block *entry = entry_of(g);
+    entry->lr = v->lr;
+    entry->step_size = v->step_size;
+    entry->sqrt_bc2 = v->sqrt_bc2;
+    entry->pad = 0.0f;
+    entry->seq = seq;
+    entry->id = g->launches + 1;
+    std::atomic_thread_fence(std::memory_order_seq_cst);
+    om_status s = om::check_hip(ctx, hipGraphLaunch(g->exec, ctx->stream), "om_graph_launch");
+    if (s) return s;
+    g->launches++;
+    if (g->rb) om::readback_posted(g->rb, seq, g->rb_bytes);
+    return OM_OK;
+}
+
+om_status om_graph_destroy(om_graph *g) {
+    if (!g) return OM_OK;
+    om_status s = om::check_hip(g->ctx, hipStreamSynchronize(g->ctx->stream), "om_graph_destroy");
+    free_graph(g);
+    return s;
+}
+
+}  // extern "C"

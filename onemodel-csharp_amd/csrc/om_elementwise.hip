@@ -109,12 +109,13 @@ __global__ void __launch_bounds__(kBlock) k_sum_partial(const float *__restrict_
     double t = omd::block_sum<kBlock / 64>(acc, sh);
     if (threadIdx.x == 0) part[blockIdx.x] = t;
 }
-// Optionally also posts the result to a readback buffer as k_readback does: the value, a system-scope fence, then
-// the sequence number.
+// Optionally also posts the result to a readback buffer as k_readback does: the value as a system-scope
+// write-through store, a wait for its completion, then the sequence number (no L2 write-back).
 struct PostTo {
     char *dst;
     uint64_t *seq_at;
     uint64_t seq;
+    const uint64_t *seq_dev;  // inside a step graph: the number is read here when the kernel runs
 };
 __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ part, int np, float *__restrict__ out,
                                                   double divisor, PostTo post) {
@@ -125,9 +126,10 @@ __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ par
         const float v = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;
         out[0] = v;
         if (post.dst) {
-            *reinterpret_cast<float *>(post.dst) = v;
-            __threadfence_system();
-            *reinterpret_cast<volatile uint64_t *>(post.seq_at) = post.seq;
+            __hip_atomic_store(reinterpret_cast<float *>(post.dst), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(post.seq_at, post.seq_dev ? *post.seq_dev : post.seq, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 }
@@ -310,9 +312,9 @@ static om_status mse_fwd(om_ctx *ctx, const float *pred, const float *target, fl
     if (s) return s;
     double *part = reinterpret_cast<double *>(scr);
     const int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
-    PostTo post{nullptr, nullptr, 0};
+    PostTo post{nullptr, nullptr, 0, nullptr};
     if (rb) {
-        s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq);
+        s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq, &post.seq_dev);
         if (s) return s;
     }
     hipLaunchKernelGGL(k_mse_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, pred, target, diff, n, part, unit);

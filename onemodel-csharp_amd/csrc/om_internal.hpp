@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
+#include <cstddef>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -40,6 +41,29 @@ struct om_ctx {
     // (looked up once per device at context creation; NULL if that failed).
     void *noalloc_scratch = nullptr;
     int num_cus = 256;
+    // The step graph being captured on the stream (om_graph_capture_begin .. _end), else NULL.
+    struct om_graph *cap = nullptr;
+};
+
+// The per-step values a step graph's kernels read (om_step_values plus the readback's sequence number and the
+// launch number), 32 bytes.
+struct om_step_block {
+    float lr, step_size, sqrt_bc2, pad;
+    uint64_t seq, id;
+};
+static_assert(sizeof(om_step_block) == 32 && offsetof(om_step_block, id) == 24, "k_step_begin reads it as 2 x 16 B");
+
+struct om_graph {
+    om_ctx *ctx = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    // Pinned, fine-grained host memory: [entry the host writes before a launch][ack the graph's first node writes
+    // after reading the entry]. `dev` is device memory the first node copies the entry into for the later nodes.
+    char *host = nullptr;
+    om_step_block *dev = nullptr;
+    uint64_t launches = 0;
+    om_readback *rb = nullptr;  // the capture's readback post, if any
+    uint64_t rb_bytes = 0;
 };
 
 namespace om {
@@ -54,12 +78,17 @@ om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
 // Sets ctx->noalloc_scratch to the device address of the fixed scratch array on ctx->device (the current device),
 // looking it up on the first call for that device only.
 om_status noalloc_init(om_ctx *ctx);
+// OM_E_STATE with a message when a step graph is being captured on ctx's stream (for calls a graph cannot hold).
+om_status refuse_in_capture(om_ctx *ctx, const char *what);
 // The stream every launch of the context goes to.
 inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->stream; }
 // A readback post written by another entry point's kernel: checks that r belongs to ctx and holds `bytes`, waits for
 // the previous post's copy (the pinned buffer is reused), and returns the device addresses of the buffer and of its
-// sequence word with the sequence number the post carries; readback_posted records the launched post.
-om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq);
+// sequence word with the sequence number the post carries; readback_posted records the launched post. Inside a
+// step-graph capture nothing is waited for, *seq_dev is the device word the kernel must read the number from (else
+// NULL), and the post is registered with the graph, whose launches advance the readback.
+om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq,
+                          const uint64_t **seq_dev);
 void readback_posted(om_readback *r, uint64_t seq, uint64_t bytes);
 // out[col] (+)= (float) sum over c < chunks of part[c * cols + col], in double, a wavefront per column; a second
 // (part2, out2) pair of the same shape is reduced in the same launch when given.

@@ -38,10 +38,19 @@ __device__ __forceinline__ void adam_one(float &p, float g, float &m, float &v, 
 
 // gs (may be NULL): a device-side gradient coefficient, applied as g * c when c < 1 — GradClip.ClipNorm's in-place
 // scaling (Schedules.cs:70-76) folded into the update's read of g, with the same single float rounding.
+// step (may be NULL): inside a step graph, the step's rate and bias-correction scalars, read when the kernel runs;
+// the decoupled decay factor is then formed here with the host's float rounding, 1 - lr * wd.
 __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const float *__restrict__ g,
                                                  float *__restrict__ m, float *__restrict__ v,
                                                  float *__restrict__ vmax, int64_t n, AdamArgs a,
-                                                 const float *__restrict__ gs) {
+                                                 const float *__restrict__ gs,
+                                                 const om_step_block *__restrict__ step) {
+    if (step) {
+        a.lr = step->lr;
+        a.step_size = step->step_size;
+        a.sqrt_bc2 = step->sqrt_bc2;
+        a.decay = 1.0f - a.lr * a.wd;
+    }
     const float c = gs ? *gs : 1.0f;
     const bool sc = c < 1.0f;
     int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -130,7 +139,9 @@ static om_status adam_launch(om_ctx *ctx, const char *what, float *p, const floa
     a.decoupled = decoupled;
     // Enough waves to cover HBM latency on 256 CUs, grid-stride beyond that.
     unsigned grid = om::grid1d((n + 3) / 4, kBlock, (int64_t)ctx->num_cus * 8);
-    hipLaunchKernelGGL(k_adam, dim3(grid), dim3(kBlock), 0, ctx->stream, p, g, m, v, vmax, n, a, grad_scale);
+    // Inside a step-graph capture the per-step scalars come from the graph's device block (om_graph_launch).
+    const om_step_block *step = ctx->cap ? ctx->cap->dev : nullptr;
+    hipLaunchKernelGGL(k_adam, dim3(grid), dim3(kBlock), 0, ctx->stream, p, g, m, v, vmax, n, a, grad_scale, step);
     return OM_LAUNCH_CHECK(ctx, what);
 }
 
@@ -156,6 +167,7 @@ om_status om_sgd_step(om_ctx *ctx, float *p, const float *g, float *buf, int64_t
     OM_REQUIRE(ctx, n >= 0, "om_sgd_step: negative length");
     if (n == 0) return OM_OK;
     OM_REQUIRE(ctx, p && g, "om_sgd_step: NULL pointer");
+    if (om_status st = om::refuse_in_capture(ctx, "om_sgd_step")) return st;
     hipLaunchKernelGGL(k_sgd, dim3(om::grid1d(n, kBlock, (int64_t)ctx->num_cus * 8)), dim3(kBlock), 0, ctx->stream, p,
                        g, buf, n, lr, momentum, 1.0f - dampening, weight_decay, nesterov, first);
     return OM_LAUNCH_CHECK(ctx, "om_sgd_step");

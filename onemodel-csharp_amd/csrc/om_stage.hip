@@ -137,12 +137,14 @@ om_status om_stager_commit(om_stager *s, int slot, uint64_t bytes, void **device
 
 om_status om_stager_acquire(om_stager *s, int slot) {
     if (!valid_slot(s, slot)) return OM_E_ARG;
+    if (om_status st = om::refuse_in_capture(s->ctx, "om_stager_acquire")) return st;
     return om::check_hip(s->ctx, hipStreamWaitEvent(s->ctx->stream, s->uploaded[slot], 0), "om_stager_acquire");
 }
 
 om_status om_stager_release(om_stager *s, int slot) {
     if (!valid_slot(s, slot)) return OM_E_ARG;
     om_ctx *ctx = s->ctx;
+    if (om_status st = om::refuse_in_capture(ctx, "om_stager_release")) return st;
     om_status st = om::check_hip(ctx, hipEventRecord(s->consumed[slot], ctx->stream), "om_stager_release");
     if (st) return st;
     s->consume_pending[slot] = 1;
@@ -170,13 +172,19 @@ namespace {
 
 constexpr uint64_t kReadbackMax = 64 << 10;
 
-// Copies n bytes to dst, then, once every thread's stores are visible system-wide, writes seq after the data.
+// Copies n bytes to dst, then, once every thread's stores have completed, writes seq after the data. The stores are
+// system-scope write-through stores (global_store sc0 sc1) into the fine-grained host buffer and each thread waits
+// for its own before the barrier, so the sequence number cannot overtake the data; no L2 write-back or invalidate
+// is needed, which a system-scope fence would do to the whole L2 of the workgroup's XCD in the middle of a step.
+// Inside a step graph the number is read from seq_dev when the kernel runs.
 __global__ void __launch_bounds__(256) k_readback(char *__restrict__ dst, const char *__restrict__ src, uint64_t n,
-                                                  uint64_t *seq_at, uint64_t seq) {
-    for (uint64_t i = threadIdx.x; i < n; i += 256) dst[i] = src[i];
-    __threadfence_system();
+                                                  uint64_t *seq_at, uint64_t seq, const uint64_t *seq_dev) {
+    for (uint64_t i = threadIdx.x; i < n; i += 256)
+        __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) *reinterpret_cast<volatile uint64_t *>(seq_at) = seq;
+    if (threadIdx.x == 0)
+        __hip_atomic_store(seq_at, seq_dev ? *seq_dev : seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 volatile uint64_t *seq_host(const om_readback *r) {
@@ -202,9 +210,23 @@ om_status await(om_readback *r) {
 
 namespace om {
 
-om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq) {
+om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **dst, uint64_t **seq_at, uint64_t *seq,
+                          const uint64_t **seq_dev) {
     OM_REQUIRE(ctx, r && r->ctx == ctx, "readback post: the readback belongs to another context");
     OM_REQUIRE(ctx, bytes > 0 && bytes <= r->bytes, "readback post: need 1 .. %llu bytes", (unsigned long long)r->bytes);
+    *seq_dev = nullptr;
+    if (om_graph *g = ctx->cap) {
+        // Recorded into a step graph: each launch of the graph posts, with the number om_graph_launch assigns.
+        if (g->rb && g->rb != r)
+            return om::fail(ctx, OM_E_STATE, "readback post: a step graph holds one readback, this is a second one");
+        g->rb = r;
+        g->rb_bytes = bytes;
+        *dst = r->host_dev;
+        *seq_at = reinterpret_cast<uint64_t *>(r->host_dev + (r->bytes + 7) / 8 * 8);
+        *seq = 0;
+        *seq_dev = &g->dev->seq;
+        return OM_OK;
+    }
     // The pinned buffer may still be the target of the previous post.
     if (r->posted) {
         om_status st = await(r);
@@ -217,6 +239,7 @@ om_status readback_target(om_ctx *ctx, om_readback *r, uint64_t bytes, char **ds
 }
 
 void readback_posted(om_readback *r, uint64_t seq, uint64_t bytes) {
+    if (r->ctx->cap) return;  // recorded, not run: om_graph_launch advances the readback
     r->seq = seq;
     r->posted = bytes;
 }
@@ -235,7 +258,8 @@ om_status om_readback_create(om_ctx *ctx, uint64_t bytes, om_readback **out) {
     r->ctx = ctx;
     r->bytes = bytes;
     const uint64_t total = (bytes + 7) / 8 * 8 + sizeof(uint64_t);
-    hipError_t e = hipHostMalloc((void **)&r->host, total, hipHostMallocDefault);
+    // Fine-grained: the device's write-through stores land in host memory without a cache flush.
+    hipError_t e = hipHostMalloc((void **)&r->host, total, hipHostMallocCoherent);
     if (e == hipSuccess) e = hipHostGetDevicePointer((void **)&r->host_dev, r->host, 0);
     if (e != hipSuccess) {
         if (r->host) (void)hipHostFree(r->host);
@@ -262,10 +286,11 @@ om_status om_readback_post(om_readback *r, const void *src, uint64_t bytes) {
     OM_REQUIRE(ctx, src, "om_readback_post: NULL source");
     char *dst;
     uint64_t *seq_at, seq;
-    om_status st = om::readback_target(ctx, r, bytes, &dst, &seq_at, &seq);
+    const uint64_t *seq_dev;
+    om_status st = om::readback_target(ctx, r, bytes, &dst, &seq_at, &seq, &seq_dev);
     if (st) return st;
     hipLaunchKernelGGL(k_readback, dim3(1), dim3(256), 0, ctx->stream, dst, static_cast<const char *>(src), bytes,
-                       seq_at, seq);
+                       seq_at, seq, seq_dev);
     st = OM_LAUNCH_CHECK(ctx, "om_readback_post");
     if (st) return st;
     om::readback_posted(r, seq, bytes);

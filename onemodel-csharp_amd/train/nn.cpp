@@ -4,6 +4,7 @@
 #include <cstring>
 #include <deque>
 #include <map>
+#include <utility>
 
 #include "checkpoint.hpp"
 #include "om_train.h"
@@ -204,6 +205,7 @@ struct Input {
     float *home_data = nullptr;                    // the input's own device buffer (a staged batch replaces it
     int32_t *home_idata = nullptr;                 // for one step)
     std::vector<int32_t> home_hi;                  // int inputs: the own host copy while a staged batch is active
+    bool host_read = false;  // the step's launches take arguments from the host copy (a new value needs a new graph)
     void set_range(int32_t l, int32_t h) {
         lo = l;
         hi_bound = h;
@@ -257,6 +259,15 @@ struct omt_model {
     // The loss of the last omt_forward, kept for omt_backward; its records are released by that backward, so a second
     // omt_backward runs through a released graph (Engine.cs:136-141). Dropped at the next step's start.
     Tensor graph_loss;
+    // Step graphs (om_graph_*): with graph_on, omt_step runs one step as usual, captures the next into a HIP graph
+    // (launched at once) and replays that graph afterwards, doing on the host only what a step changes there. Dropped
+    // (captured again) when something a recorded launch depends on changes; never used with SGD (host-valued rate
+    // and first-step flags), dropout (a new mask seed every step) or staged batches (new input addresses).
+    bool graph_on = false;
+    bool has_dropout = false;
+    om_graph *graph = nullptr;
+    int graph_warm = 0;          // steps run outside a graph since the graph was last dropped
+    om_step_values last_vals{};  // what the last optimizer step passed to om_adam_step
     std::string err;
 
     Input &add_input(const std::string &name, std::vector<int> shape, std::vector<float> host, bool requires_grad) {
@@ -299,6 +310,7 @@ struct omt_model {
             if (i.name == name) return i;
         throw Error(OM_E_ARG, "no input " + name);
     }
+    Input &input(const std::string &name) { return const_cast<Input &>(std::as_const(*this).input(name)); }
 
     // Lays the parameters out contiguously (Parameters() order, 16-byte aligned) in four persistent blocks: values,
     // gradients, first and second moments; uploads the initial values once.
@@ -413,6 +425,7 @@ struct omt_model {
         }
         float ss, sq;
         om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
+        last_vals = om_step_values{lr, ss, sq};
         const int dec = opt_kind == OPT_ADAMW ? 1 : 0;
         for (auto [beg, n] : live_runs()) {
             float *vm = amsgrad ? vmaxb + beg : nullptr;
@@ -849,8 +862,81 @@ struct omt_model {
     // backward and the update, so those still run while the caller gets the value and queues the next step. Later
     // work on the context's stream is ordered after them.
     float step() {
+        if (graphable()) {
+            if (graph) return step_replay();
+            if (graph_warm > 0) return step_capture();
+        }
+        const bool warmable = graphable();
         begin_step();
         BatchScope batch{this};
+        step_body(batch);
+        graph_warm = warmable ? graph_warm + 1 : 0;
+        return wait_loss();
+    }
+    bool graphable() const {
+        return graph_on && opt_kind != OPT_SGD && !has_dropout && staged.empty() && active_slot < 0 && begun_slot < 0;
+    }
+    // Drops the step graph; the next graphable step runs outside a graph and the one after it captures again.
+    void graph_drop() {
+        graph_warm = 0;
+        if (!graph) return;
+        om_graph *g = graph;
+        graph = nullptr;
+        check(device->ctx(), om_graph_destroy(g), "om_graph_destroy");
+    }
+    float wait_loss() {
+        float v = 0.0f;
+        check(device->ctx(), om_readback_wait(loss_rb, &v, sizeof(float)), "loss readback");
+        return v;
+    }
+    // The step recorded into a graph and launched. If anything fails inside the capture, the capture is dropped,
+    // the host state the step changed is put back, graphs are switched off for the model and the step runs as usual
+    // (so a failure that is not the capture's own is reported by that run).
+    float step_capture() {
+        const int64_t count0 = step_count;
+        const float lr0 = lr;
+        begin_step();
+        om_ctx *c = device->ctx();
+        check(c, om_graph_capture_begin(c), "om_graph_capture_begin");
+        om_graph *g = nullptr;
+        try {
+            BatchScope batch{this};
+            step_body(batch);
+            check(c, om_graph_capture_end(c, &g), "om_graph_capture_end");
+        } catch (const Error &) {
+            (void)om_graph_capture_abort(c);
+            step_count = count0;
+            lr = lr0;
+            graph_on = false;
+            graph_warm = 0;
+            begin_step();
+            BatchScope batch{this};
+            step_body(batch);
+            return wait_loss();
+        }
+        graph = g;
+        check(c, om_graph_launch(g, &last_vals), "om_graph_launch");
+        return wait_loss();
+    }
+    // A replay: on the host, what ZeroGrad + forward + backward + Step change there — step memory rewound, the
+    // parameters' versions raised by the in-place update, the rate from the schedule, the step count — while the
+    // graph does the device work with this step's rate and bias corrections.
+    float step_replay() {
+        begin_step();
+        for (auto &p : params)
+            if (p.second->grad_exists && p.second->requires_grad) touch(p.second);
+        if (schedule) lr = schedule->lr_at(step_count);
+        if (!std::isfinite(lr) || lr < 0.0f) throw Error(OM_E_ARG, "learning rate must be finite and not negative");
+        float ss, sq;
+        om_adam_scalars(lr, beta1, beta2, step_count + 1, &ss, &sq);
+        last_vals = om_step_values{lr, ss, sq};
+        check(device->ctx(), om_graph_launch(graph, &last_vals), "om_graph_launch");
+        step_count++;
+        return wait_loss();
+    }
+    // ZeroGrad, the forward with the loss posted for readback, loss.Backward() and optimizer.Step() (with ClipNorm
+    // when set): the launches of one step, queued on the model's stream.
+    void step_body(BatchScope &batch) {
         zero_grad(leaves);
         if (!loss_rb) check(device->ctx(), om_readback_create(device->ctx(), sizeof(float), &loss_rb), "readback");
         device->arm_loss_post(loss_rb);  // a loss op that posts its own value takes it (MSE)
@@ -875,9 +961,6 @@ struct omt_model {
         } else {
             optimizer_step();
         }
-        float v = 0.0f;
-        check(device->ctx(), om_readback_wait(loss_rb, &v, sizeof(float)), "loss readback");
-        return v;
     }
 };
 
@@ -973,6 +1056,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.add_int_input("labels", {(int)tot}, ints(4, 3, tot, 1, 37));
         M.add_int_input("in_len", {B}, std::vector<int32_t>(B, 32));
         M.add_int_input("tgt_len", {B}, tl);
+        for (const char *n : {"labels", "in_len", "tgt_len"}) M.input(n).host_read = true;  // CTC checks them on the host
         M.loss_fn = [mp](omt_model &s) {
             static const int pools[4][2] = {{2, 2}, {2, 2}, {2, 1}, {2, 1}};
             Tensor h = s.input("x").t;
@@ -1064,6 +1148,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         // layer i's two streams 77 + 2i and 78 + 2i; CheckpointTests.cs:21-30).
         const int B = pick(sc.batch, 16), L = pick(sc.seq, 6), NL = pick(sc.layers, 2);
         const float drop = cfg == 9 ? 0.1f : 0.0f;
+        M.has_dropout = drop > 0.0f;
         Generator gm(3);
         struct Classifier : Module {
             Embedding *emb;
@@ -1172,6 +1257,7 @@ om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_mod
 void omt_destroy(omt_model *m) {
     if (!m) return;
     set_dev(m->device.get());
+    if (m->graph) om_graph_destroy(m->graph);
     if (m->stager) om_stager_destroy(m->stager);
     if (m->loss_rb) om_readback_destroy(m->loss_rb);
     m->root.reset();
@@ -1218,6 +1304,7 @@ om_status omt_set_clip(omt_model *m, float max_norm, int infinity_norm) {
     if (!m) return OM_E_ARG;
     return guard(m, [&] {
         if (!(max_norm >= 0.0f)) throw Error(OM_E_ARG, "omt_set_clip: max_norm must be positive (or 0 to switch off)");
+        m->graph_drop();  // the clip launches are part of the recorded step
         m->clip_max = max_norm;
         m->clip_inf = infinity_norm;
     });
@@ -1236,6 +1323,14 @@ om_status omt_step(omt_model *m, float *loss) {
         if (loss) *loss = v;
     });
 }
+om_status omt_set_step_graph(omt_model *m, int on) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        m->graph_drop();
+        m->graph_on = on != 0;
+    });
+}
+int omt_step_graph_ready(omt_model *m) { return m && m->graph && m->graphable() ? 1 : 0; }
 om_status omt_forward_backward(omt_model *m, float *loss) {
     if (!m) return OM_E_ARG;
     return guard(m, [&] {
@@ -1319,6 +1414,7 @@ om_status omt_checkpoint_save(omt_model *m, const char *path, int with_optimizer
 om_status omt_checkpoint_load(omt_model *m, const char *path, int with_optimizer, int *had_optimizer) {
     if (!m || !path || !*path) return OM_E_ARG;
     return guard(m, [&] {
+        m->graph_drop();
         const bool had = m->load_checkpoint(path, with_optimizer != 0);
         if (had_optimizer) *had_optimizer = had ? 1 : 0;
     });
@@ -1357,6 +1453,7 @@ om_status omt_set_optimizer(omt_model *m, int kind, float lr, float beta1, float
                             float momentum, float dampening, int nesterov, int amsgrad) {
     if (!m) return OM_E_ARG;
     return guard(m, [&] {
+        m->graph_drop();  // new optimizer state and kind
         m->set_optimizer(kind, lr, beta1, beta2, eps, weight_decay, momentum, dampening, nesterov != 0, amsgrad != 0);
     });
 }
@@ -1379,7 +1476,10 @@ om_status omt_batch_begin(omt_model *m, void **host) {
 }
 om_status omt_batch_commit(omt_model *m) {
     if (!m) return OM_E_ARG;
-    return guard(m, [&] { m->batch_commit(); });
+    return guard(m, [&] {
+        m->graph_drop();  // staged steps replace the inputs' addresses
+        m->batch_commit();
+    });
 }
 int omt_batch_queued(omt_model *m) { return m ? (int)m->staged.size() : 0; }
 
@@ -1438,6 +1538,7 @@ om_status omt_input_write(omt_model *m, int i, const void *host, int64_t numel) 
     return guard(m, [&] {
         Input &in = m->inputs[i];
         if (numel != in.t->numel) throw Error(OM_E_ARG, "omt_input_write: wrong element count for " + in.name);
+        if (in.host_read) m->graph_drop();
         if (in.is_int) {
             const int32_t *v = static_cast<const int32_t *>(host);
             for (int64_t k = 0; k < numel; k++)
