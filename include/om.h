@@ -107,7 +107,7 @@ om_status om_readback_wait(om_readback *r, void *dst_host, uint64_t bytes);
  * from the om_step_values given to each om_graph_launch: the rate and Adam's two bias-correction scalars of
  * om_adam_step / om_adam_step_scaled (their by-value lr, step_size and sqrt_bc2 are ignored inside a capture, and
  * 1 - lr * weight_decay is formed on the device with the same float rounding), and the sequence number of the
- * capture's one readback post (om_readback_post or om_mse_fwd_post; om_graph_launch advances the readback as a
+ * capture's one readback post (om_readback_post, om_mse_fwd_post or om_xent_fwd_unit; om_graph_launch advances the readback as a
  * post would, so om_readback_wait works as after an eager post). A caller captures again whenever anything else
  * it passed would change.
  * Inside a capture, calls that would wait for the device or read host memory when the graph runs fail with
@@ -299,6 +299,15 @@ om_status om_nll_fwd(om_ctx *ctx, const float *logp, const int32_t *target, floa
  * reference's rounding order: dlogits = d - exp(logp) * (float)sum(d), d = -g/count at the target. */
 om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,
                       int rows, int cols, int mean, int ignore_index, int accumulate);
+/* Losses.CrossEntropy = NllLoss(LogSoftmax(logits)) (Losses.cs:20-40) forward, also writing dlogits_unit = the
+ * om_xent_bwd result for a unit upstream gradient (g = 1, mean reduction), so a loss that is the root of the
+ * backward needs no gradient launch of its own: logp, *loss and *bad_row as om_logsoftmax_fwd then om_nll_fwd give
+ * them, bit for bit, and dlogits_unit bit for bit what om_xent_bwd(one, ...) writes. Two launches; with rb (may be
+ * NULL) the second also posts the loss as om_readback_post(rb, loss, 4) would. No counterpart in the reference:
+ * its loss and gradient are separate CPU passes. */
+om_status om_xent_fwd_unit(om_ctx *ctx, const float *logits, const int32_t *target, float *logp, float *loss,
+                           int32_t *bad_row, float *dlogits_unit, int rows, int cols, int ignore_index,
+                           om_readback *rb);
 
 /* ---------------------------------------------------------------------------------------------- attention */
 /* Ops.Attention (Ops.Layers.cs:746-807) and AttentionBackward (BackwardNn.cs:636-701). q,o are [B,Lq,H,D] and

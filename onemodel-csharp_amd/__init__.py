@@ -64,6 +64,7 @@ _OM_SIGS = {
     "om_mse_fwd": [vp, vp, vp, vp, vp, i64],
     "om_mse_fwd_unit": [vp, vp, vp, vp, vp, vp, i64],
     "om_mse_fwd_post": [vp, vp, vp, vp, vp, vp, i64, vp],
+    "om_xent_fwd_unit": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, vp],
     "om_mse_bwd": [vp, vp, vp, vp, i64, ci],
     "om_sum_all": [vp, vp, vp, i64, ci],
     "om_mean_axis": [vp, vp, vp, ci, ci, ci],

@@ -259,9 +259,6 @@ static bool launch_x2(const Params &p, int batch, bool ta, bool tb, hipStream_t 
 struct XTile {
     int bm, bn, bkt;
 };
-const XTile kXTiles[] = {{64, 64, 32},  {64, 96, 32},   {96, 64, 32},  {64, 128, 32}, {128, 64, 32},
-                         {128, 128, 32}, {64, 64, 64},  {64, 96, 64},  {128, 128, 64}};
-
 // Launches tile t; false when t (or its GELU variant) is not instantiated.
 static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
     // bkt 33 / 65 select the eight-wavefront variant of the 32 / 64 chunk.
@@ -269,6 +266,7 @@ static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool
     if (t.bkt == 33 && t.bm == 64 && t.bn == 64) return launch_x2<64, 64, 32, true>(p, batch, ta, tb, st);
     if (t.bkt == 65 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 64, false>(p, batch, ta, tb, st);
     if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, false>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 128 && t.bn == 96) return launch_x2<128, 96, 32, true>(p, batch, ta, tb, st);
 #define OMG_X(BM, BN, BKT, G) \
     if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, G>(p, batch, ta, tb, st, cus);
     OMG_X(64, 64, 32, true)
@@ -276,6 +274,7 @@ static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool
     OMG_X(96, 64, 32, false)
     OMG_X(64, 128, 32, false)
     OMG_X(128, 64, 32, false)
+    OMG_X(128, 96, 32, true)
     OMG_X(128, 128, 32, false)
     OMG_X(64, 64, 64, true)
     OMG_X(64, 96, 64, false)
@@ -296,7 +295,9 @@ static bool x_fits(const XTile &t, const Params &p, int splits, int k_split) {
 
 namespace {
 // Tuned choices for the products of the training path's configurations (MI355X, random operands, one sweep of
-// the tile-exact kernels over tiles x chunk depths x split counts): exact shape -> tile and split count.
+// the tile-exact kernels over tiles x chunk depths x split counts; C5's 768-wide rows re-swept with the 128 x 96
+// tile, which makes 4096 x 768 exactly one tile per CU: 8 % faster for the FFN's second product and the attention
+// output, 2-3 % for the q|k|v projection and two input gradients): exact shape -> tile and split count.
 struct Tuned {
     int m, n, k;
     bool ta, tb;
@@ -306,13 +307,13 @@ const Tuned kTuned[] = {
     // Linear forward y = x W^T (NT)
     {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 64, 64, 1},
     {4096, 384, 1536, false, true, 64, 96, 32, 1},    {4096, 1152, 384, false, true, 64, 96, 32, 1},
-    {4096, 768, 768, false, true, 64, 64, 32, 1},     {4096, 3072, 768, false, true, 128, 128, 32, 1},
-    {4096, 768, 3072, false, true, 64, 64, 32, 1},    {4096, 2304, 768, false, true, 64, 64, 32, 1},
+    {4096, 768, 768, false, true, 128, 96, 32, 1},    {4096, 3072, 768, false, true, 128, 128, 32, 1},
+    {4096, 768, 3072, false, true, 128, 96, 32, 1},   {4096, 2304, 768, false, true, 64, 96, 32, 1},
     // input gradient dx = g W (NN); bkt 33 = the eight-wavefront kernel with 32-deep chunks
     {4096, 384, 384, false, false, 64, 96, 33, 1},    {4096, 384, 1536, false, false, 64, 96, 33, 1},
     {4096, 1536, 384, false, false, 64, 64, 33, 1},   {4096, 384, 1152, false, false, 64, 96, 33, 1},
-    {4096, 768, 768, false, false, 64, 64, 32, 1},    {4096, 768, 3072, false, false, 64, 64, 32, 1},
-    {4096, 3072, 768, false, false, 128, 128, 33, 1}, {4096, 768, 2304, false, false, 64, 64, 32, 1},
+    {4096, 768, 768, false, false, 64, 64, 32, 1},    {4096, 768, 3072, false, false, 128, 96, 33, 1},
+    {4096, 3072, 768, false, false, 128, 128, 33, 1}, {4096, 768, 2304, false, false, 128, 96, 33, 1},
     // weight gradient dW = g^T x (TN), K = tokens
     {384, 384, 4096, true, false, 64, 96, 33, 8},     {1536, 384, 4096, true, false, 64, 96, 32, 8},
     {384, 1536, 4096, true, false, 64, 96, 32, 8},    {1152, 384, 4096, true, false, 64, 64, 32, 4},
@@ -339,9 +340,10 @@ Choice with_splits(int bm, int bn, int bkt, int k, int splits) {
     return c;
 }
 
-// Tuning runs: OM_GEMM_X="bm,bn,bkt[,splits]" forces a tile-exact configuration where it fits.
+// Tuning runs: OM_GEMM_X="bm,bn,bkt[,splits]" forces a tile-exact configuration where it fits (read at every call,
+// so one process can compare configurations).
 bool env_override(Choice &c, int k) {
-    static const char *s = std::getenv("OM_GEMM_X");
+    const char *s = std::getenv("OM_GEMM_X");
     if (!s || !*s || !strcmp(s, "off")) return false;
     int bm = 0, bn = 0, bk = 32, sp = 1;
     if (sscanf(s, "%d,%d,%d,%d", &bm, &bn, &bk, &sp) < 3) return false;
@@ -358,7 +360,7 @@ int group_band() {
     return b;
 }
 bool x_disabled() {
-    static const char *s = std::getenv("OM_GEMM_X");
+    const char *s = std::getenv("OM_GEMM_X");
     return s && !strcmp(s, "off");
 }
 }  // namespace

@@ -12,9 +12,12 @@
 //                 the reference's order, so bit-exact, and no atomics.
 //   Dropout       the mask is the reference's counter-based SplitMix64 function of (seed, draw, index), recomputed
 //                 by the backward instead of stored: y = x * m, dx = g * m, bit-exact.
+#include <rocprim/device/device_radix_sort.hpp>
+
 #include "om_internal.hpp"
 
 #include <cmath>
+#include <cstdlib>
 
 namespace {
 
@@ -217,6 +220,48 @@ __global__ void __launch_bounds__(kBlock) k_embedding_bwd(const float *__restric
     }
 }
 
+// The same sums for large tables, where a scan of every id per row would cost rows x n_ids: the (id, position)
+// pairs are sorted by id first (a stable radix sort, so each id's positions stay in increasing order), and row r's
+// wavefront finds its run of positions by binary search in the sorted ids and adds those gradient rows in that order,
+// which is k_embedding_bwd's order: the results are the same bits. Positions with the padding id (or an id outside
+// the table) carry the key `rows`, which sorts after every row.
+__global__ void __launch_bounds__(kBlock) k_embedding_keys(const int32_t *__restrict__ ids, int32_t *__restrict__ key,
+                                                           int32_t *__restrict__ pos, int64_t n_ids, int rows,
+                                                           int pad) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n_ids) return;
+    const int id = ids[i];
+    key[i] = (id >= 0 && id < rows && id != pad) ? id : rows;
+    pos[i] = (int32_t)i;
+}
+__device__ __forceinline__ int64_t lower_bound_key(const int32_t *__restrict__ key, int64_t n, int v) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (key[mid] < v) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+__global__ void __launch_bounds__(kBlock) k_embedding_bwd_sorted(const float *__restrict__ g,
+                                                                 const int32_t *__restrict__ key,
+                                                                 const int32_t *__restrict__ pos,
+                                                                 float *__restrict__ dtable, int64_t n_ids, int dim,
+                                                                 int rows, int acc) {
+    const int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;  // whole wavefronts leave together
+    const int64_t lo = lower_bound_key(key, n_ids, r), hi = lower_bound_key(key, n_ids, r + 1);
+    float *out = dtable + (int64_t)r * dim;
+    for (int j0 = 0; j0 < dim; j0 += 64) {
+        const int j = j0 + lane;
+        float v = 0.0f;
+        if (j < dim)
+            for (int64_t s = lo; s < hi; s++) v += g[(int64_t)pos[s] * dim + j];
+        if (j < dim) out[j] = acc ? out[j] + v : v;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ Dropout
 // Generator.Mix (Generator.cs:41-47), the SplitMix64 output function.
 __host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
@@ -345,8 +390,39 @@ om_status om_embedding_bwd(om_ctx *ctx, const float *g, const int32_t *ids, floa
                            int rows, int padding_index, int accumulate) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && ids && dtable && n_ids >= 0 && dim > 0 && rows > 0, "om_embedding_bwd: bad arguments");
-    hipLaunchKernelGGL(k_embedding_bwd, dim3((rows + kBlock / 64 - 1) / (kBlock / 64)), dim3(kBlock), 0, ctx->stream,
-                       g, ids, dtable, n_ids, dim, rows, padding_index, accumulate);
+    const unsigned row_grid = (unsigned)((rows + kBlock / 64 - 1) / (kBlock / 64));
+    // Small tables (or few ids): one launch that scans the ids for every row. Beyond about 2^22 id visits the sort
+    // costs less than the scan. OM_EMBEDDING_SORT=0 keeps every size on the scan (for comparisons).
+    const char *env = std::getenv("OM_EMBEDDING_SORT");
+    const bool no_sort = env && env[0] == '0';
+    if (no_sort || (double)rows * (double)n_ids <= (double)(1 << 22) || n_ids > INT32_MAX) {
+        hipLaunchKernelGGL(k_embedding_bwd, dim3(row_grid), dim3(kBlock), 0, ctx->stream, g, ids, dtable, n_ids, dim,
+                           rows, padding_index, accumulate);
+        return OM_LAUNCH_CHECK(ctx, "om_embedding_bwd");
+    }
+    // The radix sort's launches may include memory fills a step graph must not hold.
+    if (om_status st = om::refuse_in_capture(ctx, "om_embedding_bwd (large table)")) return st;
+    int bits = 1;
+    while (bits < 31 && (1ll << bits) <= (long long)rows) bits++;  // keys 0 .. rows
+    size_t temp_bytes = 0;
+    hipError_t e = rocprim::radix_sort_pairs(nullptr, temp_bytes, (int32_t *)nullptr, (int32_t *)nullptr,
+                                             (int32_t *)nullptr, (int32_t *)nullptr, (size_t)n_ids, 0, bits,
+                                             ctx->stream);
+    if (e != hipSuccess) return om::check_hip(ctx, e, "om_embedding_bwd sort size");
+    const uint64_t pair = (uint64_t)n_ids * sizeof(int32_t), pad_pair = (pair + 255) / 256 * 256;
+    float *scr;
+    om_status st = om::scratch(ctx, 4 * pad_pair + temp_bytes, &scr);
+    if (st) return st;
+    char *base = reinterpret_cast<char *>(scr);
+    int32_t *k_in = reinterpret_cast<int32_t *>(base), *p_in = reinterpret_cast<int32_t *>(base + pad_pair);
+    int32_t *k_out = reinterpret_cast<int32_t *>(base + 2 * pad_pair), *p_out = reinterpret_cast<int32_t *>(base + 3 * pad_pair);
+    hipLaunchKernelGGL(k_embedding_keys, dim3(om::grid1d(n_ids, kBlock)), dim3(kBlock), 0, ctx->stream, ids, k_in,
+                       p_in, n_ids, rows, padding_index);
+    e = rocprim::radix_sort_pairs(base + 4 * pad_pair, temp_bytes, k_in, k_out, p_in, p_out, (size_t)n_ids, 0, bits,
+                                  ctx->stream);
+    if (e != hipSuccess) return om::check_hip(ctx, e, "om_embedding_bwd sort");
+    hipLaunchKernelGGL(k_embedding_bwd_sorted, dim3(row_grid), dim3(kBlock), 0, ctx->stream, g, k_out, p_out, dtable,
+                       n_ids, dim, rows, accumulate);
     return OM_LAUNCH_CHECK(ctx, "om_embedding_bwd");
 }
 

@@ -426,11 +426,20 @@ __global__ void __launch_bounds__(kBlock) k_logsoftmax_bwd_rows(const float *__r
     }
 }
 
+// A loss value posted to a readback buffer by the launch that computes it: the value as a system-scope write-through
+// store, a wait for its completion, then the sequence number (read from seq_dev inside a step graph).
+struct LossPost {
+    char *dst;
+    uint64_t *seq_at;
+    uint64_t seq;
+    const uint64_t *seq_dev;
+};
+
 // NllLoss forward (Ops.Layers.cs:644-699): one block; double sum of -logp[i, t_i] over counted rows; the first
 // out-of-range row (smallest index) is reported.
 __global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ logp, const int32_t *__restrict__ tg,
                                                     float *__restrict__ loss, int32_t *__restrict__ bad, int rows,
-                                                    int cols, int mean, int ignore) {
+                                                    int cols, int mean, int ignore, LossPost post) {
     __shared__ double sh[kBlock / 64];
     __shared__ int shbad;
     if (threadIdx.x == 0) shbad = 0x7FFFFFFF;
@@ -453,8 +462,59 @@ __global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ lo
     if (threadIdx.x == 0) {
         int b = shbad == 0x7FFFFFFF ? -1 : shbad;
         if (bad) bad[0] = b;
-        loss[0] = b >= 0 ? __int_as_float(0x7FC00000)
-                         : (float)(mean ? total / (count > 1.0 ? count : 1.0) : total);
+        const float v = b >= 0 ? __int_as_float(0x7FC00000)
+                               : (float)(mean ? total / (count > 1.0 ? count : 1.0) : total);
+        loss[0] = v;
+        if (post.dst) {
+            __hip_atomic_store(reinterpret_cast<float *>(post.dst), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __builtin_amdgcn_s_waitcnt(0);
+            __hip_atomic_store(post.seq_at, post.seq_dev ? *post.seq_dev : post.seq, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
+// Cross-entropy forward with the unit gradient: per row (a wavefront each), k_logsoftmax_rows' arithmetic writing
+// logp, then k_xent_bwd's for g = 1 and the mean reduction, reading the logp values just computed. The count of
+// rows that are not ignored, which the gradient's scale needs, is formed by every block from all targets (an exact
+// integer count, so the same in every block).
+__global__ void __launch_bounds__(kBlock) k_xent_fwd_rows(const float *__restrict__ x, const int32_t *__restrict__ tg,
+                                                          float *__restrict__ y, float *__restrict__ dx, int rows,
+                                                          int cols, int ignore) {
+    __shared__ int shc[kBlock / 64];
+    int c = 0;
+    for (int i = threadIdx.x; i < rows; i += kBlock) c += tg[i] != ignore ? 1 : 0;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+    if ((threadIdx.x & 63) == 0) shc[threadIdx.x >> 6] = c;
+    __syncthreads();
+    int count = 0;
+#pragma unroll
+    for (int i = 0; i < kBlock / 64; i++) count += shc[i];
+    int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float *xr = x + (int64_t)r * cols;
+    float *yr = y + (int64_t)r * cols, *dr = dx + (int64_t)r * cols;
+    float mx = -__int_as_float(0x7F800000);
+    for (int j = lane; j < cols; j += 64) mx = xr[j] > mx ? xr[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float w = __shfl_xor(mx, o, 64);
+        mx = w > mx ? w : mx;
+    }
+    double sum = 0.0;
+    for (int j = lane; j < cols; j += 64) sum += (double)expf(xr[j] - mx);
+    sum = omd::wave_sum(sum);
+    const float lse = mx + logf((float)sum);
+    const float scale = 1.0f / (float)(count > 1 ? count : 1);
+    const int t = tg[r];
+    const bool counted = t != ignore;
+    const float sr = counted ? -scale : 0.0f;
+    for (int j = lane; j < cols; j += 64) {
+        const float lp = xr[j] - lse;
+        yr[j] = lp;
+        const float d = (counted && j == t) ? -scale : 0.0f;
+        dr[j] = d - expf(lp) * sr;
     }
 }
 
@@ -715,8 +775,29 @@ om_status om_nll_fwd(om_ctx *ctx, const float *logp, const int32_t *target, floa
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, logp && target && loss && rows >= 0 && cols > 0, "om_nll_fwd: bad arguments");
     hipLaunchKernelGGL(k_nll_fwd, dim3(1), dim3(kBlock), 0, ctx->stream, logp, target, loss, bad_row, rows, cols, mean,
-                       ignore_index);
+                       ignore_index, LossPost{nullptr, nullptr, 0, nullptr});
     return OM_LAUNCH_CHECK(ctx, "om_nll_fwd");
+}
+
+om_status om_xent_fwd_unit(om_ctx *ctx, const float *logits, const int32_t *target, float *logp, float *loss,
+                           int32_t *bad_row, float *dlogits_unit, int rows, int cols, int ignore_index,
+                           om_readback *rb) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, logits && target && logp && loss && dlogits_unit && rows >= 0 && cols > 0,
+               "om_xent_fwd_unit: bad arguments");
+    LossPost post{nullptr, nullptr, 0, nullptr};
+    if (rb) {
+        om_status s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq, &post.seq_dev);
+        if (s) return s;
+    }
+    if (rows > 0)
+        hipLaunchKernelGGL(k_xent_fwd_rows, dim3(rows_grid(rows, 64)), dim3(kBlock), 0, ctx->stream, logits, target,
+                           logp, dlogits_unit, rows, cols, ignore_index);
+    hipLaunchKernelGGL(k_nll_fwd, dim3(1), dim3(kBlock), 0, ctx->stream, logp, target, loss, bad_row, rows, cols, 1,
+                       ignore_index, post);
+    om_status s = OM_LAUNCH_CHECK(ctx, "om_xent_fwd_unit");
+    if (s == OM_OK && rb) om::readback_posted(rb, post.seq, sizeof(float));
+    return s;
 }
 
 om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,

@@ -679,13 +679,28 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels) {
                     " and " + shape_str(labels->shape));
     const int rows = logits->shape[0], cols = logits->shape[1];
     Tensor logp = make(logits->shape);
-    OMT(om_logsoftmax_fwd(C(), logits->data, logp->data, rows, cols));
     Tensor loss = make({});
-    OMT(om_nll_fwd(C(), logp->data, labels->idata, loss->data, nullptr, rows, cols, 1, -100));
-    if (tracked({&logits})) {
+    const bool rec = tracked({&logits});
+    // As for Mse: the gradient for a unit upstream gradient comes with the forward (and the loss posts itself when
+    // the step offers its readback), since the loss is normally the backward's root, seeded with exactly that unit.
+    float *unit = rec ? dev().step_floats(logits->numel) : nullptr;
+    if (unit) {
+        om_readback *rb = dev().take_loss_post();
+        OMT(om_xent_fwd_unit(C(), logits->data, labels->idata, logp->data, loss->data, nullptr, unit, rows, cols, -100,
+                             rb));
+        if (rb) dev().set_loss_posted(loss->data);
+    } else {
+        OMT(om_logsoftmax_fwd(C(), logits->data, logp->data, rows, cols));
+        OMT(om_nll_fwd(C(), logp->data, labels->idata, loss->data, nullptr, rows, cols, 1, -100));
+    }
+    if (rec) {
         float *lp = logp->data;
         const int32_t *tg = labels->idata;
-        attach(loss, "CrossEntropy", {logits}, [lp, tg, rows, cols](Engine &e, Record &r, const float *g) {
+        attach(loss, "CrossEntropy", {logits}, [lp, tg, rows, cols, unit](Engine &e, Record &r, const float *g) {
+            if (g == dev().one()) {
+                e.emit_alias(r, 0, unit);
+                return;
+            }
             int a;
             float *dz = e.dest(r, 0, &a);
             OMT(om_xent_bwd(C(), g, lp, tg, dz, rows, cols, 1, -100, a));

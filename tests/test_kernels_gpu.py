@@ -407,9 +407,17 @@ def test_cross_entropy(dev, T, rows, cols):
     assert scaled(dev.get(LP), lp) <= 1e-6
     assert abs(dev.get(L)[0] - loss) <= 1e-6 * abs(loss) and dev.get(BAD)[0] == -1
     assert scaled(dev.get(DZ), dz) <= 1e-6
+    # the fused forward with the unit gradient gives the same bits as the three separate launches (g = 1)
+    LP2, L2, BAD2, DZ2 = dev.empty(z.shape), dev.empty((1,)), dev.empty((1,), np.int32), dev.empty(z.shape)
+    dev.call("om_xent_fwd_unit", Z, TG, LP2, L2, BAD2, DZ2, rows, cols, -100, None)
+    for a, b in ((LP2, LP), (L2, L), (DZ2, DZ)):
+        assert np.array_equal(dev.get(a).view(np.uint32), dev.get(b).view(np.uint32))
+    assert dev.get(BAD2)[0] == -1
     tg[5] = cols  # out of range: reported, as the reference's ArgumentOutOfRangeException
     dev.call("om_nll_fwd", LP, dev.put(tg), L, BAD, rows, cols, 1, -100)
     assert dev.get(BAD)[0] == 5
+    dev.call("om_xent_fwd_unit", Z, dev.put(tg), LP2, L2, BAD2, DZ2, rows, cols, -100, None)
+    assert dev.get(BAD2)[0] == 5 and np.isnan(dev.get(L2)[0])
 
 
 # ------------------------------------------------------------------------------------------------ attention

@@ -100,12 +100,17 @@ def test_avgpool2d_bit_exact(dev, T, geo):
     assert np.array_equal(bits(dev.get(DX)), bits(dx + np.float32(0.25)))
 
 
-@pytest.mark.parametrize("rows,dim,n_ids,pad", [(11, 16, 96, -1), (50, 8, 1000, 3), (300, 130, 257, 0),
-                                                (30522, 64, 4096, 0)])
-def test_embedding_bit_exact(dev, T, rows, dim, n_ids, pad):
+# The last three take the sorted path (rows x ids above 2^22): ids drawn from 40 values (long runs per id) or from the
+# whole vocabulary, and a padding id that appears.
+@pytest.mark.parametrize("rows,dim,n_ids,pad,spread", [(11, 16, 96, -1, 40), (50, 8, 1000, 3, 40),
+                                                       (300, 130, 257, 0, 40), (1024, 64, 4096, 5, 40),
+                                                       (30522, 64, 4096, 0, 40), (30522, 768, 4096, 7, 30522),
+                                                       (4000, 33, 20000, 2, 4000)])
+def test_embedding_bit_exact(dev, T, rows, dim, n_ids, pad, spread):
     rng = np.random.default_rng(rows + n_ids)
     table = rng.standard_normal((rows, dim)).astype(np.float32)
-    ids = rng.integers(0, min(rows, 40), n_ids).astype(np.int32)  # repeated ids: order of the sums matters
+    ids = rng.integers(0, min(rows, spread), n_ids).astype(np.int32)  # repeated ids: order of the sums matters
+    ids[::97] = pad if pad >= 0 else ids[::97]
     g = rng.standard_normal((n_ids, dim)).astype(np.float32)
     y, dt = np.empty((n_ids, dim), np.float32), np.empty_like(table)
     T.lib().or_embedding_fwd(T.fp(table), T.ip(ids), T.fp(y), n_ids, dim)
