@@ -249,6 +249,13 @@ om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mea
 om_status om_mean_axis(om_ctx *ctx, const float *x, float *y, int outer, int n, int inner);
 om_status om_mean_axis_bwd(om_ctx *ctx, const float *g, float *dx, int outer, int n, int inner, int accumulate);
 om_status om_mean_all_bwd(om_ctx *ctx, const float *g_scalar, float *dx, int64_t n, int accumulate);
+/* Ops.Relu followed by the mean over each row of [outer, n] (a conv block's ReLU and global average pool,
+ * Ops.Layers.cs:463-472), in one pass: y[o] bit for bit om_relu_fwd then om_mean_axis(outer, n, 1). The backward
+ * (mean backward then ReLU backward, BackwardNn.cs:145-168 and the Relu rule) reads the pre-activation x:
+ * dx (+)= x > 0 ? g[o] / n : 0, bit for bit the two separate rules. No counterpart in the reference as one call. */
+om_status om_relu_mean_rows(om_ctx *ctx, const float *x, float *y, int outer, int n);
+om_status om_relu_mean_rows_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int outer, int n,
+                                int accumulate);
 
 /* ---------------------------------------------------------------------------------------------- normalisation */
 /* Ops.LayerNorm (Ops.Layers.cs:109-141; NormKernels.cs:79-127): saves mean and 1/sigma per row. */
@@ -364,6 +371,10 @@ om_status om_attention_bwd_flash(om_ctx *ctx, const float *q, const float *k, co
  * deterministic split over images and pixels, db = fp64 sums. Output pointers may be NULL. */
 om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
                         int H, int W, int Cout, int KH, int KW, int stride, int pad);
+/* Ops.Conv2d followed by Ops.Relu, the ReLU applied in the convolution's epilogue (3x3, stride 1, padding 1; other
+ * geometries run the two launches): y bit for bit om_conv2d_fwd then om_relu_fwd. No counterpart as one call. */
+om_status om_conv2d_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N,
+                             int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad);
 om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
                         int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad, int acc_dx,
                         int acc_params);
@@ -373,6 +384,11 @@ om_status om_maxpool_fwd(om_ctx *ctx, const float *x, float *y, int32_t *idx, in
                          int KW, int SH, int SW, int PH, int PW);
 om_status om_maxpool_bwd(om_ctx *ctx, const float *g, const int32_t *idx, float *dx, int N, int C, int H, int W,
                          int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW, int accumulate);
+/* MaxPoolBackward then the backward of the ReLU that produced the pool's input y, in one pass: dx (+)= the pooled
+ * gradient where y > 0, else 0; bit for bit om_maxpool_bwd then om_relu_bwd. No counterpart as one call. */
+om_status om_maxpool_relu_bwd(om_ctx *ctx, const float *g, const int32_t *idx, const float *y, float *dx, int N,
+                              int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW,
+                              int accumulate);
 /* Ops.AvgPool2d (Ops.Layers.cs:405-455) over `planes` = N*C planes of H x W: each output is its window's in-order
  * float sum divided by the window size (counting the zero padding when count_include_pad, else only real pixels);
  * and AvgPoolBackward (BackwardNn.cs:464-492), each input pixel gathering its windows' shares in the reference's

@@ -70,6 +70,8 @@ _OM_SIGS = {
     "om_mean_axis": [vp, vp, vp, ci, ci, ci],
     "om_mean_axis_bwd": [vp, vp, vp, ci, ci, ci, ci],
     "om_mean_all_bwd": [vp, vp, vp, i64, ci],
+    "om_relu_mean_rows": [vp, vp, vp, ci, ci],
+    "om_relu_mean_rows_bwd": [vp, vp, vp, vp, ci, ci, ci],
     "om_layernorm_fwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, f32],
     "om_layernorm_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci],
     "om_layernorm_bwd_add": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci],
@@ -88,9 +90,11 @@ _OM_SIGS = {
     "om_attention_fwd_fused": [vp, vp, vp, vp, ci, vp, ci, vp, ci, ci, ci, ci, ci, f32],
     "om_attention_bwd_fused": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
     "om_conv2d_fwd": [vp, vp, vp, vp, vp] + [ci] * 9,
+    "om_conv2d_relu_fwd": [vp, vp, vp, vp, vp] + [ci] * 9,
     "om_conv2d_bwd": [vp, vp, vp, vp, vp, vp, vp] + [ci] * 9 + [ci, ci],
     "om_maxpool_fwd": [vp, vp, vp, vp] + [ci] * 10,
     "om_maxpool_bwd": [vp, vp, vp, vp] + [ci] * 12 + [ci],
+    "om_maxpool_relu_bwd": [vp, vp, vp, vp, vp] + [ci] * 12 + [ci],
     "om_ctc_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, vp],
     "om_ctc_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci],
     "om_adam_step": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32],

@@ -13,9 +13,9 @@
 
 // 3x3, stride 1, padding 1 kernels (om_conv3.hip); each returns false when the shape is not one it takes.
 bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin, int H,
-                  int W, int Cout, int acc, om_status *st, bool flip_weights);
-bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, int Cin, int H, int W, int Cout,
-                 int acc, om_status *st);
+                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu);
+bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *db, int N, int Cin, int H, int W,
+                 int Cout, int acc, om_status *st);
 
 namespace {
 
@@ -371,10 +371,11 @@ __global__ void k_maxpool_fwd(const float *__restrict__ x, float *__restrict__ y
     }
 }
 // MaxPoolBackward (BackwardOps.cs:285-298) as a gather: each input element adds the gradients of the outputs whose
-// saved index is that element, in increasing output order (the order of the reference's scatter loop).
+// saved index is that element, in increasing output order (the order of the reference's scatter loop). With relu_y
+// (the pool's input, a ReLU's output) the ReLU backward follows in the same pass: the sum where relu_y > 0, else 0.
 __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__restrict__ idx, float *__restrict__ dx,
                               int N, int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH,
-                              int PW, int acc) {
+                              int PW, int acc, const float *__restrict__ relu_y) {
     int64_t total = (int64_t)N * C * H * W, stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
         int ix = (int)(e % W);
@@ -394,6 +395,7 @@ __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__rest
                 int64_t o = (nc * OH + oy) * OW + ox;
                 if (idx[o] == (int32_t)e) s += g[o];
             }
+        if (relu_y) s = relu_y[e] > 0.0f ? s : 0.0f;
         dx[e] = acc ? dx[e] + s : s;
     }
 }
@@ -402,14 +404,14 @@ __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__rest
 
 extern "C" {
 
-om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
-                        int H, int W, int Cout, int KH, int KW, int stride, int pad) {
+static om_status conv_fwd(om_ctx *ctx, const char *what, const float *x, const float *w, const float *bias, float *y,
+                          int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad, bool relu) {
     OM_CHECK_CTX(ctx);
     int OH, OW;
-    om_status s = conv_check(ctx, "om_conv2d_fwd", N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
+    om_status s = conv_check(ctx, what, N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
     if (s) return s;
-    OM_REQUIRE(ctx, x && w && y, "om_conv2d_fwd: NULL pointer");
-    if (conv3_geometry(KH, KW, stride, pad) && om_conv3_fwd(ctx, x, w, bias, y, N, Cin, H, W, Cout, 0, &s, false))
+    OM_REQUIRE(ctx, x && w && y, "%s: NULL pointer", what);
+    if (conv3_geometry(KH, KW, stride, pad) && om_conv3_fwd(ctx, x, w, bias, y, N, Cin, H, W, Cout, 0, &s, false, relu))
         return s;
     Params p = conv_params(N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
     p.m = Cout;
@@ -430,7 +432,20 @@ om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float
     int bm, bn;
     conv_tiles(p.m, p.n, N, ctx->num_cus, bm, bn);
     launch_conv<0>(p, bm, bn, vec, ctx->stream);
-    return OM_LAUNCH_CHECK(ctx, "om_conv2d_fwd");
+    s = OM_LAUNCH_CHECK(ctx, what);
+    // the general kernel has no ReLU epilogue: ReLU in place
+    if (!s && relu) s = om_relu_fwd(ctx, y, y, (int64_t)N * Cout * OH * OW);
+    return s;
+}
+
+om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
+                        int H, int W, int Cout, int KH, int KW, int stride, int pad) {
+    return conv_fwd(ctx, "om_conv2d_fwd", x, w, bias, y, N, Cin, H, W, Cout, KH, KW, stride, pad, false);
+}
+
+om_status om_conv2d_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
+                             int H, int W, int Cout, int KH, int KW, int stride, int pad) {
+    return conv_fwd(ctx, "om_conv2d_relu_fwd", x, w, bias, y, N, Cin, H, W, Cout, KH, KW, stride, pad, true);
 }
 
 om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
@@ -442,6 +457,13 @@ om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float
     if (s) return s;
     OM_REQUIRE(ctx, g && (!dx || w) && (!dw || x), "om_conv2d_bwd: NULL pointer");
     const int P = OH * OW, KK = KH * KW, Kc = Cin * KK;
+    const bool c3 = conv3_geometry(KH, KW, stride, pad);
+    // the staged weight-gradient kernels also produce the bias gradient from the g tiles they stage
+    if (dw && c3 && om_conv3_dw(ctx, g, x, dw, db, N, Cin, H, W, Cout, acc_params, &s)) {
+        if (s) return s;
+        dw = nullptr;  // done
+        db = nullptr;
+    }
     if (db) {
         float *scr;
         s = om::scratch(ctx, sizeof(double) * (uint64_t)N * Cout, &scr);
@@ -454,12 +476,7 @@ om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd db");
         if (s) return s;
     }
-    const bool c3 = conv3_geometry(KH, KW, stride, pad);
-    if (dw && c3 && om_conv3_dw(ctx, g, x, dw, N, Cin, H, W, Cout, acc_params, &s)) {
-        if (s) return s;
-        dw = nullptr;  // done
-    }
-    if (dx && c3 && om_conv3_fwd(ctx, g, w, nullptr, dx, N, Cout, H, W, Cin, acc_dx, &s, true)) {
+    if (dx && c3 && om_conv3_fwd(ctx, g, w, nullptr, dx, N, Cout, H, W, Cin, acc_dx, &s, true, false)) {
         if (s) return s;
         dx = nullptr;  // done
     }
@@ -548,8 +565,19 @@ om_status om_maxpool_bwd(om_ctx *ctx, const float *g, const int32_t *idx, float 
     OM_REQUIRE(ctx, g && idx && dx && N > 0 && C > 0 && H > 0 && W > 0 && OH > 0 && OW > 0 && SH > 0 && SW > 0,
                "om_maxpool_bwd: bad arguments");
     hipLaunchKernelGGL(k_maxpool_bwd, dim3(om::grid1d((int64_t)N * C * H * W, 256, 1 << 20)), dim3(256), 0,
-                       ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate);
+                       ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, nullptr);
     return OM_LAUNCH_CHECK(ctx, "om_maxpool_bwd");
+}
+
+om_status om_maxpool_relu_bwd(om_ctx *ctx, const float *g, const int32_t *idx, const float *y, float *dx, int N,
+                              int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW,
+                              int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && idx && y && dx && N > 0 && C > 0 && H > 0 && W > 0 && OH > 0 && OW > 0 && SH > 0 && SW > 0,
+               "om_maxpool_relu_bwd: bad arguments");
+    hipLaunchKernelGGL(k_maxpool_bwd, dim3(om::grid1d((int64_t)N * C * H * W, 256, 1 << 20)), dim3(256), 0,
+                       ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, y);
+    return OM_LAUNCH_CHECK(ctx, "om_maxpool_relu_bwd");
 }
 
 }  // extern "C"

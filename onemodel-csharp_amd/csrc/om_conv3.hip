@@ -3,13 +3,16 @@
 // BackwardNn.cs:317-402).
 //
 // Forward: y[n][co][p] = bias[co] + sum over taps t = (ky, kx) and channels ci of W[co][ci][t] x[n][ci][p + shift(t)]
-// (zero outside the image). A workgroup takes 128 output pixels (flattened, so any width works) of one image and a
-// block of 32 or 64 output channels; per chunk of 8 input channels it stages the input rows those pixels touch, halo
-// included, into LDS (each input value is then read by all nine taps from there) and the chunk's weights, laid out
-// [tap][co][ci]. Each lane keeps the LDS offsets of its two pixels; a tap is a constant shift of them, so the inner
-// loop has no index arithmetic. Four wavefronts of 32 pixels x all the block's channels, v_mfma_f32_16x16x4f32.
+// (zero outside the image), optionally followed by ReLU. A workgroup takes 128 output pixels (flattened, so any width
+// works) of one image and a block of 32 or 64 output channels; per chunk of 8 input channels it stages the input rows
+// those pixels touch, halo included, into LDS (each input value is then read by all nine taps from there) and the
+// chunk's weights, laid out [tap][co][ci]. The weights come straight from the layer's [Cout][Cin][3][3] tensor: a
+// chunk is 72 contiguous floats per output channel, loaded as float4 and scattered into that layout by the stores.
+// Each lane keeps the LDS offsets of its two pixels; a tap is a constant shift of them, so the inner loop has no index
+// arithmetic. Four wavefronts of 32 pixels x all the block's channels, v_mfma_f32_16x16x4f32.
 // dX: for stride 1 and padding 1, dx[n][ci][q] = sum over taps and co of W[co][ci][8 - t] g[n][co][q + shift(t)]:
-// the same kernel over g with the weights flipped and transposed ([ci][tap][co]).
+// the same kernel over g (FLIP), whose chunk of 8 of the layer's output channels is 9 x BM contiguous floats of W per
+// channel, stored flipped and transposed ([8 - t][ci][co]).
 // dW: dW[co][ci][t] = sum over images and pixels of g[n][co][p] x[n][ci][p + shift(t)]: a workgroup takes 64 output
 // channels x 16 input channels x all nine taps and a slot of (image, 64-pixel chunk) work items, stages each chunk's
 // g block and input rows, and accumulates in registers; the slots' partials are summed in slot order afterwards, so
@@ -31,6 +34,12 @@ constexpr int kThreads = 256;
 constexpr int kFwdCk = 8;    // input channels per staged chunk (forward, dX)
 constexpr int kFwdPx = 128;  // output pixels per workgroup (forward, dX)
 constexpr int kWLd = kFwdCk + 4;  // row stride of the staged weights [tap][co][ci]
+// tap stride of the staged weights: BM rows plus 4 floats, so the nine taps of one channel's scattered stores start
+// on different banks
+template <int BM>
+constexpr int w_tap_stride() {
+    return BM * kWLd + 4;
+}
 constexpr int kDwCi = 16;    // input channels per workgroup (dW)
 constexpr int kDwCo = 64;    // output channels per workgroup (dW)
 constexpr int kDwPx = 64;    // pixels per staged chunk (dW)
@@ -96,19 +105,23 @@ __device__ __forceinline__ void zero_halo(float *dst, int chans, int W, int R, i
     }
 }
 
-// out[n][co][p] (+)= bias[co] + sum_{tap, ci} wr[co][tap][ci] in[n][ci][p + shift(tap)], BM output channels per
-// workgroup. in is [N][cin][H][W], out [N][cout][H][W], wr [cout][9][cin]. With nsplit > 1 (few tiles: small images)
-// the input channels are cut into nsplit runs of cps chunks, one per workgroup, each writing its partial sums to
-// ws[split] ([N][cout][H][W], no bias); k_conv3_sum adds them in split order.
-template <int BM, int NS>
-__global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict__ in, const float *__restrict__ wr,
+// ReLU forward (ReluUn, TrainElementwise.cs): x where x > 0 or NaN, else +0.
+__device__ __forceinline__ float relu1(float v) { return v > 0.0f ? v : (v == v ? 0.0f : v); }
+
+// out[n][co][p] (+)= bias[co] + sum_{tap, ci} W[co][ci][tap] in[n][ci][p + shift(tap)] (then ReLU when relu), BM
+// output channels per workgroup. in is [N][cin][H][W], out [N][cout][H][W], wt the layer's weights: [cout][cin][9], or
+// with FLIP (the input gradient) [cin][cout][9] read as W[co][ci][8 - tap] with this call's co and ci swapped. With
+// nsplit > 1 (few tiles: small images) the input channels are cut into nsplit runs of cps chunks, one per workgroup,
+// each writing its partial sums to ws[split] ([N][cout][H][W], no bias); k_conv3_sum adds them in split order.
+template <int BM, int NS, bool FLIP>
+__global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict__ in, const float *__restrict__ wt,
                                                         const float *__restrict__ bias, float *out, int cin, int cout,
                                                         int H, int W, int R, int ps, int ntile, int acc, int N,
-                                                        int nsplit, int cps, float *__restrict__ ws) {
+                                                        int nsplit, int cps, float *__restrict__ ws, int relu) {
     extern __shared__ __attribute__((aligned(16))) float lds[];
-    constexpr int MB = BM / 16, NWI = (9 * BM * 2 + kThreads - 1) / kThreads;
-    float *Ws = lds;                   // [9][BM][kWLd]
-    float *Xs = lds + 9 * BM * kWLd;   // [kFwdCk][ps]
+    constexpr int MB = BM / 16, WF4 = 18 * BM, NWI = (WF4 + kThreads - 1) / kThreads, TS = w_tap_stride<BM>();
+    float *Ws = lds;           // [9][BM][kWLd], taps TS apart
+    float *Xs = lds + 9 * TS;  // [kFwdCk][ps]
     const int P = H * W, rs = W + 8, ncb = cout / BM;
     const int lin = xcd_lin();
     const int tile = lin % ntile, cb = (lin / ntile) % ncb, n = (lin / ntile / ncb) % N, split = lin / ntile / ncb / N;
@@ -123,15 +136,25 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
         pv[j] = p < P;
         boff[j] = pv[j] ? (p / W - oy0) * rs + p % W + 3 : 0;  // column ix + kx - 1 sits at 4 + ix + kx - 1
     }
-    // the weight float4s this thread stages: global offset without the chunk's c0, and LDS offset
-    int wgo[NWI], wlo[NWI];
+    // The weight float4s this thread stages: global offset without the chunk's part, and the LDS offsets of the four
+    // values. Forward: float4 f is floats 4 q .. 4 q + 3 (q = f % 18) of output channel co = f / 18's 72-float run
+    // [ci][tap] of the chunk. FLIP: float4 f is floats 4 q .. (q = f % (9 BM / 4)) of the run [ci][tap] of the chunk's
+    // input channel f / (9 BM / 4) (one of the layer's output channels), over this block's BM channels.
+    int wgo[NWI], wlo[NWI][4];
     floatx4 wv4[NWI];
 #pragma unroll
     for (int i = 0; i < NWI; i++) {
-        const int f = threadIdx.x + i * kThreads, half = f & 1, co = (f >> 1) % BM, tap = (f >> 1) / BM;
-        wlo[i] = f < 9 * BM * 2 ? (tap * BM + co) * kWLd + 4 * half : -1;
-        wgo[i] = ((co0 + co) * 9 + tap) * cin + 4 * half;
+        const int f = threadIdx.x + i * kThreads;
+        const bool ok = f < WF4;
+        const int per = FLIP ? 9 * BM / 4 : 18, row = f / per, q = f % per;
+        wgo[i] = FLIP ? (row * cout + co0) * 9 + 4 * q : (co0 + row) * cin * 9 + 4 * q;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int e = 4 * q + k, c = e / 9, tap = e % 9;
+            wlo[i][k] = !ok ? -1 : FLIP ? (8 - tap) * TS + c * kWLd + row : tap * TS + row * kWLd + c;
+        }
     }
+    const int64_t wstep = FLIP ? (int64_t)cout * 9 : 9;  // global offset of the next input channel's run
     RowStage<NS> xs;
     xs.init(kFwdCk, W, R, ps);
     zero_halo(Xs, kFwdCk, W, R, ps);
@@ -142,7 +165,7 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
     auto load = [&](int c0) {
 #pragma unroll
         for (int i = 0; i < NWI; i++)
-            if (wlo[i] >= 0) wv4[i] = *reinterpret_cast<const floatx4 *>(wr + wgo[i] + c0);
+            if (wlo[i][0] >= 0) wv4[i] = *reinterpret_cast<const floatx4 *>(wt + wgo[i] + c0 * wstep);
         xs.load(inn + (int64_t)c0 * P, H, W, oy0);
     };
     load(c_beg);
@@ -150,7 +173,9 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
         __syncthreads();  // the previous chunk's reads are done
 #pragma unroll
         for (int i = 0; i < NWI; i++)
-            if (wlo[i] >= 0) *reinterpret_cast<floatx4 *>(Ws + wlo[i]) = wv4[i];
+            if (wlo[i][0] >= 0)
+#pragma unroll
+                for (int k = 0; k < 4; k++) Ws[wlo[i][k]] = wv4[i][k];
         xs.store(Xs);
         __syncthreads();
         if (c0 + kFwdCk < c_end) load(c0 + kFwdCk);  // in flight while this chunk computes
@@ -160,7 +185,7 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
             floatx2 a[MB];
 #pragma unroll
             for (int i = 0; i < MB; i++)
-                a[i] = *reinterpret_cast<const floatx2 *>(Ws + (tap * BM + 16 * i + t) * kWLd + 2 * kl);
+                a[i] = *reinterpret_cast<const floatx2 *>(Ws + tap * TS + (16 * i + t) * kWLd + 2 * kl);
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 const float *xc = Xs + (2 * kl + u) * ps + toff;
@@ -197,41 +222,36 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
             for (int j = 0; j < 2; j++) {
                 if (!pv[j]) continue;
                 const int p = p0 + 32 * w + 16 * j + t;
-                const float v = bias ? accv[i][j][r] + bv : accv[i][j][r];
+                float v = bias ? accv[i][j][r] + bv : accv[i][j][r];
+                if (relu) v = relu1(v);
                 orow[p] = acc ? orow[p] + v : v;
             }
         }
 }
 
-// out (+)= the sum of the nsplit partials in split order, plus bias[co] (the unsplit kernel's arithmetic order).
+// out (+)= the sum of the nsplit partials in split order, plus bias[co] (the unsplit kernel's arithmetic order), then
+// ReLU when relu.
 __global__ void k_conv3_sum(const float *__restrict__ ws, int nsplit, int64_t total, int P, int cout,
-                            const float *__restrict__ bias, float *out, int acc) {
+                            const float *__restrict__ bias, float *out, int acc, int relu) {
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         float v = ws[e];
         for (int s = 1; s < nsplit; s++) v += ws[(int64_t)s * total + e];
         if (bias) v = v + bias[(e / P) % cout];
+        if (relu) v = relu1(v);
         out[e] = acc ? out[e] + v : v;
     }
 }
 
-// wr[co][tap][ci] = W[co][ci][tap] (forward); with flip, wr[ci][tap][co] = W[co][ci][8 - tap] (dX).
-__global__ void k_conv3_wt(const float *__restrict__ w, float *__restrict__ wr, int cout, int cin, int flip) {
-    const int64_t total = (int64_t)cout * cin * 9;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-        const int tap = (int)(e % 9);
-        const int64_t cc = e / 9;
-        const int ci = (int)(cc % cin), co = (int)(cc / cin);
-        if (flip) wr[((int64_t)ci * 9 + (8 - tap)) * cout + co] = w[e];
-        else wr[((int64_t)co * 9 + tap) * cin + ci] = w[e];
-    }
-}
-
 // part[slot][co][tap][ci] = the slot's items' sums of g[n][co][p] x[n][ci][p + shift(tap)]. The next item's g
-// block and input rows are loaded into registers while the current one computes.
+// block and input rows are loaded into registers while the current one computes. With dbp, the workgroups of the
+// first input-channel block also sum the staged g block per output channel in double (the bias gradient's partial of
+// the slot, dbp[slot][co]): thread (co = tid / 4, quarter = tid % 4) adds pixels 16 quarter .. 16 quarter + 15 of
+// every item in order, and the quarters are combined in order at the end.
 template <int NS>
 __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__ g, const float *__restrict__ x,
                                                        float *__restrict__ part, int cin, int cout, int H, int W,
-                                                       int R, int ps, int nchunks, int items, int per) {
+                                                       int R, int ps, int nchunks, int items, int per,
+                                                       double *__restrict__ dbp) {
     constexpr int NG = kDwCo * kDwPx / 4 / kThreads;
     __shared__ __attribute__((aligned(16))) float Gs[kDwCo * kGLd];
     __shared__ int boff[kDwPx];
@@ -255,6 +275,9 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
     floatx4 accv[9];
 #pragma unroll
     for (int tap = 0; tap < 9; tap++) accv[tap] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const bool do_db = dbp && cib == 0;  // uniform over the workgroup
+    const int dco = threadIdx.x >> 2, dq = threadIdx.x & 3;
+    double dbs = 0.0;
     const int i0 = slot * per, i1 = min(items, i0 + per);
     auto load = [&](int item) {
         const int n = item / nchunks, p0 = (item - n * nchunks) * kDwPx;
@@ -278,6 +301,11 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
         }
         __syncthreads();
         if (item + 1 < i1) load(item + 1);  // in flight while this item computes
+        if (do_db) {
+            const float *gr = Gs + dco * kGLd + 16 * dq;
+#pragma unroll
+            for (int j = 0; j < 16; j++) dbs += (double)gr[j];
+        }
 #pragma unroll
         for (int ks = 0; ks < kDwPx / 16; ks++) {
             const floatx4 a = *reinterpret_cast<const floatx4 *>(Gs + (16 * w + t) * kGLd + 16 * ks + 4 * kl);
@@ -295,19 +323,41 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
 #pragma unroll
         for (int r = 0; r < 4; r++)
             part[(((int64_t)slot * cout + co0 + 16 * w + 4 * kl + r) * 9 + tap) * cin + ci0 + t] = accv[tap][r];
+    if (do_db) {
+        const double a1 = __shfl_down(dbs, 1, 64), a2 = __shfl_down(dbs, 2, 64), a3 = __shfl_down(dbs, 3, 64);
+        if (dq == 0) dbp[(int64_t)slot * cout + co0 + dco] = ((dbs + a1) + a2) + a3;
+    }
 }
 
 // dW[co][ci][tap] (+)= the sum over slots of part[slot][co][tap][ci]: a workgroup takes 64 consecutive elements (one
 // per lane) and its four wavefronts the four quarters of the slot range, each summed in slot order; the quarters are
 // then added in order, so the result depends only on the shape. (Many slots per element: one thread walking them all
 // would keep too few loads in flight.)
+// The blocks after the weights' (when dbp is given) finish the bias gradient the same way, in double: db[co] (+)=
+// (float) of the four quarters' sums of dbp[slot][co] over the slots, added in order.
 __global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout, int cin,
-                                                         float *dw, int acc) {
+                                                         float *dw, int acc, const double *__restrict__ dbp,
+                                                         float *db) {
     __shared__ float qs[4][64];
+    __shared__ double qd[4][64];
     const int64_t total = (int64_t)cout * 9 * cin;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
     const int k0 = (int)((int64_t)slots * w / 4), k1 = (int)((int64_t)slots * (w + 1) / 4);
+    const int64_t nbw = (total + 63) / 64;
+    if ((int64_t)blockIdx.x >= nbw) {  // bias gradient (uniform over the block)
+        const int co = (int)(((int64_t)blockIdx.x - nbw) * 64 + lane);
+        double sd = 0.0;
+        if (co < cout)
+            for (int k = k0; k < k1; k++) sd += dbp[(int64_t)k * cout + co];
+        qd[w][lane] = sd;
+        __syncthreads();
+        if (w == 0 && co < cout) {
+            const float v = (float)(((qd[0][lane] + qd[1][lane]) + qd[2][lane]) + qd[3][lane]);
+            db[co] = acc ? db[co] + v : v;
+        }
+        return;
+    }
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
     float s = 0.0f;
     if (e < total) {
 #pragma unroll 8
@@ -333,7 +383,7 @@ __global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict
 // fixed butterfly into part[block][co][tap]; k_conv3_dw_reduce adds the blocks in order.
 __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ g, const float *__restrict__ x,
                                                       float *__restrict__ part, int cout, int H, int W, int br,
-                                                      int nbands) {
+                                                      int nbands, double *__restrict__ dbp) {
     extern __shared__ float xs[];  // [br + 2][W + 2]
     const int n = blockIdx.x / nbands, y0 = (blockIdx.x % nbands) * br, rows = min(br, H - y0), xw = W + 2;
     for (int f = threadIdx.x; f < (br + 2) * xw; f += blockDim.x) {
@@ -347,10 +397,13 @@ __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ 
     const int64_t P = (int64_t)H * W;
     const float *gn = g + ((int64_t)n * cout + co0) * P + (int64_t)y0 * W;
     float acc[8][9];
+    double dsum[8];  // the bias gradient's partials (when dbp): lane-ordered double sums of g, then the butterfly
 #pragma unroll
-    for (int k = 0; k < 8; k++)
+    for (int k = 0; k < 8; k++) {
+        dsum[k] = 0.0;
 #pragma unroll
         for (int tap = 0; tap < 9; tap++) acc[k][tap] = 0.0f;
+    }
     const int np = rows * W;
     for (int q = lane; q < np; q += 64) {
         const int r = q / W, c = q - r * W;
@@ -360,8 +413,16 @@ __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ 
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             const float gv = gn[k * P + q];
+            dsum[k] += (double)gv;
 #pragma unroll
             for (int tap = 0; tap < 9; tap++) acc[k][tap] = acc[k][tap] + gv * xv[tap];
+        }
+    }
+    if (dbp) {
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const double v = omd::wave_sum(dsum[k]);
+            if (lane == 0) dbp[(int64_t)blockIdx.x * cout + co0 + k] = v;
         }
     }
 #pragma unroll
@@ -394,7 +455,7 @@ int stage_ns(int chans, int W, int R) {
 
 // The 3x3 / stride 1 / padding 1 paths; each returns false (launching nothing) when the shape is not one it takes.
 bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin, int H,
-                  int W, int Cout, int acc, om_status *st, bool flip_weights) {
+                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu) {
     *st = OM_OK;
     const int P = H * W;
     if (Cin % kFwdCk || Cout % 32 || W % 4 || (int64_t)N * Cin * P > INT32_MAX || (int64_t)N * Cout * P > INT32_MAX ||
@@ -405,18 +466,10 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
     const int ns = stage_ns(kFwdCk, W, R);
     if (!ns) return false;
     const int BM = Cout % 64 == 0 ? 64 : 32;
-    float *wr;
-    *st = om::scratch(ctx, sizeof(float) * (uint64_t)Cout * Cin * 9, &wr);
-    if (*st) return true;
-    // forward: W [Cout][Cin][9] -> wr [Cout][9][Cin]; dX (flip): the layer's W [Cout_l][Cin_l][9], where this call's
-    // Cin is Cout_l and its Cout is Cin_l -> wr [Cin_l][9][Cout_l] with the taps reversed
-    const int64_t nw = (int64_t)Cout * Cin * 9;
-    if (flip_weights)
-        hipLaunchKernelGGL(k_conv3_wt, dim3(om::grid1d(nw, 256, 1024)), dim3(256), 0, ctx->stream, w, wr, Cin, Cout, 1);
-    else
-        hipLaunchKernelGGL(k_conv3_wt, dim3(om::grid1d(nw, 256, 1024)), dim3(256), 0, ctx->stream, w, wr, Cout, Cin, 0);
+    // forward: the layer's W [Cout][Cin][9]; dX (flip): the layer's W [Cout_l][Cin_l][9], where this call's Cin is
+    // Cout_l and its Cout is Cin_l (the kernel reads it flipped and transposed)
     const int ntile = (P + kFwdPx - 1) / kFwdPx;
-    const size_t lds = sizeof(float) * (9 * (size_t)BM * kWLd + (size_t)kFwdCk * ps);
+    const size_t lds = sizeof(float) * (9 * (size_t)(BM * kWLd + 4) + (size_t)kFwdCk * ps);
     const int64_t tiles = (int64_t)ntile * (Cout / BM) * N;
     // Fewer tiles than two per CU (small images): split the input channels, at least two chunks per split.
     const int chunks = Cin / kFwdCk;
@@ -434,23 +487,28 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
         if (*st) return true;
     }
     const dim3 grid((unsigned)(tiles * nsplit));
+    const int rl = relu && nsplit == 1 ? 1 : 0;  // with splits the sum applies it
 #define OMC3(BM_, NS_)                                                                                             \
     if (BM == BM_ && ns == NS_) {                                                                                  \
-        hipLaunchKernelGGL((k_conv3_fwd<BM_, NS_>), grid, dim3(kThreads), lds, ctx->stream, x, wr, bias, y, Cin, Cout, \
-                           H, W, R, ps, ntile, acc, N, nsplit, cps, ws);                                           \
+        if (flip_weights)                                                                                          \
+            hipLaunchKernelGGL((k_conv3_fwd<BM_, NS_, true>), grid, dim3(kThreads), lds, ctx->stream, x, w, bias, y, \
+                               Cin, Cout, H, W, R, ps, ntile, acc, N, nsplit, cps, ws, rl);                         \
+        else                                                                                                       \
+            hipLaunchKernelGGL((k_conv3_fwd<BM_, NS_, false>), grid, dim3(kThreads), lds, ctx->stream, x, w, bias, \
+                               y, Cin, Cout, H, W, R, ps, ntile, acc, N, nsplit, cps, ws, rl);                      \
     }
     OMC3(64, 1) OMC3(64, 2) OMC3(64, 3) OMC3(64, 4) OMC3(64, 6) OMC3(64, 8)
     OMC3(32, 1) OMC3(32, 2) OMC3(32, 3) OMC3(32, 4) OMC3(32, 6) OMC3(32, 8)
 #undef OMC3
     if (nsplit > 1)
         hipLaunchKernelGGL(k_conv3_sum, dim3(om::grid1d(total, 256, 4096)), dim3(256), 0, ctx->stream, ws, nsplit,
-                           total, P, Cout, bias, y, acc);
+                           total, P, Cout, bias, y, acc, relu ? 1 : 0);
     *st = OM_LAUNCH_CHECK(ctx, flip_weights ? "om_conv2d_bwd dx" : "om_conv2d_fwd");
     return true;
 }
 
-bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, int Cin, int H, int W, int Cout,
-                 int acc, om_status *st) {
+bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *db, int N, int Cin, int H, int W,
+                 int Cout, int acc, om_status *st) {
     *st = OM_OK;
     const int P = H * W;
     if (Cin == 1 && Cout % 8 == 0 && Cout <= 128 && (int64_t)N * Cout * P <= INT32_MAX && (W + 2) * 4 <= 16384) {
@@ -461,14 +519,17 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, 
         while (br > 1 && (int64_t)(br + 2) * (W + 2) * 4 > 65536) br = (br + 1) / 2;
         nb = (H + br - 1) / br;
         const int blocks = N * nb;
+        const uint64_t pbytes = (sizeof(float) * (uint64_t)blocks * Cout * 9 + 255) / 256 * 256;
         float *part;
-        *st = om::scratch(ctx, sizeof(float) * (uint64_t)blocks * Cout * 9, &part);
+        *st = om::scratch(ctx, pbytes + (db ? sizeof(double) * (uint64_t)blocks * Cout : 0), &part);
         if (*st) return true;
+        double *dbp = db ? reinterpret_cast<double *>(reinterpret_cast<char *>(part) + pbytes) : nullptr;
         const size_t lds = sizeof(float) * (size_t)(br + 2) * (W + 2);
         hipLaunchKernelGGL(k_conv3_dw_c1, dim3((unsigned)blocks), dim3(64 * (Cout / 8)), lds, ctx->stream, g, x, part,
-                           Cout, H, W, br, nb);
-        hipLaunchKernelGGL(k_conv3_dw_reduce, dim3((unsigned)((Cout * 9 + 63) / 64)), dim3(256), 0, ctx->stream,
-                           part, blocks, Cout, 1, dw, acc);
+                           Cout, H, W, br, nb, dbp);
+        const unsigned rb = (unsigned)((Cout * 9 + 63) / 64 + (db ? (Cout + 63) / 64 : 0));
+        hipLaunchKernelGGL(k_conv3_dw_reduce, dim3(rb), dim3(256), 0, ctx->stream, part, blocks, Cout, 1, dw, acc, dbp,
+                           db);
         *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
         return true;
     }
@@ -485,20 +546,23 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, int N, 
     if (slots > items / 2) slots = items / 2 > 0 ? items / 2 : 1;
     const int per = (items + slots - 1) / slots;
     slots = (items + per - 1) / per;
+    const uint64_t pbytes = (sizeof(float) * (uint64_t)slots * Cout * 9 * Cin + 255) / 256 * 256;
     float *part;
-    *st = om::scratch(ctx, sizeof(float) * (uint64_t)slots * Cout * 9 * Cin, &part);
+    *st = om::scratch(ctx, pbytes + (db ? sizeof(double) * (uint64_t)slots * Cout : 0), &part);
     if (*st) return true;
+    double *dbp = db ? reinterpret_cast<double *>(reinterpret_cast<char *>(part) + pbytes) : nullptr;
     const size_t lds = sizeof(float) * (size_t)kDwCi * ps;
     const dim3 grid((unsigned)((int64_t)slots * blocks));
 #define OMW3(NS_)                                                                                                 \
     if (ns == NS_)                                                                                                \
         hipLaunchKernelGGL(k_conv3_dw<NS_>, grid, dim3(kThreads), lds, ctx->stream, g, x, part, Cin, Cout, H, W, R, ps, \
-                           nchunks, items, per);
+                           nchunks, items, per, dbp);
     OMW3(1) OMW3(2) OMW3(3) OMW3(4) OMW3(6) OMW3(8)
 #undef OMW3
     const int64_t total = (int64_t)Cout * 9 * Cin;
-    hipLaunchKernelGGL(k_conv3_dw_reduce, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, ctx->stream, part, slots,
-                       Cout, Cin, dw, acc);
+    const unsigned rb = (unsigned)((total + 63) / 64 + (db ? (Cout + 63) / 64 : 0));
+    hipLaunchKernelGGL(k_conv3_dw_reduce, dim3(rb), dim3(256), 0, ctx->stream, part, slots, Cout, Cin, dw, acc, dbp,
+                       db);
     *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
     return true;
 }

@@ -198,6 +198,37 @@ __global__ void __launch_bounds__(kBlock) k_mean_rows(const float *__restrict__ 
     acc = omd::wave_sum(acc);
     if (lane == 0) y[wave] = (float)(acc / n);
 }
+// ReLU then the mean of each row (a global average pool over planes): k_mean_rows' sums of the ReLU outputs, in its
+// order (lane-strided, loads four strides ahead), so the bits equal om_relu_fwd followed by om_mean_axis.
+__global__ void __launch_bounds__(kBlock) k_relu_mean_rows(const float *__restrict__ x, float *__restrict__ y,
+                                                           int outer, int n) {
+    int wave = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    if (wave >= outer) return;
+    const float *xr = x + (int64_t)wave * n;
+    double acc = 0.0;
+    int k = lane;
+    for (; k + 192 < n; k += 256) {
+        const float a = xr[k], b = xr[k + 64], c = xr[k + 128], d = xr[k + 192];
+        acc += (double)ReluF{}(a, 0.f);
+        acc += (double)ReluF{}(b, 0.f);
+        acc += (double)ReluF{}(c, 0.f);
+        acc += (double)ReluF{}(d, 0.f);
+    }
+    for (; k < n; k += 64) acc += (double)ReluF{}(xr[k], 0.f);
+    acc = omd::wave_sum(acc);
+    if (lane == 0) y[wave] = (float)(acc / n);
+}
+// Its backward: the mean's backward (g / n broadcast over the row) and ReLU's (kept where x > 0) in one pass.
+__global__ void __launch_bounds__(kBlock) k_relu_mean_rows_bwd(const float *__restrict__ g,
+                                                               const float *__restrict__ x, float *__restrict__ dx,
+                                                               int outer, int n, int acc) {
+    const int64_t total = (int64_t)outer * n, stride = (int64_t)gridDim.x * kBlock;
+    const float fn = (float)n;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
+        const float v = x[t] > 0.0f ? g[t / n] / fn : 0.0f;
+        dx[t] = acc ? dx[t] + v : v;
+    }
+}
 __global__ void __launch_bounds__(kBlock) k_mean_inner(const float *__restrict__ x, float *__restrict__ y, int outer,
                                                        int n, int inner) {
     int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
@@ -441,6 +472,23 @@ om_status om_mean_axis_bwd(om_ctx *ctx, const float *g, float *dx, int outer, in
     hipLaunchKernelGGL(k_mean_axis_bwd, dim3(ew_grid((int64_t)outer * n * inner)), dim3(kBlock), 0, ctx->stream, g,
                        dx, outer, n, inner, accumulate);
     return OM_LAUNCH_CHECK(ctx, "om_mean_axis_bwd");
+}
+
+om_status om_relu_mean_rows(om_ctx *ctx, const float *x, float *y, int outer, int n) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && outer > 0 && n > 0, "om_relu_mean_rows: bad arguments");
+    hipLaunchKernelGGL(k_relu_mean_rows, dim3(om::grid1d((int64_t)outer * 64, kBlock, 1 << 30)), dim3(kBlock), 0,
+                       ctx->stream, x, y, outer, n);
+    return OM_LAUNCH_CHECK(ctx, "om_relu_mean_rows");
+}
+
+om_status om_relu_mean_rows_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int outer, int n,
+                                int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && x && dx && outer > 0 && n > 0, "om_relu_mean_rows_bwd: bad arguments");
+    hipLaunchKernelGGL(k_relu_mean_rows_bwd, dim3(ew_grid((int64_t)outer * n)), dim3(kBlock), 0, ctx->stream, g, x, dx,
+                       outer, n, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_relu_mean_rows_bwd");
 }
 
 om_status om_mean_all_bwd(om_ctx *ctx, const float *g, float *dx, int64_t n, int accumulate) {

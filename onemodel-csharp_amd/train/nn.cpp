@@ -1010,11 +1010,11 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.root = std::move(m);
         M.add_input("x", {B, 64, HW, HW}, normal(2, 1, (int64_t)B * 64 * HW * HW), true);
         M.add_int_input("labels", {B}, ints(2, 2, B, 0, 10));
-        M.loss_fn = [mp, B](omt_model &s) {
-            Tensor h = relu((*mp->conv)(s.input("x").t));
-            // GlobalAvgPool2d (Ops.Layers.cs:463-472) = Reshape + Mean(axis 2) + Reshape, then Flatten
-            Tensor gap = reshape(mean_axis(reshape(h, {B, 64, -1}), 2), {B, 64, 1, 1});
-            return cross_entropy((*mp->fc)(reshape(gap, {B, 64})), s.input("labels").t);
+        M.loss_fn = [mp](omt_model &s) {
+            // Relu, then GlobalAvgPool2d (Ops.Layers.cs:463-472: Reshape + Mean(axis 2) + Reshape) and Flatten, as
+            // one record
+            Tensor gap = relu_mean_plane((*mp->conv)(s.input("x").t));
+            return cross_entropy((*mp->fc)(gap), s.input("labels").t);
         };
     } else if (cfg == 3) {
         const int B = pick(sc.batch, 32), L = pick(sc.seq, 128), D = 384, H = 12, F = 1536;
@@ -1060,7 +1060,12 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.loss_fn = [mp](omt_model &s) {
             static const int pools[4][2] = {{2, 2}, {2, 2}, {2, 1}, {2, 1}};
             Tensor h = s.input("x").t;
-            for (int i = 0; i < 4; i++) h = max_pool2d(relu((*mp->conv[i])(h)), pools[i][0], pools[i][1], pools[i][0], pools[i][1]);
+            // Conv2d -> Relu -> MaxPool2d per stage, one record each
+            for (int i = 0; i < 4; i++) {
+                const Conv2d &cv = *mp->conv[i];
+                h = conv2d_relu_pool(h, cv.w, cv.b, cv.stride, cv.pad, pools[i][0], pools[i][1], pools[i][0],
+                                     pools[i][1]);
+            }
             Tensor f = mean_axis(h, 2);        // [B, 256, T]
             Tensor seq = permute(f, {2, 0, 1});  // [T, B, 256]
             Tensor lp = log_softmax((*mp->head)(seq));

@@ -755,31 +755,85 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     return loss;
 }
 
-Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad) {
+struct ConvGeom {
+    int N, Cin, H, W, Cout, KH, KW, OH, OW, stride, pad;
+};
+static ConvGeom conv_geom(const Tensor &x, const Tensor &w, int stride, int pad) {
     if (x->shape.size() != 4 || w->shape.size() != 4 || w->shape[1] != x->shape[1])
         shape_error("Conv2d: weights " + shape_str(w->shape) + " do not fit input " + shape_str(x->shape));
-    const int N = x->shape[0], Cin = x->shape[1], H = x->shape[2], W = x->shape[3];
-    const int Cout = w->shape[0], KH = w->shape[2], KW = w->shape[3];
-    const int OH = (H + 2 * pad - KH) / stride + 1, OW = (W + 2 * pad - KW) / stride + 1;
-    if (OH < 1 || OW < 1) shape_error("Invalid convolution geometry for input " + shape_str(x->shape));
-    Tensor y = make({N, Cout, OH, OW});
-    OMT(om_conv2d_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, N, Cin, H, W, Cout, KH, KW, stride, pad));
+    ConvGeom c{x->shape[0], x->shape[1], x->shape[2], x->shape[3], w->shape[0], w->shape[2], w->shape[3], 0, 0,
+               stride, pad};
+    c.OH = (c.H + 2 * pad - c.KH) / stride + 1;
+    c.OW = (c.W + 2 * pad - c.KW) / stride + 1;
+    if (c.OH < 1 || c.OW < 1) shape_error("Invalid convolution geometry for input " + shape_str(x->shape));
+    return c;
+}
+// ConvBackward (BackwardNn.cs:317-402) of record r (inputs x, w[, b]) for the output gradient g.
+static void conv_backward(Engine &e, Record &r, const float *g, const ConvGeom &c) {
+    int ax, aw, ab = 0;
+    float *dx = e.dest(r, 0, &ax);
+    float *dw = e.dest(r, 1, &aw);
+    float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+    if (dw && db && aw != ab) {
+        if (!aw) OMT(om_zero(C(), dw, sizeof(float) * (uint64_t)r.inputs[1]->numel));
+        if (!ab) OMT(om_zero(C(), db, sizeof(float) * (uint64_t)c.Cout));
+        aw = ab = 1;
+    }
+    OMT(om_conv2d_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, c.N, c.Cin, c.H, c.W, c.Cout, c.KH,
+                      c.KW, c.stride, c.pad, ax, dw ? aw : ab));
+}
+
+Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad) {
+    const ConvGeom c = conv_geom(x, w, stride, pad);
+    Tensor y = make({c.N, c.Cout, c.OH, c.OW});
+    OMT(om_conv2d_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, c.N, c.Cin, c.H, c.W, c.Cout, c.KH, c.KW,
+                      stride, pad));
     if (tracked({&x, &w, &b})) {
         std::vector<Tensor> ins{x, w};
         if (b) ins.push_back(b);
-        attach(y, "Conv2d", ins, [=](Engine &e, Record &r, const float *g) {
-            int ax, aw, ab = 0;
-            float *dx = e.dest(r, 0, &ax);
-            float *dw = e.dest(r, 1, &aw);
-            float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
-            if (dw && db && aw != ab) {
-                if (!aw) OMT(om_zero(C(), dw, sizeof(float) * (uint64_t)r.inputs[1]->numel));
-                if (!ab) OMT(om_zero(C(), db, sizeof(float) * (uint64_t)Cout));
-                aw = ab = 1;
-            }
-            OMT(om_conv2d_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, N, Cin, H, W, Cout, KH, KW,
-                              stride, pad, ax, dw ? aw : ab));
-        }, {x, w});
+        attach(y, "Conv2d", ins, [=](Engine &e, Record &r, const float *g) { conv_backward(e, r, g, c); }, {x, w});
+    }
+    return y;
+}
+
+Tensor conv2d_relu_pool(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad, int kh, int kw, int sh,
+                        int sw) {
+    const ConvGeom c = conv_geom(x, w, stride, pad);
+    const int PH = (c.OH - kh) / sh + 1, PW = (c.OW - kw) / sw + 1;
+    if (PH < 1 || PW < 1) shape_error("MaxPool2d: window larger than the input");
+    Tensor a = make({c.N, c.Cout, c.OH, c.OW});  // Relu(Conv2d(x))
+    OMT(om_conv2d_relu_fwd(C(), x->data, w->data, b ? b->data : nullptr, a->data, c.N, c.Cin, c.H, c.W, c.Cout, c.KH,
+                           c.KW, stride, pad));
+    Tensor y = make({c.N, c.Cout, PH, PW});
+    const bool rec = tracked({&x, &w, &b});
+    int32_t *idx = rec ? dev().step_ints((int64_t)c.N * c.Cout * PH * PW) : nullptr;
+    OMT(om_maxpool_fwd(C(), a->data, y->data, idx, c.N, c.Cout, c.OH, c.OW, kh, kw, sh, sw, 0, 0));
+    if (rec) {
+        std::vector<Tensor> ins{x, w};
+        if (b) ins.push_back(b);
+        const float *ad = a->data;
+        attach(y, "Conv2dReluMaxPool", ins, [=](Engine &e, Record &r, const float *g) {
+            // MaxPool's rule then Relu's, in one pass, into the convolution's output gradient
+            float *ga = dev().step_floats((int64_t)c.N * c.Cout * c.OH * c.OW);
+            OMT(om_maxpool_relu_bwd(C(), g, idx, ad, ga, c.N, c.Cout, c.OH, c.OW, PH, PW, kh, kw, sh, sw, 0, 0, 0));
+            conv_backward(e, r, ga, c);
+        }, {x, w, a});
+    }
+    return y;
+}
+
+Tensor relu_mean_plane(const Tensor &x) {
+    if (x->shape.size() != 4) shape_error("ReluMean needs an (N,C,H,W) input, not " + shape_str(x->shape));
+    const int N = x->shape[0], Cc = x->shape[1], plane = x->shape[2] * x->shape[3];
+    Tensor y = make({N, Cc});
+    OMT(om_relu_mean_rows(C(), x->data, y->data, N * Cc, plane));
+    if (tracked({&x})) {
+        const float *xd = x->data;
+        attach(y, "ReluMean", {x}, [=](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            if (dx) OMT(om_relu_mean_rows_bwd(C(), g, xd, dx, N * Cc, plane, a));
+        }, {x});
     }
     return y;
 }

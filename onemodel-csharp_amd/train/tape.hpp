@@ -208,6 +208,14 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels);  // Losses.Cro
 Tensor mse(const Tensor &pred, const Tensor &target);              // Losses.Mse: Mean((pred-target)^2)
 Tensor conv2d(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad);
 Tensor max_pool2d(const Tensor &x, int kh, int kw, int sh, int sw);
+// MaxPool2d(Relu(Conv2d(x))) (a CRNN stage, Layers.cs Conv2d / Relu / MaxPool2d) as one record: the ReLU runs in the
+// convolution's epilogue, and the backward runs MaxPool's and Relu's rules in one pass before ConvBackward. The same
+// arithmetic as the three ops, so the same bits.
+Tensor conv2d_relu_pool(const Tensor &x, const Tensor &w, const Tensor &b, int stride, int pad, int kh, int kw, int sh,
+                        int sw);
+// Mean over each (H, W) plane of Relu(x), [N, C, H, W] -> [N, C] (a conv block's ReLU and GlobalAvgPool2d with its
+// Flatten, Ops.Layers.cs:463-472) as one record: one pass forward, one backward; the same bits as the separate ops.
+Tensor relu_mean_plane(const Tensor &x);
 // The int arrays on the host; d_* are optional int tensors holding the same values on the device (a model's int
 // inputs keep such a copy), which spare the step three uploads from pageable memory. They are saved for the backward
 // like any tensor it reads, so an in-place write between forward and backward fails that backward.

@@ -670,6 +670,11 @@ def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     assert scaled(dev.get(DX), dx) <= TOL
     assert scaled(dev.get(DW), dw) <= TOL
     assert scaled(dev.get(DB), db) <= 1e-7
+    # the ReLU in the convolution's epilogue: the same bits as the convolution followed by om_relu_fwd
+    YR, YR2 = dev.empty(y.shape), dev.empty(y.shape)
+    dev.call("om_conv2d_relu_fwd", X, Wd, Bd, YR, N, Cin, H, W, Cout, K, K, S, P)
+    dev.call("om_relu_fwd", Y, YR2, y.size)
+    assert np.array_equal(dev.get(YR).view(np.uint32), dev.get(YR2).view(np.uint32))
     # accumulating into the existing gradients, and the same bits on a second run
     first = [dev.get(t).copy() for t in (DX, DW, DB)]
     dev.call("om_conv2d_bwd", G, X, Wd, DX, DW, DB, N, Cin, H, W, Cout, K, K, S, P, 1, 1)
@@ -699,6 +704,39 @@ def test_maxpool_bit_exact(dev, T, shape, k, s):
     assert np.array_equal(dev.get(I), idx)
     assert np.array_equal(dev.get(Y).view(np.uint32), y.view(np.uint32))
     assert np.array_equal(dev.get(DX), dx)
+    # with the backward of the ReLU that produced the pool's input (x read as that ReLU's output): the pooled
+    # gradient where x > 0, the same bits as om_maxpool_bwd then om_relu_bwd, accumulating as asked
+    DX2 = dev.empty(x.shape, fill=0.5)
+    dev.call("om_maxpool_relu_bwd", G, I, X, DX2, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], 0, 0, 1)
+    ref = np.where(x > 0, dx, np.float32(0.0)).astype(np.float32) + np.float32(0.5)
+    assert np.array_equal(dev.get(DX2).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,Cc,H,W", [(32, 64, 56, 56), (2, 3, 5, 7), (4, 16, 1, 300)])
+def test_relu_mean_plane(dev, T, N, Cc, H, W):
+    """ReLU + mean over each plane (forward and backward) in one launch each: the same bits as om_relu_fwd +
+    om_mean_axis and om_mean_axis_bwd + om_relu_bwd, which the oracle pins (mean within 1e-7, ReLU bit-exact)."""
+    rng = np.random.default_rng(N + H)
+    x = rnd(rng, N, Cc, H, W)
+    x.reshape(-1)[3] = 0.0
+    x.reshape(-1)[5] = -0.0
+    g = rnd(rng, N, Cc)
+    P = H * W
+    X, G = dev.put(x), dev.put(g)
+    Y, R, Y2 = dev.empty((N, Cc)), dev.empty(x.shape), dev.empty((N, Cc))
+    dev.call("om_relu_mean_rows", X, Y, N * Cc, P)
+    dev.call("om_relu_fwd", X, R, x.size)
+    dev.call("om_mean_axis", R, Y2, N * Cc, P, 1)
+    assert np.array_equal(dev.get(Y).view(np.uint32), dev.get(Y2).view(np.uint32))
+    r = np.maximum(x, np.float32(0.0))
+    assert scaled(dev.get(Y), r.reshape(N * Cc, P).astype(np.float64).mean(axis=1).reshape(N, Cc)) <= 1e-7
+    DX, T1, DX2 = dev.empty(x.shape, fill=0.25), dev.empty(x.shape), dev.empty(x.shape, fill=0.25)
+    dev.call("om_relu_mean_rows_bwd", G, X, DX, N * Cc, P, 1)
+    dev.call("om_mean_axis_bwd", G, T1, N * Cc, P, 1, 0)
+    dev.call("om_relu_bwd", T1, R, DX2, x.size, 1)
+    assert np.array_equal(dev.get(DX).view(np.uint32), dev.get(DX2).view(np.uint32))
+    ref = np.where(x > 0, (g / np.float32(P)).astype(np.float32)[:, :, None, None], np.float32(0)) + np.float32(0.25)
+    assert np.array_equal(dev.get(DX).view(np.uint32), ref.astype(np.float32).view(np.uint32))
 
 
 # ------------------------------------------------------------------------------------------------ CTC
