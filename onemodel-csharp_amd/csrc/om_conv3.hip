@@ -34,11 +34,11 @@ constexpr int kThreads = 256;
 constexpr int kFwdCk = 8;    // input channels per staged chunk (forward, dX)
 constexpr int kFwdPx = 128;  // output pixels per workgroup (forward, dX)
 constexpr int kWLd = kFwdCk + 4;  // row stride of the staged weights [tap][co][ci]
-// tap stride of the staged weights: BM rows plus 4 floats, so the nine taps of one channel's scattered stores start
+// tap stride of the staged weights: BM rows plus 8 floats, so the nine taps of one channel's scattered stores start
 // on different banks
 template <int BM>
 constexpr int w_tap_stride() {
-    return BM * kWLd + 4;
+    return BM * kWLd + 8;
 }
 constexpr int kDwCi = 16;    // input channels per workgroup (dW)
 constexpr int kDwCo = 64;    // output channels per workgroup (dW)
@@ -138,15 +138,16 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
     }
     // The weight float4s this thread stages: global offset without the chunk's part, and the LDS offsets of the four
     // values. Forward: float4 f is floats 4 q .. 4 q + 3 (q = f % 18) of output channel co = f / 18's 72-float run
-    // [ci][tap] of the chunk. FLIP: float4 f is floats 4 q .. (q = f % (9 BM / 4)) of the run [ci][tap] of the chunk's
-    // input channel f / (9 BM / 4) (one of the layer's output channels), over this block's BM channels.
+    // [ci][tap] of the chunk. FLIP: float4 f is floats 4 q .. (q = f / 8) of the run [ci][tap] of the chunk's input
+    // channel f % 8 (one of the layer's output channels), over this block's BM channels; the eight channels vary
+    // fastest over the lanes, so a wavefront's scattered stores of one component fall on eight-wide runs of banks.
     int wgo[NWI], wlo[NWI][4];
     floatx4 wv4[NWI];
 #pragma unroll
     for (int i = 0; i < NWI; i++) {
         const int f = threadIdx.x + i * kThreads;
         const bool ok = f < WF4;
-        const int per = FLIP ? 9 * BM / 4 : 18, row = f / per, q = f % per;
+        const int row = FLIP ? f % kFwdCk : f / 18, q = FLIP ? f / kFwdCk : f % 18;
         wgo[i] = FLIP ? (row * cout + co0) * 9 + 4 * q : (co0 + row) * cin * 9 + 4 * q;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -347,8 +348,10 @@ __global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict
     if ((int64_t)blockIdx.x >= nbw) {  // bias gradient (uniform over the block)
         const int co = (int)(((int64_t)blockIdx.x - nbw) * 64 + lane);
         double sd = 0.0;
-        if (co < cout)
+        if (co < cout) {
+#pragma unroll 8
             for (int k = k0; k < k1; k++) sd += dbp[(int64_t)k * cout + co];
+        }
         qd[w][lane] = sd;
         __syncthreads();
         if (w == 0 && co < cout) {
@@ -469,7 +472,8 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
     // forward: the layer's W [Cout][Cin][9]; dX (flip): the layer's W [Cout_l][Cin_l][9], where this call's Cin is
     // Cout_l and its Cout is Cin_l (the kernel reads it flipped and transposed)
     const int ntile = (P + kFwdPx - 1) / kFwdPx;
-    const size_t lds = sizeof(float) * (9 * (size_t)(BM * kWLd + 4) + (size_t)kFwdCk * ps);
+    const size_t lds = sizeof(float) * (9 * (size_t)(BM == 64 ? w_tap_stride<64>() : w_tap_stride<32>()) +
+                                        (size_t)kFwdCk * ps);
     const int64_t tiles = (int64_t)ntile * (Cout / BM) * N;
     // Fewer tiles than two per CU (small images): split the input channels, at least two chunks per split.
     const int chunks = Cin / kFwdCk;
