@@ -147,6 +147,12 @@ om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, co
 /* Ops.Linear forward (Ops.Layers.cs:715-733): y[rows,out] = x[rows,in] * w[out,in]^T + b[out] (b may be NULL). */
 om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
                         int out);
+/* 1 when om_linear_fwd / om_linear_bwd take their one-launch path for this shape (rows <= 256, out <= 32,
+ * rows * in * out <= 2^21: a classifier head over a small batch, whose time is launch latency): the forward is one
+ * launch, and om_linear_bwd computes dx, dw and db together in one launch, each output a single fmaf chain in
+ * increasing k (the reference fast-mode Dense.Gemm's accumulation order) and db a double sum in increasing row. A
+ * caller that groups weight gradients (om_linear_bwd_dw_group) should pass such layers to om_linear_bwd instead. */
+int om_linear_small(int rows, int in, int out);
 /* Linear backward = MatMul backward + Permute backward + bias SumTo (BackwardOps.cs:69-82, 107-118, 201-269):
  * dx = g w, dw = g^T x written directly as [out,in], db = fp64 column sums of g (computed inside the dW launch when
  * both are requested and the tile allows it). Each output pointer may be NULL; the acc_* flags add into the

@@ -42,6 +42,7 @@ _OM_SIGS = {
     "om_fill": [vp, vp, f32, i64],
     "om_gemm": [vp, ci, ci, ci, ci, ci, vp, ci, vp, ci, vp, ci, vp, ci, C.POINTER(om_batch)],
     "om_linear_fwd": [vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_linear_small": [ci, ci, ci],
     "om_linear_bwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci],
     "om_linear_fwd_resid": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_gelu_fwd": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
@@ -132,6 +133,7 @@ _OM_SIGS = {
     "om_attention_bwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
+            "om_linear_small": ci,
             "om_layernorm_bwd_chunks": ci,
             "om_stager_slot_bytes": u64}
 

@@ -7,6 +7,7 @@
 // is half empty costs as much as a full one.
 #include <cstdlib>
 #include <cstring>
+#include <utility>
 
 #include "om_gemm.hpp"
 #include "om_gemm_x.hpp"
@@ -636,6 +637,134 @@ Params dense_params(int m, int n, int k, const float *a, int64_t lda, const floa
 
 }  // namespace omg
 
+// ------------------------------------------------------------------------------------------------------------------
+// Linear layers too small for the MFMA engine to pay (rows <= 256, out <= 32, rows * in * out <= 2^21: a classifier
+// head over a small batch). Their time is launch latency, so the forward is one launch and the whole backward (dx,
+// dW, db) another. Each output is one fmaf chain over k in increasing order, as the reference's fast-mode Dense.Gemm
+// accumulates, then the bias add; the bias gradient is a double sum over rows in increasing order.
+namespace {
+using omg::floatx4;
+constexpr int kSmallRows = 256, kSmallOut = 32;
+bool linear_small(int rows, int in, int out) {
+    return rows >= 1 && rows <= kSmallRows && out >= 1 && out <= kSmallOut && in >= 1 &&
+           (int64_t)rows * in * out <= ((int64_t)1 << 21);
+}
+// y[r][o] = (sum over i of x[r][i] w[o][i]) + b[o] (+ resid[r][o]: the Linear then the residual Add, as the
+// engine's epilogue orders them): a thread per output.
+__global__ void __launch_bounds__(256) k_linear_small_fwd(const float *__restrict__ x, const float *__restrict__ w,
+                                                          const float *__restrict__ b, const float *__restrict__ resid,
+                                                          float *__restrict__ y, int rows, int in, int out) {
+    const int t = blockIdx.x * 256 + threadIdx.x;
+    if (t >= rows * out) return;
+    const int r = t / out, o = t - r * out;
+    const float *xr = x + (int64_t)r * in, *wr = w + (int64_t)o * in;
+    float acc = 0.0f;
+    // Loads run sixteen float4 ahead of the chain (which is sequential in i, as the reference's).
+    int i = 0;
+    if ((in & 3) == 0) {
+        const floatx4 *x4 = reinterpret_cast<const floatx4 *>(xr), *w4 = reinterpret_cast<const floatx4 *>(wr);
+        const int n4 = in >> 2;
+        int q = 0;
+        for (; q + 16 <= n4; q += 16) {
+            floatx4 xa[16], wa[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                xa[u] = x4[q + u];
+                wa[u] = w4[q + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc = __builtin_fmaf(xa[u][e], wa[u][e], acc);
+        }
+        for (; q < n4; q++) {
+            const floatx4 xa = x4[q], wa = w4[q];
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc = __builtin_fmaf(xa[e], wa[e], acc);
+        }
+        i = in;
+    }
+#pragma unroll 8
+    for (; i < in; i++) acc = __builtin_fmaf(xr[i], wr[i], acc);
+    float v = b ? acc + b[o] : acc;
+    if (resid) v = v + resid[t];
+    y[t] = v;
+}
+// dx[r][i] (+)= sum over o of g[r][o] w[o][i]; dw[o][i] (+)= sum over r of g[r][o] x[r][i]; db[o] (+)= (float) double
+// sum over r of g[r][o]. A thread per input column i (g staged in LDS, the column's weights in registers); OUT is
+// the layer's output count, a compile-time constant so the loops over it unroll and their LDS reads batch.
+template <int OUT>
+__global__ void __launch_bounds__(256) k_linear_small_bwd(const float *__restrict__ g, const float *__restrict__ x,
+                                                          const float *__restrict__ w, float *dx, float *dw, float *db,
+                                                          int rows, int in, int ax, int aw, int ab) {
+    __shared__ float gs[kSmallRows * OUT];
+    for (int e = threadIdx.x; e < rows * OUT; e += 256) gs[e] = g[e];
+    __syncthreads();
+    if (blockIdx.x == 0 && db && (int)threadIdx.x < OUT) {
+        const int o = threadIdx.x;
+        double s = 0.0;
+        for (int r = 0; r < rows; r++) s += gs[r * OUT + o];
+        const float v = (float)s;
+        db[o] = ab ? db[o] + v : v;
+    }
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= in) return;
+    if (dx) {
+        float wv[OUT];
+#pragma unroll
+        for (int o = 0; o < OUT; o++) wv[o] = w[(int64_t)o * in + i];
+#pragma unroll 2
+        for (int r = 0; r < rows; r++) {
+            float gv[OUT];
+#pragma unroll
+            for (int o = 0; o < OUT; o++) gv[o] = gs[r * OUT + o];
+            float acc = 0.0f;
+#pragma unroll
+            for (int o = 0; o < OUT; o++) acc = __builtin_fmaf(gv[o], wv[o], acc);
+            float *d = dx + (int64_t)r * in + i;
+            *d = ax ? *d + acc : acc;
+        }
+    }
+    if (dw) {
+        float acc[OUT];
+#pragma unroll
+        for (int o = 0; o < OUT; o++) acc[o] = 0.0f;
+        // x's column loads run eight rows ahead of the sums
+        int r = 0;
+        for (; r + 8 <= rows; r += 8) {
+            float xv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) xv[u] = x[(int64_t)(r + u) * in + i];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gs[(r + u) * OUT + o], xv[u], acc[o]);
+        }
+        for (; r < rows; r++) {
+            const float xv = x[(int64_t)r * in + i];
+#pragma unroll
+            for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gs[r * OUT + o], xv, acc[o]);
+        }
+#pragma unroll
+        for (int o = 0; o < OUT; o++) {
+            float *d = dw + (int64_t)o * in + i;
+            *d = aw ? *d + acc[o] : acc[o];
+        }
+    }
+}
+template <int OUT>
+void launch_small_bwd(hipStream_t st, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
+                      int rows, int in, int ax, int aw, int ab) {
+    hipLaunchKernelGGL(k_linear_small_bwd<OUT>, dim3((unsigned)((in + 255) / 256)), dim3(256), 0, st, g, x, w, dx, dw,
+                       db, rows, in, ax, aw, ab);
+}
+template <int... OS>
+void small_bwd_dispatch(std::integer_sequence<int, OS...>, int out, hipStream_t st, const float *g, const float *x,
+                        const float *w, float *dx, float *dw, float *db, int rows, int in, int ax, int aw, int ab) {
+    ((out == OS + 1 ? (launch_small_bwd<OS + 1>(st, g, x, w, dx, dw, db, rows, in, ax, aw, ab), 0) : 0), ...);
+}
+}  // namespace
+
 extern "C" {
 
 om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, const float *a, int lda,
@@ -667,10 +796,17 @@ om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, co
     return omg::launch_dense(ctx, p, trans_a != 0, trans_b != 0, nb, "om_gemm");
 }
 
+int om_linear_small(int rows, int in, int out) { return linear_small(rows, in, out) ? 1 : 0; }
+
 om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
                         int out) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && rows >= 0 && in > 0 && out > 0, "om_linear_fwd: bad arguments");
+    if (linear_small(rows, in, out)) {
+        hipLaunchKernelGGL(k_linear_small_fwd, dim3((unsigned)((rows * out + 255) / 256)), dim3(256), 0,
+                           om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
+        return OM_LAUNCH_CHECK(ctx, "om_linear_fwd");
+    }
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
     p.bias = b;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd");
@@ -681,6 +817,12 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && rows >= 0 && in > 0 && out > 0, "om_linear_bwd: bad arguments");
     OM_REQUIRE(ctx, (!dx || w) && (!dw || x), "om_linear_bwd: a needed saved tensor is NULL");
+    if (linear_small(rows, in, out)) {
+        if (!dx && !dw && !db) return OM_OK;
+        small_bwd_dispatch(std::make_integer_sequence<int, kSmallOut>{}, out, om::cur_stream(ctx), g, x, w, dx, dw, db,
+                           rows, in, acc_dx, acc_dw, acc_db);
+        return OM_LAUNCH_CHECK(ctx, "om_linear_bwd");
+    }
     om_status s = OM_OK;
     if (dx) {
         omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dx, in);
@@ -704,6 +846,11 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
                               float *y, int rows, int in, int out) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && resid && rows >= 0 && in > 0 && out > 0, "om_linear_fwd_resid: bad arguments");
+    if (linear_small(rows, in, out)) {  // the same products as om_linear_fwd's for this shape
+        hipLaunchKernelGGL(k_linear_small_fwd, dim3((unsigned)((rows * out + 255) / 256)), dim3(256), 0,
+                           om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
+        return OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid");
+    }
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
     p.bias = b;
     p.resid = resid;

@@ -330,6 +330,13 @@ Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
         attach(y, "Linear", ins, [rows, in, out](Engine &e, Record &r, const float *g) {
             int ax, aw, ab = 0;
             float *dx = e.dest(r, 0, &ax);
+            if (om_linear_small(rows, in, out)) {  // dx, dw and db in one launch
+                float *dw = e.dest(r, 1, &aw);
+                float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+                OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw,
+                                  ab));
+                return;
+            }
             if (dx) OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, in, out,
                                       ax, 0, 0));
             float *dw = e.dest(r, 1, &aw);

@@ -106,6 +106,8 @@ def test_gemm_rejects_bad_shapes(dev):
 
 # ------------------------------------------------------------------------------------------------ Linear
 @pytest.mark.parametrize("rows,inf,outf", [(64, 784, 256), (64, 256, 10), (4096, 384, 1536), (300, 37, 9),
+                                           # one-launch small layers (C2's head, bounds of the small path)
+                                           (32, 64, 10), (256, 37, 32), (1, 5, 1), (256, 300, 27),
                                            (512, 256, 128), (4096, 1536, 384), (4096, 384, 1152),
                                            # C5 at full size: FFN pair, attention output, packed q|k|v, token head
                                            (4096, 768, 3072), (4096, 3072, 768), (4096, 768, 768), (4096, 768, 2304),
@@ -125,6 +127,11 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     assert scaled(dev.get(DX), dx_r) <= TOL
     assert scaled(dev.get(DW), dw_r) <= TOL
     assert scaled(dev.get(DB), db_r) <= 1e-7  # fp64 column sums: equal after rounding
+    if dev.ctx.L.om_linear_small(rows, inf, outf):
+        # the one-launch path accumulates in the reference's order (one fmaf chain in increasing k, then the bias;
+        # db in double by increasing row): the oracle's bits exactly
+        for got, ref in ((Y, y_ref), (DX, dx_r), (DW, dw_r), (DB, db_r)):
+            assert np.array_equal(dev.get(got).view(np.uint32), ref.view(np.uint32))
     # accumulate into existing leaves
     dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 1, 1, 1)
     assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
