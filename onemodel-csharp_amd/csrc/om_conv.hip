@@ -399,6 +399,40 @@ __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__rest
         dx[e] = acc ? dx[e] + s : s;
     }
 }
+// The same for windows that tile the input exactly (stride = window, no padding, H and W multiples of the window:
+// every input element lies in exactly one window): a thread per window writes its KH x KW inputs, the window's
+// gradient at the saved index (0 + g, as the gather's sum starting from zero gives) and zero elsewhere.
+__global__ void k_maxpool_bwd_tiled(const float *__restrict__ g, const int32_t *__restrict__ idx,
+                                    float *__restrict__ dx, int planes, int H, int W, int OH, int OW, int KH, int KW,
+                                    int acc, const float *__restrict__ relu_y) {
+    const int total = planes * OH * OW;
+    for (int o = blockIdx.x * blockDim.x + threadIdx.x; o < total; o += gridDim.x * blockDim.x) {
+        const int ox = o % OW, t = o / OW, oy = t % OH, pl = t / OH;
+        const int win = idx[o];
+        const float gv = 0.0f + g[o];
+        for (int ky = 0; ky < KH; ky++) {
+            const int e0 = (pl * H + oy * KH + ky) * W + ox * KW;
+            for (int kx = 0; kx < KW; kx++) {
+                const int e = e0 + kx;
+                float v = e == win ? gv : 0.0f;
+                if (relu_y) v = relu_y[e] > 0.0f ? v : 0.0f;
+                dx[e] = acc ? dx[e] + v : v;
+            }
+        }
+    }
+}
+// Launches the tiled form where it applies, else the gather.
+void maxpool_bwd_launch(hipStream_t st, const float *g, const int32_t *idx, float *dx, int N, int C, int H, int W,
+                        int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW, int acc, const float *relu_y) {
+    if (SH == KH && SW == KW && PH == 0 && PW == 0 && H == OH * KH && W == OW * KW &&
+        (int64_t)N * C * H * W <= INT32_MAX) {
+        hipLaunchKernelGGL(k_maxpool_bwd_tiled, dim3(om::grid1d((int64_t)N * C * OH * OW, 256, 1 << 20)), dim3(256), 0,
+                           st, g, idx, dx, N * C, H, W, OH, OW, KH, KW, acc, relu_y);
+        return;
+    }
+    hipLaunchKernelGGL(k_maxpool_bwd, dim3(om::grid1d((int64_t)N * C * H * W, 256, 1 << 20)), dim3(256), 0, st, g, idx,
+                       dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, acc, relu_y);
+}
 
 }  // namespace
 
@@ -564,8 +598,7 @@ om_status om_maxpool_bwd(om_ctx *ctx, const float *g, const int32_t *idx, float 
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && idx && dx && N > 0 && C > 0 && H > 0 && W > 0 && OH > 0 && OW > 0 && SH > 0 && SW > 0,
                "om_maxpool_bwd: bad arguments");
-    hipLaunchKernelGGL(k_maxpool_bwd, dim3(om::grid1d((int64_t)N * C * H * W, 256, 1 << 20)), dim3(256), 0,
-                       ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, nullptr);
+    maxpool_bwd_launch(ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, nullptr);
     return OM_LAUNCH_CHECK(ctx, "om_maxpool_bwd");
 }
 
@@ -575,8 +608,7 @@ om_status om_maxpool_relu_bwd(om_ctx *ctx, const float *g, const int32_t *idx, c
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && idx && y && dx && N > 0 && C > 0 && H > 0 && W > 0 && OH > 0 && OW > 0 && SH > 0 && SW > 0,
                "om_maxpool_relu_bwd: bad arguments");
-    hipLaunchKernelGGL(k_maxpool_bwd, dim3(om::grid1d((int64_t)N * C * H * W, 256, 1 << 20)), dim3(256), 0,
-                       ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, y);
+    maxpool_bwd_launch(ctx->stream, g, idx, dx, N, C, H, W, OH, OW, KH, KW, SH, SW, PH, PW, accumulate, y);
     return OM_LAUNCH_CHECK(ctx, "om_maxpool_relu_bwd");
 }
 

@@ -335,15 +335,17 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
 // then added in order, so the result depends only on the shape. (Many slots per element: one thread walking them all
 // would keep too few loads in flight.)
 // The blocks after the weights' (when dbp is given) finish the bias gradient the same way, in double: db[co] (+)=
-// (float) of the four quarters' sums of dbp[slot][co] over the slots, added in order.
-__global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout, int cin,
-                                                         float *dw, int acc, const double *__restrict__ dbp,
-                                                         float *db) {
-    __shared__ float qs[4][64];
-    __shared__ double qd[4][64];
+// (float) of the quarters' sums of dbp[slot][co] over the slots, added in order. NW wavefronts split the slots (16
+// where each output has hundreds of them and few blocks run: the chains of loads are then NW times shorter).
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout,
+                                                             int cin, float *dw, int acc,
+                                                             const double *__restrict__ dbp, float *db) {
+    __shared__ float qs[NW][64];
+    __shared__ double qd[NW][64];
     const int64_t total = (int64_t)cout * 9 * cin;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int k0 = (int)((int64_t)slots * w / 4), k1 = (int)((int64_t)slots * (w + 1) / 4);
+    const int k0 = (int)((int64_t)slots * w / NW), k1 = (int)((int64_t)slots * (w + 1) / NW);
     const int64_t nbw = (total + 63) / 64;
     if ((int64_t)blockIdx.x >= nbw) {  // bias gradient (uniform over the block)
         const int co = (int)(((int64_t)blockIdx.x - nbw) * 64 + lane);
@@ -355,7 +357,10 @@ __global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict
         qd[w][lane] = sd;
         __syncthreads();
         if (w == 0 && co < cout) {
-            const float v = (float)(((qd[0][lane] + qd[1][lane]) + qd[2][lane]) + qd[3][lane]);
+            double t = qd[0][lane];
+#pragma unroll
+            for (int q = 1; q < NW; q++) t += qd[q][lane];
+            const float v = (float)t;
             db[co] = acc ? db[co] + v : v;
         }
         return;
@@ -369,7 +374,9 @@ __global__ void __launch_bounds__(256) k_conv3_dw_reduce(const float *__restrict
     qs[w][lane] = s;
     __syncthreads();
     if (w == 0 && e < total) {
-        const float v = ((qs[0][lane] + qs[1][lane]) + qs[2][lane]) + qs[3][lane];
+        float v = qs[0][lane];
+#pragma unroll
+        for (int q = 1; q < NW; q++) v += qs[q][lane];
         const int ci = (int)(e % cin);
         const int64_t ct = e / cin;
         const int tap = (int)(ct % 9), co = (int)(ct / 9);
@@ -532,8 +539,8 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *
         hipLaunchKernelGGL(k_conv3_dw_c1, dim3((unsigned)blocks), dim3(64 * (Cout / 8)), lds, ctx->stream, g, x, part,
                            Cout, H, W, br, nb, dbp);
         const unsigned rb = (unsigned)((Cout * 9 + 63) / 64 + (db ? (Cout + 63) / 64 : 0));
-        hipLaunchKernelGGL(k_conv3_dw_reduce, dim3(rb), dim3(256), 0, ctx->stream, part, blocks, Cout, 1, dw, acc, dbp,
-                           db);
+        hipLaunchKernelGGL(k_conv3_dw_reduce<16>, dim3(rb), dim3(1024), 0, ctx->stream, part, blocks, Cout, 1, dw, acc,
+                           dbp, db);
         *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
         return true;
     }
@@ -565,8 +572,12 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *
 #undef OMW3
     const int64_t total = (int64_t)Cout * 9 * Cin;
     const unsigned rb = (unsigned)((total + 63) / 64 + (db ? (Cout + 63) / 64 : 0));
-    hipLaunchKernelGGL(k_conv3_dw_reduce, dim3(rb), dim3(256), 0, ctx->stream, part, slots, Cout, Cin, dw, acc, dbp,
-                       db);
+    if (slots >= 256 && rb < (unsigned)ctx->num_cus)
+        hipLaunchKernelGGL(k_conv3_dw_reduce<16>, dim3(rb), dim3(1024), 0, ctx->stream, part, slots, Cout, Cin, dw, acc,
+                           dbp, db);
+    else
+        hipLaunchKernelGGL(k_conv3_dw_reduce<4>, dim3(rb), dim3(256), 0, ctx->stream, part, slots, Cout, Cin, dw, acc,
+                           dbp, db);
     *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_bwd dw");
     return true;
 }

@@ -321,8 +321,24 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
     const bool none = len == 0 || (isinf(nll) && nll > 0);
     double scale = reduction == 0 ? (double)g[b] : (double)g[0];
     if (reduction == 1) scale = scale / (double)(L > 1 ? L : 1) / (double)B;
-    for (int idx = threadIdx.x; idx < T * C; idx += blockDim.x) {
-        const int t = idx / C, c = idx - t * C;
+    // Jobs 0 .. T - 1 are the blank class's entries (its chain runs over all L + 1 even positions), one per thread of
+    // the first wavefronts; the other classes' entries (at most a few positions each) follow in (t, c) order, so no
+    // wavefront holds more than its share of long chains.
+    const bool blank_ok = blank >= 0 && blank < C;
+    for (int job = threadIdx.x; job < T * C; job += blockDim.x) {
+        int t, c;
+        if (!blank_ok) {
+            t = job / C;
+            c = job - t * C;
+        } else if (job < T) {
+            t = job;
+            c = blank;
+        } else {
+            const int k = job - T;
+            t = k / (C - 1);
+            const int cc = k - t * (C - 1);
+            c = cc < blank ? cc : cc + 1;
+        }
         float *d = dlp + ((int64_t)t * B + b) * C + c;
         float v = acc ? *d : 0.0f;
         if (!none && t < len) {
