@@ -119,8 +119,21 @@ struct PostTo {
 };
 __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ part, int np, float *__restrict__ out,
                                                   double divisor, PostTo post) {
+    // Lane l adds part[l], part[l + 64], ... in that order; the loads of a round of 16 are all issued before the
+    // first add (the partials were just written on every XCD, so each load waits for memory).
+    constexpr int R = 16;
     double acc = 0.0;
-    for (int i = threadIdx.x; i < np; i += 64) acc += part[i];
+    for (int base = 0; base < np; base += 64 * R) {
+        double v[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int i = base + 64 * u + (int)threadIdx.x;
+            v[u] = i < np ? part[i] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (base + 64 * u + (int)threadIdx.x < np) acc += v[u];
+    }
     acc = omd::wave_sum(acc);
     if (threadIdx.x == 0) {
         const float v = divisor > 0.0 ? (float)(acc / divisor) : (float)acc;

@@ -650,113 +650,181 @@ bool linear_small(int rows, int in, int out) {
            (int64_t)rows * in * out <= ((int64_t)1 << 21);
 }
 // y[r][o] = (sum over i of x[r][i] w[o][i]) + b[o] (+ resid[r][o]: the Linear then the residual Add, as the
-// engine's epilogue orders them): a thread per output.
+// engine's epilogue orders them): a thread per output, each an fmaf chain over i in increasing order. A workgroup
+// takes small_rt(out) consecutive rows with all their outputs; its x rows and all of w pass through LDS in chunks of
+// kSmallKC columns, loaded by the whole workgroup (a few loads per thread, all in flight together), the next chunk's
+// loads issued before the chains over the current one run. VEC: in % 4 == 0 and 16-byte aligned x and w.
+constexpr int kSmallKC = 128, kSmallLd = kSmallKC + 4, kSmallRtMax = 64;
+__host__ __device__ constexpr int small_rt(int out) { return 256 / out < kSmallRtMax ? 256 / out : kSmallRtMax; }
+constexpr int small_stage_rows() {
+    int m = 0;
+    for (int o = 1; o <= kSmallOut; o++) m = small_rt(o) + o > m ? small_rt(o) + o : m;
+    return m;
+}
+constexpr int kSmallStage = small_stage_rows();  // x rows plus w rows of a workgroup, at most
+template <bool VEC>
 __global__ void __launch_bounds__(256) k_linear_small_fwd(const float *__restrict__ x, const float *__restrict__ w,
                                                           const float *__restrict__ b, const float *__restrict__ resid,
                                                           float *__restrict__ y, int rows, int in, int out) {
-    const int t = blockIdx.x * 256 + threadIdx.x;
-    if (t >= rows * out) return;
-    const int r = t / out, o = t - r * out;
-    const float *xr = x + (int64_t)r * in, *wr = w + (int64_t)o * in;
-    float acc = 0.0f;
-    // Loads run sixteen float4 ahead of the chain (which is sequential in i, as the reference's).
-    int i = 0;
-    if ((in & 3) == 0) {
-        const floatx4 *x4 = reinterpret_cast<const floatx4 *>(xr), *w4 = reinterpret_cast<const floatx4 *>(wr);
-        const int n4 = in >> 2;
-        int q = 0;
-        for (; q + 16 <= n4; q += 16) {
-            floatx4 xa[16], wa[16];
+    constexpr int Q = VEC ? kSmallKC / 4 : kSmallKC;  // load items per staged row and chunk
+    constexpr int PER = (kSmallStage * Q + 255) / 256;
+    __shared__ __attribute__((aligned(16))) float st[kSmallStage * kSmallLd];
+    const int r0 = blockIdx.x * small_rt(out), nr = min(small_rt(out), rows - r0), srows = nr + out;
+    const int tid = threadIdx.x, rl = tid / out, o = tid - rl * out;
+    const bool live = rl < nr;
+    // staged row s: x row r0 + s for s < nr, then w row s - nr
+    auto src = [&](int s) { return s < nr ? x + (int64_t)(r0 + s) * in : w + (int64_t)(s - nr) * in; };
+    floatx4 rv[VEC ? PER : 1];
+    float rs[VEC ? 1 : PER];
+    auto load = [&](int k0, int kn) {
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                xa[u] = x4[q + u];
-                wa[u] = w4[q + u];
+        for (int u = 0; u < PER; u++) {
+            const int f = tid + 256 * u, s = f / Q, q = f - s * Q;
+            if (VEC) {
+                if (s < srows && 4 * q < kn) rv[u] = *reinterpret_cast<const floatx4 *>(src(s) + k0 + 4 * q);
+            } else {
+                if (s < srows && q < kn) rs[u] = src(s)[k0 + q];
             }
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc = __builtin_fmaf(xa[u][e], wa[u][e], acc);
         }
-        for (; q < n4; q++) {
-            const floatx4 xa = x4[q], wa = w4[q];
+    };
+    auto stage = [&](int kn) {
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc = __builtin_fmaf(xa[e], wa[e], acc);
+        for (int u = 0; u < PER; u++) {
+            const int f = tid + 256 * u, s = f / Q, q = f - s * Q;
+            if (VEC) {
+                if (s < srows && 4 * q < kn) *reinterpret_cast<floatx4 *>(&st[s * kSmallLd + 4 * q]) = rv[u];
+            } else {
+                if (s < srows && q < kn) st[s * kSmallLd + q] = rs[u];
+            }
         }
-        i = in;
-    }
+    };
+    const int nchunk = (in + kSmallKC - 1) / kSmallKC;
+    load(0, min(kSmallKC, in));
+    float acc = 0.0f;
+    const float *xs = st + rl * kSmallLd, *ws = st + (nr + o) * kSmallLd;
+    for (int c = 0; c < nchunk; c++) {
+        const int kn = min(kSmallKC, in - c * kSmallKC);
+        stage(kn);
+        __syncthreads();
+        if (c + 1 < nchunk) load((c + 1) * kSmallKC, min(kSmallKC, in - (c + 1) * kSmallKC));
+        if (live) {
+            int k = 0;
 #pragma unroll 8
-    for (; i < in; i++) acc = __builtin_fmaf(xr[i], wr[i], acc);
+            for (; k + 4 <= kn; k += 4) {
+                const floatx4 a = *reinterpret_cast<const floatx4 *>(xs + k);
+                const floatx4 bb = *reinterpret_cast<const floatx4 *>(ws + k);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc = __builtin_fmaf(a[e], bb[e], acc);
+            }
+            for (; k < kn; k++) acc = __builtin_fmaf(xs[k], ws[k], acc);
+        }
+        __syncthreads();
+    }
+    if (!live) return;
+    const int t = (r0 + rl) * out + o;
     float v = b ? acc + b[o] : acc;
     if (resid) v = v + resid[t];
     y[t] = v;
 }
-// dx[r][i] (+)= sum over o of g[r][o] w[o][i]; dw[o][i] (+)= sum over r of g[r][o] x[r][i]; db[o] (+)= (float) double
-// sum over r of g[r][o]. A thread per input column i (g staged in LDS, the column's weights in registers); OUT is
-// the layer's output count, a compile-time constant so the loops over it unroll and their LDS reads batch.
+void launch_small_fwd(hipStream_t st, const float *x, const float *w, const float *b, const float *resid, float *y,
+                      int rows, int in, int out) {
+    const dim3 grid((unsigned)((rows + small_rt(out) - 1) / small_rt(out)));
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (in % 4 == 0 && al(x) && al(w))
+        hipLaunchKernelGGL(k_linear_small_fwd<true>, grid, dim3(256), 0, st, x, w, b, resid, y, rows, in, out);
+    else
+        hipLaunchKernelGGL(k_linear_small_fwd<false>, grid, dim3(256), 0, st, x, w, b, resid, y, rows, in, out);
+}
+// The backward over a grid of (input columns / 256, 1 + row blocks): workgroups with blockIdx.y = 0 form
+// dw[o][i] (+)= sum over r of g[r][o] x[r][i] (a thread per input column i, an fmaf chain per o over r in increasing
+// order, x's column loads running kSmallRc rows ahead) and db[o] (+)= (float) double sum over r of g[r][o]; the others
+// form dx[r][i] (+)= sum over o of g[r][o] w[o][i] for kSmallDxRows rows each (an fmaf chain over o in increasing
+// order). Every lane of a workgroup reads the same g[r][o] at the same time: uniform addresses of read-only memory,
+// which the compiler turns into scalar loads (no LDS staging, no barrier). OUT is the layer's output count, a
+// compile-time constant so the loops over it unroll.
+constexpr int kSmallDxRows = 16, kSmallRc = 32;
 template <int OUT>
 __global__ void __launch_bounds__(256) k_linear_small_bwd(const float *__restrict__ g, const float *__restrict__ x,
-                                                          const float *__restrict__ w, float *dx, float *dw, float *db,
-                                                          int rows, int in, int ax, int aw, int ab) {
-    __shared__ float gs[kSmallRows * OUT];
-    for (int e = threadIdx.x; e < rows * OUT; e += 256) gs[e] = g[e];
-    __syncthreads();
-    if (blockIdx.x == 0 && db && (int)threadIdx.x < OUT) {
-        const int o = threadIdx.x;
-        double s = 0.0;
-        for (int r = 0; r < rows; r++) s += gs[r * OUT + o];
-        const float v = (float)s;
-        db[o] = ab ? db[o] + v : v;
-    }
+                                                          const float *__restrict__ w, float *__restrict__ dx,
+                                                          float *__restrict__ dw, float *__restrict__ db, int rows,
+                                                          int in, int ax, int aw, int ab) {
     const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= in) return;
-    if (dx) {
+    if (blockIdx.y > 0) {
+        const int r0 = (blockIdx.y - 1) * kSmallDxRows, nr = min(kSmallDxRows, rows - r0);
+        if (i >= in) return;
         float wv[OUT];
 #pragma unroll
         for (int o = 0; o < OUT; o++) wv[o] = w[(int64_t)o * in + i];
-#pragma unroll 2
-        for (int r = 0; r < rows; r++) {
-            float gv[OUT];
-#pragma unroll
-            for (int o = 0; o < OUT; o++) gv[o] = gs[r * OUT + o];
+#pragma unroll 4
+        for (int r = 0; r < nr; r++) {
+            const float *gr = g + (int64_t)(r0 + r) * OUT;
             float acc = 0.0f;
 #pragma unroll
-            for (int o = 0; o < OUT; o++) acc = __builtin_fmaf(gv[o], wv[o], acc);
-            float *d = dx + (int64_t)r * in + i;
+            for (int o = 0; o < OUT; o++) acc = __builtin_fmaf(gr[o], wv[o], acc);
+            float *d = dx + (int64_t)(r0 + r) * in + i;
             *d = ax ? *d + acc : acc;
         }
+        return;
     }
-    if (dw) {
-        float acc[OUT];
+    if (blockIdx.x == 0 && db && (int)threadIdx.x < OUT) {
+        // rows in increasing order, the loads of sixteen issued before their adds
+        const int o = threadIdx.x;
+        double s = 0.0;
+        for (int r0 = 0; r0 < rows; r0 += 16) {
+            float v[16];
 #pragma unroll
-        for (int o = 0; o < OUT; o++) acc[o] = 0.0f;
-        // x's column loads run eight rows ahead of the sums
-        int r = 0;
-        for (; r + 8 <= rows; r += 8) {
-            float xv[8];
+            for (int u = 0; u < 16; u++) v[u] = g[(int64_t)min(r0 + u, rows - 1) * OUT + o];
 #pragma unroll
-            for (int u = 0; u < 8; u++) xv[u] = x[(int64_t)(r + u) * in + i];
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-#pragma unroll
-                for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gs[(r + u) * OUT + o], xv[u], acc[o]);
+            for (int u = 0; u < 16; u++)
+                if (r0 + u < rows) s += v[u];
         }
-        for (; r < rows; r++) {
-            const float xv = x[(int64_t)r * in + i];
+        const float v = (float)s;
+        db[o] = ab ? db[o] + v : v;
+    }
+    if (!dw || i >= in) return;
+    // rows past the end load the last row again (never used), so every load is unconditional
+    float xa[kSmallRc], xb[kSmallRc];
+    auto ld = [&](float(&d)[kSmallRc], int rb) {
 #pragma unroll
-            for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gs[r * OUT + o], xv, acc[o]);
-        }
+        for (int u = 0; u < kSmallRc; u++) d[u] = x[(int64_t)min(rb + u, rows - 1) * in + i];
+    };
+    float acc[OUT];
 #pragma unroll
-        for (int o = 0; o < OUT; o++) {
-            float *d = dw + (int64_t)o * in + i;
-            *d = aw ? *d + acc[o] : acc[o];
+    for (int o = 0; o < OUT; o++) acc[o] = 0.0f;
+    auto use = [&](const float(&d)[kSmallRc], int rb) {
+        const float *gr = g + (int64_t)rb * OUT;
+        if (rb + kSmallRc <= rows) {
+#pragma unroll
+            for (int u = 0; u < kSmallRc; u++)
+#pragma unroll
+                for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gr[u * OUT + o], d[u], acc[o]);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kSmallRc; u++) {
+                if (rb + u >= rows) break;
+#pragma unroll
+                for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gr[u * OUT + o], d[u], acc[o]);
+            }
         }
+    };
+    ld(xa, 0);
+    for (int rb = 0; rb < rows; rb += 2 * kSmallRc) {
+        if (rb + kSmallRc < rows) ld(xb, rb + kSmallRc);
+        use(xa, rb);
+        if (rb + 2 * kSmallRc < rows) ld(xa, rb + 2 * kSmallRc);
+        if (rb + kSmallRc < rows) use(xb, rb + kSmallRc);
+    }
+#pragma unroll
+    for (int o = 0; o < OUT; o++) {
+        float *d = dw + (int64_t)o * in + i;
+        *d = aw ? *d + acc[o] : acc[o];
     }
 }
 template <int OUT>
 void launch_small_bwd(hipStream_t st, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
                       int rows, int in, int ax, int aw, int ab) {
-    hipLaunchKernelGGL(k_linear_small_bwd<OUT>, dim3((unsigned)((in + 255) / 256)), dim3(256), 0, st, g, x, w, dx, dw,
-                       db, rows, in, ax, aw, ab);
+    const dim3 grid((unsigned)((in + 255) / 256), 1u + (dx ? (unsigned)((rows + kSmallDxRows - 1) / kSmallDxRows) : 0u));
+    hipLaunchKernelGGL(k_linear_small_bwd<OUT>, grid, dim3(256), 0, st, g, x, w, dx, dw, db, rows, in, ax, aw, ab);
 }
 template <int... OS>
 void small_bwd_dispatch(std::integer_sequence<int, OS...>, int out, hipStream_t st, const float *g, const float *x,
@@ -803,8 +871,7 @@ om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && rows >= 0 && in > 0 && out > 0, "om_linear_fwd: bad arguments");
     if (linear_small(rows, in, out)) {
-        hipLaunchKernelGGL(k_linear_small_fwd, dim3((unsigned)((rows * out + 255) / 256)), dim3(256), 0,
-                           om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
+        launch_small_fwd(om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd");
     }
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
@@ -847,8 +914,7 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && resid && rows >= 0 && in > 0 && out > 0, "om_linear_fwd_resid: bad arguments");
     if (linear_small(rows, in, out)) {  // the same products as om_linear_fwd's for this shape
-        hipLaunchKernelGGL(k_linear_small_fwd, dim3((unsigned)((rows * out + 255) / 256)), dim3(256), 0,
-                           om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
+        launch_small_fwd(om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid");
     }
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);

@@ -446,15 +446,34 @@ __global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ lo
     __syncthreads();
     double acc = 0.0;
     double cnt = 0.0;
-    for (int i = threadIdx.x; i < rows; i += kBlock) {
-        int t = tg[i];
-        if (t == ignore) continue;
-        if ((unsigned)t >= (unsigned)cols) {
-            atomicMin(&shbad, i);
-            continue;
+    // Rows i = threadIdx.x + kBlock u in increasing u, eight at a time: the eight targets load together, then the
+    // eight gathered log-probabilities, then the sums run in row order.
+    constexpr int R = 8;
+    for (int base = 0; base < rows; base += kBlock * R) {
+        int t[R];
+        float lp[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int i = base + kBlock * u + (int)threadIdx.x;
+            t[u] = i < rows ? tg[i] : ignore;
         }
-        acc -= (double)logp[(int64_t)i * cols + t];
-        cnt += 1.0;
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int i = base + kBlock * u + (int)threadIdx.x;
+            const bool use = i < rows && t[u] != ignore && (unsigned)t[u] < (unsigned)cols;
+            lp[u] = use ? logp[(int64_t)i * cols + t[u]] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int i = base + kBlock * u + (int)threadIdx.x;
+            if (i >= rows || t[u] == ignore) continue;
+            if ((unsigned)t[u] >= (unsigned)cols) {
+                atomicMin(&shbad, i);
+                continue;
+            }
+            acc -= (double)lp[u];
+            cnt += 1.0;
+        }
     }
     double total = omd::block_sum<kBlock / 64>(acc, sh);
     double count = omd::block_sum<kBlock / 64>(cnt, sh);
