@@ -525,6 +525,11 @@ static om_status launch_group_reduce(om_ctx *ctx, const GroupParams &g, int spli
     return OM_LAUNCH_CHECK(ctx, "grouped reduce");
 }
 
+// A weight gradient the grouped launch can take: whole 64 x 64 tiles over 16-byte aligned operands.
+static bool dw_groupable(const om_linear_dw &d) {
+    auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+    return d.dw && d.out % 64 == 0 && d.in % 64 == 0 && al(d.g) && al(d.x) && al(d.dw);
+}
 static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int rows, int ncs, const om_column_sum *cs,
                             om_status *st) {
     *st = OM_OK;
@@ -532,8 +537,7 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
     bool n96 = true;
     for (int i = 0; i < count; i++) {
         const om_linear_dw &d = it[i];
-        auto al = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
-        if (!d.dw || d.out % 64 || d.in % 64 || !al(d.g) || !al(d.x) || !al(d.dw)) return false;
+        if (!dw_groupable(d)) return false;
         if (d.in % 96) n96 = false;
     }
     // 64 x 64 tiles, split until there are about six workgroups per CU (measured on the four C3 weight gradients:
@@ -644,7 +648,7 @@ Params dense_params(int m, int n, int k, const float *a, int64_t lda, const floa
 // accumulates, then the bias add; the bias gradient is a double sum over rows in increasing order.
 namespace {
 using omg::floatx4;
-constexpr int kSmallRows = 256, kSmallOut = 32;
+constexpr int kSmallRows = 256, kSmallOut = 32, kNarrowOut = 64, kNarrowIn = 8192;
 bool linear_small(int rows, int in, int out) {
     return rows >= 1 && rows <= kSmallRows && out >= 1 && out <= kSmallOut && in >= 1 &&
            (int64_t)rows * in * out <= ((int64_t)1 << 21);
@@ -658,7 +662,7 @@ constexpr int kSmallKC = 128, kSmallLd = kSmallKC + 4, kSmallRtMax = 64;
 __host__ __device__ constexpr int small_rt(int out) { return 256 / out < kSmallRtMax ? 256 / out : kSmallRtMax; }
 constexpr int small_stage_rows() {
     int m = 0;
-    for (int o = 1; o <= kSmallOut; o++) m = small_rt(o) + o > m ? small_rt(o) + o : m;
+    for (int o = 1; o <= kNarrowOut; o++) m = small_rt(o) + o > m ? small_rt(o) + o : m;
     return m;
 }
 constexpr int kSmallStage = small_stage_rows();  // x rows plus w rows of a workgroup, at most
@@ -674,49 +678,86 @@ __global__ void __launch_bounds__(256) k_linear_small_fwd(const float *__restric
     const bool live = rl < nr;
     // staged row s: x row r0 + s for s < nr, then w row s - nr
     auto src = [&](int s) { return s < nr ? x + (int64_t)(r0 + s) * in : w + (int64_t)(s - nr) * in; };
-    floatx4 rv[VEC ? PER : 1];
-    float rs[VEC ? 1 : PER];
-    auto load = [&](int k0, int kn) {
+    // two register sets: the loads of chunk c + 2 are in flight while chunk c is multiplied
+    floatx4 rv[2][VEC ? PER : 1];
+    float rs[2][VEC ? 1 : PER];
+    auto load = [&](int set, int c) {
+        const int k0 = c * kSmallKC, kn = min(kSmallKC, in - k0);
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int f = tid + 256 * u, s = f / Q, q = f - s * Q;
             if (VEC) {
-                if (s < srows && 4 * q < kn) rv[u] = *reinterpret_cast<const floatx4 *>(src(s) + k0 + 4 * q);
+                if (s < srows && 4 * q < kn) rv[set][u] = *reinterpret_cast<const floatx4 *>(src(s) + k0 + 4 * q);
             } else {
-                if (s < srows && q < kn) rs[u] = src(s)[k0 + q];
+                if (s < srows && q < kn) rs[set][u] = src(s)[k0 + q];
             }
         }
     };
-    auto stage = [&](int kn) {
+    auto stage = [&](int set, int kn) {
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int f = tid + 256 * u, s = f / Q, q = f - s * Q;
             if (VEC) {
-                if (s < srows && 4 * q < kn) *reinterpret_cast<floatx4 *>(&st[s * kSmallLd + 4 * q]) = rv[u];
+                if (s < srows && 4 * q < kn) *reinterpret_cast<floatx4 *>(&st[s * kSmallLd + 4 * q]) = rv[set][u];
             } else {
-                if (s < srows && q < kn) st[s * kSmallLd + q] = rs[u];
+                if (s < srows && q < kn) st[s * kSmallLd + q] = rs[set][u];
             }
         }
     };
     const int nchunk = (in + kSmallKC - 1) / kSmallKC;
-    load(0, min(kSmallKC, in));
+    load(0, 0);
+    if (nchunk > 1) load(1, 1);
     float acc = 0.0f;
     const float *xs = st + rl * kSmallLd, *ws = st + (nr + o) * kSmallLd;
     for (int c = 0; c < nchunk; c++) {
         const int kn = min(kSmallKC, in - c * kSmallKC);
-        stage(kn);
-        __syncthreads();
-        if (c + 1 < nchunk) load((c + 1) * kSmallKC, min(kSmallKC, in - (c + 1) * kSmallKC));
+        // the set index is static in each branch, so the register sets stay registers
+        if ((c & 1) == 0) {
+            stage(0, kn);
+            __syncthreads();
+            if (c + 2 < nchunk) load(0, c + 2);
+        } else {
+            stage(1, kn);
+            __syncthreads();
+            if (c + 2 < nchunk) load(1, c + 2);
+        }
         if (live) {
-            int k = 0;
-#pragma unroll 8
-            for (; k + 4 <= kn; k += 4) {
-                const floatx4 a = *reinterpret_cast<const floatx4 *>(xs + k);
-                const floatx4 bb = *reinterpret_cast<const floatx4 *>(ws + k);
+            if (kn == kSmallKC) {
+                // a whole chunk: 32 values of each row read ahead of the 32 fmafs that use them
+                floatx4 xa[8], wa[8], xb[8], wb[8];
+                auto rd = [&](floatx4(&xd)[8], floatx4(&wd)[8], int k0) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) acc = __builtin_fmaf(a[e], bb[e], acc);
+                    for (int u = 0; u < 8; u++) {
+                        xd[u] = *reinterpret_cast<const floatx4 *>(xs + k0 + 4 * u);
+                        wd[u] = *reinterpret_cast<const floatx4 *>(ws + k0 + 4 * u);
+                    }
+                };
+                auto mac = [&](const floatx4(&xd)[8], const floatx4(&wd)[8]) {
+#pragma unroll
+                    for (int u = 0; u < 8; u++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) acc = __builtin_fmaf(xd[u][e], wd[u][e], acc);
+                };
+                static_assert(kSmallKC == 128, "four groups of 32 per chunk");
+                rd(xa, wa, 0);
+                rd(xb, wb, 32);
+                mac(xa, wa);
+                rd(xa, wa, 64);
+                mac(xb, wb);
+                rd(xb, wb, 96);
+                mac(xa, wa);
+                mac(xb, wb);
+            } else {
+                int k = 0;
+#pragma unroll 8
+                for (; k + 4 <= kn; k += 4) {
+                    const floatx4 a = *reinterpret_cast<const floatx4 *>(xs + k);
+                    const floatx4 bb = *reinterpret_cast<const floatx4 *>(ws + k);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc = __builtin_fmaf(a[e], bb[e], acc);
+                }
+                for (; k < kn; k++) acc = __builtin_fmaf(xs[k], ws[k], acc);
             }
-            for (; k < kn; k++) acc = __builtin_fmaf(xs[k], ws[k], acc);
         }
         __syncthreads();
     }
@@ -743,6 +784,26 @@ void launch_small_fwd(hipStream_t st, const float *x, const float *w, const floa
 // which the compiler turns into scalar loads (no LDS staging, no barrier). OUT is the layer's output count, a
 // compile-time constant so the loops over it unroll.
 constexpr int kSmallDxRows = 16, kSmallRc = 32;
+// dx[r][i] (+)= sum over o of g[r][o] w[o][i] for rows r0 .. r0 + kSmallDxRows - 1, column i: an fmaf chain over o in
+// increasing order per row (OUT = the layer's output count).
+template <int OUT>
+__device__ __forceinline__ void dx_rows(const float *__restrict__ g, const float *__restrict__ w, float *__restrict__ dx,
+                                        int rows, int in, int ax, int r0, int i) {
+    const int nr = min(kSmallDxRows, rows - r0);
+    if (i >= in) return;
+    float wv[OUT];
+#pragma unroll
+    for (int o = 0; o < OUT; o++) wv[o] = w[(int64_t)o * in + i];
+#pragma unroll 4
+    for (int r = 0; r < nr; r++) {
+        const float *gr = g + (int64_t)(r0 + r) * OUT;
+        float acc = 0.0f;
+#pragma unroll
+        for (int o = 0; o < OUT; o++) acc = __builtin_fmaf(gr[o], wv[o], acc);
+        float *d = dx + (int64_t)(r0 + r) * in + i;
+        *d = ax ? *d + acc : acc;
+    }
+}
 template <int OUT>
 __global__ void __launch_bounds__(256) k_linear_small_bwd(const float *__restrict__ g, const float *__restrict__ x,
                                                           const float *__restrict__ w, float *__restrict__ dx,
@@ -750,20 +811,7 @@ __global__ void __launch_bounds__(256) k_linear_small_bwd(const float *__restric
                                                           int in, int ax, int aw, int ab) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (blockIdx.y > 0) {
-        const int r0 = (blockIdx.y - 1) * kSmallDxRows, nr = min(kSmallDxRows, rows - r0);
-        if (i >= in) return;
-        float wv[OUT];
-#pragma unroll
-        for (int o = 0; o < OUT; o++) wv[o] = w[(int64_t)o * in + i];
-#pragma unroll 4
-        for (int r = 0; r < nr; r++) {
-            const float *gr = g + (int64_t)(r0 + r) * OUT;
-            float acc = 0.0f;
-#pragma unroll
-            for (int o = 0; o < OUT; o++) acc = __builtin_fmaf(gr[o], wv[o], acc);
-            float *d = dx + (int64_t)(r0 + r) * in + i;
-            *d = ax ? *d + acc : acc;
-        }
+        dx_rows<OUT>(g, w, dx, rows, in, ax, (blockIdx.y - 1) * kSmallDxRows, i);
         return;
     }
     if (blockIdx.x == 0 && db && (int)threadIdx.x < OUT) {
@@ -831,6 +879,204 @@ void small_bwd_dispatch(std::integer_sequence<int, OS...>, int out, hipStream_t 
                         const float *w, float *dx, float *dw, float *db, int rows, int in, int ax, int aw, int ab) {
     ((out == OS + 1 ? (launch_small_bwd<OS + 1>(st, g, x, w, dx, dw, db, rows, in, ax, aw, ab), 0) : 0), ...);
 }
+
+// ------------------------------------------------------------------------------------------------------------------
+// Narrow Linear layers: out <= 64 with more rows than the one-launch path takes (a classifier head over a sequence or
+// a batch of tokens), where 64-wide MFMA tiles would be mostly padding. The forward is k_linear_small_fwd (any row
+// count; one fmaf chain per output as the reference accumulates); dx runs dx_rows over row blocks; dW and db sum
+// row chunks (narrow_chunk) into partials, which a second launch adds in chunk order.
+constexpr int kNarrowMaxChunks = 64;
+bool linear_narrow(int rows, int in, int out) {
+    return rows >= 1 && rows <= (1 << 20) && out >= 1 && out <= kNarrowOut && in >= 1 && in <= kNarrowIn &&
+           !linear_small(rows, in, out);
+}
+// Rows per chunk: about 1024 workgroups over the column blocks and chunks (short chunks put all of a lane's x loads
+// in flight at once), at most kNarrowMaxChunks chunks, whole groups of four rows.
+int narrow_chunk(int rows, int in) {
+    const int ncb = (in + 63) / 64;
+    int nch = (1024 + ncb - 1) / ncb;
+    if (nch > kNarrowMaxChunks) nch = kNarrowMaxChunks;
+    if (nch < 1) nch = 1;
+    const int c = (rows + nch - 1) / nch;
+    return (c + 3) / 4 * 4;
+}
+template <int OUT>
+__global__ void __launch_bounds__(256) k_linear_narrow_dx(const float *__restrict__ g, const float *__restrict__ w,
+                                                          float *__restrict__ dx, int rows, int in, int ax) {
+    dx_rows<OUT>(g, w, dx, rows, in, ax, blockIdx.y * kSmallDxRows, blockIdx.x * 256 + threadIdx.x);
+}
+// part[c][o][i] = sum over the rows of chunk c of g[r][o] x[r][i]: lane l of every wavefront takes column
+// 64 blockIdx.x + l, wavefront q the chunk's rows q, q + 4, ... (an fmaf chain per o in increasing row order, x's loads
+// sixteen rows ahead); g passes through LDS in blocks of kNarrowSub rows (every lane reads the same g[r][o]: broadcast
+// reads). The four wavefronts' sums are then added in wavefront order. The chunk's bias partial dbp[c][o] = double sum
+// of its rows in increasing order, read from the same LDS blocks (the workgroups of the first column block).
+constexpr int kNarrowSub = 256;
+template <int OUT>
+__global__ void __launch_bounds__(256) k_linear_narrow_dw(const float *__restrict__ g, const float *__restrict__ x,
+                                                          float *__restrict__ part, double *__restrict__ dbp, int rows,
+                                                          int in, int chunk) {
+    constexpr int OP = (OUT + 3) / 4 * 4;  // LDS row stride of g: 16-byte rows
+    static_assert(kNarrowSub * OP >= 3 * OUT * 64, "the wavefront sums reuse the g block");
+    __shared__ __attribute__((aligned(16))) float gs[kNarrowSub * OP];
+    const int lane = threadIdx.x & 63, q = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = blockIdx.x * 64 + lane, ic = min(i, in - 1);  // columns past the end read column in - 1, unused
+    const int r0 = blockIdx.y * chunk, r1 = min(rows, r0 + chunk);
+    float acc[OUT];
+#pragma unroll
+    for (int o = 0; o < OUT; o++) acc[o] = 0.0f;
+    double dbacc = 0.0;
+    constexpr int G = 16;
+    for (int rb = r0; rb < r1; rb += kNarrowSub) {
+        const int nb = min(kNarrowSub, r1 - rb);
+        // this wavefront's rows of the block: rb + q + 4 j, j < nmine (rows past the end load the block's last row
+        // again, unused)
+        const int nmine = nb > q ? (nb - q + 3) / 4 : 0;
+        auto ld = [&](float(&d)[G], int j0) {
+#pragma unroll
+            for (int u = 0; u < G; u++) d[u] = x[(int64_t)min(rb + q + 4 * (j0 + u), rb + nb - 1) * in + ic];
+        };
+        auto use = [&](const float(&d)[G], int j0) {
+#pragma unroll
+            for (int u = 0; u < G; u++) {
+                if (j0 + u >= nmine) break;
+                const float *gr = gs + (q + 4 * (j0 + u)) * OP;
+#pragma unroll
+                for (int o = 0; o < OUT; o++) acc[o] = __builtin_fmaf(gr[o], d[u], acc[o]);
+            }
+        };
+        float xa[G], xb[G];
+        if (nmine > 0) ld(xa, 0);
+        __syncthreads();  // the previous block's reads are done
+        const float *gb = g + (int64_t)rb * OUT;
+        for (int e0 = 0; e0 < nb * OUT; e0 += 256 * 8) {  // eight loads per thread in flight together
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int e = e0 + 256 * u + (int)threadIdx.x;
+                v[u] = e < nb * OUT ? gb[e] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int e = e0 + 256 * u + (int)threadIdx.x;
+                if (e < nb * OUT) {
+                    const int rr = e / OUT, o = e - rr * OUT;
+                    gs[rr * OP + o] = v[u];
+                }
+            }
+        }
+        __syncthreads();
+        if (dbp && blockIdx.x == 0 && (int)threadIdx.x < OUT) {
+            // the bias partial from the block in LDS, rows in increasing order, sixteen reads ahead of their adds
+            const int o = threadIdx.x;
+            for (int r = 0; r < nb; r += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = gs[min(r + u, nb - 1) * OP + o];
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (r + u < nb) dbacc += v[u];
+            }
+        }
+        for (int j = 0; j < nmine; j += 2 * G) {
+            if (j + G < nmine) ld(xb, j + G);
+            use(xa, j);
+            if (j + 2 * G < nmine) ld(xa, j + 2 * G);
+            if (j + G < nmine) use(xb, j + G);
+        }
+    }
+    __syncthreads();
+    float *sh = gs;  // [3][OUT][64]
+    if (q > 0) {
+#pragma unroll
+        for (int o = 0; o < OUT; o++) sh[((q - 1) * OUT + o) * 64 + lane] = acc[o];
+    }
+    __syncthreads();
+    if (q == 0 && i < in) {
+#pragma unroll
+        for (int o = 0; o < OUT; o++) {
+            float v = acc[o] + sh[o * 64 + lane];
+            v = v + sh[(OUT + o) * 64 + lane];
+            v = v + sh[(2 * OUT + o) * 64 + lane];
+            part[((int64_t)blockIdx.y * OUT + o) * in + i] = v;
+        }
+    }
+    if (dbp && blockIdx.x == 0 && (int)threadIdx.x < OUT) dbp[(int64_t)blockIdx.y * OUT + threadIdx.x] = dbacc;
+}
+// dw[o][i] (+)= part[0][o][i] + part[1][o][i] + ... (chunk order); db[o] (+)= (float) of dbp[0][o] + dbp[1][o] + ...
+__global__ void __launch_bounds__(256) k_linear_narrow_reduce(const float *__restrict__ part,
+                                                              const double *__restrict__ dbp, float *__restrict__ dw,
+                                                              float *__restrict__ db, int nchunk, int in, int out,
+                                                              int aw, int ab) {
+    static_assert(kNarrowMaxChunks == 64, "the partials of one output load in one round");
+    const int64_t n = (int64_t)out * in, t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t < n) {
+        float pv[kNarrowMaxChunks];  // every partial's load issued before the first add
+#pragma unroll
+        for (int c = 0; c < kNarrowMaxChunks; c++) pv[c] = part[(int64_t)min(c, nchunk - 1) * n + t];
+        float v = pv[0];
+#pragma unroll
+        for (int c = 1; c < kNarrowMaxChunks; c++)
+            if (c < nchunk) v = v + pv[c];
+        dw[t] = aw ? dw[t] + v : v;
+    }
+    if (db && t < out) {
+        double s = 0.0;
+        for (int c0 = 0; c0 < nchunk; c0 += 16) {
+            double pv[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) pv[u] = dbp[(int64_t)min(c0 + u, nchunk - 1) * out + t];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (c0 + u < nchunk) s = c0 + u == 0 ? pv[u] : s + pv[u];
+        }
+        const float v = (float)s;
+        db[t] = ab ? db[t] + v : v;
+    }
+}
+template <int OUT>
+void launch_narrow(hipStream_t st, const float *g, const float *x, const float *w, float *dx, float *part, double *dbp,
+                   int rows, int in, int ax, int chunk) {
+    if (dx)
+        hipLaunchKernelGGL(k_linear_narrow_dx<OUT>,
+                           dim3((unsigned)((in + 255) / 256), (unsigned)((rows + kSmallDxRows - 1) / kSmallDxRows)),
+                           dim3(256), 0, st, g, w, dx, rows, in, ax);
+    if (part)
+        hipLaunchKernelGGL(k_linear_narrow_dw<OUT>,
+                           dim3((unsigned)((in + 63) / 64), (unsigned)((rows + chunk - 1) / chunk)), dim3(256), 0, st,
+                           g, x, part, dbp, rows, in, chunk);
+}
+template <int... OS>
+void narrow_dispatch(std::integer_sequence<int, OS...>, hipStream_t st, const float *g, const float *x, const float *w,
+                     float *dx, float *part, double *dbp, int rows, int in, int out, int ax, int chunk) {
+    ((out == OS + 1 ? (launch_narrow<OS + 1>(st, g, x, w, dx, part, dbp, rows, in, ax, chunk), 0) : 0), ...);
+}
+// The whole backward of a narrow layer: dx (when asked), and dW with db in two launches (db alone: om_colsum).
+om_status narrow_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
+                     int rows, int in, int out, int ax, int aw, int ab) {
+    const hipStream_t st = om::cur_stream(ctx);
+    float *part = nullptr;
+    double *dbp = nullptr;
+    const int chunk = narrow_chunk(rows, in), nchunk = (rows + chunk - 1) / chunk;
+    if (dw) {
+        const uint64_t pbytes = ((uint64_t)nchunk * out * in * sizeof(float) + 255) / 256 * 256;
+        float *ws;
+        om_status s = om::scratch(ctx, pbytes + (uint64_t)nchunk * out * sizeof(double), &ws);
+        if (s) return s;
+        part = ws;
+        if (db) dbp = reinterpret_cast<double *>(reinterpret_cast<char *>(ws) + pbytes);
+    }
+    if (dx || dw)
+        narrow_dispatch(std::make_integer_sequence<int, kNarrowOut>{}, st, g, x, w, dx, part, dbp, rows, in, out, ax,
+                        chunk);
+    if (dw) {
+        const int64_t n = (int64_t)out * in;
+        hipLaunchKernelGGL(k_linear_narrow_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part, dbp, dw,
+                           db, nchunk, in, out, aw, ab);
+    }
+    om_status s = OM_LAUNCH_CHECK(ctx, "om_linear_bwd (narrow)");
+    if (!s && db && !dw) s = om_colsum(ctx, g, db, rows, out, ab);
+    return s;
+}
 }  // namespace
 
 extern "C" {
@@ -870,7 +1116,7 @@ om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float
                         int out) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && rows >= 0 && in > 0 && out > 0, "om_linear_fwd: bad arguments");
-    if (linear_small(rows, in, out)) {
+    if (linear_small(rows, in, out) || linear_narrow(rows, in, out)) {
         launch_small_fwd(om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd");
     }
@@ -889,6 +1135,10 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         small_bwd_dispatch(std::make_integer_sequence<int, kSmallOut>{}, out, om::cur_stream(ctx), g, x, w, dx, dw, db,
                            rows, in, acc_dx, acc_dw, acc_db);
         return OM_LAUNCH_CHECK(ctx, "om_linear_bwd");
+    }
+    if (linear_narrow(rows, in, out)) {
+        if (!dx && !dw && !db) return OM_OK;
+        return narrow_bwd(ctx, g, x, w, dx, dw, db, rows, in, out, acc_dx, acc_dw, acc_db);
     }
     om_status s = OM_OK;
     if (dx) {
@@ -913,7 +1163,7 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
                               float *y, int rows, int in, int out) {
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, x && w && y && resid && rows >= 0 && in > 0 && out > 0, "om_linear_fwd_resid: bad arguments");
-    if (linear_small(rows, in, out)) {  // the same products as om_linear_fwd's for this shape
+    if (linear_small(rows, in, out) || linear_narrow(rows, in, out)) {  // om_linear_fwd's products for this shape
         launch_small_fwd(om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid");
     }
@@ -961,20 +1211,30 @@ om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, in
     for (int j = 0; j < n_cs; j++)
         OM_REQUIRE(ctx, cs[j].part && cs[j].out && cs[j].chunks > 0 && cs[j].cols > 0,
                    "om_param_grads_group: column-sum item %d has a NULL pointer or a non-positive size", j);
+    // The products the grouped launch can take go there together (with the column sums); the others, and all of
+    // them when fewer than two fit, run one by one. Outputs do not overlap, so the order between the two sets does
+    // not change any result.
     om_status s = OM_OK;
-    const bool grouped = omg::launch_dw_group(ctx, n_dw, dw, rows, n_cs, cs, &s);
-    if (!grouped) {
-        for (int i = 0; i < n_dw && !s; i++) {
-            const om_linear_dw &d = dw[i];
-            if (d.dw || d.db)
-                s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw,
-                                  d.acc_db);
+    om_linear_dw fit[omg::kMaxGroup];
+    int nfit = 0;
+    for (int i = 0; i < n_dw; i++)
+        if (omg::dw_groupable(dw[i]) && nfit < omg::kMaxGroup) fit[nfit++] = dw[i];
+    const bool grouped = nfit >= 2 && omg::launch_dw_group(ctx, nfit, fit, rows, n_cs, cs, &s);
+    if (s) return s;
+    int taken = 0;
+    for (int i = 0; i < n_dw && !s; i++) {
+        const om_linear_dw &d = dw[i];
+        if (grouped && taken < nfit && omg::dw_groupable(d)) {
+            taken++;
+            continue;
         }
-        if (!s && n_cs) {
-            omg::GroupParams g{};
-            omg::set_column_sums(g, n_cs, cs);
-            s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
-        }
+        if (d.dw || d.db)
+            s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw, d.acc_db);
+    }
+    if (!s && !grouped && n_cs) {
+        omg::GroupParams g{};
+        omg::set_column_sums(g, n_cs, cs);
+        s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
     }
     return s;
 }

@@ -97,6 +97,13 @@ void Record::unpack_check() const {
 
 void Engine::queue_dw(const om_linear_dw &item, int rows) {
     if (!item.dw && !item.db) return;
+    if (!item.dw || item.out % 64 || item.in % 64) {
+        // Never part of a grouped launch (it takes whole 64 x 64 tiles): run it now, so that it does not take one of
+        // the four places of a group (a classifier head would otherwise push every later layer's products one place
+        // along, splitting each layer's four over two launches).
+        OMT(om_param_grads_group(C(), 1, &item, rows, 0, nullptr));
+        return;
+    }
     if (!dw_queue_.empty() && (rows != dw_rows_ || dw_queue_.size() == 4)) flush_dw();
     dw_queue_.push_back(item);
     dw_rows_ = rows;

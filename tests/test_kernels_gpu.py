@@ -111,7 +111,12 @@ def test_gemm_rejects_bad_shapes(dev):
                                            (512, 256, 128), (4096, 1536, 384), (4096, 384, 1152),
                                            # C5 at full size: FFN pair, attention output, packed q|k|v, token head
                                            (4096, 768, 3072), (4096, 3072, 768), (4096, 768, 768), (4096, 768, 2304),
-                                           (4096, 768, 9)])
+                                           (4096, 768, 9),
+                                           # narrow layers (out <= 64 past the one-launch bounds): C4's head, an
+                                           # output count at the top of a rounded-up instance, unaligned rows,
+                                           # several input chunks, one output, the row-chunk cap
+                                           (1024, 256, 37), (2048, 100, 64), (1000, 33, 33), (300, 2000, 5),
+                                           (257, 17, 1), (20000, 8, 3)])
 def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     rng = np.random.default_rng(rows + inf + outf)
     x, w, b, g = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf), rnd(rng, rows, outf)
@@ -132,6 +137,10 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
         # db in double by increasing row): the oracle's bits exactly
         for got, ref in ((Y, y_ref), (DX, dx_r), (DW, dw_r), (DB, db_r)):
             assert np.array_equal(dev.get(got).view(np.uint32), ref.view(np.uint32))
+    elif outf <= 64 and inf <= 8192:
+        # narrow layers: y and dx are the same chains (bit for bit); dW and db add row chunks, within tolerance
+        for got, ref in ((Y, y_ref), (DX, dx_r)):
+            assert np.array_equal(dev.get(got).view(np.uint32), ref.view(np.uint32))
     # accumulate into existing leaves
     dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 1, 1, 1)
     assert scaled(dev.get(DW), dw_r + dw_r) <= TOL
@@ -145,7 +154,8 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     (100, [(20, 36), (36, 20)]),                       # ragged: item by item through om_linear_bwd
     (4096, [(768, 3072), (3072, 768), (768, 768), (768, 2304)]),  # C5's four weight gradients of one layer
     (4096, [(768, 768)]),                              # C5's attention output alone
-], ids=["ffn-pair", "attention-triple", "small-64", "ragged", "c5-layer", "c5-single"])
+    (4096, [(768, 9), (768, 768), (20, 36), (768, 2304)]),  # mixed: the two that fit grouped, the others alone
+], ids=["ffn-pair", "attention-triple", "small-64", "ragged", "c5-layer", "c5-single", "mixed"])
 def test_linear_dw_group(dev, T, rows, shapes):
     """om_linear_bwd_dw_group: every item's dW and db to the GEMM tolerance against the oracle (the last item of
     each group without a bias gradient), then a second call accumulating into the same leaves."""
