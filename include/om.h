@@ -43,6 +43,14 @@ om_status om_ctx_sync(om_ctx *ctx);
 const char *om_last_error(om_ctx *ctx);
 /* The context's hipStream_t, for callers that time or order work around the library's launches. */
 void *om_ctx_stream(om_ctx *ctx);
+/* Launch timing probe (measurement; no counterpart in the reference, for callers that report how long the parameter
+ * gradients take inside real steps): while on, every om_param_grads_group call (and so om_linear_bwd_dw_group)
+ * records a HIP event on the context's stream before its first launch and one after its last (at most 1024 calls per
+ * series; none while a step graph is captured). om_ctx_probe(ctx, 1) starts a new series, om_ctx_probe(ctx, 0) stops
+ * recording; om_ctx_probe_read waits for the stream and gives the number of calls recorded and their mean duration in
+ * milliseconds (0 when there are none). */
+om_status om_ctx_probe(om_ctx *ctx, int on);
+om_status om_ctx_probe_read(om_ctx *ctx, int *calls, double *mean_ms);
 /* Version of this ABI (major * 100 + minor). */
 int om_abi_version(void);
 

@@ -30,6 +30,8 @@ _OM_SIGS = {
     "om_ctx_sync": [vp],
     "om_last_error": [vp],
     "om_ctx_stream": [vp],
+    "om_ctx_probe": [vp, ci],
+    "om_ctx_probe_read": [vp, C.POINTER(ci), C.POINTER(C.c_double)],
     "om_abi_version": [],
     "om_arena_reserve": [vp, u64, u64],
     "om_alloc": [vp, ci, u64, C.POINTER(vp)],

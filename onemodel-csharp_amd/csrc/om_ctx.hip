@@ -76,9 +76,26 @@ static om_status add_slab(om_ctx *ctx, om_region &r, uint64_t bytes) {
     return OM_OK;
 }
 
+constexpr int kProbeMax = 1024;
+int om::probe_begin(om_ctx *ctx) {
+    if (!ctx->probe_on || ctx->cap || ctx->probe_n >= kProbeMax) return -1;
+    const int i = ctx->probe_n;
+    while ((int)ctx->probe_ev.size() < 2 * (i + 1)) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return -1;
+        ctx->probe_ev.push_back(e);
+    }
+    if (hipEventRecord(ctx->probe_ev[2 * i], ctx->stream) != hipSuccess) return -1;
+    return i;
+}
+void om::probe_end(om_ctx *ctx, int slot) {
+    if (slot < 0 || slot != ctx->probe_n) return;
+    if (hipEventRecord(ctx->probe_ev[2 * slot + 1], ctx->stream) == hipSuccess) ctx->probe_n++;
+}
+
 extern "C" {
 
-int om_abi_version(void) { return 101; }
+int om_abi_version(void) { return 102; }
 
 om_status om_ctx_create(int device, om_ctx **out) {
     if (!out) return om::fail(nullptr, OM_E_ARG, "om_ctx_create: out is NULL");
@@ -121,8 +138,34 @@ om_status om_ctx_destroy(om_ctx *ctx) {
         for (auto &s : r.slabs) (void)hipFree(s.base);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->scratch2) (void)hipFree(ctx->scratch2);
+    for (hipEvent_t e : ctx->probe_ev) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(ctx->stream);
     delete ctx;
+    return OM_OK;
+}
+
+om_status om_ctx_probe(om_ctx *ctx, int on) {
+    OM_CHECK_CTX(ctx);
+    if (on) ctx->probe_n = 0;
+    ctx->probe_on = on != 0;
+    return OM_OK;
+}
+
+om_status om_ctx_probe_read(om_ctx *ctx, int *calls, double *mean_ms) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, calls && mean_ms, "om_ctx_probe_read: NULL output");
+    if (om_status s = om::refuse_in_capture(ctx, "om_ctx_probe_read")) return s;
+    if (om_status s = om::check_hip(ctx, hipStreamSynchronize(ctx->stream), "om_ctx_probe_read")) return s;
+    double sum = 0.0;
+    for (int i = 0; i < ctx->probe_n; i++) {
+        float ms = 0.0f;
+        if (om_status s = om::check_hip(ctx, hipEventElapsedTime(&ms, ctx->probe_ev[2 * i], ctx->probe_ev[2 * i + 1]),
+                                        "om_ctx_probe_read"))
+            return s;
+        sum += ms;
+    }
+    *calls = ctx->probe_n;
+    *mean_ms = ctx->probe_n ? sum / ctx->probe_n : 0.0;
     return OM_OK;
 }
 

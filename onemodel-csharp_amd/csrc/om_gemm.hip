@@ -1079,6 +1079,37 @@ om_status narrow_bwd(om_ctx *ctx, const float *g, const float *x, const float *w
 }
 }  // namespace
 
+static om_status param_grads(om_ctx *ctx, int n_dw, const om_linear_dw *dw, int rows, int n_cs,
+                             const om_column_sum *cs) {
+    // The products the grouped launch can take go there together (with the column sums); the others, and all of
+    // them when fewer than two fit, run one by one. Outputs do not overlap, so the order between the two sets does
+    // not change any result.
+    om_status s = OM_OK;
+    om_linear_dw fit[omg::kMaxGroup];
+    int nfit = 0;
+    for (int i = 0; i < n_dw; i++)
+        if (omg::dw_groupable(dw[i]) && nfit < omg::kMaxGroup) fit[nfit++] = dw[i];
+    const bool grouped = nfit >= 2 && omg::launch_dw_group(ctx, nfit, fit, rows, n_cs, cs, &s);
+    if (s) return s;
+    int taken = 0;
+    for (int i = 0; i < n_dw && !s; i++) {
+        const om_linear_dw &d = dw[i];
+        if (grouped && taken < nfit && omg::dw_groupable(d)) {
+            taken++;
+            continue;
+        }
+        if (d.dw || d.db)
+            s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw, d.acc_db);
+    }
+    if (!s && !grouped && n_cs) {
+        omg::GroupParams g{};
+        omg::set_column_sums(g, n_cs, cs);
+        s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
+    }
+    return s;
+}
+
+
 extern "C" {
 
 om_status om_gemm(om_ctx *ctx, int trans_a, int trans_b, int m, int n, int k, const float *a, int lda,
@@ -1211,31 +1242,9 @@ om_status om_param_grads_group(om_ctx *ctx, int n_dw, const om_linear_dw *dw, in
     for (int j = 0; j < n_cs; j++)
         OM_REQUIRE(ctx, cs[j].part && cs[j].out && cs[j].chunks > 0 && cs[j].cols > 0,
                    "om_param_grads_group: column-sum item %d has a NULL pointer or a non-positive size", j);
-    // The products the grouped launch can take go there together (with the column sums); the others, and all of
-    // them when fewer than two fit, run one by one. Outputs do not overlap, so the order between the two sets does
-    // not change any result.
-    om_status s = OM_OK;
-    om_linear_dw fit[omg::kMaxGroup];
-    int nfit = 0;
-    for (int i = 0; i < n_dw; i++)
-        if (omg::dw_groupable(dw[i]) && nfit < omg::kMaxGroup) fit[nfit++] = dw[i];
-    const bool grouped = nfit >= 2 && omg::launch_dw_group(ctx, nfit, fit, rows, n_cs, cs, &s);
-    if (s) return s;
-    int taken = 0;
-    for (int i = 0; i < n_dw && !s; i++) {
-        const om_linear_dw &d = dw[i];
-        if (grouped && taken < nfit && omg::dw_groupable(d)) {
-            taken++;
-            continue;
-        }
-        if (d.dw || d.db)
-            s = om_linear_bwd(ctx, d.g, d.x, nullptr, nullptr, d.dw, d.db, rows, d.in, d.out, 0, d.acc_dw, d.acc_db);
-    }
-    if (!s && !grouped && n_cs) {
-        omg::GroupParams g{};
-        omg::set_column_sums(g, n_cs, cs);
-        s = omg::launch_group_reduce(ctx, g, 1, om::cur_stream(ctx));
-    }
+    const int probe = om::probe_begin(ctx);
+    const om_status s = param_grads(ctx, n_dw, dw, rows, n_cs, cs);
+    om::probe_end(ctx, probe);
     return s;
 }
 

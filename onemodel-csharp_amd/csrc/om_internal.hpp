@@ -43,6 +43,10 @@ struct om_ctx {
     int num_cus = 256;
     // The step graph being captured on the stream (om_graph_capture_begin .. _end), else NULL.
     struct om_graph *cap = nullptr;
+    // Launch timing probe (om_ctx_probe): events [2 i] / [2 i + 1] bracket the i-th recorded om_param_grads_group call.
+    bool probe_on = false;
+    int probe_n = 0;
+    std::vector<hipEvent_t> probe_ev;
 };
 
 // The per-step values a step graph's kernels read (om_step_values plus the readback's sequence number and the
@@ -80,6 +84,10 @@ om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
 om_status noalloc_init(om_ctx *ctx);
 // OM_E_STATE with a message when a step graph is being captured on ctx's stream (for calls a graph cannot hold).
 om_status refuse_in_capture(om_ctx *ctx, const char *what);
+// The launch timing probe around one call: probe_begin records the start event and returns the call's slot (-1 when
+// the probe is off, full or the stream is being captured); probe_end records the end event of that slot.
+int probe_begin(om_ctx *ctx);
+void probe_end(om_ctx *ctx, int slot);
 // The stream every launch of the context goes to.
 inline hipStream_t cur_stream(const om_ctx *ctx) { return ctx->stream; }
 // A readback post written by another entry point's kernel: checks that r belongs to ctx and holds `bytes`, waits for

@@ -176,3 +176,28 @@ def test_capture_refuses_host_waits(pkg):
     assert L.om_graph_capture_abort(d.ctx.h) == 0
     d.call("om_fill", x, 3.0, 8)
     assert np.array_equal(d.get(x), np.full(8, 3.0, np.float32))
+
+
+def test_launch_probe(pkg):
+    """om_ctx_probe brackets om_param_grads_group calls with events: one call per C3 step is recorded, none while
+    the probe is off or inside a step graph's replays, and a new series starts from zero."""
+    import ctypes as C
+    m = pkg.Model(3, batch=2)
+    try:
+        L = pkg.load_hip()
+        calls, ms = C.c_int(), C.c_double()
+        assert L.om_ctx_probe(m.ctx, 1) == 0
+        for _ in range(3):
+            m.step()
+        assert L.om_ctx_probe(m.ctx, 0) == 0
+        m.step()  # not recorded
+        assert L.om_ctx_probe_read(m.ctx, C.byref(calls), C.byref(ms)) == 0
+        assert calls.value == 3 and 0.0 < ms.value < 100.0
+        m.set_step_graph(True)
+        assert L.om_ctx_probe(m.ctx, 1) == 0
+        for _ in range(4):
+            m.step()  # eager, recorded, then replays with no library calls
+        assert L.om_ctx_probe_read(m.ctx, C.byref(calls), C.byref(ms)) == 0
+        assert calls.value == 1  # only the first (eager) step; the capture records nothing
+    finally:
+        m.close()
