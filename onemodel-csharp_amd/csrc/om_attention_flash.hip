@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(256) k_flash_fwd(const float *__restrict__ q, 
 // queries); K and V^T of the (batch, head) staged in LDS, S^T = K Q^T with this lane's query on the lane index t,
 // E = 2^(x - max) in the registers that hold S^T, which are the B operand of O^T = V^T E^T, and O = O^T / l. The
 // statistics are the streaming forward's (m in log2 units, 1/l), so either backward can follow either forward.
-template <int D, int L>
+template <int D, int L, bool MASK>
 __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                   int64_t mask_bstride, float *__restrict__ o, int ldo,
@@ -197,19 +197,8 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, t = lane & 15, kl = lane >> 4;
     const int qrow = qb * 64 + 16 * w + t;  // this lane's query
     const int64_t row0 = (int64_t)b * L;
-    floatx4 qf[DB];  // B operand of S^T = K Q^T: Q[qrow][16 blk + 4 kl + u]
-    const float *qg = q + (row0 + qrow) * ld + h * D;
-#pragma unroll
-    for (int blk = 0; blk < DB; blk++) qf[blk] = *reinterpret_cast<const floatx4 *>(qg + 16 * blk + 4 * kl);
-    floatx4 mv[NB];  // mask of query t over keys 16 j + 4 kl + r (scaled to log2 units below)
-    if (mask) {
-        const float *mr = mask + b * mask_bstride + (int64_t)qrow * L + 4 * kl;
-#pragma unroll
-        for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
-    } else {
-#pragma unroll
-        for (int j = 0; j < NB; j++) mv[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    }
+    // Loads in the order the work needs them: K (the first product's A operand, via LDS), Q, then the mask (the
+    // largest, needed only after S^T), so the first MFMAs can start while the mask is still arriving.
     // K rows: thread f takes row f / Q4, four d from (f % Q4) * 4. V^T: key f % L, four d from (f / L) * 4, so each
     // LDS store row of V^T is contiguous across the lanes; V's loads are issued once K is in LDS and arrive while
     // S^T and the softmax run.
@@ -219,6 +208,21 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
     for (int i = 0; i < PER; i++) {
         const int f = (int)threadIdx.x + 256 * i;
         kx[i] = *reinterpret_cast<const floatx4 *>(kg + (int64_t)(f / Q4) * ld + (f % Q4) * 4);
+    }
+    floatx4 qf[DB];  // B operand of S^T = K Q^T: Q[qrow][16 blk + 4 kl + u]
+    const float *qg = q + (row0 + qrow) * ld + h * D;
+#pragma unroll
+    for (int blk = 0; blk < DB; blk++) qf[blk] = *reinterpret_cast<const floatx4 *>(qg + 16 * blk + 4 * kl);
+    // mask of query t over keys 16 j + 4 kl + r (scaled to log2 units below); MASK is a template parameter so that no
+    // branch joins the paths before the waits for K (a join makes the compiler wait for every load of either path)
+    floatx4 mv[NB];
+    if constexpr (MASK) {
+        const float *mr = mask + b * mask_bstride + (int64_t)qrow * L + 4 * kl;
+#pragma unroll
+        for (int j = 0; j < NB; j++) mv[j] = *reinterpret_cast<const floatx4 *>(mr + 16 * j);
+    } else {
+#pragma unroll
+        for (int j = 0; j < NB; j++) mv[j] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -242,6 +246,9 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
 #pragma unroll
             for (int u = 0; u < 4; u++) s[j] = mfma4(a[u], qf[blk][u], s[j]);
         }
+    // Nothing that reads the mask may be scheduled among the MFMAs above: it would make them wait for the mask's
+    // loads, which are issued last so that this product can run while they arrive.
+    __builtin_amdgcn_sched_barrier(0);
     float mx = -__int_as_float(0x7F800000);
 #pragma unroll
     for (int j = 0; j < NB; j++)
@@ -265,6 +272,7 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
         }
     ps += __shfl_xor(ps, 16, 64);
     ps += __shfl_xor(ps, 32, 64);
+    __builtin_amdgcn_sched_barrier(0);  // the softmax above runs while V's loads are in flight, not after them
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int f = (int)threadIdx.x + 256 * i;
@@ -480,7 +488,7 @@ __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ 
 //      dS stays in registers;
 //   4. dS into LDS over Q and dO ([query][key]), then dQ = dS K over this block's 64 keys for two blocks of 16
 //      queries per wavefront: the final dQ when L = 64, else a partial summed by k_flash_dq_reduce.
-template <int L>
+template <int L, bool MASK>
 __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q, const float *__restrict__ k,
                                                      const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                      int64_t mask_bstride, const float *__restrict__ g, int ldg,
@@ -570,11 +578,11 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
     // 2, 3. Per phase: delta of its queries; then per block of 16 queries S, dP, P, dS, with dV^T and dK^T accumulating
     // over all L queries. The mask values of block i + 1 (this lane's key at queries 16 (i + 1) + 4 kl + r) load while
     // block i runs.
-    const float *mbase = mask ? mask + b * mask_bstride + mykey : nullptr;
+    const float *mbase = MASK ? mask + b * mask_bstride + mykey : nullptr;
     float mkc[4], mkn[4];
     auto mask_load = [&](float(&dst)[4], int i) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) dst[r] = mbase ? mbase[(int64_t)(16 * i + 4 * kl + r) * L] : 0.0f;
+        for (int r = 0; r < 4; r++) dst[r] = MASK ? mbase[(int64_t)(16 * i + 4 * kl + r) * L] : 0.0f;
     };
     mask_load(mkc, 0);
     floatx4 dsv[NQB];
@@ -755,12 +763,12 @@ om_status om_attention_fwd_flash(om_ctx *ctx, const float *q, const float *k, co
     const dim3 grid((unsigned)((int64_t)B * H * (L / kChunk)));
     const float c = scale * kLog2e;
     if (short_rows(L, d) && short_path() == kRows) {
-        if (L == 128)
-            hipLaunchKernelGGL((k_rows_fwd<32, 128>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
-                               o, ld_o, stats, stats + n, H, c);
-        else
-            hipLaunchKernelGGL((k_rows_fwd<32, 64>), grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride,
-                               o, ld_o, stats, stats + n, H, c);
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o, stats,
+                               stats + n, H, c);
+        };
+        if (L == 128) mask ? launch(k_rows_fwd<32, 128, true>) : launch(k_rows_fwd<32, 128, false>);
+        else mask ? launch(k_rows_fwd<32, 64, true>) : launch(k_rows_fwd<32, 64, false>);
     } else if (d == 64)
         hipLaunchKernelGGL(k_flash_fwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o,
                            stats, stats + n, H, L, c);
@@ -797,12 +805,14 @@ om_status om_attention_bwd_flash(om_ctx *ctx, const float *q, const float *k, co
             s = om::scratch2(ctx, sizeof(float) * (uint64_t)nb * n * d, &part);
             if (s) return s;
         }
+        auto launch_bwd = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g, ld_g, o, ld_o,
+                               stats, stats + n, dk, dv, dq, ld_d, part, H, c, scale, acc);
+        };
         if (L == 128)
-            hipLaunchKernelGGL(k_rows_bwd<128>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g,
-                               ld_g, o, ld_o, stats, stats + n, dk, dv, dq, ld_d, part, H, c, scale, acc);
+            mask ? launch_bwd(k_rows_bwd<128, true>) : launch_bwd(k_rows_bwd<128, false>);
         else
-            hipLaunchKernelGGL(k_rows_bwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g,
-                               ld_g, o, ld_o, stats, stats + n, dk, dv, dq, ld_d, part, H, c, scale, acc);
+            mask ? launch_bwd(k_rows_bwd<64, true>) : launch_bwd(k_rows_bwd<64, false>);
         if (part)
             hipLaunchKernelGGL(k_flash_dq_reduce<32>, dim3((unsigned)((n * 8 + 255) / 256)), dim3(256), 0,
                                ctx->stream, part, nb, n, dq, ld_d, H, L, acc);
