@@ -56,7 +56,7 @@ __device__ __forceinline__ void block_coords(int nb, int H, int &blk, int &h, in
     b = bh / H;
 }
 
-template <int D>
+template <int D, bool MASK>
 __global__ void __launch_bounds__(256) k_flash_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                    const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                    int64_t mask_bstride, float *__restrict__ o, int ldo,
@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(256) k_flash_fwd(const float *__restrict__ q, 
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             floatx4 mk = floatx4{0.f, 0.f, 0.f, 0.f};
-            if (mrow) mk = *reinterpret_cast<const floatx4 *>(mrow + kc * kChunk + 16 * j);
+            if constexpr (MASK) mk = *reinterpret_cast<const floatx4 *>(mrow + kc * kChunk + 16 * j);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float x = __builtin_fmaf(s[j][r], c, mk[r] * kLog2e);
@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(256) k_flash_delta(const float *__restrict__ g
     if (row < rows && sub == 0) delta[row] = (float)acc;
 }
 
-template <int D>
+template <int D, bool MASK>
 __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ q, const float *__restrict__ k,
                                                    const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                    int64_t mask_bstride, const float *__restrict__ g, int ldg,
@@ -413,7 +413,7 @@ __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ 
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int qq = 16 * i + 4 * kl + r;
-                const float mk = mbase ? mbase[(int64_t)(qc * kChunk + qq) * L] * kLog2e : 0.0f;
+                const float mk = MASK ? mbase[(int64_t)(qc * kChunk + qq) * L] * kLog2e : 0.0f;
                 const float x = __builtin_fmaf(s[i][r], c, mk);
                 const float p = exp2_hw(x - St[0][qq]) * St[1][qq];
                 s[i][r] = p;
@@ -769,12 +769,14 @@ om_status om_attention_fwd_flash(om_ctx *ctx, const float *q, const float *k, co
         };
         if (L == 128) mask ? launch(k_rows_fwd<32, 128, true>) : launch(k_rows_fwd<32, 128, false>);
         else mask ? launch(k_rows_fwd<32, 64, true>) : launch(k_rows_fwd<32, 64, false>);
-    } else if (d == 64)
-        hipLaunchKernelGGL(k_flash_fwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o,
-                           stats, stats + n, H, L, c);
-    else
-        hipLaunchKernelGGL(k_flash_fwd<32>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o,
-                           stats, stats + n, H, L, c);
+    } else {
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, o, ld_o, stats,
+                               stats + n, H, L, c);
+        };
+        if (d == 64) mask ? launch(k_flash_fwd<64, true>) : launch(k_flash_fwd<64, false>);
+        else mask ? launch(k_flash_fwd<32, true>) : launch(k_flash_fwd<32, false>);
+    }
     return OM_LAUNCH_CHECK(ctx, "om_attention_fwd_flash");
 }
 
@@ -823,19 +825,21 @@ om_status om_attention_bwd_flash(om_ctx *ctx, const float *q, const float *k, co
     if (s) return s;
     float *delta = scr, *part = dq ? scr + ((n + 63) / 64) * 64 : nullptr;
     const unsigned rows_grid = (unsigned)((n * 16 + 255) / 256);
+    auto launch_flash_bwd = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g, ld_g, stats,
+                           stats + n, delta, dk, dv, ld_d, part, H, L, c, scale, acc);
+    };
     if (d == 64) {
         hipLaunchKernelGGL(k_flash_delta<64>, dim3(rows_grid), dim3(256), 0, ctx->stream, g, ld_g, o, ld_o, delta, H,
                            L, n);
-        hipLaunchKernelGGL(k_flash_bwd<64>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g, ld_g,
-                           stats, stats + n, delta, dk, dv, ld_d, part, H, L, c, scale, acc);
+        mask ? launch_flash_bwd(k_flash_bwd<64, true>) : launch_flash_bwd(k_flash_bwd<64, false>);
         if (dq)
             hipLaunchKernelGGL(k_flash_dq_reduce<64>, dim3((unsigned)((n * 16 + 255) / 256)), dim3(256), 0,
                                ctx->stream, part, nb, n, dq, ld_d, H, L, acc);
     } else {
         hipLaunchKernelGGL(k_flash_delta<32>, dim3(rows_grid), dim3(256), 0, ctx->stream, g, ld_g, o, ld_o, delta, H,
                            L, n);
-        hipLaunchKernelGGL(k_flash_bwd<32>, grid, dim3(256), 0, ctx->stream, q, k, v, ld_qkv, mask, mstride, g, ld_g,
-                           stats, stats + n, delta, dk, dv, ld_d, part, H, L, c, scale, acc);
+        mask ? launch_flash_bwd(k_flash_bwd<32, true>) : launch_flash_bwd(k_flash_bwd<32, false>);
         if (dq)
             hipLaunchKernelGGL(k_flash_dq_reduce<32>, dim3((unsigned)((n * 8 + 255) / 256)), dim3(256), 0,
                                ctx->stream, part, nb, n, dq, ld_d, H, L, acc);
