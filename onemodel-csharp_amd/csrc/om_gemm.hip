@@ -133,35 +133,40 @@ __global__ void k_splitk_reduce_s(Params p) {
         for (int64_t i = gid; i < p.m; i += stride) reduce_bias_row<S>(p, (int)i);
     for (int64_t q = gid; q < quads; q += stride) reduce_quad<S>(p, q);
 }
-// The reduce of a grouped weight-gradient launch: the same per-row and per-quad work over every product in turn.
+// The reduce of a grouped weight-gradient launch: the column sums, and the same per-row and per-quad work over every
+// product. Each kind of work has blocks of its own, in that order (the column sums, a wavefront per column, are the
+// longest chains and are dispatched first), so they run at once instead of one after another in the same threads.
 template <int S>
-__global__ void k_splitk_reduce_group(GroupParams g) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (int64_t r = gid; r < g.rstart[g.count]; r += stride) {
-        int i = 0;
-#pragma unroll
-        for (int j = 1; j < kMaxGroup; j++)
-            if (j < g.count && r >= g.rstart[j]) i = j;
-        reduce_bias_row<S>(g.p[i], (int)(r - g.rstart[i]));
-    }
-    for (int64_t q = gid; q < g.qstart[g.count]; q += stride) {
-        int i = 0;
-#pragma unroll
-        for (int j = 1; j < kMaxGroup; j++)
-            if (j < g.count && q >= g.qstart[j]) i = j;
-        reduce_quad<S>(g.p[i], q - g.qstart[i]);
-    }
-    // column sums, a wavefront per column (the loop bound is uniform over each wavefront)
-    const int lane = threadIdx.x & 63;
-    for (int64_t w = gid >> 6; w < g.cstart[g.ncs]; w += stride >> 6) {
+__global__ void k_splitk_reduce_group(GroupParams g, int cblocks, int rblocks) {
+    const int b = blockIdx.x;
+    if (b < cblocks) {
+        const int64_t w = (int64_t)b * (blockDim.x >> 6) + (threadIdx.x >> 6);
+        if (w >= g.cstart[g.ncs]) return;  // uniform over each wavefront
         int i = 0;
 #pragma unroll
         for (int j = 1; j < kMaxColSums; j++)
             if (j < g.ncs && w >= g.cstart[j]) i = j;
         const ColSumItem &c = g.cs[i];
-        omd::column_sum_wave(c.part, c.out, c.chunks, c.cols, (int)(w - g.cstart[i]), c.acc, lane);
+        omd::column_sum_wave(c.part, c.out, c.chunks, c.cols, (int)(w - g.cstart[i]), c.acc, threadIdx.x & 63);
+        return;
     }
+    if (b < cblocks + rblocks) {
+        const int64_t r = (int64_t)(b - cblocks) * blockDim.x + threadIdx.x;
+        if (r >= g.rstart[g.count]) return;
+        int i = 0;
+#pragma unroll
+        for (int j = 1; j < kMaxGroup; j++)
+            if (j < g.count && r >= g.rstart[j]) i = j;
+        reduce_bias_row<S>(g.p[i], (int)(r - g.rstart[i]));
+        return;
+    }
+    const int64_t q = (int64_t)(b - cblocks - rblocks) * blockDim.x + threadIdx.x;
+    if (q >= g.qstart[g.count]) return;
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < kMaxGroup; j++)
+        if (j < g.count && q >= g.qstart[j]) i = j;
+    reduce_quad<S>(g.p[i], q - g.qstart[i]);
 }
 
 template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
@@ -513,15 +518,17 @@ static void set_column_sums(GroupParams &g, int ncs, const om_column_sum *cs) {
 
 // The grouped reduce: split-K partials (S splits) of g's products, their fused bias sums and g's column sums.
 static om_status launch_group_reduce(om_ctx *ctx, const GroupParams &g, int splits, hipStream_t stream) {
-    int64_t units = g.qstart[g.count] > g.rstart[g.count] ? g.qstart[g.count] : g.rstart[g.count];
-    if (64 * (int64_t)g.cstart[g.ncs] > units) units = 64 * (int64_t)g.cstart[g.ncs];
-    if (units == 0) return OM_OK;
-    const dim3 grid(om::grid1d(units, 256, 4096));
-    if (splits <= 1) hipLaunchKernelGGL(k_splitk_reduce_group<1>, grid, dim3(256), 0, stream, g);
-    else if (splits == 2) hipLaunchKernelGGL(k_splitk_reduce_group<2>, grid, dim3(256), 0, stream, g);
-    else if (splits == 4) hipLaunchKernelGGL(k_splitk_reduce_group<4>, grid, dim3(256), 0, stream, g);
-    else if (splits == 8) hipLaunchKernelGGL(k_splitk_reduce_group<8>, grid, dim3(256), 0, stream, g);
-    else hipLaunchKernelGGL(k_splitk_reduce_group<16>, grid, dim3(256), 0, stream, g);
+    const int64_t qb = (g.qstart[g.count] + 255) / 256, rb = (g.rstart[g.count] + 255) / 256;
+    const int64_t cb = ((int64_t)g.cstart[g.ncs] + 3) / 4;
+    if (qb + rb + cb == 0) return OM_OK;
+    OM_REQUIRE(ctx, qb + rb + cb < ((int64_t)1 << 31), "grouped reduce: %lld blocks", (long long)(qb + rb + cb));
+    const dim3 grid((unsigned)(qb + rb + cb));
+    const int c = (int)cb, r = (int)rb;
+    if (splits <= 1) hipLaunchKernelGGL(k_splitk_reduce_group<1>, grid, dim3(256), 0, stream, g, c, r);
+    else if (splits == 2) hipLaunchKernelGGL(k_splitk_reduce_group<2>, grid, dim3(256), 0, stream, g, c, r);
+    else if (splits == 4) hipLaunchKernelGGL(k_splitk_reduce_group<4>, grid, dim3(256), 0, stream, g, c, r);
+    else if (splits == 8) hipLaunchKernelGGL(k_splitk_reduce_group<8>, grid, dim3(256), 0, stream, g, c, r);
+    else hipLaunchKernelGGL(k_splitk_reduce_group<16>, grid, dim3(256), 0, stream, g, c, r);
     return OM_LAUNCH_CHECK(ctx, "grouped reduce");
 }
 

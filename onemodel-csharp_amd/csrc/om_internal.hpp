@@ -181,8 +181,19 @@ __device__ __forceinline__ float max16(float v) {
 // of part[c * cols + col] in increasing c, then the fixed butterfly; lane 0 writes out[col] (+)= the float of the sum.
 __device__ __forceinline__ void column_sum_wave(const double *part, float *out, int chunks, int cols, int col, int acc,
                                                 int lane) {
+    // eight of a lane's loads in flight before their adds (same order: c = lane, lane + 64, ...)
     double s = 0.0;
-    for (int c = lane; c < chunks; c += 64) s += part[(int64_t)c * cols + col];
+    for (int c0 = 0; c0 < chunks; c0 += 64 * 8) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + 64 * u + lane;
+            v[u] = c < chunks ? part[(int64_t)c * cols + col] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (c0 + 64 * u + lane < chunks) s += v[u];
+    }
     s = wave_sum(s);
     if (lane == 0) {
         float v = (float)s;

@@ -493,6 +493,35 @@ __global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ lo
     }
 }
 
+// One row of the cross-entropy forward with the unit gradient (a wavefront): logp = x - (max + log(double sum of
+// exp(x - max))), then k_xent_bwd's arithmetic for g = 1: dx = d - exp(logp) s with d = -scale at the target (when the
+// row counts) and s = -scale (0 for an ignored row). lpt, when given, receives logp at the target (0 <= t < cols).
+__device__ __forceinline__ void xent_row(const float *__restrict__ x, float *__restrict__ y, float *__restrict__ dx,
+                                         int r, int cols, int t, int ignore, float scale, int lane, float *lpt) {
+    const float *xr = x + (int64_t)r * cols;
+    float *yr = y + (int64_t)r * cols, *dr = dx + (int64_t)r * cols;
+    float mx = -__int_as_float(0x7F800000);
+    for (int j = lane; j < cols; j += 64) mx = xr[j] > mx ? xr[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float w = __shfl_xor(mx, o, 64);
+        mx = w > mx ? w : mx;
+    }
+    double sum = 0.0;
+    for (int j = lane; j < cols; j += 64) sum += (double)expf(xr[j] - mx);
+    sum = omd::wave_sum(sum);
+    const float lse = mx + logf((float)sum);
+    const bool counted = t != ignore;
+    const float sr = counted ? -scale : 0.0f;
+    for (int j = lane; j < cols; j += 64) {
+        const float lp = xr[j] - lse;
+        yr[j] = lp;
+        if (lpt && j == t) *lpt = lp;
+        const float d = (counted && j == t) ? -scale : 0.0f;
+        dr[j] = d - expf(lp) * sr;
+    }
+}
+
 // Cross-entropy forward with the unit gradient: per row (a wavefront each), k_logsoftmax_rows' arithmetic writing
 // logp, then k_xent_bwd's for g = 1 and the mean reduction, reading the logp values just computed. The count of
 // rows that are not ignored, which the gradient's scale needs, is formed by every block from all targets (an exact
@@ -512,29 +541,7 @@ __global__ void __launch_bounds__(kBlock) k_xent_fwd_rows(const float *__restric
     for (int i = 0; i < kBlock / 64; i++) count += shc[i];
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
-    const float *xr = x + (int64_t)r * cols;
-    float *yr = y + (int64_t)r * cols, *dr = dx + (int64_t)r * cols;
-    float mx = -__int_as_float(0x7F800000);
-    for (int j = lane; j < cols; j += 64) mx = xr[j] > mx ? xr[j] : mx;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float w = __shfl_xor(mx, o, 64);
-        mx = w > mx ? w : mx;
-    }
-    double sum = 0.0;
-    for (int j = lane; j < cols; j += 64) sum += (double)expf(xr[j] - mx);
-    sum = omd::wave_sum(sum);
-    const float lse = mx + logf((float)sum);
-    const float scale = 1.0f / (float)(count > 1 ? count : 1);
-    const int t = tg[r];
-    const bool counted = t != ignore;
-    const float sr = counted ? -scale : 0.0f;
-    for (int j = lane; j < cols; j += 64) {
-        const float lp = xr[j] - lse;
-        yr[j] = lp;
-        const float d = (counted && j == t) ? -scale : 0.0f;
-        dr[j] = d - expf(lp) * sr;
-    }
+    xent_row(x, y, dx, r, cols, tg[r], ignore, 1.0f / (float)(count > 1 ? count : 1), lane, nullptr);
 }
 
 // Fused NllBackward + LogSoftmax backward (BackwardNn.cs:54-80, 602-632). scale = g/max(1,count) (or g); the NLL

@@ -402,7 +402,7 @@ def test_softmax_rows(dev, T, rows, cols):
     assert np.array_equal(np.isfinite(dgot), ok) and scaled(dgot[ok], dref[ok]) <= 1e-6
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 10), (4096, 9), (1024, 37)])
+@pytest.mark.parametrize("rows,cols", [(64, 10), (4096, 9), (1024, 37), (7, 3), (1000, 100), (1025, 5)])
 def test_cross_entropy(dev, T, rows, cols):
     rng = np.random.default_rng(cols)
     z = rnd(rng, rows, cols, scale=2.0)
