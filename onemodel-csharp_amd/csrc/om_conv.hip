@@ -462,14 +462,12 @@ static om_status conv_fwd(om_ctx *ctx, const char *what, const float *x, const f
     p.sc_outer = (int64_t)Cout * p.n;
     p.bias = bias;
     p.bias_per_row = 1;
+    p.epi = relu ? omg::EPI_RELU : omg::EPI_NONE;  // ReLU after the bias, in the store
     bool vec = ((uintptr_t)w % 16 == 0) && p.k % 4 == 0;
     int bm, bn;
     conv_tiles(p.m, p.n, N, ctx->num_cus, bm, bn);
     launch_conv<0>(p, bm, bn, vec, ctx->stream);
-    s = OM_LAUNCH_CHECK(ctx, what);
-    // the general kernel has no ReLU epilogue: ReLU in place
-    if (!s && relu) s = om_relu_fwd(ctx, y, y, (int64_t)N * Cout * OH * OW);
-    return s;
+    return OM_LAUNCH_CHECK(ctx, what);
 }
 
 om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,

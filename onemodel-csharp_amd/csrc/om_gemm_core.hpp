@@ -61,7 +61,8 @@ struct Params {
     //   epi EPI_GELU: C gets v (the pre-activation, which GELU's backward reads) and out2 gets gelu(v);
     //   epi EPI_GELU_GRAD: C gets gelu_grad(v, aux[row * ldaux + col]) (GELU's backward of the product).
     //   epi EPI_GELU_SLOPE: C gets gelu(v) and out2 gets GELU's slope at v (all GELU's backward needs);
-    //   epi EPI_MUL_AUX: C gets v * aux[row * ldaux + col] (GELU's backward of the product, given that slope).
+    //   epi EPI_MUL_AUX: C gets v * aux[row * ldaux + col] (GELU's backward of the product, given that slope);
+    //   epi EPI_RELU: C gets ReluUn(v) (v > 0 ? v : 0, NaN kept), om_relu_fwd's arithmetic (a convolution stage).
     const float *resid;
     int64_t ldr;
     int epi;
@@ -77,7 +78,7 @@ struct Params {
     int db_acc;
 };
 
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4 };
+enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4, EPI_RELU = 5 };
 
 // Several products launched together (the grouped weight-gradient kernel and its reduce): product i owns workgroups
 // [start[i], start[i+1]) of the GEMM launch, float4 quads [qstart[i], qstart[i+1]) and bias rows
@@ -113,6 +114,7 @@ __device__ __forceinline__ void epilogue(const Params &p, float *cbase, int64_t 
     if (mask) v = v + mask[(int64_t)row * p.n + col];
     if (p.bias) v = v + p.bias[p.bias_per_row ? row : col];
     if (p.resid) v = v + p.resid[(int64_t)row * p.ldr + col];
+    if (p.epi == EPI_RELU) v = v > 0.0f ? v : (v == v ? 0.0f : v);
     if constexpr (GELU) {
         if (p.epi == EPI_GELU) {
             p.out2[(int64_t)row * p.ld2 + col] = omd::gelu(v);

@@ -223,6 +223,12 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
 #pragma unroll
                 for (int j = 0; j < TN; j++) v[r][j] = v[r][j] + t[r][j];
         }
+        if (p.epi == EPI_RELU) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) v[r][j] = v[r][j] > 0.0f ? v[r][j] : (v[r][j] == v[r][j] ? 0.0f : v[r][j]);
+        }
         if constexpr (GELU) {
             if (p.epi == EPI_GELU) {
 #pragma unroll
