@@ -457,6 +457,20 @@ om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
                      const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
                      const int32_t *h_targets, int n_targets, const float *g, float *dlp, int T, int B, int C,
                      int blank, int reduction, int accumulate);
+/* The same pair with each recursion run once (the values of om_ctc_fwd / om_ctc_bwd, bit for bit; the reference's
+ * CtcBackward recomputes alpha and then runs beta, BackwardRecurrent.cs:253-296): om_ctc_fwd_tables also runs the beta
+ * recursion, beside alpha on another wavefront, and keeps both tables in `tables` (device memory of at least
+ * om_ctc_tables_bytes(T, B, max(tgt_len)) bytes, given as tables_bytes); om_ctc_bwd_tables forms the gradient from
+ * them, with the same arguments as om_ctc_bwd, so the backward repeats neither recursion. */
+uint64_t om_ctc_tables_bytes(int T, int B, int max_tgt_len);
+om_status om_ctc_fwd_tables(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                            const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                            const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
+                            int zero_infinity, float *loss, double *tables, uint64_t tables_bytes);
+om_status om_ctc_bwd_tables(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                            const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                            const int32_t *h_targets, int n_targets, const float *g, float *dlp, int T, int B, int C,
+                            int blank, int reduction, int accumulate, const double *tables, uint64_t tables_bytes);
 
 /* ---------------------------------------------------------------------------------------------- optimizer */
 /* Adam.UpdateRange (Optimizers.cs:554-589) over n contiguous elements: the tape keeps parameters, gradients and

@@ -100,6 +100,9 @@ _OM_SIGS = {
     "om_maxpool_relu_bwd": [vp, vp, vp, vp, vp] + [ci] * 12 + [ci],
     "om_ctc_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, vp],
     "om_ctc_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci],
+    "om_ctc_tables_bytes": [ci, ci, ci],
+    "om_ctc_fwd_tables": [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci, ci, vp, vp, u64],
+    "om_ctc_bwd_tables": [vp, vp, vp, vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, ci, vp, u64],
     "om_adam_step": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32],
     "om_adam_scalars": [f32, f32, f32, i64, C.POINTER(f32), C.POINTER(f32)],
     "om_adam_step_scaled": [vp, vp, vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, ci, f32, f32, vp],
@@ -135,6 +138,7 @@ _OM_SIGS = {
     "om_attention_bwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
 }
 _RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
+            "om_ctc_tables_bytes": u64,
             "om_linear_small": ci,
             "om_layernorm_bwd_chunks": ci,
             "om_stager_slot_bytes": u64}

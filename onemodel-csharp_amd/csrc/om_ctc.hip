@@ -243,32 +243,11 @@ __device__ void recursions(const float *lp, int B, int C, int b, int len, const 
     }
 }
 
-// CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence, in two phases. First the alpha recursion (recomputed, as
-// the reference recomputes it) and the beta recursion run side by side on two wavefronts, alpha forward and beta
-// backward in t, one barrier per step (each lane owns extended positions s, s + 64, ...). Then every (t, class)
-// entry of the gradient is independent: the workgroup's threads take them in turn, and each accumulates
-// logadd(alpha + beta) over the class's positions in increasing s, exactly the reference's order, so the values are
-// those of the sequential loop bit for bit.
-constexpr int kBwdBlock = 256;
-__global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
-                                                       const int32_t *__restrict__ in_len,
-                                                       const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
-                                                       float *__restrict__ dlp, int T, int B, int C, int blank,
-                                                       int reduction, int max_ext, int acc, double *__restrict__ ws,
-                                                       int in_lds) {
-    __shared__ double nll_s;
-    extern __shared__ double tables[];
+// Both recursions of one sequence into alpha and beta (any ext): the two-wavefront form above when a lane's positions
+// fit NPL <= 4, else wavefront 0 walks alpha up and wavefront 1 beta down over all positions.
+__device__ void both_recursions(const float *lp, int B, int C, int b, int len, const int32_t *tgt, int blank, int ext,
+                                double *alpha, double *beta, int wave, int lane) {
     const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
-    const int b = blockIdx.x;
-    const int len = in_len[b], L = tgt_len[b];
-    int off = 0;
-    for (int i = 0; i < b; i++) off += tgt_len[i];
-    const int32_t *tgt = targets + off;
-    const int tt = T > 0 ? T : 1;
-    double *alpha = in_lds ? tables : ws + (int64_t)b * 2 * tt * max_ext;
-    double *beta = alpha + (int64_t)tt * max_ext;
-    const int ext = 2 * L + 1;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (ext <= 64) recursions<1>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
     else if (ext <= 128) recursions<2>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
     else if (ext <= 256) recursions<4>(lp, B, C, b, len, tgt, blank, ext, alpha, beta, wave, lane);
@@ -304,26 +283,30 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
-        double nll;
-        if (len == 0) {
-            nll = L == 0 ? 0.0 : __longlong_as_double(0x7FF0000000000000LL);
-        } else {
-            double p = alpha[(len - 1) * ext + ext - 1];
-            if (ext >= 2) p = ctc_logadd(p, alpha[(len - 1) * ext + ext - 2]);
-            nll = is_neg_inf(p) ? __longlong_as_double(0x7FF0000000000000LL) : -p;
-        }
-        nll_s = nll;
-    }
-    __syncthreads();
-    const double nll = nll_s;
+}
+
+// The sequence's negative log-likelihood from its alpha table (CtcLossMath.Alpha's end), as alpha_pass forms it.
+__device__ __forceinline__ double nll_from_alpha(const double *alpha, int len, int L, int ext) {
+    if (len == 0) return L == 0 ? 0.0 : __longlong_as_double(0x7FF0000000000000LL);
+    double p = alpha[(len - 1) * ext + ext - 1];
+    if (ext >= 2) p = ctc_logadd(p, alpha[(len - 1) * ext + ext - 2]);
+    return is_neg_inf(p) ? __longlong_as_double(0x7FF0000000000000LL) : -p;
+}
+
+// The gradient phase: every (t, class) entry of dlp for sequence b is independent; the workgroup's threads take them
+// in turn, and each accumulates logadd(alpha + beta) over the class's positions in increasing s, exactly the
+// reference's order, so the values are those of the sequential loop bit for bit. Jobs 0 .. T - 1 are the blank
+// class's entries (its chain runs over all L + 1 even positions), one per thread of the first wavefronts; the other
+// classes' entries (at most a few positions each) follow in (t, c) order, so no wavefront holds more than its share of
+// long chains.
+__device__ void gradient_phase(const float *lp, const int32_t *tgt, const double *alpha, const double *beta, double nll,
+                               const float *g, float *dlp, int T, int B, int C, int b, int len, int L, int ext,
+                               int blank, int reduction, int acc) {
+    const double NEG = -__longlong_as_double(0x7FF0000000000000LL);
     // +inf (an impossible alignment) and an empty input give a zero gradient (CtcBackward, BackwardRecurrent.cs)
     const bool none = len == 0 || (isinf(nll) && nll > 0);
     double scale = reduction == 0 ? (double)g[b] : (double)g[0];
     if (reduction == 1) scale = scale / (double)(L > 1 ? L : 1) / (double)B;
-    // Jobs 0 .. T - 1 are the blank class's entries (its chain runs over all L + 1 even positions), one per thread of
-    // the first wavefronts; the other classes' entries (at most a few positions each) follow in (t, c) order, so no
-    // wavefront holds more than its share of long chains.
     const bool blank_ok = blank >= 0 && blank < C;
     for (int job = threadIdx.x; job < T * C; job += blockDim.x) {
         int t, c;
@@ -355,6 +338,102 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
         }
         *d = v;
     }
+}
+
+__device__ __forceinline__ const int32_t *seq_targets(const int32_t *targets, const int32_t *tgt_len, int b) {
+    int off = 0;
+    for (int i = 0; i < b; i++) off += tgt_len[i];
+    return targets + off;
+}
+
+// CtcLossMath.Gradient (CtcLoss.cs:219-281) per sequence, in two phases: the alpha recursion (recomputed, as the
+// reference recomputes it) and the beta recursion side by side on two wavefronts, alpha forward and beta backward in
+// t, one barrier per step (each lane owns extended positions s, s + 64, ...); then the gradient phase.
+constexpr int kBwdBlock = 256;
+__global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__ lp, const int32_t *__restrict__ targets,
+                                                       const int32_t *__restrict__ in_len,
+                                                       const int32_t *__restrict__ tgt_len, const float *__restrict__ g,
+                                                       float *__restrict__ dlp, int T, int B, int C, int blank,
+                                                       int reduction, int max_ext, int acc, double *__restrict__ ws,
+                                                       int in_lds) {
+    __shared__ double nll_s;
+    extern __shared__ double tables[];
+    const int b = blockIdx.x;
+    const int len = in_len[b], L = tgt_len[b];
+    const int32_t *tgt = seq_targets(targets, tgt_len, b);
+    const int tt = T > 0 ? T : 1;
+    double *alpha = in_lds ? tables : ws + (int64_t)b * 2 * tt * max_ext;
+    double *beta = alpha + (int64_t)tt * max_ext;
+    const int ext = 2 * L + 1;
+    both_recursions(lp, B, C, b, len, tgt, blank, ext, alpha, beta, threadIdx.x >> 6, threadIdx.x & 63);
+    if (threadIdx.x == 0) nll_s = nll_from_alpha(alpha, len, L, ext);
+    __syncthreads();
+    gradient_phase(lp, tgt, alpha, beta, nll_s, g, dlp, T, B, C, b, len, L, ext, blank, reduction, acc);
+}
+
+// The forward of the saved-tables pair: k_ctc_bwd's recursions (alpha as k_ctc_fwd forms it, beta beside it on the
+// second wavefront) with the sequence's loss term in per[b]; the tables end in `saved` (alpha [tt][max_ext] then beta,
+// per sequence), through LDS when they fit there.
+__global__ void __launch_bounds__(kBwdBlock) k_ctc_fwd_tables(const float *__restrict__ lp,
+                                                              const int32_t *__restrict__ targets,
+                                                              const int32_t *__restrict__ in_len,
+                                                              const int32_t *__restrict__ tgt_len, int T, int B, int C,
+                                                              int blank, int max_ext, double *__restrict__ saved,
+                                                              double *__restrict__ per, int in_lds) {
+    extern __shared__ double tables[];
+    const int b = blockIdx.x;
+    const int len = in_len[b], L = tgt_len[b];
+    const int32_t *tgt = seq_targets(targets, tgt_len, b);
+    const int tt = T > 0 ? T : 1;
+    double *out = saved + (int64_t)b * 2 * tt * max_ext;
+    double *alpha = in_lds ? tables : out;
+    double *beta = alpha + (int64_t)tt * max_ext;
+    const int ext = 2 * L + 1;
+    both_recursions(lp, B, C, b, len, tgt, blank, ext, alpha, beta, threadIdx.x >> 6, threadIdx.x & 63);
+    if (threadIdx.x == 0) per[b] = nll_from_alpha(alpha, len, L, ext);
+    if (in_lds) {
+        __syncthreads();
+        // the rows the recursions wrote (t < len, s < ext) of both tables; the rest is never read
+        for (int e = threadIdx.x; e < 2 * len * ext; e += blockDim.x) {
+            const int h = e / (len * ext), r = e - h * len * ext, t = r / ext, s = r - t * ext;
+            const int64_t o = (int64_t)h * tt * max_ext + (int64_t)t * ext + s;
+            out[o] = tables[o];
+        }
+    }
+}
+
+// The gradient of the saved-tables pair: k_ctc_bwd's gradient phase over the tables k_ctc_fwd_tables left in `saved`
+// (staged into LDS when they fit), with the loss term formed again from alpha.
+__global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd_tables(const float *__restrict__ lp,
+                                                              const int32_t *__restrict__ targets,
+                                                              const int32_t *__restrict__ in_len,
+                                                              const int32_t *__restrict__ tgt_len,
+                                                              const float *__restrict__ g, float *__restrict__ dlp,
+                                                              int T, int B, int C, int blank, int reduction,
+                                                              int max_ext, int acc, const double *__restrict__ saved,
+                                                              int in_lds) {
+    __shared__ double nll_s;
+    extern __shared__ double tables[];
+    const int b = blockIdx.x;
+    const int len = in_len[b], L = tgt_len[b];
+    const int32_t *tgt = seq_targets(targets, tgt_len, b);
+    const int tt = T > 0 ? T : 1;
+    const double *src = saved + (int64_t)b * 2 * tt * max_ext;
+    const int ext = 2 * L + 1;
+    const double *alpha = src;
+    if (in_lds) {
+        for (int e = threadIdx.x; e < 2 * len * ext; e += blockDim.x) {
+            const int h = e / (len * ext), r = e - h * len * ext, t = r / ext, s = r - t * ext;
+            const int64_t o = (int64_t)h * tt * max_ext + (int64_t)t * ext + s;
+            tables[o] = src[o];
+        }
+        __syncthreads();
+        alpha = tables;
+    }
+    const double *beta = alpha + (int64_t)tt * max_ext;
+    if (threadIdx.x == 0) nll_s = nll_from_alpha(alpha, len, L, ext);
+    __syncthreads();
+    gradient_phase(lp, tgt, alpha, beta, nll_s, g, dlp, T, B, C, b, len, L, ext, blank, reduction, acc);
 }
 
 // The host-side checks both entry points run on the host copies of the lengths and labels (CtcLoss.cs:40-153 raises
@@ -438,6 +517,58 @@ om_status om_ctc_bwd(om_ctx *ctx, const float *lp, const int32_t *targets, const
                        tgt_len, g, dlp, T, B, C, blank, reduction, max_ext, accumulate,
                        reinterpret_cast<double *>(scr), in_lds ? 1 : 0);
     return OM_LAUNCH_CHECK(ctx, "om_ctc_bwd");
+}
+
+uint64_t om_ctc_tables_bytes(int T, int B, int max_tgt_len) {
+    if (T < 0 || B < 0 || max_tgt_len < 0) return 0;
+    return sizeof(double) * 2 * (uint64_t)B * (uint64_t)(T > 0 ? T : 1) * (uint64_t)(2 * (int64_t)max_tgt_len + 1);
+}
+
+om_status om_ctc_fwd_tables(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                            const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                            const int32_t *h_targets, int n_targets, int T, int B, int C, int blank, int reduction,
+                            int zero_infinity, float *loss, double *tables, uint64_t tables_bytes) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && loss && tables, "om_ctc_fwd_tables: NULL pointer");
+    int max_ext = 1;
+    om_status s = check_args(ctx, "om_ctc_fwd_tables", h_in_len, h_tgt_len, h_targets, n_targets, T, B, C, blank,
+                             reduction, &max_ext);
+    if (s) return s;
+    const uint64_t tt = T > 0 ? T : 1, table = sizeof(double) * tt * max_ext;  // one of the two tables
+    OM_REQUIRE(ctx, tables_bytes >= 2 * table * B,
+               "om_ctc_fwd_tables: the tables need %llu bytes (om_ctc_tables_bytes), %llu given",
+               (unsigned long long)(2 * table * B), (unsigned long long)tables_bytes);
+    float *scr;
+    s = om::scratch(ctx, sizeof(double) * B, &scr);
+    if (s) return s;
+    double *per = reinterpret_cast<double *>(scr);
+    const bool in_lds = table <= kLdsTable;
+    hipLaunchKernelGGL(k_ctc_fwd_tables, dim3(B), dim3(kBwdBlock), in_lds ? 2 * table : 0, ctx->stream, lp, targets,
+                       in_len, tgt_len, T, B, C, blank, max_ext, tables, per, in_lds ? 1 : 0);
+    hipLaunchKernelGGL(k_ctc_reduce, dim3(1), dim3(64), 0, ctx->stream, per, tgt_len, B, reduction, zero_infinity,
+                       loss);
+    return OM_LAUNCH_CHECK(ctx, "om_ctc_fwd_tables");
+}
+
+om_status om_ctc_bwd_tables(om_ctx *ctx, const float *lp, const int32_t *targets, const int32_t *in_len,
+                            const int32_t *tgt_len, const int32_t *h_in_len, const int32_t *h_tgt_len,
+                            const int32_t *h_targets, int n_targets, const float *g, float *dlp, int T, int B, int C,
+                            int blank, int reduction, int accumulate, const double *tables, uint64_t tables_bytes) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, lp && targets && in_len && tgt_len && g && dlp && tables, "om_ctc_bwd_tables: NULL pointer");
+    int max_ext = 1;
+    om_status s = check_args(ctx, "om_ctc_bwd_tables", h_in_len, h_tgt_len, h_targets, n_targets, T, B, C, blank,
+                             reduction, &max_ext);
+    if (s) return s;
+    const uint64_t tt = T > 0 ? T : 1, table = sizeof(double) * tt * max_ext;
+    OM_REQUIRE(ctx, tables_bytes >= 2 * table * B,
+               "om_ctc_bwd_tables: the tables need %llu bytes (om_ctc_tables_bytes), %llu given",
+               (unsigned long long)(2 * table * B), (unsigned long long)tables_bytes);
+    const bool in_lds = table <= kLdsTable;
+    hipLaunchKernelGGL(k_ctc_bwd_tables, dim3(B), dim3(kBwdBlock), in_lds ? 2 * table : 0, ctx->stream, lp, targets,
+                       in_len, tgt_len, g, dlp, T, B, C, blank, reduction, max_ext, accumulate, tables,
+                       in_lds ? 1 : 0);
+    return OM_LAUNCH_CHECK(ctx, "om_ctc_bwd_tables");
 }
 
 }  // extern "C"

@@ -887,16 +887,25 @@ Tensor ctc_loss(const Tensor &lp, const std::vector<int32_t> &targets, const std
     if (!dil) dil = upload(in_len);
     if (!dtl) dtl = upload(tgt_len);
     Tensor loss = reduction == 0 ? make({B}) : make({});
-    OMT(om_ctc_fwd(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(), (int)targets.size(), T,
-                   B, Cc, blank, reduction, 0, loss->data));
-    if (tracked({&lp})) {
-        attach(loss, "CtcLoss", {lp}, [=](Engine &e, Record &r, const float *g) {
-            int a;
-            float *d = e.dest(r, 0, &a);
-            OMT(om_ctc_bwd(C(), r.inputs[0]->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
-                           (int)targets.size(), g, d, T, B, Cc, blank, reduction, a));
-        }, {lp, d_targets, d_in_len, d_tgt_len});
+    if (!tracked({&lp})) {
+        OMT(om_ctc_fwd(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
+                       (int)targets.size(), T, B, Cc, blank, reduction, 0, loss->data));
+        return loss;
     }
+    // the forward also runs the beta recursion (beside alpha) and keeps both tables for the backward, which then only
+    // forms the gradient
+    int max_tgt = 0;
+    for (int32_t l : tgt_len) max_tgt = l > max_tgt ? l : max_tgt;
+    const uint64_t tb = om_ctc_tables_bytes(T, B, max_tgt);
+    double *tables = reinterpret_cast<double *>(dev().step_floats((int64_t)((tb + 3) / 4)));
+    OMT(om_ctc_fwd_tables(C(), lp->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
+                          (int)targets.size(), T, B, Cc, blank, reduction, 0, loss->data, tables, tb));
+    attach(loss, "CtcLoss", {lp}, [=](Engine &e, Record &r, const float *g) {
+        int a;
+        float *d = e.dest(r, 0, &a);
+        OMT(om_ctc_bwd_tables(C(), r.inputs[0]->data, dt, dil, dtl, in_len.data(), tgt_len.data(), targets.data(),
+                              (int)targets.size(), g, d, T, B, Cc, blank, reduction, a, tables, tb));
+    }, {lp, d_targets, d_in_len, d_tgt_len});
     return loss;
 }
 

@@ -802,6 +802,17 @@ def test_ctc_bit_exact(dev, T, red):
         got = dev.get(L)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
         assert np.array_equal(dev.get(D).view(np.uint32), dref.view(np.uint32)), name
+        # the pair that runs each recursion once (beta beside alpha in the forward, tables kept): the same bits
+        tb = dev.ctx.L.om_ctc_tables_bytes(Tn, B, int(tl.max()) if tl.size else 0)
+        TB, L2, D2 = dev.empty((tb // 4 + 1,)), dev.empty((n_out,)), dev.empty(lp.shape, fill=123.0)
+        dev.call("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L2, TB, tb)
+        dev.call("om_ctc_bwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D2, Tn, B, Cc, 0, red, 0, TB, tb)
+        assert np.array_equal(dev.get(L2).view(np.uint32), ref.view(np.uint32)), name
+        assert np.array_equal(dev.get(D2).view(np.uint32), dref.view(np.uint32)), name
+        # a tables buffer smaller than om_ctc_tables_bytes is refused before any launch
+        assert dev.status("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L2, TB,
+                          tb - 8) == 1
+        assert b"om_ctc_tables_bytes" in dev.ctx.L.om_last_error(dev.ctx.h)
 
 
 def test_ctc_rejects_bad_targets(dev):
