@@ -1086,6 +1086,126 @@ om_status narrow_bwd(om_ctx *ctx, const float *g, const float *x, const float *w
 }
 }  // namespace
 
+// ------------------------------------------------------------------------------------------------------------------
+// Linear layers over a small batch whose product is too large for the VALU paths above but only a few dozen 16 x 16
+// MFMA blocks (C1's first layer: 64 rows, 784 -> 256). The engine runs these as a split-K product, its reduce and,
+// for dW, two column-sum launches for the bias gradient; here the forward and the weight gradient (with the bias
+// gradient) are one launch each, whose time is a short MFMA chain.
+namespace {
+constexpr int kMidW = 8;  // wavefronts per forward workgroup, each taking every eighth K block of 16
+bool linear_mid(int rows, int in, int out) {
+    return !linear_small(rows, in, out) && !linear_narrow(rows, in, out) && rows >= 16 && rows <= 256 &&
+           rows % 16 == 0 && in % 16 == 0 && out % 16 == 0 && in <= 8192 &&
+           (int64_t)(rows / 16) * (out / 16) <= 256;
+}
+bool al16p(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// y[r][o] = (sum over i of x[r][i] w[o][i]) + b[o] (+ resid[r][o]): a workgroup per 16 x 16 block of y. MFMA step s
+// of K block kb takes k = 16 kb + 4 kl + s (lane l16 + 16 kl: x row r0 + l16 as A, w row o0 + l16 as B), so a lane
+// loads one float4 of each per block, straight from global memory. Wavefront v takes blocks v, v + 8, ..., four
+// blocks' loads in flight at a time; wavefront 0 then adds the others' partial sums in wavefront order and applies
+// the bias and the residual (the engine's epilogue order).
+__global__ void __launch_bounds__(64 * kMidW) k_linear_mid_fwd(const float *__restrict__ x, const float *__restrict__ w,
+                                                               const float *__restrict__ b,
+                                                               const float *__restrict__ resid, float *__restrict__ y,
+                                                               int in, int out) {
+    __shared__ floatx4 part[kMidW - 1][64];
+    const int tb = out / 16, r0 = (blockIdx.x / tb) * 16, o0 = (blockIdx.x % tb) * 16;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
+    const float *xa = x + (int64_t)(r0 + l16) * in + 4 * kl, *wb = w + (int64_t)(o0 + l16) * in + 4 * kl;
+    const int nkb = in / 16;
+    constexpr int R = 4;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kb0 = wv; kb0 < nkb; kb0 += kMidW * R) {
+        floatx4 av[R], bv[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int kb = min(kb0 + kMidW * u, nkb - 1);  // clamped: such a block's loads are not used
+            av[u] = *reinterpret_cast<const floatx4 *>(xa + 16 * kb);
+            bv[u] = *reinterpret_cast<const floatx4 *>(wb + 16 * kb);
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (kb0 + kMidW * u < nkb)  // uniform over the wavefront
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][s], bv[u][s], acc, 0, 0, 0);
+    }
+    if (wv > 0) part[wv - 1][lane] = acc;
+    __syncthreads();
+    if (wv > 0) return;
+#pragma unroll
+    for (int v = 0; v < kMidW - 1; v++) acc += part[v][lane];
+    const int col = o0 + l16;
+    const float bc = b ? b[col] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int64_t at = (int64_t)(r0 + 4 * kl + r) * out + col;
+        float v = acc[r];
+        if (b) v = v + bc;
+        if (resid) v = v + resid[at];
+        y[at] = v;
+    }
+}
+
+// dw[o][i] (+)= sum over r of g[r][o] x[r][i]: a wavefront per 16 x 16 block of dw, K = rows in blocks of 16 (MFMA
+// step s of block kb takes r = 16 kb + 4 kl + s: g[r][o0 + l16] as A, x[r][i0 + l16] as B), four blocks' loads in
+// flight at a time. The workgroups after the dw blocks' own give each thread a column o of g for db[o] (+)= the sum
+// over r of g[r][o] in double, in increasing r.
+__global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__ g, const float *__restrict__ x,
+                                                       float *__restrict__ dw, float *__restrict__ db, int rows,
+                                                       int in, int out, int nblk, int acc_dw, int acc_db) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
+    const int dw_groups = (nblk + 3) / 4;
+    if ((int)blockIdx.x >= dw_groups) {
+        const int o = ((int)blockIdx.x - dw_groups) * 256 + (int)threadIdx.x;
+        if (o >= out) return;
+        double s = 0.0;
+#pragma unroll 8
+        for (int r = 0; r < rows; r++) s += (double)g[(int64_t)r * out + o];
+        const float v = (float)s;
+        db[o] = acc_db ? db[o] + v : v;
+        return;
+    }
+    const int blk = (int)blockIdx.x * 4 + wv;
+    if (blk >= nblk) return;
+    const int ti = in / 16, o0 = (blk / ti) * 16, i0 = (blk % ti) * 16;
+    const float *ga = g + (int64_t)4 * kl * out + o0 + l16, *xb = x + (int64_t)4 * kl * in + i0 + l16;
+    constexpr int R = 4;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int nkb = rows / 16;
+    for (int kb0 = 0; kb0 < nkb; kb0 += R) {
+        float av[R][4], bv[R][4];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int kb = min(kb0 + u, nkb - 1);  // clamped: such a block's loads are not used
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                av[u][s] = ga[(int64_t)(16 * kb + s) * out];
+                bv[u][s] = xb[(int64_t)(16 * kb + s) * in];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (kb0 + u < nkb)
+#pragma unroll
+                for (int s = 0; s < 4; s++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u][s], bv[u][s], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float *p = dw + (int64_t)(o0 + 4 * kl + r) * in + i0 + l16;
+        *p = acc_dw ? *p + acc[r] : acc[r];
+    }
+}
+
+bool launch_mid_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid, float *y,
+                    int rows, int in, int out) {
+    if (!linear_mid(rows, in, out) || !al16p(x) || !al16p(w)) return false;
+    hipLaunchKernelGGL(k_linear_mid_fwd, dim3((unsigned)((rows / 16) * (out / 16))), dim3(64 * kMidW), 0,
+                       om::cur_stream(ctx), x, w, b, resid, y, in, out);
+    return true;
+}
+}  // namespace
+
 static om_status param_grads(om_ctx *ctx, int n_dw, const om_linear_dw *dw, int rows, int n_cs,
                              const om_column_sum *cs) {
     // The products the grouped launch can take go there together (with the column sums); the others, and all of
@@ -1158,6 +1278,7 @@ om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float
         launch_small_fwd(om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd");
     }
+    if (launch_mid_fwd(ctx, x, w, b, nullptr, y, rows, in, out)) return OM_LAUNCH_CHECK(ctx, "om_linear_fwd");
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
     p.bias = b;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd");
@@ -1185,6 +1306,13 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
         s = omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd dx");
         if (s) return s;
     }
+    if (dw && linear_mid(rows, in, out)) {  // dW and db in one launch
+        const int nblk = (out / 16) * (in / 16);
+        const unsigned grid = (unsigned)((nblk + 3) / 4 + (db ? (out + 255) / 256 : 0));
+        hipLaunchKernelGGL(k_linear_mid_dw, dim3(grid), dim3(256), 0, om::cur_stream(ctx), g, x, dw, db, rows, in, out,
+                           nblk, acc_dw, acc_db);
+        return OM_LAUNCH_CHECK(ctx, "om_linear_bwd dw");
+    }
     bool db_done = false;
     if (dw) {
         omg::Params p = omg::dense_params(out, in, rows, g, out, x, in, dw, in);
@@ -1205,6 +1333,7 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
         launch_small_fwd(om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
         return OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid");
     }
+    if (launch_mid_fwd(ctx, x, w, b, resid, y, rows, in, out)) return OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid");
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
     p.bias = b;
     p.resid = resid;

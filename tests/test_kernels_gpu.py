@@ -116,7 +116,11 @@ def test_gemm_rejects_bad_shapes(dev):
                                            # output count at the top of a rounded-up instance, unaligned rows,
                                            # several input chunks, one output, the row-chunk cap
                                            (1024, 256, 37), (2048, 100, 64), (1000, 33, 33), (300, 2000, 5),
-                                           (257, 17, 1), (20000, 8, 3)])
+                                           (257, 17, 1), (20000, 8, 3),
+                                           # one-launch MFMA layers over a small batch (C1's first layer above):
+                                           # one block, K blocks that leave some wavefronts a short last round,
+                                           # the block-count bound, a long K
+                                           (16, 16, 16), (64, 208, 80), (256, 256, 256), (16, 4096, 128)])
 def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     rng = np.random.default_rng(rows + inf + outf)
     x, w, b, g = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf), rnd(rng, rows, outf)
