@@ -171,6 +171,11 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
  * y = resid + (x w^T + b), in that rounding order, in one launch. */
 om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,
                               float *y, int rows, int in, int out);
+/* Linear followed by ReLU (Ops.Layers.cs:715-733, then Ops.Relu): y = relu(x w^T + b), bit for bit om_linear_fwd then
+ * om_relu_fwd, with the ReLU applied in the product's epilogue (the one-launch small layers run the two launches).
+ * No counterpart as one call; the ReLU's backward reads y. */
+om_status om_linear_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
+                             int out);
 /* Linear followed by GELU (erf form, Ops.Nn.cs:86-112) in one launch: h = x w^T + b (the pre-activation GELU's
  * backward reads) and a = gelu(h), both [rows, out]. */
 om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *h, float *a, int rows,

@@ -95,7 +95,7 @@ void om::probe_end(om_ctx *ctx, int slot) {
 
 extern "C" {
 
-int om_abi_version(void) { return 102; }
+int om_abi_version(void) { return 103; }
 
 om_status om_ctx_create(int device, om_ctx **out) {
     if (!out) return om::fail(nullptr, OM_E_ARG, "om_ctx_create: out is NULL");

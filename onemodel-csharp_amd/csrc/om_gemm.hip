@@ -202,6 +202,10 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 #undef OMG_CASE
 }
 
+// The epilogues only some tile instances carry (G = true): GELU and its backward terms. EPI_RELU, like the bias and
+// the residual, is applied by every instance.
+static bool gelu_epi(int epi) { return epi != EPI_NONE && epi != EPI_RELU; }
+
 // OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for comparisons); otherwise NT tiles with
 // 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
 static bool dma_disabled() {
@@ -213,7 +217,7 @@ static bool dma_disabled() {
 template <int BM, int BN, int BKT, bool G>
 static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
-    const bool gelu = p.epi != EPI_NONE;
+    const bool gelu = gelu_epi(p.epi);
     if (gelu && (!G || ta)) return false;
 #define OMG_L(K, NTH, TA_, TB_)                                                                                  \
     if (gelu)                                                                                                    \
@@ -247,7 +251,7 @@ static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t s
 template <int BM, int BN, int BKT, bool G>
 static bool launch_x2(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
-    const bool gelu = p.epi != EPI_NONE;
+    const bool gelu = gelu_epi(p.epi);
     if (gelu && (!G || ta)) return false;
     if (!ta && !tb) {
         OMG_L(k_gemm_x2, 2 * NT, false, false)
@@ -440,9 +444,9 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     bool fast = vec && !(ta && tb) && p.k > 0 && p.m > 32 && p.n > 32 && p.m % 4 == 0 && p.n % 4 == 0 &&
                 p.k % 4 == 0;
     Choice c = p.k <= 0 ? Choice{64, 64, 1, 1, 16}
-                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus, p.epi != EPI_NONE)
+                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus, gelu_epi(p.epi))
                                 : choose(p.m, p.n, p.k, batch, ctx->num_cus));
-    if (fast && p.epi != EPI_NONE) {  // only some tiles carry the GELU epilogue
+    if (fast && gelu_epi(p.epi)) {  // only some tiles carry the GELU epilogue
         const bool ok = ((c.bkt == 32 || c.bkt == 33) && c.bm == 64 && (c.bn == 64 || c.bn == 96)) ||
                         (c.bkt == 64 && c.bm == 64 && c.bn == 64);
         if (!ok) c = with_splits(64, 64, 32, p.k, c.splits);
@@ -1104,11 +1108,11 @@ bool al16p(const void *p) { return ((uintptr_t)p & 15) == 0; }
 // of K block kb takes k = 16 kb + 4 kl + s (lane l16 + 16 kl: x row r0 + l16 as A, w row o0 + l16 as B), so a lane
 // loads one float4 of each per block, straight from global memory. Wavefront v takes blocks v, v + 8, ..., four
 // blocks' loads in flight at a time; wavefront 0 then adds the others' partial sums in wavefront order and applies
-// the bias and the residual (the engine's epilogue order).
+// the bias, the residual and the ReLU (the engine's epilogue order).
 __global__ void __launch_bounds__(64 * kMidW) k_linear_mid_fwd(const float *__restrict__ x, const float *__restrict__ w,
                                                                const float *__restrict__ b,
                                                                const float *__restrict__ resid, float *__restrict__ y,
-                                                               int in, int out) {
+                                                               int in, int out, int relu) {
     __shared__ floatx4 part[kMidW - 1][64];
     const int tb = out / 16, r0 = (blockIdx.x / tb) * 16, o0 = (blockIdx.x % tb) * 16;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
@@ -1143,6 +1147,7 @@ __global__ void __launch_bounds__(64 * kMidW) k_linear_mid_fwd(const float *__re
         float v = acc[r];
         if (b) v = v + bc;
         if (resid) v = v + resid[at];
+        if (relu) v = v > 0.0f ? v : (v == v ? 0.0f : v);
         y[at] = v;
     }
 }
@@ -1198,10 +1203,10 @@ __global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__
 }
 
 bool launch_mid_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid, float *y,
-                    int rows, int in, int out) {
+                    int rows, int in, int out, bool relu = false) {
     if (!linear_mid(rows, in, out) || !al16p(x) || !al16p(w)) return false;
     hipLaunchKernelGGL(k_linear_mid_fwd, dim3((unsigned)((rows / 16) * (out / 16))), dim3(64 * kMidW), 0,
-                       om::cur_stream(ctx), x, w, b, resid, y, in, out);
+                       om::cur_stream(ctx), x, w, b, resid, y, in, out, relu ? 1 : 0);
     return true;
 }
 }  // namespace
@@ -1282,6 +1287,22 @@ om_status om_linear_fwd(om_ctx *ctx, const float *x, const float *w, const float
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
     p.bias = b;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd");
+}
+
+om_status om_linear_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
+                             int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && y && rows >= 0 && in > 0 && out > 0, "om_linear_relu_fwd: bad arguments");
+    if (linear_small(rows, in, out) || linear_narrow(rows, in, out)) {  // the one-launch chains, then the ReLU
+        launch_small_fwd(om::cur_stream(ctx), x, w, b, nullptr, y, rows, in, out);
+        om_status s = OM_LAUNCH_CHECK(ctx, "om_linear_relu_fwd");
+        return s ? s : om_relu_fwd(ctx, y, y, (int64_t)rows * out);
+    }
+    if (launch_mid_fwd(ctx, x, w, b, nullptr, y, rows, in, out, true)) return OM_LAUNCH_CHECK(ctx, "om_linear_relu_fwd");
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
+    p.bias = b;
+    p.epi = omg::EPI_RELU;
+    return omg::launch_dense(ctx, p, false, true, 1, "om_linear_relu_fwd");
 }
 
 om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,

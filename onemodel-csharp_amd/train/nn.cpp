@@ -995,7 +995,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.add_input("x", {B, 784}, normal(1, 1, (int64_t)B * 784), false);
         M.add_int_input("labels", {B}, ints(1, 2, B, 0, 10));
         M.loss_fn = [mp](omt_model &s) {
-            return cross_entropy((*mp->l2)(relu((*mp->l1)(s.input("x").t))), s.input("labels").t);
+            return cross_entropy((*mp->l2)(mp->l1->relu_of(s.input("x").t)), s.input("labels").t);
         };
     } else if (cfg == 2) {
         const int B = pick(sc.batch, 32), HW = pick(sc.hw, 56);
@@ -1107,7 +1107,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.add_input("x", {B, 20}, std::vector<float>((size_t)B * 20, 0.0f), false);
         M.add_int_input("labels", {B}, std::vector<int32_t>(B, 0)).set_range(0, 4);
         M.loss_fn = [mp](omt_model &s) {
-            return cross_entropy((*mp->l2)(relu((*mp->l1)(s.input("x").t))), s.input("labels").t);
+            return cross_entropy((*mp->l2)(mp->l1->relu_of(s.input("x").t)), s.input("labels").t);
         };
         M.opt_kind = OPT_SGD;
         M.lr = 0.05f;

@@ -322,6 +322,24 @@ static void attach(const Tensor &out, const char *op, std::vector<Tensor> inputs
     out->grad_fn = r;
 }
 
+// The Linear's backward from the gradient g of its output (inputs x, w and optionally b of record r): dx now, dW and
+// db queued for the grouped weight-gradient launch, or all three in one launch for the small layers.
+static void linear_backward(Engine &e, Record &r, const float *g, int rows, int in, int out) {
+    int ax, aw, ab = 0;
+    float *dx = e.dest(r, 0, &ax);
+    if (om_linear_small(rows, in, out)) {  // dx, dw and db in one launch
+        float *dw = e.dest(r, 1, &aw);
+        float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+        OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw, ab));
+        return;
+    }
+    if (dx) OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, in, out, ax, 0,
+                              0));
+    float *dw = e.dest(r, 1, &aw);
+    float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+    e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
+}
+
 Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
     if (w->shape.size() != 2 || x->shape.empty() || x->shape.back() != w->shape[1])
         shape_error("Linear: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w->shape) + " ([out, in]).");
@@ -335,21 +353,34 @@ Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
         std::vector<Tensor> ins{x, w};
         if (b) ins.push_back(b);
         attach(y, "Linear", ins, [rows, in, out](Engine &e, Record &r, const float *g) {
-            int ax, aw, ab = 0;
-            float *dx = e.dest(r, 0, &ax);
-            if (om_linear_small(rows, in, out)) {  // dx, dw and db in one launch
-                float *dw = e.dest(r, 1, &aw);
-                float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
-                OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, db, rows, in, out, ax, aw,
-                                  ab));
-                return;
-            }
-            if (dx) OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, in, out,
-                                      ax, 0, 0));
-            float *dw = e.dest(r, 1, &aw);
-            float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
-            e.queue_dw(om_linear_dw{g, r.inputs[0]->data, dw, db, in, out, aw, ab}, rows);
+            linear_backward(e, r, g, rows, in, out);
         }, {x, w});
+    }
+    return y;
+}
+
+// Linear then ReLU as one record (the pair of a conv stage's fused record, for dense layers): the forward is one
+// launch with the ReLU in the product's epilogue; the backward applies the ReLU's rule (g where y > 0, from the
+// saved output) and runs the Linear's backward on that gradient.
+Tensor linear_relu(const Tensor &x, const Tensor &w, const Tensor &b) {
+    if (w->shape.size() != 2 || x->shape.empty() || x->shape.back() != w->shape[1])
+        shape_error("Linear: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w->shape) + " ([out, in]).");
+    const int in = w->shape[1], out = w->shape[0];
+    const int rows = (int)(x->numel / in);
+    std::vector<int> ys = x->shape;
+    ys.back() = out;
+    Tensor y = make(ys);
+    OMT(om_linear_relu_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, rows, in, out));
+    if (tracked({&x, &w, &b})) {
+        std::vector<Tensor> ins{x, w};
+        if (b) ins.push_back(b);
+        float *yd = y->data;
+        attach(y, "LinearRelu", ins, [rows, in, out, yd](Engine &e, Record &r, const float *g) {
+            const int64_t n = (int64_t)rows * out;
+            float *gp = dev().step_floats(n);
+            OMT(om_relu_bwd(C(), g, yd, gp, n, 0));
+            linear_backward(e, r, gp, rows, in, out);
+        }, {x, w, y});
     }
     return y;
 }

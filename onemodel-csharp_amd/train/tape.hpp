@@ -179,6 +179,8 @@ void settle_grads(const std::vector<Tensor> &leaves);
 // ------------------------------------------------------------------------------------------------ ops
 // Each records a backward record when an input requires a gradient (the reference's Ops.*).
 Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b);
+// relu(Linear(x)) as one record: one launch forward (the ReLU in the product's epilogue, the same bits as the pair).
+Tensor linear_relu(const Tensor &x, const Tensor &w, const Tensor &b);
 // resid + Linear(x) (Ops.Layers.cs:715-733 then Ops.Add): one launch forward, the residual's gradient is g itself.
 Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const Tensor &resid);
 // The feed-forward sub-block resid + Linear2(GELU(Linear1(x))) as one record (resid may be empty): forward is two
@@ -298,6 +300,8 @@ class Linear : public Module {
    public:
     Linear(int in, int out, Generator &g, bool bias = true);
     Tensor operator()(const Tensor &x) const { return linear(x, w, b); }
+    // relu(this(x)) as one record (linear_relu)
+    Tensor relu_of(const Tensor &x) const { return linear_relu(x, w, b); }
     Tensor w, b;
 };
 class Conv2d : public Module {

@@ -133,6 +133,11 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     dev.call("om_linear_fwd", X, W, Bb, Y, rows, inf, outf)
     dev.call("om_linear_bwd", G, X, W, DX, DW, DB, rows, inf, outf, 0, 0, 0)
     assert scaled(dev.get(Y), y_ref) <= TOL
+    # Linear then ReLU in one call: om_linear_fwd then om_relu_fwd, bit for bit, on every path
+    YR, RR = dev.empty((rows, outf)), dev.empty((rows, outf))
+    dev.call("om_linear_relu_fwd", X, W, Bb, YR, rows, inf, outf)
+    dev.call("om_relu_fwd", Y, RR, rows * outf)
+    assert np.array_equal(dev.get(YR).view(np.uint32), dev.get(RR).view(np.uint32))
     assert scaled(dev.get(DX), dx_r) <= TOL
     assert scaled(dev.get(DW), dw_r) <= TOL
     assert scaled(dev.get(DB), db_r) <= 1e-7  # fp64 column sums: equal after rounding
