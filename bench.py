@@ -135,16 +135,16 @@ DOMINANT_ROWS = 4096
 DOMINANT_SHAPES = [(1536, 384), (384, 1536), (384, 384), (384, 1152)]
 
 
-def time_dominant_in_step(pkg, model, steps: int = 50):
+def time_dominant_in_step(pkg, model, graphed: bool, steps: int = 50):
     """The dominant launch as the training step runs it: the C3 step's one om_param_grads_group call (the grouped
     weight gradients of the block's four Linear layers with their fused bias gradients, the MFMA kernel plus its
     split-K reduce), bracketed by HIP events on the model's stream by the library's launch probe (om_ctx_probe) over
-    `steps` eager training steps. Returns (calls recorded, mean ms per call)."""
+    `steps` eager training steps. Step graphs are switched off for these steps (a replayed graph makes no library
+    calls to bracket, and a step that records one brackets nothing) whatever their state, and switched back on after
+    when `graphed` (the bench's mode). Returns (calls recorded, mean ms per call)."""
     L = pkg.load_hip()
     ctx = model.ctx
-    graphed = model.step_graph_ready
-    if graphed:
-        model.set_step_graph(False)  # a replayed graph makes no library calls to bracket
+    model.set_step_graph(False)
     assert L.om_ctx_probe(ctx, 1) == 0, L.om_last_error(ctx)
     for _ in range(steps):
         model.step()
@@ -700,7 +700,7 @@ def main():
         out["pcie_inclusive"] = time_staged(pkg, model, a.steps)
     if a.config == 3:
         # the roofline of the dominant launch as it runs inside training steps (events around the launch itself)
-        calls, ms = time_dominant_in_step(pkg, model)
+        calls, ms = time_dominant_in_step(pkg, model, graphed)
         flops = sum(2.0 * DOMINANT_ROWS * i * o for i, o in DOMINANT_SHAPES)
         if calls != 50 or ms <= 0.0:
             raise SystemExit(f"bench.py: the launch probe recorded {calls} grouped weight-gradient calls in 50 steps")

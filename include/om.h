@@ -176,6 +176,11 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
  * No counterpart as one call; the ReLU's backward reads y. */
 om_status om_linear_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *y, int rows, int in,
                              int out);
+/* Its backward: the ReLU's rule (om_relu_bwd: g where y > 0, y the saved output) and then om_linear_bwd on that
+ * gradient, with om_linear_bwd's arguments and accumulate flags. For a small batch whose product takes one launch,
+ * dW and db without dx are one launch with the rule applied to g as it is read (the same values). */
+om_status om_linear_relu_bwd(om_ctx *ctx, const float *g, const float *y, const float *x, const float *w, float *dx,
+                             float *dw, float *db, int rows, int in, int out, int acc_dx, int acc_dw, int acc_db);
 /* Linear followed by GELU (erf form, Ops.Nn.cs:86-112) in one launch: h = x w^T + b (the pre-activation GELU's
  * backward reads) and a = gelu(h), both [rows, out]. */
 om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *h, float *a, int rows,

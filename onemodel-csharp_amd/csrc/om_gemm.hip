@@ -1155,10 +1155,22 @@ __global__ void __launch_bounds__(64 * kMidW) k_linear_mid_fwd(const float *__re
 // dw[o][i] (+)= sum over r of g[r][o] x[r][i]: a wavefront per 16 x 16 block of dw, K = rows in blocks of 16 (MFMA
 // step s of block kb takes r = 16 kb + 4 kl + s: g[r][o0 + l16] as A, x[r][i0 + l16] as B), four blocks' loads in
 // flight at a time. The workgroups after the dw blocks' own give each thread a column o of g for db[o] (+)= the sum
-// over r of g[r][o] in double, in increasing r.
-__global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__ g, const float *__restrict__ x,
-                                                       float *__restrict__ dw, float *__restrict__ db, int rows,
-                                                       int in, int out, int nblk, int acc_dw, int acc_db) {
+// over r of g[r][o] in double, in increasing r. RELU: g[r][o] stands for the ReLU rule's y[r][o] > 0 ? g[r][o] : 0
+// (om_relu_bwd's arithmetic, y the ReLU's output [rows, out]) throughout; both loads are issued unconditionally and
+// the rule is a select, so no load waits on another.
+template <bool RELU>
+__global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__ g, const float *__restrict__ y,
+                                                       const float *__restrict__ x, float *__restrict__ dw,
+                                                       float *__restrict__ db, int rows, int in, int out, int nblk,
+                                                       int acc_dw, int acc_db) {
+    auto gv = [&](int64_t at) {
+        const float gg = g[at];
+        if constexpr (RELU) {
+            const float yy = y[at];
+            return yy > 0.0f ? gg : 0.0f;
+        }
+        return gg;
+    };
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
     const int dw_groups = (nblk + 3) / 4;
     if ((int)blockIdx.x >= dw_groups) {
@@ -1166,7 +1178,7 @@ __global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__
         if (o >= out) return;
         double s = 0.0;
 #pragma unroll 8
-        for (int r = 0; r < rows; r++) s += (double)g[(int64_t)r * out + o];
+        for (int r = 0; r < rows; r++) s += (double)gv((int64_t)r * out + o);
         const float v = (float)s;
         db[o] = acc_db ? db[o] + v : v;
         return;
@@ -1174,7 +1186,8 @@ __global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__
     const int blk = (int)blockIdx.x * 4 + wv;
     if (blk >= nblk) return;
     const int ti = in / 16, o0 = (blk / ti) * 16, i0 = (blk % ti) * 16;
-    const float *ga = g + (int64_t)4 * kl * out + o0 + l16, *xb = x + (int64_t)4 * kl * in + i0 + l16;
+    const int64_t ga = (int64_t)4 * kl * out + o0 + l16;
+    const float *xb = x + (int64_t)4 * kl * in + i0 + l16;
     constexpr int R = 4;
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
     const int nkb = rows / 16;
@@ -1185,7 +1198,7 @@ __global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__
             const int kb = min(kb0 + u, nkb - 1);  // clamped: such a block's loads are not used
 #pragma unroll
             for (int s = 0; s < 4; s++) {
-                av[u][s] = ga[(int64_t)(16 * kb + s) * out];
+                av[u][s] = gv(ga + (int64_t)(16 * kb + s) * out);
                 bv[u][s] = xb[(int64_t)(16 * kb + s) * in];
             }
         }
@@ -1330,8 +1343,8 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
     if (dw && linear_mid(rows, in, out)) {  // dW and db in one launch
         const int nblk = (out / 16) * (in / 16);
         const unsigned grid = (unsigned)((nblk + 3) / 4 + (db ? (out + 255) / 256 : 0));
-        hipLaunchKernelGGL(k_linear_mid_dw, dim3(grid), dim3(256), 0, om::cur_stream(ctx), g, x, dw, db, rows, in, out,
-                           nblk, acc_dw, acc_db);
+        hipLaunchKernelGGL(k_linear_mid_dw<false>, dim3(grid), dim3(256), 0, om::cur_stream(ctx), g, nullptr, x, dw, db,
+                           rows, in, out, nblk, acc_dw, acc_db);
         return OM_LAUNCH_CHECK(ctx, "om_linear_bwd dw");
     }
     bool db_done = false;
@@ -1344,6 +1357,27 @@ om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float
     }
     if (!s && db && !db_done) s = om_colsum(ctx, g, db, rows, out, acc_db);
     return s;
+}
+
+om_status om_linear_relu_bwd(om_ctx *ctx, const float *g, const float *y, const float *x, const float *w, float *dx,
+                             float *dw, float *db, int rows, int in, int out, int acc_dx, int acc_dw, int acc_db) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && y && rows >= 0 && in > 0 && out > 0, "om_linear_relu_bwd: bad arguments");
+    OM_REQUIRE(ctx, (!dx || w) && (!dw || x), "om_linear_relu_bwd: a needed saved tensor is NULL");
+    if (!dx && !dw && !db) return OM_OK;
+    if (!dx && dw && linear_mid(rows, in, out)) {  // the ReLU rule inside the dW and db launch
+        const int nblk = (out / 16) * (in / 16);
+        const unsigned grid = (unsigned)((nblk + 3) / 4 + (db ? (out + 255) / 256 : 0));
+        hipLaunchKernelGGL(k_linear_mid_dw<true>, dim3(grid), dim3(256), 0, om::cur_stream(ctx), g, y, x, dw, db, rows,
+                           in, out, nblk, acc_dw, acc_db);
+        return OM_LAUNCH_CHECK(ctx, "om_linear_relu_bwd");
+    }
+    // the ReLU rule into the second scratch slot (the products below may use the first), then Linear's backward
+    float *gp;
+    om_status s = om::scratch2(ctx, sizeof(float) * (uint64_t)rows * out, &gp);
+    if (s) return s;
+    s = om_relu_bwd(ctx, g, y, gp, (int64_t)rows * out, 0);
+    return s ? s : om_linear_bwd(ctx, gp, x, w, dx, dw, db, rows, in, out, acc_dx, acc_dw, acc_db);
 }
 
 om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,

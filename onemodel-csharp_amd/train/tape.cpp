@@ -376,6 +376,16 @@ Tensor linear_relu(const Tensor &x, const Tensor &w, const Tensor &b) {
         if (b) ins.push_back(b);
         float *yd = y->data;
         attach(y, "LinearRelu", ins, [rows, in, out, yd](Engine &e, Record &r, const float *g) {
+            if (!r.needs(0) && (in % 64 || out % 64) && !om_linear_small(rows, in, out)) {
+                // dW and db only, of a product no grouped launch takes (it would run now anyway): om_linear_relu_bwd,
+                // which applies the ReLU's rule as it reads g where the product is one launch
+                int aw, ab = 0;
+                float *dw = e.dest(r, 1, &aw);
+                float *db = r.inputs.size() > 2 ? e.dest(r, 2, &ab) : nullptr;
+                OMT(om_linear_relu_bwd(C(), g, yd, r.inputs[0]->data, r.inputs[1]->data, nullptr, dw, db, rows, in,
+                                       out, 0, aw, ab));
+                return;
+            }
             const int64_t n = (int64_t)rows * out;
             float *gp = dev().step_floats(n);
             OMT(om_relu_bwd(C(), g, yd, gp, n, 0));

@@ -138,6 +138,17 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     dev.call("om_linear_relu_fwd", X, W, Bb, YR, rows, inf, outf)
     dev.call("om_relu_fwd", Y, RR, rows * outf)
     assert np.array_equal(dev.get(YR).view(np.uint32), dev.get(RR).view(np.uint32))
+    # and its backward: the ReLU's rule then om_linear_bwd, bit for bit, with and without dx
+    GP = dev.empty((rows, outf))
+    dev.call("om_relu_bwd", G, YR, GP, rows * outf, 0)
+    for with_dx in (False, True):
+        outs1 = [dev.empty(x.shape) if with_dx else None, dev.empty(w.shape), dev.empty(b.shape)]
+        outs2 = [dev.empty(x.shape) if with_dx else None, dev.empty(w.shape), dev.empty(b.shape)]
+        dev.call("om_linear_bwd", GP, X, W, *outs1, rows, inf, outf, 0, 0, 0)
+        dev.call("om_linear_relu_bwd", G, YR, X, W, *outs2, rows, inf, outf, 0, 0, 0)
+        for o1, o2 in zip(outs1, outs2):
+            if o1 is not None:
+                assert np.array_equal(dev.get(o1).view(np.uint32), dev.get(o2).view(np.uint32)), with_dx
     assert scaled(dev.get(DX), dx_r) <= TOL
     assert scaled(dev.get(DW), dw_r) <= TOL
     assert scaled(dev.get(DB), db_r) <= 1e-7  # fp64 column sums: equal after rounding
