@@ -415,17 +415,31 @@ __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ 
         for (int tap = 0; tap < 9; tap++) acc[k][tap] = 0.0f;
     }
     const int np = rows * W;
-    for (int q = lane; q < np; q += 64) {
-        const int r = q / W, c = q - r * W;
-        float xv[9];
+    // Pixels q = lane, lane + 64, ... in that order; the g loads of U of them are issued before the first is used
+    // (clamped in range; a pixel past the band adds nothing).
+    constexpr int U = 4;
+    for (int q0 = lane; q0 < np; q0 += 64 * U) {
+        float gv[U][8];
 #pragma unroll
-        for (int tap = 0; tap < 9; tap++) xv[tap] = xs[(r + tap / 3) * xw + c + tap % 3];
+        for (int u = 0; u < U; u++) {
+            const int q = min(q0 + 64 * u, np - 1);
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const float gv = gn[k * P + q];
-            dsum[k] += (double)gv;
+            for (int k = 0; k < 8; k++) gv[u][k] = gn[k * P + q];
+        }
 #pragma unroll
-            for (int tap = 0; tap < 9; tap++) acc[k][tap] = acc[k][tap] + gv * xv[tap];
+        for (int u = 0; u < U; u++) {
+            const int q = q0 + 64 * u;
+            if (q >= np) break;
+            const int r = q / W, c = q - r * W;
+            float xv[9];
+#pragma unroll
+            for (int tap = 0; tap < 9; tap++) xv[tap] = xs[(r + tap / 3) * xw + c + tap % 3];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                dsum[k] += (double)gv[u][k];
+#pragma unroll
+                for (int tap = 0; tap < 9; tap++) acc[k][tap] = acc[k][tap] + gv[u][k] * xv[tap];
+            }
         }
     }
     if (dbp) {
