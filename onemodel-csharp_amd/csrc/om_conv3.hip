@@ -449,15 +449,30 @@ __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ 
             if (lane == 0) dbp[(int64_t)blockIdx.x * cout + co0 + k] = v;
         }
     }
+    // The 72 sums acc[k][tap] over the wavefront's lanes by halving: at lane bit 5, 4 and 3 in turn a lane keeps the
+    // half of its values its bit selects, adds the partner's copy of that half and hands the partner the other half;
+    // the last 9 (one channel's taps) are summed over the remaining 8 lanes by a butterfly. Lane 8 j then holds the
+    // nine tap sums of channel co0 + j.
+    float v1[36], v2[18], v3[9];
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
 #pragma unroll
-    for (int k = 0; k < 8; k++)
+    for (int i = 0; i < 36; i++) {
+        const float lo = acc[i / 9][i % 9], hi = acc[(36 + i) / 9][(36 + i) % 9];
+        v1[i] = (b5 ? hi : lo) + __shfl_xor(b5 ? lo : hi, 32, 64);
+    }
 #pragma unroll
-        for (int tap = 0; tap < 9; tap++) {
-            float v = acc[k][tap];
+    for (int i = 0; i < 18; i++) v2[i] = (b4 ? v1[18 + i] : v1[i]) + __shfl_xor(b4 ? v1[i] : v1[18 + i], 16, 64);
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-            if (lane == 0) part[((int64_t)blockIdx.x * cout + co0 + k) * 9 + tap] = v;
-        }
+    for (int i = 0; i < 9; i++) {
+        v3[i] = (b3 ? v2[9 + i] : v2[i]) + __shfl_xor(b3 ? v2[i] : v2[9 + i], 8, 64);
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) v3[i] += __shfl_xor(v3[i], o, 64);
+    }
+    if ((lane & 7) == 0) {
+        const int k = lane >> 3;  // 4 b5 + 2 b4 + b3
+#pragma unroll
+        for (int tap = 0; tap < 9; tap++) part[((int64_t)blockIdx.x * cout + co0 + k) * 9 + tap] = v3[tap];
+    }
 }
 
 // Rows of the staged input a run of `px` flattened output pixels can touch, halo included, and the LDS plane stride
