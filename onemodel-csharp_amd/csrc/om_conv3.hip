@@ -475,6 +475,53 @@ __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ 
     }
 }
 
+// Forward of a 3x3 / stride 1 / padding 1 convolution with one input channel (a CRNN's first layer over a grayscale
+// image): y[n][co][p] = (sum over taps t of w[co][t] x[n][p + shift(t)], an fmaf chain in tap order) + bias[co], then
+// the ReLU when asked. A workgroup takes one image's band of br rows: the band's input with its halo and all weights
+// and biases are staged in LDS, each thread keeps one pixel's nine neighbours in registers and walks the output
+// channels four at a time (broadcast LDS reads of their weights), and consecutive threads store consecutive pixels
+// of a channel.
+constexpr int kC1MaxCout = 128;
+__global__ void __launch_bounds__(256) k_conv3_fwd_c1(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ bias, float *__restrict__ y, int cout,
+                                                      int H, int W, int br, int nbands, int relu) {
+    extern __shared__ float xs[];  // [br + 2][W + 2]
+    __shared__ float ws[kC1MaxCout * 9], bs[kC1MaxCout];
+    const int n = blockIdx.x / nbands, y0 = (blockIdx.x % nbands) * br, rows = min(br, H - y0), xw = W + 2;
+    for (int f = threadIdx.x; f < cout * 9; f += blockDim.x) ws[f] = w[f];
+    for (int f = threadIdx.x; f < cout; f += blockDim.x) bs[f] = bias ? bias[f] : 0.0f;
+    for (int f = threadIdx.x; f < (br + 2) * xw; f += blockDim.x) {
+        const int r = f / xw, c = f - r * xw, iy = y0 - 1 + r, ix = c - 1;
+        xs[f] = (r < rows + 2 && (unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W)
+                    ? x[((int64_t)n * H + iy) * W + ix]
+                    : 0.0f;
+    }
+    __syncthreads();
+    const int64_t P = (int64_t)H * W;
+    const int np = rows * W;
+    for (int q = threadIdx.x; q < np; q += blockDim.x) {
+        const int r = q / W, c = q - r * W;
+        float xv[9];
+#pragma unroll
+        for (int tap = 0; tap < 9; tap++) xv[tap] = xs[(r + tap / 3) * xw + c + tap % 3];
+        float *yp = y + (int64_t)n * cout * P + (int64_t)y0 * W + q;
+        auto one = [&](int co) {
+            float v = 0.0f;
+#pragma unroll
+            for (int tap = 0; tap < 9; tap++) v = __builtin_fmaf(ws[co * 9 + tap], xv[tap], v);
+            if (bias) v = v + bs[co];
+            if (relu) v = v > 0.0f ? v : (v == v ? 0.0f : v);
+            yp[co * P] = v;
+        };
+        int co = 0;
+        for (; co + 4 <= cout; co += 4) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) one(co + u);
+        }
+        for (; co < cout; co++) one(co);
+    }
+}
+
 // Rows of the staged input a run of `px` flattened output pixels can touch, halo included, and the LDS plane stride
 // (rows of W + 8 floats, padded so that 2 * ps is 16 mod 64 floats: lanes of the four k groups read different banks).
 void stage_geometry(int W, int px, int &R, int &ps) {
@@ -497,6 +544,20 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
                   int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu) {
     *st = OM_OK;
     const int P = H * W;
+    if (Cin == 1 && !flip_weights && !acc && Cout <= kC1MaxCout && (int64_t)N * Cout * P <= INT32_MAX &&
+        (int64_t)(W + 2) * 4 * 3 <= 65536) {
+        // bands of rows, about four workgroups per CU over the images, each band's input under 64 KB of LDS
+        const int want = (int)((4LL * ctx->num_cus + N - 1) / N);
+        int nb = want < H ? want : H;
+        int br = (H + nb - 1) / nb;
+        while (br > 1 && (int64_t)(br + 2) * (W + 2) * 4 > 65536) br = (br + 1) / 2;
+        nb = (H + br - 1) / br;
+        const size_t lds = sizeof(float) * (size_t)(br + 2) * (W + 2);
+        hipLaunchKernelGGL(k_conv3_fwd_c1, dim3((unsigned)(N * nb)), dim3(256), lds, ctx->stream, x, w, bias, y, Cout, H,
+                           W, br, nb, relu ? 1 : 0);
+        *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_fwd");
+        return true;
+    }
     if (Cin % kFwdCk || Cout % 32 || W % 4 || (int64_t)N * Cin * P > INT32_MAX || (int64_t)N * Cout * P > INT32_MAX ||
         (int64_t)Cout * 9 * Cin > INT32_MAX)
         return false;
