@@ -399,6 +399,13 @@ om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float
  * geometries run the two launches): y bit for bit om_conv2d_fwd then om_relu_fwd. No counterpart as one call. */
 om_status om_conv2d_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N,
                              int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad);
+/* A conv stage's forward (Ops.Conv2d, Ops.Relu, then Ops.MaxPool2d with no padding): a = relu(conv(x) + b) as
+ * om_conv2d_relu_fwd writes it, then y and idx as om_maxpool_fwd(a, ..., pkh, pkw, psh, psw, 0, 0) writes them, bit for
+ * bit. Where the convolution sums input-channel splits in a pass of its own and the windows tile a exactly (stride
+ * equal to the window), that pass also pools. No counterpart as one call. idx may be NULL. */
+om_status om_conv2d_relu_pool_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *a, float *y,
+                                  int32_t *idx, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride,
+                                  int pad, int pkh, int pkw, int psh, int psw);
 om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
                         int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride, int pad, int acc_dx,
                         int acc_params);

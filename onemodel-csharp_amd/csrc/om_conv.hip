@@ -11,9 +11,12 @@
 
 #include <cstdlib>
 
-// 3x3, stride 1, padding 1 kernels (om_conv3.hip); each returns false when the shape is not one it takes.
+// 3x3, stride 1, padding 1 kernels (om_conv3.hip); each returns false when the shape is not one it takes. With
+// `pool` (a ReLU stage whose max pool windows tile the output exactly), a forward that sums input-channel splits in
+// a pass of its own pools in that pass and sets *pooled.
 bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin, int H,
-                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu);
+                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu, const Conv3Pool *pool = nullptr,
+                  bool *pooled = nullptr);
 bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *db, int N, int Cin, int H, int W,
                  int Cout, int acc, om_status *st);
 
@@ -478,6 +481,30 @@ om_status om_conv2d_fwd(om_ctx *ctx, const float *x, const float *w, const float
 om_status om_conv2d_relu_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin,
                              int H, int W, int Cout, int KH, int KW, int stride, int pad) {
     return conv_fwd(ctx, "om_conv2d_relu_fwd", x, w, bias, y, N, Cin, H, W, Cout, KH, KW, stride, pad, true);
+}
+
+om_status om_conv2d_relu_pool_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *a, float *y,
+                                  int32_t *idx, int N, int Cin, int H, int W, int Cout, int KH, int KW, int stride,
+                                  int pad, int pkh, int pkw, int psh, int psw) {
+    OM_CHECK_CTX(ctx);
+    int OH, OW;
+    om_status s = conv_check(ctx, "om_conv2d_relu_pool_fwd", N, Cin, H, W, Cout, KH, KW, stride, pad, OH, OW);
+    if (s) return s;
+    OM_REQUIRE(ctx, x && w && a && y, "om_conv2d_relu_pool_fwd: NULL pointer");
+    OM_REQUIRE(ctx, pkh > 0 && pkw > 0 && psh > 0 && psw > 0 && pkh <= OH && pkw <= OW,
+               "om_conv2d_relu_pool_fwd: bad pooling window %dx%d / %dx%d over %dx%d", pkh, pkw, psh, psw, OH, OW);
+    OM_REQUIRE(ctx, (int64_t)N * Cout * OH * OW <= INT32_MAX, "om_conv2d_relu_pool_fwd: Int32 indices cannot address "
+                                                              "the convolution's output");
+    if (conv3_geometry(KH, KW, stride, pad) && psh == pkh && psw == pkw && OH % pkh == 0 && OW % pkw == 0) {
+        const Conv3Pool pool{y, idx, pkh, pkw};
+        bool pooled = false;
+        if (om_conv3_fwd(ctx, x, w, bias, a, N, Cin, H, W, Cout, 0, &s, false, true, &pool, &pooled)) {
+            if (s || pooled) return s;
+            return om_maxpool_fwd(ctx, a, y, idx, N, Cout, OH, OW, pkh, pkw, psh, psw, 0, 0);
+        }
+    }
+    s = om_conv2d_relu_fwd(ctx, x, w, bias, a, N, Cin, H, W, Cout, KH, KW, stride, pad);
+    return s ? s : om_maxpool_fwd(ctx, a, y, idx, N, Cout, OH, OW, pkh, pkw, psh, psw, 0, 0);
 }
 
 om_status om_conv2d_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,

@@ -243,6 +243,42 @@ __global__ void k_conv3_sum(const float *__restrict__ ws, int nsplit, int64_t to
     }
 }
 
+// k_conv3_sum for a ReLU stage followed by a max pool whose kh x kw windows (stride kh, kw) tile the output exactly:
+// a thread per pooled output adds the partials of each window element in split order, adds the bias and applies the
+// ReLU (k_conv3_sum's arithmetic), stores the element, and pools the window as k_maxpool_fwd does ((ky, kx) order;
+// the first candidate, a strictly larger value unless the best is NaN, or the first NaN wins; idx the element's flat
+// index).
+__global__ void k_conv3_sum_pool(const float *__restrict__ ws, int nsplit, int64_t total, int H, int W, int cout,
+                                 const float *__restrict__ bias, float *__restrict__ out, float *__restrict__ py,
+                                 int32_t *__restrict__ pidx, int kh, int kw, int64_t pooled) {
+    const int OH = H / kh, OW = W / kw;
+    for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < pooled; o += (int64_t)gridDim.x * blockDim.x) {
+        const int ox = (int)(o % OW);
+        const int64_t t = o / OW;
+        const int oy = (int)(t % OH);
+        const int64_t nc = t / OH;
+        const float bv = bias ? bias[nc % cout] : 0.0f;
+        float best = -__int_as_float(0x7F800000);
+        int bi = -1;
+        for (int ky = 0; ky < kh; ky++)
+            for (int kx = 0; kx < kw; kx++) {
+                const int64_t e = (nc * H + oy * kh + ky) * W + ox * kw + kx;
+                float v = ws[e];
+                for (int sp = 1; sp < nsplit; sp++) v += ws[(int64_t)sp * total + e];
+                if (bias) v = v + bv;
+                v = relu1(v);
+                out[e] = v;
+                const bool wins = bi < 0 || (v > best && best == best) || (v != v && best == best);
+                if (wins) {
+                    best = v;
+                    bi = (int)e;
+                }
+            }
+        py[o] = best;
+        if (pidx) pidx[o] = bi;
+    }
+}
+
 // part[slot][co][tap][ci] = the slot's items' sums of g[n][co][p] x[n][ci][p + shift(tap)]. The next item's g
 // block and input rows are loaded into registers while the current one computes. With dbp, the workgroups of the
 // first input-channel block also sum the staged g block per output channel in double (the bias gradient's partial of
@@ -541,7 +577,9 @@ int stage_ns(int chans, int W, int R) {
 
 // The 3x3 / stride 1 / padding 1 paths; each returns false (launching nothing) when the shape is not one it takes.
 bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias, float *y, int N, int Cin, int H,
-                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu) {
+                  int W, int Cout, int acc, om_status *st, bool flip_weights, bool relu, const Conv3Pool *pool,
+                  bool *pooled) {
+    if (pooled) *pooled = false;
     *st = OM_OK;
     const int P = H * W;
     if (Cin == 1 && !flip_weights && !acc && Cout <= kC1MaxCout && (int64_t)N * Cout * P <= INT32_MAX &&
@@ -601,9 +639,15 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
     OMC3(64, 1) OMC3(64, 2) OMC3(64, 3) OMC3(64, 4) OMC3(64, 6) OMC3(64, 8)
     OMC3(32, 1) OMC3(32, 2) OMC3(32, 3) OMC3(32, 4) OMC3(32, 6) OMC3(32, 8)
 #undef OMC3
-    if (nsplit > 1)
+    if (nsplit > 1 && pool && relu && !acc && pooled) {  // the sum, the ReLU and the max pool in one pass
+        const int64_t npool = (int64_t)N * Cout * (H / pool->kh) * (W / pool->kw);
+        hipLaunchKernelGGL(k_conv3_sum_pool, dim3(om::grid1d(npool, 256, 4096)), dim3(256), 0, ctx->stream, ws, nsplit,
+                           total, H, W, Cout, bias, y, pool->y, pool->idx, pool->kh, pool->kw, npool);
+        *pooled = true;
+    } else if (nsplit > 1) {
         hipLaunchKernelGGL(k_conv3_sum, dim3(om::grid1d(total, 256, 4096)), dim3(256), 0, ctx->stream, ws, nsplit,
                            total, P, Cout, bias, y, acc, relu ? 1 : 0);
+    }
     *st = OM_LAUNCH_CHECK(ctx, flip_weights ? "om_conv2d_bwd dx" : "om_conv2d_fwd");
     return true;
 }

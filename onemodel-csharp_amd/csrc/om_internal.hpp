@@ -26,6 +26,14 @@ struct om_region {
     uint64_t default_slab = 0;
 };
 
+// A max pool that a 3x3 convolution's split-sum pass can do in the same pass: kh x kw windows, stride kh, kw, no
+// padding, tiling the convolution's output exactly; y and idx as om_maxpool_fwd's.
+struct Conv3Pool {
+    float *y;
+    int32_t *idx;
+    int kh, kw;
+};
+
 struct om_ctx {
     int device = 0;
     hipStream_t stream = nullptr;

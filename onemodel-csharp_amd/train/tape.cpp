@@ -857,12 +857,11 @@ Tensor conv2d_relu_pool(const Tensor &x, const Tensor &w, const Tensor &b, int s
     const int PH = (c.OH - kh) / sh + 1, PW = (c.OW - kw) / sw + 1;
     if (PH < 1 || PW < 1) shape_error("MaxPool2d: window larger than the input");
     Tensor a = make({c.N, c.Cout, c.OH, c.OW});  // Relu(Conv2d(x))
-    OMT(om_conv2d_relu_fwd(C(), x->data, w->data, b ? b->data : nullptr, a->data, c.N, c.Cin, c.H, c.W, c.Cout, c.KH,
-                           c.KW, stride, pad));
     Tensor y = make({c.N, c.Cout, PH, PW});
     const bool rec = tracked({&x, &w, &b});
     int32_t *idx = rec ? dev().step_ints((int64_t)c.N * c.Cout * PH * PW) : nullptr;
-    OMT(om_maxpool_fwd(C(), a->data, y->data, idx, c.N, c.Cout, c.OH, c.OW, kh, kw, sh, sw, 0, 0));
+    OMT(om_conv2d_relu_pool_fwd(C(), x->data, w->data, b ? b->data : nullptr, a->data, y->data, idx, c.N, c.Cin, c.H,
+                                c.W, c.Cout, c.KH, c.KW, stride, pad, kh, kw, sh, sw));
     if (rec) {
         std::vector<Tensor> ins{x, w};
         if (b) ins.push_back(b);

@@ -714,6 +714,19 @@ def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     dev.call("om_conv2d_relu_fwd", X, Wd, Bd, YR, N, Cin, H, W, Cout, K, K, S, P)
     dev.call("om_relu_fwd", Y, YR2, y.size)
     assert np.array_equal(dev.get(YR).view(np.uint32), dev.get(YR2).view(np.uint32))
+    # a conv stage in one call (the ReLU's zeros make ties in most windows): a, the pooled values and their indices
+    # equal om_conv2d_relu_fwd then om_maxpool_fwd, for windows that tile the output and ones that do not
+    for (kh, kw), (sh, sw) in (((2, 2), (2, 2)), ((2, 1), (2, 1)), ((3, 3), (2, 2))):
+        if kh > OH or kw > OW:
+            continue
+        PH, PW = (OH - kh) // sh + 1, (OW - kw) // sw + 1
+        A1, P1, I1 = dev.empty(y.shape), dev.empty((N, Cout, PH, PW)), dev.empty((N, Cout, PH, PW), np.int32)
+        P2, I2 = dev.empty((N, Cout, PH, PW)), dev.empty((N, Cout, PH, PW), np.int32)
+        dev.call("om_conv2d_relu_pool_fwd", X, Wd, Bd, A1, P1, I1, N, Cin, H, W, Cout, K, K, S, P, kh, kw, sh, sw)
+        dev.call("om_maxpool_fwd", YR, P2, I2, N, Cout, OH, OW, kh, kw, sh, sw, 0, 0)
+        assert np.array_equal(dev.get(A1).view(np.uint32), dev.get(YR).view(np.uint32)), (kh, kw)
+        assert np.array_equal(dev.get(P1).view(np.uint32), dev.get(P2).view(np.uint32)), (kh, kw)
+        assert np.array_equal(dev.get(I1), dev.get(I2)), (kh, kw)
     # accumulating into the existing gradients, and the same bits on a second run
     first = [dev.get(t).copy() for t in (DX, DW, DB)]
     dev.call("om_conv2d_bwd", G, X, Wd, DX, DW, DB, N, Cin, H, W, Cout, K, K, S, P, 1, 1)
