@@ -333,8 +333,10 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
         for (int k = 0; k < NG; k++) *reinterpret_cast<floatx4 *>(Gs + gco[k] * kGLd + gpx[k]) = gv[k];
         xs.store(Xs);
         if (threadIdx.x < kDwPx) {
-            const int p = p0 + threadIdx.x;
-            boff[threadIdx.x] = p < P ? (p / W - oy0) * rs + p % W + 3 : 0;
+            // a pixel past the image (the last chunk's tail) reads the last pixel's staged, finite neighbours: its g
+            // is zero, and zero times a finite value adds nothing (LDS that nothing wrote may hold a NaN)
+            const int p = min(p0 + (int)threadIdx.x, P - 1);
+            boff[threadIdx.x] = (p / W - oy0) * rs + p % W + 3;
         }
         __syncthreads();
         if (item + 1 < i1) load(item + 1);  // in flight while this item computes
@@ -558,6 +560,62 @@ __global__ void __launch_bounds__(256) k_conv3_fwd_c1(const float *__restrict__ 
     }
 }
 
+// k_conv3_fwd_c1 with the ReLU, followed by a max pool whose KH x KW windows (stride KH, KW) tile the output: a
+// workgroup per pooled row of an image (its KH + 2 input rows staged in LDS), a thread per window and every fourth
+// channel. Each window element is k_conv3_fwd_c1's chain, bias and ReLU, stored; the window is pooled as
+// k_maxpool_fwd does ((ky, kx) order; the first candidate, a strictly larger value unless the best is NaN, or the
+// first NaN wins; idx the element's flat index).
+template <int KH, int KW>
+__global__ void __launch_bounds__(256) k_conv3_fwd_c1_pool(const float *__restrict__ x, const float *__restrict__ w,
+                                                           const float *__restrict__ bias, float *__restrict__ a,
+                                                           float *__restrict__ py, int32_t *__restrict__ pidx,
+                                                           int cout, int H, int W) {
+    extern __shared__ float xs[];  // [KH + 2][W + 2]
+    __shared__ float ws[kC1MaxCout * 9], bs[kC1MaxCout];
+    const int OH2 = H / KH, OW2 = W / KW, xw = W + 2;
+    const int n = blockIdx.x / OH2, oy = blockIdx.x % OH2, y0 = oy * KH;
+    for (int f = threadIdx.x; f < cout * 9; f += blockDim.x) ws[f] = w[f];
+    for (int f = threadIdx.x; f < cout; f += blockDim.x) bs[f] = bias ? bias[f] : 0.0f;
+    for (int f = threadIdx.x; f < (KH + 2) * xw; f += blockDim.x) {
+        const int r = f / xw, c = f - r * xw, iy = y0 - 1 + r, ix = c - 1;
+        xs[f] = ((unsigned)iy < (unsigned)H && (unsigned)ix < (unsigned)W) ? x[((int64_t)n * H + iy) * W + ix] : 0.0f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t P2 = (int64_t)OH2 * OW2;
+    for (int ox = lane; ox < OW2; ox += 64) {
+        float xv[KH + 2][KW + 2];  // the window's input patch, halo included
+#pragma unroll
+        for (int r = 0; r < KH + 2; r++)
+#pragma unroll
+            for (int c = 0; c < KW + 2; c++) xv[r][c] = xs[r * xw + ox * KW + c];
+        for (int co = wv; co < cout; co += 4) {
+            float best = -__int_as_float(0x7F800000);
+            int bi = -1;
+#pragma unroll
+            for (int ky = 0; ky < KH; ky++)
+#pragma unroll
+                for (int kx = 0; kx < KW; kx++) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int tap = 0; tap < 9; tap++) v = __builtin_fmaf(ws[co * 9 + tap], xv[ky + tap / 3][kx + tap % 3], v);
+                    if (bias) v = v + bs[co];
+                    v = v > 0.0f ? v : (v == v ? 0.0f : v);
+                    const int64_t e = (((int64_t)n * cout + co) * H + y0 + ky) * W + ox * KW + kx;
+                    a[e] = v;
+                    const bool wins = bi < 0 || (v > best && best == best) || (v != v && best == best);
+                    if (wins) {
+                        best = v;
+                        bi = (int)e;
+                    }
+                }
+            const int64_t o = ((int64_t)n * cout + co) * P2 + (int64_t)oy * OW2 + ox;
+            py[o] = best;
+            if (pidx) pidx[o] = bi;
+        }
+    }
+}
+
 // Rows of the staged input a run of `px` flattened output pixels can touch, halo included, and the LDS plane stride
 // (rows of W + 8 floats, padded so that 2 * ps is 16 mod 64 floats: lanes of the four k groups read different banks).
 void stage_geometry(int W, int px, int &R, int &ps) {
@@ -582,6 +640,21 @@ bool om_conv3_fwd(om_ctx *ctx, const float *x, const float *w, const float *bias
     if (pooled) *pooled = false;
     *st = OM_OK;
     const int P = H * W;
+    if (Cin == 1 && !flip_weights && !acc && Cout <= kC1MaxCout && (int64_t)N * Cout * P <= INT32_MAX && pool &&
+        relu && pooled && pool->kh == 2 && (pool->kw == 2 || pool->kw == 1) && H % 2 == 0 && W % pool->kw == 0 &&
+        (int64_t)(W + 2) * 4 * 4 <= 65536) {  // the stage's convolution, ReLU and max pool in one launch
+        const size_t lds = sizeof(float) * 4 * (size_t)(W + 2);
+        const dim3 grid((unsigned)(N * (H / 2)));
+        if (pool->kw == 2)
+            hipLaunchKernelGGL((k_conv3_fwd_c1_pool<2, 2>), grid, dim3(256), lds, ctx->stream, x, w, bias, y, pool->y,
+                               pool->idx, Cout, H, W);
+        else
+            hipLaunchKernelGGL((k_conv3_fwd_c1_pool<2, 1>), grid, dim3(256), lds, ctx->stream, x, w, bias, y, pool->y,
+                               pool->idx, Cout, H, W);
+        *pooled = true;
+        *st = OM_LAUNCH_CHECK(ctx, "om_conv2d_relu_pool_fwd");
+        return true;
+    }
     if (Cin == 1 && !flip_weights && !acc && Cout <= kC1MaxCout && (int64_t)N * Cout * P <= INT32_MAX &&
         (int64_t)(W + 2) * 4 * 3 <= 65536) {
         // bands of rows, about four workgroups per CU over the images, each band's input under 64 KB of LDS

@@ -691,7 +691,8 @@ def test_attention_bwd_kernels_agree(dev, L, masked):
                                                   (3, 16, 7, 12, 32, 3, 1, 1), (2, 32, 9, 20, 64, 3, 1, 1),
                                                   (2, 48, 5, 36, 96, 3, 1, 1),
                                                   # one input channel at odd sizes and a ragged last band
-                                                  (3, 1, 7, 9, 5, 3, 1, 1), (2, 1, 33, 20, 16, 3, 1, 1)])
+                                                  (3, 1, 7, 9, 5, 3, 1, 1), (2, 1, 33, 20, 16, 3, 1, 1),
+                                                  (2, 1, 6, 130, 9, 3, 1, 1)])
 def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
     rng = np.random.default_rng(N * Cin + Cout)
     x, w, b = rnd(rng, N, Cin, H, W), rnd(rng, Cout, Cin, K, K, scale=0.2), rnd(rng, Cout)
