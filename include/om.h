@@ -167,6 +167,11 @@ int om_linear_small(int rows, int in, int out);
  * destination instead of overwriting it (leaf accumulation). */
 om_status om_linear_bwd(om_ctx *ctx, const float *g, const float *x, const float *w, float *dx, float *dw, float *db,
                         int rows, int in, int out, int acc_dx, int acc_dw, int acc_db);
+/* Linear's input gradient plus a residual's gradient arriving at the same tensor (a post-LN block's sub-layer input,
+ * which is also its residual): dx = (g w) + r, the bits of om_linear_bwd's dx followed by om_axpy(1, r, dx), with the
+ * add in the product's epilogue. No counterpart as one call. */
+om_status om_linear_bwd_dx_resid(om_ctx *ctx, const float *g, const float *w, const float *r, float *dx, int rows,
+                                 int in, int out);
 /* Linear followed by the residual Add of an encoder block (Ops.Layers.cs:715-733, then Ops.Add, Ops.cs:15-56):
  * y = resid + (x w^T + b), in that rounding order, in one launch. */
 om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,

@@ -1443,6 +1443,20 @@ om_status om_linear_bwd_dw_group(om_ctx *ctx, int count, const om_linear_dw *ite
     return om_param_grads_group(ctx, count, items, rows, 0, nullptr);
 }
 
+om_status om_linear_bwd_dx_resid(om_ctx *ctx, const float *g, const float *w, const float *r, float *dx, int rows,
+                                 int in, int out) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && w && r && dx && rows >= 0 && in > 0 && out > 0, "om_linear_bwd_dx_resid: bad arguments");
+    if (linear_small(rows, in, out) || linear_narrow(rows, in, out)) {  // their own dx kernels, then the add
+        om_status s = om_linear_bwd(ctx, g, nullptr, w, dx, nullptr, nullptr, rows, in, out, 0, 0, 0);
+        return s ? s : om_axpy(ctx, 1.0f, r, dx, (int64_t)rows * in);
+    }
+    omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dx, in);
+    p.resid = r;  // the engine's epilogue: fl(fl(g w) + r), the bits of the product stored and then added
+    p.ldr = in;
+    return omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd_dx_resid");
+}
+
 om_status om_linear_bwd_dx_slope(om_ctx *ctx, const float *g, const float *w, const float *s, float *dh, int rows,
                                  int in, int out) {
     OM_CHECK_CTX(ctx);

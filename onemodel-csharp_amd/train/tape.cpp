@@ -560,6 +560,7 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
             int n = 0;
             if (dw2 || db2) items[n++] = om_linear_dw{g, a, dw2, db2, f, o, aw2, ab2};
             const bool below = r.needs(0) || r.needs(1) || r.needs(2);
+            bool folded = false;
             if (below) {
                 float *dh = dev().step_floats((int64_t)rows * f);
                 OMT(om_linear_bwd_dx_slope(C(), g, r.inputs[3]->data, sl, dh, rows, f, o));
@@ -567,13 +568,18 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
                 float *dx = e.dest(r, 0, &ax);
                 float *dw1 = e.dest(r, 1, &aw1);
                 float *db1 = r.inputs[2] ? e.dest(r, 2, &ab1) : nullptr;
-                if (dx)
+                // the input is also the residual (a post-LN block) and its gradient starts here: the residual's
+                // gradient g goes into the product's epilogue instead of a later add (the same bits)
+                folded = dx && !ax && r.needs(5) && r.inputs[5].get() == r.inputs[0].get();
+                if (folded)
+                    OMT(om_linear_bwd_dx_resid(C(), dh, r.inputs[1]->data, g, dx, rows, d, f));
+                else if (dx)
                     OMT(om_linear_bwd(C(), dh, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr, rows, d, f,
                                       ax, 0, 0));
                 if (dw1 || db1) items[n++] = om_linear_dw{dh, r.inputs[0]->data, dw1, db1, d, f, aw1, ab1};
             }
             for (int i = 0; i < n; i++) e.queue_dw(items[i], rows);
-            if (r.needs(5)) e.emit_alias(r, 5, g);
+            if (r.needs(5) && !folded) e.emit_alias(r, 5, g);
         }, {x, w1, w2});
     }
     return y;

@@ -138,6 +138,13 @@ def test_linear_fwd_bwd(dev, T, rows, inf, outf):
     dev.call("om_linear_relu_fwd", X, W, Bb, YR, rows, inf, outf)
     dev.call("om_relu_fwd", Y, RR, rows * outf)
     assert np.array_equal(dev.get(YR).view(np.uint32), dev.get(RR).view(np.uint32))
+    # the input gradient with a residual's gradient added in the epilogue: om_linear_bwd's dx then om_axpy, bit for bit
+    RG = dev.put(rnd(rng, rows, inf))
+    DXR, DX1 = dev.empty(x.shape), dev.empty(x.shape)
+    dev.call("om_linear_bwd_dx_resid", G, W, RG, DXR, rows, inf, outf)
+    dev.call("om_linear_bwd", G, X, W, DX1, None, None, rows, inf, outf, 0, 0, 0)
+    dev.call("om_axpy", C.c_float(1.0), RG, DX1, rows * inf)
+    assert np.array_equal(dev.get(DXR).view(np.uint32), dev.get(DX1).view(np.uint32))
     # and its backward: the ReLU's rule then om_linear_bwd, bit for bit, with and without dx
     GP = dev.empty((rows, outf))
     dev.call("om_relu_bwd", G, YR, GP, rows * outf, 0)
