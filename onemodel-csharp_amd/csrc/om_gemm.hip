@@ -794,7 +794,7 @@ void launch_small_fwd(hipStream_t st, const float *x, const float *w, const floa
 // order). Every lane of a workgroup reads the same g[r][o] at the same time: uniform addresses of read-only memory,
 // which the compiler turns into scalar loads (no LDS staging, no barrier). OUT is the layer's output count, a
 // compile-time constant so the loops over it unroll.
-constexpr int kSmallDxRows = 16, kSmallRc = 32;
+constexpr int kSmallDxRows = 8, kSmallRc = 32;
 // dx[r][i] (+)= sum over o of g[r][o] w[o][i] for rows r0 .. r0 + kSmallDxRows - 1, column i: an fmaf chain over o in
 // increasing order per row (OUT = the layer's output count).
 template <int OUT>
