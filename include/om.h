@@ -235,6 +235,11 @@ om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, 
 
 /* ---------------------------------------------------------------------------------------------- elementwise */
 /* ReluUn / ReluGradBin (TrainElementwise.cs:41-45, 93-98; Ops.cs:94-107; BackwardOps.cs:66-68). */
+/* The CRNN's sequence head (Mean over axis 2 of x [B, C, H, W], then Permute(2, 0, 1)): y [W, B, C] bit for bit
+ * om_mean_axis then om_permute, in one launch; the backward dx [B, C, H, W] (+)= g[w][b][c] / H, the bits of the
+ * permute's and the mean's backward in turn. No counterpart as one call. */
+om_status om_mean_permute_fwd(om_ctx *ctx, const float *x, float *y, int B, int C, int H, int W);
+om_status om_mean_permute_bwd(om_ctx *ctx, const float *g, float *dx, int B, int C, int H, int W, int accumulate);
 om_status om_relu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n);
 om_status om_relu_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int64_t n, int accumulate);
 /* Ops.Gelu erf form and GeluGradBin (Ops.Nn.cs:86-112; TrainElementwise.cs:59-85; Transcendental.cs:167-263). */

@@ -49,6 +49,8 @@ _OM_SIGS = {
     "om_linear_fwd_resid": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_relu_fwd": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd_dx_resid": [vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_mean_permute_fwd": [vp, vp, vp, ci, ci, ci, ci],
+    "om_mean_permute_bwd": [vp, vp, vp, ci, ci, ci, ci, ci],
     "om_conv2d_relu_pool_fwd": [vp, vp, vp, vp, vp, vp, vp] + [ci] * 13,
     "om_linear_relu_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci],
     "om_linear_gelu_fwd": [vp, vp, vp, vp, vp, vp, ci, ci, ci],

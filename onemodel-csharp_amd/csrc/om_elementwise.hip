@@ -251,6 +251,30 @@ __global__ void __launch_bounds__(kBlock) k_mean_inner(const float *__restrict__
     for (int k = 0; k < n; k++) acc += (double)x[((int64_t)o * n + k) * inner + i];
     y[t] = (float)(acc / n);
 }
+// The CRNN's sequence head: the mean over H of x [B, C, H, W] (k_mean_inner's arithmetic) written as y [W, B, C]
+// (Permute(2, 0, 1) of the mean), and its backward: dx[b][c][h][w] (+)= g[w][b][c] / H (k_mean_axis_bwd's).
+__global__ void __launch_bounds__(kBlock) k_mean_permute_fwd(const float *__restrict__ x, float *__restrict__ y, int B,
+                                                             int Cc, int H, int W) {
+    const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (t >= (int64_t)B * Cc * W) return;
+    const int c = (int)(t % Cc), b = (int)((t / Cc) % B), w = (int)(t / ((int64_t)Cc * B));
+    const float *xp = x + ((int64_t)b * Cc + c) * H * W + w;
+    double acc = 0.0;
+    for (int k = 0; k < H; k++) acc += (double)xp[(int64_t)k * W];
+    y[t] = (float)(acc / H);
+}
+__global__ void __launch_bounds__(kBlock) k_mean_permute_bwd(const float *__restrict__ g, float *__restrict__ dx, int B,
+                                                             int Cc, int H, int W, int acc) {
+    const int64_t total = (int64_t)B * Cc * H * W, stride = (int64_t)gridDim.x * kBlock;
+    const float fn = (float)H;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
+        const int w = (int)(t % W);
+        const int64_t bc = t / ((int64_t)H * W);
+        const int c = (int)(bc % Cc), b = (int)(bc / Cc);
+        const float v = g[((int64_t)w * B + b) * Cc + c] / fn;
+        dx[t] = acc ? dx[t] + v : v;
+    }
+}
 __global__ void __launch_bounds__(kBlock) k_mean_axis_bwd(const float *__restrict__ g, float *__restrict__ dx,
                                                           int outer, int n, int inner, int acc) {
     int64_t total = (int64_t)outer * n * inner, stride = (int64_t)gridDim.x * kBlock;
@@ -386,6 +410,23 @@ om_status om_mse_fwd_post(om_ctx *ctx, const float *pred, const float *target, f
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, pred && target && loss && n > 0 && rb && (diff || dpred_unit), "om_mse_fwd_post: bad arguments");
     return mse_fwd(ctx, pred, target, diff, loss, dpred_unit, n, rb);
+}
+
+om_status om_mean_permute_fwd(om_ctx *ctx, const float *x, float *y, int B, int C, int H, int W) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && y && B > 0 && C > 0 && H > 0 && W > 0, "om_mean_permute_fwd: bad arguments");
+    const int64_t n = (int64_t)B * C * W;
+    hipLaunchKernelGGL(k_mean_permute_fwd, dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, ctx->stream, x,
+                       y, B, C, H, W);
+    return OM_LAUNCH_CHECK(ctx, "om_mean_permute_fwd");
+}
+
+om_status om_mean_permute_bwd(om_ctx *ctx, const float *g, float *dx, int B, int C, int H, int W, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g && dx && B > 0 && C > 0 && H > 0 && W > 0, "om_mean_permute_bwd: bad arguments");
+    hipLaunchKernelGGL(k_mean_permute_bwd, dim3(ew_grid((int64_t)B * C * H * W)), dim3(kBlock), 0, ctx->stream, g, dx,
+                       B, C, H, W, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_mean_permute_bwd");
 }
 
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate) {

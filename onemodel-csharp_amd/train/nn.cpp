@@ -1066,8 +1066,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
                 h = conv2d_relu_pool(h, cv.w, cv.b, cv.stride, cv.pad, pools[i][0], pools[i][1], pools[i][0],
                                      pools[i][1]);
             }
-            Tensor f = mean_axis(h, 2);        // [B, 256, T]
-            Tensor seq = permute(f, {2, 0, 1});  // [T, B, 256]
+            Tensor seq = mean_permute_seq(h);  // Mean(axis 2) [B, 256, T], then Permute(2, 0, 1): [T, B, 256]
             Tensor lp = log_softmax((*mp->head)(seq));
             const Input &lb = s.input("labels"), &il = s.input("in_len"), &tl = s.input("tgt_len");
             return ctc_loss(lp, lb.hi, il.hi, tl.hi, 0, 1, lb.t, il.t, tl.t);

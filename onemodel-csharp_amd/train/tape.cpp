@@ -718,6 +718,22 @@ Tensor mean_axis(const Tensor &x, int axis) {
     return y;
 }
 
+// Mean over axis 2 of x [B, C, H, W], then Permute(2, 0, 1) to [W, B, C], as one record (the CRNN's sequence head):
+// one launch each way, the bits of the two ops.
+Tensor mean_permute_seq(const Tensor &x) {
+    if (x->shape.size() != 4) shape_error("Mean then Permute: input " + shape_str(x->shape) + " is not [B, C, H, W].");
+    const int B = x->shape[0], Cc = x->shape[1], H = x->shape[2], W = x->shape[3];
+    Tensor y = make({W, B, Cc});
+    OMT(om_mean_permute_fwd(C(), x->data, y->data, B, Cc, H, W));
+    if (tracked({&x}))
+        attach(y, "MeanPermute", {x}, [B, Cc, H, W](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            if (dx) OMT(om_mean_permute_bwd(C(), g, dx, B, Cc, H, W, a));
+        });
+    return y;
+}
+
 Tensor log_softmax(const Tensor &x) {
     const int cols = x->shape.back();
     const int rows = (int)(x->numel / cols);

@@ -189,6 +189,8 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
 Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
            const Tensor &resid);
 Tensor relu(const Tensor &x);
+// Mean over axis 2 of [B, C, H, W] then Permute(2, 0, 1): [W, B, C], one record, the bits of the two ops.
+Tensor mean_permute_seq(const Tensor &x);
 Tensor gelu(const Tensor &x);
 Tensor add(const Tensor &a, const Tensor &b);
 Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, float eps);

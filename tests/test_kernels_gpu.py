@@ -745,6 +745,29 @@ def test_conv2d(dev, T, N, Cin, H, W, Cout, K, S, P):
         assert np.array_equal(a.view(np.uint32), dev.get(t).view(np.uint32))
 
 
+@pytest.mark.parametrize("B,Cc,H,W", [(32, 256, 2, 32), (3, 5, 7, 11), (1, 1, 1, 1)])
+def test_mean_permute_bit_exact(dev, B, Cc, H, W):
+    """The CRNN's sequence head in one call each way: om_mean_permute_fwd equals om_mean_axis (axis 2) then
+    om_permute(2, 0, 1), and om_mean_permute_bwd equals the permute's backward then om_mean_axis_bwd, bit for bit,
+    also accumulating."""
+    rng = np.random.default_rng(B * Cc + H * W)
+    x, g = rnd(rng, B, Cc, H, W), rnd(rng, W, B, Cc)
+    X, G = dev.put(x), dev.put(g)
+    Y, M, YP = dev.empty((W, B, Cc)), dev.empty((B, Cc, W)), dev.empty((W, B, Cc))
+    dev.call("om_mean_permute_fwd", X, Y, B, Cc, H, W)
+    dev.call("om_mean_axis", X, M, B * Cc, H, W)
+    shape, perm = (C.c_int32 * 3)(B, Cc, W), (C.c_int32 * 3)(2, 0, 1)
+    dev.call("om_permute", M, YP, 3, shape, perm, 0)
+    assert np.array_equal(dev.get(Y).view(np.uint32), dev.get(YP).view(np.uint32))
+    GB, DX1, DX2 = dev.empty((B, Cc, W)), dev.empty(x.shape), dev.empty(x.shape)
+    gshape, gperm = (C.c_int32 * 3)(W, B, Cc), (C.c_int32 * 3)(1, 2, 0)
+    dev.call("om_permute", G, GB, 3, gshape, gperm, 0)
+    for acc in (0, 1):
+        dev.call("om_mean_permute_bwd", G, DX1, B, Cc, H, W, acc)
+        dev.call("om_mean_axis_bwd", GB, DX2, B * Cc, H, W, acc)
+        assert np.array_equal(dev.get(DX1).view(np.uint32), dev.get(DX2).view(np.uint32)), acc
+
+
 @pytest.mark.parametrize("shape,k,s", [((2, 3, 8, 12), (2, 2), (2, 2)), ((2, 4, 8, 6), (2, 1), (2, 1)),
                                        ((1, 2, 9, 9), (3, 3), (2, 2))])
 def test_maxpool_bit_exact(dev, T, shape, k, s):
