@@ -624,6 +624,31 @@ def cpu_baseline(cfg: int, seconds: float):
                       f"oracle/tape.py, {tot:.1f} s, OpenMP {threads} threads"}
 
 
+def time_per_op(pkg, cfg, steps, warmup):
+    """The same configuration built with the reference's own record structure (omt_config_create_records,
+    OMT_RECORDS_PER_OP: every rule one C-ABI call when the engine reaches it, no composite records, no colocated q|k|v,
+    no grouped weight gradients), timed like the headline: eager launches, then from a step graph."""
+    m = pkg.Model(cfg, per_op=True)
+    try:
+        out = {}
+        for mode in ("eager", "step_graph"):
+            if mode == "step_graph":
+                m.set_step_graph(True)
+            for _ in range(warmup):
+                m.step()
+            pkg.load_hip().om_ctx_sync(m.ctx)
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                m.step()
+            pkg.load_hip().om_ctx_sync(m.ctx)
+            out[mode] = round(steps / (time.perf_counter() - t0), 3)
+        per = sorted(HipEvents().per_step(pkg.load_hip().om_ctx_stream(m.ctx), m.step, max(50, steps)))
+        out["median_ms"] = round(per[len(per) // 2], 4)
+        return out
+    finally:
+        m.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -696,6 +721,15 @@ def main():
                           "replayed from a recorded HIP graph (omt_set_step_graph); the results are bit-identical, "
                           "value is the faster of the two"},
     }
+    po = time_per_op(pkg, a.config, a.steps, a.warmup)
+    out["modes"]["per_op"] = po["eager"]
+    out["modes"]["per_op_step_graph"] = po["step_graph"]
+    out["modes"]["per_op_median_ms"] = po["median_ms"]
+    out["modes"]["per_op_note"] = ("the reference's own records (omt_config_create_records, OMT_RECORDS_PER_OP): "
+                                   "Linear as Reshape/MatMul/Add/Reshape, three q/k/v Linears over weights of their "
+                                   "own, Conv2d/Relu/MaxPool2d apart, Mean then Permute, Mse as Sub/Mul/Mean, "
+                                   "CrossEntropy as LogSoftmax/NllLoss, every rule one C-ABI call made when the engine "
+                                   "reaches it (no grouped weight gradients); eager launches and from a step graph")
     if a.config == 3:
         out["pcie_inclusive"] = time_staged(pkg, model, a.steps)
     if a.config == 3:

@@ -249,6 +249,10 @@ om_status om_gelu_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, in
 om_status om_add(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
 om_status om_sub(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
 om_status om_mul(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n);
+/* y[r][c] = x[r][c] + b[c] over [rows, cols]: Ops.Add with b broadcast over the rows (Ops.cs:15-56), the bias add of
+ * Ops.Linear (Ops.Layers.cs:715-733) as the reference records it, a separate op after the MatMul. Its backward is
+ * the identity for x and om_colsum (BackwardOps.SumTo) for b. */
+om_status om_add_rows(om_ctx *ctx, const float *x, const float *b, float *y, int rows, int cols);
 /* dst += src, or dst = src * alpha + dst (Engine.AddInto, Engine.cs:331-344; Neg backward is alpha = -1). */
 om_status om_axpy(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n);
 /* dst = src * alpha (a copy when alpha is 1). */
@@ -307,12 +311,15 @@ om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, cons
                                int cols, int acc_params);
 /* om_layernorm_bwd without any device allocation, for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. The dgamma/dbeta fp64
- * partials (2 * ceil(rows / r) * cols doubles, r = 16 rows per chunk when cols is 384 or 768, else 8) go to one fixed
- * device array of OM_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; larger shapes are refused with
- * OM_E_ARG before anything is launched. The partials are rewritten by every call, so nothing has to start at zero;
- * calls that overlap on one GPU (contexts on other streams or threads) share the array and race. Results are
- * om_layernorm_bwd's, bit for bit. */
+ * partials (2 * ceil(rows / r) * cols doubles, r = 16 rows per chunk when cols is 384 or 768, else 8) go to the
+ * calling context's own slot of one fixed device array per GPU (OM_NOALLOC_SLOTS slots of OM_NOALLOC_SCRATCH_BYTES,
+ * held until the process ends). A context claims its slot on its first call and keeps it until om_ctx_destroy;
+ * when every slot of the device is held by other live contexts the call fails with OM_E_STATE, and larger shapes are
+ * refused with OM_E_ARG, both before anything is launched. The partials are rewritten by every call, so nothing has
+ * to start at zero; calls on one context are ordered by its stream, and contexts never share a slot, so calls from
+ * several contexts (threads, streams) on one GPU do not race. Results are om_layernorm_bwd's, bit for bit. */
 #define OM_NOALLOC_SCRATCH_BYTES (8u << 20)
+#define OM_NOALLOC_SLOTS 4
 om_status om_layernorm_bwd_noalloc(om_ctx *ctx, const float *g, const float *x, const float *gamma,
                                    const float *mean, const float *rstd, float *dx, float *dgamma, float *dbeta,
                                    int rows, int cols, int acc_dx, int acc_params);
@@ -336,6 +343,10 @@ om_status om_logsoftmax_bwd(om_ctx *ctx, const float *g, const float *y, float *
  * is reported through *bad_row (device int32, -1 when none), the reference's ArgumentOutOfRangeException. */
 om_status om_nll_fwd(om_ctx *ctx, const float *logp, const int32_t *target, float *loss, int32_t *bad_row, int rows,
                      int cols, int mean, int ignore_index);
+/* NllBackward (BackwardNn.cs:602-632): dlogp (+)= -scale at [i, target[i]] for every row whose target is not
+ * ignore_index and 0 elsewhere, scale = g / max(1, count of such rows) with mean, else g (g_scalar a device float). */
+om_status om_nll_bwd(om_ctx *ctx, const float *g_scalar, const int32_t *target, float *dlogp, int rows, int cols,
+                     int mean, int ignore_index, int accumulate);
 /* Fused softmax cross-entropy gradient = LogSoftmax backward of NllBackward (BackwardNn.cs:54-80, 602-632), in the
  * reference's rounding order: dlogits = d - exp(logp) * (float)sum(d), d = -g/count at the target. */
 om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,

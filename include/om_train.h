@@ -39,6 +39,18 @@ typedef struct {
  * 10 = MLP 64-128-[128]-[128]-64 whose middle Linear is applied twice, so its gradient sums two uses
  * (BackwardEngineTests.cs:13-25 at layer level), CE, AdamW(1e-3, wd 0.01), batch 256. */
 om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out);
+/* The same with a choice of record structure. OMT_RECORDS_FUSED (what omt_config_create builds): composite records
+ * that a C# drop-in would need as module-level fused ops (a Linear with its bias in one record, q|k|v as one product
+ * over weights the arena lays out side by side, the feed-forward sub-block with its GELU and residual, a conv stage
+ * with its ReLU and max pool, MSE and cross-entropy as one record each) and weight gradients queued by the engine and
+ * launched together. OMT_RECORDS_PER_OP: exactly the records the reference's ops and modules create, each rule one
+ * C-ABI call made when Engine.Execute reaches it (Engine.cs:160-191), no queue, no colocation: Linear = Reshape,
+ * MatMul(x, W.T()), Add(bias), Reshape (Ops.Layers.cs:715-733); MultiHeadAttention = three Linears, Attention, one
+ * Linear (Layers.cs:497-516); Conv2d, Relu and MaxPool2d apart; Mean then Permute; Mse = Sub, Mul, Mean and
+ * CrossEntropy = LogSoftmax, NllLoss (Losses.cs:20-91). Views stay views (the kernels address the reshaped, transposed
+ * and head-permuted tensors in place). Both build the same parameters in the same order from the same generator. */
+enum { OMT_RECORDS_FUSED = 0, OMT_RECORDS_PER_OP = 1 };
+om_status omt_config_create_records(int device, int cfg, const omt_scale *scale, int records, omt_model **out);
 void omt_destroy(omt_model *m);
 const char *omt_last_error(omt_model *m); /* m may be NULL for creation errors */
 

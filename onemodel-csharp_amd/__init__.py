@@ -65,6 +65,7 @@ _OM_SIGS = {
     "om_gelu_fwd": [vp, vp, vp, i64],
     "om_gelu_bwd": [vp, vp, vp, vp, i64, ci],
     "om_add": [vp, vp, vp, vp, i64],
+    "om_add_rows": [vp, vp, vp, vp, ci, ci],
     "om_sub": [vp, vp, vp, vp, i64],
     "om_mul": [vp, vp, vp, vp, i64],
     "om_axpy": [vp, f32, vp, vp, i64],
@@ -92,6 +93,7 @@ _OM_SIGS = {
     "om_logsoftmax_bwd": [vp, vp, vp, vp, ci, ci, ci],
     "om_nll_fwd": [vp, vp, vp, vp, vp, ci, ci, ci, ci],
     "om_xent_bwd": [vp, vp, vp, vp, vp, ci, ci, ci, ci, ci],
+    "om_nll_bwd": [vp, vp, vp, vp, ci, ci, ci, ci, ci],
     "om_attention_fwd": [vp, vp, vp, vp, vp, ci, vp, vp, ci, ci, ci, ci, ci, f32],
     "om_attention_bwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
     "om_attention_fwd_ld": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, ci, ci, ci, ci, ci, f32],
@@ -200,6 +202,7 @@ class omt_scale(C.Structure):
 
 _OMT_SIGS = {
     "omt_config_create": ([ci, ci, C.POINTER(omt_scale), C.POINTER(vp)], i32),
+    "omt_config_create_records": ([ci, ci, C.POINTER(omt_scale), ci, C.POINTER(vp)], i32),
     "omt_destroy": ([vp], None),
     "omt_last_error": ([vp], C.c_char_p),
     "omt_step": ([vp, C.POINTER(f32)], i32),
@@ -282,13 +285,15 @@ class Model:
     """One benchmark configuration on the device (include/om_train.h): `step()` is ZeroGrad + forward +
     loss.Backward() + AdamW.Step() and returns the loss."""
 
-    def __init__(self, cfg: int, device: int = 0, batch=0, seq=0, layers=0, hw=0):
+    def __init__(self, cfg: int, device: int = 0, batch=0, seq=0, layers=0, hw=0, per_op: bool = False):
+        """per_op: build the reference's own record structure (omt_config_create_records, OMT_RECORDS_PER_OP)
+        instead of the composite records."""
         import numpy as np
         self.np = np
         self.L = load_train()
         h = vp()
         sc = omt_scale(batch, seq, layers, hw)
-        st = self.L.omt_config_create(device, cfg, C.byref(sc), C.byref(h))
+        st = self.L.omt_config_create_records(device, cfg, C.byref(sc), 1 if per_op else 0, C.byref(h))
         if st != 0:
             raise OmError(f"omt_config_create({cfg}) failed ({st}): {self.L.omt_last_error(None).decode()}")
         self.h = h

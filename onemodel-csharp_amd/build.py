@@ -30,6 +30,11 @@ HIP_FLAGS = [
     "-fhip-fp32-correctly-rounded-divide-sqrt", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-result",
 ]
+# OM_TUNING_KNOBS=1 at build time makes a tuning build, whose comparison knobs (OM_GEMM_X, OM_GEMM_DMA,
+# OM_GROUP_BAND, OM_CONV3, OM_ATTN_PATH, OM_EMBEDDING_SORT) are read from the environment at run time; the default
+# build reads none, so its kernel choices depend on the shapes alone.
+if os.environ.get("OM_TUNING_KNOBS") == "1":
+    HIP_FLAGS.append("-DOM_TUNING_KNOBS")
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function"]
 
 

@@ -711,13 +711,13 @@ __global__ void __launch_bounds__(256) k_flash_dq_reduce(const float *__restrict
 bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 // Kernels for D = 32 and L = 64 or 128, where a workgroup holds whole rows. By default the whole-row forward with
-// statistics (k_rows_fwd) and the streaming backward. Comparison runs: OM_ATTN_PATH=exact runs the pair of
-// om_attention_fused.hip instead (the reference's exact softmax recompute, no statistics), OM_ATTN_PATH=stream the
-// streaming forward too.
+// statistics (k_rows_fwd) and the streaming backward. Comparison runs (tuning builds, om::tuning_env):
+// OM_ATTN_PATH=exact runs the pair of om_attention_fused.hip instead (the reference's exact softmax recompute, no
+// statistics), OM_ATTN_PATH=stream the streaming forward too.
 enum ShortPath { kRows, kExact, kStream };
 ShortPath short_path() {
     static const ShortPath p = [] {
-        const char *s = std::getenv("OM_ATTN_PATH");
+        const char *s = om::tuning_env("OM_ATTN_PATH");
         if (s && s[0] == 'e') return kExact;
         if (s && s[0] == 's') return kStream;
         return kRows;

@@ -22,10 +22,10 @@ bool om_conv3_dw(om_ctx *ctx, const float *g, const float *x, float *dw, float *
 
 namespace {
 
-// The 3x3 / stride 1 / padding 1 geometry the staged kernels take (OM_CONV3=0 keeps every shape on k_conv, for
-// comparisons).
+// The 3x3 / stride 1 / padding 1 geometry the staged kernels take (in a tuning build OM_CONV3=0 keeps every shape on
+// k_conv, for comparisons).
 bool conv3_geometry(int KH, int KW, int stride, int pad) {
-    static const char *s = std::getenv("OM_CONV3");
+    static const char *s = om::tuning_env("OM_CONV3");
     return KH == 3 && KW == 3 && stride == 1 && pad == 1 && !(s && s[0] == '0');
 }
 

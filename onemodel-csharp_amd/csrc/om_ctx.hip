@@ -134,6 +134,7 @@ om_status om_ctx_destroy(om_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->cap) (void)om_graph_capture_abort(ctx);
     (void)hipStreamSynchronize(ctx->stream);
+    om::noalloc_release(ctx);  // the stream is idle: no launch of this context still uses its slot
     for (auto &r : ctx->region)
         for (auto &s : r.slabs) (void)hipFree(s.base);
     if (ctx->scratch) (void)hipFree(ctx->scratch);

@@ -87,6 +87,22 @@ om_status map2(om_ctx *ctx, const char *name, const float *a, const float *b, fl
     return OM_LAUNCH_CHECK(ctx, name);
 }
 
+// Ops.Add with the second operand broadcast over the rows (Ops.cs:15-56), as a Linear's bias add issues it
+// (Ops.Layers.cs:715-733): y[r][c] = x[r][c] + b[c], one rounding per element.
+__global__ void __launch_bounds__(kBlock) k_add_rows4(const float4 *__restrict__ x, const float4 *__restrict__ b,
+                                                      float4 *__restrict__ y, int64_t n4, int cols4) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
+        const float4 v = x[i], w = b[i % cols4];
+        y[i] = float4{v.x + w.x, v.y + w.y, v.z + w.z, v.w + w.w};
+    }
+}
+__global__ void __launch_bounds__(kBlock) k_add_rows(const float *__restrict__ x, const float *__restrict__ b,
+                                                     float *__restrict__ y, int64_t n, int cols) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) y[i] = x[i] + b[i % cols];
+}
+
 __global__ void __launch_bounds__(kBlock) k_axpy(float alpha, const float *__restrict__ s, float *__restrict__ d,
                                                  int64_t n, int overwrite) {
     int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -462,6 +478,20 @@ om_status om_sub(om_ctx *ctx, const float *a, const float *b, float *y, int64_t 
 om_status om_mul(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n) {
     OM_REQUIRE(ctx, b || n == 0, "om_mul: NULL operand");
     return map2(ctx, "om_mul", a, b, y, n, 0, MulF{});
+}
+om_status om_add_rows(om_ctx *ctx, const float *x, const float *b, float *y, int rows, int cols) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, rows >= 0 && cols > 0, "om_add_rows: bad shape");
+    if (rows == 0) return OM_OK;
+    OM_REQUIRE(ctx, x && b && y, "om_add_rows: NULL pointer");
+    const int64_t n = (int64_t)rows * cols;
+    if (cols % 4 == 0 && aligned4(x) && aligned4(b) && aligned4(y))
+        hipLaunchKernelGGL(k_add_rows4, dim3(ew_grid(n / 4)), dim3(kBlock), 0, ctx->stream,
+                           reinterpret_cast<const float4 *>(x), reinterpret_cast<const float4 *>(b),
+                           reinterpret_cast<float4 *>(y), n / 4, cols / 4);
+    else
+        hipLaunchKernelGGL(k_add_rows, dim3(ew_grid(n)), dim3(kBlock), 0, ctx->stream, x, b, y, n, cols);
+    return OM_LAUNCH_CHECK(ctx, "om_add_rows");
 }
 om_status om_axpy(om_ctx *ctx, float alpha, const float *src, float *dst, int64_t n) {
     OM_CHECK_CTX(ctx);

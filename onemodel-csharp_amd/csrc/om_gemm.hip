@@ -206,10 +206,10 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 // the residual, is applied by every instance.
 static bool gelu_epi(int epi) { return epi != EPI_NONE && epi != EPI_RELU; }
 
-// OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for comparisons); otherwise NT tiles with
-// 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
+// In a tuning build (om::tuning_env), OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for
+// comparisons); otherwise NT tiles with 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
 static bool dma_disabled() {
-    static const char *s = std::getenv("OM_GEMM_DMA");
+    static const char *s = om::tuning_env("OM_GEMM_DMA");
     return s && s[0] == '0';
 }
 
@@ -350,27 +350,27 @@ Choice with_splits(int bm, int bn, int bkt, int k, int splits) {
     return c;
 }
 
-// Tuning runs: OM_GEMM_X="bm,bn,bkt[,splits]" forces a tile-exact configuration where it fits (read at every call,
-// so one process can compare configurations).
+// Tuning builds (om::tuning_env): OM_GEMM_X="bm,bn,bkt[,splits]" forces a tile-exact configuration where it fits (read
+// at every call, so one process can compare configurations).
 bool env_override(Choice &c, int k) {
-    const char *s = std::getenv("OM_GEMM_X");
+    const char *s = om::tuning_env("OM_GEMM_X");
     if (!s || !*s || !strcmp(s, "off")) return false;
     int bm = 0, bn = 0, bk = 32, sp = 1;
     if (sscanf(s, "%d,%d,%d,%d", &bm, &bn, &bk, &sp) < 3) return false;
     c = with_splits(bm, bn, bk, k, sp);
     return true;
 }
-// Tile order of the grouped weight gradients: bands of OM_GROUP_BAND tile rows walked column by column (0:
-// row-major), for comparison runs.
+// Tile order of the grouped weight gradients (tuning builds): bands of OM_GROUP_BAND tile rows walked column by column
+// (0: row-major), for comparison runs.
 int group_band() {
     static const int b = [] {
-        const char *s = std::getenv("OM_GROUP_BAND");
+        const char *s = om::tuning_env("OM_GROUP_BAND");
         return s && *s ? atoi(s) : 0;
     }();
     return b;
 }
 bool x_disabled() {
-    const char *s = std::getenv("OM_GEMM_X");
+    const char *s = om::tuning_env("OM_GEMM_X");
     return s && !strcmp(s, "off");
 }
 }  // namespace

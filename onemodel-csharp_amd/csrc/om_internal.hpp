@@ -8,6 +8,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -46,8 +47,10 @@ struct om_ctx {
     float *scratch2 = nullptr;
     uint64_t scratch2_bytes = 0;
     // Device address of the fixed scratch array the allocation-free entry point uses on this context's device
-    // (looked up once per device at context creation; NULL if that failed).
+    // (looked up once per device at context creation; NULL if that failed), and the slot of it this context holds
+    // (claimed by its first allocation-free call, released by om_ctx_destroy; -1 while it holds none).
     void *noalloc_scratch = nullptr;
+    int noalloc_slot = -1;
     int num_cus = 256;
     // The step graph being captured on the stream (om_graph_capture_begin .. _end), else NULL.
     struct om_graph *cap = nullptr;
@@ -90,6 +93,22 @@ om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
 // Sets ctx->noalloc_scratch to the device address of the fixed scratch array on ctx->device (the current device),
 // looking it up on the first call for that device only.
 om_status noalloc_init(om_ctx *ctx);
+// The context's own slot of that array (OM_NOALLOC_SCRATCH_BYTES bytes), claimed on the first call: no two live
+// contexts on one device share a slot, so their calls cannot overwrite each other's partials. OM_E_STATE when every
+// slot of the device is held by another live context.
+om_status noalloc_slot(om_ctx *ctx, double **out);
+void noalloc_release(om_ctx *ctx);
+// Comparison knobs: environment variables that force a tile, a kernel family or a code path for A/B runs. They are
+// read only in a tuning build (compiled with -DOM_TUNING_KNOBS); the product build's choices depend on the shapes
+// alone, so its results repeat bit for bit for a given shape whatever the environment.
+inline const char *tuning_env(const char *name) {
+#ifdef OM_TUNING_KNOBS
+    return std::getenv(name);
+#else
+    (void)name;
+    return nullptr;
+#endif
+}
 // OM_E_STATE with a message when a step graph is being captured on ctx's stream (for calls a graph cannot hold).
 om_status refuse_in_capture(om_ctx *ctx, const char *what);
 // The launch timing probe around one call: probe_begin records the start event and returns the call's slot (-1 when

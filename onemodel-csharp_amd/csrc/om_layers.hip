@@ -392,8 +392,8 @@ om_status om_embedding_bwd(om_ctx *ctx, const float *g, const int32_t *ids, floa
     OM_REQUIRE(ctx, g && ids && dtable && n_ids >= 0 && dim > 0 && rows > 0, "om_embedding_bwd: bad arguments");
     const unsigned row_grid = (unsigned)((rows + kBlock / 64 - 1) / (kBlock / 64));
     // Small tables (or few ids): one launch that scans the ids for every row. Beyond about 2^22 id visits the sort
-    // costs less than the scan. OM_EMBEDDING_SORT=0 keeps every size on the scan (for comparisons).
-    const char *env = std::getenv("OM_EMBEDDING_SORT");
+    // costs less than the scan. In a tuning build OM_EMBEDDING_SORT=0 keeps every size on the scan (for comparisons).
+    const char *env = om::tuning_env("OM_EMBEDDING_SORT");
     const bool no_sort = env && env[0] == '0';
     if (no_sort || (double)rows * (double)n_ids <= (double)(1 << 22) || n_ids > INT32_MAX) {
         hipLaunchKernelGGL(k_embedding_bwd, dim3(row_grid), dim3(kBlock), 0, ctx->stream, g, ids, dtable, n_ids, dim,

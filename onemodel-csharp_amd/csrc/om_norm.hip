@@ -574,6 +574,22 @@ __global__ void __launch_bounds__(kBlock) k_xent_bwd(const float *__restrict__ g
     }
 }
 
+// NllBackward (BackwardNn.cs:602-632) alone: scale = g/max(1,count) (or g); dx is -scale at each counted row's target
+// and 0 elsewhere (Tensor.Zeros), added into an existing gradient when acc (Engine.AddInto).
+__global__ void __launch_bounds__(kBlock) k_nll_bwd(const float *__restrict__ gs, const int *__restrict__ count,
+                                                    const int32_t *__restrict__ tg, float *__restrict__ dx, int rows,
+                                                    int cols, int mean, int ignore, int acc) {
+    const int64_t n = (int64_t)rows * cols, stride = (int64_t)gridDim.x * kBlock;
+    const float g = gs[0];
+    const int c = count[0];
+    const float scale = mean ? g / (float)(c > 1 ? c : 1) : g;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / cols), j = (int)(i % cols), t = tg[r];
+        const float d = (t != ignore && j == t) ? -scale : 0.0f;
+        dx[i] = acc ? dx[i] + d : d;
+    }
+}
+
 inline unsigned rows_grid(int rows, int lanes_per_row) {
     return om::grid1d((int64_t)rows * lanes_per_row, kBlock, 1 << 30);
 }
@@ -654,19 +670,24 @@ static om_status ln_bwd_main(om_ctx *ctx, const float *g, const float *x, const 
     return OM_LAUNCH_CHECK(ctx, "om_layernorm_bwd");
 }
 
-// Fixed device scratch for om_layernorm_bwd_noalloc's fp64 dgamma / dbeta partials (2 * chunks * cols doubles), one
-// copy per GPU for the life of the process. Host code never passes this name to a kernel: it is a host-side stand-in;
-// kernels get the device address that noalloc_init looks up per device.
-static __device__ __align__(256) unsigned char ln_scratch[OM_NOALLOC_SCRATCH_BYTES];
+// Fixed device scratch for om_layernorm_bwd_noalloc's fp64 dgamma / dbeta partials (2 * chunks * cols doubles):
+// OM_NOALLOC_SLOTS slots of OM_NOALLOC_SCRATCH_BYTES, one copy per GPU for the life of the process. Each live
+// context that calls the entry point holds a slot of its own, so calls from contexts on other streams or threads of
+// one GPU never share memory. Host code never passes this name to a kernel: it is a host-side stand-in; kernels get
+// the device address that noalloc_init looks up per device.
+static __device__ __align__(256) unsigned char ln_scratch[(size_t)OM_NOALLOC_SLOTS * OM_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_ln_scratch_mu;
-void *g_ln_scratch_at[kMaxDevices];  // per device: ln_scratch's device address, once looked up
+void *g_ln_scratch_at[kMaxDevices];     // per device: ln_scratch's device address, once looked up
+unsigned g_ln_slots_held[kMaxDevices];  // per device: bit i set while a live context holds slot i
+static_assert(OM_NOALLOC_SLOTS <= 32, "the slot mask is 32 bits");
 }  // namespace
 
 om_status om::noalloc_init(om_ctx *ctx) {
     ctx->noalloc_scratch = nullptr;
+    ctx->noalloc_slot = -1;
     if (ctx->device < 0 || ctx->device >= kMaxDevices)
         return om::fail(ctx, OM_E_DEVICE, "allocation-free scratch: device %d is beyond %d", ctx->device, kMaxDevices);
     std::lock_guard<std::mutex> g(g_ln_scratch_mu);
@@ -678,6 +699,35 @@ om_status om::noalloc_init(om_ctx *ctx) {
     }
     ctx->noalloc_scratch = g_ln_scratch_at[ctx->device];
     return OM_OK;
+}
+
+om_status om::noalloc_slot(om_ctx *ctx, double **out) {
+    if (!ctx->noalloc_scratch)
+        return om::fail(ctx, OM_E_STATE, "om_layernorm_bwd_noalloc: the fixed scratch has no device address here");
+    if (ctx->noalloc_slot < 0) {
+        std::lock_guard<std::mutex> g(g_ln_scratch_mu);
+        unsigned &held = g_ln_slots_held[ctx->device];
+        for (int i = 0; i < OM_NOALLOC_SLOTS && ctx->noalloc_slot < 0; i++)
+            if (!(held & (1u << i))) {
+                held |= 1u << i;
+                ctx->noalloc_slot = i;
+            }
+        if (ctx->noalloc_slot < 0)
+            return om::fail(ctx, OM_E_STATE,
+                            "om_layernorm_bwd_noalloc: all %d slots of the fixed scratch on device %d are held by "
+                            "other live contexts",
+                            OM_NOALLOC_SLOTS, ctx->device);
+    }
+    *out = reinterpret_cast<double *>(static_cast<unsigned char *>(ctx->noalloc_scratch) +
+                                      (size_t)ctx->noalloc_slot * OM_NOALLOC_SCRATCH_BYTES);
+    return OM_OK;
+}
+
+void om::noalloc_release(om_ctx *ctx) {
+    if (ctx->noalloc_slot < 0 || ctx->device < 0 || ctx->device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> g(g_ln_scratch_mu);
+    g_ln_slots_held[ctx->device] &= ~(1u << ctx->noalloc_slot);
+    ctx->noalloc_slot = -1;
 }
 
 // fixed: the partials' device memory when the caller provides it (the allocation-free entry point), else NULL and
@@ -730,10 +780,13 @@ om_status om_layernorm_bwd_noalloc(om_ctx *ctx, const float *g, const float *x, 
                "om_layernorm_bwd_noalloc: %d x %d needs %llu bytes of dgamma/dbeta partials, more than the %llu of "
                "its fixed scratch",
                rows, cols, (unsigned long long)need, (unsigned long long)OM_NOALLOC_SCRATCH_BYTES);
-    if (need && !ctx->noalloc_scratch)
-        return om::fail(ctx, OM_E_STATE, "om_layernorm_bwd_noalloc: the fixed scratch has no device address here");
+    double *slot = nullptr;
+    if (need) {
+        om_status s = om::noalloc_slot(ctx, &slot);
+        if (s) return s;
+    }
     return ln_bwd(ctx, g, x, gamma, mean, rstd, dx, acc_dx && dx ? dx : nullptr, dgamma, dbeta, rows, cols,
-                  acc_params, static_cast<double *>(ctx->noalloc_scratch));
+                  acc_params, slot);
 }
 
 int om_layernorm_bwd_chunks(int rows, int cols) {
@@ -824,6 +877,21 @@ om_status om_xent_fwd_unit(om_ctx *ctx, const float *logits, const int32_t *targ
     om_status s = OM_LAUNCH_CHECK(ctx, "om_xent_fwd_unit");
     if (s == OM_OK && rb) om::readback_posted(rb, post.seq, sizeof(float));
     return s;
+}
+
+om_status om_nll_bwd(om_ctx *ctx, const float *g_scalar, const int32_t *target, float *dlogp, int rows, int cols,
+                     int mean, int ignore_index, int accumulate) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, g_scalar && target && dlogp && rows >= 0 && cols > 0, "om_nll_bwd: bad arguments");
+    if (rows == 0) return OM_OK;
+    float *scr;
+    om_status s = om::scratch(ctx, 256, &scr);
+    if (s) return s;
+    int *count = reinterpret_cast<int *>(scr);
+    hipLaunchKernelGGL(k_xent_count, dim3(1), dim3(kBlock), 0, ctx->stream, target, rows, ignore_index, count);
+    hipLaunchKernelGGL(k_nll_bwd, dim3(om::grid1d((int64_t)rows * cols, kBlock, 4096)), dim3(kBlock), 0, ctx->stream,
+                       g_scalar, count, target, dlogp, rows, cols, mean, ignore_index, accumulate);
+    return OM_LAUNCH_CHECK(ctx, "om_nll_bwd");
 }
 
 om_status om_xent_bwd(om_ctx *ctx, const float *g_scalar, const float *logp, const int32_t *target, float *dlogits,

@@ -132,14 +132,20 @@ MultiHeadAttention::MultiHeadAttention(int width, int heads_, Generator &g) : he
     k = child("k", std::make_unique<Linear>(width, width, g));
     v = child("v", std::make_unique<Linear>(width, width, g));
     o = child("o", std::make_unique<Linear>(width, width, g));
-    colocate({q->w, k->w, v->w});  // one [3W, W] weight and one [3W] bias for the packed projection
-    colocate({q->b, k->b, v->b});
+    if (!dev().per_op) {
+        colocate({q->w, k->w, v->w});  // one [3W, W] weight and one [3W] bias for the packed projection
+        colocate({q->b, k->b, v->b});
+    }
 }
 Tensor MultiHeadAttention::operator()(const Tensor &x, const Tensor &mask) const {
-    // Layers.cs:497-516: q/k/v projections, split heads, attention, merge heads, output projection.
+    // Layers.cs:497-516: q/k/v projections, split heads, attention, merge heads, output projection. The per-op records
+    // are the three Linears, the attention over their outputs (the split and merge permutes are views the kernels
+    // address in place) and the output Linear.
+    if (dev().per_op) return (*o)(attention_heads((*q)(x), (*k)(x), (*v)(x), mask, heads));
     return (*o)(attention_qkv(x, q->w, q->b, k->w, k->b, v->w, v->b, mask, heads));
 }
 Tensor MultiHeadAttention::residual(const Tensor &x, const Tensor &mask, const Tensor &resid) const {
+    if (dev().per_op) return add(resid, (*this)(x, mask));  // Ops.Add(input, attn)
     return linear_residual(attention_qkv(x, q->w, q->b, k->w, k->b, v->w, v->b, mask, heads), o->w, o->b, resid);
 }
 
@@ -161,6 +167,14 @@ struct EncoderLayer : Module {
         }
     }
     Tensor operator()(const Tensor &x, const Tensor &mask) const {
+        if (dev().per_op) {  // TransformerEncoderLayer.Forward (Layers.cs:557-577) record for record
+            Tensor a = (*attn)(x, mask);
+            if (drop1) a = (*drop1)(a);
+            Tensor x1 = (*norm1)(add(x, a));
+            Tensor f = (*ff2)(gelu((*ff1)(x1)));
+            if (drop2) f = (*drop2)(f);
+            return (*norm2)(add(x1, f));
+        }
         if (drop1) {  // norm1(x + drop1(attn(x))), norm2(x1 + drop2(ff2(gelu(ff1(x1)))))
             Tensor x1 = (*norm1)(add(x, (*drop1)((*attn)(x, mask))));
             return (*norm2)(add(x1, (*drop2)(ffn(x1, ff1->w, ff1->b, ff2->w, ff2->b, nullptr))));
@@ -185,6 +199,10 @@ struct PreNormBlock : Module {
     }
     Tensor operator()(const Tensor &x, const Tensor &mask) const {
         // h = x + attn(ln1(x)); y = h + ff2(gelu(ff1(ln2(h)))), the Adds and GELU fused into the Linear launches
+        if (dev().per_op) {
+            Tensor h = add(x, (*attn)((*ln1)(x), mask));
+            return add(h, (*ff2)(gelu((*ff1)((*ln2)(h)))));
+        }
         Tensor h = attn->residual((*ln1)(x), mask, x);
         return ffn((*ln2)(h), ff1->w, ff1->b, ff2->w, ff2->b, h);
     }
@@ -1013,6 +1031,12 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.loss_fn = [mp](omt_model &s) {
             // Relu, then GlobalAvgPool2d (Ops.Layers.cs:463-472: Reshape + Mean(axis 2) + Reshape) and Flatten, as
             // one record
+            if (dev().per_op) {  // Relu, GlobalAvgPool2d (Reshape, Mean(axis 2), Reshape), Flatten
+                Tensor a = relu((*mp->conv)(s.input("x").t));
+                const int N = a->shape[0], Cc = a->shape[1], P = a->shape[2] * a->shape[3];
+                Tensor gap = reshape(mean_axis(reshape(a, {N, Cc, P}), 2), {N, Cc, 1, 1});
+                return cross_entropy((*mp->fc)(reshape(gap, {N, Cc})), s.input("labels").t);
+            }
             Tensor gap = relu_mean_plane((*mp->conv)(s.input("x").t));
             return cross_entropy((*mp->fc)(gap), s.input("labels").t);
         };
@@ -1063,10 +1087,14 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
             // Conv2d -> Relu -> MaxPool2d per stage, one record each
             for (int i = 0; i < 4; i++) {
                 const Conv2d &cv = *mp->conv[i];
-                h = conv2d_relu_pool(h, cv.w, cv.b, cv.stride, cv.pad, pools[i][0], pools[i][1], pools[i][0],
-                                     pools[i][1]);
+                if (dev().per_op)
+                    h = max_pool2d(relu(cv(h)), pools[i][0], pools[i][1], pools[i][0], pools[i][1]);
+                else
+                    h = conv2d_relu_pool(h, cv.w, cv.b, cv.stride, cv.pad, pools[i][0], pools[i][1], pools[i][0],
+                                         pools[i][1]);
             }
-            Tensor seq = mean_permute_seq(h);  // Mean(axis 2) [B, 256, T], then Permute(2, 0, 1): [T, B, 256]
+            // Mean(axis 2) [B, 256, T], then Permute(2, 0, 1): [T, B, 256]
+            Tensor seq = dev().per_op ? permute(mean_axis(h, 2), {2, 0, 1}) : mean_permute_seq(h);
             Tensor lp = log_softmax((*mp->head)(seq));
             const Input &lb = s.input("labels"), &il = s.input("in_len"), &tl = s.input("tgt_len");
             return ctc_loss(lp, lb.hi, il.hi, tl.hi, 0, 1, lb.t, il.t, tl.t);
@@ -1237,11 +1265,20 @@ static om_status guard(omt_model *m, F f) {
 extern "C" {
 
 om_status omt_config_create(int device, int cfg, const omt_scale *scale, omt_model **out) {
+    return omt_config_create_records(device, cfg, scale, OMT_RECORDS_FUSED, out);
+}
+
+om_status omt_config_create_records(int device, int cfg, const omt_scale *scale, int records, omt_model **out) {
     if (!out) return OM_E_ARG;
     *out = nullptr;
+    if (records != OMT_RECORDS_FUSED && records != OMT_RECORDS_PER_OP) {
+        g_create_err = "omt_config_create_records: records must be OMT_RECORDS_FUSED or OMT_RECORDS_PER_OP";
+        return OM_E_ARG;
+    }
     auto *m = new omt_model();
     om_status s = guard(nullptr, [&] {
         m->device = std::make_unique<Device>(device);
+        m->device->per_op = records == OMT_RECORDS_PER_OP;
         set_dev(m->device.get());
         omt_scale sc{0, 0, 0, 0};
         if (scale) sc = *scale;

@@ -347,6 +347,11 @@ Tensor linear(const Tensor &x, const Tensor &w, const Tensor &b) {
     const int rows = (int)(x->numel / in);
     std::vector<int> ys = x->shape;
     ys.back() = out;
+    if (dev().per_op) {  // Reshape, MatMul(x, W.T()), Add(bias), Reshape: Ops.Layers.cs:715-733
+        Tensor y = matmul_wt(reshape(x, {rows, in}), w);
+        if (b) y = add_rows(y, b);
+        return reshape(y, ys);
+    }
     Tensor y = make(ys);
     OMT(om_linear_fwd(C(), x->data, w->data, b ? b->data : nullptr, y->data, rows, in, out));
     if (tracked({&x, &w, &b})) {
@@ -410,6 +415,116 @@ Tensor relu(const Tensor &x) {
     return y;
 }
 
+Tensor matmul_wt(const Tensor &x, const Tensor &w) {
+    if (w->shape.size() != 2 || x->shape.size() != 2 || x->shape[1] != w->shape[1])
+        shape_error("MatMul: " + shape_str(x->shape) + " does not fit the transposed weights " + shape_str(w->shape));
+    const int rows = x->shape[0], in = w->shape[1], out = w->shape[0];
+    Tensor y = make({rows, out});
+    OMT(om_linear_fwd(C(), x->data, w->data, nullptr, y->data, rows, in, out));
+    if (tracked({&x, &w}))
+        attach(y, "MatMul", {x, w}, [rows, in, out](Engine &e, Record &r, const float *g) {
+            // dA = g B^T and dB = A^T g (BackwardOps.cs:69-82) with B = W.T(): dW = g^T x, written as [out, in]
+            int ax, aw;
+            float *dx = e.dest(r, 0, &ax);
+            float *dw = e.dest(r, 1, &aw);
+            if (dx || dw)
+                OMT(om_linear_bwd(C(), g, r.inputs[0]->data, r.inputs[1]->data, dx, dw, nullptr, rows, in, out, ax,
+                                  aw, 0));
+        }, {x, w});
+    return y;
+}
+
+Tensor add_rows(const Tensor &x, const Tensor &b) {
+    const int cols = b->numel > 0 ? (int)b->numel : 1;
+    if (b->shape.size() != 1 || x->shape.empty() || x->shape.back() != cols)
+        shape_error("Add: " + shape_str(b->shape) + " does not broadcast to " + shape_str(x->shape));
+    const int rows = (int)(x->numel / cols);
+    Tensor y = make(x->shape);
+    OMT(om_add_rows(C(), x->data, b->data, y->data, rows, cols));
+    if (tracked({&x, &b}))
+        attach(y, "Add", {x, b}, [rows, cols](Engine &e, Record &r, const float *g) {
+            e.emit_alias(r, 0, g);
+            int a;
+            float *db = e.dest(r, 1, &a);  // EmitSummed: SumTo over the broadcast rows in double
+            if (db) OMT(om_colsum(C(), g, db, rows, cols, a));
+        });
+    return y;
+}
+
+Tensor sub(const Tensor &a, const Tensor &b) {
+    if (a->shape != b->shape) shape_error("Sub: shapes " + shape_str(a->shape) + " and " + shape_str(b->shape) + " differ.");
+    Tensor y = make(a->shape);
+    OMT(om_sub(C(), a->data, b->data, y->data, a->numel));
+    if (tracked({&a, &b})) {
+        const int64_t n = a->numel;
+        attach(y, "Sub", {a, b}, [n](Engine &e, Record &r, const float *g) {
+            e.emit_alias(r, 0, g);
+            int acc;
+            float *d = e.dest(r, 1, &acc);  // Neg's rule: -g
+            if (d) OMT(acc ? om_axpy(C(), -1.0f, g, d, n) : om_scale(C(), -1.0f, g, d, n));
+        });
+    }
+    return y;
+}
+
+Tensor mul(const Tensor &a, const Tensor &b) {
+    if (a->shape != b->shape) shape_error("Mul: shapes " + shape_str(a->shape) + " and " + shape_str(b->shape) + " differ.");
+    Tensor y = make(a->shape);
+    OMT(om_mul(C(), a->data, b->data, y->data, a->numel));
+    if (tracked({&a, &b})) {
+        const int64_t n = a->numel;
+        attach(y, "Mul", {a, b}, [n](Engine &e, Record &r, const float *g) {
+            // g * b to a, g * a to b (BackwardOps.cs:23-65); an emission into an existing gradient is added to it
+            for (int i = 0; i < 2; i++) {
+                int acc;
+                float *d = e.dest(r, i, &acc);
+                if (!d) continue;
+                const float *other = r.inputs[1 - i]->data;
+                if (!acc) {
+                    OMT(om_mul(C(), g, other, d, n));
+                } else {
+                    float *t = dev().step_floats(n);
+                    OMT(om_mul(C(), g, other, t, n));
+                    OMT(om_axpy(C(), 1.0f, t, d, n));
+                }
+            }
+        }, {a, b});
+    }
+    return y;
+}
+
+Tensor mean_all(const Tensor &x) {
+    Tensor y = make({});
+    OMT(om_sum_all(C(), x->data, y->data, x->numel, 1));
+    if (tracked({&x})) {
+        const int64_t n = x->numel;
+        attach(y, "Mean", {x}, [n](Engine &e, Record &r, const float *g) {
+            int a;
+            float *dx = e.dest(r, 0, &a);
+            if (dx) OMT(om_mean_all_bwd(C(), g, dx, n, a));
+        });
+    }
+    return y;
+}
+
+Tensor nll_loss(const Tensor &logp, const Tensor &labels) {
+    if (logp->shape.size() != 2 || !labels->idata || labels->shape != std::vector<int>{logp->shape[0]})
+        shape_error("NllLoss needs [N, C] log-probabilities and [N] Int32 targets, not " + shape_str(logp->shape) +
+                    " and " + shape_str(labels->shape));
+    const int rows = logp->shape[0], cols = logp->shape[1];
+    Tensor loss = make({});
+    OMT(om_nll_fwd(C(), logp->data, labels->idata, loss->data, nullptr, rows, cols, 1, -100));
+    if (tracked({&logp})) {
+        const int32_t *tg = labels->idata;
+        attach(loss, "NllLoss", {logp}, [tg, rows, cols](Engine &e, Record &r, const float *g) {
+            int a;
+            float *d = e.dest(r, 0, &a);
+            if (d) OMT(om_nll_bwd(C(), g, tg, d, rows, cols, 1, -100, a));
+        }, {labels});
+    }
+    return loss;
+}
+
 Tensor gelu(const Tensor &x) {
     Tensor y = make(x->shape);
     OMT(om_gelu_fwd(C(), x->data, y->data, x->numel));
@@ -447,7 +562,22 @@ Tensor layer_norm(const Tensor &x, const Tensor &gamma, const Tensor &beta, floa
     float *mean = rec ? dev().step_floats(rows) : nullptr;
     float *rstd = rec ? dev().step_floats(rows) : nullptr;
     OMT(om_layernorm_fwd(C(), x->data, gamma->data, beta->data, y->data, mean, rstd, rows, cols, eps));
-    if (rec)
+    if (rec && dev().per_op) {
+        attach(y, "LayerNorm", {x, gamma, beta}, [rows, cols, mean, rstd](Engine &e, Record &r, const float *g) {
+            // dx, dgamma and dbeta now, in one call (two when the parameter gradients' accumulation differs)
+            int ax, ag, ab;
+            float *dx = e.dest(r, 0, &ax);
+            float *dg = e.dest(r, 1, &ag);
+            float *db = e.dest(r, 2, &ab);
+            const float *xd = r.inputs[0]->data, *gd = r.inputs[1]->data;
+            if (!dg || !db || ag == ab) {
+                OMT(om_layernorm_bwd(C(), g, xd, gd, mean, rstd, dx, dg, db, rows, cols, ax, dg ? ag : ab));
+            } else {
+                OMT(om_layernorm_bwd(C(), g, xd, gd, mean, rstd, dx, dg, nullptr, rows, cols, ax, ag));
+                OMT(om_layernorm_bwd(C(), g, xd, gd, mean, rstd, nullptr, nullptr, db, rows, cols, 0, ab));
+            }
+        }, {x, gamma});
+    } else if (rec)
         attach(y, "LayerNorm", {x, gamma, beta}, [rows, cols, mean, rstd](Engine &e, Record &r, const float *g) {
             // dx now; dgamma / dbeta as fp64 partials in step memory whose column sums are queued with the weight
             // gradients (om_param_grads_group)
@@ -754,6 +884,7 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels) {
     if (logits->shape.size() != 2 || !labels->idata || labels->shape != std::vector<int>{logits->shape[0]})
         shape_error("NllLoss needs [N, C] log-probabilities and [N] Int32 targets, not " + shape_str(logits->shape) +
                     " and " + shape_str(labels->shape));
+    if (dev().per_op) return nll_loss(log_softmax(logits), labels);  // Losses.cs:20-40
     const int rows = logits->shape[0], cols = logits->shape[1];
     Tensor logp = make(logits->shape);
     Tensor loss = make({});
@@ -789,6 +920,10 @@ Tensor cross_entropy(const Tensor &logits, const Tensor &labels) {
 Tensor mse(const Tensor &pred, const Tensor &target) {
     if (pred->shape != target->shape)
         shape_error("Mse: shapes " + shape_str(pred->shape) + " and " + shape_str(target->shape) + " differ.");
+    if (dev().per_op) {  // Losses.Mse (Losses.cs:86-91): d = Sub(pred, target); Mean(Mul(d, d))
+        Tensor d = sub(pred, target);
+        return mean_all(mul(d, d));
+    }
     const int64_t n = pred->numel;
     Tensor loss = make({});
     const bool rec = tracked({&pred, &target});

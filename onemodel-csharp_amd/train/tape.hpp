@@ -88,6 +88,14 @@ class Device {
     explicit Device(int device);
     ~Device();
     om_ctx *ctx() const { return ctx_; }
+    // Record structure of the ops and modules built on this device. false (the default): composite records (a
+    // Linear with its bias, q|k|v as one product over colocated weights, the feed-forward sub-block, a conv stage,
+    // fused losses) and the engine's grouped weight-gradient launches. true: exactly the reference's records, each
+    // rule one C-ABI call run when the engine reaches it (a Linear is Reshape, MatMul with W.T(), Add of the bias,
+    // Reshape, Ops.Layers.cs:715-733; MultiHeadAttention three Linears, the attention and one Linear,
+    // Layers.cs:497-516; losses as Sub/Mul/Mean and LogSoftmax/NllLoss, Losses.cs:20-91). Views (Reshape, W.T(),
+    // the head split/merge permutes) stay views: the kernels address them in place. Fixed before modules are built.
+    bool per_op = false;
     float *step_floats(int64_t n);
     int32_t *step_ints(int64_t n);
     void *persistent(uint64_t bytes);
@@ -189,6 +197,16 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
 Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
            const Tensor &resid);
 Tensor relu(const Tensor &x);
+// The pieces of the reference's per-op records: Ops.MatMul(x2d, W.T()) of x [rows, in] and w [out, in], one record
+// whose rule is MatMul's backward with the W.T() view's Permute backward folded in (dW written as [out, in]);
+// Ops.Add with b [cols] broadcast over the rows of x [rows, cols]; Sub, Mul (same shapes); Ops.Mean over all elements;
+// Ops.NllLoss with the mean reduction and ignore index -100 over [N, C] log-probabilities.
+Tensor matmul_wt(const Tensor &x, const Tensor &w);
+Tensor add_rows(const Tensor &x, const Tensor &b);
+Tensor sub(const Tensor &a, const Tensor &b);
+Tensor mul(const Tensor &a, const Tensor &b);
+Tensor mean_all(const Tensor &x);
+Tensor nll_loss(const Tensor &logp, const Tensor &labels);
 // Mean over axis 2 of [B, C, H, W] then Permute(2, 0, 1): [W, B, C], one record, the bits of the two ops.
 Tensor mean_permute_seq(const Tensor &x);
 Tensor gelu(const Tensor &x);
@@ -303,7 +321,7 @@ class Linear : public Module {
     Linear(int in, int out, Generator &g, bool bias = true);
     Tensor operator()(const Tensor &x) const { return linear(x, w, b); }
     // relu(this(x)) as one record (linear_relu)
-    Tensor relu_of(const Tensor &x) const { return linear_relu(x, w, b); }
+    Tensor relu_of(const Tensor &x) const { return dev().per_op ? relu(linear(x, w, b)) : linear_relu(x, w, b); }
     Tensor w, b;
 };
 class Conv2d : public Module {

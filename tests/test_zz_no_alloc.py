@@ -3,8 +3,10 @@
 Its results must equal om_layernorm_bwd's bit for bit (same kernels, same fixed-order sums, the partials only moved
 into the library's fixed device array), on two calls in a row with the second smaller than the first (the array
 keeps the first call's partials, which the second must not read); it must not allocate device memory (a fresh
-context's first om_layernorm_bwd grows the context scratch, the allocation-free call does not); and a shape whose
-partials exceed the fixed array is refused before anything runs.
+context's first om_layernorm_bwd grows the context scratch, the allocation-free call does not); a shape whose
+partials exceed the fixed array is refused before anything runs; two contexts whose calls run at the same time on
+one GPU (separate streams) each get om_layernorm_bwd's bits, since each holds a slot of its own; and a context that
+finds every slot held by other live contexts is refused until one of them is destroyed.
 """
 import ctypes as C
 
@@ -14,7 +16,9 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 OM_E_ARG = 1
-FIXED_BYTES = 8 << 20  # OM_NOALLOC_SCRATCH_BYTES
+OM_E_STATE = 4
+FIXED_BYTES = 8 << 20  # OM_NOALLOC_SCRATCH_BYTES: one context's slot
+SLOTS = 4  # OM_NOALLOC_SLOTS
 
 
 def _free_bytes():
@@ -92,3 +96,51 @@ def test_noalloc_refuses_partials_beyond_its_array():
         assert np.all(dev.get(dg) == 3.0)
     finally:
         dev.ctx.close()
+
+
+def test_noalloc_contexts_on_one_gpu_do_not_race():
+    from gpu_util import Dev
+    a, b = Dev(), Dev()  # two contexts, two streams, one GPU
+    try:
+        rng = np.random.default_rng(5)
+        rows, cols = 4096, 768
+        ca, cb = _case(a, rng, rows, cols), _case(b, rng, rows, cols)
+        a.ctx.sync()
+        b.ctx.sync()
+        for _ in range(3):  # queued back to back on both streams, so the kernels of the two contexts overlap
+            _run(a, "om_layernorm_bwd_noalloc", ca[0], ca[1][1], rows, cols, 0, 0)
+            _run(b, "om_layernorm_bwd_noalloc", cb[0], cb[1][1], rows, cols, 0, 0)
+        a.ctx.sync()
+        b.ctx.sync()
+        for dev, (bufs, outs) in ((a, ca), (b, cb)):
+            _run(dev, "om_layernorm_bwd", bufs, outs[0], rows, cols, 0, 0)
+            for ref, got in zip(outs[0], outs[1]):
+                assert np.array_equal(dev.get(ref).view(np.uint32), dev.get(got).view(np.uint32))
+    finally:
+        a.ctx.close()
+        b.ctx.close()
+
+
+def test_noalloc_slots_are_per_live_context():
+    from gpu_util import Dev
+    devs = [Dev() for _ in range(SLOTS + 1)]
+    try:
+        rng = np.random.default_rng(9)
+        rows, cols = 64, 384
+        cases = [_case(d, rng, rows, cols) for d in devs]
+        for d, (bufs, outs) in zip(devs[:SLOTS], cases):
+            _run(d, "om_layernorm_bwd_noalloc", bufs, outs[1], rows, cols, 0, 0)
+        last, (bufs, outs) = devs[SLOTS], cases[SLOTS]
+        dg = outs[1][1]
+        before = last.get(dg)
+        st = last.status("om_layernorm_bwd_noalloc", *bufs, *outs[1], rows, cols, 0, 0)
+        assert st == OM_E_STATE and b"slots" in last.ctx.L.om_last_error(last.ctx.h)
+        assert np.array_equal(last.get(dg), before)  # nothing ran
+        devs[0].ctx.close()  # its slot is released
+        _run(last, "om_layernorm_bwd_noalloc", bufs, outs[1], rows, cols, 0, 0)
+        _run(last, "om_layernorm_bwd", bufs, outs[0], rows, cols, 0, 0)
+        for ref, got in zip(outs[0], outs[1]):
+            assert np.array_equal(last.get(ref).view(np.uint32), last.get(got).view(np.uint32))
+    finally:
+        for d in devs[1:]:
+            d.ctx.close()
