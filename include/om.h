@@ -51,6 +51,16 @@ void *om_ctx_stream(om_ctx *ctx);
  * milliseconds (0 when there are none). */
 om_status om_ctx_probe(om_ctx *ctx, int on);
 om_status om_ctx_probe_read(om_ctx *ctx, int *calls, double *mean_ms);
+/* How the GELU epilogues of products (om_linear_gelu_fwd, om_linear_gelu_fwd_slope, om_linear_bwd_dx_gelu) evaluate
+ * erf and exp. OM_GELU_FAST (the default): erfc from the degree-9 Chebyshev fit of Numerical Recipes' erfcc
+ * (fractional error below 1.2e-7) with the hardware reciprocal and exponential; GELU within 1.2e-7 max(1, |x|) of
+ * the exact value and its slope within 2.2e-7, about 35 vector instructions per element, which lets the wide tiles
+ * of the plain products carry the epilogue. OM_GELU_REFERENCE: the reference's polynomials (Transcendental.GeluErf,
+ * Transcendental.cs:252; GeluGradBin, TrainElementwise.cs:59-85), bit for bit, about 180 instructions per element.
+ * om_gelu_fwd and om_gelu_bwd always use the reference's polynomials. A step graph records the mode in force when
+ * it was captured. No counterpart in the reference (whose GELU is the polynomial in both of its modes). */
+enum { OM_GELU_FAST = 0, OM_GELU_REFERENCE = 1 };
+om_status om_ctx_set_gelu(om_ctx *ctx, int mode);
 /* Version of this ABI (major * 100 + minor). */
 int om_abi_version(void);
 

@@ -69,6 +69,9 @@ om_status omt_step(omt_model *m, float *loss);
 om_status omt_set_step_graph(omt_model *m, int on);
 /* 1 when the next omt_step will replay a recorded graph. */
 int omt_step_graph_ready(omt_model *m);
+/* om_ctx_set_gelu on the model's context (OM_GELU_FAST, the default, or OM_GELU_REFERENCE for the reference's GELU
+ * polynomials bit for bit in the feed-forward products' epilogues); a recorded step graph is dropped. */
+om_status omt_set_gelu(omt_model *m, int mode);
 /* ZeroGrad, forward and backward only (gradients are left in the arena). */
 om_status omt_forward_backward(omt_model *m, float *loss);
 /* The same two halves as separate calls, for callers that act between them: omt_forward runs ZeroGrad and the

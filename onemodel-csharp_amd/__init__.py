@@ -31,6 +31,7 @@ _OM_SIGS = {
     "om_last_error": [vp],
     "om_ctx_stream": [vp],
     "om_ctx_probe": [vp, ci],
+    "om_ctx_set_gelu": [vp, ci],
     "om_ctx_probe_read": [vp, C.POINTER(ci), C.POINTER(C.c_double)],
     "om_abi_version": [],
     "om_arena_reserve": [vp, u64, u64],
@@ -203,6 +204,7 @@ class omt_scale(C.Structure):
 _OMT_SIGS = {
     "omt_config_create": ([ci, ci, C.POINTER(omt_scale), C.POINTER(vp)], i32),
     "omt_config_create_records": ([ci, ci, C.POINTER(omt_scale), ci, C.POINTER(vp)], i32),
+    "omt_set_gelu": ([vp, ci], i32),
     "omt_destroy": ([vp], None),
     "omt_last_error": ([vp], C.c_char_p),
     "omt_step": ([vp, C.POINTER(f32)], i32),
@@ -307,6 +309,11 @@ class Model:
         v = f32()
         self._check(self.L.omt_step(self.h, C.byref(v)), "omt_step")
         return v.value
+
+    def set_gelu(self, mode: int):
+        """GELU epilogues of the feed-forward products: 0 fast (default), 1 the reference's polynomials bit for bit
+        (omt_set_gelu)."""
+        self._check(self.L.omt_set_gelu(self.h, int(mode)), "omt_set_gelu")
 
     def set_step_graph(self, on: bool = True):
         """Runs later step() calls from a recorded HIP graph of the step (omt_set_step_graph)."""

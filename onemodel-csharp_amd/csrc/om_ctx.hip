@@ -145,6 +145,14 @@ om_status om_ctx_destroy(om_ctx *ctx) {
     return OM_OK;
 }
 
+om_status om_ctx_set_gelu(om_ctx *ctx, int mode) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, mode == OM_GELU_FAST || mode == OM_GELU_REFERENCE,
+               "om_ctx_set_gelu: mode must be OM_GELU_FAST or OM_GELU_REFERENCE");
+    ctx->gelu_mode = mode;
+    return OM_OK;
+}
+
 om_status om_ctx_probe(om_ctx *ctx, int on) {
     OM_CHECK_CTX(ctx);
     if (on) ctx->probe_n = 0;

@@ -202,9 +202,24 @@ static void launch_general(const Params &p, int batch, bool ta, bool tb, bool ve
 #undef OMG_CASE
 }
 
-// The epilogues only some tile instances carry (G = true): GELU and its backward terms. EPI_RELU, like the bias and
-// the residual, is applied by every instance.
+// The epilogues only some tile instances carry: GELU and its backward terms. EPI_RELU, like the bias and the
+// residual, is applied by every instance. An instance's epilogue family GK is 0 (none of them), 1 (the reference's
+// polynomials: EPI_GELU, EPI_GELU_GRAD, EPI_GELU_SLOPE) or 2 (the same with erf and exp of stated error:
+// EPI_GELU_F, EPI_GELU_GRAD_F, EPI_GELU_SLOPE_F); both families also carry EPI_MUL_AUX (no transcendental).
 static bool gelu_epi(int epi) { return epi != EPI_NONE && epi != EPI_RELU; }
+// 1 or 2: the family the epilogue needs; 3: either (EPI_MUL_AUX); 0: none.
+static int epi_family(int epi) {
+    if (epi == EPI_GELU || epi == EPI_GELU_GRAD || epi == EPI_GELU_SLOPE) return 1;
+    if (epi == EPI_GELU_F || epi == EPI_GELU_GRAD_F || epi == EPI_GELU_SLOPE_F) return 2;
+    return epi == EPI_MUL_AUX ? 3 : 0;
+}
+// The family an instance set GM (bit 0: family 1 instantiated, bit 1: family 2) runs epilogue `epi` with, or -1.
+static int pick_family(int GM, int epi) {
+    const int f = epi_family(epi);
+    if (f == 0) return 0;
+    if (f == 3) return (GM & 2) ? 2 : (GM & 1) ? 1 : -1;
+    return (GM & f) ? f : -1;
+}
 
 // In a tuning build (om::tuning_env), OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for
 // comparisons); otherwise NT tiles with 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
@@ -213,17 +228,28 @@ static bool dma_disabled() {
     return s && s[0] == '0';
 }
 
-// Tile-exact set (om_gemm_x.hpp): NN, NT, TN; GELU epilogue variants (NN / NT only) where G instantiates them.
-template <int BM, int BN, int BKT, bool G>
+// Launches kernel K with the epilogue family gk, instantiating only the families GM holds.
+#define OMG_L(K, NTH, TA_, TB_)                                                                                  \
+    do {                                                                                                         \
+        if constexpr ((GM & 1) != 0)                                                                             \
+            if (gk == 1) {                                                                                       \
+                hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, 1>), dim3(total), dim3(NTH), 0, st, p);         \
+                break;                                                                                           \
+            }                                                                                                    \
+        if constexpr ((GM & 2) != 0)                                                                             \
+            if (gk == 2) {                                                                                       \
+                hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, 2>), dim3(total), dim3(NTH), 0, st, p);         \
+                break;                                                                                           \
+            }                                                                                                    \
+        hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, 0>), dim3(total), dim3(NTH), 0, st, p);                 \
+    } while (0);
+
+// Tile-exact set (om_gemm_x.hpp): NN, NT, TN; GELU epilogue variants (NN / NT only) of the families GM holds.
+template <int BM, int BN, int BKT, int GM>
 static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
-    const bool gelu = gelu_epi(p.epi);
-    if (gelu && (!G || ta)) return false;
-#define OMG_L(K, NTH, TA_, TB_)                                                                                  \
-    if (gelu)                                                                                                    \
-        hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, G>), dim3(total), dim3(NTH), 0, st, p);                 \
-    else                                                                                                         \
-        hipLaunchKernelGGL((gx::K<BM, BN, BKT, TA_, TB_, false>), dim3(total), dim3(NTH), 0, st, p);
+    const int gk = pick_family(GM, p.epi);
+    if (gk < 0 || (gk > 0 && ta)) return false;
     if (!ta && !tb) {
         OMG_L(k_gemm_x, NT, false, false)
     } else if (!ta && tb) {
@@ -234,61 +260,62 @@ static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t s
         if constexpr (BKT == 32) {
             constexpr int lds = 4 * (64 + 3 * (BM + BN) * BKT);
             const unsigned per_cu = (160u << 10) / lds;
-            if (!gelu && !dma_disabled() && total <= per_cu * (unsigned)cus) {
-                hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, false>), dim3(total), dim3(NT), 0, st, p);
+            if (gk == 0 && !dma_disabled() && total <= per_cu * (unsigned)cus) {
+                hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, 0>), dim3(total), dim3(NT), 0, st, p);
                 return true;
             }
         }
         OMG_L(k_gemm_x, NT, false, true)
     } else if (ta && !tb) {
-        hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false, false>), dim3(total), dim3(NT), 0, st, p);
+        hipLaunchKernelGGL((gx::k_gemm_x<BM, BN, BKT, true, false, 0>), dim3(total), dim3(NT), 0, st, p);
     } else {
         return false;
     }
     return true;
 }
 // Eight-wavefront variant (om_gemm_x.hpp, k_gemm_x2).
-template <int BM, int BN, int BKT, bool G>
+template <int BM, int BN, int BKT, int GM>
 static bool launch_x2(const Params &p, int batch, bool ta, bool tb, hipStream_t st) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
-    const bool gelu = gelu_epi(p.epi);
-    if (gelu && (!G || ta)) return false;
+    const int gk = pick_family(GM, p.epi);
+    if (gk < 0 || (gk > 0 && ta)) return false;
     if (!ta && !tb) {
         OMG_L(k_gemm_x2, 2 * NT, false, false)
     } else if (!ta && tb) {
         OMG_L(k_gemm_x2, 2 * NT, false, true)
     } else if (ta && !tb) {
-        hipLaunchKernelGGL((gx::k_gemm_x2<BM, BN, BKT, true, false, false>), dim3(total), dim3(2 * NT), 0, st, p);
+        hipLaunchKernelGGL((gx::k_gemm_x2<BM, BN, BKT, true, false, 0>), dim3(total), dim3(2 * NT), 0, st, p);
     } else {
         return false;
     }
-#undef OMG_L
     return true;
 }
+#undef OMG_L
 
 struct XTile {
     int bm, bn, bkt;
 };
-// Launches tile t; false when t (or its GELU variant) is not instantiated.
+// Launches tile t; false when t (or its variant for the product's epilogue) is not instantiated.
 static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
-    // bkt 33 / 65 select the eight-wavefront variant of the 32 / 64 chunk.
-    if (t.bkt == 33 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 32, true>(p, batch, ta, tb, st);
-    if (t.bkt == 33 && t.bm == 64 && t.bn == 64) return launch_x2<64, 64, 32, true>(p, batch, ta, tb, st);
-    if (t.bkt == 65 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 64, false>(p, batch, ta, tb, st);
-    if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, false>(p, batch, ta, tb, st);
-    if (t.bkt == 33 && t.bm == 128 && t.bn == 96) return launch_x2<128, 96, 32, true>(p, batch, ta, tb, st);
-#define OMG_X(BM, BN, BKT, G) \
-    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, G>(p, batch, ta, tb, st, cus);
-    OMG_X(64, 64, 32, true)
-    OMG_X(64, 96, 32, true)
-    OMG_X(96, 64, 32, false)
-    OMG_X(64, 128, 32, false)
-    OMG_X(128, 64, 32, false)
-    OMG_X(128, 96, 32, true)
-    OMG_X(128, 128, 32, false)
-    OMG_X(64, 64, 64, true)
-    OMG_X(64, 96, 64, false)
-    OMG_X(128, 128, 64, false)
+    // bkt 33 / 65 select the eight-wavefront variant of the 32 / 64 chunk. The last template argument lists the
+    // GELU epilogue families the tile instantiates (bit 0: the reference's polynomials, bit 1: the fast pair).
+    if (t.bkt == 33 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 32, 3>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 64 && t.bn == 64) return launch_x2<64, 64, 32, 1>(p, batch, ta, tb, st);
+    if (t.bkt == 65 && t.bm == 64 && t.bn == 96) return launch_x2<64, 96, 64, 0>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, 2>(p, batch, ta, tb, st);
+    if (t.bkt == 33 && t.bm == 128 && t.bn == 96) return launch_x2<128, 96, 32, 3>(p, batch, ta, tb, st);
+#define OMG_X(BM, BN, BKT, GM) \
+    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, GM>(p, batch, ta, tb, st, cus);
+    OMG_X(64, 64, 32, 3)
+    OMG_X(64, 96, 32, 3)
+    OMG_X(96, 64, 32, 0)
+    OMG_X(64, 128, 32, 2)
+    OMG_X(128, 64, 32, 2)
+    OMG_X(128, 96, 32, 3)
+    OMG_X(128, 128, 32, 2)
+    OMG_X(64, 64, 64, 1)
+    OMG_X(64, 96, 64, 0)
+    OMG_X(128, 128, 64, 0)
 #undef OMG_X
     return false;
 }
@@ -331,10 +358,17 @@ const Tuned kTuned[] = {
     {768, 3072, 4096, true, false, 64, 96, 32, 2},    {2304, 768, 4096, true, false, 64, 96, 32, 2},
 };
 // The same for products with a GELU epilogue (GELU and its slope in the forward, the slope product in the input
-// gradient), whose element-wise tail shifts the best tile.
+// gradient), whose element-wise tail shifts the best tile: the reference's polynomials (family 1) and the slope
+// product beside them ...
 const Tuned kTunedEpi[] = {
     {4096, 1536, 384, false, true, 64, 64, 32, 1},
     {4096, 1536, 384, false, false, 64, 96, 33, 1},
+};
+// ... and the fast pair (family 2) with its slope product, whose shorter tail lets the wide tiles of the plain
+// products through.
+const Tuned kTunedGeluFast[] = {
+    {4096, 1536, 384, false, true, 128, 96, 32, 1},   {4096, 3072, 768, false, true, 64, 96, 32, 1},
+    {4096, 1536, 384, false, false, 64, 96, 33, 1},   {4096, 3072, 768, false, false, 64, 64, 32, 1},
 };
 
 // K length of one split: k / splits rounded up to whole chunks.
@@ -381,10 +415,14 @@ bool x_disabled() {
 //     slices of at least 256 k, with tiles x splits near three workgroups per CU (64 x 96 tiles when N allows);
 //   - otherwise 64 x 96 when N is a multiple of 96 and its tiles fit in one round of the CUs (4096 x 384 becomes
 //     exactly 256 tiles: one per CU), else 64 x 64 (occupancy 4, best once there are several tiles per CU).
-Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, bool epi) {
+Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, int family) {
     Choice best{64, 64, 1, k, 32};
     if (env_override(best, k)) return best;
-    if (batch == 1 && epi)
+    if (batch == 1 && family == 2)
+        for (const Tuned &t : kTunedGeluFast)
+            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
+                return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+    if (batch == 1 && family == 1)
         for (const Tuned &t : kTunedEpi)
             if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
                 return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
@@ -443,12 +481,21 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
                p.sa_outer % 4 == 0 && p.sa_inner % 4 == 0 && p.sb_outer % 4 == 0 && p.sb_inner % 4 == 0;
     bool fast = vec && !(ta && tb) && p.k > 0 && p.m > 32 && p.n > 32 && p.m % 4 == 0 && p.n % 4 == 0 &&
                 p.k % 4 == 0;
+    // The slope product (EPI_MUL_AUX) takes the tiles of the GELU products of the context's mode, so that in either
+    // mode om_linear_bwd_dx_slope of the forward's slope and om_linear_bwd_dx_gelu give the same bits.
+    int fam = epi_family(p.epi);
+    if (fam == 3) fam = ctx->gelu_mode == OM_GELU_REFERENCE ? 1 : 2;
     Choice c = p.k <= 0 ? Choice{64, 64, 1, 1, 16}
-                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus, gelu_epi(p.epi))
+                        : (fast ? choose_fast(p.m, p.n, p.k, batch, ta, tb, ctx->num_cus, fam)
                                 : choose(p.m, p.n, p.k, batch, ctx->num_cus));
-    if (fast && gelu_epi(p.epi)) {  // only some tiles carry the GELU epilogue
+    if (fast && fam == 1) {  // only some tiles carry the reference's GELU polynomials
         const bool ok = ((c.bkt == 32 || c.bkt == 33) && c.bm == 64 && (c.bn == 64 || c.bn == 96)) ||
                         (c.bkt == 64 && c.bm == 64 && c.bn == 64);
+        if (!ok) c = with_splits(64, 64, 32, p.k, c.splits);
+    } else if (fast && fam == 2) {  // the fast pair and the slope product: the tiles of dispatch_x's list
+        const bool ok = (c.bkt == 32 && ((c.bm == 64 && (c.bn == 64 || c.bn == 96 || c.bn == 128)) ||
+                                         (c.bm == 128 && (c.bn == 64 || c.bn == 96 || c.bn == 128)))) ||
+                        (c.bkt == 33 && ((c.bm == 64 && c.bn == 96) || (c.bm == 128 && (c.bn == 96 || c.bn == 128))));
         if (!ok) c = with_splits(64, 64, 32, p.k, c.splits);
     }
     bool use_x = fast && !x_disabled() && x_fits(XTile{c.bm, c.bn, c.bkt}, p, c.splits, c.k_split);
@@ -1402,7 +1449,7 @@ om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const 
     OM_REQUIRE(ctx, x && w && h && a && rows >= 0 && in > 0 && out > 0, "om_linear_gelu_fwd: bad arguments");
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, h, out);
     p.bias = b;
-    p.epi = omg::EPI_GELU;
+    p.epi = ctx->gelu_mode == OM_GELU_REFERENCE ? omg::EPI_GELU : omg::EPI_GELU_F;
     p.out2 = a;
     p.ld2 = out;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd");
@@ -1415,7 +1462,7 @@ om_status om_linear_gelu_fwd_slope(om_ctx *ctx, const float *x, const float *w, 
                "om_linear_gelu_fwd_slope: bad arguments");
     omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, a, out);
     p.bias = b;
-    p.epi = omg::EPI_GELU_SLOPE;
+    p.epi = ctx->gelu_mode == OM_GELU_REFERENCE ? omg::EPI_GELU_SLOPE : omg::EPI_GELU_SLOPE_F;
     p.out2 = s;
     p.ld2 = out;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_gelu_fwd_slope");
@@ -1473,7 +1520,7 @@ om_status om_linear_bwd_dx_gelu(om_ctx *ctx, const float *g, const float *w, con
     OM_CHECK_CTX(ctx);
     OM_REQUIRE(ctx, g && w && h && dh && rows >= 0 && in > 0 && out > 0, "om_linear_bwd_dx_gelu: bad arguments");
     omg::Params p = omg::dense_params(rows, in, out, g, out, w, in, dh, in);
-    p.epi = omg::EPI_GELU_GRAD;
+    p.epi = ctx->gelu_mode == OM_GELU_REFERENCE ? omg::EPI_GELU_GRAD : omg::EPI_GELU_GRAD_F;
     p.aux = h;
     p.ldaux = in;
     return omg::launch_dense(ctx, p, false, false, 1, "om_linear_bwd_dx_gelu");

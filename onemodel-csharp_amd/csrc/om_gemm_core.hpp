@@ -78,7 +78,11 @@ struct Params {
     int db_acc;
 };
 
-enum { EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4, EPI_RELU = 5 };
+enum {
+    EPI_NONE = 0, EPI_GELU = 1, EPI_GELU_GRAD = 2, EPI_GELU_SLOPE = 3, EPI_MUL_AUX = 4, EPI_RELU = 5,
+    // EPI_GELU, EPI_GELU_GRAD and EPI_GELU_SLOPE with erf and exp of stated error (omd::gelu_and_slope_fast)
+    EPI_GELU_F = 6, EPI_GELU_GRAD_F = 7, EPI_GELU_SLOPE_F = 8
+};
 
 // Several products launched together (the grouped weight-gradient kernel and its reduce): product i owns workgroups
 // [start[i], start[i+1]) of the GEMM launch, float4 quads [qstart[i], qstart[i+1]) and bias rows
@@ -127,6 +131,15 @@ __device__ __forceinline__ void epilogue(const Params &p, float *cbase, int64_t 
             v = a;
         } else if (p.epi == EPI_MUL_AUX) {
             v = omd::canon(v * p.aux[(int64_t)row * p.ldaux + col]);
+        } else if (p.epi == EPI_GELU_F) {
+            p.out2[(int64_t)row * p.ld2 + col] = omd::gelu_fast(v);
+        } else if (p.epi == EPI_GELU_GRAD_F) {
+            v = omd::gelu_grad_fast(v, p.aux[(int64_t)row * p.ldaux + col]);
+        } else if (p.epi == EPI_GELU_SLOPE_F) {
+            float a, s;
+            omd::gelu_and_slope_fast(v, a, s);
+            p.out2[(int64_t)row * p.ld2 + col] = s;
+            v = a;
         }
     }
     float *dst = cbase + (int64_t)row * ldc + col;

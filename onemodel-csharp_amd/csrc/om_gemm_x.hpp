@@ -159,7 +159,7 @@ struct ColSum {
 // and column l16 of the block, mapped back through the interleaving of R-layout operands. Every operand the epilogue
 // reads (bias, residual, GELU input, mask, the old C) is gathered into registers first, in runs of independent loads,
 // and the arithmetic follows in the reference's order: alpha, mask, bias, residual, GELU, then accumulate.
-template <int TM, int TN, bool AK, bool BKL, bool GELU>
+template <int TM, int TN, bool AK, bool BKL, int GK>
 __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&acc)[TM][TN], float *C,
                                               const float *mask, int m0, int n0, int wm0, int wn0, int l16, int kl,
                                               int split) {
@@ -229,7 +229,7 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
 #pragma unroll
                 for (int j = 0; j < TN; j++) v[r][j] = v[r][j] > 0.0f ? v[r][j] : (v[r][j] == v[r][j] ? 0.0f : v[r][j]);
         }
-        if constexpr (GELU) {
+        if constexpr (GK == 1) {  // the reference's polynomials
             if (p.epi == EPI_GELU) {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
@@ -251,7 +251,33 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
                         p.out2[(int64_t)rowv[r] * p.ld2 + colv[j]] = s;
                         v[r][j] = a;
                     }
-            } else if (p.epi == EPI_MUL_AUX) {
+            }
+        } else if constexpr (GK == 2) {  // erf and exp of stated error (omd::gelu_and_slope_fast)
+            if (p.epi == EPI_GELU_F) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) p.out2[(int64_t)rowv[r] * p.ld2 + colv[j]] = omd::gelu_fast(v[r][j]);
+            } else if (p.epi == EPI_GELU_GRAD_F) {
+                gather(p.aux, p.ldaux);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) v[r][j] = omd::gelu_grad_fast(v[r][j], t[r][j]);
+            } else if (p.epi == EPI_GELU_SLOPE_F) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        float a, s;
+                        omd::gelu_and_slope_fast(v[r][j], a, s);
+                        p.out2[(int64_t)rowv[r] * p.ld2 + colv[j]] = s;
+                        v[r][j] = a;
+                    }
+            }
+        }
+        if constexpr (GK != 0) {
+            if (p.epi == EPI_MUL_AUX) {
                 gather(p.aux, p.ldaux);
 #pragma unroll
                 for (int r = 0; r < 4; r++)
@@ -275,7 +301,7 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
 
 // One tile (tm, tn) of batch-and-split index zz, by one workgroup of NT threads: the body of k_gemm_x and of the
 // grouped weight-gradient kernel.
-template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU>
+template <int BM, int BN, int BKT, bool TA, bool TB, int GK>
 __device__ __forceinline__ void gemm_x_tile(const Params &p, int tm, int tn, int zz) {
     constexpr bool AK = !TA, BKL = TB;  // operands in K layout
     constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
@@ -391,14 +417,14 @@ __device__ __forceinline__ void gemm_x_tile(const Params &p, int tm, int tn, int
 
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
-    tile_epilogue<TM, TN, AK, BKL, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
+    tile_epilogue<TM, TN, AK, BKL, GK>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
 }
 
-template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
+template <int BM, int BN, int BKT, bool TA, bool TB, int GK = 0>
 __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
     int tm, tn, zz;
     tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
-    gemm_x_tile<BM, BN, BKT, TA, TB, GELU>(p, tm, tn, zz);
+    gemm_x_tile<BM, BN, BKT, TA, TB, GK>(p, tm, tn, zz);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -434,7 +460,7 @@ __device__ __forceinline__ void dma_chunk(const float *src, int64_t ld, unsigned
     }
 }
 
-template <int BM, int BN, int BKT, bool GELU>
+template <int BM, int BN, int BKT, int GK>
 __device__ __forceinline__ void gemm_xd_tile(const Params &p, int tm, int tn, int zz) {
     constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;
     constexpr int SA = BM * BKT, SB = BN * BKT, STAGE = SA + SB;
@@ -516,14 +542,14 @@ __device__ __forceinline__ void gemm_xd_tile(const Params &p, int tm, int tn, in
 
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
-    tile_epilogue<TM, TN, true, true, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
+    tile_epilogue<TM, TN, true, true, GK>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
 }
 
-template <int BM, int BN, int BKT, bool GELU = false>
+template <int BM, int BN, int BKT, int GK = 0>
 __global__ void __launch_bounds__(NT) k_gemm_xd(Params p) {
     int tm, tn, zz;
     tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
-    gemm_xd_tile<BM, BN, BKT, GELU>(p, tm, tn, zz);
+    gemm_xd_tile<BM, BN, BKT, GK>(p, tm, tn, zz);
 }
 
 // Weight gradients of several products in one launch (om_linear_bwd_dw_group): product i owns the workgroups
@@ -557,7 +583,7 @@ __global__ void __launch_bounds__(NT) k_gemm_x_tn_group(GroupParams g) {
 // blocks between them (group g takes blocks g, g+2, ...), so every SIMD runs two wavefronts of the tile and one's LDS
 // and barrier waits hide behind the other's MFMAs. At the end group 1 hands its partial sums to group 0 through LDS
 // and group 0 adds them (in that fixed order) and runs the epilogue. For products with about one tile per CU.
-template <int BM, int BN, int BKT, bool TA, bool TB, bool GELU = false>
+template <int BM, int BN, int BKT, bool TA, bool TB, int GK = 0>
 __global__ void __launch_bounds__(2 * NT) k_gemm_x2(Params p) {
     constexpr int NTH = 2 * NT;
     constexpr bool AK = !TA, BKL = TB;
@@ -678,7 +704,7 @@ __global__ void __launch_bounds__(2 * NT) k_gemm_x2(Params p) {
 
     float *C = p.c + outer * p.sc_outer + inner * p.sc_inner;
     const float *mask = p.mask ? p.mask + outer * p.mask_outer_stride : nullptr;
-    tile_epilogue<TM, TN, AK, BKL, GELU>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
+    tile_epilogue<TM, TN, AK, BKL, GK>(p, acc, C, mask, m0, n0, wm0, wn0, l16, kl, split);
 }
 
 }  // namespace gx

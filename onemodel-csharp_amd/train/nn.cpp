@@ -1372,6 +1372,13 @@ om_status omt_set_step_graph(omt_model *m, int on) {
     });
 }
 int omt_step_graph_ready(omt_model *m) { return m && m->graph && m->graphable() ? 1 : 0; }
+om_status omt_set_gelu(omt_model *m, int mode) {
+    if (!m) return OM_E_ARG;
+    return guard(m, [&] {
+        check(m->device->ctx(), om_ctx_set_gelu(m->device->ctx(), mode), "om_ctx_set_gelu");
+        m->graph_drop();  // recorded launches carry the old epilogue
+    });
+}
 om_status omt_forward_backward(omt_model *m, float *loss) {
     if (!m) return OM_E_ARG;
     return guard(m, [&] {

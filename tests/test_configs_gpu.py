@@ -63,11 +63,12 @@ def _adam_sensitivity(g_dev, g_or, p_after, lr=1e-3, eps=1e-8):
     return sens + slack
 
 
-def _step_parity(pkg, cfg, sc, per_op):
+def _step_parity(pkg, cfg, sc, per_op, gelu=0):
     from oracle import models
     from oracle import tape as T
     m = pkg.Model(cfg, per_op=per_op, **sc)
     try:
+        m.set_gelu(gelu)
         oc = models.make_config(cfg, sc)
         names = [n for n, _ in m.params()]
         assert len(names) == len(oc.params)
@@ -136,7 +137,7 @@ def _step_parity(pkg, cfg, sc, per_op):
             e = float(np.max(np.abs(after[well] - p.data[well]), initial=0.0)) / pmax
             worst_post = max(worst_post, e)
             assert e <= 1e-5, (names[i], e)
-        print(f"C{cfg} {sc} per_op={per_op}: loss rel {abs(loss_dev - loss_or) / abs(loss_or):.2e}, worst grad "
+        print(f"C{cfg} {sc} per_op={per_op} gelu={gelu}: loss rel {abs(loss_dev - loss_or) / abs(loss_or):.2e}, worst grad "
               f"{worst:.2e}, worst post-step {worst_post:.2e}, elements outside the implied bar {ill_total}/{n_total} "
               f"({100.0 * ill_total / max(n_total, 1):.2f}%), worst step difference / sensitivity bound {worst_sens:.3f}")
     finally:
@@ -151,6 +152,13 @@ def test_config_step_parity(pkg, case):
 @pytest.mark.parametrize("case", PER_OP_CASES, ids=_ids)
 def test_config_step_parity_per_op_records(pkg, case):
     _step_parity(pkg, case[0], case[1], True)
+
+
+@pytest.mark.parametrize("case", [(3, {}), (5, {"batch": 1, "layers": 2})], ids=_ids)
+def test_config_step_parity_reference_gelu(pkg, case):
+    """The feed-forward products with the reference's GELU polynomials in their epilogues (omt_set_gelu,
+    OM_GELU_REFERENCE) instead of the default fast pair."""
+    _step_parity(pkg, case[0], case[1], False, gelu=1)
 
 
 def test_per_op_records_build_the_same_model(pkg):

@@ -219,12 +219,41 @@ def test_linear_dw_group(dev, T, rows, shapes):
             assert scaled(dev.get(DB), db_r + db_r) <= 1e-7
 
 
+OM_GELU_FAST, OM_GELU_REFERENCE = 0, 1
+
+
+def _gelu64(x):
+    """GELU and its slope in double precision (scipy's erfc)."""
+    from scipy.special import erfc
+    x = x.astype(np.float64)
+    cdf = 0.5 * erfc(-x / np.sqrt(2.0))
+    return x * cdf, cdf + x * np.exp(-0.5 * x * x) / np.sqrt(2.0 * np.pi)
+
+
+# The fast pair's stated error (om_ctx_set_gelu): GELU within 1.2e-7 max(1, |x|) and its slope within 2.2e-7 of the
+# exact values for correctly rounded reciprocal and exponential; the hardware's are within 1 ulp, which the bounds
+# below allow for (about 1e-7 more each).
+FAST_GELU_TOL, FAST_SLOPE_TOL = 2.5e-7, 4e-7
+
+
 @pytest.mark.parametrize("rows,inf,outf", [(4096, 384, 1536), (4096, 1536, 384), (256, 64, 192), (100, 36, 20),
                                            (4096, 768, 3072), (4096, 3072, 768), (4096, 768, 768)])
-def test_linear_fused_epilogues(dev, T, rows, inf, outf):
+@pytest.mark.parametrize("mode", [OM_GELU_REFERENCE, OM_GELU_FAST], ids=["reference", "fast"])
+def test_linear_fused_epilogues(dev, T, rows, inf, outf, mode):
     """om_linear_fwd_resid (Linear then the residual Add), om_linear_gelu_fwd (Linear then GELU, keeping the
-    pre-activation) and om_linear_bwd_dx_gelu (GELU's backward of g w): the GEMM part to the GEMM tolerance, the
-    fused element-wise steps bit for bit on the device's own GEMM results."""
+    pre-activation) and om_linear_bwd_dx_gelu (GELU's backward of g w): the GEMM part to the GEMM tolerance; with
+    the reference's polynomials (OM_GELU_REFERENCE) the fused element-wise steps bit for bit on the device's own
+    GEMM results, with the fast pair (OM_GELU_FAST, the default) within its stated error of the exact GELU and
+    slope of those results."""
+    dev.call("om_ctx_set_gelu", mode)
+    try:
+        _fused_epilogues(dev, T, rows, inf, outf, mode)
+    finally:
+        dev.call("om_ctx_set_gelu", OM_GELU_FAST)
+
+
+def _fused_epilogues(dev, T, rows, inf, outf, mode):
+    exact = mode == OM_GELU_REFERENCE
     rng = np.random.default_rng(rows + 3 * inf + outf)
     x, w, b = rnd(rng, rows, inf), rnd(rng, outf, inf, scale=0.1), rnd(rng, outf)
     resid, g = rnd(rng, rows, outf), rnd(rng, rows, outf)
@@ -240,9 +269,13 @@ def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     dev.call("om_linear_gelu_fwd", X, W, Bb, H, A, rows, inf, outf)
     h = dev.get(H)
     assert scaled(h, lin) <= TOL
-    a_ref = np.empty_like(h)
-    T.lib().or_gelu_fwd(T.fp(h), T.fp(a_ref), C.c_int64(h.size))
-    assert np.array_equal(dev.get(A).view(np.uint32), a_ref.view(np.uint32))
+    if exact:
+        a_ref = np.empty_like(h)
+        T.lib().or_gelu_fwd(T.fp(h), T.fp(a_ref), C.c_int64(h.size))
+        assert np.array_equal(dev.get(A).view(np.uint32), a_ref.view(np.uint32))
+    else:
+        a64, _ = _gelu64(h)
+        assert np.all(np.abs(dev.get(A) - a64) <= FAST_GELU_TOL * np.maximum(1.0, np.abs(h)))
     # dh = GELU'(h) * (g w): g [rows, outf] against w [outf, inf] is the backward of a Linear(inf -> outf) whose
     # input went through GELU; here h plays that input, so use a pre-activation of shape [rows, inf].
     hin = rnd(rng, rows, inf, scale=2.0)
@@ -261,9 +294,15 @@ def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     dev.call("om_linear_bwd_dx_slope", G, W, ONES, DA, rows, inf, outf)
     da_dev = dev.get(DA)
     assert scaled(da_dev, da) <= TOL
-    dh_exact = np.empty_like(da_dev)
-    T.lib().or_gelu_bwd(T.fp(da_dev), T.fp(hin), T.fp(dh_exact), C.c_int64(da_dev.size))
-    assert np.array_equal(dev.get(DH).view(np.uint32), dh_exact.view(np.uint32))
+    if exact:
+        dh_exact = np.empty_like(da_dev)
+        T.lib().or_gelu_bwd(T.fp(da_dev), T.fp(hin), T.fp(dh_exact), C.c_int64(da_dev.size))
+        assert np.array_equal(dev.get(DH).view(np.uint32), dh_exact.view(np.uint32))
+    else:
+        # the fast GELU backward of the same product (its tile may differ from the slope product's, so the product
+        # is held to the GEMM tolerance and the slope to its stated error)
+        _, s64 = _gelu64(hin)
+        assert scaled(dev.get(DH), da_dev.astype(np.float64) * s64) <= TOL
     dev.call("om_linear_bwd", G, X, W, DA, None, None, rows, inf, outf, 0, 0, 0)
     assert scaled(dev.get(DA), da) <= TOL
     # The slope pair: the forward's a equals om_linear_gelu_fwd's, its s is GELU's slope at h (GeluGradBin with a unit
@@ -271,14 +310,36 @@ def test_linear_fused_epilogues(dev, T, rows, inf, outf):
     A2, S = dev.empty((rows, outf)), dev.empty((rows, outf))
     dev.call("om_linear_gelu_fwd_slope", X, W, Bb, A2, S, rows, inf, outf)
     assert np.array_equal(dev.get(A2).view(np.uint32), dev.get(A).view(np.uint32))
-    s_ref = np.empty_like(h)
-    T.lib().or_gelu_bwd(T.fp(np.ones_like(h)), T.fp(h), T.fp(s_ref), C.c_int64(h.size))
-    assert np.array_equal(dev.get(S).view(np.uint32), s_ref.view(np.uint32))
-    s_in = np.empty_like(hin)
-    T.lib().or_gelu_bwd(T.fp(np.ones_like(hin)), T.fp(hin), T.fp(s_in), C.c_int64(hin.size))
-    SI, DH2 = dev.put(s_in), dev.empty((rows, inf))
-    dev.call("om_linear_bwd_dx_slope", G, W, SI, DH2, rows, inf, outf)
-    assert np.array_equal(dev.get(DH2).view(np.uint32), dev.get(DH).view(np.uint32))
+    if exact:
+        s_ref = np.empty_like(h)
+        T.lib().or_gelu_bwd(T.fp(np.ones_like(h)), T.fp(h), T.fp(s_ref), C.c_int64(h.size))
+        assert np.array_equal(dev.get(S).view(np.uint32), s_ref.view(np.uint32))
+        s_in = np.empty_like(hin)
+        T.lib().or_gelu_bwd(T.fp(np.ones_like(hin)), T.fp(hin), T.fp(s_in), C.c_int64(hin.size))
+        SI, DH2 = dev.put(s_in), dev.empty((rows, inf))
+        dev.call("om_linear_bwd_dx_slope", G, W, SI, DH2, rows, inf, outf)
+        assert np.array_equal(dev.get(DH2).view(np.uint32), dev.get(DH).view(np.uint32))
+    else:
+        _, s64 = _gelu64(h)
+        assert np.all(np.abs(dev.get(S) - s64) <= FAST_SLOPE_TOL)
+
+
+def test_fast_gelu_pair_accuracy(dev):
+    """The fast pair itself over [-12, 12] (inputs passed through an identity product, which reproduces them
+    exactly): GELU and its slope within the stated error of double-precision values, signs and the tails right."""
+    rows, n = 4096, 64
+    x = np.linspace(-12.0, 12.0, rows * n).astype(np.float32).reshape(rows, n)
+    X, I = dev.put(x), dev.put(np.eye(n, dtype=np.float32))
+    A, S = dev.empty((rows, n)), dev.empty((rows, n))
+    dev.call("om_ctx_set_gelu", OM_GELU_FAST)
+    dev.call("om_linear_gelu_fwd_slope", X, I, None, A, S, rows, n, n)
+    a, s = dev.get(A), dev.get(S)
+    a64, s64 = _gelu64(x)
+    assert np.all(np.abs(a - a64) <= FAST_GELU_TOL * np.maximum(1.0, np.abs(x)))
+    assert np.all(np.abs(s - s64) <= FAST_SLOPE_TOL)
+    assert np.all(a[x > 0] > 0) and np.all(a[x < -1e-3] <= 0)
+    assert np.array_equal(a[x >= 6], x[x >= 6])  # cdf rounds to 1 there
+    assert np.all(np.abs(a[x <= -9]) <= 1e-17)
 
 
 # ------------------------------------------------------------------------------------------------ element-wise
