@@ -63,6 +63,10 @@ enum { OM_GELU_FAST = 0, OM_GELU_REFERENCE = 1 };
 om_status om_ctx_set_gelu(om_ctx *ctx, int mode);
 /* Version of this ABI (major * 100 + minor). */
 int om_abi_version(void);
+/* 1 for a checked build (compiled with -DOM_CHECKED: every kernel's LDS, every om_alloc allocation and the context
+ * scratch handed out filled with 0xFF bytes, a NaN for floats, so results computed from memory nothing wrote turn
+ * into NaN; the reference's Checked configuration, BufferPool.cs:21-22), 0 for the product build. */
+int om_build_checked(void);
 
 /* ---------------------------------------------------------------------------------------------- arena */
 /* Device memory in two regions, in the spirit of the reference's buffer lifetimes (ActivationScope.cs:18-106,
@@ -76,6 +80,10 @@ om_status om_alloc(om_ctx *ctx, int region, uint64_t bytes, void **out);
 om_status om_step_reset(om_ctx *ctx);
 /* Bytes in use and reserved, per region. */
 om_status om_arena_stats(om_ctx *ctx, int region, uint64_t *used, uint64_t *reserved);
+/* Fault injection for callers' out-of-memory handling (no counterpart in the reference): from now on om_alloc in
+ * `region` fails with OM_E_OOM, as if the device were full, when the bytes handed out since the region's last reset
+ * (the step region: om_step_reset) would exceed `bytes`; 0 removes the limit. Nothing else changes. */
+om_status om_arena_set_limit(om_ctx *ctx, int region, uint64_t bytes);
 /* Host<->device copies at step edges (a region is the unit of transfer, ExecutionBackend.cs:8-13). */
 om_status om_upload(om_ctx *ctx, void *dst_device, const void *src_host, uint64_t bytes);
 om_status om_download(om_ctx *ctx, void *dst_host, const void *src_device, uint64_t bytes);

@@ -34,10 +34,12 @@ _OM_SIGS = {
     "om_ctx_set_gelu": [vp, ci],
     "om_ctx_probe_read": [vp, C.POINTER(ci), C.POINTER(C.c_double)],
     "om_abi_version": [],
+    "om_build_checked": [],
     "om_arena_reserve": [vp, u64, u64],
     "om_alloc": [vp, ci, u64, C.POINTER(vp)],
     "om_step_reset": [vp],
     "om_arena_stats": [vp, ci, C.POINTER(u64), C.POINTER(u64)],
+    "om_arena_set_limit": [vp, ci, u64],
     "om_upload": [vp, vp, vp, u64],
     "om_download": [vp, vp, vp, u64],
     "om_copy": [vp, vp, vp, u64],
@@ -146,7 +148,8 @@ _OM_SIGS = {
     "om_attention_fwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, ci, ci, ci, ci, f32],
     "om_attention_bwd_flash": [vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, ci, vp, vp, vp, ci, ci, ci, ci, ci, f32, ci],
 }
-_RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_adam_scalars": None,
+_RESTYPE = {"om_last_error": C.c_char_p, "om_ctx_stream": vp, "om_abi_version": ci, "om_build_checked": ci,
+            "om_adam_scalars": None,
             "om_ctc_tables_bytes": u64,
             "om_linear_small": ci,
             "om_layernorm_bwd_chunks": ci,

@@ -45,43 +45,58 @@ def _run(cmd):
     return r.stdout
 
 
-def build_hip(jobs: int = 8) -> str:
-    os.makedirs(LIB, exist_ok=True)
-    os.makedirs(OBJ, exist_ok=True)
+def _obj_dir(lib: str) -> str:
+    """Object files of one output directory's build (builds into different directories may run at once)."""
+    return OBJ if os.path.abspath(lib) == LIB else os.path.join(OBJ + "_" + os.path.basename(os.path.abspath(lib)))
+
+
+def build_hip(jobs: int = 8, lib: str = LIB, extra=()) -> str:
+    os.makedirs(lib, exist_ok=True)
+    obj = _obj_dir(lib)
+    os.makedirs(obj, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    objs = [os.path.join(OBJ, os.path.basename(s) + ".o") for s in srcs]
+    objs = [os.path.join(obj, os.path.basename(s) + ".o") for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, "-c", so[0], "-o", so[1]]), zip(srcs, objs)))
-    out = os.path.join(LIB, "libom_hip.so")
+        list(ex.map(lambda so: _run([HIPCC, *HIP_FLAGS, *extra, "-c", so[0], "-o", so[1]]), zip(srcs, objs)))
+    out = os.path.join(lib, "libom_hip.so")
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, out)
     return out
 
 
-def build_train() -> str | None:
+def build_train(lib: str = LIB) -> str | None:
     srcs = sorted(glob.glob(os.path.join(TRAIN, "*.cpp")))
     if not srcs:
         return None
-    out = os.path.join(LIB, "libom_train.so")
+    out = os.path.join(lib, "libom_train.so")
     tmp = out + ".tmp"
     rocm_inc = "/opt/rocm/include"
     _run(["g++", *CXX_FLAGS, "-shared", "-I", os.path.join(ROOT, "include"), "-I", rocm_inc, "-o", tmp, *srcs,
-          "-L", LIB, "-lom_hip", "-Wl,-rpath,$ORIGIN"])
+          "-L", lib, "-lom_hip", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, out)
     return out
 
 
-def build_all() -> list[str]:
-    built = [build_hip()]
-    t = build_train()
+def build_all(lib: str = LIB, checked: bool = False) -> list[str]:
+    """Both libraries into `lib`. checked: the checked build (-DOM_CHECKED: LDS, arena allocations and context scratch
+    handed out filled with 0xFF, a NaN for floats), for a test run that flushes out reads of memory nothing wrote."""
+    built = [build_hip(lib=lib, extra=("-DOM_CHECKED",) if checked else ())]
+    t = build_train(lib)
     if t:
         built.append(t)
-    shutil.rmtree(OBJ, ignore_errors=True)
+    shutil.rmtree(_obj_dir(lib), ignore_errors=True)
     return built
 
 
 if __name__ == "__main__":
-    for p in build_all():
+    # python build.py                 the product libraries into lib/
+    # python build.py --checked DIR   the checked build into DIR (copy both files over lib/ to run the tests with it)
+    args = sys.argv[1:]
+    if args[:1] == ["--checked"] and len(args) == 2:
+        out = build_all(os.path.abspath(args[1]), checked=True)
+    else:
+        out = build_all()
+    for p in out:
         print("built", p)
     sys.exit(0)

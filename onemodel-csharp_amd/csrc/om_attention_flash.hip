@@ -62,6 +62,7 @@ __global__ void __launch_bounds__(256) k_flash_fwd(const float *__restrict__ q, 
                                                    int64_t mask_bstride, float *__restrict__ o, int ldo,
                                                    float *__restrict__ stat_m, float *__restrict__ stat_r, int H,
                                                    int L, float c) {
+    OM_LDS_POISON();
     constexpr int DB = D / 16, LDK = D + 4, Q4 = D / 4, PER = kChunk * Q4 / 256;
     static_assert(kChunk * Q4 % 256 == 0, "a chunk is whole rounds of the workgroup");
     __shared__ __attribute__((aligned(16))) float Ks[kChunk * LDK];  // [key][d]
@@ -188,6 +189,7 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
                                                   int64_t mask_bstride, float *__restrict__ o, int ldo,
                                                   float *__restrict__ stat_m, float *__restrict__ stat_r, int H,
                                                   float c) {
+    OM_LDS_POISON();
     constexpr int DB = D / 16, NB = L / 16, LDK = D + 4, LDV = L + 4, Q4 = D / 4, PER = L * Q4 / 256;
     static_assert(L * Q4 % 256 == 0, "K and V are whole rounds of the workgroup");
     __shared__ __attribute__((aligned(16))) float Ks[L * LDK];  // [key][d]
@@ -307,6 +309,7 @@ __global__ void __launch_bounds__(256) k_rows_fwd(const float *__restrict__ q, c
 template <int D>
 __global__ void __launch_bounds__(256) k_flash_delta(const float *__restrict__ g, int ldg, const float *__restrict__ o,
                                                      int ldo, float *__restrict__ delta, int H, int L, int64_t rows) {
+    OM_LDS_POISON();
     const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
     const int sub = threadIdx.x & 15;
     double acc = 0.0;
@@ -332,6 +335,7 @@ __global__ void __launch_bounds__(256, 2) k_flash_bwd(const float *__restrict__ 
                                                    const float *__restrict__ delta, float *dk, float *dv, int ldd,
                                                    float *__restrict__ dq_part, int H, int L, float c, float scale,
                                                    int acc) {
+    OM_LDS_POISON();
     constexpr int DB = D / 16, LDX = D + 4, Q4 = D / 4, PER = kChunk * Q4 / 256;
     constexpr int QSZ = kChunk * LDX > kChunk * LDSC ? kChunk * LDX : kChunk * LDSC;
     __shared__ __attribute__((aligned(16))) float QS[QSZ];            // the chunk's Q [q][d], then dS [q][key]
@@ -497,6 +501,7 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
                                                      float *dk, float *dv, float *dq, int ldd,
                                                      float *__restrict__ dq_part, int H, float c, float scale,
                                                      int acc) {
+    OM_LDS_POISON();
     constexpr int D = 32, LDX = D + 4, NQB = L / 16, Q4 = D / 4, PERK = kChunk * Q4 / 256;
     constexpr int RP = 64, NPH = L / RP, PERP = RP * Q4 / 256;  // queries per phase, phases, float4 per thread
     constexpr int TPQ = 256 / RP, DPT = D / TPQ;  // threads per query and d per thread for delta
@@ -696,6 +701,7 @@ __global__ void __launch_bounds__(256, 3) k_rows_bwd(const float *__restrict__ q
 template <int D>
 __global__ void __launch_bounds__(256) k_flash_dq_reduce(const float *__restrict__ part, int nkb, int64_t rows,
                                                          float *dq, int ldd, int H, int L, int acc) {
+    OM_LDS_POISON();
     constexpr int Q4 = D / 4;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= rows * Q4) return;

@@ -174,6 +174,7 @@ template <int D, int L>
 __global__ void __launch_bounds__(256) k_attn_fwd(const float *__restrict__ q, const float *__restrict__ k,
                                                   const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                   int64_t mask_bstride, float *__restrict__ o, int ldo, float scale) {
+    OM_LDS_POISON();
     constexpr int LDK = D + 4, LDV = L + 4, NB = L / 16, DB = D / 16;
     __shared__ __attribute__((aligned(16))) float Ks[L * LDK];  // [key][d]
     __shared__ __attribute__((aligned(16))) float Vt[D * LDV];  // [d][key]
@@ -284,6 +285,7 @@ __global__ void __launch_bounds__(L * 4) k_attn_bwd(const float *__restrict__ q,
                                                     const float *__restrict__ v, int ld, const float *__restrict__ mask,
                                                     int64_t mask_bstride, const float *__restrict__ g, int ldg,
                                                     float *dq, float *dk, float *dv, int ldd, float scale, int acc) {
+    OM_LDS_POISON();
     constexpr int NTH = L * 4, LDX = D + 4, LDT = L + 4, NB = L / 16;
     __shared__ __attribute__((aligned(16))) float Qs[L * LDX];
     __shared__ __attribute__((aligned(16))) float Ks[L * LDX];
@@ -381,6 +383,7 @@ __global__ void __launch_bounds__(L * 4, 2) k_attn_bwd_q(const float *__restrict
                                                          const float *__restrict__ mask, int64_t mask_bstride,
                                                          const float *__restrict__ g, int ldg, float *dq, float *dk,
                                                          float *dv, int ldd, float scale, int acc) {
+    OM_LDS_POISON();
     constexpr int NTH = L * 4, LDX = D + 4, NB = L / 16, NW = L / 16, QT = 32, LDT = QT + 4, DB = D / 16;
     static_assert(D == 32, "the quarter's dQ is four 16 x 16 blocks");
     static_assert(QT * LDT <= L * LDX / 1 && L * LDT <= L * LDX, "a quarter of P^T fits where V was");

@@ -83,6 +83,7 @@ __device__ __forceinline__ double block_combine(double v, double *sh) {
 
 template <bool INF>
 __global__ void __launch_bounds__(kBlock) k_norm_partial(Segs s, double *__restrict__ part) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     int64_t len;
     bool vec;
@@ -106,6 +107,7 @@ template <bool INF>
 __global__ void __launch_bounds__(kBlock) k_norm_final(const double *__restrict__ part, int64_t nparts,
                                                        float max_norm, float *__restrict__ total,
                                                        float *__restrict__ coef) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     double acc = 0.0;
     for (int64_t i = threadIdx.x; i < nparts; i += kBlock) acc = combine<INF>(acc, part[i]);
@@ -119,6 +121,7 @@ __global__ void __launch_bounds__(kBlock) k_norm_final(const double *__restrict_
 }
 
 __global__ void __launch_bounds__(kBlock) k_scale_segs(Segs s, const float *__restrict__ coef) {
+    OM_LDS_POISON();
     const float c = *coef;
     if (!(c < 1.0f)) return;
     int64_t len;
@@ -144,6 +147,7 @@ __global__ void __launch_bounds__(kBlock) k_scale_segs(Segs s, const float *__re
 __device__ __forceinline__ float clamp_value(float v, float c) { return v > c ? c : v < -c ? -c : v; }
 
 __global__ void __launch_bounds__(kBlock) k_clip_value(Segs s, float c) {
+    OM_LDS_POISON();
     int64_t len;
     bool vec;
     float *g = chunk_of(s, blockIdx.x, len, vec);

@@ -168,6 +168,7 @@ struct LoadConvDx {
 // mode 2: dW partial (A = g_n [Cout][P], B = im2col(x_n)^T, C = ws[n*splits + s] [Cout][Cin*KK], K range split s)
 template <int BM, int BN, int MODE, bool VEC>
 __global__ void __launch_bounds__(NT) k_conv(Params p) {
+    OM_LDS_POISON();
     __shared__ __attribute__((aligned(16))) float As[2 * lds_size<BM, BK, true>()];
     __shared__ __attribute__((aligned(16))) float Bs[2 * lds_size<BN, BK, false>()];
     const int tiles_n = (p.n + BN - 1) / BN, tiles_m = (p.m + BM - 1) / BM;
@@ -219,6 +220,7 @@ __global__ void __launch_bounds__(NT) k_conv(Params p) {
 // four wavefronts the four quarters of the slot range, each in slot order, added in order at the end.
 __global__ void __launch_bounds__(256) k_conv_dw_reduce(const float *__restrict__ ws, int slots, int64_t total,
                                                         float *__restrict__ dw, int acc) {
+    OM_LDS_POISON();
     __shared__ float qs[4][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int64_t e = (int64_t)blockIdx.x * 64 + lane;
@@ -237,6 +239,7 @@ __global__ void __launch_bounds__(256) k_conv_dw_reduce(const float *__restrict_
 }
 // Wt[ci][co*KK + r] = W[co][ci][r]
 __global__ void k_conv_wt(const float *__restrict__ w, float *__restrict__ wt, int cout, int cin, int kk) {
+    OM_LDS_POISON();
     int64_t total = (int64_t)cout * cin * kk, stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
         int r = (int)(e % kk);
@@ -248,6 +251,7 @@ __global__ void k_conv_wt(const float *__restrict__ w, float *__restrict__ wt, i
 // dbias: per (n, co) plane a double sum (a wavefront per plane), then per co the planes in image order
 // (BackwardNn.cs:325-345).
 __global__ void k_conv_db_planes(const float *__restrict__ g, int planes, int plane, double *__restrict__ part) {
+    OM_LDS_POISON();
     int wv = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (wv >= planes) return;
     const float *r = g + (int64_t)wv * plane;
@@ -258,6 +262,7 @@ __global__ void k_conv_db_planes(const float *__restrict__ g, int planes, int pl
 }
 // A wavefront per output channel: lane l adds the planes of images l, l + 64, ... in order, then the fixed butterfly.
 __global__ void k_conv_db_final(const double *__restrict__ part, int n, int cout, float *__restrict__ db, int acc) {
+    OM_LDS_POISON();
     const int co = (int)(((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6), lane = threadIdx.x & 63;
     if (co >= cout) return;  // whole wavefronts leave together
     double s = 0.0;
@@ -346,6 +351,7 @@ Params conv_params(int N, int Cin, int H, int W, int Cout, int KH, int KW, int s
 // a strictly larger value (unless the best is NaN), or the first NaN wins.
 __global__ void k_maxpool_fwd(const float *__restrict__ x, float *__restrict__ y, int32_t *__restrict__ idx, int N,
                               int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW) {
+    OM_LDS_POISON();
     int64_t total = (int64_t)N * C * OH * OW, stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
         int ox = (int)(o % OW);
@@ -379,6 +385,7 @@ __global__ void k_maxpool_fwd(const float *__restrict__ x, float *__restrict__ y
 __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__restrict__ idx, float *__restrict__ dx,
                               int N, int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH,
                               int PW, int acc, const float *__restrict__ relu_y) {
+    OM_LDS_POISON();
     int64_t total = (int64_t)N * C * H * W, stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += stride) {
         int ix = (int)(e % W);
@@ -408,6 +415,7 @@ __global__ void k_maxpool_bwd(const float *__restrict__ g, const int32_t *__rest
 __global__ void k_maxpool_bwd_tiled(const float *__restrict__ g, const int32_t *__restrict__ idx,
                                     float *__restrict__ dx, int planes, int H, int W, int OH, int OW, int KH, int KW,
                                     int acc, const float *__restrict__ relu_y) {
+    OM_LDS_POISON();
     const int total = planes * OH * OW;
     for (int o = blockIdx.x * blockDim.x + threadIdx.x; o < total; o += gridDim.x * blockDim.x) {
         const int ox = o % OW, t = o / OW, oy = t % OH, pl = t / OH;

@@ -118,6 +118,7 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
                                                         const float *__restrict__ bias, float *out, int cin, int cout,
                                                         int H, int W, int R, int ps, int ntile, int acc, int N,
                                                         int nsplit, int cps, float *__restrict__ ws, int relu) {
+    OM_LDS_POISON();
     extern __shared__ __attribute__((aligned(16))) float lds[];
     constexpr int MB = BM / 16, WF4 = 18 * BM, NWI = (WF4 + kThreads - 1) / kThreads, TS = w_tap_stride<BM>();
     float *Ws = lds;           // [9][BM][kWLd], taps TS apart
@@ -234,6 +235,7 @@ __global__ void __launch_bounds__(kThreads) k_conv3_fwd(const float *__restrict_
 // ReLU when relu.
 __global__ void k_conv3_sum(const float *__restrict__ ws, int nsplit, int64_t total, int P, int cout,
                             const float *__restrict__ bias, float *out, int acc, int relu) {
+    OM_LDS_POISON();
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         float v = ws[e];
         for (int s = 1; s < nsplit; s++) v += ws[(int64_t)s * total + e];
@@ -251,6 +253,7 @@ __global__ void k_conv3_sum(const float *__restrict__ ws, int nsplit, int64_t to
 __global__ void k_conv3_sum_pool(const float *__restrict__ ws, int nsplit, int64_t total, int H, int W, int cout,
                                  const float *__restrict__ bias, float *__restrict__ out, float *__restrict__ py,
                                  int32_t *__restrict__ pidx, int kh, int kw, int64_t pooled) {
+    OM_LDS_POISON();
     const int OH = H / kh, OW = W / kw;
     for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < pooled; o += (int64_t)gridDim.x * blockDim.x) {
         const int ox = (int)(o % OW);
@@ -289,6 +292,7 @@ __global__ void __launch_bounds__(kThreads) k_conv3_dw(const float *__restrict__
                                                        float *__restrict__ part, int cin, int cout, int H, int W,
                                                        int R, int ps, int nchunks, int items, int per,
                                                        double *__restrict__ dbp) {
+    OM_LDS_POISON();
     constexpr int NG = kDwCo * kDwPx / 4 / kThreads;
     __shared__ __attribute__((aligned(16))) float Gs[kDwCo * kGLd];
     __shared__ int boff[kDwPx];
@@ -379,6 +383,7 @@ template <int NW>
 __global__ void __launch_bounds__(64 * NW) k_conv3_dw_reduce(const float *__restrict__ part, int slots, int cout,
                                                              int cin, float *dw, int acc,
                                                              const double *__restrict__ dbp, float *db) {
+    OM_LDS_POISON();
     __shared__ float qs[NW][64];
     __shared__ double qd[NW][64];
     const int64_t total = (int64_t)cout * 9 * cin;
@@ -432,6 +437,7 @@ __global__ void __launch_bounds__(64 * NW) k_conv3_dw_reduce(const float *__rest
 __global__ void __launch_bounds__(1024) k_conv3_dw_c1(const float *__restrict__ g, const float *__restrict__ x,
                                                       float *__restrict__ part, int cout, int H, int W, int br,
                                                       int nbands, double *__restrict__ dbp) {
+    OM_LDS_POISON();
     extern __shared__ float xs[];  // [br + 2][W + 2]
     const int n = blockIdx.x / nbands, y0 = (blockIdx.x % nbands) * br, rows = min(br, H - y0), xw = W + 2;
     for (int f = threadIdx.x; f < (br + 2) * xw; f += blockDim.x) {
@@ -523,6 +529,7 @@ constexpr int kC1MaxCout = 128;
 __global__ void __launch_bounds__(256) k_conv3_fwd_c1(const float *__restrict__ x, const float *__restrict__ w,
                                                       const float *__restrict__ bias, float *__restrict__ y, int cout,
                                                       int H, int W, int br, int nbands, int relu) {
+    OM_LDS_POISON();
     extern __shared__ float xs[];  // [br + 2][W + 2]
     __shared__ float ws[kC1MaxCout * 9], bs[kC1MaxCout];
     const int n = blockIdx.x / nbands, y0 = (blockIdx.x % nbands) * br, rows = min(br, H - y0), xw = W + 2;
@@ -570,6 +577,7 @@ __global__ void __launch_bounds__(256) k_conv3_fwd_c1_pool(const float *__restri
                                                            const float *__restrict__ bias, float *__restrict__ a,
                                                            float *__restrict__ py, int32_t *__restrict__ pidx,
                                                            int cout, int H, int W) {
+    OM_LDS_POISON();
     extern __shared__ float xs[];  // [KH + 2][W + 2]
     __shared__ float ws[kC1MaxCout * 9], bs[kC1MaxCout];
     const int OH2 = H / KH, OW2 = W / KW, xw = W + 2;

@@ -185,6 +185,7 @@ __global__ void __launch_bounds__(kBlock) k_ctc_fwd(const float *__restrict__ lp
                                                     const int32_t *__restrict__ tgt_len, int T, int B, int C, int blank,
                                                     int max_ext, double *__restrict__ alpha_ws,
                                                     double *__restrict__ per, int in_lds) {
+    OM_LDS_POISON();
     __shared__ double nll;
     extern __shared__ double tables[];
     int b = blockIdx.x;
@@ -201,6 +202,7 @@ __global__ void __launch_bounds__(kBlock) k_ctc_fwd(const float *__restrict__ lp
 // Reduction in sequence order (CtcLoss.cs:98-125).
 __global__ void k_ctc_reduce(const double *__restrict__ per, const int32_t *__restrict__ tgt_len, int B, int reduction,
                              int zero_inf, float *__restrict__ loss) {
+    OM_LDS_POISON();
     if (threadIdx.x != 0) return;
     double sum = 0.0;
     for (int b = 0; b < B; b++) {
@@ -356,6 +358,7 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd(const float *__restrict__
                                                        float *__restrict__ dlp, int T, int B, int C, int blank,
                                                        int reduction, int max_ext, int acc, double *__restrict__ ws,
                                                        int in_lds) {
+    OM_LDS_POISON();
     __shared__ double nll_s;
     extern __shared__ double tables[];
     const int b = blockIdx.x;
@@ -380,6 +383,7 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_fwd_tables(const float *__res
                                                               const int32_t *__restrict__ tgt_len, int T, int B, int C,
                                                               int blank, int max_ext, double *__restrict__ saved,
                                                               double *__restrict__ per, int in_lds) {
+    OM_LDS_POISON();
     extern __shared__ double tables[];
     const int b = blockIdx.x;
     const int len = in_len[b], L = tgt_len[b];
@@ -412,6 +416,7 @@ __global__ void __launch_bounds__(kBwdBlock) k_ctc_bwd_tables(const float *__res
                                                               int T, int B, int C, int blank, int reduction,
                                                               int max_ext, int acc, const double *__restrict__ saved,
                                                               int in_lds) {
+    OM_LDS_POISON();
     __shared__ double nll_s;
     extern __shared__ double tables[];
     const int b = blockIdx.x;

@@ -59,10 +59,12 @@ static om_status grow(om_ctx *ctx, float *&buf, uint64_t &have, uint64_t bytes, 
     return OM_OK;
 }
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out) {
-    return grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out, "scratch alloc");
+    om_status s = grow(ctx, ctx->scratch, ctx->scratch_bytes, bytes, out, "scratch alloc");
+    return s ? s : poison(ctx, *out, bytes);
 }
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out) {
-    return grow(ctx, ctx->scratch2, ctx->scratch2_bytes, bytes, out, "scratch alloc");
+    om_status s = grow(ctx, ctx->scratch2, ctx->scratch2_bytes, bytes, out, "scratch alloc");
+    return s ? s : poison(ctx, *out, bytes);
 }
 
 }  // namespace om
@@ -95,7 +97,14 @@ void om::probe_end(om_ctx *ctx, int slot) {
 
 extern "C" {
 
-int om_abi_version(void) { return 103; }
+int om_abi_version(void) { return 104; }
+int om_build_checked(void) {
+#ifdef OM_CHECKED
+    return 1;
+#else
+    return 0;
+#endif
+}
 
 om_status om_ctx_create(int device, om_ctx **out) {
     if (!out) return om::fail(nullptr, OM_E_ARG, "om_ctx_create: out is NULL");
@@ -216,6 +225,10 @@ om_status om_alloc(om_ctx *ctx, int region, uint64_t bytes, void **out) {
     om_region &r = ctx->region[region];
     uint64_t need = (bytes + 255) & ~uint64_t(255);
     if (need == 0) need = 256;
+    if (r.limit && r.used + need > r.limit)
+        return om::fail(ctx, OM_E_OOM, "om_alloc: %llu bytes in region %d: over the limit of %llu bytes set by "
+                        "om_arena_set_limit (%llu in use)", (unsigned long long)bytes, region,
+                        (unsigned long long)r.limit, (unsigned long long)r.used);
     while (true) {
         if (r.cur < r.slabs.size()) {
             om_slab &s = r.slabs[r.cur];
@@ -223,7 +236,7 @@ om_status om_alloc(om_ctx *ctx, int region, uint64_t bytes, void **out) {
                 *out = s.base + r.off;
                 r.off += need;
                 r.used += need;
-                return OM_OK;
+                return om::poison(ctx, *out, need);
             }
             if (r.cur + 1 < r.slabs.size()) {  // next slab already exists: move on
                 r.cur++;
@@ -246,6 +259,13 @@ om_status om_step_reset(om_ctx *ctx) {
     r.cur = 0;
     r.off = 0;
     r.used = 0;
+    return OM_OK;
+}
+
+om_status om_arena_set_limit(om_ctx *ctx, int region, uint64_t bytes) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, region == 0 || region == 1, "om_arena_set_limit: bad region %d", region);
+    ctx->region[region].limit = bytes;
     return OM_OK;
 }
 
@@ -288,14 +308,37 @@ om_status om_copy(om_ctx *ctx, void *dst, const void *src, uint64_t bytes) {
 }  // extern "C"
 
 __global__ void k_fill(float *__restrict__ d, float v, int64_t n) {
+    OM_LDS_POISON();
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) d[i] = v;
+}
+__global__ void k_fill_bits(unsigned *__restrict__ d, unsigned v, int64_t n) {
+    OM_LDS_POISON();
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; i < n; i += stride) d[i] = v;
 }
 __global__ void k_zero_bytes(unsigned char *__restrict__ d, int64_t n) {
+    OM_LDS_POISON();
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; i < n; i += stride) d[i] = 0;
+}
+
+om_status om::poison(om_ctx *ctx, void *p, uint64_t bytes) {
+#ifdef OM_CHECKED
+    const int64_t n = (int64_t)(bytes / 4);  // allocations and scratch are 256-byte aligned: whole words
+    if (n > 0)
+        hipLaunchKernelGGL(k_fill_bits, dim3(om::grid1d(n, 256, 8192)), dim3(256), 0, ctx->stream,
+                           static_cast<unsigned *>(p), 0xFFFFFFFFu, n);
+    return OM_LAUNCH_CHECK(ctx, "checked-build poison fill");
+#else
+    (void)ctx;
+    (void)p;
+    (void)bytes;
+    return OM_OK;
+#endif
 }
 
 extern "C" om_status om_fill(om_ctx *ctx, float *dst, float value, int64_t n) {
@@ -326,6 +369,7 @@ namespace {
 // still being read. No system-scope fence: the later nodes read `dev` in stream order, and the host needs only the
 // ack word itself.
 __global__ void k_step_begin(const om_step_block *entry, om_step_block *dev, uint64_t *ack) {
+    OM_LDS_POISON();
     if (threadIdx.x != 0) return;
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     const u32x4 *src = reinterpret_cast<const u32x4 *>(entry);

@@ -37,6 +37,7 @@ struct MulF {
 template <class F, bool ACC>
 __global__ void __launch_bounds__(kBlock) k_map2(const float *__restrict__ a, const float *__restrict__ b,
                                                  float *__restrict__ y, int64_t n, F f) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     int64_t n4 = n >> 2;
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
@@ -62,6 +63,7 @@ __global__ void __launch_bounds__(kBlock) k_map2(const float *__restrict__ a, co
 template <class F, bool ACC>
 __global__ void __launch_bounds__(kBlock) k_map2_scalar(const float *__restrict__ a, const float *__restrict__ b,
                                                         float *__restrict__ y, int64_t n, F f) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float r = f(a[i], b ? b[i] : a[i]);
@@ -91,6 +93,7 @@ om_status map2(om_ctx *ctx, const char *name, const float *a, const float *b, fl
 // (Ops.Layers.cs:715-733): y[r][c] = x[r][c] + b[c], one rounding per element.
 __global__ void __launch_bounds__(kBlock) k_add_rows4(const float4 *__restrict__ x, const float4 *__restrict__ b,
                                                       float4 *__restrict__ y, int64_t n4, int cols4) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n4; i += stride) {
         const float4 v = x[i], w = b[i % cols4];
@@ -99,12 +102,14 @@ __global__ void __launch_bounds__(kBlock) k_add_rows4(const float4 *__restrict__
 }
 __global__ void __launch_bounds__(kBlock) k_add_rows(const float *__restrict__ x, const float *__restrict__ b,
                                                      float *__restrict__ y, int64_t n, int cols) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) y[i] = x[i] + b[i % cols];
 }
 
 __global__ void __launch_bounds__(kBlock) k_axpy(float alpha, const float *__restrict__ s, float *__restrict__ d,
                                                  int64_t n, int overwrite) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float v = alpha == 1.0f ? s[i] : s[i] * alpha;
@@ -118,6 +123,7 @@ __global__ void __launch_bounds__(kBlock) k_axpy(float alpha, const float *__res
 constexpr int kSumBlocks = 1024;
 __global__ void __launch_bounds__(kBlock) k_sum_partial(const float *__restrict__ x, int64_t n,
                                                         double *__restrict__ part) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     double acc = 0.0;
     int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -135,6 +141,7 @@ struct PostTo {
 };
 __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ part, int np, float *__restrict__ out,
                                                   double divisor, PostTo post) {
+    OM_LDS_POISON();
     // Lane l adds part[l], part[l + 64], ... in that order; the loads of a round of 16 are all issued before the
     // first add (the partials were just written on every XCD, so each load waits for memory).
     constexpr int R = 16;
@@ -169,6 +176,7 @@ __global__ void __launch_bounds__(64) k_sum_final(const double *__restrict__ par
 constexpr int kColChunk = 64;
 __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restrict__ g, int rows, int cols,
                                                            double *__restrict__ part) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int col = blockIdx.x * 64 + lane;
@@ -193,6 +201,7 @@ __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restri
 __global__ void __launch_bounds__(256) om_k_chunk_final(const double *__restrict__ part, float *__restrict__ out,
                                                         const double *__restrict__ part2, float *__restrict__ out2,
                                                         int chunks, int cols, int acc) {
+    OM_LDS_POISON();
     int col = (blockIdx.x * 256 + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (col >= 2 * cols || (col >= cols && !part2)) return;
     const double *src = part;
@@ -219,6 +228,7 @@ namespace {
 // otherwise one thread per output (threads along inner read contiguous memory).
 __global__ void __launch_bounds__(kBlock) k_mean_rows(const float *__restrict__ x, float *__restrict__ y, int outer,
                                                       int n) {
+    OM_LDS_POISON();
     int wave = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (wave >= outer) return;
     const float *xr = x + (int64_t)wave * n;
@@ -231,6 +241,7 @@ __global__ void __launch_bounds__(kBlock) k_mean_rows(const float *__restrict__ 
 // order (lane-strided, loads four strides ahead), so the bits equal om_relu_fwd followed by om_mean_axis.
 __global__ void __launch_bounds__(kBlock) k_relu_mean_rows(const float *__restrict__ x, float *__restrict__ y,
                                                            int outer, int n) {
+    OM_LDS_POISON();
     int wave = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (wave >= outer) return;
     const float *xr = x + (int64_t)wave * n;
@@ -251,6 +262,7 @@ __global__ void __launch_bounds__(kBlock) k_relu_mean_rows(const float *__restri
 __global__ void __launch_bounds__(kBlock) k_relu_mean_rows_bwd(const float *__restrict__ g,
                                                                const float *__restrict__ x, float *__restrict__ dx,
                                                                int outer, int n, int acc) {
+    OM_LDS_POISON();
     const int64_t total = (int64_t)outer * n, stride = (int64_t)gridDim.x * kBlock;
     const float fn = (float)n;
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
@@ -260,6 +272,7 @@ __global__ void __launch_bounds__(kBlock) k_relu_mean_rows_bwd(const float *__re
 }
 __global__ void __launch_bounds__(kBlock) k_mean_inner(const float *__restrict__ x, float *__restrict__ y, int outer,
                                                        int n, int inner) {
+    OM_LDS_POISON();
     int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= (int64_t)outer * inner) return;
     int o = (int)(t / inner), i = (int)(t % inner);
@@ -271,6 +284,7 @@ __global__ void __launch_bounds__(kBlock) k_mean_inner(const float *__restrict__
 // (Permute(2, 0, 1) of the mean), and its backward: dx[b][c][h][w] (+)= g[w][b][c] / H (k_mean_axis_bwd's).
 __global__ void __launch_bounds__(kBlock) k_mean_permute_fwd(const float *__restrict__ x, float *__restrict__ y, int B,
                                                              int Cc, int H, int W) {
+    OM_LDS_POISON();
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= (int64_t)B * Cc * W) return;
     const int c = (int)(t % Cc), b = (int)((t / Cc) % B), w = (int)(t / ((int64_t)Cc * B));
@@ -281,6 +295,7 @@ __global__ void __launch_bounds__(kBlock) k_mean_permute_fwd(const float *__rest
 }
 __global__ void __launch_bounds__(kBlock) k_mean_permute_bwd(const float *__restrict__ g, float *__restrict__ dx, int B,
                                                              int Cc, int H, int W, int acc) {
+    OM_LDS_POISON();
     const int64_t total = (int64_t)B * Cc * H * W, stride = (int64_t)gridDim.x * kBlock;
     const float fn = (float)H;
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
@@ -293,6 +308,7 @@ __global__ void __launch_bounds__(kBlock) k_mean_permute_bwd(const float *__rest
 }
 __global__ void __launch_bounds__(kBlock) k_mean_axis_bwd(const float *__restrict__ g, float *__restrict__ dx,
                                                           int outer, int n, int inner, int acc) {
+    OM_LDS_POISON();
     int64_t total = (int64_t)outer * n * inner, stride = (int64_t)gridDim.x * kBlock;
     float fn = (float)n;
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < total; t += stride) {
@@ -303,6 +319,7 @@ __global__ void __launch_bounds__(kBlock) k_mean_axis_bwd(const float *__restric
 }
 __global__ void __launch_bounds__(kBlock) k_mean_all_bwd(const float *__restrict__ g, float *__restrict__ dx,
                                                          int64_t n, int acc) {
+    OM_LDS_POISON();
     float v = g[0] / (float)n;
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) dx[t] = acc ? dx[t] + v : v;
@@ -316,6 +333,7 @@ struct PermDesc {
 };
 __global__ void __launch_bounds__(kBlock) k_permute(const float *__restrict__ x, float *__restrict__ y, int64_t n,
                                                     PermDesc d, int acc) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         int64_t r = i, off = 0;
@@ -334,6 +352,7 @@ __global__ void __launch_bounds__(kBlock) k_permute(const float *__restrict__ x,
 __global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict__ p, const float *__restrict__ t,
                                                         float *__restrict__ diff, int64_t n,
                                                         double *__restrict__ part, float *__restrict__ unit) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     const float dsq = 1.0f / (float)n;
     double acc = 0.0;
@@ -352,6 +371,7 @@ __global__ void __launch_bounds__(kBlock) k_mse_partial(const float *__restrict_
 }
 __global__ void __launch_bounds__(kBlock) k_mse_bwd(const float *__restrict__ gs, const float *__restrict__ diff,
                                                     float *__restrict__ dp, int64_t n, int acc) {
+    OM_LDS_POISON();
     float dsq = gs[0] / (float)n;
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {

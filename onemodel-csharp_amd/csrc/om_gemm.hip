@@ -16,6 +16,7 @@ namespace omg {
 
 template <int BM, int BN, int BKT, bool TA, bool TB, bool VEC>
 __global__ void __launch_bounds__(NT) k_gemm(Params p) {
+    OM_LDS_POISON();
     using LA = typename std::conditional<TA, LoadRContig<BM, BKT, VEC>, LoadKContig<BM, BKT, VEC>>::type;
     using LB = typename std::conditional<TB, LoadKContig<BN, BKT, VEC>, LoadRContig<BN, BKT, VEC>>::type;
     __shared__ __attribute__((aligned(16))) float As[2 * lds_size<BM, BKT, LA::KLAYOUT>()];
@@ -49,6 +50,7 @@ __global__ void __launch_bounds__(NT) k_gemm(Params p) {
 // Adds the split-K partials in split order and applies the epilogue; four consecutive columns per thread. A fused
 // bias gradient's per-split column sums are finished here too (in split order, in double).
 __global__ void k_splitk_reduce(Params p) {
+    OM_LDS_POISON();
     const int64_t total = (int64_t)p.m * p.n;
     const int nq = (p.n + 3) / 4;
     const int64_t quads = (int64_t)p.m * nq;
@@ -126,6 +128,7 @@ __device__ __forceinline__ void reduce_quad(const Params &p, int64_t q) {
 }
 template <int S>
 __global__ void k_splitk_reduce_s(Params p) {
+    OM_LDS_POISON();
     const int64_t quads = (int64_t)p.m * (p.n / 4);
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -138,6 +141,7 @@ __global__ void k_splitk_reduce_s(Params p) {
 // longest chains and are dispatched first), so they run at once instead of one after another in the same threads.
 template <int S>
 __global__ void k_splitk_reduce_group(GroupParams g, int cblocks, int rblocks) {
+    OM_LDS_POISON();
     const int b = blockIdx.x;
     if (b < cblocks) {
         const int64_t w = (int64_t)b * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -728,6 +732,7 @@ template <bool VEC>
 __global__ void __launch_bounds__(256) k_linear_small_fwd(const float *__restrict__ x, const float *__restrict__ w,
                                                           const float *__restrict__ b, const float *__restrict__ resid,
                                                           float *__restrict__ y, int rows, int in, int out) {
+    OM_LDS_POISON();
     constexpr int Q = VEC ? kSmallKC / 4 : kSmallKC;  // load items per staged row and chunk
     constexpr int PER = (kSmallStage * Q + 255) / 256;
     __shared__ __attribute__((aligned(16))) float st[kSmallStage * kSmallLd];
@@ -867,6 +872,7 @@ __global__ void __launch_bounds__(256) k_linear_small_bwd(const float *__restric
                                                           const float *__restrict__ w, float *__restrict__ dx,
                                                           float *__restrict__ dw, float *__restrict__ db, int rows,
                                                           int in, int ax, int aw, int ab) {
+    OM_LDS_POISON();
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (blockIdx.y > 0) {
         dx_rows<OUT>(g, w, dx, rows, in, ax, (blockIdx.y - 1) * kSmallDxRows, i);
@@ -961,6 +967,7 @@ int narrow_chunk(int rows, int in) {
 template <int OUT>
 __global__ void __launch_bounds__(256) k_linear_narrow_dx(const float *__restrict__ g, const float *__restrict__ w,
                                                           float *__restrict__ dx, int rows, int in, int ax) {
+    OM_LDS_POISON();
     dx_rows<OUT>(g, w, dx, rows, in, ax, blockIdx.y * kSmallDxRows, blockIdx.x * 256 + threadIdx.x);
 }
 // part[c][o][i] = sum over the rows of chunk c of g[r][o] x[r][i]: lane l of every wavefront takes column
@@ -973,6 +980,7 @@ template <int OUT>
 __global__ void __launch_bounds__(256) k_linear_narrow_dw(const float *__restrict__ g, const float *__restrict__ x,
                                                           float *__restrict__ part, double *__restrict__ dbp, int rows,
                                                           int in, int chunk) {
+    OM_LDS_POISON();
     constexpr int OP = (OUT + 3) / 4 * 4;  // LDS row stride of g: 16-byte rows
     static_assert(kNarrowSub * OP >= 3 * OUT * 64, "the wavefront sums reuse the g block");
     __shared__ __attribute__((aligned(16))) float gs[kNarrowSub * OP];
@@ -1065,6 +1073,7 @@ __global__ void __launch_bounds__(256) k_linear_narrow_reduce(const float *__res
                                                               const double *__restrict__ dbp, float *__restrict__ dw,
                                                               float *__restrict__ db, int nchunk, int in, int out,
                                                               int aw, int ab) {
+    OM_LDS_POISON();
     static_assert(kNarrowMaxChunks == 64, "the partials of one output load in one round");
     const int64_t n = (int64_t)out * in, t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (t < n) {
@@ -1160,6 +1169,7 @@ __global__ void __launch_bounds__(64 * kMidW) k_linear_mid_fwd(const float *__re
                                                                const float *__restrict__ b,
                                                                const float *__restrict__ resid, float *__restrict__ y,
                                                                int in, int out, int relu) {
+    OM_LDS_POISON();
     __shared__ floatx4 part[kMidW - 1][64];
     const int tb = out / 16, r0 = (blockIdx.x / tb) * 16, o0 = (blockIdx.x % tb) * 16;
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, l16 = lane & 15, kl = lane >> 4;
@@ -1210,6 +1220,7 @@ __global__ void __launch_bounds__(256) k_linear_mid_dw(const float *__restrict__
                                                        const float *__restrict__ x, float *__restrict__ dw,
                                                        float *__restrict__ db, int rows, int in, int out, int nblk,
                                                        int acc_dw, int acc_db) {
+    OM_LDS_POISON();
     auto gv = [&](int64_t at) {
         const float gg = g[at];
         if constexpr (RELU) {

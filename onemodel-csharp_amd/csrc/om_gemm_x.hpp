@@ -422,6 +422,7 @@ __device__ __forceinline__ void gemm_x_tile(const Params &p, int tm, int tn, int
 
 template <int BM, int BN, int BKT, bool TA, bool TB, int GK = 0>
 __global__ void __launch_bounds__(NT) k_gemm_x(Params p) {
+    OM_LDS_POISON();
     int tm, tn, zz;
     tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
     gemm_x_tile<BM, BN, BKT, TA, TB, GK>(p, tm, tn, zz);
@@ -547,6 +548,7 @@ __device__ __forceinline__ void gemm_xd_tile(const Params &p, int tm, int tn, in
 
 template <int BM, int BN, int BKT, int GK = 0>
 __global__ void __launch_bounds__(NT) k_gemm_xd(Params p) {
+    OM_LDS_POISON();
     int tm, tn, zz;
     tile_coords(p, p.n / BN, p.m / BM, tm, tn, zz);
     gemm_xd_tile<BM, BN, BKT, GK>(p, tm, tn, zz);
@@ -556,6 +558,7 @@ __global__ void __launch_bounds__(NT) k_gemm_xd(Params p) {
 // [start[i], start[i+1]) of the XCD-remapped grid, each a (tile, split) of its own Params, run by the same tile body.
 template <int BM, int BN, int BKT>
 __global__ void __launch_bounds__(NT) k_gemm_x_tn_group(GroupParams g) {
+    OM_LDS_POISON();
     int lin = blockIdx.x;
     const int total = gridDim.x;
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
@@ -585,6 +588,7 @@ __global__ void __launch_bounds__(NT) k_gemm_x_tn_group(GroupParams g) {
 // and group 0 adds them (in that fixed order) and runs the epilogue. For products with about one tile per CU.
 template <int BM, int BN, int BKT, bool TA, bool TB, int GK = 0>
 __global__ void __launch_bounds__(2 * NT) k_gemm_x2(Params p) {
+    OM_LDS_POISON();
     constexpr int NTH = 2 * NT;
     constexpr bool AK = !TA, BKL = TB;
     constexpr int TM = BM / 32, TN = BN / 32, NB = BKT / 16;

@@ -3,6 +3,9 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#ifdef OM_CHECKED
+#include <hsa/hsa.h>
+#endif
 
 #include <cstdarg>
 #include <cstddef>
@@ -25,6 +28,7 @@ struct om_region {
     uint64_t off = 0;     // bytes used in slabs[cur]
     uint64_t used = 0;    // bytes handed out in this region since the last reset
     uint64_t default_slab = 0;
+    uint64_t limit = 0;   // om_arena_set_limit: at most this many bytes handed out (0: no limit)
 };
 
 // A max pool that a 3x3 convolution's split-sum pass can do in the same pass: kh x kw windows, stride kh, kw, no
@@ -83,6 +87,30 @@ struct om_graph {
     uint64_t rb_bytes = 0;
 };
 
+// Checked builds (compiled with -DOM_CHECKED; the reference's Checked configuration fills rented memory with 0xFF,
+// "a NaN for floats, so a read of memory nobody wrote is visible", BufferPool.cs:21-22): every workgroup fills its
+// whole LDS allocation (static and dynamic: the dispatch packet's group segment size) with 0xFF before the kernel's
+// own code runs (OM_LDS_POISON, the first statement of every kernel), and om_alloc and the context scratch hand out
+// memory filled with 0xFF, so a value computed from LDS or scratch that nothing wrote in this launch or call becomes
+// NaN. Product builds compile OM_LDS_POISON to nothing.
+#ifdef OM_CHECKED
+__device__ __forceinline__ void om_poison_lds() {
+    const hsa_kernel_dispatch_packet_t *pk = (const hsa_kernel_dispatch_packet_t *)__builtin_amdgcn_dispatch_ptr();
+    const unsigned words = pk->group_segment_size / 4u;
+    const unsigned nt = blockDim.x * blockDim.y * blockDim.z;
+    const unsigned t = threadIdx.x + blockDim.x * (threadIdx.y + blockDim.y * threadIdx.z);
+    typedef __attribute__((address_space(3))) unsigned lds_u32;
+    lds_u32 *lds = reinterpret_cast<lds_u32 *>(static_cast<uintptr_t>(0));  // LDS address 0, not the null pointer
+    for (unsigned i = t; i < words; i += nt) lds[i] = 0xFFFFFFFFu;
+    __syncthreads();
+}
+#define OM_LDS_POISON() om_poison_lds()
+#else
+#define OM_LDS_POISON() \
+    do {                \
+    } while (0)
+#endif
+
 namespace om {
 
 om_status fail(om_ctx *ctx, om_status code, const char *fmt, ...);
@@ -92,6 +120,8 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
 // The same for the second slot (never used by the GEMM engine itself).
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
+// Checked builds: fills [p, p + bytes) with 0xFF on the context's stream (nothing otherwise).
+om_status poison(om_ctx *ctx, void *p, uint64_t bytes);
 // Sets ctx->noalloc_scratch to the device address of the fixed scratch array on ctx->device (the current device),
 // looking it up on the first call for that device only.
 om_status noalloc_init(om_ctx *ctx);

@@ -46,6 +46,7 @@ __global__ void __launch_bounds__(kBlock) k_bn_fwd(const float *__restrict__ x, 
                                                    float *__restrict__ rv, float *__restrict__ y,
                                                    float *__restrict__ mean_out, float *__restrict__ inv_out, int n,
                                                    int c, int plane, int training, float momentum, float eps) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     __shared__ float stat[2];
     const int ch = blockIdx.x;
@@ -96,6 +97,7 @@ __global__ void __launch_bounds__(kBlock) k_bn_bwd(const float *__restrict__ g, 
                                                    const float *__restrict__ inv, float *__restrict__ dx,
                                                    float *__restrict__ dgamma, float *__restrict__ dbeta, int n,
                                                    int c, int plane, int training, int acc_dx, int acc_params) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     const int ch = blockIdx.x;
     const int64_t total = (int64_t)n * plane;
@@ -144,6 +146,7 @@ __device__ __forceinline__ void window(const PoolGeo &q, int oy, int ox, int &y0
 
 __global__ void __launch_bounds__(kBlock) k_avgpool_fwd(const float *__restrict__ x, float *__restrict__ y,
                                                         int64_t planes, PoolGeo q) {
+    OM_LDS_POISON();
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= planes * q.oh * q.ow) return;
     const int ox = (int)(t % q.ow), oy = (int)((t / q.ow) % q.oh);
@@ -159,6 +162,7 @@ __global__ void __launch_bounds__(kBlock) k_avgpool_fwd(const float *__restrict_
 
 __global__ void __launch_bounds__(kBlock) k_avgpool_bwd(const float *__restrict__ g, float *__restrict__ dx,
                                                         int64_t planes, PoolGeo q, int acc) {
+    OM_LDS_POISON();
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= planes * q.h * q.w) return;
     const int xx = (int)(t % q.w), yy = (int)((t / q.w) % q.h);
@@ -181,6 +185,7 @@ __global__ void __launch_bounds__(kBlock) k_avgpool_bwd(const float *__restrict_
 __global__ void __launch_bounds__(kBlock) k_embedding_fwd(const float *__restrict__ table,
                                                           const int32_t *__restrict__ ids, float *__restrict__ y,
                                                           int64_t n_ids, int dim, int rows) {
+    OM_LDS_POISON();
     const int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (t >= n_ids * dim) return;
     const int64_t i = t / dim;
@@ -197,6 +202,7 @@ __global__ void __launch_bounds__(kBlock) k_embedding_fwd(const float *__restric
 __global__ void __launch_bounds__(kBlock) k_embedding_bwd(const float *__restrict__ g, const int32_t *__restrict__ ids,
                                                           float *__restrict__ dtable, int64_t n_ids, int dim,
                                                           int rows, int pad, int acc) {
+    OM_LDS_POISON();
     const int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;  // whole wavefronts leave together
@@ -228,6 +234,7 @@ __global__ void __launch_bounds__(kBlock) k_embedding_bwd(const float *__restric
 __global__ void __launch_bounds__(kBlock) k_embedding_keys(const int32_t *__restrict__ ids, int32_t *__restrict__ key,
                                                            int32_t *__restrict__ pos, int64_t n_ids, int rows,
                                                            int pad) {
+    OM_LDS_POISON();
     const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (i >= n_ids) return;
     const int id = ids[i];
@@ -248,6 +255,7 @@ __global__ void __launch_bounds__(kBlock) k_embedding_bwd_sorted(const float *__
                                                                  const int32_t *__restrict__ pos,
                                                                  float *__restrict__ dtable, int64_t n_ids, int dim,
                                                                  int rows, int acc) {
+    OM_LDS_POISON();
     const int r = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (r >= rows) return;  // whole wavefronts leave together
@@ -275,6 +283,7 @@ __host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
 // Ops.Mul, or the backward's g * mask).
 __global__ void __launch_bounds__(kBlock) k_dropout(const float *__restrict__ in, float *__restrict__ out, int64_t n,
                                                     float p, float scale, uint64_t stream, int acc) {
+    OM_LDS_POISON();
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         const uint64_t bits = mix64(stream + (uint64_t)(i + 1) * 0x9E3779B97F4A7C15ull);

@@ -19,6 +19,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd(const float *__restrict__ x, 
                                                    const float *__restrict__ beta, float *__restrict__ y,
                                                    float *__restrict__ mean_out, float *__restrict__ rstd_out,
                                                    int rows, int cols, float eps) {
+    OM_LDS_POISON();
     int row = (blockIdx.x * kBlock + threadIdx.x) >> 4;
     int t = threadIdx.x & 15;
     if (row >= rows) return;  // whole 16-lane groups leave together
@@ -51,6 +52,7 @@ __global__ void __launch_bounds__(NTH) k_ln_fwd_lds(const float *__restrict__ x,
                                                     const float *__restrict__ beta, float *__restrict__ y,
                                                     float *__restrict__ mean_out, float *__restrict__ rstd_out,
                                                     int rows, int cols, float eps) {
+    OM_LDS_POISON();
     constexpr int NR = NTH / 16;  // rows per block, a 16-lane group each
     extern __shared__ float sh[];  // [NR][cols + 16]
     const int ld = cols + 16, c4 = cols >> 2;
@@ -99,6 +101,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_fwd_w(const float *__restrict__ x
                                                      const float *__restrict__ beta, float *__restrict__ y,
                                                      float *__restrict__ mean_out, float *__restrict__ rstd_out,
                                                      int rows, float eps) {
+    OM_LDS_POISON();
     constexpr int PER = COLS / 16;
     const int row = (blockIdx.x * kBlock + threadIdx.x) >> 4, t = threadIdx.x & 15;
     if (row >= rows) return;  // whole 16-lane groups leave together
@@ -144,6 +147,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd(const float *__restrict__ g, 
                                                    const float *__restrict__ rstd, float *dx, const float *dxin,
                                                    double *__restrict__ part_g, double *__restrict__ part_b, int rows,
                                                    int cols, int rows_per_chunk) {
+    OM_LDS_POISON();
     __shared__ double lds[kBlock / 64][64 * PER];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int r0 = blockIdx.x * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
@@ -224,6 +228,7 @@ __global__ void __launch_bounds__(NW * 64) k_ln_bwd_w(const float *__restrict__ 
                                                      const float *__restrict__ rstd, float *dx, const float *dxin,
                                                      double *__restrict__ part_g, double *__restrict__ part_b,
                                                      int rows) {
+    OM_LDS_POISON();
     constexpr int PER = COLS / 64;
     __shared__ double lds[NW][COLS];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -304,6 +309,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_bwd_dx_wide(const float *__restri
                                                            const float *__restrict__ mean,
                                                            const float *__restrict__ rstd, float *dx,
                                                            const float *dxin, int rows, int cols) {
+    OM_LDS_POISON();
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *xr = x + (int64_t)r * cols, *gr = g + (int64_t)r * cols;
@@ -333,6 +339,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_param_partial_wide(const float *_
                                                                   double *__restrict__ part_g,
                                                                   double *__restrict__ part_b, int rows, int cols,
                                                                   int rows_per_chunk) {
+    OM_LDS_POISON();
     int col = blockIdx.x * kBlock + threadIdx.x;
     if (col >= cols) return;
     int r0 = blockIdx.y * rows_per_chunk, r1 = min(rows, r0 + rows_per_chunk);
@@ -349,6 +356,7 @@ __global__ void __launch_bounds__(kBlock) k_ln_param_partial_wide(const float *_
 
 // Softmax rows, exact flavour (Softmax.cs:70-133): max, e = expNonPositive(x - max), l = Sum16(e), y = e / l.
 __global__ void __launch_bounds__(kBlock) k_softmax_rows(const float *x, float *y, int rows, int cols) {
+    OM_LDS_POISON();
     int row = (blockIdx.x * kBlock + threadIdx.x) >> 4;
     int t = threadIdx.x & 15;
     if (row >= rows) return;
@@ -375,6 +383,7 @@ __global__ void __launch_bounds__(kBlock) k_softmax_rows(const float *x, float *
 __global__ void __launch_bounds__(kBlock) k_softmax_bwd_rows(const float *g, const float *__restrict__ y, float *dx,
                                                              int rows, int cols, float scale, int use_scale,
                                                              int acc) {
+    OM_LDS_POISON();
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *gr = g + (int64_t)r * cols, *yr = y + (int64_t)r * cols;
@@ -393,6 +402,7 @@ __global__ void __launch_bounds__(kBlock) k_softmax_bwd_rows(const float *g, con
 // LogSoftmax rows (Ops.Layers.cs:47-96): max, double sum of exp(x - max), lse = max + log((float)sum).
 __global__ void __launch_bounds__(kBlock) k_logsoftmax_rows(const float *__restrict__ x, float *__restrict__ y,
                                                             int rows, int cols) {
+    OM_LDS_POISON();
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *xr = x + (int64_t)r * cols;
@@ -413,6 +423,7 @@ __global__ void __launch_bounds__(kBlock) k_logsoftmax_rows(const float *__restr
 __global__ void __launch_bounds__(kBlock) k_logsoftmax_bwd_rows(const float *__restrict__ g,
                                                                 const float *__restrict__ y, float *__restrict__ dx,
                                                                 int rows, int cols, int acc) {
+    OM_LDS_POISON();
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *gr = g + (int64_t)r * cols, *yr = y + (int64_t)r * cols;
@@ -440,6 +451,7 @@ struct LossPost {
 __global__ void __launch_bounds__(kBlock) k_nll_fwd(const float *__restrict__ logp, const int32_t *__restrict__ tg,
                                                     float *__restrict__ loss, int32_t *__restrict__ bad, int rows,
                                                     int cols, int mean, int ignore, LossPost post) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     __shared__ int shbad;
     if (threadIdx.x == 0) shbad = 0x7FFFFFFF;
@@ -529,6 +541,7 @@ __device__ __forceinline__ void xent_row(const float *__restrict__ x, float *__r
 __global__ void __launch_bounds__(kBlock) k_xent_fwd_rows(const float *__restrict__ x, const int32_t *__restrict__ tg,
                                                           float *__restrict__ y, float *__restrict__ dx, int rows,
                                                           int cols, int ignore) {
+    OM_LDS_POISON();
     __shared__ int shc[kBlock / 64];
     int c = 0;
     for (int i = threadIdx.x; i < rows; i += kBlock) c += tg[i] != ignore ? 1 : 0;
@@ -548,6 +561,7 @@ __global__ void __launch_bounds__(kBlock) k_xent_fwd_rows(const float *__restric
 // gradient d has -scale at the target; its double row sum is s = -scale (0 for an ignored row); dx = d - exp(y)*s.
 __global__ void __launch_bounds__(kBlock) k_xent_count(const int32_t *__restrict__ tg, int rows, int ignore,
                                                        int *__restrict__ count) {
+    OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     double c = 0.0;
     for (int i = threadIdx.x; i < rows; i += kBlock) c += tg[i] != ignore ? 1.0 : 0.0;
@@ -558,6 +572,7 @@ __global__ void __launch_bounds__(kBlock) k_xent_bwd(const float *__restrict__ g
                                                      const float *__restrict__ y, const int32_t *__restrict__ tg,
                                                      float *__restrict__ dx, int rows, int cols, int mean, int ignore,
                                                      int acc) {
+    OM_LDS_POISON();
     int r = (blockIdx.x * kBlock + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     float g = gs[0];
@@ -579,6 +594,7 @@ __global__ void __launch_bounds__(kBlock) k_xent_bwd(const float *__restrict__ g
 __global__ void __launch_bounds__(kBlock) k_nll_bwd(const float *__restrict__ gs, const int *__restrict__ count,
                                                     const int32_t *__restrict__ tg, float *__restrict__ dx, int rows,
                                                     int cols, int mean, int ignore, int acc) {
+    OM_LDS_POISON();
     const int64_t n = (int64_t)rows * cols, stride = (int64_t)gridDim.x * kBlock;
     const float g = gs[0];
     const int c = count[0];

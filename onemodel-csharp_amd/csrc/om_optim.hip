@@ -45,6 +45,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const fl
                                                  float *__restrict__ vmax, int64_t n, AdamArgs a,
                                                  const float *__restrict__ gs,
                                                  const om_step_block *__restrict__ step) {
+    OM_LDS_POISON();
     if (step) {
         a.lr = step->lr;
         a.step_size = step->step_size;
@@ -82,6 +83,7 @@ __global__ void __launch_bounds__(kBlock) k_adam(float *__restrict__ p, const fl
 __global__ void __launch_bounds__(kBlock) k_sgd(float *__restrict__ p, const float *__restrict__ g,
                                                 float *__restrict__ buf, int64_t n, float lr, float mu, float keep,
                                                 float wd, int nesterov, int first) {
+    OM_LDS_POISON();
     int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
         float gi = g[i];

@@ -179,6 +179,7 @@ constexpr uint64_t kReadbackMax = 64 << 10;
 // Inside a step graph the number is read from seq_dev when the kernel runs.
 __global__ void __launch_bounds__(256) k_readback(char *__restrict__ dst, const char *__restrict__ src, uint64_t n,
                                                   uint64_t *seq_at, uint64_t seq, const uint64_t *seq_dev) {
+    OM_LDS_POISON();
     for (uint64_t i = threadIdx.x; i < n; i += 256)
         __hip_atomic_store(dst + i, src[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __builtin_amdgcn_s_waitcnt(0);

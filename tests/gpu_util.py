@@ -14,7 +14,9 @@ import sys
 import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-PKG_DIR = os.path.join(ROOT, "onemodel-csharp_amd")
+# OM_TEST_PKG_DIR points the tests at another copy of the package (the sanitizer run of tests/test_sanitized_host.py
+# loads a copy whose lib/libom_train.so is built with AddressSanitizer and UndefinedBehaviorSanitizer).
+PKG_DIR = os.environ.get("OM_TEST_PKG_DIR") or os.path.join(ROOT, "onemodel-csharp_amd")
 
 
 def load_pkg():

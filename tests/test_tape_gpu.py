@@ -217,3 +217,63 @@ def test_failed_step_returns_its_staged_batch(pkg):
             assert m.forward_backward() == home
     finally:
         m.close()
+
+
+OM_E_OOM = 2
+OM_REGION_STEP = 1
+
+
+@pytest.mark.parametrize("cfg,sc,frac", [(3, {"batch": 4}, 0.3), (3, {"batch": 4}, 0.97), (4, {"batch": 4}, 0.6),
+                                         (1, {}, 0.5), (5, {"batch": 1, "layers": 1}, 0.9)],
+                         ids=["C3-forward", "C3-backward", "C4", "C1", "C5"])
+def test_out_of_memory_mid_step_leaves_the_training_state_intact(pkg, cfg, sc, frac):
+    """A device allocation that fails in the middle of a step (om_arena_set_limit caps the step region below what the
+    step takes, so om_alloc returns OM_E_OOM there, as on a full device): the step fails with OM_E_OOM; parameters,
+    Adam's moments and the step count are unchanged (the optimizer never ran); with the limit lifted the next step
+    succeeds, and the run equals an undisturbed one bit for bit (the failed step left nothing behind that a later
+    step reads)."""
+    import ctypes as C
+    a, b = pkg.Model(cfg, **sc), pkg.Model(cfg, **sc)
+    try:
+        L = pkg.load_hip()
+        n = len(a.params())
+        assert a.step() == b.step()
+        used = C.c_uint64()
+        assert L.om_arena_stats(b.ctx, OM_REGION_STEP, C.byref(used), None) == 0 and used.value > 0
+        state = [[b.read_param(i, w) for w in (0, 2, 3)] for i in range(n)]
+        assert L.om_arena_set_limit(b.ctx, OM_REGION_STEP, int(used.value * frac)) == 0
+        with pytest.raises(pkg.OmError) as e:
+            b.step()
+        assert e.value.code == OM_E_OOM and "om_arena_set_limit" in str(e.value)
+        assert b.step_count == 1
+        for i in range(n):
+            for w, before in zip((0, 2, 3), state[i]):
+                assert np.array_equal(b.read_param(i, w).view(np.uint32), before.view(np.uint32)), (i, w)
+        assert L.om_arena_set_limit(b.ctx, OM_REGION_STEP, 0) == 0
+        for _ in range(2):
+            assert a.step() == b.step()
+        assert a.step_count == b.step_count == 3
+        for i in range(n):
+            for w in (0, 1, 2, 3):
+                assert np.array_equal(a.read_param(i, w).view(np.uint32), b.read_param(i, w).view(np.uint32)), (i, w)
+    finally:
+        a.close()
+        b.close()
+
+
+def test_checked_build_hands_out_poisoned_memory(pkg):
+    """In a checked build (om_build_checked) a fresh allocation reads as 0xFF bytes (a NaN for floats), so a kernel
+    that computes from memory nothing wrote produces NaN; the product build leaves it as it is."""
+    import ctypes as C
+    L = pkg.load_hip()
+    if not L.om_build_checked():
+        pytest.skip("product build: allocations are not filled")
+    ctx = pkg.Context(0)
+    try:
+        p = C.c_void_p()
+        assert L.om_alloc(ctx.h, OM_REGION_STEP, 4096, C.byref(p)) == 0
+        out = np.zeros(1024, np.uint32)
+        assert L.om_download(ctx.h, out.ctypes.data, p, 4096) == 0
+        assert np.all(out == 0xFFFFFFFF)
+    finally:
+        ctx.close()
