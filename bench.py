@@ -659,6 +659,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time the step without step graphs only")
+    ap.add_argument("--no-per-op", action="store_true",
+                    help="skip the per-op record structure's rate (profiling runs of the fused step alone)")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches a counter run needs (no timing line)")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only the C3 products beside torch.mm (hipBLASLt / rocBLAS), as a markdown table")
@@ -721,10 +723,11 @@ def main():
                           "replayed from a recorded HIP graph (omt_set_step_graph); the results are bit-identical, "
                           "value is the faster of the two"},
     }
-    po = time_per_op(pkg, a.config, a.steps, a.warmup)
-    out["modes"]["per_op"] = po["eager"]
-    out["modes"]["per_op_step_graph"] = po["step_graph"]
-    out["modes"]["per_op_median_ms"] = po["median_ms"]
+    po = None if a.no_per_op else time_per_op(pkg, a.config, a.steps, a.warmup)
+    if po:
+        out["modes"]["per_op"] = po["eager"]
+        out["modes"]["per_op_step_graph"] = po["step_graph"]
+        out["modes"]["per_op_median_ms"] = po["median_ms"]
     out["modes"]["per_op_note"] = ("the reference's own records (omt_config_create_records, OMT_RECORDS_PER_OP): "
                                    "Linear as Reshape/MatMul/Add/Reshape, three q/k/v Linears over weights of their "
                                    "own, Conv2d/Relu/MaxPool2d apart, Mean then Permute, Mse as Sub/Mul/Mean, "
