@@ -46,7 +46,7 @@ def pkg():
 # The reference's own record structure (omt_config_create_records with OMT_RECORDS_PER_OP: Linear as Reshape, MatMul,
 # Add, Reshape; three q/k/v Linears over weights of their own; Conv2d, Relu and MaxPool2d apart; Mean then Permute;
 # Mse as Sub, Mul, Mean; CrossEntropy as LogSoftmax, NllLoss; no grouped weight gradients) against the same oracle.
-PER_OP_CASES = [(1, {}), (2, {"batch": 4}), (2, {}), (3, {}), (4, {"batch": 8}), (4, {}), (5, {})]
+PER_OP_CASES = [(1, {}), (2, {"batch": 4}), (2, {}), (3, {}), (4, {"batch": 8}), (4, {}), (5, {}), (10, {})]
 
 
 def _adam_sensitivity(g_dev, g_or, p_after, lr=1e-3, eps=1e-8):

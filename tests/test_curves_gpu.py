@@ -26,8 +26,8 @@ def pkg():
     return load_pkg()
 
 
-def run_device(pkg, cfg, o, mapping, feed):
-    m = pkg.Model(cfg)
+def run_device(pkg, cfg, o, mapping, feed, per_op=False):
+    m = pkg.Model(cfg, per_op=per_op)
     try:
         names = [n for n, _ in m.params()]
         for p, k in mapping:
@@ -59,29 +59,35 @@ def check_against(losses, final, want_losses, want_params, mapping, noise, loss_
     return rel, worst
 
 
-def test_mlp_sgd_momentum_curve(pkg):
+# per_op: the same curves with the reference's own record structure (omt_config_create_records, OMT_RECORDS_PER_OP)
+PER_OP = pytest.mark.parametrize("per_op", [False, True], ids=["fused", "per_op"])
+
+
+@PER_OP
+def test_mlp_sgd_momentum_curve(pkg, per_op):
     from oracle import models
     o = load_golden("training_mlp")
 
     def feed(m, idx):
         m.write_input("x", o["in.x"][idx])
         m.write_input("labels", o["in.y"][idx].astype(np.int32))
-    losses, _, final, _ = run_device(pkg, 6, o, MLP_MAP, feed)
+    losses, _, final, _ = run_device(pkg, 6, o, MLP_MAP, feed, per_op)
     rel, worst = check_against(losses, final, o["out.loss"], lambda p, k: o["out." + k], MLP_MAP, (), 1e-3, 1e-3)
     assert losses[-1] < losses[0]
     ol, of = models.mlp_curve(o)
     rel_o, worst_o = check_against(losses, final, ol, lambda p, k: of[k], MLP_MAP, (), 1e-5, 1e-5)
-    print(f"mlp: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
+    print(f"mlp per_op={per_op}: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
 
 
-def test_cnn_adamw_cosine_clip_curve(pkg):
+@PER_OP
+def test_cnn_adamw_cosine_clip_curve(pkg, per_op):
     from oracle import models
     o = load_golden("training_cnn")
 
     def feed(m, idx):
         m.write_input("x", o["in.x"][idx])
         m.write_input("labels", o["in.y"][idx].astype(np.int32))
-    losses, norms, final, bufs = run_device(pkg, 7, o, models.CNN_MAP, feed)
+    losses, norms, final, bufs = run_device(pkg, 7, o, models.CNN_MAP, feed, per_op)
     noise = ("0.bias", "4.bias")
     rel, worst = check_against(losses, final, o["out.loss"], lambda p, k: o["out." + k], models.CNN_MAP, noise,
                                1e-3, 1e-3)
@@ -94,10 +100,11 @@ def test_cnn_adamw_cosine_clip_curve(pkg):
     rel_o, worst_o = check_against(losses, final, ol, lambda p, k: of[p], models.CNN_MAP, noise, 1e-5, 1e-5)
     assert float(np.max(np.abs(norms.astype(np.float64) - on) / on)) < 1e-5
     assert scaled(bufs["5.running_var"], ost["rv2"]) < 1e-5 and scaled(bufs["1.running_var"], ost["rv1"]) < 1e-5
-    print(f"cnn: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
+    print(f"cnn per_op={per_op}: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
 
 
-def test_encoder_adam_warmup_curve(pkg):
+@PER_OP
+def test_encoder_adam_warmup_curve(pkg, per_op):
     from oracle import models
     o = load_golden("training_encoder")
     ids = o["in.ids"].astype(np.int32)
@@ -106,13 +113,13 @@ def test_encoder_adam_warmup_curve(pkg):
         m.write_input("ids", ids[idx])
         m.write_input("labels", o["in.y"][idx].astype(np.int32))
     mapping = models.encoder_map()
-    losses, _, final, _ = run_device(pkg, 8, o, mapping, feed)
+    losses, _, final, _ = run_device(pkg, 8, o, mapping, feed, per_op)
     noise = ("attn.k.bias",)
     rel, worst = check_against(losses, final, o["out.loss"], lambda p, k: o["out." + k], mapping, noise, 1e-3, 1e-3)
     assert losses[-1] < losses[0]
     ol, of = models.encoder_curve(o)
     rel_o, worst_o = check_against(losses, final, ol, lambda p, k: of[p], mapping, noise, 1e-5, 1e-5)
-    print(f"encoder: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
+    print(f"encoder per_op={per_op}: vs torch loss {rel:.2e} params {worst:.2e}; vs oracle loss {rel_o:.2e} params {worst_o:.2e}")
 
 
 def test_input_write_rejects_out_of_range_ids(pkg):
