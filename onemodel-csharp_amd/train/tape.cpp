@@ -750,7 +750,12 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
                    OMT(om_attention_bwd_flash(C(), qkv, qkv + W, qkv + 2 * W, 3 * w, md, 1, od, w, st, g, w, dqkv,
                                               dqkv + W, dqkv + 2 * W, 3 * w, B, heads, L, D, 0.0f, 0));
                    int ax, a[6];
-                   float *dx = e.dest(r, 0, &ax);
+                   // x's gradient may already be a residual's gradient another record still holds (a post-LN
+                   // layer's input feeds both the attention and the residual Add): it then goes in as the addend of
+                   // the input-gradient product (dx = addend + dqkv W, the bits of the product added to it), which
+                   // spares a copy of it before the add
+                   const float *dx_add = nullptr;
+                   float *dx = e.dest_add(r, 0, &ax, &dx_add);
                    float *d[6];
                    for (int i = 0; i < 6; i++) d[i] = e.dest(r, 1 + i, &a[i]);
                    // d = {dwq, dbq, dwk, dbk, dwv, dbv}: one dW / db launch when the three leaves' gradients are the
@@ -763,6 +768,10 @@ Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const 
                    const bool any_w = d[0] || d[2] || d[4], any_b = d[1] || d[3] || d[5];
                    float *dw = !any_w ? nullptr : dw_direct ? d[0] : dev().step_floats(3 * WW);
                    float *db = !any_b ? nullptr : db_direct ? d[1] : dev().step_floats(3 * W);
+                   if (dx && dx_add) {
+                       OMT(om_linear_bwd_dx_resid(C(), dqkv, r.inputs[1]->data, dx_add, dx, rows, w, 3 * w));
+                       dx = nullptr;
+                   }
                    if ((!any_w || dw_direct) && (!any_b || db_direct)) {
                        // the packed leaves' gradients directly: the input gradient now, dW and db queued
                        if (dx) OMT(om_linear_bwd(C(), dqkv, r.inputs[0]->data, r.inputs[1]->data, dx, nullptr, nullptr,
