@@ -57,8 +57,8 @@ om_status om_ctx_probe_read(om_ctx *ctx, int *calls, double *mean_ms);
  * the exact value and its slope within 2.2e-7, about 35 vector instructions per element, which lets the wide tiles
  * of the plain products carry the epilogue. OM_GELU_REFERENCE: the reference's polynomials (Transcendental.GeluErf,
  * Transcendental.cs:252; GeluGradBin, TrainElementwise.cs:59-85), bit for bit, about 180 instructions per element.
- * om_gelu_fwd and om_gelu_bwd always use the reference's polynomials. A step graph records the mode in force when
- * it was captured. No counterpart in the reference (whose GELU is the polynomial in both of its modes). */
+ * om_gelu_fwd and om_gelu_bwd follow the same mode. A step graph records the mode in force when it was captured. No
+ * counterpart in the reference (whose GELU is the polynomial in both of its modes). */
 enum { OM_GELU_FAST = 0, OM_GELU_REFERENCE = 1 };
 om_status om_ctx_set_gelu(om_ctx *ctx, int mode);
 /* Version of this ABI (major * 100 + minor). */
@@ -260,7 +260,8 @@ om_status om_mean_permute_fwd(om_ctx *ctx, const float *x, float *y, int B, int 
 om_status om_mean_permute_bwd(om_ctx *ctx, const float *g, float *dx, int B, int C, int H, int W, int accumulate);
 om_status om_relu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n);
 om_status om_relu_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, int64_t n, int accumulate);
-/* Ops.Gelu erf form and GeluGradBin (Ops.Nn.cs:86-112; TrainElementwise.cs:59-85; Transcendental.cs:167-263). */
+/* Ops.Gelu erf form and GeluGradBin (Ops.Nn.cs:86-112; TrainElementwise.cs:59-85; Transcendental.cs:167-263): the
+ * reference's polynomials bit for bit under OM_GELU_REFERENCE, the fast pair of om_ctx_set_gelu otherwise. */
 om_status om_gelu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n);
 om_status om_gelu_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int64_t n, int accumulate);
 /* y = a + b, y = a - b, y = a * b (same shapes; Ops.cs:15-56). */
@@ -299,6 +300,10 @@ om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, floa
 /* ---------------------------------------------------------------------------------------------- reductions */
 /* Ops.Sum / Ops.Mean over all elements in double (Ops.Nn.cs:162-231); *out is a device float. */
 om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mean);
+/* The same, with the result also posted to rb as om_readback_post(rb, out, 4) would post it, by the launch that
+ * finishes the sum (a loss that is a Mean: the step's readback without a copy launch of its own). Waits for rb's
+ * previous post like om_readback_post. */
+om_status om_sum_all_post(om_ctx *ctx, const float *x, float *out, int64_t n, int mean, om_readback *rb);
 /* Mean over the middle axis of [outer, n, inner] (Ops.Nn.cs:186-231) and its backward: dx = g / n broadcast
  * (BackwardNn.cs:145-168). The backward reads g from device memory; g_scalar_index < 0 means g has [outer, inner]
  * values, otherwise it is one scalar at g[0] broadcast to everything (Mean over all elements). */

@@ -80,6 +80,7 @@ _OM_SIGS = {
     "om_xent_fwd_unit": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, vp],
     "om_mse_bwd": [vp, vp, vp, vp, i64, ci],
     "om_sum_all": [vp, vp, vp, i64, ci],
+    "om_sum_all_post": [vp, vp, vp, i64, ci, vp],
     "om_mean_axis": [vp, vp, vp, ci, ci, ci],
     "om_mean_axis_bwd": [vp, vp, vp, ci, ci, ci, ci],
     "om_mean_all_bwd": [vp, vp, vp, i64, ci],

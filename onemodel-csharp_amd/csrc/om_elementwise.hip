@@ -24,6 +24,12 @@ struct GeluF {
 struct GeluGradF {
     __device__ float operator()(float g, float v) const { return omd::gelu_grad(g, v); }
 };
+struct GeluFastF {
+    __device__ float operator()(float x, float) const { return omd::gelu_fast(x); }
+};
+struct GeluGradFastF {
+    __device__ float operator()(float g, float v) const { return omd::gelu_grad_fast(g, v); }
+};
 struct AddF {
     __device__ float operator()(float a, float b) const { return a + b; }
 };
@@ -181,9 +187,18 @@ __global__ void __launch_bounds__(kBlock) k_colsum_partial(const float *__restri
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int col = blockIdx.x * 64 + lane;
     const int r0 = blockIdx.y * kColChunk, r1 = min(rows, r0 + kColChunk);
+    // this lane's rows r0 + w, r0 + w + 4, ...: all loads issued before the first add, then added in that order
+    constexpr int PER = kColChunk / (kBlock / 64);
+    float v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int r = r0 + w + i * (kBlock / 64);
+        v[i] = (col < cols && r < r1) ? g[(int64_t)r * cols + col] : 0.0f;
+    }
     double acc = 0.0;
-    if (col < cols)
-        for (int r = r0 + w; r < r1; r += kBlock / 64) acc += (double)g[(int64_t)r * cols + col];
+#pragma unroll
+    for (int i = 0; i < PER; i++)
+        if (r0 + w + i * (kBlock / 64) < r1) acc += (double)v[i];
     sh[w][lane] = acc;
     __syncthreads();
     if (w == 0 && col < cols) {
@@ -481,10 +496,13 @@ om_status om_relu_bwd(om_ctx *ctx, const float *g, const float *y, float *dx, in
     return map2(ctx, "om_relu_bwd", g, y, dx, n, accumulate, ReluGradF{});
 }
 om_status om_gelu_fwd(om_ctx *ctx, const float *x, float *y, int64_t n) {
+    if (ctx && ctx->gelu_mode != OM_GELU_REFERENCE) return map2(ctx, "om_gelu_fwd", x, nullptr, y, n, 0, GeluFastF{});
     return map2(ctx, "om_gelu_fwd", x, nullptr, y, n, 0, GeluF{});
 }
 om_status om_gelu_bwd(om_ctx *ctx, const float *g, const float *x, float *dx, int64_t n, int accumulate) {
     OM_REQUIRE(ctx, x || n == 0, "om_gelu_bwd: NULL saved input");
+    if (ctx && ctx->gelu_mode != OM_GELU_REFERENCE)
+        return map2(ctx, "om_gelu_bwd", g, x, dx, n, accumulate, GeluGradFastF{});
     return map2(ctx, "om_gelu_bwd", g, x, dx, n, accumulate, GeluGradF{});
 }
 om_status om_add(om_ctx *ctx, const float *a, const float *b, float *y, int64_t n) {
@@ -540,6 +558,24 @@ om_status om_sum_all(om_ctx *ctx, const float *x, float *out, int64_t n, int mea
     hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, out, mean ? (double)n : 0.0,
                        PostTo{nullptr, nullptr, 0});
     return OM_LAUNCH_CHECK(ctx, "om_sum_all");
+}
+
+om_status om_sum_all_post(om_ctx *ctx, const float *x, float *out, int64_t n, int mean, om_readback *rb) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && out && n >= 0 && rb, "om_sum_all_post: bad arguments");
+    float *scr;
+    om_status s = om::scratch(ctx, sizeof(double) * kSumBlocks, &scr);
+    if (s) return s;
+    double *part = reinterpret_cast<double *>(scr);
+    PostTo post{nullptr, nullptr, 0, nullptr};
+    s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq, &post.seq_dev);
+    if (s) return s;
+    int nb = (int)om::grid1d(n, kBlock, kSumBlocks);
+    hipLaunchKernelGGL(k_sum_partial, dim3(nb), dim3(kBlock), 0, ctx->stream, x, n, part);
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, nb, out, mean ? (double)n : 0.0, post);
+    s = OM_LAUNCH_CHECK(ctx, "om_sum_all_post");
+    if (s == OM_OK) om::readback_posted(rb, post.seq, sizeof(float));
+    return s;
 }
 
 om_status om_colsum(om_ctx *ctx, const float *g, float *db, int rows, int cols, int accumulate) {

@@ -346,7 +346,7 @@ struct Tuned {
 };
 const Tuned kTuned[] = {
     // Linear forward y = x W^T (NT)
-    {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 64, 64, 1},
+    {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 128, 32, 1},
     {4096, 384, 1536, false, true, 64, 96, 32, 1},    {4096, 1152, 384, false, true, 64, 96, 32, 1},
     {4096, 768, 768, false, true, 128, 96, 32, 1},    {4096, 3072, 768, false, true, 128, 128, 32, 1},
     {4096, 768, 3072, false, true, 128, 96, 32, 1},   {4096, 2304, 768, false, true, 64, 96, 32, 1},

@@ -495,7 +495,12 @@ Tensor mul(const Tensor &a, const Tensor &b) {
 
 Tensor mean_all(const Tensor &x) {
     Tensor y = make({});
-    OMT(om_sum_all(C(), x->data, y->data, x->numel, 1));
+    if (om_readback *rb = dev().take_loss_post()) {  // the step's loss readback, when this Mean is the loss
+        OMT(om_sum_all_post(C(), x->data, y->data, x->numel, 1, rb));
+        dev().set_loss_posted(y->data);
+    } else {
+        OMT(om_sum_all(C(), x->data, y->data, x->numel, 1));
+    }
     if (tracked({&x})) {
         const int64_t n = x->numel;
         attach(y, "Mean", {x}, [n](Engine &e, Record &r, const float *g) {

@@ -357,12 +357,26 @@ def test_relu_gelu_bit_exact(dev, T):
     T.lib().or_relu_bwd(T.fp(g), T.fp(ry), T.fp(rd), C.c_int64(n))
     dev.call("om_relu_bwd", G, Y, D, n, 0)
     assert np.array_equal(dev.get(D).view(np.uint32), rd.view(np.uint32))
-    T.lib().or_gelu_fwd(T.fp(x), T.fp(ry), C.c_int64(n))
+    dev.call("om_ctx_set_gelu", OM_GELU_REFERENCE)
+    try:  # the reference's polynomials, bit for bit
+        T.lib().or_gelu_fwd(T.fp(x), T.fp(ry), C.c_int64(n))
+        dev.call("om_gelu_fwd", X, Y, n)
+        assert np.array_equal(dev.get(Y).view(np.uint32), ry.view(np.uint32))
+        T.lib().or_gelu_bwd(T.fp(g), T.fp(x), T.fp(rd), C.c_int64(n))
+        dev.call("om_gelu_bwd", G, X, D, n, 0)
+        assert np.array_equal(dev.get(D).view(np.uint32), rd.view(np.uint32))
+    finally:
+        dev.call("om_ctx_set_gelu", OM_GELU_FAST)
+    # the default fast pair: within its stated error, and the reference's special values
     dev.call("om_gelu_fwd", X, Y, n)
-    assert np.array_equal(dev.get(Y).view(np.uint32), ry.view(np.uint32))
-    T.lib().or_gelu_bwd(T.fp(g), T.fp(x), T.fp(rd), C.c_int64(n))
     dev.call("om_gelu_bwd", G, X, D, n, 0)
-    assert np.array_equal(dev.get(D).view(np.uint32), rd.view(np.uint32))
+    y, d = dev.get(Y), dev.get(D)
+    fin = np.isfinite(x)
+    a64, s64 = _gelu64(x[fin])
+    assert np.all(np.abs(y[fin] - a64) <= FAST_GELU_TOL * np.maximum(1.0, np.abs(x[fin])))
+    bound = (FAST_SLOPE_TOL + 1e-7) * np.abs(g[fin]) + 1e-30  # the slope's error plus the product's rounding
+    assert np.all(np.abs(d[fin] - g[fin].astype(np.float64) * s64) <= bound)
+    assert y[x == np.inf][0] == np.inf and y[x == -np.inf][0] == 0.0 and np.isnan(y[np.isnan(x)][0])
 
 
 def test_add_sub_mul_axpy_mean(dev, T):
