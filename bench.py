@@ -624,14 +624,15 @@ def cpu_baseline(cfg: int, seconds: float):
                       f"oracle/tape.py, {tot:.1f} s, OpenMP {threads} threads"}
 
 
-def time_per_op(pkg, cfg, steps, warmup):
+def time_per_op(pkg, cfg, steps, warmup, graph=True):
     """The same configuration built with the reference's own record structure (omt_config_create_records,
     OMT_RECORDS_PER_OP: every rule one C-ABI call when the engine reaches it, no composite records, no colocated q|k|v,
-    no grouped weight gradients), timed like the headline: eager launches, then from a step graph."""
+    no grouped weight gradients), timed like the headline: eager launches, then (unless graph is False) from a step
+    graph."""
     m = pkg.Model(cfg, per_op=True)
     try:
-        out = {}
-        for mode in ("eager", "step_graph"):
+        out = {"step_graph": None}
+        for mode in ("eager", "step_graph") if graph else ("eager",):
             if mode == "step_graph":
                 m.set_step_graph(True)
             for _ in range(warmup):
@@ -723,7 +724,7 @@ def main():
                           "replayed from a recorded HIP graph (omt_set_step_graph); the results are bit-identical, "
                           "value is the faster of the two"},
     }
-    po = None if a.no_per_op else time_per_op(pkg, a.config, a.steps, a.warmup)
+    po = None if a.no_per_op else time_per_op(pkg, a.config, a.steps, a.warmup, graph=not a.no_graph)
     if po:
         out["modes"]["per_op"] = po["eager"]
         out["modes"]["per_op_step_graph"] = po["step_graph"]
