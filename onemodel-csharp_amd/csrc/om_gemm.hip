@@ -398,14 +398,15 @@ bool env_override(Choice &c, int k) {
     c = with_splits(bm, bn, bk, k, sp);
     return true;
 }
-// Tile order of the grouped weight gradients (tuning builds): bands of OM_GROUP_BAND tile rows walked column by column
-// (0: row-major), for comparison runs.
-int group_band() {
+// Tile order of the grouped weight gradients: bands of 8 tile rows walked column by column when the group runs
+// unsplit (C5's layers: 1728 tiles, 517 -> ~490 us per launch, the step 7.37 -> 7.26 ms), row-major when it splits K
+// (C3's four products: banding cut the fetch but slowed the step). Tuning builds read OM_GROUP_BAND (0: row-major).
+int group_band(int splits) {
     static const int b = [] {
         const char *s = om::tuning_env("OM_GROUP_BAND");
-        return s && *s ? atoi(s) : 0;
+        return s && *s ? atoi(s) : -1;
     }();
-    return b;
+    return b >= 0 ? b : (splits == 1 ? 8 : 0);
 }
 bool x_disabled() {
     const char *s = om::tuning_env("OM_GEMM_X");
@@ -622,7 +623,7 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
     const int k_split = rows / splits;
     GroupParams g{};
     g.count = count;
-    g.band = group_band();
+    g.band = group_band(splits);
     uint64_t ws_floats = 0, cs_doubles = 0;
     for (int i = 0; i < count; i++) {
         const om_linear_dw &d = it[i];
