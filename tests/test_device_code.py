@@ -73,3 +73,21 @@ def test_only_the_lds_loads_touch_m0(tmp_path):
                 raise AssertionError(f"{func}: m0 set but not used by the next instruction ({ins})")
             prev = ins
     assert moves == loads and loads > 0, (moves, loads)
+
+
+def test_every_kernel_poisons_its_lds_first():
+    """The checked build fills each workgroup's LDS with 0xFF before the kernel's own code (OM_LDS_POISON), so a read
+    of LDS that nothing wrote yields NaN. That only holds if every kernel starts with the macro."""
+    import glob
+    srcs = sorted(glob.glob(os.path.join(ROOT, "onemodel-csharp_amd", "csrc", "*.hip")) +
+                  glob.glob(os.path.join(ROOT, "onemodel-csharp_amd", "csrc", "*.hpp")))
+    kernels, missing = 0, []
+    for path in srcs:
+        text = open(path).read()
+        for m in re.finditer(r"__global__[^{;]*\{", text):
+            kernels += 1
+            first = text[m.end():].lstrip().split("\n", 1)[0]
+            if not first.startswith("OM_LDS_POISON();"):
+                name = re.findall(r"(\w+)\s*\(", text[m.start():m.end()])
+                missing.append((os.path.basename(path), name[0] if name else "?"))
+    assert kernels > 50 and not missing, missing
