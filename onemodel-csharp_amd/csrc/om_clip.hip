@@ -4,7 +4,8 @@
 //   1. k_norm_partial: one workgroup per 8192-element chunk of a segment writes the chunk's fp64 partial (sum of
 //      squares, or largest |g|) to scratch. Inside a chunk, thread t takes the float4 groups t, t+256, ... in
 //      increasing order and the 256 per-thread values are combined by a fixed butterfly and wave order.
-//   2. k_norm_final: one workgroup sums the partials in chunk order (fixed tree), takes the square root, and writes
+//   2. k_norm_final: one workgroup sums the partials in a fixed order (thread t takes partials t, t+256, ... with
+//      sixteen loads in flight, then the block's fixed tree), takes the square root, and writes
 //      the norm (float) and the clip coefficient min-tested by the consumers: coef = (float)(maxNorm / (norm + 1e-6)),
 //      or 1 when the norm is not finite (the reference scales nothing then).
 //   3. k_scale_segs: every element g *= coef when coef < 1 (skipped by the whole grid otherwise) — or nothing, when the
@@ -110,7 +111,19 @@ __global__ void __launch_bounds__(kBlock) k_norm_final(const double *__restrict_
     OM_LDS_POISON();
     __shared__ double sh[kBlock / 64];
     double acc = 0.0;
-    for (int64_t i = threadIdx.x; i < nparts; i += kBlock) acc = combine<INF>(acc, part[i]);
+    // thread t combines part[t], part[t + 256], ... in that order, sixteen loads in flight before their combines
+    constexpr int R = 16;
+    for (int64_t base = 0; base < nparts; base += (int64_t)kBlock * R) {
+        double v[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            const int64_t i = base + (int64_t)u * kBlock + threadIdx.x;
+            v[u] = i < nparts ? part[i] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++)
+            if (base + (int64_t)u * kBlock + threadIdx.x < nparts) acc = combine<INF>(acc, v[u]);
+    }
     acc = block_combine<INF>(acc, sh);
     if (threadIdx.x == 0) {
         const double norm = INF ? acc : sqrt(acc);
