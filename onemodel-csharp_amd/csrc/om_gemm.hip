@@ -225,11 +225,16 @@ static int pick_family(int GM, int epi) {
     return (GM & f) ? f : -1;
 }
 
-// In a tuning build (om::tuning_env), OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads (for
-// comparisons); otherwise NT tiles with 32-deep chunks run k_gemm_xd, whose chunks load straight into LDS.
+// In a tuning build (om::tuning_env), OM_GEMM_DMA=0 keeps NT products on k_gemm_x's register-staged loads and
+// OM_GEMM_DMA=2 puts every NT product with 32-deep chunks (plain or fast GELU) on k_gemm_xd, whose chunks load
+// straight into LDS, however many rounds its tiles take (for comparisons); otherwise launch_x's rule decides.
 static bool dma_disabled() {
     static const char *s = om::tuning_env("OM_GEMM_DMA");
     return s && s[0] == '0';
+}
+static bool dma_forced() {
+    static const char *s = om::tuning_env("OM_GEMM_DMA");
+    return s && s[0] == '2';
 }
 
 // Launches kernel K with the epilogue family gk, instantiating only the families GM holds.
@@ -250,7 +255,7 @@ static bool dma_disabled() {
 
 // Tile-exact set (om_gemm_x.hpp): NN, NT, TN; GELU epilogue variants (NN / NT only) of the families GM holds.
 template <int BM, int BN, int BKT, int GM>
-static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
+static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus, int dma) {
     const unsigned total = (unsigned)((int64_t)(p.m / BM) * (p.n / BN) * batch * p.splits);
     const int gk = pick_family(GM, p.epi);
     if (gk < 0 || (gk > 0 && ta)) return false;
@@ -259,14 +264,24 @@ static bool launch_x(const Params &p, int batch, bool ta, bool tb, hipStream_t s
     } else if (!ta && tb) {
         // Both operands K-contiguous: chunks load straight into LDS, when the grid fits in one round of the CUs at
         // the occupancy the three LDS stages allow (C3: the 256-tile products gain 7-8 %, the 768-tile q|k|v
-        // projection would lose 14 % to a second round). Not for the GELU epilogues, whose element-wise tail hides
-        // better behind the register-staged kernel's higher occupancy (75 against 81 us for the C3 FFN product).
+        // projection would lose 14 % to a second round), or when the tuned table asks for it (dma): the FFN's first
+        // products and C5's q|k|v projection, several rounds, plain or with the fast GELU pair (3-7 % faster). Not
+        // for the reference's polynomials, whose element-wise tail hides better behind the register-staged kernel's
+        // higher occupancy (75 against 81 us for the C3 FFN product).
         if constexpr (BKT == 32) {
             constexpr int lds = 4 * (64 + 3 * (BM + BN) * BKT);
             const unsigned per_cu = (160u << 10) / lds;
-            if (gk == 0 && !dma_disabled() && total <= per_cu * (unsigned)cus) {
-                hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, 0>), dim3(total), dim3(NT), 0, st, p);
-                return true;
+            const bool want = (gk == 0 && total <= per_cu * (unsigned)cus) || ((dma || dma_forced()) && gk != 1);
+            if (want && !dma_disabled()) {
+                if constexpr ((GM & 2) != 0)
+                    if (gk == 2) {
+                        hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, 2>), dim3(total), dim3(NT), 0, st, p);
+                        return true;
+                    }
+                if (gk == 0) {
+                    hipLaunchKernelGGL((gx::k_gemm_xd<BM, BN, BKT, 0>), dim3(total), dim3(NT), 0, st, p);
+                    return true;
+                }
             }
         }
         OMG_L(k_gemm_x, NT, false, true)
@@ -298,6 +313,7 @@ static bool launch_x2(const Params &p, int batch, bool ta, bool tb, hipStream_t 
 
 struct XTile {
     int bm, bn, bkt;
+    int dma = 0;  // Choice::dma
 };
 // Launches tile t; false when t (or its variant for the product's epilogue) is not instantiated.
 static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool tb, hipStream_t st, int cus) {
@@ -309,7 +325,7 @@ static bool dispatch_x(const XTile &t, const Params &p, int batch, bool ta, bool
     if (t.bkt == 33 && t.bm == 128 && t.bn == 128) return launch_x2<128, 128, 32, 2>(p, batch, ta, tb, st);
     if (t.bkt == 33 && t.bm == 128 && t.bn == 96) return launch_x2<128, 96, 32, 3>(p, batch, ta, tb, st);
 #define OMG_X(BM, BN, BKT, GM) \
-    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, GM>(p, batch, ta, tb, st, cus);
+    if (t.bm == BM && t.bn == BN && t.bkt == BKT) return launch_x<BM, BN, BKT, GM>(p, batch, ta, tb, st, cus, t.dma);
     OMG_X(64, 64, 32, 3)
     OMG_X(64, 96, 32, 3)
     OMG_X(96, 64, 32, 0)
@@ -343,13 +359,14 @@ struct Tuned {
     int m, n, k;
     bool ta, tb;
     int bm, bn, bkt, splits;
+    int dma = 0;  // Choice::dma
 };
 const Tuned kTuned[] = {
     // Linear forward y = x W^T (NT)
-    {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 128, 32, 1},
+    {4096, 384, 384, false, true, 64, 96, 32, 1},     {4096, 1536, 384, false, true, 64, 96, 32, 1, 1},
     {4096, 384, 1536, false, true, 64, 96, 32, 1},    {4096, 1152, 384, false, true, 64, 96, 32, 1},
-    {4096, 768, 768, false, true, 128, 96, 32, 1},    {4096, 3072, 768, false, true, 128, 128, 32, 1},
-    {4096, 768, 3072, false, true, 128, 96, 32, 1},   {4096, 2304, 768, false, true, 64, 96, 32, 1},
+    {4096, 768, 768, false, true, 128, 96, 32, 1},    {4096, 3072, 768, false, true, 128, 128, 32, 1, 1},
+    {4096, 768, 3072, false, true, 128, 96, 32, 1},   {4096, 2304, 768, false, true, 64, 96, 32, 1, 1},
     // input gradient dx = g W (NN); bkt 33 = the eight-wavefront kernel with 32-deep chunks
     {4096, 384, 384, false, false, 64, 96, 33, 1},    {4096, 384, 1536, false, false, 64, 96, 33, 1},
     {4096, 1536, 384, false, false, 64, 64, 33, 1},   {4096, 384, 1152, false, false, 64, 96, 33, 1},
@@ -371,7 +388,7 @@ const Tuned kTunedEpi[] = {
 // ... and the fast pair (family 2) with its slope product, whose shorter tail lets the wide tiles of the plain
 // products through.
 const Tuned kTunedGeluFast[] = {
-    {4096, 1536, 384, false, true, 128, 96, 32, 1},   {4096, 3072, 768, false, true, 64, 96, 32, 1},
+    {4096, 1536, 384, false, true, 64, 96, 32, 1, 1}, {4096, 3072, 768, false, true, 128, 128, 32, 1, 1},
     {4096, 1536, 384, false, false, 64, 96, 33, 1},   {4096, 3072, 768, false, false, 64, 64, 32, 1},
 };
 
@@ -425,16 +442,22 @@ Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, in
     if (env_override(best, k)) return best;
     if (batch == 1 && family == 2)
         for (const Tuned &t : kTunedGeluFast)
-            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
-                return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb) {
+                Choice c = with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+                c.dma = t.dma;
+                return c;
+            }
     if (batch == 1 && family == 1)
         for (const Tuned &t : kTunedEpi)
             if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
                 return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
     if (batch == 1)
         for (const Tuned &t : kTuned)
-            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb)
-                return with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+            if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb) {
+                Choice c = with_splits(t.bm, t.bn, t.bkt, k, t.splits);
+                c.dma = t.dma;
+                return c;
+            }
     const bool n96 = n % 96 == 0 && m >= 64;
     int64_t tiles = (int64_t)((m + 63) / 64) * (n96 ? n / 96 : (n + 63) / 64) * batch;
     // A handful of tiles over a long-enough K (an MLP's first layer: 4 tiles over K = 784) leaves most CUs idle, and
@@ -526,7 +549,7 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
     }
     if (colsum_fused) *colsum_fused = cs;
     hipStream_t st = om::cur_stream(ctx);
-    bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt}, p, batch, ta, tb, st, ctx->num_cus);
+    bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt, c.dma}, p, batch, ta, tb, st, ctx->num_cus);
     if (launched) {
     } else if (fast) {
         if (c.bm == 128 && c.bn == 192) launch_fast<128, 192>(p, batch, ta, tb, st);

@@ -8,6 +8,7 @@ namespace omg {
 // Tile shape and K split chosen from the shape and the CU count only (so results never depend on anything else).
 struct Choice {
     int bm, bn, splits, k_split, bkt;
+    int dma = 0;  // 1: an NT product on the direct-to-LDS kernel even when its tiles take more than one round
 };
 Choice choose(int m, int n, int k, int batch, int cus);
 // A zeroed Params for a single dense product C[m,n] = A[m,k] B[k,n] with the given leading dimensions.
