@@ -386,9 +386,12 @@ const Tuned kTunedEpi[] = {
     {4096, 1536, 384, false, false, 64, 96, 33, 1},
 };
 // ... and the fast pair (family 2) with its slope product, whose shorter tail lets the wide tiles of the plain
-// products through.
+// products through. The forward products run on the direct-to-LDS kernel; their tiles were picked by the step time
+// (C3 0.5304 ms at 64 x 64 against 0.5310 at 64 x 96 and 0.5333 for the register-staged 128 x 96; C5 7.166 ms at
+// 64 x 96 against 7.199 at 128 x 128 and 7.185 register-staged), which ranks them differently from the products
+// timed alone on warm operands.
 const Tuned kTunedGeluFast[] = {
-    {4096, 1536, 384, false, true, 64, 96, 32, 1, 1}, {4096, 3072, 768, false, true, 128, 128, 32, 1, 1},
+    {4096, 1536, 384, false, true, 64, 64, 32, 1, 1}, {4096, 3072, 768, false, true, 64, 96, 32, 1, 1},
     {4096, 1536, 384, false, false, 64, 96, 33, 1},   {4096, 3072, 768, false, false, 64, 64, 32, 1},
 };
 
