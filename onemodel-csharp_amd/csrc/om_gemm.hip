@@ -432,6 +432,27 @@ bool x_disabled() {
     const char *s = om::tuning_env("OM_GEMM_X");
     return s && !strcmp(s, "off");
 }
+// Tuning builds: OM_GEMM_T="m,n,k,ta,tb,family:bm,bn,bkt,splits,dma;..." replaces the tuned choice of the products of
+// exactly that shape and epilogue family (for step-level comparisons of one product's tile).
+struct ShapeOverride {
+    int m, n, k, ta, tb, fam, bm, bn, bkt, splits, dma;
+};
+const std::vector<ShapeOverride> &shape_overrides() {
+    static const std::vector<ShapeOverride> v = [] {
+        std::vector<ShapeOverride> out;
+        const char *s = om::tuning_env("OM_GEMM_T");
+        while (s && *s) {
+            ShapeOverride o{};
+            if (sscanf(s, "%d,%d,%d,%d,%d,%d:%d,%d,%d,%d,%d", &o.m, &o.n, &o.k, &o.ta, &o.tb, &o.fam, &o.bm, &o.bn,
+                       &o.bkt, &o.splits, &o.dma) == 11)
+                out.push_back(o);
+            s = strchr(s, ';');
+            if (s) s++;
+        }
+        return out;
+    }();
+    return v;
+}
 }  // namespace
 
 // Aligned operands: the tuned table for the training path's products, else the rule it was distilled into
@@ -443,6 +464,12 @@ bool x_disabled() {
 Choice choose_fast(int m, int n, int k, int batch, bool ta, bool tb, int cus, int family) {
     Choice best{64, 64, 1, k, 32};
     if (env_override(best, k)) return best;
+    for (const ShapeOverride &o : shape_overrides())
+        if (o.m == m && o.n == n && o.k == k && o.ta == (int)ta && o.tb == (int)tb && o.fam == family && batch == 1) {
+            Choice c = with_splits(o.bm, o.bn, o.bkt, k, o.splits);
+            c.dma = o.dma;
+            return c;
+        }
     if (batch == 1 && family == 2)
         for (const Tuned &t : kTunedGeluFast)
             if (t.m == m && t.n == n && t.k == k && t.ta == ta && t.tb == tb) {
