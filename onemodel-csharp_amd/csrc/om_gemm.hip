@@ -665,6 +665,13 @@ static bool launch_dw_group(om_ctx *ctx, int count, const om_linear_dw *it, int 
     while (splits < 16 && tiles * splits < 6 * (int64_t)ctx->num_cus && rows % (2 * splits * 32) == 0 &&
            rows / (2 * splits) >= 256)
         splits *= 2;
+    if (const char *gx = om::tuning_env("OM_GROUP_X")) {  // tuning builds: OM_GROUP_X="bn,splits" for this launch only
+        int fbn = 0, fsp = 0;
+        if (sscanf(gx, "%d,%d", &fbn, &fsp) == 2 && (fbn == 64 || (fbn == 96 && n96))) {
+            bn = fbn;
+            splits = fsp;
+        }
+    }
     Choice forced{};
     if (env_override(forced, rows)) {  // OM_GEMM_X="64,bn,32,splits" for measurements
         if (forced.bm != 64 || forced.bkt != 32 || (forced.bn != 64 && forced.bn != 96) || (forced.bn == 96 && !n96))
