@@ -296,6 +296,15 @@ om_status om_mse_fwd_unit(om_ctx *ctx, const float *pred, const float *target, f
 om_status om_mse_fwd_post(om_ctx *ctx, const float *pred, const float *target, float *diff, float *loss,
                           float *dpred_unit, int64_t n, om_readback *rb);
 om_status om_mse_bwd(om_ctx *ctx, const float *g_scalar, const float *diff, float *dpred, int64_t n, int accumulate);
+/* An encoder block's last Linear with its residual Add, followed by the MSE loss of its output against target
+ * (Ops.Layers.cs:715-733, Ops.Add, then Losses.Mse, Losses.cs:86-91): y as om_linear_fwd_resid writes it, and the
+ * loss, dpred_unit (and the post to rb when rb is not NULL) as om_mse_fwd_unit / om_mse_fwd_post of that y. The squared
+ * differences are formed and summed in the product's epilogue (fp64 per wavefront, then one launch adds those
+ * partials), so y, dpred_unit and each term are the same bits as the two calls and the loss differs from their
+ * value only in the order of the fp64 additions. No counterpart as one call. */
+om_status om_linear_fwd_resid_mse(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,
+                                  const float *target, float *y, float *dpred_unit, float *loss, int rows, int in,
+                                  int out, om_readback *rb);
 
 /* ---------------------------------------------------------------------------------------------- reductions */
 /* Ops.Sum / Ops.Mean over all elements in double (Ops.Nn.cs:162-231); *out is a device float. */

@@ -50,6 +50,7 @@ _OM_SIGS = {
     "om_linear_small": [ci, ci, ci],
     "om_linear_bwd": [vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, ci, ci, ci],
     "om_linear_fwd_resid": [vp, vp, vp, vp, vp, vp, ci, ci, ci],
+    "om_linear_fwd_resid_mse": [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci, ci, vp],
     "om_linear_relu_fwd": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_linear_bwd_dx_resid": [vp, vp, vp, vp, vp, ci, ci, ci],
     "om_mean_permute_fwd": [vp, vp, vp, ci, ci, ci, ci],

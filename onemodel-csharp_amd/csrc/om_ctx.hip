@@ -97,7 +97,7 @@ void om::probe_end(om_ctx *ctx, int slot) {
 
 extern "C" {
 
-int om_abi_version(void) { return 104; }
+int om_abi_version(void) { return 105; }
 int om_build_checked(void) {
 #ifdef OM_CHECKED
     return 1;

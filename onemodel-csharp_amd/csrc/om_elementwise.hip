@@ -639,3 +639,20 @@ om_status om_mean_all_bwd(om_ctx *ctx, const float *g, float *dx, int64_t n, int
 }
 
 }  // extern "C"
+
+om_status om::mse_of(om_ctx *ctx, const float *pred, const float *target, float *unit, float *loss, int64_t n,
+                     om_readback *rb) {
+    return mse_fwd(ctx, pred, target, nullptr, loss, unit, n, rb);
+}
+
+om_status om::mse_final(om_ctx *ctx, const double *part, int np, float *loss, int64_t n, om_readback *rb) {
+    PostTo post{nullptr, nullptr, 0, nullptr};
+    if (rb) {
+        om_status s = om::readback_target(ctx, rb, sizeof(float), &post.dst, &post.seq_at, &post.seq, &post.seq_dev);
+        if (s) return s;
+    }
+    hipLaunchKernelGGL(k_sum_final, dim3(1), dim3(64), 0, ctx->stream, part, np, loss, (double)n, post);
+    om_status s = OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid_mse");
+    if (s == OM_OK && rb) om::readback_posted(rb, post.seq, sizeof(float));
+    return s;
+}

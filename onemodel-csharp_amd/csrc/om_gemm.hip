@@ -531,8 +531,10 @@ Choice choose(int m, int n, int k, int batch, int cus) {
     return c;
 }
 
-om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what, bool *colsum_fused) {
+om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what, bool *colsum_fused,
+                       int *mse_slots) {
     if (colsum_fused) *colsum_fused = false;
+    if (mse_slots) *mse_slots = 0;
     if (p.m <= 0 || p.n <= 0 || batch <= 0) return OM_OK;
     p.batch = batch;
     bool vec = ((uintptr_t)p.a % 16 == 0) && ((uintptr_t)p.b % 16 == 0) && p.lda % 4 == 0 && p.ldb % 4 == 0 &&
@@ -578,8 +580,16 @@ om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const
         p.ws = reinterpret_cast<float *>(reinterpret_cast<char *>(ws) + cbytes);
     }
     if (colsum_fused) *colsum_fused = cs;
+    // The fused MSE needs the tile-exact epilogue over one split (one workgroup per tile, four wavefronts each).
+    const bool mse = p.mse_t && use_x && p.splits == 1 && batch == 1;
+    if (!mse) {
+        p.mse_t = nullptr;
+        p.mse_unit = nullptr;
+        p.mse_part = nullptr;
+    }
     hipStream_t st = om::cur_stream(ctx);
     bool launched = use_x && dispatch_x(XTile{c.bm, c.bn, c.bkt, c.dma}, p, batch, ta, tb, st, ctx->num_cus);
+    if (mse && launched && mse_slots) *mse_slots = (p.m / c.bm) * (p.n / c.bn) * 4;
     if (launched) {
     } else if (fast) {
         if (c.bm == 128 && c.bn == 192) launch_fast<128, 192>(p, batch, ta, tb, st);
@@ -1513,6 +1523,41 @@ om_status om_linear_fwd_resid(om_ctx *ctx, const float *x, const float *w, const
     p.resid = resid;
     p.ldr = out;
     return omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd_resid");
+}
+
+om_status om_linear_fwd_resid_mse(om_ctx *ctx, const float *x, const float *w, const float *b, const float *resid,
+                                  const float *target, float *y, float *dpred_unit, float *loss, int rows, int in,
+                                  int out, om_readback *rb) {
+    OM_CHECK_CTX(ctx);
+    OM_REQUIRE(ctx, x && w && y && resid && target && dpred_unit && loss && rows > 0 && in > 0 && out > 0,
+               "om_linear_fwd_resid_mse: bad arguments");
+    const int64_t n = (int64_t)rows * out;
+    if (linear_small(rows, in, out) || linear_narrow(rows, in, out)) {  // om_linear_fwd_resid's products
+        launch_small_fwd(om::cur_stream(ctx), x, w, b, resid, y, rows, in, out);
+        om_status s = OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid_mse");
+        return s ? s : om::mse_of(ctx, y, target, dpred_unit, loss, n, rb);
+    }
+    if (launch_mid_fwd(ctx, x, w, b, resid, y, rows, in, out)) {
+        om_status s = OM_LAUNCH_CHECK(ctx, "om_linear_fwd_resid_mse");
+        return s ? s : om::mse_of(ctx, y, target, dpred_unit, loss, n, rb);
+    }
+    // one partial per wavefront of every tile; no tile is smaller than 64 x 64
+    float *scr;
+    om_status s = om::scratch2(ctx, sizeof(double) * 4 * (uint64_t)((rows + 63) / 64) * ((out + 63) / 64), &scr);
+    if (s) return s;
+    omg::Params p = omg::dense_params(rows, out, in, x, in, w, in, y, out);
+    p.bias = b;
+    p.resid = resid;
+    p.ldr = out;
+    p.mse_t = target;
+    p.mse_unit = dpred_unit;
+    p.mse_part = reinterpret_cast<double *>(scr);
+    p.mse_dsq = 1.0f / (float)n;
+    int slots = 0;
+    s = omg::launch_dense(ctx, p, false, true, 1, "om_linear_fwd_resid_mse", nullptr, &slots);
+    if (s) return s;
+    if (slots > 0) return om::mse_final(ctx, reinterpret_cast<const double *>(scr), slots, loss, n, rb);
+    return om::mse_of(ctx, y, target, dpred_unit, loss, n, rb);  // the kernel it took has no such epilogue
 }
 
 om_status om_linear_gelu_fwd(om_ctx *ctx, const float *x, const float *w, const float *b, float *h, float *a, int rows,

@@ -16,8 +16,10 @@ Params dense_params(int m, int n, int k, const float *a, int64_t lda, const floa
                     int64_t ldc);
 // Launches a dense (optionally batched) product; adds the split-K reduce when the chooser splits K.
 // With p.db set on a weight-gradient product (ta, !tb), the bias gradient db (+)= column sums of A is fused into the
-// launch when the chosen kernel supports it; *colsum_fused reports whether it was (else p.db was ignored).
+// launch when the chosen kernel supports it; *colsum_fused reports whether it was (else p.db was ignored). With p.mse_t
+// set, *mse_slots reports the wavefront partials of the fused MSE written to p.mse_part (0: the launch took a kernel
+// without that epilogue, and p.mse_t was ignored).
 om_status launch_dense(om_ctx *ctx, Params p, bool ta, bool tb, int batch, const char *what,
-                       bool *colsum_fused = nullptr);
+                       bool *colsum_fused = nullptr, int *mse_slots = nullptr);
 
 }  // namespace omg

@@ -76,6 +76,14 @@ struct Params {
     double *colsum_ws;
     float *db;
     int db_acc;
+    // The MSE loss of the stored values against mse_t (laid out as C), after every other epilogue step (tile-exact
+    // kernels, one split): mse_unit gets the gradient for a unit upstream gradient (k_mse_partial's arithmetic with
+    // mse_dsq = 1 / numel) and mse_part[4 * blockIdx.x + wavefront] the wavefront's fp64 sum of the squared
+    // differences (its elements in epilogue order, then a butterfly).
+    const float *mse_t;
+    float *mse_unit;
+    double *mse_part;
+    float mse_dsq;
 };
 
 enum {

@@ -171,6 +171,7 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
 #pragma unroll
         for (int j = 0; j < TN; j++) bcol[j] = p.bias[colv[j]];
     }
+    double mse_acc = 0.0;
     // One MFMA row block (i) at a time keeps the gathered operands to 4 x TN registers each.
 #pragma unroll
     for (int i = 0; i < TM; i++) {
@@ -296,6 +297,22 @@ __device__ __forceinline__ void tile_epilogue(const Params &p, const floatx4 (&a
         for (int r = 0; r < 4; r++)
 #pragma unroll
             for (int j = 0; j < TN; j++) C[(int64_t)rowv[r] * p.ldc + colv[j]] = v[r][j];
+        if (p.mse_t) {  // d = stored value - target; the unit gradient 2 (d / n) as (d dsq) + (d dsq); sum of fl(d d)
+            gather(p.mse_t, p.ldc);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const float d = v[r][j] - t[r][j];
+                    const float u = p.mse_dsq * d;
+                    p.mse_unit[(int64_t)rowv[r] * p.ldc + colv[j]] = u + u;
+                    mse_acc += (double)(d * d);
+                }
+        }
+    }
+    if (p.mse_t) {  // uniform over the launch; every lane of the wavefront is here
+        mse_acc = omd::wave_sum(mse_acc);
+        if ((threadIdx.x & 63) == 0) p.mse_part[4 * blockIdx.x + (threadIdx.x >> 6)] = mse_acc;
     }
 }
 

@@ -120,6 +120,12 @@ om_status check_hip(om_ctx *ctx, hipError_t e, const char *what);
 om_status scratch(om_ctx *ctx, uint64_t bytes, float **out);
 // The same for the second slot (never used by the GEMM engine itself).
 om_status scratch2(om_ctx *ctx, uint64_t bytes, float **out);
+// The MSE loss of pred against target over n elements, with the gradient for a unit upstream gradient in unit and
+// the value posted to rb when given (om_mse_fwd_unit / om_mse_fwd_post); mse_final finishes it from per-wavefront
+// fp64 partials of the squared differences (the fused epilogue of om_linear_fwd_resid_mse).
+om_status mse_of(om_ctx *ctx, const float *pred, const float *target, float *unit, float *loss, int64_t n,
+                 om_readback *rb);
+om_status mse_final(om_ctx *ctx, const double *part, int np, float *loss, int64_t n, om_readback *rb);
 // Checked builds: fills [p, p + bytes) with 0xFF on the context's stream (nothing otherwise).
 om_status poison(om_ctx *ctx, void *p, uint64_t bytes);
 // Sets ctx->noalloc_scratch to the device address of the fixed scratch array on ctx->device (the current device),

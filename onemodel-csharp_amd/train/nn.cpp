@@ -206,6 +206,12 @@ struct PreNormBlock : Module {
         Tensor h = attn->residual((*ln1)(x), mask, x);
         return ffn((*ln2)(h), ff1->w, ff1->b, ff2->w, ff2->b, h);
     }
+    // Losses.Mse of the block's output against target; the composite records form the loss in the last product
+    Tensor mse_loss(const Tensor &x, const Tensor &mask, const Tensor &target) const {
+        if (dev().per_op) return mse((*this)(x, mask), target);
+        Tensor h = attn->residual((*ln1)(x), mask, x);
+        return ffn_mse((*ln2)(h), ff1->w, ff1->b, ff2->w, ff2->b, h, target);
+    }
 };
 
 }  // namespace omt
@@ -1055,7 +1061,7 @@ static void build(omt_model &M, int cfg, const omt_scale &sc) {
         M.add_int_input("lengths", {B}, len);
         M.add_input("mask", {B, L, L}, std::move(mask), false);
         M.loss_fn = [mp](omt_model &s) {
-            return mse((*mp)(s.input("x").t, s.input("mask").t), s.input("target").t);
+            return mp->mse_loss(s.input("x").t, s.input("mask").t, s.input("target").t);
         };
     } else if (cfg == 4) {
         const int B = pick(sc.batch, 32);

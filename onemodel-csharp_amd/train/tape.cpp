@@ -666,24 +666,12 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
     return y;
 }
 
-Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
-           const Tensor &resid) {
-    if (w1->shape.size() != 2 || w2->shape.size() != 2 || x->shape.empty() || x->shape.back() != w1->shape[1] ||
-        w2->shape[1] != w1->shape[0])
-        shape_error("FeedForward: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w1->shape) +
-                    " and " + shape_str(w2->shape));
-    const int d = w1->shape[1], f = w1->shape[0], o = w2->shape[0];
-    const int rows = (int)(x->numel / d);
-    std::vector<int> ys = x->shape;
-    ys.back() = o;
-    if (resid && resid->shape != ys)
-        shape_error("Add: shapes " + shape_str(resid->shape) + " and " + shape_str(ys) + " differ.");
-    float *a = dev().step_floats((int64_t)rows * f);   // GELU output, read by Linear2's weight gradient
-    float *sl = dev().step_floats((int64_t)rows * f);  // GELU's slope at the pre-activation, all its backward needs
-    OMT(om_linear_gelu_fwd_slope(C(), x->data, w1->data, b1 ? b1->data : nullptr, a, sl, rows, d, f));
-    Tensor y = make(ys);
-    if (resid) OMT(om_linear_fwd_resid(C(), a, w2->data, b2 ? b2->data : nullptr, resid->data, y->data, rows, f, o));
-    else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
+static void attach_mse(const Tensor &loss, const Tensor &pred, const Tensor &target, float *diff, float *unit,
+                       int64_t n);
+
+// The FeedForward record of y = Linear2(GELU(Linear1(x))) (+ resid): a is the GELU output, sl GELU's slope.
+static void attach_ffn(const Tensor &y, const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2,
+                       const Tensor &b2, const Tensor &resid, float *a, float *sl, int rows, int d, int f, int o) {
     if (tracked({&x, &w1, &b1, &w2, &b2, &resid})) {
         attach(y, "FeedForward", {x, w1, b1, w2, b2, resid}, [sl, a, rows, d, f, o](Engine &e, Record &r, const float *g) {
             // The input-gradient chain (dh = (g W2) * GELU's slope, then dx = dh W1); both layers' weight and bias
@@ -717,7 +705,66 @@ Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2
             if (r.needs(5) && !folded) e.emit_alias(r, 5, g);
         }, {x, w1, w2});
     }
+}
+
+// Shapes of the feed-forward sub-block; returns rows, the widths d, f, o and the output shape.
+static void ffn_shapes(const Tensor &x, const Tensor &w1, const Tensor &w2, const Tensor &resid, int &rows, int &d,
+                       int &f, int &o, std::vector<int> &ys) {
+    if (w1->shape.size() != 2 || w2->shape.size() != 2 || x->shape.empty() || x->shape.back() != w1->shape[1] ||
+        w2->shape[1] != w1->shape[0])
+        shape_error("FeedForward: input " + shape_str(x->shape) + " does not fit weights " + shape_str(w1->shape) +
+                    " and " + shape_str(w2->shape));
+    d = w1->shape[1];
+    f = w1->shape[0];
+    o = w2->shape[0];
+    rows = (int)(x->numel / d);
+    ys = x->shape;
+    ys.back() = o;
+    if (resid && resid->shape != ys)
+        shape_error("Add: shapes " + shape_str(resid->shape) + " and " + shape_str(ys) + " differ.");
+}
+
+Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
+           const Tensor &resid) {
+    int rows, d, f, o;
+    std::vector<int> ys;
+    ffn_shapes(x, w1, w2, resid, rows, d, f, o, ys);
+    float *a = dev().step_floats((int64_t)rows * f);   // GELU output, read by Linear2's weight gradient
+    float *sl = dev().step_floats((int64_t)rows * f);  // GELU's slope at the pre-activation, all its backward needs
+    OMT(om_linear_gelu_fwd_slope(C(), x->data, w1->data, b1 ? b1->data : nullptr, a, sl, rows, d, f));
+    Tensor y = make(ys);
+    if (resid) OMT(om_linear_fwd_resid(C(), a, w2->data, b2 ? b2->data : nullptr, resid->data, y->data, rows, f, o));
+    else OMT(om_linear_fwd(C(), a, w2->data, b2 ? b2->data : nullptr, y->data, rows, f, o));
+    attach_ffn(y, x, w1, b1, w2, b2, resid, a, sl, rows, d, f, o);
     return y;
+}
+
+Tensor ffn_mse(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
+               const Tensor &resid, const Tensor &target) {
+    // One record pair, two launches fewer: the second product's epilogue also forms the loss's squared differences
+    // and the unit gradient (om_linear_fwd_resid_mse). Taken when the loss's backward needs exactly what mse() keeps
+    // for a tracked prediction and an untracked target (no diff); otherwise the two ops as they are.
+    const bool fuse = resid && target && !target->requires_grad && tracked({&x, &w1, &b1, &w2, &b2, &resid});
+    if (!fuse) return mse(ffn(x, w1, b1, w2, b2, resid), target);
+    int rows, d, f, o;
+    std::vector<int> ys;
+    ffn_shapes(x, w1, w2, resid, rows, d, f, o, ys);
+    if (target->shape != ys)
+        shape_error("Mse: shapes " + shape_str(ys) + " and " + shape_str(target->shape) + " differ.");
+    float *a = dev().step_floats((int64_t)rows * f);
+    float *sl = dev().step_floats((int64_t)rows * f);
+    OMT(om_linear_gelu_fwd_slope(C(), x->data, w1->data, b1 ? b1->data : nullptr, a, sl, rows, d, f));
+    Tensor y = make(ys);
+    const int64_t n = y->numel;
+    float *unit = dev().step_floats(n);
+    Tensor loss = make({});
+    om_readback *rb = dev().take_loss_post();
+    OMT(om_linear_fwd_resid_mse(C(), a, w2->data, b2 ? b2->data : nullptr, resid->data, target->data, y->data, unit,
+                                loss->data, rows, f, o, rb));
+    if (rb) dev().set_loss_posted(loss->data);
+    attach_ffn(y, x, w1, b1, w2, b2, resid, a, sl, rows, d, f, o);
+    attach_mse(loss, y, target, nullptr, unit, n);
+    return loss;
 }
 
 Tensor attention_qkv(const Tensor &x, const Tensor &wq, const Tensor &bq, const Tensor &wk, const Tensor &bk,
@@ -954,7 +1001,14 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
     } else {
         OMT(om_mse_fwd(C(), pred->data, target->data, diff, loss->data, n));
     }
-    if (rec)
+    if (rec) attach_mse(loss, pred, target, diff, unit, n);
+    return loss;
+}
+
+// The Mse record (Losses.cs:86-91) of a loss already computed: diff (may be NULL: recomputed with om_sub when needed)
+// and the gradient for a unit upstream gradient (may be NULL).
+static void attach_mse(const Tensor &loss, const Tensor &pred, const Tensor &target, float *diff, float *unit,
+                       int64_t n) {
         attach(loss, "Mse", {pred, target}, [diff, unit, n](Engine &e, Record &r, const float *g) {
             const float *d = diff;
             if (!d && (g != dev().one() || r.needs(1))) {
@@ -978,7 +1032,6 @@ Tensor mse(const Tensor &pred, const Tensor &target) {
                 else OMT(om_scale(C(), -1.0f, t, dt, n));
             }
         });
-    return loss;
 }
 
 struct ConvGeom {

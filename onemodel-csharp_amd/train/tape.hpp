@@ -196,6 +196,10 @@ Tensor linear_residual(const Tensor &x, const Tensor &w, const Tensor &b, const 
 // (with its bias gradient), the input gradient through GELU in one launch, then Linear1's backward.
 Tensor ffn(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
            const Tensor &resid);
+// mse(ffn(x, w1, b1, w2, b2, resid), target) with the loss formed in the second product's epilogue (the same
+// records; one launch for the product and the squared differences, one for the sum)
+Tensor ffn_mse(const Tensor &x, const Tensor &w1, const Tensor &b1, const Tensor &w2, const Tensor &b2,
+               const Tensor &resid, const Tensor &target);
 Tensor relu(const Tensor &x);
 // The pieces of the reference's per-op records: Ops.MatMul(x2d, W.T()) of x [rows, in] and w [out, in], one record
 // whose rule is MatMul's backward with the W.T() view's Permute backward folded in (dW written as [out, in]);

@@ -24,7 +24,7 @@ def test_hip_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(pkg.om_symbols())  # the ctypes binding covers the header exactly
-    assert L.om_abi_version() == 104
+    assert L.om_abi_version() == 105
 
 
 def test_train_library_exports_every_declared_symbol():

@@ -238,3 +238,44 @@ def test_mse_posts_its_loss_from_its_own_launch(pkg):
     finally:
         L.om_readback_destroy(r)
         d.ctx.close()
+
+
+@pytest.mark.parametrize("rows,inf,outf", [(4096, 1536, 384), (4096, 3072, 768), (256, 64, 192), (100, 36, 20),
+                                           (300, 96, 40)])
+def test_linear_resid_mse_in_one_product(pkg, rows, inf, outf):
+    """om_linear_fwd_resid_mse: y and the unit gradient bit for bit those of om_linear_fwd_resid followed by
+    om_mse_fwd_unit, the loss within fp64 reordering of theirs (and of the float64 mean), and with a readback the same
+    loss posted; shapes that take the epilogue (tile-exact products) and shapes that take the two calls."""
+    from gpu_util import Dev
+    d = Dev()
+    L = d.ctx.L
+    r = C.c_void_p()
+    d.call("om_readback_create", C.c_uint64(4), C.byref(r))
+    rng = np.random.default_rng(rows + inf + outf)
+    try:
+        x = rng.standard_normal((rows, inf)).astype(np.float32)
+        w = (0.05 * rng.standard_normal((outf, inf))).astype(np.float32)
+        b = rng.standard_normal(outf).astype(np.float32)
+        res = rng.standard_normal((rows, outf)).astype(np.float32)
+        tgt = rng.standard_normal((rows, outf)).astype(np.float32)
+        X, W, B, R, TG = d.put(x), d.put(w), d.put(b), d.put(res), d.put(tgt)
+        n = rows * outf
+        Y1, L1, U1 = d.empty((rows, outf)), d.empty((1,)), d.empty((n,))
+        d.call("om_linear_fwd_resid", X, W, B, R, Y1, rows, inf, outf)
+        d.call("om_mse_fwd_unit", Y1, TG, None, L1, U1, C.c_int64(n))
+        for post in (None, r):
+            Y2, L2, U2 = d.empty((rows, outf)), d.empty((1,)), d.empty((n,))
+            d.call("om_linear_fwd_resid_mse", X, W, B, R, TG, Y2, U2, L2, rows, inf, outf, post)
+            assert np.array_equal(d.get(Y2).view(np.uint32), d.get(Y1).view(np.uint32))
+            assert np.array_equal(d.get(U2).view(np.uint32), d.get(U1).view(np.uint32))
+            l1, l2 = float(d.get(L1)[0]), float(d.get(L2)[0])
+            assert abs(l2 - l1) <= 2.5e-7 * abs(l1), (l1, l2)
+            ref = np.mean((d.get(Y1).astype(np.float64) - tgt) ** 2)
+            assert abs(l2 - ref) <= 1e-6 * ref
+            if post is not None:
+                got = np.zeros(1, np.float32)
+                assert L.om_readback_wait(r, got.ctypes.data, C.c_uint64(4)) == 0
+                assert got[0] == np.float32(l2)
+    finally:
+        L.om_readback_destroy(r)
+        d.ctx.close()
