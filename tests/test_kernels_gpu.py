@@ -902,7 +902,7 @@ def ctc_cases():
     from conftest import load_golden
     o = load_golden("autograd_crnn")
     yield "fixture", o["out.lp"], o["in.targets"].astype(np.int32), o["in.input_lengths"].astype(np.int32), \
-        o["in.target_lengths"].astype(np.int32)
+        o["in.target_lengths"].astype(np.int32), 0, 0
     rng = np.random.default_rng(11)
     Tn, B, Cc = 32, 32, 37
     z = rng.standard_normal((Tn, B, Cc)).astype(np.float32)
@@ -913,7 +913,9 @@ def ctc_cases():
     il[1] = 3  # too short for its target: +inf / zero gradient
     tl[1] = 5
     labels = rng.integers(1, Cc, int(tl.sum())).astype(np.int32)
-    yield "c4", lp, labels, il, tl
+    yield "c4", lp, labels, il, tl, 0, 0
+    # the same shape with the last class as the blank and zero_infinity (sequence 1's +inf loss becomes 0)
+    yield "c4-blank-last", lp, (labels - 1).astype(np.int32), il, tl, Cc - 1, 1
     # long sequences: T x (2 L + 1) doubles beyond what the kernels keep in LDS (4096), so alpha and beta live in
     # device scratch
     Tn, B, Cc = 160, 3, 12
@@ -922,37 +924,46 @@ def ctc_cases():
     tl = np.array([30, 12, 40], np.int32)
     il = np.array([Tn, 100, Tn], np.int32)
     labels = rng.integers(1, Cc, int(tl.sum())).astype(np.int32)
-    yield "long", lp, labels, il, tl
+    yield "long", lp, labels, il, tl, 0, 0
+    # CtcLossTests.cs:58-64: LogSoftmax of uniform(-1.5, 1.5) [5, 4, 4], targets [0, 1, 2, 2], input lengths
+    # [5, 5, 2, 1], target lengths [0, 2, 2, 0], blank 3, zero_infinity: two empty targets, and [2, 2] needs three
+    # frames where its input has two (loss +inf, zeroed)
+    z = rng.uniform(-1.5, 1.5, (5, 4, 4)).astype(np.float32)
+    lp = (z - np.log(np.exp(z.astype(np.float64)).sum(-1, keepdims=True))).astype(np.float32)
+    yield "empty-impossible-blank3", lp, np.array([0, 1, 2, 2], np.int32), np.array([5, 5, 2, 1], np.int32), \
+        np.array([0, 2, 2, 0], np.int32), 3, 1
 
 
 @pytest.mark.parametrize("red", [0, 1, 2])
 def test_ctc_bit_exact(dev, T, red):
-    for name, lp, tg, il, tl in ctc_cases():
+    for name, lp, tg, il, tl, blank, zi in ctc_cases():
         Tn, B, Cc = lp.shape
         n_out = B if red == 0 else 1
         ref = np.empty(n_out, np.float32)
-        T.lib().or_ctc_loss(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), Tn, B, Cc, 0, red, 0, T.fp(ref))
+        T.lib().or_ctc_loss(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), Tn, B, Cc, blank, red, zi, T.fp(ref))
+        assert np.isfinite(ref).all() or not zi, name
         gin = np.linspace(0.5, 1.5, n_out).astype(np.float32)
         dref = np.empty_like(lp)
-        T.lib().or_ctc_grad(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), T.fp(gin), Tn, B, Cc, 0, red, T.fp(dref))
+        T.lib().or_ctc_grad(T.fp(lp), T.ip(tg), T.ip(il), T.ip(tl), T.fp(gin), Tn, B, Cc, blank, red, T.fp(dref))
         LP, TG, IL, TL, L, GIN, D = dev.put(lp), dev.put(tg), dev.put(il), dev.put(tl), dev.empty((n_out,)), \
             dev.put(gin), dev.empty(lp.shape, fill=123.0)
         hil, htl, htg = (a.ctypes.data_as(C.c_void_p) for a in (il, tl, tg))
-        dev.call("om_ctc_fwd", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L)
-        dev.call("om_ctc_bwd", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D, Tn, B, Cc, 0, red, 0)
+        dev.call("om_ctc_fwd", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, blank, red, zi, L)
+        dev.call("om_ctc_bwd", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D, Tn, B, Cc, blank, red, 0)
         got = dev.get(L)
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), name
         assert np.array_equal(dev.get(D).view(np.uint32), dref.view(np.uint32)), name
         # the pair that runs each recursion once (beta beside alpha in the forward, tables kept): the same bits
         tb = dev.ctx.L.om_ctc_tables_bytes(Tn, B, int(tl.max()) if tl.size else 0)
         TB, L2, D2 = dev.empty((tb // 4 + 1,)), dev.empty((n_out,)), dev.empty(lp.shape, fill=123.0)
-        dev.call("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L2, TB, tb)
-        dev.call("om_ctc_bwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D2, Tn, B, Cc, 0, red, 0, TB, tb)
+        dev.call("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, blank, red, zi, L2, TB, tb)
+        dev.call("om_ctc_bwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, GIN, D2, Tn, B, Cc, blank, red, 0, TB,
+                 tb)
         assert np.array_equal(dev.get(L2).view(np.uint32), ref.view(np.uint32)), name
         assert np.array_equal(dev.get(D2).view(np.uint32), dref.view(np.uint32)), name
         # a tables buffer smaller than om_ctc_tables_bytes is refused before any launch
-        assert dev.status("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, 0, red, 0, L2, TB,
-                          tb - 8) == 1
+        assert dev.status("om_ctc_fwd_tables", LP, TG, IL, TL, hil, htl, htg, tg.size, Tn, B, Cc, blank, red, zi, L2,
+                          TB, tb - 8) == 1
         assert b"om_ctc_tables_bytes" in dev.ctx.L.om_last_error(dev.ctx.h)
 
 
