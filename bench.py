@@ -690,7 +690,7 @@ def main():
         return time.perf_counter() - t0, last
 
     # The step as the tape runs it launch by launch, then (unless --no-graph) the same step recorded once into a
-    # HIP graph and replayed (omt_set_step_graph; bit-identical results): the headline is the graph's rate.
+    # HIP graph and replayed (omt_set_step_graph; bit-identical results): the headline is the faster of the two.
     el_eager, loss = timed_window()
     el, el_graph = el_eager, None
     if not a.no_graph:

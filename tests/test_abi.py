@@ -72,3 +72,15 @@ def test_adam_scalars_host_helper_matches_oracle(oracle):
         oracle.lib().or_adam_scalars(C.c_float(1e-3), C.c_float(0.9), C.c_float(0.999), C.c_int64(t), C.byref(c),
                                      C.byref(d))
         assert (a.value, b.value) == (c.value, d.value)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 (or a WORLD_SIZE above 1 from a launcher) exits with status 2 and a
+    message saying so, before it loads the library or touches a device."""
+    import subprocess
+    import sys
+    for args, env in ((["--gpus", "2"], {}), (["--gpus", "1"], {"WORLD_SIZE": "8"})):
+        r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), *args], capture_output=True, text=True,
+                           env={**os.environ, **env}, timeout=120)
+        assert r.returncode == 2, (args, env, r.stdout, r.stderr)
+        assert "one GPU only" in r.stderr and r.stdout == ""
