@@ -349,7 +349,9 @@ om_status om_layernorm_bwd_add(om_ctx *ctx, const float *g, const float *x, cons
  * when every slot of the device is held by other live contexts the call fails with OM_E_STATE, and larger shapes are
  * refused with OM_E_ARG, both before anything is launched. The partials are rewritten by every call, so nothing has
  * to start at zero; calls on one context are ordered by its stream, and contexts never share a slot, so calls from
- * several contexts (threads, streams) on one GPU do not race. Results are om_layernorm_bwd's, bit for bit. */
+ * several contexts (threads, streams) on one GPU do not race. A graph captured with this call keeps using the slot
+ * of the context it was captured on: replay it only while that context is alive (after om_ctx_destroy the slot may
+ * go to another context). Results are om_layernorm_bwd's, bit for bit. */
 #define OM_NOALLOC_SCRATCH_BYTES (8u << 20)
 #define OM_NOALLOC_SLOTS 4
 om_status om_layernorm_bwd_noalloc(om_ctx *ctx, const float *g, const float *x, const float *gamma,
