@@ -732,6 +732,107 @@ def test_attention_flash(dev, T, B, H, L, D, masked, packed, acc):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+def _attention_oracle(T, tq, tk, tv, tg, mask, B, H, Lq, Lk, D, scale):
+    """The oracle's attention forward and backward on [B, H, L, D] tensors (mask [B, Lq, Lk] or None)."""
+    o = np.empty_like(tq)
+    mp = T.fp(mask) if mask is not None else None
+    T.lib().or_attention_fwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(o), B, H, Lq, Lk, D, C.c_float(scale))
+    dq, dk, dv = np.empty_like(tq), np.empty_like(tk), np.empty_like(tv)
+    T.lib().or_attention_bwd(T.fp(tq), T.fp(tk), T.fp(tv), mp, 1, T.fp(tg), T.fp(dq), T.fp(dk), T.fp(dv), B, H, Lq,
+                             Lk, D, C.c_float(scale))
+    return o, dq, dk, dv
+
+
+def _same_nans_then_close(got, ref, what):
+    """NaN exactly where the oracle has NaN; every other entry within the 1e-5 scaled bar."""
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), what
+    fin = ~np.isnan(ref)
+    assert scaled(got[fin], ref[fin]) <= TOL, what
+
+
+@pytest.mark.parametrize("B,H,Lq,Lk,D,mask_kind,scale", [
+    (2, 2, 5, 7, 4, None, 0.0),      # GradCheckTests.cs:151: Lq 5, Lk 7, D 4, the default scale 1/sqrt(D)
+    (2, 2, 5, 7, 4, "finite", 0.0),  # :152-160: a [B, Lq, Lk] mask with a quarter of its entries -3
+    (1, 2, 4, 4, 6, None, 0.3),      # :161: an explicit scale
+    (2, 2, 8, 8, 4, "row", 0.0),     # a query row with every key masked
+], ids=["lq5-lk7", "lq5-lk7-mask-3", "scale0.3", "masked-row"])
+def test_attention_reference_gradcheck_shapes(dev, T, B, H, Lq, Lk, D, mask_kind, scale):
+    """The reference's own attention gradient-check shapes (cross-attention lengths, a small even D, a finite
+    additive mask, an explicit scale) through om_attention_fwd / om_attention_bwd against the oracle, and a fully
+    masked query row, which gives NaN in that row's outputs (docs/kernels-attention.md:33-35) and, through the
+    backward, in that row's dQ and in dK and dV of its (batch, head): the same NaN positions as the oracle, every
+    other value within 1e-5 scaled."""
+    rng = np.random.default_rng(Lq * 100 + Lk * 10 + D)
+    q, g = rnd(rng, B, Lq, H, D), rnd(rng, B, Lq, H, D)
+    k, v = rnd(rng, B, Lk, H, D), rnd(rng, B, Lk, H, D)
+    mask = None
+    if mask_kind == "finite":
+        mask = np.where(rng.integers(0, 4, (B, Lq, Lk)) == 0, -3.0, 0.0).astype(np.float32)
+    elif mask_kind == "row":
+        mask = np.where(rng.integers(0, 4, (B, Lq, Lk)) == 0, -np.inf, 0.0).astype(np.float32)
+        mask[:, :, 0] = 0.0  # every other row keeps a key
+        mask[1, 3, :] = -np.inf
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(D))) if scale == 0.0 else scale
+    tq, tk, tv, tg = (np.ascontiguousarray(a.transpose(0, 2, 1, 3)) for a in (q, k, v, g))
+    o_ref, dq, dk, dv = _attention_oracle(T, tq, tk, tv, tg, mask, B, H, Lq, Lk, D, sc)
+    if mask_kind == "row":
+        assert np.isnan(o_ref[1, :, 3]).all() and np.isnan(dk[1]).all() and np.isnan(dv[1]).all()
+        assert not any(np.isnan(t[0]).any() for t in (o_ref, dq, dk, dv))
+    Q, K, V, G = dev.put(q), dev.put(k), dev.put(v), dev.put(g)
+    M = dev.put(mask) if mask is not None else None
+    O, P, DS = dev.empty(q.shape), dev.empty((B, H, Lq, Lk)), dev.empty((B, H, Lq, Lk))
+    DQ, DK, DV = dev.empty(q.shape), dev.empty(k.shape), dev.empty(v.shape)
+    dev.call("om_attention_fwd", Q, K, V, M, 1, O, P, B, H, Lq, Lk, D, C.c_float(sc))
+    dev.call("om_attention_bwd", Q, K, V, P, G, DQ, DK, DV, DS, B, H, Lq, Lk, D, C.c_float(sc), 0)
+    back = lambda t: dev.get(t).transpose(0, 2, 1, 3)
+    _same_nans_then_close(back(O), o_ref, "o")
+    for name, got, ref in (("dq", DQ, dq), ("dk", DK, dk), ("dv", DV, dv)):
+        _same_nans_then_close(back(got), ref, name)
+
+
+@pytest.mark.parametrize("L,D,path", [(64, 32, "flash"), (128, 32, "flash"), (128, 64, "flash"), (64, 32, "fused")],
+                         ids=["rows-L64", "rows-L128", "stream-d64", "fused-L64"])
+def test_attention_fully_masked_row(dev, T, L, D, path):
+    """A query row whose keys are all masked through the entry points the tape calls (the whole-row kernels with
+    statistics at D = 32, the streaming kernels at D = 64, the exact fused kernels): NaN in the row's output and, in
+    the backward, NaN in that row's dQ and in dK and dV of its (batch, head), as the oracle; everything else within
+    1e-5 scaled."""
+    B, H = 2, 3
+    W = H * D
+    rng = np.random.default_rng(L + D + (path == "fused"))
+    qkv, g = rnd(rng, B, L, 3 * W), rnd(rng, B, L, W)
+    lens = rng.integers(L // 2, L + 1, B)
+    mask = np.zeros((B, L, L), np.float32)
+    for b in range(B):
+        mask[b, :, lens[b]:] = -np.inf
+    mask[1, 5, :] = -np.inf
+    heads = lambda a: np.ascontiguousarray(a.reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    tq, tk, tv = (heads(qkv[:, :, i * W:(i + 1) * W]) for i in range(3))
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref, dq, dk, dv = _attention_oracle(T, tq, tk, tv, heads(g), mask, B, H, L, L, D, sc)
+    # the case the test is for: NaN in row 5 of batch 1 and its dQ, in all of batch 1's dK and dV, nowhere in batch 0
+    assert np.isnan(o_ref[1, :, 5]).all() and np.isnan(dq[1, :, 5]).all() and np.isnan(dk[1]).all()
+    assert np.isnan(dv[1]).all() and not any(np.isnan(t[0]).any() for t in (o_ref, dq, dk, dv))
+    QKV, G, M = dev.put(qkv), dev.put(g), dev.put(mask)
+    qp = [QKV.data_ptr() + 4 * i * W for i in range(3)]
+    DQKV = dev.empty((B, L, 3 * W), fill=0.0)
+    dp = [DQKV.data_ptr() + 4 * i * W for i in range(3)]
+    O = dev.empty((B, L, W))
+    if path == "flash":
+        ST = dev.empty((2, B, H, L))
+        dev.call("om_attention_fwd_flash", qp[0], qp[1], qp[2], 3 * W, M, 1, O, W, ST, B, H, L, D, C.c_float(sc))
+        dev.call("om_attention_bwd_flash", qp[0], qp[1], qp[2], 3 * W, M, 1, O, W, ST, G, W, dp[0], dp[1], dp[2],
+                 3 * W, B, H, L, D, C.c_float(sc), 0)
+    else:
+        dev.call("om_attention_fwd_fused", qp[0], qp[1], qp[2], 3 * W, M, 1, O, W, B, H, L, D, C.c_float(sc))
+        dev.call("om_attention_bwd_fused", qp[0], qp[1], qp[2], 3 * W, M, 1, G, W, dp[0], dp[1], dp[2], 3 * W, B, H,
+                 L, D, C.c_float(sc), 0)
+    _same_nans_then_close(heads(dev.get(O)), o_ref, "o")
+    d = dev.get(DQKV)
+    for i, (name, ref) in enumerate((("dq", dq), ("dk", dk), ("dv", dv))):
+        _same_nans_then_close(heads(d[:, :, i * W:(i + 1) * W]), ref, name)
+
+
 @pytest.mark.parametrize("L,masked", [(128, True), (128, False), (64, True)])
 def test_attention_bwd_kernels_agree(dev, L, masked):
     """The backward's two fused kernels give the same bits: 24 x 12 (head, batch) pairs run the quarter-staged
