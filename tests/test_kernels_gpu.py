@@ -944,29 +944,32 @@ def test_mean_permute_bit_exact(dev, B, Cc, H, W):
         assert np.array_equal(dev.get(DX1).view(np.uint32), dev.get(DX2).view(np.uint32)), acc
 
 
-@pytest.mark.parametrize("shape,k,s", [((2, 3, 8, 12), (2, 2), (2, 2)), ((2, 4, 8, 6), (2, 1), (2, 1)),
-                                       ((1, 2, 9, 9), (3, 3), (2, 2))])
-def test_maxpool_bit_exact(dev, T, shape, k, s):
+@pytest.mark.parametrize("shape,k,s,p", [((2, 3, 8, 12), (2, 2), (2, 2), (0, 0)), ((2, 4, 8, 6), (2, 1), (2, 1), (0, 0)),
+                                         ((1, 2, 9, 9), (3, 3), (2, 2), (0, 0)),
+                                         # GradCheckTests.cs:86: 3x3, stride 2, padding 1 (overlapping windows, and
+                                         # windows at the border whose padded taps never win)
+                                         ((2, 3, 9, 10), (3, 3), (2, 2), (1, 1))])
+def test_maxpool_bit_exact(dev, T, shape, k, s, p):
     rng = np.random.default_rng(sum(shape))
     x = rng.integers(-2, 3, shape).astype(np.float32)  # many ties
     x.reshape(-1)[7] = np.nan
     N, Cc, H, W = shape
-    OH, OW = (H - k[0]) // s[0] + 1, (W - k[1]) // s[1] + 1
+    OH, OW = (H + 2 * p[0] - k[0]) // s[0] + 1, (W + 2 * p[1] - k[1]) // s[1] + 1
     y, idx = np.empty((N, Cc, OH, OW), np.float32), np.empty((N, Cc, OH, OW), np.int32)
-    T.lib().or_maxpool_fwd(T.fp(x), T.fp(y), T.ip(idx), N, Cc, H, W, k[0], k[1], s[0], s[1], 0, 0)
+    T.lib().or_maxpool_fwd(T.fp(x), T.fp(y), T.ip(idx), N, Cc, H, W, k[0], k[1], s[0], s[1], p[0], p[1])
     g = rnd(rng, *y.shape)
     dx = np.empty_like(x)
     T.lib().or_maxpool_bwd(T.fp(g), T.ip(idx), T.fp(dx), C.c_int64(idx.size), C.c_int64(x.size))
     X, Y, I, G, DX = dev.put(x), dev.empty(y.shape), dev.empty(y.shape, np.int32), dev.put(g), dev.empty(x.shape)
-    dev.call("om_maxpool_fwd", X, Y, I, N, Cc, H, W, k[0], k[1], s[0], s[1], 0, 0)
-    dev.call("om_maxpool_bwd", G, I, DX, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], 0, 0, 0)
+    dev.call("om_maxpool_fwd", X, Y, I, N, Cc, H, W, k[0], k[1], s[0], s[1], p[0], p[1])
+    dev.call("om_maxpool_bwd", G, I, DX, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], p[0], p[1], 0)
     assert np.array_equal(dev.get(I), idx)
     assert np.array_equal(dev.get(Y).view(np.uint32), y.view(np.uint32))
     assert np.array_equal(dev.get(DX), dx)
     # with the backward of the ReLU that produced the pool's input (x read as that ReLU's output): the pooled
     # gradient where x > 0, the same bits as om_maxpool_bwd then om_relu_bwd, accumulating as asked
     DX2 = dev.empty(x.shape, fill=0.5)
-    dev.call("om_maxpool_relu_bwd", G, I, X, DX2, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], 0, 0, 1)
+    dev.call("om_maxpool_relu_bwd", G, I, X, DX2, N, Cc, H, W, OH, OW, k[0], k[1], s[0], s[1], p[0], p[1], 1)
     ref = np.where(x > 0, dx, np.float32(0.0)).astype(np.float32) + np.float32(0.5)
     assert np.array_equal(dev.get(DX2).view(np.uint32), ref.view(np.uint32))
 
