@@ -504,6 +504,37 @@ def test_softmax_rows(dev, T, rows, cols):
     assert np.array_equal(np.isfinite(dgot), ok) and scaled(dgot[ok], dref[ok]) <= 1e-6
 
 
+@pytest.mark.parametrize("mean,ignore,all_ignored", [(0, 0, False), (1, 0, False), (0, -100, False), (1, 0, True),
+                                                    (0, 0, True)], ids=["sum-ignore0", "mean-ignore0", "sum",
+                                                                        "mean-all-ignored", "sum-all-ignored"])
+def test_nll_reductions_and_ignore_index(dev, T, mean, ignore, all_ignored):
+    """NllLoss with sum reduction and a real class as ignore_index (GradCheckTests.cs:144: "NllLoss sum ignore=0"),
+    and batches whose every row is ignored (the count in the mean is then taken as 1, so the loss is 0 and the
+    gradient 0): om_nll_fwd, om_nll_bwd and the fused om_xent_bwd against the oracle."""
+    rows, cols = 300, 7
+    rng = np.random.default_rng(rows + mean + 3 * all_ignored)
+    z = rnd(rng, rows, cols, scale=2.0)
+    tg = np.full(rows, ignore, np.int32) if all_ignored else rng.integers(0, cols, rows).astype(np.int32)
+    lp = np.empty_like(z)
+    T.lib().or_logsoftmax_fwd(T.fp(z), T.fp(lp), rows, cols)
+    bad = C.c_int(0)
+    loss = T.lib().or_nll_fwd(T.fp(lp), T.ip(tg), rows, cols, mean, ignore, C.byref(bad))
+    gval = np.float32(0.75)
+    dn, dz = np.empty_like(z), np.empty_like(z)
+    T.lib().or_nll_bwd(C.c_float(gval), T.ip(tg), T.fp(dn), rows, cols, mean, ignore)
+    T.lib().or_logsoftmax_bwd(T.fp(dn), T.fp(lp), T.fp(dz), rows, cols)
+    if all_ignored:
+        assert loss == 0.0 and not dn.any()
+    LP, TG, L, BAD = dev.put(lp), dev.put(tg), dev.empty((1,)), dev.empty((1,), np.int32)
+    GS, DN, DZ = dev.put(np.array([gval], np.float32)), dev.empty(z.shape, fill=9.0), dev.empty(z.shape)
+    dev.call("om_nll_fwd", LP, TG, L, BAD, rows, cols, mean, ignore)
+    dev.call("om_nll_bwd", GS, TG, DN, rows, cols, mean, ignore, 0)
+    dev.call("om_xent_bwd", GS, LP, TG, DZ, rows, cols, mean, ignore, 0)
+    assert abs(dev.get(L)[0] - loss) <= 1e-6 * max(1.0, abs(loss)) and dev.get(BAD)[0] == -1
+    assert np.array_equal(dev.get(DN).view(np.uint32), dn.view(np.uint32))
+    assert scaled(dev.get(DZ), dz) <= 1e-6
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 10), (4096, 9), (1024, 37), (7, 3), (1000, 100), (1025, 5)])
 def test_cross_entropy(dev, T, rows, cols):
     rng = np.random.default_rng(cols)
