@@ -445,6 +445,10 @@ def test_mse_and_its_unit_gradient(dev, T):
 def test_layernorm(dev, T, rows, cols):
     rng = np.random.default_rng(rows + cols)
     x, g = rnd(rng, rows, cols, scale=2.0) + 0.5, rnd(rng, rows, cols)
+    # rows of zero variance (rstd = 1/sqrt(eps)), and a row whose mean is far above its spread (the variance's
+    # differences cancel): still the reference's bits
+    x[2], x[5] = np.float32(1.5), np.float32(0.0)
+    x[6] = np.float32(1000.0) + np.float32(0.01) * x[6]
     gam, bet = (1 + 0.1 * rnd(rng, cols)), 0.1 * rnd(rng, cols)
     y, mu, iv = np.empty_like(x), np.empty(rows, np.float32), np.empty(rows, np.float32)
     T.lib().or_layernorm_fwd(T.fp(x), T.fp(gam), T.fp(bet), T.fp(y), T.fp(mu), T.fp(iv), rows, cols, C.c_float(1e-5))
