@@ -543,6 +543,8 @@ def test_nll_reductions_and_ignore_index(dev, T, mean, ignore, all_ignored):
 def test_cross_entropy(dev, T, rows, cols):
     rng = np.random.default_rng(cols)
     z = rnd(rng, rows, cols, scale=2.0)
+    z[1] *= np.float32(500.0)  # logits far beyond exp's range: the row maximum is subtracted first
+    z[2] = np.float32(-3.0e4)  # a constant, very negative row: log(cols) below its value
     tg = rng.integers(0, cols, rows).astype(np.int32)
     tg[3] = -100  # ignored row
     lp = np.empty_like(z)
