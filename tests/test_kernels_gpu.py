@@ -55,6 +55,8 @@ def test_mfma_fragment_layout(dev):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("m,n,k", [(64, 64, 64), (37, 53, 29), (256, 384, 384), (5, 300, 1000), (384, 384, 4096),
                                    (130, 10, 257),
+                                   # inner dimensions shorter than one MFMA step or chunk (masked k loads)
+                                   (70, 50, 1), (33, 129, 3), (600, 2, 7),
                                    # C5's products: the FFN pair and the 768-wide projections over 4096 tokens, and
                                    # the weight-gradient shapes with K = 4096 (the tuned table's C5 rows)
                                    (4096, 3072, 768), (4096, 768, 3072), (4096, 768, 768), (3072, 768, 4096)])
@@ -117,6 +119,8 @@ def test_gemm_rejects_bad_shapes(dev):
                                            # several input chunks, one output, the row-chunk cap
                                            (1024, 256, 37), (2048, 100, 64), (1000, 33, 33), (300, 2000, 5),
                                            (257, 17, 1), (20000, 8, 3),
+                                           # one input feature on the small, narrow and dense paths
+                                           (64, 1, 10), (100, 1, 40), (2048, 1, 384),
                                            # one-launch MFMA layers over a small batch (C1's first layer above):
                                            # one block, K blocks that leave some wavefronts a short last round,
                                            # the block-count bound, a long K
