@@ -831,6 +831,37 @@ def test_attention_reference_gradcheck_shapes(dev, T, B, H, Lq, Lk, D, mask_kind
         _same_nans_then_close(back(got), ref, name)
 
 
+@pytest.mark.parametrize("L", [1, 3, 65, 100])
+def test_attention_flash_entry_at_other_lengths(dev, T, L):
+    """The entry points the tape calls (om_attention_{fwd,bwd}_flash) at sequence lengths none of the fast kernels
+    takes (one key, a few, just past a block of 64, and not a multiple of 64): they fall back to the recomputing
+    path and still match the oracle within 1e-5 scaled, with a padding mask."""
+    B, H, D = 3, 2, 32
+    W = H * D
+    rng = np.random.default_rng(L + 1000)
+    qkv, g = rnd(rng, B, L, 3 * W), rnd(rng, B, L, W)
+    lens = rng.integers((L + 1) // 2, L + 1, B)
+    mask = np.zeros((B, L, L), np.float32)
+    for b in range(B):
+        mask[b, :, lens[b]:] = -np.inf
+    heads = lambda a: np.ascontiguousarray(a.reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    tq, tk, tv = (heads(qkv[:, :, i * W:(i + 1) * W]) for i in range(3))
+    sc = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    o_ref, dq, dk, dv = _attention_oracle(T, tq, tk, tv, heads(g), mask, B, H, L, L, D, sc)
+    QKV, G, M = dev.put(qkv), dev.put(g), dev.put(mask)
+    qp = [QKV.data_ptr() + 4 * i * W for i in range(3)]
+    DQKV = dev.empty((B, L, 3 * W), fill=0.0)
+    dp = [DQKV.data_ptr() + 4 * i * W for i in range(3)]
+    O, ST = dev.empty((B, L, W)), dev.empty((2, B, H, L))
+    dev.call("om_attention_fwd_flash", qp[0], qp[1], qp[2], 3 * W, M, 1, O, W, ST, B, H, L, D, C.c_float(sc))
+    dev.call("om_attention_bwd_flash", qp[0], qp[1], qp[2], 3 * W, M, 1, O, W, ST, G, W, dp[0], dp[1], dp[2], 3 * W,
+             B, H, L, D, C.c_float(sc), 0)
+    assert scaled(heads(dev.get(O)), o_ref) <= TOL
+    d = dev.get(DQKV)
+    for i, ref in enumerate((dq, dk, dv)):
+        assert scaled(heads(d[:, :, i * W:(i + 1) * W]), ref) <= TOL
+
+
 @pytest.mark.parametrize("L,D,path", [(64, 32, "flash"), (128, 32, "flash"), (128, 64, "flash"), (64, 32, "fused")],
                          ids=["rows-L64", "rows-L128", "stream-d64", "fused-L64"])
 def test_attention_fully_masked_row(dev, T, L, D, path):
